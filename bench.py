@@ -1,0 +1,571 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused-layer kernel path on one MI355X.
+
+    python bench.py [--workload c2] [--steps K] [--warmup W] [--gpus 1]
+
+Workloads (shapes of the Qwen3-ASR decoder/encoder; synthetic seeded data,
+random-init weights -- no checkpoints):
+  c1  0.6B decode-token chain, B=1: add+RMSNorm[1,1024] + q/k head-norm+RoPE + SwiGLU[3072]
+  c2  0.6B prefill chain, T=512: embed gather + add+RMSNorm + q/k norm+RoPE + SwiGLU  (default)
+  c3  audio-encoder ops: PE add + LayerNorm on [3000,896], erf-GELU on [3000,3584]
+  c4  1.7B INT8 decode gate/up matvec + SwiGLU, B=1, 28 distinct layers per step
+  c5  1.7B batched decode, B=256: add+RMSNorm + q/k norm+RoPE + quantize + INT8 MFMA gate/up GEMM+SwiGLU
+
+A step is one pass of the workload's kernel chain over one buffer set; sets
+rotate so the working set exceeds the 256 MB last-level cache. Steps are
+captured once into a HIP graph and replayed; the K timed steps are bracketed by
+synchronisation and HIP events on the launch stream. Each kernel's average
+duration is measured the same way (its launches alone, K of them, graph
+replay), and its algorithmic bytes per launch give roofline.achieved.
+
+Prints ONE JSON line. The CPU baseline is the oracle (a C restatement of the
+reference Rust kernels) timed on this host for a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "fused-layer-kernel GB/s (% MI355X HBM peak) + decode tokens/s, 0.6B/1.7B shapes"
+HBM_PEAK_GBS = 8000.0
+LLC_BYTES = 256 << 20
+ROTATE_BYTES = 2 * LLC_BYTES  # each kernel's rotating footprint must exceed 2x the LLC
+
+DEC_0_6B = dict(hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, inter=3072, eps=1e-6, theta=1e6)
+DEC_1_7B = dict(hidden=2048, n_heads=16, n_kv_heads=8, head_dim=128, inter=6144, eps=1e-6, theta=1e6)
+ENC_0_6B = dict(d_model=896, ffn=3584, eps=1e-5, pe_rows=13)
+VOCAB = 151936
+F = 4  # bytes per fp32
+
+
+def sets_for(bytes_per_set: int, minimum: int = 2) -> int:
+    return max(minimum, math.ceil(ROTATE_BYTES / max(1, bytes_per_set)))
+
+
+# ---------------------------------------------------------------------------
+# Workloads
+# ---------------------------------------------------------------------------
+class Workload:
+    name = ""
+    description = ""
+    unit_tokens = 1  # tokens per step (for tokens/s)
+    step_bytes = 0   # algorithmic bytes per step (SURVEY per-unit figure)
+
+    def __init__(self, dev, torch):
+        self.dev = dev
+        self.torch = torch
+        self.gen = torch.Generator(device=dev).manual_seed(1234)
+        self.kernels = {}  # name -> (launch(i), algorithmic bytes per launch)
+
+    def randn(self, n, scale=1.0, mean=0.0):
+        t = self.torch.randn(n, generator=self.gen, device=self.dev)
+        if scale != 1.0:
+            t.mul_(scale)
+        if mean != 0.0:
+            t.add_(mean)
+        return t
+
+    def step(self, i: int) -> None:
+        for launch, _ in self.kernels.values():
+            launch(i)
+
+    def config(self) -> dict:
+        return {}
+
+
+class C1DecodeChain(Workload):
+    name = "c1"
+    description = ("qwen3-asr-0.6b decode-token chain B=1: add+RMSNorm[1,1024] + q/k head-RMSNorm"
+                   "+RoPE(theta 1e6, pos~U[0,511]) + SwiGLU[3072]")
+    unit_tokens = 1
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        c = DEC_0_6B
+        H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
+        self.S = 64
+        self.x = [self.randn(H) for _ in range(self.S)]
+        self.d = [self.randn(H) for _ in range(self.S)]
+        self.y = [torch.empty(H, device=dev) for _ in range(self.S)]
+        self.q = [self.randn(nq * hd) for _ in range(self.S)]
+        self.k = [self.randn(nk * hd) for _ in range(self.S)]
+        self.g = [self.randn(I) for _ in range(self.S)]
+        self.u = [self.randn(I) for _ in range(self.S)]
+        self.o = [torch.empty(I, device=dev) for _ in range(self.S)]
+        self.w = self.randn(H, 0.1, 1.0)
+        self.qw, self.kw = self.randn(hd, 0.1, 1.0), self.randn(hd, 0.1, 1.0)
+        self.rope = K.RopeCache(dev)
+        self.rope.ensure(512, hd, c["theta"])
+        self.pos = [torch.randint(0, 512, (1,), generator=self.gen, device=dev, dtype=torch.int32)
+                    for _ in range(self.S)]
+        S = self.S
+        self.kernels = {
+            "add_rms_norm": (lambda i: K.add_rms_norm(self.x[i % S], self.d[i % S], self.w, self.y[i % S], 1, H, c["eps"]),
+                             5 * H * F),
+            "head_rms_norm_rope": (lambda i: K.head_rms_norm_rope(
+                self.q[i % S], self.k[i % S], self.qw, self.kw, self.rope.cos, self.rope.sin,
+                self.pos[i % S], 1, nq, nk, hd, c["eps"]),
+                2 * (nq + nk) * hd * F + 2 * hd * F + 2 * hd * F * 2),
+            "swiglu": (lambda i: K.swiglu_split(self.o[i % S], self.g[i % S], self.u[i % S], I), 3 * I * F),
+        }
+        self.step_bytes = 83968
+
+    def config(self):
+        return {"batch": 1, "hidden": 1024, "heads": "16q/8kv x 128", "intermediate": 3072}
+
+
+class C2PrefillChain(Workload):
+    name = "c2"
+    description = ("qwen3-asr-0.6b prefill chain T=512: fp32 embed gather from [151936,1024] + "
+                   "add+RMSNorm[512,1024] + q/k head-RMSNorm+RoPE(pos 0..511) + SwiGLU[512,3072]")
+    unit_tokens = 512
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        c = DEC_0_6B
+        T = 512
+        H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
+        smallest = 5 * T * H * F  # add+RMSNorm bytes: the smallest kernel footprint
+        self.S = sets_for(smallest)
+        self.table = self.randn(VOCAB * H, 0.02)
+        S = self.S
+        self.ids = [torch.randint(0, VOCAB, (T,), generator=self.gen, device=dev, dtype=torch.int32)
+                    for _ in range(S)]
+        self.x = [torch.empty(T * H, device=dev) for _ in range(S)]
+        self.d = [self.randn(T * H) for _ in range(S)]
+        self.y = [torch.empty(T * H, device=dev) for _ in range(S)]
+        self.q = [self.randn(T * nq * hd) for _ in range(S)]
+        self.k = [self.randn(T * nk * hd) for _ in range(S)]
+        self.gu = [self.randn(T * 2 * I) for _ in range(S)]
+        self.o = [torch.empty(T * I, device=dev) for _ in range(S)]
+        self.w = self.randn(H, 0.1, 1.0)
+        self.qw, self.kw = self.randn(hd, 0.1, 1.0), self.randn(hd, 0.1, 1.0)
+        self.rope = K.RopeCache(dev)
+        self.rope.ensure(T, hd, c["theta"])
+        self.pos = torch.arange(T, device=dev, dtype=torch.int32)
+        self.kernels = {
+            "embed_gather": (lambda i: K.embed_gather_f32(self.x[i % S], self.table, self.ids[i % S], T, H),
+                             T * 4 + 2 * T * H * F),
+            "add_rms_norm": (lambda i: K.add_rms_norm(self.x[i % S], self.d[i % S], self.w, self.y[i % S], T, H, c["eps"]),
+                             5 * T * H * F + H * F),
+            "head_rms_norm_rope": (lambda i: K.head_rms_norm_rope(
+                self.q[i % S], self.k[i % S], self.qw, self.kw, self.rope.cos, self.rope.sin, self.pos,
+                T, nq, nk, hd, c["eps"]),
+                2 * T * (nq + nk) * hd * F + 2 * hd * F + 2 * T * hd * F),
+            "swiglu_multiply": (lambda i: K.swiglu_multiply(self.o[i % S], self.gu[i % S], T, I),
+                                3 * T * I * F),
+        }
+        self.step_bytes = 46668800
+
+    def config(self):
+        return {"seq_len": 512, "hidden": 1024, "heads": "16q/8kv x 128", "intermediate": 3072,
+                "vocab": VOCAB, "buffer_sets": self.S}
+
+
+class C3EncoderOps(Workload):
+    name = "c3"
+    description = ("qwen3-asr-0.6b audio-encoder ops: sinusoidal PE add (13-row per-chunk table) + "
+                   "LayerNorm(eps 1e-5) on [3000,896], exact erf-GELU on [3000,3584]")
+    unit_tokens = 3000
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        c = ENC_0_6B
+        T, D, FF, P = 3000, c["d_model"], c["ffn"], c["pe_rows"]
+        self.S = sets_for(2 * T * D * F)
+        S = self.S
+        self.x = [self.randn(T * D) for _ in range(S)]
+        self.y = [torch.empty(T * D, device=dev) for _ in range(S)]
+        self.h = [self.randn(T * FF) for _ in range(S)]
+        self.w, self.b = self.randn(D, 0.1, 1.0), self.randn(D, 0.02)
+        self.pe = torch.empty(P * D, device=dev)
+        K.sinusoidal_pe(self.pe, P, D)
+        self.kernels = {
+            "pe_add": (lambda i: K.pe_add(self.x[i % S], self.pe, T, D, P), 2 * T * D * F),
+            "layer_norm": (lambda i: K.layer_norm(self.y[i % S], self.x[i % S], self.w, self.b, T, D, c["eps"]),
+                           2 * T * D * F + 2 * D * F),
+            "gelu_erf": (lambda i: K.gelu_erf(self.h[i % S], T * FF), 2 * T * FF * F),
+        }
+        self.step_bytes = 129031168
+
+    def config(self):
+        return {"rows": 3000, "d_model": 896, "ffn": 3584, "pe_period": 13, "buffer_sets": self.S}
+
+
+class C4Int8Matvec(Workload):
+    name = "c4"
+    description = ("qwen3-asr-1.7b INT8 W8A8 gate/up matvec [12288,2048] + SwiGLU, B=1, 28 distinct "
+                   "layers per step (fp32 x quantized per-vector in-kernel)")
+    unit_tokens = 1
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        c = DEC_1_7B
+        H, I, L = c["hidden"], c["inter"], 28
+        self.layers = []
+        for _ in range(L):
+            w = self.randn(2 * I * H, 0.02)
+            q, s = K.quantize_f32_to_int8(w, 2 * I, H)
+            del w
+            self.layers.append(K.QuantWeight(q, s, 2 * I, H))
+        self.xs = [self.randn(H) for _ in range(L)]
+        self.outs = [torch.empty(I, device=dev) for _ in range(L)]
+        self.L = L
+        self.H, self.I = H, I
+        layer_bytes = 2 * I * H + 2 * I * F + H * F + I * F
+
+        def all_layers(i):
+            for l in range(L):
+                K.gate_up_swiglu_w8a8_f32in(self.outs[l], self.layers[l], self.xs[l], H, I)
+
+        self.kernels = {"gate_up_swiglu_w8a8_matvec": (lambda i: K.gate_up_swiglu_w8a8_f32in(
+            self.outs[i % L], self.layers[i % L], self.xs[i % L], H, I), layer_bytes)}
+        self.all_layers = all_layers
+        self.layer_bytes = layer_bytes
+        self.step_bytes = L * 25247744
+
+    def step(self, i):
+        self.all_layers(i)
+
+    def config(self):
+        return {"batch": 1, "in_dim": 2048, "gate_up_rows": 12288, "layers": 28}
+
+
+class C5BatchedDecode(Workload):
+    name = "c5"
+    description = ("qwen3-asr-1.7b batched decode B=256 (positions U[0,2047]): add+RMSNorm[256,2048] + "
+                   "q/k head-RMSNorm+RoPE + per-row int8 quantize + W8A8 MFMA gate/up GEMM "
+                   "[256,2048]x[2048,12288] + SwiGLU; 28 distinct layers rotate")
+    unit_tokens = 256
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        c = DEC_1_7B
+        B, L = 256, 28
+        H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
+        self.layers = []
+        for _ in range(L):
+            w = self.randn(2 * I * H, 0.02)
+            q, s = K.quantize_f32_to_int8(w, 2 * I, H)
+            del w
+            self.layers.append(K.QuantWeight(q, s, 2 * I, H))
+        S = L
+        self.x = [self.randn(B * H) for _ in range(S)]
+        self.d = [self.randn(B * H) for _ in range(S)]
+        self.y = [torch.empty(B * H, device=dev) for _ in range(S)]
+        self.q = [self.randn(B * nq * hd) for _ in range(S)]
+        self.k = [self.randn(B * nk * hd) for _ in range(S)]
+        self.xq = [torch.empty(B * H, dtype=torch.int8, device=dev) for _ in range(S)]
+        self.xsc = [torch.empty(B, device=dev) for _ in range(S)]
+        self.o = [torch.empty(B * I, device=dev) for _ in range(S)]
+        self.w = self.randn(H, 0.1, 1.0)
+        self.qw, self.kw = self.randn(hd, 0.1, 1.0), self.randn(hd, 0.1, 1.0)
+        self.rope = K.RopeCache(dev)
+        self.rope.ensure(2048, hd, c["theta"])
+        self.pos = [torch.randint(0, 2048, (B,), generator=self.gen, device=dev, dtype=torch.int32)
+                    for _ in range(S)]
+        self.kernels = {
+            "add_rms_norm": (lambda i: K.add_rms_norm(self.x[i % S], self.d[i % S], self.w, self.y[i % S], B, H, c["eps"]),
+                             5 * B * H * F + H * F),
+            "head_rms_norm_rope": (lambda i: K.head_rms_norm_rope(
+                self.q[i % S], self.k[i % S], self.qw, self.kw, self.rope.cos, self.rope.sin,
+                self.pos[i % S], B, nq, nk, hd, c["eps"]),
+                2 * B * (nq + nk) * hd * F + 2 * hd * F + 2 * B * hd * F + B * 4),
+            "quantize_rows": (lambda i: K.quantize_rows_i8(self.xq[i % S], self.xsc[i % S], self.y[i % S], B, H),
+                              B * H * F + B * H + B * F),
+            "gate_up_swiglu_w8a8_gemm": (lambda i: K.gate_up_swiglu_w8a8(
+                self.o[i % S], self.layers[i % L], self.xq[i % S], self.xsc[i % S], B, H, I),
+                2 * I * H + 2 * I * F + B * H + B * F + B * I * F),
+        }
+        self.step_bytes = 50653184
+        self.gemm_ops = 2 * B * 2 * I * H
+
+    def config(self):
+        return {"batch": 256, "hidden": 2048, "heads": "16q/8kv x 128", "intermediate": 6144,
+                "layers_rotated": 28}
+
+
+WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c4": C4Int8Matvec,
+             "c5": C5BatchedDecode}
+
+
+# ---------------------------------------------------------------------------
+# Timing
+# ---------------------------------------------------------------------------
+def time_replay(torch, fn, n: int, use_graph: bool, reps: int = 1) -> float:
+    """Average ms per call of fn(i), i = 0..n-1, measured with HIP events on the
+    current stream. With use_graph, the n calls are captured once and replayed."""
+    stream = torch.cuda.current_stream()
+    if use_graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i)
+        g.replay()  # warm the graph once
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            g.replay()
+            e.record(stream)
+            torch.cuda.synchronize()
+            best = min(best, s.elapsed_time(e))
+        del g
+        return best / n
+    best = float("inf")
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for i in range(n):
+            fn(i)
+        e.record(stream)
+        torch.cuda.synchronize()
+        best = min(best, s.elapsed_time(e))
+    return best / n
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (oracle, reference thread model)
+# ---------------------------------------------------------------------------
+def cpu_baseline(name: str, seconds: float) -> dict:
+    import numpy as np
+
+    import oracle
+
+    r = np.random.default_rng(99)
+
+    def run_until(fn, budget):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= budget:
+                return n, dt
+
+    nproc = os.cpu_count() or 1
+    if name in ("c1", "c2", "c5"):
+        c = DEC_0_6B if name != "c5" else DEC_1_7B
+        T = {"c1": 1, "c2": 512, "c5": 256}[name]
+        H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
+        x = r.standard_normal(T * H, dtype=np.float32)
+        d = r.standard_normal(T * H, dtype=np.float32)
+        w = (1 + 0.1 * r.standard_normal(H)).astype(np.float32)
+        q = r.standard_normal(T * nq * hd, dtype=np.float32)
+        k = r.standard_normal(T * nk * hd, dtype=np.float32)
+        qw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+        kw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+        cos, sin = oracle.rope_table(2048, hd, c["theta"])
+        pos = (np.arange(T) if name == "c2" else r.integers(0, 2048 if name == "c5" else 512, T)).astype(np.int32)
+        gu = r.standard_normal(T * 2 * I, dtype=np.float32)
+        table = ids = None
+        if name == "c2":
+            table = (0.02 * r.standard_normal((VOCAB, H), dtype=np.float32))
+            ids = r.integers(0, VOCAB, T).astype(np.int32)
+        wq = ws = None
+        if name == "c5":
+            wq, ws = oracle.quantize_f32_to_int8((0.02 * r.standard_normal(2 * I * H, dtype=np.float32)), 2 * I, H)
+
+        def step():
+            if table is not None:
+                xx = oracle.embed_gather_f32(table, ids, H)
+            else:
+                xx = x
+            oracle.add_rms_norm(xx, d, w, T, H, c["eps"])
+            oracle.head_rms_norm_rope(q, k, qw, kw, cos, sin, pos, T, nq, nk, hd, c["eps"])
+            if name == "c5":
+                # the reference's INT8 path: W8A32 matvec per token, then swiglu_multiply
+                gate_up = oracle.linear_nobias_int8(x, wq, ws, T, H, 2 * I, n_threads=min(nproc, 16))
+                oracle.swiglu_multiply(gate_up, T, I)
+            elif name == "c1":
+                oracle.swiglu_split(gu[:I], gu[I:2 * I])
+            else:
+                oracle.swiglu_multiply(gu, T, I)
+
+        n, dt = run_until(step, seconds)
+        wl_bytes = {"c1": 83968, "c2": 46668800, "c5": 50653184}[name]
+        per = dt / n
+        threads = min(nproc, 16) if name == "c5" else 1
+        return {"value": wl_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "ms_per_step": per * 1e3, "tokens_per_s": T / per if name != "c5" else T / (28 * per),
+                "sample": f"{n} full steps of the {name} chain (T={T}) on the oracle, "
+                          f"{'single-threaded norms/RoPE/SwiGLU' + (', INT8 W8A32 matvec on ' + str(threads) + ' threads' if name == 'c5' else '')}"}
+    if name == "c3":
+        T, D, FF = 3000, 896, 3584
+        x = r.standard_normal(T * D, dtype=np.float32)
+        h = r.standard_normal(T * FF, dtype=np.float32)
+        w = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+        b = (0.02 * r.standard_normal(D)).astype(np.float32)
+        pe = oracle.sinusoidal_pe(13, D)
+
+        def step():
+            xx = oracle.pe_add(x, pe, T, D, 13)
+            oracle.layer_norm(xx, w, b, T, D, 1e-5)
+            oracle.gelu_tanh(h)  # the reference CPU path's GELU (tanh form)
+
+        n, dt = run_until(step, seconds)
+        per = dt / n
+        return {"value": 129031168 / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "ms_per_step": per * 1e3,
+                "sample": f"{n} full c3 steps on the oracle, single-threaded; GELU is the reference's tanh form"}
+    if name == "c4":
+        H, I = 2048, 6144
+        wq, ws = oracle.quantize_f32_to_int8((0.02 * r.standard_normal(2 * I * H, dtype=np.float32)), 2 * I, H)
+        x = r.standard_normal(H, dtype=np.float32)
+        threads = min(nproc, 16)
+
+        def step():
+            gate_up = oracle.linear_nobias_int8(x, wq, ws, 1, H, 2 * I, n_threads=threads)
+            oracle.swiglu_multiply(gate_up, 1, I)
+
+        n, dt = run_until(step, seconds)
+        per = dt / n
+        return {"value": 25247744 / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "ms_per_step": per * 1e3 * 28, "tokens_per_s": 1.0 / (28 * per),
+                "sample": f"{n} layer matvecs (W8A32, the reference's INT8 path) + SwiGLU on the oracle, "
+                          f"{threads} threads; one weight matrix reused, so it is LLC-warm"}
+    raise ValueError(name)
+
+
+# ---------------------------------------------------------------------------
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true", help="launch from the host instead of graph replay")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards as pure data parallelism with no exchange; see the design notes)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from qwenasr_amd import _lib
+
+    _lib.lib()  # fail loudly if the HIP library is missing
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    wl = WORKLOADS[args.workload](dev, torch)
+    torch.cuda.synchronize()
+    use_graph = not args.eager
+    K, W = args.steps, args.warmup
+    print(f"[bench] workload {wl.name}: {len(wl.kernels)} kernels, warmup {W}, steps {K}, "
+          f"{'graph replay' if use_graph else 'eager'}", file=sys.stderr, flush=True)
+
+    # warmup (eager, then the timed region replays a graph of K steps)
+    for i in range(W):
+        wl.step(i)
+    torch.cuda.synchronize()
+
+    reps = 3
+    if use_graph:
+        try:
+            ms_step = time_replay(torch, wl.step, K, True, reps)
+        except Exception as ex:  # capture unsupported: fall back to eager timing
+            print(f"[bench] graph capture failed ({ex}); timing eagerly", file=sys.stderr)
+            use_graph = False
+    if not use_graph:
+        ms_step = time_replay(torch, wl.step, K, False, reps)
+    print(f"[bench] step {ms_step * 1e3:.2f} us", file=sys.stderr, flush=True)
+
+    per_kernel = {}
+    for kname, (launch, nbytes) in wl.kernels.items():
+        ms = time_replay(torch, launch, K, use_graph, reps)
+        per_kernel[kname] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / (ms * 1e-3) / 1e9,
+                             "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        print(f"[bench] {kname}: {ms * 1e3:.2f} us, {per_kernel[kname]['GB/s']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+
+    value = wl.step_bytes / (ms_step * 1e-3) / 1e9
+    if wl.name == "c4":
+        tokens_per_s = 1.0 / (ms_step * 1e-3)  # one step = one token through 28 layers
+    elif wl.name == "c5":
+        tokens_per_s = wl.unit_tokens / (28 * ms_step * 1e-3)
+    elif wl.name == "c1":
+        tokens_per_s = 1.0 / (28 * ms_step * 1e-3)
+    else:
+        tokens_per_s = wl.unit_tokens / (ms_step * 1e-3)
+
+    # dominant kernel = largest share of the step time
+    dom_name = max(per_kernel, key=lambda k: per_kernel[k]["us"] * (28 if wl.name == "c4" else 1))
+    dom = per_kernel[dom_name]
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get(wl.name, {}).get(dom_name)
+        except (ValueError, OSError):
+            traffic = None
+    roofline = {"bound": "hbm", "kernel": dom_name, "achieved": round(dom["GB/s"], 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["frac_hbm"], 4),
+                "traffic": traffic, "avg_us": round(dom["us"], 3),
+                "algorithmic_bytes": dom["bytes"]}
+    if wl.name == "c5":
+        g = per_kernel["gate_up_swiglu_w8a8_gemm"]
+        roofline["gemm_mfma_int8_TOPS"] = round(wl.gemm_ops / (g["us"] * 1e-6) / 1e12, 1)
+        roofline["gemm_mfma_frac_of_5000_TOPS"] = round(wl.gemm_ops / (g["us"] * 1e-6) / 5.0e15, 4)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s sample)...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(wl.name, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if wl.name in ("c1", "c2", "c3") else "int8/int32->f32",
+        "data": "synthetic (seeded torch.randn inputs, random-init weights; no checkpoints)",
+        "config": {"workload": wl.description, **wl.config(),
+                   "timing": "hipGraph replay of K steps, HIP events" if use_graph else "eager launches, HIP events"},
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "tokens_per_s": round(tokens_per_s, 1),
+        "per_kernel": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                       for k, v in per_kernel.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

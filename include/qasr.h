@@ -1,0 +1,237 @@
+/*
+ * qasr.h — C-ABI of the MI355X (gfx950) fused-layer kernel library for the
+ * QwenASR decoder/encoder hot path.
+ *
+ * Every entry point:
+ *   - takes DEVICE pointers (memory from hipMalloc or a torch CUDA tensor),
+ *     the dimensions in the same order as the Rust function it replaces, and a
+ *     HIP stream passed as `void*` (NULL = the default stream);
+ *   - only enqueues work: it never synchronises, never copies to the host and
+ *     never allocates (the RoPE-table helpers are the one documented exception:
+ *     they are setup calls, like RopeCache::ensure);
+ *   - returns a qasr_status; on failure qasr_last_error() gives a message
+ *     (thread-local, valid until the next failing call on that thread).
+ *
+ * The Rust reference returns `()` and panics on bad dimensions (slice bounds).
+ * Here a bad dimension or null pointer is QASR_ERR_INVALID_ARG and nothing is
+ * launched. Data-dependent faults that the reference would panic on (a token id
+ * or RoPE position outside its table) cannot be checked on the host without a
+ * synchronisation, so the kernels poison that row with NaN instead of reading
+ * out of bounds.
+ *
+ * Reference citations are relative to crates/qwen-asr/src/ of
+ * ZhaoChaoqun/QwenASR.
+ */
+#ifndef QASR_H
+#define QASR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum qasr_status {
+  QASR_OK = 0,
+  QASR_ERR_INVALID_ARG = 1, /* null pointer, zero-size contract breach, overflow */
+  QASR_ERR_UNSUPPORTED = 2, /* a shape the kernels do not implement */
+  QASR_ERR_HIP = 3          /* the HIP runtime rejected the launch */
+} qasr_status;
+
+/* Library version, (major << 16) | (minor << 8) | patch. */
+int qasr_version(void);
+
+/* Message describing the last failing call on this thread ("" if none). */
+const char* qasr_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* Elementwise and normalisation (decoder + encoder)                         */
+/* ------------------------------------------------------------------------ */
+
+/* a[i] += b[i], i < n.  Replaces kernels::add_inplace (kernels/mod.rs:486-488). */
+int qasr_add_inplace_f32(float* a, const float* b, size_t n, void* stream);
+
+/* out[s,:] = x[s,:] * (1/sqrt(sum(x^2)/hidden + eps)) * weight.
+ * Replaces kernels::rms_norm (kernels/mod.rs:897-918, x86 body avx.rs:374-415).
+ * out may alias x. */
+int qasr_rms_norm_f32(float* out, const float* x, const float* weight,
+                      size_t seq_len, size_t hidden, float eps, void* stream);
+
+/* Fused residual add + RMSNorm: x[s,:] += delta[s,:]; out[s,:] = rms_norm(x[s,:]).
+ * Replaces the pair add_inplace + rms_norm at decoder.rs:908+910, 924->878,
+ * 823+827 and 838->789 (kernels/mod.rs:486-488 then 897-918). x is updated
+ * in place (the residual stream); out may alias delta. */
+int qasr_add_rms_norm_f32(float* x, const float* delta, const float* weight,
+                          float* out, size_t seq_len, size_t hidden, float eps,
+                          void* stream);
+
+/* LayerNorm: out = ((x - mean) * inv_std) * weight + bias (fused multiply-add),
+ * inv_std = 1/sqrt(var + eps), two-pass mean/variance per row.
+ * Replaces kernels::layer_norm (kernels/mod.rs:866-895, avx.rs:417-481). */
+int qasr_layer_norm_f32(float* out, const float* x, const float* weight,
+                        const float* bias, size_t seq_len, size_t hidden,
+                        float eps, void* stream);
+
+/* In-place per-head RMSNorm with a shared head_dim-long weight (q_norm/k_norm).
+ * Replaces kernels::rms_norm_per_head (kernels/mod.rs:920-935). */
+int qasr_rms_norm_per_head_f32(float* x, const float* weight, size_t seq_len,
+                               size_t n_heads, size_t head_dim, float eps,
+                               void* stream);
+
+/* In-place NeoX half-rotation RoPE; row s uses cos_vals/sin_vals row s
+ * (each row head_dim long: [c(0..half) | c(0..half)]).
+ * Replaces kernels::apply_rope_neox (kernels/mod.rs:1247-1267). */
+int qasr_apply_rope_neox_f32(float* x, const float* cos_vals,
+                             const float* sin_vals, size_t seq,
+                             size_t n_heads, size_t head_dim, void* stream);
+
+/* Fused q/k head RMSNorm + RoPE with per-row positions:
+ *   q[s,h,:] = rope(rms_norm_head(q[s,h,:], q_norm_w), positions[s])
+ *   k[s,h,:] = rope(rms_norm_head(k[s,h,:], k_norm_w), positions[s])
+ * cos_tab/sin_tab are RopeCache tables of table_rows rows of head_dim floats
+ * (decoder.rs:253-289). positions == NULL means row s uses position s.
+ * A position outside [0, table_rows) poisons that row's q and k with NaN.
+ * Replaces rms_norm_per_head x2 + apply_rope_neox x2 at decoder.rs:455-459,
+ * 543-547, 799-803, 888-892 (kernels/mod.rs:920-935, 1247-1267). k may be NULL
+ * when n_kv_heads == 0. */
+int qasr_head_rms_norm_rope_f32(float* q, float* k, const float* q_norm_w,
+                                const float* k_norm_w, const float* cos_tab,
+                                const float* sin_tab, const int32_t* positions,
+                                size_t seq, size_t n_heads, size_t n_kv_heads,
+                                size_t head_dim, size_t table_rows, float eps,
+                                void* stream);
+
+/* Fill RoPE table rows [pos_begin, pos_end) for theta and head_dim:
+ *   inv_freq[d] = 1 / theta^((2d)/head_dim)   (f32 powf, computed on the host
+ *   once per call exactly as RopeCache::ensure does, decoder.rs:262-266)
+ *   angle = (f32)pos * inv_freq[d]; row = [cos(angle) | cos(angle)], same for sin.
+ * cos_tab/sin_tab must hold pos_end rows of head_dim floats. This is the
+ * table-growth step of RopeCache::ensure (decoder.rs:253-289); head_dim even,
+ * head_dim <= 512. */
+int qasr_rope_table_fill_f32(float* cos_tab, float* sin_tab, size_t pos_begin,
+                             size_t pos_end, size_t head_dim, float theta,
+                             void* stream);
+
+/* out[s,j] = silu(gate_up[s,2j]) * gate_up[s,2j+1] on the row-interleaved
+ * gate/up buffer. Arithmetic follows the x86_64 reference: blocks of 8 use the
+ * degree-5 fast_exp polynomial, the row tail uses expf.
+ * Replaces kernels::swiglu_multiply (kernels/mod.rs:965-985, avx.rs:483-514,
+ * 565-599). */
+int qasr_swiglu_multiply_f32(float* out, const float* gate_up, size_t seq_len,
+                             size_t intermediate, void* stream);
+
+/* out[j] = silu(gate[j]) * up[j] with silu(g) = g / (1 + expf(-g)) on split
+ * gate/up buffers. out may alias gate (then it is swiglu_multiply_inplace,
+ * kernels/mod.rs:988-994); the decode loop's inline SwiGLU uses the same
+ * arithmetic (decoder.rs:571-576, 916-921). */
+int qasr_swiglu_split_f32(float* out, const float* gate, const float* up,
+                          size_t n, void* stream);
+
+/* x[i] = x[i] / (1 + expf(-x[i])).  Replaces kernels::silu (kernels/mod.rs:941-946). */
+int qasr_silu_f32(float* x, size_t n, void* stream);
+
+/* tanh-approximation GELU in place, x86_64 reference arithmetic (blocks of 8 via
+ * fast_exp, tail via tanhf). Replaces kernels::gelu (kernels/mod.rs:948-963,
+ * avx.rs:533-563). */
+int qasr_gelu_tanh_f32(float* x, size_t n, void* stream);
+
+/* Exact GELU in place: x = 0.5 * x * (1 + erf(x / sqrt(2))), evaluated as
+ * 0.5 * x * erfc(-x / sqrt(2)). The reference CPU path has only the tanh form;
+ * erf-GELU is what its Metal path calls (encoder_gpu.rs:470,480). */
+int qasr_gelu_erf_f32(float* x, size_t n, void* stream);
+
+/* pe[p, d] = sin(p * inv[d]), pe[p, half + d] = cos(p * inv[d]),
+ * inv[d] = exp(-d * ln(10000) / (half - 1)).
+ * Replaces kernels::sinusoidal_pe (kernels/mod.rs:1213-1226). */
+int qasr_sinusoidal_pe_f32(float* pe, size_t n_pos, size_t d_model, void* stream);
+
+/* x[r,:] += pe[r mod n_pos, :] for r < rows. Replaces the per-chunk
+ * sinusoidal_pe + add_inplace at encoder.rs:340-343 and 599-601, with the PE
+ * table built once by qasr_sinusoidal_pe_f32. */
+int qasr_pe_add_f32(float* x, const float* pe, size_t rows, size_t d_model,
+                    size_t n_pos, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Token-embedding gather (decoder.rs:631-646, context.rs:115-124)           */
+/* ------------------------------------------------------------------------ */
+
+/* out[i,:] = table[ids[i],:] (fp32 table of vocab rows). An id outside
+ * [0, vocab) poisons out[i,:] with NaN. */
+int qasr_embed_gather_f32(float* out, const float* table, const int32_t* ids,
+                          size_t n, size_t dim, size_t vocab, void* stream);
+
+/* out[i,:] = bf16->f32(table[ids[i],:]) by a 16-bit shift.
+ * Replaces tok_embed_bf16_to_f32 (decoder.rs:631-636) for n tokens at once. */
+int qasr_embed_gather_bf16(float* out, const uint16_t* table,
+                           const int32_t* ids, size_t n, size_t dim,
+                           size_t vocab, void* stream);
+
+/* out[i,:] = (f32)table[ids[i],:] * row_scales[ids[i]].
+ * Replaces tok_embed_int8_to_f32 (decoder.rs:639-646) for n tokens at once. */
+int qasr_embed_gather_i8(float* out, const int8_t* table,
+                         const float* row_scales, const int32_t* ids, size_t n,
+                         size_t dim, size_t vocab, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* INT8 (qwen-asr-quantize .qint8 format)                                    */
+/* ------------------------------------------------------------------------ */
+
+/* Per-row symmetric int8 quantization: absmax, scale = absmax/127,
+ * inv = 127/absmax (0 if absmax == 0), q = clamp(roundf(v*inv), -128, 127)
+ * (round half away from zero; NaN -> 0). Same routine as
+ * quantize_f32_to_int8 (quantize.rs:633-662); applied to activations it is the
+ * per-vector quantization of the W8A8 path. */
+int qasr_quantize_rows_i8(int8_t* q, float* scales, const float* x,
+                          size_t rows, size_t cols, void* stream);
+
+/* W8A32 linear, no bias: y[s,o] = (sum_k (f32)w[o,k] * x[s,k]) * scales[o].
+ * Replaces kernels::linear_nobias_int8 (kernels/mod.rs:650-661,
+ * generic.rs:37-49). */
+int qasr_linear_nobias_int8_f32(float* y, const float* x, const int8_t* w,
+                                const float* scales, size_t seq_len,
+                                size_t in_dim, size_t out_dim, void* stream);
+
+/* W8A32 linear with optional bias (bias may be NULL): y = linear_nobias + bias.
+ * Replaces kernels::linear_int8 (kernels/mod.rs:664-673). */
+int qasr_linear_int8_f32(float* y, const float* x, const int8_t* w,
+                         const float* scales, const float* bias,
+                         size_t seq_len, size_t in_dim, size_t out_dim,
+                         void* stream);
+
+/* Row-interleave separate gate [inter,hidden] and up [inter,hidden] int8
+ * matrices (and their scales) into the fused [2*inter,hidden] layout
+ * g0,u0,g1,u1,... the decoder builds at load time (decoder.rs:701-719). */
+int qasr_interleave_gate_up_i8(int8_t* w_gate_up, float* scales_gate_up,
+                               const int8_t* w_gate, const float* s_gate,
+                               const int8_t* w_up, const float* s_up,
+                               size_t intermediate, size_t hidden, void* stream);
+
+/* W8A8 gate/up projection fused with SwiGLU, int32-exact dot products:
+ *   dg = sum_k w[2j,k]*xq[b,k],  du = sum_k w[2j+1,k]*xq[b,k]     (int32)
+ *   g  = ((f32)dg * x_scales[b]) * scales[2j]
+ *   u  = ((f32)du * x_scales[b]) * scales[2j+1]
+ *   out[b,j] = (g / (1 + expf(-g))) * u
+ * w is the row-interleaved fused gate/up matrix [2*inter, in_dim] and scales
+ * its interleaved per-row scales (decoder.rs:701-719). batch == 1 runs a
+ * bandwidth-bound matvec; batch > 1 runs an MFMA int8 GEMM. in_dim % 16 == 0.
+ * No reference counterpart: the reference runs this projection W8A32
+ * (decoder.rs:912-921 -> kernels/mod.rs:650-661) followed by SwiGLU. */
+int qasr_gate_up_swiglu_w8a8(float* out, const int8_t* w, const float* scales,
+                             const int8_t* xq, const float* x_scales,
+                             size_t batch, size_t in_dim, size_t intermediate,
+                             void* stream);
+
+/* As qasr_gate_up_swiglu_w8a8 for batch == 1 with an fp32 input vector that
+ * the kernel quantizes per-vector itself (qasr_quantize_rows_i8 arithmetic),
+ * so one launch covers quantize + matvec + SwiGLU. */
+int qasr_gate_up_swiglu_w8a8_f32in(float* out, const int8_t* w,
+                                   const float* scales, const float* x,
+                                   size_t in_dim, size_t intermediate,
+                                   void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* QASR_H */

@@ -1,0 +1,171 @@
+// Shared device helpers and C-ABI glue for the gfx950 kernels.
+//
+// All kernels are written for 64-lane wavefronts. Reductions inside a wave use
+// cross-lane shuffles; reductions across the waves of a workgroup go through
+// LDS. Nothing here depends on any other GPU family.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include <string>
+
+#include "../../include/qasr.h"
+
+#define QASR_DEV __device__ __forceinline__
+
+namespace qasr {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Cross-lane reductions
+// ---------------------------------------------------------------------------
+
+// Sum over groups of WIDTH consecutive lanes (WIDTH a power of two <= 64).
+// Every lane of a group ends with the same value.
+template <int WIDTH>
+QASR_DEV float group_sum(float v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+template <int WIDTH>
+QASR_DEV float group_max(float v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m >= 1; m >>= 1) {
+    float o = __shfl_xor(v, m, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+template <int WIDTH>
+QASR_DEV int group_sum_i32(int v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+QASR_DEV float wave_sum(float v) { return group_sum<kWave>(v); }
+QASR_DEV float wave_max(float v) { return group_max<kWave>(v); }
+
+// Sum over a workgroup of BLOCK threads; every thread gets the same result
+// (the per-wave partials are added in wave order by every thread).
+// `lds` needs BLOCK/64 floats. Ends with a barrier so `lds` can be reused.
+template <int BLOCK>
+QASR_DEV float block_sum(float v, float* lds) {
+  v = wave_sum(v);
+  if constexpr (BLOCK == kWave) {
+    return v;
+  } else {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = threadIdx.x / kWave;
+    if (lane == 0) lds[w] = v;
+    __syncthreads();
+    float t = lds[0];
+#pragma unroll
+    for (int i = 1; i < BLOCK / kWave; ++i) t += lds[i];
+    __syncthreads();
+    return t;
+  }
+}
+
+template <int BLOCK>
+QASR_DEV float block_max(float v, float* lds) {
+  v = wave_max(v);
+  if constexpr (BLOCK == kWave) {
+    return v;
+  } else {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = threadIdx.x / kWave;
+    if (lane == 0) lds[w] = v;
+    __syncthreads();
+    float t = lds[0];
+#pragma unroll
+    for (int i = 1; i < BLOCK / kWave; ++i) t = lds[i] > t ? lds[i] : t;
+    __syncthreads();
+    return t;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Scalar math shared by several kernels
+// ---------------------------------------------------------------------------
+
+// silu(g) = g / (1 + exp(-g)), the libm form of decoder.rs:571-576.
+QASR_DEV float silu_expf(float g) { return g / (1.0f + expf(-g)); }
+
+// The x86_64 reference's degree-5 exp polynomial (avx.rs:483-514), one lane:
+// clamp x*log2(e) to [-126, 126], split into nearest integer i (round half to
+// even, as cvtps_epi32 does) and fraction f, then 2^i * P(f*ln2) with P the
+// Taylor polynomial of exp to degree 5 evaluated by fused multiply-adds.
+QASR_DEV float ref_fast_exp(float x) {
+  float val = x * 1.442695041f;
+  val = (val < 126.0f) ? val : 126.0f;   // minps(val, 126): NaN -> 126
+  val = (val > -126.0f) ? val : -126.0f; // maxps(val, -126)
+  const int ip = (int)__builtin_rintf(val);
+  const float fp = val - (float)ip;
+  const float e = __int_as_float((ip + 127) << 23);
+  const float f = fp * 0.6931471806f;
+  float p = __builtin_fmaf(1.0f / 120.0f, f, 1.0f / 24.0f);
+  p = __builtin_fmaf(p, f, 1.0f / 6.0f);
+  p = __builtin_fmaf(p, f, 0.5f);
+  p = __builtin_fmaf(p, f, 1.0f);
+  p = __builtin_fmaf(p, f, 1.0f);
+  return e * p;
+}
+
+QASR_DEV float qnan() { return __int_as_float(0x7fc00000); }
+
+// Round half away from zero, then clamp to int8 (NaN -> 0), the arithmetic of
+// quantize.rs:657-658: `(v * inv).round().clamp(-128, 127) as i8`.
+QASR_DEV int quant_i8(float v, float inv) {
+  float r = roundf(v * inv);
+  r = r < -128.0f ? -128.0f : r;
+  r = r > 127.0f ? 127.0f : r;
+  return (r == r) ? (int)r : 0;
+}
+
+// Number of workgroups for a grid-stride elementwise launch: enough to keep
+// every CU busy with several waves, never more than the work needs.
+inline unsigned grid_for(size_t items, unsigned block, unsigned cap = 256 * 16) {
+  size_t g = (items + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned)g;
+}
+
+// ---------------------------------------------------------------------------
+// C-ABI error plumbing
+// ---------------------------------------------------------------------------
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+// Checks hipGetLastError after a launch and converts it to a status.
+int launch_status(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Largest size any kernel indexes with 64-bit arithmetic; guards products of
+// dimensions against overflow.
+constexpr size_t kMaxElems = (size_t)1 << 40;
+
+inline bool mul_ok(size_t a, size_t b, size_t* out) {
+  if (a != 0 && b > kMaxElems / a) return false;
+  *out = a * b;
+  return true;
+}
+
+}  // namespace qasr
+
+#define QASR_REQUIRE(cond, msg)                                   \
+  do {                                                            \
+    if (!(cond)) return ::qasr::fail(QASR_ERR_INVALID_ARG, msg); \
+  } while (0)

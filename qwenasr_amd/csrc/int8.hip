@@ -1,0 +1,386 @@
+// INT8 path: per-row quantizer, W8A32 linear (drop-in for linear_nobias_int8),
+// gate/up interleave, and the W8A8 gate/up projection fused with SwiGLU.
+//
+// Weight layout is the .qint8 one: int8 row-major [out_dim, in_dim] with one f32
+// scale per output row (quantize.rs:77-84). The fused gate/up matrix has its
+// rows interleaved g0,u0,g1,u1,... (decoder.rs:701-719), so one gate/up pair is
+// 2*in_dim contiguous bytes and its SwiGLU output needs no cross-wave exchange.
+#include "common.hpp"
+
+#include "gemm_w8a8.hpp"
+
+namespace qasr {
+namespace {
+
+QASR_DEV float4 ld4(const float* p, size_t i) { return reinterpret_cast<const float4*>(p)[i]; }
+
+// ---------------------------------------------------------------------------
+// Per-row quantizer, quantize.rs:633-662.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quantize_rows_kernel(int8_t* q, float* scales,
+                                                            const float* x, int cols) {
+  __shared__ float red[256 / kWave];
+  const size_t base = (size_t)blockIdx.x * cols;
+  float m = 0.0f;
+  for (int c = threadIdx.x; c < cols; c += 256) {
+    const float a = fabsf(x[base + c]);
+    if (a > m) m = a;  // NaN never wins, as in `if abs > absmax`
+  }
+  m = block_max<256>(m, red);
+  const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+  if (threadIdx.x == 0) scales[blockIdx.x] = m / 127.0f;
+  for (int c = threadIdx.x; c < cols; c += 256) q[base + c] = (int8_t)quant_i8(x[base + c], inv);
+}
+
+// ---------------------------------------------------------------------------
+// W8A32 linear: y[s,o] = (sum_k (f32)w[o,k] * x[s,k]) * scale[o] (+ bias[o]).
+// One wave per output row; each lane owns 16-byte slices of the row, keeps
+// them in registers and reuses them for every token s.
+// ---------------------------------------------------------------------------
+template <int KCH>  // in_dim / 1024 chunks held in registers (1..8)
+__global__ __launch_bounds__(256) void w8a32_vec_kernel(float* y, const float* x, const int8_t* w,
+                                                        const float* scales, const float* bias,
+                                                        int seq, int in_dim, int out_dim) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int o = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (o >= out_dim) return;
+  const int8_t* wr = w + (size_t)o * in_dim;
+  int4 wv[KCH];
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) wv[c] = reinterpret_cast<const int4*>(wr)[c * kWave + lane];
+  const float sc = scales[o];
+  const float bs = bias ? bias[o] : 0.0f;
+  for (int s = 0; s < seq; ++s) {
+    const float* xs = x + (size_t)s * in_dim;
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int k0 = (c * kWave + lane) * 16;
+      const int wq[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float4 xv = ld4(xs + k0 + 4 * t, 0);
+        acc = __builtin_fmaf((float)(int8_t)(wq[t] & 0xff), xv.x, acc);
+        acc = __builtin_fmaf((float)(int8_t)((wq[t] >> 8) & 0xff), xv.y, acc);
+        acc = __builtin_fmaf((float)(int8_t)((wq[t] >> 16) & 0xff), xv.z, acc);
+        acc = __builtin_fmaf((float)(int8_t)((wq[t] >> 24) & 0xff), xv.w, acc);
+      }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) {
+      float r = acc * sc;
+      if (bias) r += bs;
+      y[(size_t)s * out_dim + o] = r;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void w8a32_scalar_kernel(float* y, const float* x, const int8_t* w,
+                                                           const float* scales, const float* bias,
+                                                           int seq, int in_dim, int out_dim) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int o = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (o >= out_dim) return;
+  const int8_t* wr = w + (size_t)o * in_dim;
+  for (int s = 0; s < seq; ++s) {
+    const float* xs = x + (size_t)s * in_dim;
+    float acc = 0.0f;
+    for (int k = lane; k < in_dim; k += kWave) acc = __builtin_fmaf((float)wr[k], xs[k], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) {
+      float r = acc * scales[o];
+      if (bias) r += bias[o];
+      y[(size_t)s * out_dim + o] = r;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gate/up row interleave (decoder.rs:701-719).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void interleave_kernel(int8_t* wgu, float* sgu, const int8_t* wg,
+                                                         const float* sg, const int8_t* wu,
+                                                         const float* su, size_t inter,
+                                                         size_t hidden) {
+  const size_t n = inter * hidden;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const size_t r = i / hidden, c = i - r * hidden;
+    wgu[(2 * r) * hidden + c] = wg[i];
+    wgu[(2 * r + 1) * hidden + c] = wu[i];
+    if (c == 0) {
+      sgu[2 * r] = sg[r];
+      sgu[2 * r + 1] = su[r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// W8A8 gate/up + SwiGLU, batch 1: a bandwidth-bound matvec.
+//
+// A wave owns NP consecutive gate/up pairs (NP * 2 * in_dim contiguous bytes).
+// Lane l reads 16-byte slices at byte 1024*c + 16*l of each row, so every load
+// instruction of the wave covers 1 KiB contiguous. The lane's matching 16*KCH
+// activation bytes live in registers for the whole kernel. All NP*2*KCH weight
+// loads are issued before the first v_dot4, then the 2*NP int32 sums are
+// reduced across the wave and NP lanes finish the SwiGLU epilogue.
+// ---------------------------------------------------------------------------
+QASR_DEV float swiglu_w8a8(int dg, int du, float xs, float sg, float su) {
+  const float g = ((float)dg * xs) * sg;
+  const float u = ((float)du * xs) * su;
+  return (g / (1.0f + expf(-g))) * u;
+}
+
+QASR_DEV int dot16(v4i a, v4i b, int acc) {
+  acc = __builtin_amdgcn_sdot4(a[0], b[0], acc, false);
+  acc = __builtin_amdgcn_sdot4(a[1], b[1], acc, false);
+  acc = __builtin_amdgcn_sdot4(a[2], b[2], acc, false);
+  acc = __builtin_amdgcn_sdot4(a[3], b[3], acc, false);
+  return acc;
+}
+
+// Quantizes this lane's 16*KCH activations (positions 1024*c + 16*lane + t)
+// with the per-vector absmax of the whole input (wave-wide max), packing them
+// into int8x16 registers; returns the vector's scale.
+template <int KCH>
+QASR_DEV float quantize_lane_slices(const float* x, int lane, v4i* xq) {
+  float v[KCH][16];
+  float m = 0.0f;
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float4 f = ld4(x + c * 1024 + lane * 16 + 4 * t, 0);
+      v[c][4 * t] = f.x; v[c][4 * t + 1] = f.y; v[c][4 * t + 2] = f.z; v[c][4 * t + 3] = f.w;
+    }
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const float a = fabsf(v[c][t]);
+      if (a > m) m = a;
+    }
+  }
+  m = wave_max(m);
+  const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) {
+    int p[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      p[t] = (quant_i8(v[c][4 * t], inv) & 0xff) | ((quant_i8(v[c][4 * t + 1], inv) & 0xff) << 8) |
+             ((quant_i8(v[c][4 * t + 2], inv) & 0xff) << 16) |
+             ((quant_i8(v[c][4 * t + 3], inv) & 0xff) << 24);
+    }
+    xq[c] = v4i{p[0], p[1], p[2], p[3]};
+  }
+  return m / 127.0f;
+}
+
+template <int KCH, int NP, bool F32IN>
+__global__ __launch_bounds__(256) void gateup_matvec_kernel(float* out, const int8_t* w,
+                                                            const float* scales, const int8_t* xq8,
+                                                            const float* xsc, const float* xf,
+                                                            int inter) {
+  constexpr int K = KCH * 1024;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int pair0 = (blockIdx.x * (256 / kWave) + threadIdx.x / kWave) * NP;
+  if (pair0 >= inter) return;
+
+  // Issue the weight stream first: NP pairs x 2 rows x KCH slices.
+  v4i wv[NP][2][KCH];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int pr = pair0 + p < inter ? pair0 + p : inter - 1;  // clamp the tail, result discarded
+    const v4i* row = reinterpret_cast<const v4i*>(w + (size_t)pr * 2 * K);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) wv[p][r][c] = __builtin_nontemporal_load(row + r * (K / 16) + c * kWave + lane);
+  }
+
+  v4i xq[KCH];
+  float xs;
+  if constexpr (F32IN) {
+    xs = quantize_lane_slices<KCH>(xf, lane, xq);
+  } else {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) xq[c] = reinterpret_cast<const v4i*>(xq8)[c * kWave + lane];
+    xs = xsc[0];
+  }
+
+  int acc[NP][2];
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      int a = 0;
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) a = dot16(wv[p][r][c], xq[c], a);
+      acc[p][r] = group_sum_i32<kWave>(a);
+    }
+  if (lane < NP && pair0 + lane < inter) {
+    int dg = acc[0][0], du = acc[0][1];
+#pragma unroll
+    for (int p = 1; p < NP; ++p)
+      if (lane == p) { dg = acc[p][0]; du = acc[p][1]; }
+    const int j = pair0 + lane;
+    out[j] = swiglu_w8a8(dg, du, xs, scales[2 * j], scales[2 * j + 1]);
+  }
+}
+
+// Any in_dim % 16 == 0 (and batch >= 1) without the register budget of the
+// matvec kernel: one wave per (pair, token), weight slices re-read per token.
+__global__ __launch_bounds__(256) void gateup_generic_kernel(float* out, const int8_t* w,
+                                                             const float* scales,
+                                                             const int8_t* xq, const float* xs,
+                                                             int batch, int in_dim, int inter) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long item = (long long)blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (item >= (long long)batch * inter) return;
+  const int b = (int)(item / inter), j = (int)(item % inter);
+  const v4i* g = reinterpret_cast<const v4i*>(w + (size_t)(2 * j) * in_dim);
+  const v4i* u = reinterpret_cast<const v4i*>(w + (size_t)(2 * j + 1) * in_dim);
+  const v4i* xv = reinterpret_cast<const v4i*>(xq + (size_t)b * in_dim);
+  int dg = 0, du = 0;
+  for (int c = lane; c < in_dim / 16; c += kWave) {
+    const v4i xx = xv[c];
+    dg = dot16(g[c], xx, dg);
+    du = dot16(u[c], xx, du);
+  }
+  dg = group_sum_i32<kWave>(dg);
+  du = group_sum_i32<kWave>(du);
+  if (lane == 0) out[(size_t)b * inter + j] = swiglu_w8a8(dg, du, xs[b], scales[2 * j], scales[2 * j + 1]);
+}
+
+constexpr int kMatvecPairs = 6;  // pairs per wave: 24 per 4-wave workgroup
+
+template <bool F32IN>
+int launch_matvec(float* out, const int8_t* w, const float* scales, const int8_t* xq,
+                  const float* xs, const float* xf, size_t in_dim, size_t inter, hipStream_t st) {
+  const unsigned grid =
+      (unsigned)((inter + kMatvecPairs * 4 - 1) / (kMatvecPairs * 4));
+  switch (in_dim / 1024) {
+    case 1: gateup_matvec_kernel<1, kMatvecPairs, F32IN><<<grid, 256, 0, st>>>(out, w, scales, xq, xs, xf, (int)inter); break;
+    case 2: gateup_matvec_kernel<2, kMatvecPairs, F32IN><<<grid, 256, 0, st>>>(out, w, scales, xq, xs, xf, (int)inter); break;
+    case 3: gateup_matvec_kernel<3, kMatvecPairs, F32IN><<<grid, 256, 0, st>>>(out, w, scales, xq, xs, xf, (int)inter); break;
+    case 4: gateup_matvec_kernel<4, 4, F32IN><<<(unsigned)((inter + 15) / 16), 256, 0, st>>>(out, w, scales, xq, xs, xf, (int)inter); break;
+    default: return fail(QASR_ERR_UNSUPPORTED, "gate_up matvec: in_dim must be 1024..4096 in steps of 1024");
+  }
+  return launch_status("gate_up_swiglu_w8a8 (matvec)");
+}
+
+bool matvec_shape(size_t in_dim) { return in_dim % 1024 == 0 && in_dim >= 1024 && in_dim <= 4096; }
+
+}  // namespace
+}  // namespace qasr
+
+using namespace qasr;
+
+extern "C" int qasr_quantize_rows_i8(int8_t* q, float* scales, const float* x, size_t rows,
+                                     size_t cols, void* stream) {
+  if (rows == 0) return QASR_OK;
+  QASR_REQUIRE(q && scales && x, "quantize_rows_i8: null pointer");
+  QASR_REQUIRE(rows <= 0x7fffffffu && cols <= 0x7fffffffu, "quantize_rows_i8: size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(rows, cols, &n), "quantize_rows_i8: rows * cols overflows");
+  quantize_rows_kernel<<<(unsigned)rows, 256, 0, as_stream(stream)>>>(q, scales, x, (int)cols);
+  return launch_status("quantize_rows_i8");
+}
+
+static int launch_w8a32(float* y, const float* x, const int8_t* w, const float* scales,
+                        const float* bias, size_t seq_len, size_t in_dim, size_t out_dim,
+                        void* stream) {
+  if (seq_len == 0 || out_dim == 0) return QASR_OK;
+  QASR_REQUIRE(y && x && w && scales, "linear_int8: null pointer");
+  QASR_REQUIRE(seq_len <= 0x7fffffffu && in_dim <= 0x7fffffffu && out_dim <= 0x7fffffffu,
+               "linear_int8: size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(in_dim, out_dim, &n) && mul_ok(seq_len, in_dim, &n) &&
+                   mul_ok(seq_len, out_dim, &n),
+               "linear_int8: size overflows");
+  hipStream_t st = as_stream(stream);
+  const unsigned grid = (unsigned)((out_dim + 3) / 4);
+  const int s = (int)seq_len, k = (int)in_dim, o = (int)out_dim;
+  const bool vec = in_dim >= 1024 && in_dim % 1024 == 0 && in_dim <= 8192 && aligned16(w) &&
+                   aligned16(x);
+  if (vec) {
+    switch (in_dim / 1024) {
+      case 1: w8a32_vec_kernel<1><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
+      case 2: w8a32_vec_kernel<2><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
+      case 3: w8a32_vec_kernel<3><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
+      case 4: w8a32_vec_kernel<4><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
+      case 5: w8a32_vec_kernel<5><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
+      case 6: w8a32_vec_kernel<6><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
+      case 7: w8a32_vec_kernel<7><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
+      default: w8a32_vec_kernel<8><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
+    }
+  } else {
+    w8a32_scalar_kernel<<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o);
+  }
+  return launch_status("linear_int8");
+}
+
+extern "C" int qasr_linear_nobias_int8_f32(float* y, const float* x, const int8_t* w,
+                                           const float* scales, size_t seq_len, size_t in_dim,
+                                           size_t out_dim, void* stream) {
+  return launch_w8a32(y, x, w, scales, nullptr, seq_len, in_dim, out_dim, stream);
+}
+
+extern "C" int qasr_linear_int8_f32(float* y, const float* x, const int8_t* w, const float* scales,
+                                    const float* bias, size_t seq_len, size_t in_dim,
+                                    size_t out_dim, void* stream) {
+  return launch_w8a32(y, x, w, scales, bias, seq_len, in_dim, out_dim, stream);
+}
+
+extern "C" int qasr_interleave_gate_up_i8(int8_t* w_gate_up, float* scales_gate_up,
+                                          const int8_t* w_gate, const float* s_gate,
+                                          const int8_t* w_up, const float* s_up,
+                                          size_t intermediate, size_t hidden, void* stream) {
+  if (intermediate == 0 || hidden == 0) return QASR_OK;
+  QASR_REQUIRE(w_gate_up && scales_gate_up && w_gate && s_gate && w_up && s_up,
+               "interleave_gate_up_i8: null pointer");
+  size_t n;
+  QASR_REQUIRE(mul_ok(2 * intermediate, hidden, &n), "interleave_gate_up_i8: size overflows");
+  interleave_kernel<<<grid_for(intermediate * hidden, 256), 256, 0, as_stream(stream)>>>(
+      w_gate_up, scales_gate_up, w_gate, s_gate, w_up, s_up, intermediate, hidden);
+  return launch_status("interleave_gate_up_i8");
+}
+
+extern "C" int qasr_gate_up_swiglu_w8a8(float* out, const int8_t* w, const float* scales,
+                                        const int8_t* xq, const float* x_scales, size_t batch,
+                                        size_t in_dim, size_t intermediate, void* stream) {
+  if (batch == 0 || intermediate == 0) return QASR_OK;
+  QASR_REQUIRE(out && w && scales && xq && x_scales, "gate_up_swiglu_w8a8: null pointer");
+  QASR_REQUIRE(in_dim > 0 && in_dim % 16 == 0, "gate_up_swiglu_w8a8: in_dim must be a positive multiple of 16");
+  QASR_REQUIRE(aligned16(w) && aligned16(xq), "gate_up_swiglu_w8a8: w and xq must be 16-byte aligned");
+  QASR_REQUIRE(batch <= 0x7fffffffu && intermediate <= 0x3fffffffu && in_dim <= 0x7fffffffu,
+               "gate_up_swiglu_w8a8: size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(2 * intermediate, in_dim, &n) && mul_ok(batch, in_dim, &n) &&
+                   mul_ok(batch, intermediate, &n),
+               "gate_up_swiglu_w8a8: size overflows");
+  hipStream_t st = as_stream(stream);
+  if (batch == 1 && matvec_shape(in_dim)) {
+    return launch_matvec<false>(out, w, scales, xq, x_scales, nullptr, in_dim, intermediate, st);
+  }
+  if (batch > 1 && gemm_w8a8_supported(batch, in_dim, intermediate)) {
+    return gemm_w8a8_swiglu(out, w, scales, xq, x_scales, batch, in_dim, intermediate, st);
+  }
+  const long long items = (long long)batch * (long long)intermediate;
+  gateup_generic_kernel<<<(unsigned)((items + 3) / 4), 256, 0, st>>>(
+      out, w, scales, xq, x_scales, (int)batch, (int)in_dim, (int)intermediate);
+  return launch_status("gate_up_swiglu_w8a8 (generic)");
+}
+
+extern "C" int qasr_gate_up_swiglu_w8a8_f32in(float* out, const int8_t* w, const float* scales,
+                                              const float* x, size_t in_dim, size_t intermediate,
+                                              void* stream) {
+  if (intermediate == 0) return QASR_OK;
+  QASR_REQUIRE(out && w && scales && x, "gate_up_swiglu_w8a8_f32in: null pointer");
+  QASR_REQUIRE(aligned16(w) && aligned16(x), "gate_up_swiglu_w8a8_f32in: w and x must be 16-byte aligned");
+  QASR_REQUIRE(intermediate <= 0x3fffffffu, "gate_up_swiglu_w8a8_f32in: size too large");
+  if (!matvec_shape(in_dim)) {
+    return fail(QASR_ERR_UNSUPPORTED,
+                "gate_up_swiglu_w8a8_f32in: in_dim must be 1024..4096 in steps of 1024");
+  }
+  return launch_matvec<true>(out, w, scales, nullptr, nullptr, x, in_dim, intermediate,
+                             as_stream(stream));
+}

@@ -1,0 +1,304 @@
+// Per-head q/k RMSNorm, NeoX RoPE, their fusion, and RoPE table fill.
+//
+// Layout: q [seq, n_heads, head_dim], k [seq, n_kv_heads, head_dim], fp32,
+// row-major. RoPE tables are RopeCache rows [pos, head_dim] with duplicated
+// halves ([c(0..half) | c(0..half)]), built by rope_table_kernel.
+//
+// Vector path (head_dim in {64,128,256,512}): L = head_dim/8 lanes own one head;
+// lane j of a head holds elements [4j, 4j+4) and [half+4j, half+4j+4) as two
+// float4, which are exactly the NeoX rotation partners. A wave covers 64/L
+// heads (4 heads at head_dim 128) and a head's sum of squares is a log2(L)-step
+// shuffle reduction inside its lane group; no LDS and no barrier.
+#include "common.hpp"
+
+namespace qasr {
+namespace {
+
+QASR_DEV float4 ld4(const float* p, size_t i) { return reinterpret_cast<const float4*>(p)[i]; }
+QASR_DEV void st4(float* p, size_t i, float4 v) { reinterpret_cast<float4*>(p)[i] = v; }
+
+struct HeadArgs {
+  float* q;
+  float* k;
+  const float* qw;
+  const float* kw;
+  const float* cos_tab;
+  const float* sin_tab;
+  const int32_t* positions;
+  long long q_heads;      // seq * n_heads
+  long long total_heads;  // seq * (n_heads + n_kv_heads)
+  int nq;
+  int nk;
+  long long table_rows;
+  float eps;
+};
+
+// Resolves global head index gh to its base pointer, norm weight and row.
+QASR_DEV void head_of(const HeadArgs& a, long long gh, int hd, float** base, const float** w,
+                      long long* row) {
+  if (gh < a.q_heads) {
+    *base = a.q + gh * hd;
+    *w = a.qw;
+    *row = gh / a.nq;
+  } else {
+    const long long g = gh - a.q_heads;
+    *base = a.k + g * hd;
+    *w = a.kw;
+    *row = g / a.nk;
+  }
+}
+
+template <int HD, bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
+  constexpr int L = HD / 8;
+  constexpr int HPW = kWave / L;
+  constexpr int HALF = HD / 2;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int sub = lane & (L - 1);
+  const long long gh =
+      ((long long)blockIdx.x * (256 / kWave) + threadIdx.x / kWave) * HPW + lane / L;
+  if (gh >= a.total_heads) return;  // whole lane groups leave together
+  float* base;
+  const float* w;
+  long long row;
+  head_of(a, gh, HD, &base, &w, &row);
+
+  float4 x1 = ld4(base, sub);
+  float4 x2 = ld4(base + HALF, sub);
+  if constexpr (NORM) {
+    // kernels/mod.rs:927-932: rms_inv = 1/sqrt(sum(v^2)/head_dim + eps); v = v*rms_inv*w
+    float ss = x1.x * x1.x;
+    ss += x1.y * x1.y;
+    ss += x1.z * x1.z;
+    ss += x1.w * x1.w;
+    ss += x2.x * x2.x;
+    ss += x2.y * x2.y;
+    ss += x2.z * x2.z;
+    ss += x2.w * x2.w;
+    ss = group_sum<L>(ss);
+    const float rinv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+    const float4 w1 = ld4(w, sub);
+    const float4 w2 = ld4(w + HALF, sub);
+    x1.x = (x1.x * rinv) * w1.x; x1.y = (x1.y * rinv) * w1.y;
+    x1.z = (x1.z * rinv) * w1.z; x1.w = (x1.w * rinv) * w1.w;
+    x2.x = (x2.x * rinv) * w2.x; x2.y = (x2.y * rinv) * w2.y;
+    x2.z = (x2.z * rinv) * w2.z; x2.w = (x2.w * rinv) * w2.w;
+  }
+  if constexpr (ROPE) {
+    const long long pos = a.positions ? (long long)a.positions[row] : row;
+    if (pos < 0 || pos >= a.table_rows) {
+      const float n = qnan();
+      x1 = make_float4(n, n, n, n);
+      x2 = x1;
+    } else {
+      // kernels/mod.rs:1262-1263: v[d] = x1*c[d] + (-x2)*s[d]; v[d+h] = x2*c[d+h] + x1*s[d+h]
+      const float* cr = a.cos_tab + pos * HD;
+      const float* sr = a.sin_tab + pos * HD;
+      const float4 c1 = ld4(cr, sub), c2 = ld4(cr + HALF, sub);
+      const float4 s1 = ld4(sr, sub), s2 = ld4(sr + HALF, sub);
+      float4 o1, o2;
+      o1.x = x1.x * c1.x + (-x2.x) * s1.x; o2.x = x2.x * c2.x + x1.x * s2.x;
+      o1.y = x1.y * c1.y + (-x2.y) * s1.y; o2.y = x2.y * c2.y + x1.y * s2.y;
+      o1.z = x1.z * c1.z + (-x2.z) * s1.z; o2.z = x2.z * c2.z + x1.z * s2.z;
+      o1.w = x1.w * c1.w + (-x2.w) * s1.w; o2.w = x2.w * c2.w + x1.w * s2.w;
+      x1 = o1;
+      x2 = o2;
+    }
+  }
+  st4(base, sub, x1);
+  st4(base + HALF, sub, x2);
+}
+
+// Any head_dim (even when ROPE), any alignment: one wave per head.
+template <bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void head_scalar_kernel(HeadArgs a, int hd) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long gh = (long long)blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (gh >= a.total_heads) return;
+  float* base;
+  const float* w;
+  long long row;
+  head_of(a, gh, hd, &base, &w, &row);
+  float rinv = 1.0f;
+  if constexpr (NORM) {
+    float ss = 0.0f;
+    for (int d = lane; d < hd; d += kWave) ss += base[d] * base[d];
+    ss = wave_sum(ss);
+    rinv = 1.0f / sqrtf(ss / (float)hd + a.eps);
+  }
+  if constexpr (ROPE) {
+    const int half = hd / 2;
+    const long long pos = a.positions ? (long long)a.positions[row] : row;
+    const bool bad = pos < 0 || pos >= a.table_rows;
+    const float* cr = a.cos_tab + (bad ? 0 : pos) * hd;
+    const float* sr = a.sin_tab + (bad ? 0 : pos) * hd;
+    for (int d = lane; d < half; d += kWave) {
+      float v1 = base[d], v2 = base[d + half];
+      if constexpr (NORM) {
+        v1 = (v1 * rinv) * w[d];
+        v2 = (v2 * rinv) * w[d + half];
+      }
+      if (bad) {
+        base[d] = qnan();
+        base[d + half] = qnan();
+      } else {
+        base[d] = v1 * cr[d] + (-v2) * sr[d];
+        base[d + half] = v2 * cr[d + half] + v1 * sr[d + half];
+      }
+    }
+  } else {
+    for (int d = lane; d < hd; d += kWave) base[d] = (base[d] * rinv) * w[d];
+  }
+}
+
+template <bool NORM, bool ROPE>
+int launch_heads(const HeadArgs& a, int hd, hipStream_t st) {
+  const bool vec = (hd == 64 || hd == 128 || hd == 256 || hd == 512) && aligned16(a.q) &&
+                   (a.total_heads == a.q_heads || aligned16(a.k)) &&
+                   (!NORM || (aligned16(a.qw) && (a.total_heads == a.q_heads || aligned16(a.kw)))) &&
+                   (!ROPE || (aligned16(a.cos_tab) && aligned16(a.sin_tab)));
+  if (vec) {
+    const long long hpw = kWave / (hd / 8);
+    const long long heads_per_block = hpw * (256 / kWave);
+    const unsigned grid = (unsigned)((a.total_heads + heads_per_block - 1) / heads_per_block);
+    switch (hd) {
+      case 64: head_vec_kernel<64, NORM, ROPE><<<grid, 256, 0, st>>>(a); break;
+      case 128: head_vec_kernel<128, NORM, ROPE><<<grid, 256, 0, st>>>(a); break;
+      case 256: head_vec_kernel<256, NORM, ROPE><<<grid, 256, 0, st>>>(a); break;
+      default: head_vec_kernel<512, NORM, ROPE><<<grid, 256, 0, st>>>(a); break;
+    }
+  } else {
+    const unsigned grid = (unsigned)((a.total_heads + 3) / 4);
+    head_scalar_kernel<NORM, ROPE><<<grid, 256, 0, st>>>(a, hd);
+  }
+  return launch_status(NORM ? (ROPE ? "head_rms_norm_rope" : "rms_norm_per_head")
+                            : "apply_rope_neox");
+}
+
+int check_heads(size_t seq, size_t nh, size_t nk, size_t hd, bool rope) {
+  QASR_REQUIRE(hd > 0 && hd <= 65536, "head_dim must be in [1, 65536]");
+  QASR_REQUIRE(!rope || hd % 2 == 0, "RoPE needs an even head_dim");
+  QASR_REQUIRE(nh <= 65536 && nk <= 65536, "head count too large");
+  size_t heads, n;
+  QASR_REQUIRE(mul_ok(seq, nh + nk, &heads), "seq * heads overflows");
+  QASR_REQUIRE(mul_ok(heads, hd, &n), "seq * heads * head_dim overflows");
+  QASR_REQUIRE(heads / 4 < 0x7fffffffu, "too many heads for one launch");
+  return QASR_OK;
+}
+
+// RoPE table rows [pos_begin, pos_end). inv_freq comes from the host by value.
+struct InvFreq {
+  float v[256];
+};
+
+__global__ __launch_bounds__(256) void rope_table_kernel(float* cos_tab, float* sin_tab,
+                                                         long long pos_begin, long long n_items,
+                                                         int hd, InvFreq inv) {
+  const int half = hd / 2;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n_items;
+       i += (long long)gridDim.x * 256) {
+    const long long p = pos_begin + i / half;
+    const int d = (int)(i % half);
+    // decoder.rs:279-285: angle = (pos as f32) * inv_freq[d] in f32; cos/sin of
+    // that f32 angle, here evaluated in double and rounded once.
+    const float angle = (float)p * inv.v[d];
+    const float c = (float)cos((double)angle);
+    const float s = (float)sin((double)angle);
+    cos_tab[p * hd + d] = c;
+    cos_tab[p * hd + half + d] = c;
+    sin_tab[p * hd + d] = s;
+    sin_tab[p * hd + half + d] = s;
+  }
+}
+
+}  // namespace
+}  // namespace qasr
+
+using namespace qasr;
+
+extern "C" int qasr_rms_norm_per_head_f32(float* x, const float* weight, size_t seq_len,
+                                          size_t n_heads, size_t head_dim, float eps,
+                                          void* stream) {
+  if (seq_len == 0 || n_heads == 0 || head_dim == 0) return QASR_OK;
+  QASR_REQUIRE(x && weight, "rms_norm_per_head: null pointer");
+  int rc = check_heads(seq_len, n_heads, 0, head_dim, false);
+  if (rc) return rc;
+  HeadArgs a{};
+  a.q = x;
+  a.qw = weight;
+  a.q_heads = (long long)(seq_len * n_heads);
+  a.total_heads = a.q_heads;
+  a.nq = (int)n_heads;
+  a.nk = 1;
+  a.eps = eps;
+  return launch_heads<true, false>(a, (int)head_dim, as_stream(stream));
+}
+
+extern "C" int qasr_apply_rope_neox_f32(float* x, const float* cos_vals, const float* sin_vals,
+                                        size_t seq, size_t n_heads, size_t head_dim,
+                                        void* stream) {
+  if (seq == 0 || n_heads == 0 || head_dim == 0) return QASR_OK;
+  QASR_REQUIRE(x && cos_vals && sin_vals, "apply_rope_neox: null pointer");
+  int rc = check_heads(seq, n_heads, 0, head_dim, true);
+  if (rc) return rc;
+  HeadArgs a{};
+  a.q = x;
+  a.cos_tab = cos_vals;
+  a.sin_tab = sin_vals;
+  a.positions = nullptr;
+  a.q_heads = (long long)(seq * n_heads);
+  a.total_heads = a.q_heads;
+  a.nq = (int)n_heads;
+  a.nk = 1;
+  a.table_rows = (long long)seq;
+  return launch_heads<false, true>(a, (int)head_dim, as_stream(stream));
+}
+
+extern "C" int qasr_head_rms_norm_rope_f32(float* q, float* k, const float* q_norm_w,
+                                           const float* k_norm_w, const float* cos_tab,
+                                           const float* sin_tab, const int32_t* positions,
+                                           size_t seq, size_t n_heads, size_t n_kv_heads,
+                                           size_t head_dim, size_t table_rows, float eps,
+                                           void* stream) {
+  if (seq == 0 || head_dim == 0 || n_heads + n_kv_heads == 0) return QASR_OK;
+  QASR_REQUIRE(cos_tab && sin_tab, "head_rms_norm_rope: null table");
+  QASR_REQUIRE(n_heads == 0 || (q && q_norm_w), "head_rms_norm_rope: null q");
+  QASR_REQUIRE(n_kv_heads == 0 || (k && k_norm_w), "head_rms_norm_rope: null k");
+  int rc = check_heads(seq, n_heads, n_kv_heads, head_dim, true);
+  if (rc) return rc;
+  HeadArgs a{};
+  a.q = q;
+  a.k = k;
+  a.qw = q_norm_w;
+  a.kw = k_norm_w;
+  a.cos_tab = cos_tab;
+  a.sin_tab = sin_tab;
+  a.positions = positions;
+  a.q_heads = (long long)(seq * n_heads);
+  a.total_heads = (long long)(seq * (n_heads + n_kv_heads));
+  a.nq = n_heads ? (int)n_heads : 1;
+  a.nk = n_kv_heads ? (int)n_kv_heads : 1;
+  a.table_rows = (long long)table_rows;
+  a.eps = eps;
+  return launch_heads<true, true>(a, (int)head_dim, as_stream(stream));
+}
+
+extern "C" int qasr_rope_table_fill_f32(float* cos_tab, float* sin_tab, size_t pos_begin,
+                                        size_t pos_end, size_t head_dim, float theta,
+                                        void* stream) {
+  if (pos_end <= pos_begin) return QASR_OK;
+  QASR_REQUIRE(cos_tab && sin_tab, "rope_table_fill: null pointer");
+  QASR_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 512,
+               "rope_table_fill: head_dim must be even and <= 512");
+  QASR_REQUIRE(pos_end <= ((size_t)1 << 24), "rope_table_fill: positions must be < 2^24");
+  // RopeCache::ensure (decoder.rs:262-266): inv_freq[d] = 1 / theta.powf((2d) as f32 / hd as f32)
+  InvFreq inv{};
+  const int half = (int)head_dim / 2;
+  for (int d = 0; d < half; ++d) {
+    inv.v[d] = 1.0f / powf(theta, (float)(2 * d) / (float)head_dim);
+  }
+  const long long items = (long long)(pos_end - pos_begin) * half;
+  rope_table_kernel<<<grid_for((size_t)items, 256), 256, 0, as_stream(stream)>>>(
+      cos_tab, sin_tab, (long long)pos_begin, items, (int)head_dim, inv);
+  return launch_status("rope_table_fill");
+}

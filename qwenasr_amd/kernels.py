@@ -1,0 +1,394 @@
+"""Host mirror of ``qwen_asr::kernels`` over device memory.
+
+Every function keeps the reference's name, argument order and meaning
+(crates/qwen-asr/src/kernels/mod.rs and decoder.rs), with Rust slices replaced
+by device-resident ``torch`` tensors (torch supplies device memory and the
+current HIP stream; all arithmetic runs in the gfx950 kernels of
+``libqasr_hip.so`` through the C-ABI of include/qasr.h).
+
+Error behaviour mirrors the reference: where the Rust code would panic on a
+slice that is too short, these raise ``IndexError`` before anything is
+launched; a wrong dtype/device raises ``TypeError``; a status returned by the
+C-ABI raises ``QasrError``.
+
+Calls only enqueue work on the current stream; nothing here synchronises.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import QasrError  # noqa: F401  (re-export)
+
+__all__ = [
+    "add_inplace", "rms_norm", "add_rms_norm", "rms_norm_per_head", "apply_rope_neox",
+    "head_rms_norm_rope", "swiglu_multiply", "swiglu_multiply_inplace", "swiglu_split", "silu",
+    "gelu", "gelu_erf", "layer_norm", "sinusoidal_pe", "pe_add", "tok_embed_f32_to_f32",
+    "tok_embed_bf16_to_f32", "tok_embed_int8_to_f32", "embed_gather_f32", "embed_gather_bf16",
+    "embed_gather_i8", "quantize_f32_to_int8", "quantize_rows_i8", "linear_nobias_int8",
+    "linear_int8", "interleave_gate_up", "gate_up_swiglu_w8a8", "gate_up_swiglu_w8a8_f32in",
+    "RopeCache", "QuantWeight",
+]
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(t: torch.Tensor, dtype: torch.dtype, n: int, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise TypeError(f"{name}: must be a device tensor (got {t.device})")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if t.numel() < n:
+        raise IndexError(f"{name}: range end index {n} out of range for slice of length {t.numel()}")
+
+
+F32, I8, I32, U16 = torch.float32, torch.int8, torch.int32, torch.int16
+
+
+# ---------------------------------------------------------------------------
+# Basic / normalisation (kernels/mod.rs)
+# ---------------------------------------------------------------------------
+def add_inplace(a: torch.Tensor, b: torch.Tensor, n: int) -> None:
+    """``a[i] += b[i]`` for i < n (kernels/mod.rs:486-488)."""
+    _need(a, F32, n, "a")
+    _need(b, F32, n, "b")
+    _lib.call("qasr_add_inplace_f32", _ptr(a), _ptr(b), n, _stream())
+
+
+def rms_norm(out, x, weight, seq_len: int, hidden: int, eps: float) -> None:
+    """Row RMSNorm (kernels/mod.rs:897-918)."""
+    _need(out, F32, seq_len * hidden, "out")
+    _need(x, F32, seq_len * hidden, "x")
+    _need(weight, F32, hidden, "weight")
+    _lib.call("qasr_rms_norm_f32", _ptr(out), _ptr(x), _ptr(weight), seq_len, hidden, eps, _stream())
+
+
+def add_rms_norm(x, delta, weight, out, seq_len: int, hidden: int, eps: float) -> None:
+    """Fused ``add_inplace(x, delta)`` + ``rms_norm(out, x)`` (decoder.rs:908+910)."""
+    n = seq_len * hidden
+    _need(x, F32, n, "x")
+    _need(delta, F32, n, "delta")
+    _need(weight, F32, hidden, "weight")
+    _need(out, F32, n, "out")
+    _lib.call("qasr_add_rms_norm_f32", _ptr(x), _ptr(delta), _ptr(weight), _ptr(out), seq_len,
+              hidden, eps, _stream())
+
+
+def layer_norm(out, x, weight, bias, seq_len: int, hidden: int, eps: float) -> None:
+    """Row LayerNorm (kernels/mod.rs:866-895)."""
+    _need(out, F32, seq_len * hidden, "out")
+    _need(x, F32, seq_len * hidden, "x")
+    _need(weight, F32, hidden, "weight")
+    _need(bias, F32, hidden, "bias")
+    _lib.call("qasr_layer_norm_f32", _ptr(out), _ptr(x), _ptr(weight), _ptr(bias), seq_len,
+              hidden, eps, _stream())
+
+
+def rms_norm_per_head(x, weight, seq_len: int, n_heads: int, head_dim: int, eps: float) -> None:
+    """In-place per-head RMSNorm (kernels/mod.rs:920-935)."""
+    _need(x, F32, seq_len * n_heads * head_dim, "x")
+    _need(weight, F32, head_dim, "weight")
+    _lib.call("qasr_rms_norm_per_head_f32", _ptr(x), _ptr(weight), seq_len, n_heads, head_dim,
+              eps, _stream())
+
+
+def apply_rope_neox(x, cos_vals, sin_vals, seq: int, n_heads: int, head_dim: int) -> None:
+    """In-place NeoX RoPE, row s uses cos/sin row s (kernels/mod.rs:1247-1267)."""
+    _need(x, F32, seq * n_heads * head_dim, "x")
+    _need(cos_vals, F32, seq * head_dim, "cos_vals")
+    _need(sin_vals, F32, seq * head_dim, "sin_vals")
+    _lib.call("qasr_apply_rope_neox_f32", _ptr(x), _ptr(cos_vals), _ptr(sin_vals), seq, n_heads,
+              head_dim, _stream())
+
+
+def head_rms_norm_rope(q, k, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, seq: int,
+                       n_heads: int, n_kv_heads: int, head_dim: int, eps: float) -> None:
+    """Fused q/k head RMSNorm + RoPE at per-row positions (decoder.rs:888-892).
+
+    ``positions`` is an int32 device tensor of ``seq`` entries or None (row s at
+    position s). ``cos_tab``/``sin_tab`` are RopeCache tables; a position outside
+    the table poisons that row with NaN.
+    """
+    if n_heads:
+        _need(q, F32, seq * n_heads * head_dim, "q")
+        _need(q_norm_w, F32, head_dim, "q_norm_w")
+    if n_kv_heads:
+        _need(k, F32, seq * n_kv_heads * head_dim, "k")
+        _need(k_norm_w, F32, head_dim, "k_norm_w")
+    _need(cos_tab, F32, head_dim, "cos_tab")
+    _need(sin_tab, F32, cos_tab.numel(), "sin_tab")
+    if positions is not None:
+        _need(positions, I32, seq, "positions")
+    rows = cos_tab.numel() // head_dim
+    _lib.call("qasr_head_rms_norm_rope_f32", _ptr(q if n_heads else None),
+              _ptr(k if n_kv_heads else None), _ptr(q_norm_w if n_heads else None),
+              _ptr(k_norm_w if n_kv_heads else None), _ptr(cos_tab), _ptr(sin_tab),
+              _ptr(positions), seq, n_heads, n_kv_heads, head_dim, rows, eps, _stream())
+
+
+class RopeCache:
+    """Device RoPE table with the reference's growth rule (decoder.rs:234-306).
+
+    ``ensure(required_pos, head_dim, theta)`` grows capacity by doubling from
+    1024; new rows are filled on the GPU from the f32 inverse frequencies
+    ``1/theta^(2d/head_dim)`` (computed on the host by the library, as the
+    reference does). A change of head_dim rebuilds the table from row 0.
+    """
+
+    def __init__(self, device: str | torch.device = "cuda"):
+        self.device = torch.device(device)
+        self.cos = torch.empty(0, dtype=F32, device=self.device)
+        self.sin = torch.empty(0, dtype=F32, device=self.device)
+        self.cap = 0
+        self.head_dim = 0
+        self.theta = None
+
+    def ensure(self, required_pos: int, head_dim: int, theta: float) -> None:
+        if self.head_dim != head_dim or self.theta != theta:
+            self.cap = 0
+            self.head_dim = head_dim
+            self.theta = theta
+            self.cos = torch.empty(0, dtype=F32, device=self.device)
+            self.sin = torch.empty(0, dtype=F32, device=self.device)
+        if required_pos <= self.cap:
+            return
+        new_cap = self.cap if self.cap > 0 else 1024
+        while new_cap < required_pos:
+            new_cap *= 2
+        cos = torch.empty(new_cap * head_dim, dtype=F32, device=self.device)
+        sin = torch.empty(new_cap * head_dim, dtype=F32, device=self.device)
+        if self.cap:
+            cos[: self.cap * head_dim].copy_(self.cos)
+            sin[: self.cap * head_dim].copy_(self.sin)
+        _lib.call("qasr_rope_table_fill_f32", _ptr(cos), _ptr(sin), self.cap, new_cap, head_dim,
+                  theta, _stream())
+        self.cos, self.sin, self.cap = cos, sin, new_cap
+
+    def cos_at(self, pos: int) -> torch.Tensor:
+        return self.cos[pos * self.head_dim:(pos + 1) * self.head_dim]
+
+    def sin_at(self, pos: int) -> torch.Tensor:
+        return self.sin[pos * self.head_dim:(pos + 1) * self.head_dim]
+
+    def cos_range(self, start: int, length: int) -> torch.Tensor:
+        return self.cos[start * self.head_dim:(start + length) * self.head_dim]
+
+    def sin_range(self, start: int, length: int) -> torch.Tensor:
+        return self.sin[start * self.head_dim:(start + length) * self.head_dim]
+
+
+# ---------------------------------------------------------------------------
+# Activations
+# ---------------------------------------------------------------------------
+def swiglu_multiply(out, gate_up, seq_len: int, intermediate: int) -> None:
+    """SwiGLU on the row-interleaved gate/up buffer (kernels/mod.rs:965-985)."""
+    _need(out, F32, seq_len * intermediate, "out")
+    _need(gate_up, F32, seq_len * 2 * intermediate, "gate_up")
+    _lib.call("qasr_swiglu_multiply_f32", _ptr(out), _ptr(gate_up), seq_len, intermediate,
+              _stream())
+
+
+def swiglu_multiply_inplace(gate, up) -> None:
+    """``gate = silu(gate) * up`` (kernels/mod.rs:988-994)."""
+    n = gate.numel()
+    _need(gate, F32, n, "gate")
+    _need(up, F32, n, "up")
+    _lib.call("qasr_swiglu_split_f32", _ptr(gate), _ptr(gate), _ptr(up), n, _stream())
+
+
+def swiglu_split(out, gate, up, n: int) -> None:
+    """``out = silu(gate) * up`` on split buffers (decode SwiGLU, decoder.rs:916-921)."""
+    _need(out, F32, n, "out")
+    _need(gate, F32, n, "gate")
+    _need(up, F32, n, "up")
+    _lib.call("qasr_swiglu_split_f32", _ptr(out), _ptr(gate), _ptr(up), n, _stream())
+
+
+def silu(x, n: int) -> None:
+    """In-place SiLU (kernels/mod.rs:941-946)."""
+    _need(x, F32, n, "x")
+    _lib.call("qasr_silu_f32", _ptr(x), n, _stream())
+
+
+def gelu(x, n: int) -> None:
+    """In-place tanh-approximation GELU, reference arithmetic (kernels/mod.rs:948-963)."""
+    _need(x, F32, n, "x")
+    _lib.call("qasr_gelu_tanh_f32", _ptr(x), n, _stream())
+
+
+def gelu_erf(x, n: int) -> None:
+    """In-place exact GELU 0.5*x*(1+erf(x/sqrt(2)))."""
+    _need(x, F32, n, "x")
+    _lib.call("qasr_gelu_erf_f32", _ptr(x), n, _stream())
+
+
+# ---------------------------------------------------------------------------
+# Position embeddings (encoder)
+# ---------------------------------------------------------------------------
+def sinusoidal_pe(pe, n_pos: int, d_model: int) -> None:
+    """Sinusoidal PE table [n_pos, d_model] (kernels/mod.rs:1213-1226)."""
+    _need(pe, F32, n_pos * d_model, "pe")
+    _lib.call("qasr_sinusoidal_pe_f32", _ptr(pe), n_pos, d_model, _stream())
+
+
+def pe_add(x, pe, rows: int, d_model: int, n_pos: int) -> None:
+    """``x[r] += pe[r % n_pos]`` (encoder.rs:340-343 with the table reused)."""
+    _need(x, F32, rows * d_model, "x")
+    _need(pe, F32, n_pos * d_model, "pe")
+    _lib.call("qasr_pe_add_f32", _ptr(x), _ptr(pe), rows, d_model, n_pos, _stream())
+
+
+# ---------------------------------------------------------------------------
+# Token embeddings (decoder.rs:631-646)
+# ---------------------------------------------------------------------------
+@dataclass
+class QuantWeight:
+    """Device view of a .qint8 weight (quantize.rs:77-84): int8 [out_dim, in_dim] + f32 scales."""
+
+    data: torch.Tensor
+    scales: torch.Tensor
+    out_dim: int
+    in_dim: int
+
+
+def _ids(ids) -> torch.Tensor:
+    return ids
+
+
+def embed_gather_f32(out, table, ids, n: int, dim: int) -> None:
+    _need(out, F32, n * dim, "out")
+    _need(table, F32, dim, "table")
+    _need(ids, I32, n, "ids")
+    _lib.call("qasr_embed_gather_f32", _ptr(out), _ptr(table), _ptr(ids), n, dim,
+              table.numel() // dim, _stream())
+
+
+def embed_gather_bf16(out, table, ids, n: int, dim: int) -> None:
+    """Batched tok_embed_bf16_to_f32; ``table`` holds bf16 bits as int16 or bfloat16."""
+    _need(out, F32, n * dim, "out")
+    if table.dtype == torch.bfloat16:
+        table = table.view(U16)
+    _need(table, U16, dim, "table")
+    _need(ids, I32, n, "ids")
+    _lib.call("qasr_embed_gather_bf16", _ptr(out), _ptr(table), _ptr(ids), n, dim,
+              table.numel() // dim, _stream())
+
+
+def embed_gather_i8(out, w: QuantWeight, ids, n: int, dim: int) -> None:
+    """Batched tok_embed_int8_to_f32."""
+    _need(out, F32, n * dim, "out")
+    _need(w.data, I8, w.out_dim * dim, "w.data")
+    _need(w.scales, F32, w.out_dim, "w.scales")
+    _need(ids, I32, n, "ids")
+    _lib.call("qasr_embed_gather_i8", _ptr(out), _ptr(w.data), _ptr(w.scales), _ptr(ids), n, dim,
+              w.out_dim, _stream())
+
+
+def _one_id(token_id: int, device) -> torch.Tensor:
+    return torch.tensor([token_id], dtype=I32, device=device)
+
+
+def tok_embed_f32_to_f32(dst, table, token_id: int, dim: int) -> None:
+    embed_gather_f32(dst, table, _one_id(token_id, dst.device), 1, dim)
+
+
+def tok_embed_bf16_to_f32(dst, tok_emb_bf16, token_id: int, dim: int) -> None:
+    """One token (decoder.rs:631-636)."""
+    embed_gather_bf16(dst, tok_emb_bf16, _one_id(token_id, dst.device), 1, dim)
+
+
+def tok_embed_int8_to_f32(dst, w: QuantWeight, token_id: int, dim: int) -> None:
+    """One token (decoder.rs:639-646)."""
+    embed_gather_i8(dst, w, _one_id(token_id, dst.device), 1, dim)
+
+
+# ---------------------------------------------------------------------------
+# INT8
+# ---------------------------------------------------------------------------
+def quantize_rows_i8(q, scales, x, rows: int, cols: int) -> None:
+    """Per-row int8 quantization into caller buffers (quantize.rs:633-662)."""
+    _need(q, I8, rows * cols, "q")
+    _need(scales, F32, rows, "scales")
+    _need(x, F32, rows * cols, "x")
+    _lib.call("qasr_quantize_rows_i8", _ptr(q), _ptr(scales), _ptr(x), rows, cols, _stream())
+
+
+def quantize_f32_to_int8(f32_data, out_dim: int, in_dim: int):
+    """Returns ``(int8 data, f32 scales)`` like quantize.rs:633-662 (device tensors)."""
+    q = torch.empty(out_dim * in_dim, dtype=I8, device=f32_data.device)
+    s = torch.empty(out_dim, dtype=F32, device=f32_data.device)
+    quantize_rows_i8(q, s, f32_data, out_dim, in_dim)
+    return q, s
+
+
+def linear_nobias_int8(y, x, w_int8, scales, seq_len: int, in_dim: int, out_dim: int) -> None:
+    """W8A32 ``y = scale * (W_int8 @ x)`` (kernels/mod.rs:650-661)."""
+    _need(y, F32, seq_len * out_dim, "y")
+    _need(x, F32, seq_len * in_dim, "x")
+    _need(w_int8, I8, out_dim * in_dim, "w_int8")
+    _need(scales, F32, out_dim, "scales")
+    _lib.call("qasr_linear_nobias_int8_f32", _ptr(y), _ptr(x), _ptr(w_int8), _ptr(scales),
+              seq_len, in_dim, out_dim, _stream())
+
+
+def linear_int8(y, x, w_int8, scales, bias, seq_len: int, in_dim: int, out_dim: int) -> None:
+    """W8A32 linear with optional bias (kernels/mod.rs:664-673)."""
+    _need(y, F32, seq_len * out_dim, "y")
+    _need(x, F32, seq_len * in_dim, "x")
+    _need(w_int8, I8, out_dim * in_dim, "w_int8")
+    _need(scales, F32, out_dim, "scales")
+    if bias is not None:
+        _need(bias, F32, out_dim, "bias")
+    _lib.call("qasr_linear_int8_f32", _ptr(y), _ptr(x), _ptr(w_int8), _ptr(scales), _ptr(bias),
+              seq_len, in_dim, out_dim, _stream())
+
+
+def interleave_gate_up(gate: QuantWeight, up: QuantWeight) -> QuantWeight:
+    """Fused row-interleaved gate/up weight (decoder.rs:701-719), built on the device."""
+    inter, hidden = gate.out_dim, gate.in_dim
+    if (up.out_dim, up.in_dim) != (inter, hidden):
+        raise ValueError("gate and up must have the same shape")
+    _need(gate.data, I8, inter * hidden, "gate.data")
+    _need(up.data, I8, inter * hidden, "up.data")
+    _need(gate.scales, F32, inter, "gate.scales")
+    _need(up.scales, F32, inter, "up.scales")
+    data = torch.empty(2 * inter * hidden, dtype=I8, device=gate.data.device)
+    scales = torch.empty(2 * inter, dtype=F32, device=gate.data.device)
+    _lib.call("qasr_interleave_gate_up_i8", _ptr(data), _ptr(scales), _ptr(gate.data),
+              _ptr(gate.scales), _ptr(up.data), _ptr(up.scales), inter, hidden, _stream())
+    return QuantWeight(data, scales, 2 * inter, hidden)
+
+
+def gate_up_swiglu_w8a8(out, w: QuantWeight, xq, x_scales, batch: int, in_dim: int,
+                        intermediate: int) -> None:
+    """W8A8 gate/up projection + SwiGLU on the interleaved weight (int32-exact dots)."""
+    _need(out, F32, batch * intermediate, "out")
+    _need(w.data, I8, 2 * intermediate * in_dim, "w.data")
+    _need(w.scales, F32, 2 * intermediate, "w.scales")
+    _need(xq, I8, batch * in_dim, "xq")
+    _need(x_scales, F32, batch, "x_scales")
+    _lib.call("qasr_gate_up_swiglu_w8a8", _ptr(out), _ptr(w.data), _ptr(w.scales), _ptr(xq),
+              _ptr(x_scales), batch, in_dim, intermediate, _stream())
+
+
+def gate_up_swiglu_w8a8_f32in(out, w: QuantWeight, x, in_dim: int, intermediate: int) -> None:
+    """Batch-1 W8A8 gate/up + SwiGLU quantizing the fp32 input vector in-kernel."""
+    _need(out, F32, intermediate, "out")
+    _need(w.data, I8, 2 * intermediate * in_dim, "w.data")
+    _need(w.scales, F32, 2 * intermediate, "w.scales")
+    _need(x, F32, in_dim, "x")
+    _lib.call("qasr_gate_up_swiglu_w8a8_f32in", _ptr(out), _ptr(w.data), _ptr(w.scales), _ptr(x),
+              in_dim, intermediate, _stream())

@@ -1,0 +1,134 @@
+"""C-ABI checks that need no GPU.
+
+* libqasr_hip.so loads and exports every function include/qasr.h declares, and
+  the ctypes table in qwenasr_amd/_lib.py covers exactly that set;
+* argument validation happens on the host, before any HIP call, and returns
+  the documented status codes (the reference panics on bad dimensions; here
+  nothing is launched and a message is set);
+* zero-sized calls are no-ops that succeed without touching the device.
+
+No call here reaches a kernel launch: every argument set is rejected (or is
+empty) before the library talks to the HIP runtime.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from qwenasr_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "qasr.h"
+
+FAKE = ctypes.c_void_p(0x10000)  # 64 KiB: aligned, never dereferenced (calls are rejected first)
+NULL = ctypes.c_void_p(0)
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"\b(qasr_[a-z0-9_]+)\s*\(", text)) - {"qasr_status"}
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    assert "qasr_add_rms_norm_f32" in names and "qasr_gate_up_swiglu_w8a8" in names
+    assert len(names) >= 25
+
+
+def test_library_exports_every_declared_symbol():
+    so = _lib.lib()
+    missing = [n for n in sorted(declared_functions()) if not hasattr(so, n)]
+    assert not missing, f"not exported: {missing}"
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                        text=True, check=True).stdout
+    exported = set(re.findall(r" T (qasr_[a-z0-9_]+)", nm))
+    assert declared_functions() <= exported
+    # every exported qasr_ symbol is declared (no undocumented entry points)
+    assert exported <= declared_functions(), exported - declared_functions()
+
+
+def test_ctypes_table_matches_header():
+    declared = declared_functions() - {"qasr_version", "qasr_last_error"}
+    assert set(_lib.SIGNATURES) == declared
+
+
+def test_static_archive_has_the_same_symbols():
+    a = ROOT / "qwenasr_amd" / "libqasr_hip.a"
+    assert a.exists(), "static archive not built"
+    nm = subprocess.run(["nm", "--defined-only", str(a)], capture_output=True, text=True,
+                        check=True).stdout
+    assert declared_functions() <= set(re.findall(r" T (qasr_[a-z0-9_]+)", nm))
+
+
+def test_version():
+    assert _lib.version() >= (0, 1, 0)
+
+
+def rc(name, *args):
+    return getattr(_lib.lib(), name)(*args)
+
+
+def last_error() -> str:
+    return _lib.lib().qasr_last_error().decode()
+
+
+def test_null_pointers_are_invalid_arg():
+    assert rc("qasr_rms_norm_f32", NULL, FAKE, FAKE, 4, 64, 1e-6, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert "null" in last_error()
+    assert rc("qasr_add_rms_norm_f32", FAKE, NULL, FAKE, FAKE, 4, 64, 1e-6, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert rc("qasr_layer_norm_f32", FAKE, FAKE, FAKE, NULL, 1, 8, 1e-5, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert rc("qasr_embed_gather_i8", FAKE, FAKE, NULL, FAKE, 1, 16, 10, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert rc("qasr_gate_up_swiglu_w8a8", FAKE, FAKE, FAKE, NULL, FAKE, 1, 64, 32, NULL) == _lib.QASR_ERR_INVALID_ARG
+
+
+def test_zero_sizes_are_noops():
+    # no pointers needed, nothing launched
+    assert rc("qasr_rms_norm_f32", NULL, NULL, NULL, 0, 1024, 1e-6, NULL) == _lib.QASR_OK
+    assert rc("qasr_add_inplace_f32", NULL, NULL, 0, NULL) == _lib.QASR_OK
+    assert rc("qasr_swiglu_multiply_f32", NULL, NULL, 0, 3072, NULL) == _lib.QASR_OK
+    assert rc("qasr_gelu_erf_f32", NULL, 0, NULL) == _lib.QASR_OK
+    assert rc("qasr_embed_gather_f32", NULL, NULL, NULL, 0, 1024, 10, NULL) == _lib.QASR_OK
+    assert rc("qasr_gate_up_swiglu_w8a8", NULL, NULL, NULL, NULL, NULL, 0, 2048, 6144, NULL) == _lib.QASR_OK
+
+
+def test_shape_contracts():
+    # RoPE needs an even head_dim
+    assert rc("qasr_apply_rope_neox_f32", FAKE, FAKE, FAKE, 2, 4, 127, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert "even" in last_error()
+    # W8A8 in_dim must be a multiple of 16
+    assert rc("qasr_gate_up_swiglu_w8a8", FAKE, FAKE, FAKE, FAKE, FAKE, 1, 100, 32, NULL) == _lib.QASR_ERR_INVALID_ARG
+    # the fp32-input matvec supports in_dim 1024..4096 in steps of 1024
+    assert rc("qasr_gate_up_swiglu_w8a8_f32in", FAKE, FAKE, FAKE, FAKE, 512, 32, NULL) == _lib.QASR_ERR_UNSUPPORTED
+    # misaligned weight pointer
+    assert rc("qasr_gate_up_swiglu_w8a8", FAKE, ctypes.c_void_p(0x10001), FAKE, FAKE, FAKE, 1, 64, 32,
+              NULL) == _lib.QASR_ERR_INVALID_ARG
+    # RoPE table fill: head_dim limit
+    assert rc("qasr_rope_table_fill_f32", FAKE, FAKE, 0, 10, 1024, 1e6, NULL) == _lib.QASR_ERR_INVALID_ARG
+    # add_rms_norm: out must not alias the residual
+    assert rc("qasr_add_rms_norm_f32", FAKE, FAKE, FAKE, FAKE, 1, 64, 1e-6, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert "alias" in last_error()
+    # overflowing products
+    big = (1 << 62)
+    assert rc("qasr_rms_norm_f32", FAKE, FAKE, FAKE, big, big, 1e-6, NULL) == _lib.QASR_ERR_INVALID_ARG
+    # vocab must be positive
+    assert rc("qasr_embed_gather_f32", FAKE, FAKE, FAKE, 1, 16, 0, NULL) == _lib.QASR_ERR_INVALID_ARG
+
+
+def test_python_mirror_raises_like_a_slice_panic():
+    import torch
+    from qwenasr_amd import kernels
+
+    # CPU tensors are refused before any C call
+    with pytest.raises(TypeError):
+        kernels.rms_norm(torch.empty(8), torch.empty(8), torch.empty(8), 1, 8, 1e-6)
+
+
+def test_qasr_error_carries_status_and_message():
+    with pytest.raises(_lib.QasrError) as ei:
+        _lib.call("qasr_apply_rope_neox_f32", FAKE, FAKE, FAKE, 2, 4, 127, NULL)
+    assert ei.value.code == _lib.QASR_ERR_INVALID_ARG
+    assert "even" in ei.value.msg

@@ -1,0 +1,539 @@
+"""GPU parity: every C-ABI entry point against the CPU oracle on identical seeded
+inputs, at the benchmark shapes and at ragged/edge shapes.
+
+Tolerances (the parity contract):
+  fp32 outputs          |gpu - oracle| <= 1e-5 + 1e-5 * |oracle|
+  erf-GELU              |gpu - float64 closed form| <= 1e-6
+  int8 / int32 / copies bit-exact
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import assert_close
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5
+ATOL = 1e-5
+ERF_ATOL = 1e-6
+
+
+def rng(*tag):
+    return np.random.default_rng([20261201, *tag])
+
+
+def normal(r, shape, scale=1.0, mean=0.0):
+    return (mean + scale * r.standard_normal(shape)).astype(np.float32)
+
+
+def dev_t(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+# ---------------------------------------------------------------------------
+# residual add + RMSNorm / RMSNorm / LayerNorm
+# ---------------------------------------------------------------------------
+ROW_SHAPES = [(1, 1024), (512, 1024), (256, 2048), (3, 1000), (5, 37), (2, 8192), (2, 9000)]
+
+
+@pytest.mark.parametrize("seq,hidden", ROW_SHAPES)
+def test_add_rms_norm(dev, seq, hidden):
+    from qwenasr_amd import kernels as K
+
+    r = rng(1, seq, hidden)
+    x = normal(r, seq * hidden)
+    d = normal(r, seq * hidden)
+    w = normal(r, hidden, 0.1, 1.0)
+    xt, dt, wt = dev_t(x, dev), dev_t(d, dev), dev_t(w, dev)
+    out = torch.empty_like(xt)
+    K.add_rms_norm(xt, dt, wt, out, seq, hidden, 1e-6)
+    x_ref, y_ref = oracle.add_rms_norm(x, d, w, seq, hidden, 1e-6)
+    np.testing.assert_array_equal(host(xt), x_ref)  # the residual is an f32 add: exact
+    assert_close(host(out), y_ref, RTOL, ATOL, f"add_rms_norm {seq}x{hidden}")
+
+
+@pytest.mark.parametrize("seq,hidden", ROW_SHAPES)
+def test_rms_norm(dev, seq, hidden):
+    from qwenasr_amd import kernels as K
+
+    r = rng(2, seq, hidden)
+    x = normal(r, seq * hidden)
+    w = normal(r, hidden, 0.1, 1.0)
+    xt, wt = dev_t(x, dev), dev_t(w, dev)
+    out = torch.empty_like(xt)
+    K.rms_norm(out, xt, wt, seq, hidden, 1e-6)
+    assert_close(host(out), oracle.rms_norm(x, w, seq, hidden, 1e-6), RTOL, ATOL, "rms_norm")
+    # in place (out aliases x)
+    K.rms_norm(xt, xt, wt, seq, hidden, 1e-6)
+    assert_close(host(xt), oracle.rms_norm(x, w, seq, hidden, 1e-6), RTOL, ATOL, "rms_norm inplace")
+
+
+def test_rms_norm_misaligned_rows_take_scalar_path(dev):
+    from qwenasr_amd import kernels as K
+
+    r = rng(3)
+    seq, hidden = 4, 64
+    x = normal(r, seq * hidden + 1)
+    w = normal(r, hidden, 0.1, 1.0)
+    xt = dev_t(x, dev)[1:]  # 4-byte offset: not 16-byte aligned
+    out = torch.empty(seq * hidden + 1, dtype=torch.float32, device=dev)[1:]
+    K.rms_norm(out, xt, dev_t(w, dev), seq, hidden, 1e-6)
+    assert_close(host(out), oracle.rms_norm(x[1:], w, seq, hidden, 1e-6), RTOL, ATOL, "misaligned")
+
+
+def test_rms_norm_reference_kat(dev, golden):
+    # tests/kernels.rs:60-72 on the GPU: unit gain -> RMS ~ 1
+    from qwenasr_amd import kernels as K
+
+    x = dev_t(golden["rms_kat_x"], dev)
+    out = torch.empty_like(x)
+    K.rms_norm(out, x, torch.ones(128, device=dev), 1, 128, 1e-6)
+    y = host(out)
+    assert abs(float(np.sqrt(np.mean(y.astype(np.float64) ** 2))) - 1.0) < 0.01
+    assert_close(y, golden["rms_kat_y64"], RTOL, ATOL, "kat")
+
+
+@pytest.mark.parametrize("seq,hidden", [(3000, 896), (7, 1024), (4, 45), (2, 8)])
+def test_layer_norm(dev, seq, hidden):
+    from qwenasr_amd import kernels as K
+
+    r = rng(4, seq, hidden)
+    x = normal(r, seq * hidden)
+    w = normal(r, hidden, 0.1, 1.0)
+    b = normal(r, hidden, 0.02)
+    xt = dev_t(x, dev)
+    out = torch.empty_like(xt)
+    K.layer_norm(out, xt, dev_t(w, dev), dev_t(b, dev), seq, hidden, 1e-5)
+    assert_close(host(out), oracle.layer_norm(x, w, b, seq, hidden, 1e-5), RTOL, ATOL, "layer_norm")
+
+
+def test_layer_norm_reference_kat(dev, golden):
+    from qwenasr_amd import kernels as K
+
+    x = dev_t(golden["ln_kat_x"], dev)
+    out = torch.empty_like(x)
+    K.layer_norm(out, x, torch.ones(128, device=dev), torch.zeros(128, device=dev), 1, 128, 1e-5)
+    y = host(out)
+    assert abs(float(np.mean(y))) < 0.01 and abs(float(np.var(y.astype(np.float64))) - 1) < 0.02
+
+
+# ---------------------------------------------------------------------------
+# q/k head RMSNorm + RoPE
+# ---------------------------------------------------------------------------
+def test_rope_table_matches_oracle(dev):
+    from qwenasr_amd import kernels as K
+
+    rc = K.RopeCache(dev)
+    rc.ensure(1500, 128, 1e6)  # grows 1024 -> 2048
+    assert rc.cap == 2048
+    cos, sin = oracle.rope_table(2048, 128, 1e6)
+    assert_close(host(rc.cos), cos, 0, 2.4e-7, "cos table")
+    assert_close(host(rc.sin), sin, 0, 2.4e-7, "sin table")
+    rc.ensure(3000, 128, 1e6)  # second growth keeps the first rows and fills the rest
+    assert rc.cap == 4096
+    cos4, _ = oracle.rope_table(4096, 128, 1e6)
+    assert_close(host(rc.cos), cos4, 0, 2.4e-7, "cos table grown")
+
+
+HEAD_CASES = [
+    # name, seq, n_heads, n_kv_heads, head_dim, position range
+    ("c1_decode", 1, 16, 8, 128, 512),
+    ("c2_prefill", 512, 16, 8, 128, None),
+    ("c5_streams", 256, 16, 8, 128, 2048),
+    ("hd64", 9, 4, 2, 64, 100),
+    ("hd96_scalar", 5, 3, 1, 96, 50),
+]
+
+
+@pytest.mark.parametrize("name,seq,nq,nk,hd,prange", HEAD_CASES)
+def test_head_rms_norm_rope(dev, name, seq, nq, nk, hd, prange):
+    from qwenasr_amd import kernels as K
+
+    r = rng(5, seq, nq, hd)
+    q = normal(r, seq * nq * hd)
+    k = normal(r, seq * nk * hd)
+    qw = normal(r, hd, 0.1, 1.0)
+    kw = normal(r, hd, 0.1, 1.0)
+    pos = None if prange is None else r.integers(0, prange, seq).astype(np.int32)
+    n_rows = 2048
+    rc = K.RopeCache(dev)
+    rc.ensure(n_rows, hd, 1e6)
+    cos, sin = oracle.rope_table(rc.cap, hd, 1e6)
+    qt, kt = dev_t(q, dev), dev_t(k, dev)
+    K.head_rms_norm_rope(qt, kt, dev_t(qw, dev), dev_t(kw, dev), rc.cos, rc.sin,
+                         None if pos is None else dev_t(pos, dev), seq, nq, nk, hd, 1e-6)
+    q_ref, k_ref = oracle.head_rms_norm_rope(q, k, qw, kw, cos, sin, pos, seq, nq, nk, hd, 1e-6)
+    assert_close(host(qt), q_ref, RTOL, ATOL, f"{name} q")
+    assert_close(host(kt), k_ref, RTOL, ATOL, f"{name} k")
+
+
+def test_head_rope_out_of_table_position_is_nan_row(dev):
+    from qwenasr_amd import kernels as K
+
+    r = rng(6)
+    seq, nq, nk, hd = 3, 2, 1, 128
+    q = normal(r, seq * nq * hd)
+    k = normal(r, seq * nk * hd)
+    rc = K.RopeCache(dev)
+    rc.ensure(16, hd, 1e6)
+    pos = np.array([3, 5000, 0], np.int32)  # row 1 is past the 1024-row table
+    qt, kt = dev_t(q, dev), dev_t(k, dev)
+    ones = torch.ones(hd, device=dev)
+    K.head_rms_norm_rope(qt, kt, ones, ones, rc.cos, rc.sin, dev_t(pos, dev), seq, nq, nk, hd, 1e-6)
+    qh, kh = host(qt).reshape(seq, -1), host(kt).reshape(seq, -1)
+    assert np.isnan(qh[1]).all() and np.isnan(kh[1]).all()
+    assert np.isfinite(qh[[0, 2]]).all() and np.isfinite(kh[[0, 2]]).all()
+
+
+@pytest.mark.parametrize("seq,nh,hd", [(512, 16, 128), (3, 5, 64), (2, 3, 30)])
+def test_rms_norm_per_head_and_apply_rope(dev, seq, nh, hd):
+    from qwenasr_amd import kernels as K
+
+    r = rng(7, seq, nh, hd)
+    x = normal(r, seq * nh * hd)
+    w = normal(r, hd, 0.1, 1.0)
+    xt = dev_t(x, dev)
+    K.rms_norm_per_head(xt, dev_t(w, dev), seq, nh, hd, 1e-6)
+    xn = oracle.rms_norm_per_head(x, w, seq, nh, hd, 1e-6)
+    assert_close(host(xt), xn, RTOL, ATOL, "rms_norm_per_head")
+    cos, sin = oracle.rope_table(seq + 7, hd, 1e6)
+    c = cos[7 * hd:]
+    s = sin[7 * hd:]  # rows 7..: a cos_range(start=7, len=seq) slice
+    xt2 = dev_t(xn, dev)
+    K.apply_rope_neox(xt2, dev_t(c, dev), dev_t(s, dev), seq, nh, hd)
+    assert_close(host(xt2), oracle.apply_rope_neox(xn, c, s, seq, nh, hd), RTOL, ATOL, "rope")
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU / SiLU / GELU
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("seq,inter", [(512, 3072), (1, 3072), (3, 21), (2, 3076), (4, 6144)])
+def test_swiglu_multiply(dev, seq, inter):
+    from qwenasr_amd import kernels as K
+
+    r = rng(8, seq, inter)
+    gu = normal(r, seq * 2 * inter)
+    out = torch.empty(seq * inter, dtype=torch.float32, device=dev)
+    K.swiglu_multiply(out, dev_t(gu, dev), seq, inter)
+    assert_close(host(out), oracle.swiglu_multiply(gu, seq, inter), RTOL, ATOL, "swiglu_multiply")
+
+
+@pytest.mark.parametrize("n", [3072, 6144, 1, 1027])
+def test_swiglu_split_and_silu(dev, n):
+    from qwenasr_amd import kernels as K
+
+    r = rng(9, n)
+    g, u = normal(r, n), normal(r, n)
+    out = torch.empty(n, dtype=torch.float32, device=dev)
+    K.swiglu_split(out, dev_t(g, dev), dev_t(u, dev), n)
+    assert_close(host(out), oracle.swiglu_split(g, u), RTOL, ATOL, "swiglu_split")
+    gt = dev_t(g, dev)
+    K.swiglu_multiply_inplace(gt, dev_t(u, dev))
+    assert_close(host(gt), oracle.swiglu_split(g, u), RTOL, ATOL, "swiglu inplace")
+    xt = dev_t(g, dev)
+    K.silu(xt, n)
+    assert_close(host(xt), oracle.silu(g), RTOL, ATOL, "silu")
+
+
+def test_silu_reference_kat(dev):
+    # tests/kernels.rs:115-124
+    from qwenasr_amd import kernels as K
+
+    x = np.array([0.0, 1.0, -1.0, 5.0], np.float32)
+    xt = dev_t(x, dev)
+    K.silu(xt, 4)
+    exp = x.astype(np.float64) / (1 + np.exp(-x.astype(np.float64)))
+    assert np.abs(host(xt) - exp).max() < 1e-5
+
+
+@pytest.mark.parametrize("n", [3000 * 3584, 1003, 8, 5])
+def test_gelu_erf_within_1e6_of_closed_form(dev, n):
+    from qwenasr_amd import kernels as K
+
+    r = rng(10, n)
+    x = normal(r, n)
+    xt = dev_t(x, dev)
+    K.gelu_erf(xt, n)
+    assert_close(host(xt), oracle.gelu_erf(x), 0, ERF_ATOL, "gelu_erf")
+
+
+def test_gelu_erf_tails_and_kat(dev, golden):
+    from qwenasr_amd import kernels as K
+
+    x = golden["act_x"]
+    xt = dev_t(x, dev)
+    K.gelu_erf(xt, x.size)
+    y = host(xt)
+    assert_close(y, golden["gelu_erf_y64"], 0, ERF_ATOL, "gelu_erf grid")
+    assert abs(y[0]) < 1e-5 and y[1] > 0.5 and y[2] < 0  # tests/kernels.rs:105-113
+
+
+@pytest.mark.parametrize("n", [3000 * 3584, 10, 1003])
+def test_gelu_tanh_matches_reference_arithmetic(dev, n):
+    from qwenasr_amd import kernels as K
+
+    r = rng(11, n)
+    x = normal(r, n, 2.0)
+    xt = dev_t(x, dev)
+    K.gelu(xt, n)
+    assert_close(host(xt), oracle.gelu_tanh(x), RTOL, ATOL, "gelu_tanh")
+
+
+# ---------------------------------------------------------------------------
+# Sinusoidal PE
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n_pos,dm", [(13, 896), (3000, 64), (13, 1024)])
+def test_sinusoidal_pe(dev, n_pos, dm):
+    from qwenasr_amd import kernels as K
+
+    pe = torch.empty(n_pos * dm, dtype=torch.float32, device=dev)
+    K.sinusoidal_pe(pe, n_pos, dm)
+    assert_close(host(pe), oracle.sinusoidal_pe(n_pos, dm), RTOL, ATOL, "sinusoidal_pe")
+
+
+@pytest.mark.parametrize("rows,dm,n_pos", [(3000, 896, 13), (3000, 896, 3000), (7, 30, 3)])
+def test_pe_add(dev, rows, dm, n_pos):
+    from qwenasr_amd import kernels as K
+
+    r = rng(12, rows, dm)
+    x = normal(r, rows * dm)
+    pe = oracle.sinusoidal_pe(n_pos, dm)
+    xt = dev_t(x, dev)
+    K.pe_add(xt, dev_t(pe, dev), rows, dm, n_pos)
+    np.testing.assert_array_equal(host(xt), oracle.pe_add(x, pe, rows, dm, n_pos))
+
+
+# ---------------------------------------------------------------------------
+# Embedding gathers
+# ---------------------------------------------------------------------------
+def test_embed_gather_f32_bf16_i8(dev):
+    from qwenasr_amd import kernels as K
+
+    r = rng(13)
+    vocab, dim, n = 4096, 1024, 512
+    tab = normal(r, (vocab, dim), 0.02)
+    ids = r.integers(0, vocab, n).astype(np.int32)
+    out = torch.empty(n * dim, dtype=torch.float32, device=dev)
+    K.embed_gather_f32(out, dev_t(tab, dev), dev_t(ids, dev), n, dim)
+    np.testing.assert_array_equal(host(out), oracle.embed_gather_f32(tab, ids, dim))
+
+    bits = r.integers(0, 1 << 16, (vocab, dim), dtype=np.uint16)
+    K.embed_gather_bf16(out, dev_t(bits.view(np.int16), dev), dev_t(ids, dev), n, dim)
+    np.testing.assert_array_equal(host(out).view(np.uint32), oracle.embed_gather_bf16(bits, ids, dim).view(np.uint32))
+
+    t8 = r.integers(-128, 128, (vocab, dim), dtype=np.int8)
+    s8 = r.uniform(1e-4, 1e-2, vocab).astype(np.float32)
+    w = K.QuantWeight(dev_t(t8, dev), dev_t(s8, dev), vocab, dim)
+    K.embed_gather_i8(out, w, dev_t(ids, dev), n, dim)
+    np.testing.assert_array_equal(host(out), oracle.embed_gather_i8(t8, s8, ids, dim))
+
+
+def test_embed_gather_ragged_dim_and_bad_ids(dev):
+    from qwenasr_amd import kernels as K
+
+    r = rng(14)
+    vocab, dim = 50, 30  # dim not a multiple of 4: scalar path
+    tab = normal(r, (vocab, dim))
+    ids = np.array([0, 49, -1, 50, 7], np.int32)
+    out = torch.empty(5 * dim, dtype=torch.float32, device=dev)
+    K.embed_gather_f32(out, dev_t(tab, dev), dev_t(ids, dev), 5, dim)
+    y = host(out).reshape(5, dim)
+    np.testing.assert_array_equal(y[[0, 1, 4]], tab[[0, 49, 7]])
+    assert np.isnan(y[2]).all() and np.isnan(y[3]).all()
+
+
+def test_embed_gather_full_vocab_table(dev):
+    # the benchmark table [151936, 1024], checked by exact row equality
+    from qwenasr_amd import kernels as K
+
+    vocab, dim, n = 151936, 1024, 512
+    g = torch.Generator(device=dev).manual_seed(15)
+    tab = torch.randn(vocab * dim, generator=g, device=dev) * 0.02
+    ids = torch.randint(0, vocab, (n,), generator=g, device=dev, dtype=torch.int32)
+    ids[0], ids[1] = 0, vocab - 1
+    out = torch.empty(n * dim, dtype=torch.float32, device=dev)
+    K.embed_gather_f32(out, tab, ids, n, dim)
+    ref = tab.view(vocab, dim).index_select(0, ids.long()).reshape(-1)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+def test_tok_embed_single_token(dev):
+    from qwenasr_amd import kernels as K
+
+    r = rng(16)
+    bits = r.integers(0, 1 << 16, (10, 64), dtype=np.uint16)
+    dst = torch.empty(64, dtype=torch.float32, device=dev)
+    K.tok_embed_bf16_to_f32(dst, dev_t(bits.view(np.int16), dev), 7, 64)
+    np.testing.assert_array_equal(host(dst).view(np.uint32), bits[7].astype(np.uint32) << 16)
+
+
+# ---------------------------------------------------------------------------
+# INT8: quantizer, W8A32, interleave, W8A8 + SwiGLU
+# ---------------------------------------------------------------------------
+def test_quantizer_fixture_bit_exact(dev, golden):
+    from qwenasr_amd import kernels as K
+
+    x = golden["quant_x"]
+    q = torch.empty(x.size, dtype=torch.int8, device=dev)
+    s = torch.empty(x.shape[0], dtype=torch.float32, device=dev)
+    K.quantize_rows_i8(q, s, dev_t(x.ravel(), dev), x.shape[0], x.shape[1])
+    np.testing.assert_array_equal(host(q).reshape(x.shape), golden["quant_q"])
+    np.testing.assert_array_equal(host(s), golden["quant_s"])
+
+
+@pytest.mark.parametrize("rows,cols", [(256, 2048), (1, 2048), (12288, 2048), (3, 77)])
+def test_quantizer_matches_oracle(dev, rows, cols):
+    from qwenasr_amd import kernels as K
+
+    r = rng(17, rows, cols)
+    x = normal(r, rows * cols, 0.02)
+    q, s = K.quantize_f32_to_int8(dev_t(x, dev), rows, cols)
+    q_ref, s_ref = oracle.quantize_f32_to_int8(x, rows, cols)
+    np.testing.assert_array_equal(host(q), q_ref)
+    np.testing.assert_array_equal(host(s), s_ref)
+
+
+def make_qweight(r, rows, cols):
+    w = normal(r, rows * cols, 0.02)
+    return oracle.quantize_f32_to_int8(w, rows, cols)
+
+
+@pytest.mark.parametrize("seq,in_dim,out_dim", [(1, 2048, 12288), (4, 1024, 3072), (3, 2048, 2048),
+                                                (2, 100, 33)])
+def test_linear_nobias_int8_w8a32(dev, seq, in_dim, out_dim):
+    from qwenasr_amd import kernels as K
+
+    r = rng(18, seq, in_dim, out_dim)
+    wq, ws = make_qweight(r, out_dim, in_dim)
+    x = normal(r, seq * in_dim)
+    y = torch.empty(seq * out_dim, dtype=torch.float32, device=dev)
+    K.linear_nobias_int8(y, dev_t(x, dev), dev_t(wq, dev), dev_t(ws, dev), seq, in_dim, out_dim)
+    ref = oracle.linear_nobias_int8(x, wq, ws, seq, in_dim, out_dim)
+    assert_close(host(y), ref, RTOL, ATOL, "w8a32")
+    b = normal(r, out_dim, 0.02)
+    K.linear_int8(y, dev_t(x, dev), dev_t(wq, dev), dev_t(ws, dev), dev_t(b, dev), seq, in_dim, out_dim)
+    assert_close(host(y), oracle.linear_int8(x, wq, ws, b, seq, in_dim, out_dim), RTOL, ATOL, "w8a32+bias")
+
+
+def test_linear_int8_integer_inputs_exact(dev):
+    # integer x, unit scales: the f32 accumulation is exact, so y is the int dot
+    from qwenasr_amd import kernels as K
+
+    r = rng(19)
+    in_dim, out_dim = 2048, 512
+    wq = r.integers(-128, 128, (out_dim, in_dim), dtype=np.int8)
+    x = r.integers(-20, 21, in_dim).astype(np.float32)
+    y = torch.empty(out_dim, dtype=torch.float32, device=dev)
+    K.linear_nobias_int8(y, dev_t(x, dev), dev_t(wq, dev), torch.ones(out_dim, device=dev), 1,
+                         in_dim, out_dim)
+    exact = wq.astype(np.int64) @ x.astype(np.int64)
+    np.testing.assert_array_equal(host(y).astype(np.int64), exact)
+
+
+def test_interleave_gate_up(dev):
+    from qwenasr_amd import kernels as K
+
+    r = rng(20)
+    inter, hid = 96, 256
+    gq, gs = make_qweight(r, inter, hid)
+    uq, us = make_qweight(r, inter, hid)
+    fused = K.interleave_gate_up(K.QuantWeight(dev_t(gq, dev), dev_t(gs, dev), inter, hid),
+                                 K.QuantWeight(dev_t(uq, dev), dev_t(us, dev), inter, hid))
+    wgu, sgu = oracle.interleave_gate_up(gq, gs, uq, us, inter, hid)
+    np.testing.assert_array_equal(host(fused.data), wgu)
+    np.testing.assert_array_equal(host(fused.scales), sgu)
+
+
+def gateup_inputs(r, batch, in_dim, inter):
+    wq, ws = make_qweight(r, 2 * inter, in_dim)
+    x = normal(r, batch * in_dim)
+    xq, xs = oracle.quantize_f32_to_int8(x, batch, in_dim)
+    return wq, ws, x, xq, xs
+
+
+W8A8_CASES = [
+    ("c4_matvec", 1, 2048, 6144),
+    ("c4_0.6B", 1, 1024, 3072),
+    ("c5_mfma", 256, 2048, 6144),
+    ("mfma_ragged_batch", 37, 2048, 96),
+    ("mfma_small_k", 64, 512, 256),
+    ("generic_path", 3, 400, 50),
+    ("matvec_k3072", 1, 3072, 100),
+]
+
+
+@pytest.mark.parametrize("name,batch,in_dim,inter", W8A8_CASES)
+def test_gate_up_swiglu_w8a8(dev, name, batch, in_dim, inter):
+    from qwenasr_amd import kernels as K
+
+    r = rng(21, batch, in_dim, inter)
+    wq, ws, _, xq, xs = gateup_inputs(r, batch, in_dim, inter)
+    out = torch.empty(batch * inter, dtype=torch.float32, device=dev)
+    w = K.QuantWeight(dev_t(wq, dev), dev_t(ws, dev), 2 * inter, in_dim)
+    K.gate_up_swiglu_w8a8(out, w, dev_t(xq, dev), dev_t(xs, dev), batch, in_dim, inter)
+    if batch * inter * in_dim <= 64 * 1024 * 1024:
+        ref, _ = oracle.gate_up_swiglu_w8a8(wq, ws, xq, xs, batch, in_dim, inter)
+    else:  # exact integer dots through float64 BLAS (exact below 2^53), f32 epilogue
+        ref = w8a8_reference_blas(wq, ws, xq, xs, batch, in_dim, inter)
+    assert_close(host(out), ref, RTOL, ATOL, name)
+
+
+def w8a8_reference_blas(wq, ws, xq, xs, batch, in_dim, inter):
+    dots = xq.reshape(batch, in_dim).astype(np.float64) @ wq.reshape(2 * inter, in_dim).astype(np.float64).T
+    g = ((dots[:, 0::2].astype(np.float32) * xs[:, None]) * ws[None, 0::2]).astype(np.float64)
+    u = ((dots[:, 1::2].astype(np.float32) * xs[:, None]) * ws[None, 1::2]).astype(np.float64)
+    return (g / (1 + np.exp(-g)) * u).ravel()
+
+
+@pytest.mark.parametrize("batch,in_dim,inter", [(1, 2048, 6144), (256, 2048, 6144), (5, 1024, 64)])
+def test_w8a8_int32_dots_bit_exact(dev, batch, in_dim, inter):
+    """Makes the epilogue the identity on the dots: positive gate rows and
+    activations give dg >> 104 so expf(-g) == 0 and silu(g) == g exactly; with
+    unit scales out == f32(dg) * f32(du). Any dot error shows as a bit change."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(22, batch, in_dim, inter)
+    w = np.empty((2 * inter, in_dim), np.int8)
+    w[0::2] = r.integers(1, 128, (inter, in_dim), dtype=np.int8)      # gate rows > 0
+    w[1::2] = r.integers(-128, 128, (inter, in_dim), dtype=np.int8)   # up rows: any sign
+    xq = r.integers(1, 128, (batch, in_dim), dtype=np.int8)
+    ones_w = np.ones(2 * inter, np.float32)
+    ones_x = np.ones(batch, np.float32)
+    out = torch.empty(batch * inter, dtype=torch.float32, device=dev)
+    qw = K.QuantWeight(dev_t(w, dev), dev_t(ones_w, dev), 2 * inter, in_dim)
+    K.gate_up_swiglu_w8a8(out, qw, dev_t(xq, dev), dev_t(ones_x, dev), batch, in_dim, inter)
+    dots = xq.astype(np.float64) @ w.astype(np.float64).T   # exact integers
+    assert dots[:, 0::2].min() > 200
+    exp = (dots[:, 0::2].astype(np.float32) * dots[:, 1::2].astype(np.float32)).ravel()
+    np.testing.assert_array_equal(host(out), exp)
+
+
+@pytest.mark.parametrize("in_dim,inter", [(2048, 6144), (1024, 3072), (4096, 64)])
+def test_gate_up_swiglu_w8a8_f32_input(dev, in_dim, inter):
+    from qwenasr_amd import kernels as K
+
+    r = rng(23, in_dim, inter)
+    wq, ws, x, xq, xs = gateup_inputs(r, 1, in_dim, inter)
+    out = torch.empty(inter, dtype=torch.float32, device=dev)
+    w = K.QuantWeight(dev_t(wq, dev), dev_t(ws, dev), 2 * inter, in_dim)
+    K.gate_up_swiglu_w8a8_f32in(out, w, dev_t(x, dev), in_dim, inter)
+    ref, _ = oracle.gate_up_swiglu_w8a8(wq, ws, xq, xs, 1, in_dim, inter)
+    assert_close(host(out), ref, RTOL, ATOL, "f32in")
+    # same result as quantize_rows_i8 + the int8-input entry point, bit for bit
+    q2 = torch.empty(in_dim, dtype=torch.int8, device=dev)
+    s2 = torch.empty(1, dtype=torch.float32, device=dev)
+    K.quantize_rows_i8(q2, s2, dev_t(x, dev), 1, in_dim)
+    out2 = torch.empty_like(out)
+    K.gate_up_swiglu_w8a8(out2, w, q2, s2, 1, in_dim, inter)
+    np.testing.assert_array_equal(host(out), host(out2))

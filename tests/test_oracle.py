@@ -1,0 +1,272 @@
+"""Pins the CPU oracle (oracle/qasr_oracle.c) before it is trusted as the checker.
+
+Each check compares the oracle with something it does not share code with:
+the known-answer properties of the reference's own tests
+(crates/qwen-asr/tests/kernels.rs), float64 closed forms and exact integer
+results from tests/golden/golden.npz, and mathematical invariants. The inputs
+are chosen so that a plausible mistake (a dropped eps, a swapped sin/cos, a
+sign, banker's rounding, the libm exp in place of the reference's polynomial)
+fails at least one check.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import assert_close
+
+
+# --- RMSNorm ----------------------------------------------------------------
+def test_rms_norm_reference_kat(golden):
+    # tests/kernels.rs:60-72: unit gain -> output RMS ~ 1 (+-0.01)
+    x = golden["rms_kat_x"]
+    y = oracle.rms_norm(x, np.ones(128, np.float32), 1, 128, 1e-6)
+    rms = float(np.sqrt(np.mean(y.astype(np.float64) ** 2)))
+    assert abs(rms - 1.0) < 0.01
+    assert_close(y, golden["rms_kat_y64"], 2e-6, 1e-7, "rms kat")
+
+
+@pytest.mark.parametrize("h", [64, 48, 37])
+def test_rms_norm_eps_sensitive_rows(golden, h):
+    x, w = golden[f"rms_small_x_{h}"], golden[f"rms_small_w_{h}"]
+    y = oracle.rms_norm(x.ravel(), w, x.shape[0], h, 1e-6).reshape(x.shape)
+    assert_close(y, golden[f"rms_small_y64_{h}"], 2e-6, 1e-7, f"rms h={h}")
+
+
+def test_rms_norm_zero_row_is_zero():
+    y = oracle.rms_norm(np.zeros(64, np.float32), np.ones(64, np.float32), 1, 64, 1e-6)
+    assert np.all(y == 0)
+
+
+def test_add_rms_norm_is_add_then_norm(golden):
+    r = np.random.default_rng(1)
+    x = r.standard_normal(3 * 40).astype(np.float32)
+    d = r.standard_normal(3 * 40).astype(np.float32)
+    w = (1 + 0.1 * r.standard_normal(40)).astype(np.float32)
+    x2, y = oracle.add_rms_norm(x, d, w, 3, 40, 1e-6)
+    np.testing.assert_array_equal(x2, x + d)  # f32 add is exact-rounded either way
+    s = (x + d).astype(np.float64).reshape(3, 40)
+    ref = s / np.sqrt(np.mean(s * s, axis=1, keepdims=True) + 1e-6) * w
+    assert_close(y.reshape(3, 40), ref, 2e-6, 1e-7, "add+rms")
+
+
+# --- LayerNorm ----------------------------------------------------------------
+def test_layer_norm_reference_kat(golden):
+    # tests/kernels.rs:74-89: mean ~ 0 (+-0.01), var ~ 1 (+-0.02)
+    x = golden["ln_kat_x"]
+    y = oracle.layer_norm(x, np.ones(128, np.float32), np.zeros(128, np.float32), 1, 128, 1e-5)
+    assert abs(float(np.mean(y))) < 0.01
+    assert abs(float(np.var(y.astype(np.float64))) - 1.0) < 0.02
+    assert_close(y, golden["ln_kat_y64"], 2e-6, 1e-6, "ln kat")
+
+
+@pytest.mark.parametrize("h", [64, 45])
+def test_layer_norm_offset_small_variance(golden, h):
+    x, w, b = golden[f"ln_x_{h}"], golden[f"ln_w_{h}"], golden[f"ln_b_{h}"]
+    y = oracle.layer_norm(x.ravel(), w, b, x.shape[0], h, 1e-5).reshape(x.shape)
+    # x has mean 5 and std 3e-3: f32 mean subtraction leaves ~5e-7/3e-3 relative noise
+    assert_close(y, golden[f"ln_y64_{h}"], 1e-4, 1e-4, f"ln h={h}")
+
+
+# --- head RMSNorm / RoPE ---------------------------------------------------------
+def test_rms_norm_per_head_closed_form(golden):
+    x, w = golden["head_x"], golden["head_w"]
+    y = oracle.rms_norm_per_head(x.ravel(), w, x.shape[0], x.shape[1], x.shape[2], 1e-6)
+    assert_close(y.reshape(x.shape), golden["head_y64"], 2e-6, 1e-7, "head norm")
+
+
+def test_rope_inv_freq_within_one_ulp(golden):
+    inv = oracle.rope_inv_freq(128, 1e6)
+    ref = golden["rope_inv_freq"]
+    assert inv[0] == 1.0  # theta^0
+    ulp = np.spacing(np.abs(ref))
+    assert np.all(np.abs(inv - ref) <= ulp), "inv_freq differs from 1/theta^(2d/D) by > 1 ulp"
+
+
+def test_rope_table_matches_f32_angle_closed_form(golden):
+    pos = golden["rope_pos"]
+    cos, sin = oracle.rope_table(int(pos.max()) + 1, 128, 1e6)
+    cos, sin = cos.reshape(-1, 128)[pos], sin.reshape(-1, 128)[pos]
+    inv = oracle.rope_inv_freq(128, 1e6)
+    ang = (pos.astype(np.float32)[:, None] * inv[None, :]).astype(np.float32).astype(np.float64)
+    c64 = np.concatenate([np.cos(ang), np.cos(ang)], 1)
+    s64 = np.concatenate([np.sin(ang), np.sin(ang)], 1)
+    assert_close(cos, c64, 0, 1.2e-7, "cos table")
+    assert_close(sin, s64, 0, 1.2e-7, "sin table")
+    # position 0 is the identity rotation, exactly
+    assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)
+    # column 0 has inv_freq 1: angle = p exactly
+    assert_close(cos[:, 0], np.cos(pos.astype(np.float64)), 0, 1.2e-7, "cos(p)")
+
+
+def test_rope_rotation_closed_form(golden):
+    x, c, s = golden["rope_x"], golden["rope_cos32"], golden["rope_sin32"]
+    y = oracle.apply_rope_neox(x.ravel(), c.ravel(), s.ravel(), x.shape[0], x.shape[1], 128)
+    y = y.reshape(x.shape)
+    assert_close(y, golden["rope_y64"], 1e-6, 1e-6, "rope")
+    # position 0 row: exact identity
+    np.testing.assert_array_equal(y[0], x[0])
+    # each (d, d+64) pair keeps its length
+    n_in = np.hypot(x[..., :64].astype(np.float64), x[..., 64:].astype(np.float64))
+    n_out = np.hypot(y[..., :64].astype(np.float64), y[..., 64:].astype(np.float64))
+    assert_close(n_out, n_in, 1e-6, 1e-7, "pair norm")
+
+
+def test_head_norm_rope_composition(golden):
+    r = np.random.default_rng(7)
+    seq, nq, nk, hd = 4, 3, 2, 128
+    q = r.standard_normal(seq * nq * hd).astype(np.float32)
+    k = r.standard_normal(seq * nk * hd).astype(np.float32)
+    qw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+    kw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+    cos, sin = oracle.rope_table(64, hd, 1e6)
+    pos = np.array([5, 0, 63, 17], np.int32)
+    q2, k2 = oracle.head_rms_norm_rope(q, k, qw, kw, cos, sin, pos, seq, nq, nk, hd, 1e-6)
+    # same as norm-per-head then rope with gathered table rows
+    qn = oracle.rms_norm_per_head(q, qw, seq, nq, hd, 1e-6)
+    cr = cos.reshape(64, hd)[pos].ravel()
+    sr = sin.reshape(64, hd)[pos].ravel()
+    np.testing.assert_array_equal(q2, oracle.apply_rope_neox(qn, cr, sr, seq, nq, hd))
+    kn = oracle.rms_norm_per_head(k, kw, seq, nk, hd, 1e-6)
+    np.testing.assert_array_equal(k2, oracle.apply_rope_neox(kn, cr, sr, seq, nk, hd))
+
+
+# --- activations --------------------------------------------------------------------
+def test_fast_exp_is_the_reference_polynomial(golden):
+    x, ref = golden["exp_x"], golden["exp_y64"]
+    got = np.array([oracle.fast_exp(float(v)) for v in x], np.float64)
+    rel = np.abs(got - ref) / ref
+    assert rel.max() < 1e-5            # a degree-5 polynomial on [-ln2/2, ln2/2]
+    assert rel.max() > 1e-6            # ... and not libm expf (which is < 1 ulp)
+    assert oracle.fast_exp(0.0) == 1.0
+    assert oracle.fast_exp(-1000.0) == np.float32(2.0 ** -126)  # clamp at -126
+
+
+def test_silu_reference_kat(golden):
+    # tests/kernels.rs:115-124: max abs err < 1e-5 against v/(1+exp(-v))
+    x = golden["act_x"]
+    assert_close(oracle.silu(x), golden["silu_y64"], 1e-6, 1e-7, "silu")
+
+
+def test_gelu_tanh_reference_kat(golden):
+    x = golden["act_x"]
+    y = oracle.gelu_tanh(x)
+    # tests/kernels.rs:105-113 on the first five inputs [0, 1, -1, 2, -0.5]
+    assert abs(y[0]) < 1e-5 and y[1] > 0.5 and y[2] < 0.0
+    assert_close(y, golden["gelu_tanh_y64"], 1e-5, 2e-5, "gelu tanh")
+
+
+def test_gelu_erf_closed_form(golden):
+    x = golden["act_x"]
+    assert_close(oracle.gelu_erf(x), golden["gelu_erf_y64"], 0, 1e-6, "gelu erf")
+    # tanh vs erf GELU differ by up to ~4.7e-4 (the gap the exact form closes)
+    gap = np.abs(golden["gelu_tanh_y64"] - golden["gelu_erf_y64"]).max()
+    assert 4e-4 < gap < 5e-4
+
+
+def test_swiglu_multiply_fast_blocks_and_tail():
+    r = np.random.default_rng(3)
+    seq, inter = 3, 21  # two 8-blocks via fast_exp + a 5-column libm tail per row
+    gu = r.standard_normal(seq * 2 * inter).astype(np.float32) * 3
+    y = oracle.swiglu_multiply(gu, seq, inter).reshape(seq, inter)
+    g = gu.reshape(seq, inter, 2)[..., 0].astype(np.float64)
+    u = gu.reshape(seq, inter, 2)[..., 1].astype(np.float64)
+    ref = g / (1 + np.exp(-g)) * u
+    assert_close(y, ref, 1e-5, 1e-6, "swiglu")
+    # the tail columns use libm expf: within a few ulp of exact
+    assert_close(y[:, 16:], ref[:, 16:], 1e-6, 1e-7, "swiglu tail")
+    # split form == interleaved form on the libm columns
+    ys = oracle.swiglu_split(gu.reshape(seq, inter, 2)[..., 0].copy(),
+                             gu.reshape(seq, inter, 2)[..., 1].copy()).reshape(seq, inter)
+    np.testing.assert_array_equal(ys[:, 16:], y[:, 16:])
+
+
+# --- sinusoidal PE ----------------------------------------------------------------
+@pytest.mark.parametrize("dm", [896, 64])
+def test_sinusoidal_pe_closed_form(golden, dm):
+    rows = golden[f"pe_rows_{dm}"]
+    pe = oracle.sinusoidal_pe(int(rows.max()) + 1, dm).reshape(-1, dm)[rows]
+    assert_close(pe, golden[f"pe64_{dm}"], 0, 2.4e-7, f"pe d={dm}")
+    if rows[0] == 0:
+        half = dm // 2
+        assert np.all(pe[0, :half] == 0.0) and np.all(pe[0, half:] == 1.0)
+
+
+# --- gathers ---------------------------------------------------------------------
+def test_gathers_bit_exact(golden):
+    ids = golden["gather_ids"]
+    np.testing.assert_array_equal(oracle.embed_gather_f32(golden["gather_tab32"], ids, 24),
+                                  golden["gather_tab32"][ids].ravel())
+    np.testing.assert_array_equal(oracle.embed_gather_bf16(golden["gather_bits"], ids, 24),
+                                  golden["gather_bf16_exp"].ravel())
+    np.testing.assert_array_equal(
+        oracle.embed_gather_i8(golden["gather_tab8"], golden["gather_sc8"], ids, 24),
+        golden["gather_i8_exp"].ravel())
+
+
+# --- quantizer ---------------------------------------------------------------------
+def test_quantizer_bit_exact_with_ties_and_specials(golden):
+    x = golden["quant_x"]
+    q, s = oracle.quantize_f32_to_int8(x.ravel(), x.shape[0], x.shape[1])
+    np.testing.assert_array_equal(q.reshape(x.shape), golden["quant_q"])
+    np.testing.assert_array_equal(s, golden["quant_s"])
+    row = q.reshape(x.shape)[1]
+    assert list(row[2:10]) == [3, -3, 1, -1, 2, -2, 127, -127]  # half away from zero
+    assert np.all(q.reshape(x.shape)[2] == 0) and s[2] == 0.0    # all-zero row
+
+
+def test_quantizer_bf16_matches_f32_path():
+    r = np.random.default_rng(11)
+    x = (0.02 * r.standard_normal(4 * 96)).astype(np.float32)
+    bits = (x.view(np.uint32) >> 16).astype(np.uint16)
+    xb = (bits.astype(np.uint32) << 16).view(np.float32)
+    q1, s1 = oracle.quantize_bf16_to_int8(bits, 4, 96)
+    q2, s2 = oracle.quantize_f32_to_int8(xb, 4, 96)
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_array_equal(s1, s2)
+
+
+# --- INT8 matvec / W8A8 -------------------------------------------------------------
+def test_w8a8_dots_bit_exact_and_epilogue(golden):
+    w, s, xq, xs = golden["w8a8_w"], golden["w8a8_s"], golden["w8a8_xq"], golden["w8a8_xs"]
+    B, K = xq.shape
+    inter = w.shape[0] // 2
+    out, dots = oracle.gate_up_swiglu_w8a8(w, s, xq, xs, B, K, inter)
+    np.testing.assert_array_equal(dots.reshape(B, 2 * inter), golden["w8a8_dots"])
+    assert_close(out.reshape(B, inter), golden["w8a8_y64"], 2e-6, 1e-9, "w8a8 out")
+
+
+def test_w8a32_closed_form(golden):
+    w, s, x = golden["w8a8_w"], golden["w8a8_s"], golden["w8a32_x"]
+    y = oracle.linear_nobias_int8(x, w, s, 2, w.shape[1], w.shape[0]).reshape(2, -1)
+    ref = golden["w8a32_y64"]
+    assert_close(y, ref, 1e-5, 1e-6 * np.abs(ref).max(), "w8a32")
+    # threaded row chunking gives identical rows
+    y4 = oracle.linear_nobias_int8(x, w, s, 2, w.shape[1], w.shape[0], n_threads=4)
+    np.testing.assert_array_equal(y4, y.ravel())
+
+
+def test_w8a32_is_exact_on_integer_inputs(golden):
+    # With integer-valued x and unit scales the reference's f32 sum is exact
+    # (partial sums < 2^24), so linear_nobias_int8 reproduces the int32 W8A8 dot.
+    w, xq = golden["w8a8_w"], golden["w8a8_xq"]
+    B, K = xq.shape
+    y = oracle.linear_nobias_int8(xq.astype(np.float32), w, np.ones(w.shape[0], np.float32), B, K,
+                                  w.shape[0]).reshape(B, -1)
+    np.testing.assert_array_equal(y.astype(np.int64), golden["w8a8_dots"].astype(np.int64))
+
+
+def test_interleave_layout():
+    r = np.random.default_rng(5)
+    inter, hid = 6, 32
+    wg = r.integers(-128, 128, (inter, hid), dtype=np.int8)
+    wu = r.integers(-128, 128, (inter, hid), dtype=np.int8)
+    sg = r.random(inter).astype(np.float32)
+    su = r.random(inter).astype(np.float32)
+    wgu, sgu = oracle.interleave_gate_up(wg, sg, wu, su, inter, hid)
+    wgu = wgu.reshape(2 * inter, hid)
+    np.testing.assert_array_equal(wgu[0::2], wg)
+    np.testing.assert_array_equal(wgu[1::2], wu)
+    np.testing.assert_array_equal(sgu[0::2], sg)
+    np.testing.assert_array_equal(sgu[1::2], su)
