@@ -249,9 +249,9 @@ class C4Int8Matvec(Workload):
 
 class C5BatchedDecode(Workload):
     name = "c5"
-    description = ("qwen3-asr-1.7b batched decode B=256 (positions U[0,2047]): add+RMSNorm[256,2048] + "
-                   "q/k head-RMSNorm+RoPE + per-row int8 quantize + W8A8 MFMA gate/up GEMM "
-                   "[256,2048]x[2048,12288] + SwiGLU; 28 distinct layers rotate")
+    description = ("qwen3-asr-1.7b batched decode B=256 (positions U[0,2047]): add+RMSNorm[256,2048] "
+                   "fused with per-row int8 quantization + q/k head-RMSNorm+RoPE + W8A8 MFMA gate/up "
+                   "GEMM [256,2048]x[2048,12288] + SwiGLU; 28 distinct layers rotate")
     unit_tokens = 256
 
     def __init__(self, dev, torch):
@@ -270,7 +270,6 @@ class C5BatchedDecode(Workload):
         S = L
         self.x = [self.randn(B * H) for _ in range(S)]
         self.d = [self.randn(B * H) for _ in range(S)]
-        self.y = [torch.empty(B * H, device=dev) for _ in range(S)]
         self.q = [self.randn(B * nq * hd) for _ in range(S)]
         self.k = [self.randn(B * nk * hd) for _ in range(S)]
         self.xq = [torch.empty(B * H, dtype=torch.int8, device=dev) for _ in range(S)]
@@ -283,14 +282,13 @@ class C5BatchedDecode(Workload):
         self.pos = [torch.randint(0, 2048, (B,), generator=self.gen, device=dev, dtype=torch.int32)
                     for _ in range(S)]
         self.kernels = {
-            "add_rms_norm": (lambda i: K.add_rms_norm(self.x[i % S], self.d[i % S], self.w, self.y[i % S], B, H, c["eps"]),
-                             5 * B * H * F + H * F),
+            "add_rms_norm_quant": (lambda i: K.add_rms_norm_quant(
+                self.x[i % S], self.d[i % S], self.w, None, self.xq[i % S], self.xsc[i % S], B, H, c["eps"]),
+                3 * B * H * F + H * F + B * H + B * F),
             "head_rms_norm_rope": (lambda i: K.head_rms_norm_rope(
                 self.q[i % S], self.k[i % S], self.qw, self.kw, self.rope.cos, self.rope.sin,
                 self.pos[i % S], B, nq, nk, hd, c["eps"]),
                 2 * B * (nq + nk) * hd * F + 2 * hd * F + 2 * B * hd * F + B * 4),
-            "quantize_rows": (lambda i: K.quantize_rows_i8(self.xq[i % S], self.xsc[i % S], self.y[i % S], B, H),
-                              B * H * F + B * H + B * F),
             "gate_up_swiglu_w8a8_gemm": (lambda i: K.gate_up_swiglu_w8a8(
                 self.o[i % S], self.layers[i % L], self.xq[i % S], self.xsc[i % S], B, H, I),
                 2 * I * H + 2 * I * F + B * H + B * F + B * I * F),

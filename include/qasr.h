@@ -66,6 +66,17 @@ int qasr_add_rms_norm_f32(float* x, const float* delta, const float* weight,
                           float* out, size_t seq_len, size_t hidden, float eps,
                           void* stream);
 
+/* Fused residual add + RMSNorm + per-row int8 quantization of the normalised
+ * row (the activation side of a W8A8 projection):
+ *   x[s,:] += delta[s,:] (skipped when delta == NULL); y = rms_norm(x[s,:]);
+ *   q[s,:], q_scales[s] = quantize_rows_i8(y) (qasr_quantize_rows_i8 arithmetic).
+ * out (may be NULL) receives y in fp32. Replaces add_inplace + rms_norm +
+ * the activation quantization feeding the gate/up projection
+ * (decoder.rs:908-914; kernels/mod.rs:486-488, 897-918; quantize.rs:633-662). */
+int qasr_add_rms_norm_quant_f32(float* x, const float* delta, const float* weight,
+                                float* out, int8_t* q, float* q_scales, size_t seq_len,
+                                size_t hidden, float eps, void* stream);
+
 /* LayerNorm: out = ((x - mean) * inv_std) * weight + bias (fused multiply-add),
  * inv_std = 1/sqrt(var + eps), two-pass mean/variance per row.
  * Replaces kernels::layer_norm (kernels/mod.rs:866-895, avx.rs:417-481). */

@@ -42,6 +42,7 @@ SIGNATURES: dict[str, list] = {
     "qasr_add_inplace_f32": [P, P, Z, P],
     "qasr_rms_norm_f32": [P, P, P, Z, Z, F, P],
     "qasr_add_rms_norm_f32": [P, P, P, P, Z, Z, F, P],
+    "qasr_add_rms_norm_quant_f32": [P, P, P, P, P, P, Z, Z, F, P],
     "qasr_layer_norm_f32": [P, P, P, P, Z, Z, F, P],
     "qasr_rms_norm_per_head_f32": [P, P, Z, Z, Z, F, P],
     "qasr_apply_rope_neox_f32": [P, P, P, Z, Z, Z, P],

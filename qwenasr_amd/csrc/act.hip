@@ -23,25 +23,27 @@ QASR_DEV float swiglu_ref(float g, float u, bool fast) {
   return s * u;
 }
 
+// One output float4 per thread over an exact grid. Without a row tail
+// (inter % 8 == 0) every column takes the fast_exp path and no row index is
+// needed; with one, the column comes from a 32-bit division.
+template <bool HAS_TAIL>
 __global__ __launch_bounds__(256) void swiglu_interleaved_vec_kernel(
-    float* out, const float* gu, size_t rows, int inter) {
-  const int i4 = inter >> 2;
-  const int fast_end = inter & ~7;
-  const size_t n4 = rows * (size_t)i4;
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-    const size_t r = i / i4;
-    const int j = (int)(i - r * i4) * 4;
-    const float* src = gu + r * 2 * (size_t)inter + 2 * j;
-    const float4 a = ld4(src, 0);  // g_j, u_j, g_j+1, u_j+1
-    const float4 b = ld4(src, 1);  // g_j+2, u_j+2, g_j+3, u_j+3
-    const bool fast = j < fast_end;  // a 4-block never straddles an 8-block edge
-    float4 o;
-    o.x = swiglu_ref(a.x, a.y, fast);
-    o.y = swiglu_ref(a.z, a.w, fast);
-    o.z = swiglu_ref(b.x, b.y, fast);
-    o.w = swiglu_ref(b.z, b.w, fast);
-    st4(out, i, o);
+    float* out, const float* gu, size_t n4, unsigned i4, unsigned fast_end) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const float4 a = ld4_nt(gu, 2 * i);      // g_j, u_j, g_j+1, u_j+1
+  const float4 b = ld4_nt(gu, 2 * i + 1);  // g_j+2, u_j+2, g_j+3, u_j+3
+  bool fast = true;
+  if constexpr (HAS_TAIL) {
+    const unsigned j = (unsigned)(i % i4) * 4;
+    fast = j < fast_end;  // a 4-block never straddles an 8-block edge
   }
+  float4 o;
+  o.x = swiglu_ref(a.x, a.y, fast);
+  o.y = swiglu_ref(a.z, a.w, fast);
+  o.z = swiglu_ref(b.x, b.y, fast);
+  o.w = swiglu_ref(b.z, b.w, fast);
+  st4_nt(out, i, o);
 }
 
 __global__ __launch_bounds__(256) void swiglu_interleaved_scalar_kernel(
@@ -62,16 +64,16 @@ __global__ __launch_bounds__(256) void swiglu_interleaved_scalar_kernel(
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void swiglu_split_vec_kernel(float* out, const float* g,
                                                                const float* u, size_t n4) {
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-    const float4 a = ld4(g, i);
-    const float4 b = ld4(u, i);
-    float4 o;
-    o.x = silu_expf(a.x) * b.x;
-    o.y = silu_expf(a.y) * b.y;
-    o.z = silu_expf(a.z) * b.z;
-    o.w = silu_expf(a.w) * b.w;
-    st4(out, i, o);
-  }
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const float4 a = ld4_nt(g, i);
+  const float4 b = ld4_nt(u, i);
+  float4 o;
+  o.x = silu_expf(a.x) * b.x;
+  o.y = silu_expf(a.y) * b.y;
+  o.z = silu_expf(a.z) * b.z;
+  o.w = silu_expf(a.w) * b.w;
+  st4_nt(out, i, o);
 }
 
 __global__ __launch_bounds__(256) void swiglu_split_scalar_kernel(float* out, const float* g,
@@ -108,23 +110,49 @@ QASR_DEV float gelu_tanh_ref(float v, bool fast) {
   return (0.5f * v) * (1.0f + tanhf(inner));
 }
 
-// Exact GELU, 0.5*x*(1+erf(x/sqrt2)) written as 0.5*x*erfc(-x/sqrt2) so the
-// negative tail keeps its relative accuracy (no 1 + erf cancellation).
-QASR_DEV float gelu_erf(float v) { return 0.5f * v * erfcf(-v * 0.70710678118654752f); }
+// Exact GELU, 0.5*x*(1+erf(x/sqrt2)) = x*sigmoid(Q(x)) with
+// Q(x) = 2*artanh(erf(x/sqrt2)) approximated on |x| <= 6 by the odd polynomial
+// x*P(x^2) below (weighted minimax fit; gelu_erf_fit.py derives the
+// coefficients and bounds the float32 error of exactly this evaluation by
+// 3.1e-7 absolute against float64, including 1-ulp error in exp2 and rcp).
+//   e = exp(-|q|) <= 1, t = x*e/(1+e) = x*sigmoid(-|q|)
+//   gelu = x - t (x >= 0), t (x < 0), 0 (x < -6)
+// Neither branch cancels and nothing overflows. ~20 VALU per element.
+QASR_DEV float gelu_erf(float x) {
+  constexpr float c0 = 1.5957684516906738f, c1 = 0.07266856729984283f;
+  constexpr float c2 = -6.625994137721136e-05f, c3 = -0.00011048033047700301f;
+  constexpr float c4 = 7.938220733194612e-06f, c5 = -2.668929255378316e-07f;
+  constexpr float c6 = 3.6112353107853323e-09f;
+  const float xc = fminf(fmaxf(x, -6.0f), 6.0f);
+  const float x2 = xc * xc;
+  float p = __builtin_fmaf(c6, x2, c5);
+  p = __builtin_fmaf(p, x2, c4);
+  p = __builtin_fmaf(p, x2, c3);
+  p = __builtin_fmaf(p, x2, c2);
+  p = __builtin_fmaf(p, x2, c1);
+  p = __builtin_fmaf(p, x2, c0);
+  const float q = xc * p;
+  const float e = __builtin_amdgcn_exp2f(fabsf(q) * -1.4426950408889634f);
+  const float t = (x * e) * __builtin_amdgcn_rcpf(1.0f + e);
+  const float g = x >= 0.0f ? x - t : t;
+  // beyond the clamp: exact tails (x * Phi(x) rounds to x above 6 and its
+  // magnitude is below 6e-9 under -6); this also keeps +inf -> +inf
+  return x > 6.0f ? x : (x < -6.0f ? 0.0f : g);
+}
 
 template <bool ERF>
 __global__ __launch_bounds__(256) void gelu_vec_kernel(float* x, size_t n4, size_t fast_end) {
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-    float4 v = ld4(x, i);
-    if constexpr (ERF) {
-      v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
-    } else {
-      const bool f = 4 * i < fast_end;
-      v.x = gelu_tanh_ref(v.x, f); v.y = gelu_tanh_ref(v.y, f);
-      v.z = gelu_tanh_ref(v.z, f); v.w = gelu_tanh_ref(v.w, f);
-    }
-    st4(x, i, v);
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  float4 v = ld4_nt(x, i);
+  if constexpr (ERF) {
+    v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
+  } else {
+    const bool f = 4 * i < fast_end;
+    v.x = gelu_tanh_ref(v.x, f); v.y = gelu_tanh_ref(v.y, f);
+    v.z = gelu_tanh_ref(v.z, f); v.w = gelu_tanh_ref(v.w, f);
   }
+  st4_nt(x, i, v);
 }
 
 template <bool ERF>
@@ -164,17 +192,18 @@ __global__ __launch_bounds__(256) void sinusoidal_pe_kernel(float* pe, long long
   }
 }
 
-// x[r,:] += pe[r % n_pos, :]
-__global__ __launch_bounds__(256) void pe_add_vec_kernel(float* x, const float* pe, size_t rows,
-                                                         int d4, int n_pos) {
-  const size_t n4 = rows * (size_t)d4;
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-    const size_t r = i / d4;
-    const int c = (int)(i - r * d4);
-    float4 v = ld4(x, i);
-    const float4 p = ld4(pe, (size_t)(r % n_pos) * d4 + c);
+// x[r,:] += pe[r % n_pos, :]: one workgroup per row, so the PE row index is
+// computed once per row (the 13-row table stays in L2).
+__global__ __launch_bounds__(256) void pe_add_vec_kernel(float* x, const float* pe, int d4,
+                                                         int n_pos) {
+  const size_t r = blockIdx.x;
+  const float* pr = pe + (size_t)(r % (size_t)n_pos) * d4 * 4;
+  float* xr = x + r * (size_t)d4 * 4;
+  for (int c = threadIdx.x; c < d4; c += 256) {
+    float4 v = ld4_nt(xr, c);
+    const float4 p = ld4(pr, c);
     v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
-    st4(x, i, v);
+    st4_nt(xr, c, v);
   }
 }
 
@@ -202,9 +231,16 @@ extern "C" int qasr_swiglu_multiply_f32(float* out, const float* gate_up, size_t
                "swiglu_multiply: size overflows");
   hipStream_t st = as_stream(stream);
   const int inter = (int)intermediate;
-  if (intermediate % 4 == 0 && aligned16(out) && aligned16(gate_up)) {
+  if (intermediate % 4 == 0 && aligned16(out) && aligned16(gate_up) &&
+      exact_grid_ok(seq_len * (intermediate / 4))) {
     const size_t n4 = seq_len * (intermediate / 4);
-    swiglu_interleaved_vec_kernel<<<grid_for(n4, 256), 256, 0, st>>>(out, gate_up, seq_len, inter);
+    const unsigned grid = (unsigned)((n4 + 255) / 256);
+    if (intermediate % 8 == 0) {
+      swiglu_interleaved_vec_kernel<false><<<grid, 256, 0, st>>>(out, gate_up, n4, 0, 0);
+    } else {
+      swiglu_interleaved_vec_kernel<true><<<grid, 256, 0, st>>>(
+          out, gate_up, n4, (unsigned)(intermediate / 4), (unsigned)(intermediate & ~(size_t)7));
+    }
   } else {
     swiglu_interleaved_scalar_kernel<<<grid_for(seq_len * intermediate, 256), 256, 0, st>>>(
         out, gate_up, seq_len, inter);
@@ -219,9 +255,9 @@ extern "C" int qasr_swiglu_split_f32(float* out, const float* gate, const float*
   QASR_REQUIRE(n <= kMaxElems, "swiglu_split: n too large");
   hipStream_t st = as_stream(stream);
   size_t done = 0;
-  if (aligned16(out) && aligned16(gate) && aligned16(up)) {
+  if (aligned16(out) && aligned16(gate) && aligned16(up) && exact_grid_ok(n / 4)) {
     const size_t n4 = n / 4;
-    if (n4) swiglu_split_vec_kernel<<<grid_for(n4, 256), 256, 0, st>>>(out, gate, up, n4);
+    if (n4) swiglu_split_vec_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, st>>>(out, gate, up, n4);
     done = n4 * 4;
   }
   if (done < n) {
@@ -246,9 +282,9 @@ static int launch_gelu(float* x, size_t n, void* stream) {
   hipStream_t st = as_stream(stream);
   const size_t fast_end = n & ~(size_t)7;
   size_t done = 0;
-  if (aligned16(x)) {
+  if (aligned16(x) && exact_grid_ok(n / 4)) {
     const size_t n4 = n / 4;
-    if (n4) gelu_vec_kernel<ERF><<<grid_for(n4, 256), 256, 0, st>>>(x, n4, fast_end);
+    if (n4) gelu_vec_kernel<ERF><<<(unsigned)((n4 + 255) / 256), 256, 0, st>>>(x, n4, fast_end);
     done = n4 * 4;
   }
   if (done < n) {
@@ -288,10 +324,8 @@ extern "C" int qasr_pe_add_f32(float* x, const float* pe, size_t rows, size_t d_
   QASR_REQUIRE(mul_ok(rows, d_model, &n) && d_model < 0x7fffffffu && n_pos < 0x7fffffffu,
                "pe_add: size overflows");
   hipStream_t st = as_stream(stream);
-  if (d_model % 4 == 0 && aligned16(x) && aligned16(pe)) {
-    const size_t n4 = n / 4;
-    pe_add_vec_kernel<<<grid_for(n4, 256), 256, 0, st>>>(x, pe, rows, (int)(d_model / 4),
-                                                          (int)n_pos);
+  if (d_model % 4 == 0 && aligned16(x) && aligned16(pe) && rows <= kMaxRows) {
+    pe_add_vec_kernel<<<(unsigned)rows, 256, 0, st>>>(x, pe, (int)(d_model / 4), (int)n_pos);
   } else {
     pe_add_scalar_kernel<<<grid_for(n, 256), 256, 0, st>>>(x, pe, rows, (int)d_model, (int)n_pos);
   }

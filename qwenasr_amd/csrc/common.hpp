@@ -93,6 +93,22 @@ QASR_DEV float block_max(float v, float* lds) {
 }
 
 // ---------------------------------------------------------------------------
+// 16-byte streaming loads/stores. The nontemporal forms mark the lines for
+// early eviction, which suits data each kernel touches exactly once.
+// ---------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+QASR_DEV float4 ld4_nt(const float* p, size_t i) {
+  const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p) + i);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+QASR_DEV void st4_nt(float* p, size_t i, float4 v) {
+  const v4f o = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(o, reinterpret_cast<v4f*>(p) + i);
+}
+
+// ---------------------------------------------------------------------------
 // Scalar math shared by several kernels
 // ---------------------------------------------------------------------------
 
@@ -156,6 +172,13 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // Largest size any kernel indexes with 64-bit arithmetic; guards products of
 // dimensions against overflow.
 constexpr size_t kMaxElems = (size_t)1 << 40;
+
+// A launch's total work-item count (grid x workgroup size) must fit in 32
+// bits; exact-cover grids of 256-thread workgroups stay below this bound.
+constexpr size_t kMaxGridItems = ((size_t)1 << 32) - 256;
+inline bool exact_grid_ok(size_t items) { return items <= kMaxGridItems; }
+// Most rows one row-per-workgroup launch may cover.
+constexpr size_t kMaxRows = (size_t)1 << 24;
 
 inline bool mul_ok(size_t a, size_t b, size_t* out) {
   if (a != 0 && b > kMaxElems / a) return false;

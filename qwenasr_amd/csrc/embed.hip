@@ -84,7 +84,7 @@ int launch_gather(float* out, const void* table, const float* scales, const int3
   if (n == 0 || dim == 0) return QASR_OK;
   QASR_REQUIRE(out && table && ids && (MODE != 2 || scales), "embed_gather: null pointer");
   QASR_REQUIRE(vocab > 0, "embed_gather: vocab must be positive");
-  QASR_REQUIRE(n <= 0x7fffffffu && dim <= 0x7fffffffu, "embed_gather: size too large");
+  QASR_REQUIRE(n <= kMaxRows && dim <= 0x7fffffffu, "embed_gather: size too large");
   size_t tab;
   QASR_REQUIRE(mul_ok(vocab, dim, &tab), "embed_gather: vocab * dim overflows");
   const int per = MODE == 0 ? 4 : (MODE == 1 ? 8 : 16);

@@ -10,11 +10,20 @@
 //
 // v_mfma_i32_16x16x64_i8: lane l supplies 16 int8 of A row (l % 16) and 16 int8
 // of B column (l % 16) for k-group (l / 16); the result lane l holds
-// D[4*(l/16) + v][l % 16], v = 0..3. The exact k order inside a group does not
+// D[4*(l/16) + v][l % 16], v = 0..3. The order of k inside an MFMA does not
 // matter as long as A and B use the same one, which they do: lane l loads bytes
 // [k0 + 16*(l/16), +16) of its W row and of its Xq row. With A = W and B = Xq^T a
 // lane's four results are four consecutive W rows for one token -- two complete
 // gate/up pairs -- so the SwiGLU epilogue needs no data exchange.
+//
+// Main kernel (gemm_w8a8_swiglu_lds_kernel, K = 1024 or 2048): a workgroup
+// owns 192 W rows x 64 tokens. The 64 token rows of Xq (64 x K bytes) are
+// staged once in LDS by direct global->LDS loads, with a 16-byte row pad
+// (conflict-free b128 reads); each of the 4 waves owns 48 distinct W rows and
+// streams them from HBM into registers with a PREFETCH-deep software pipeline,
+// so W never touches LDS. The 4 workgroups that share a W tile (one per 64-token block) are
+// dispatched to the same XCD back to back, so 3 of their 4 W reads hit that
+// XCD's L2. gemm_w8a8_swiglu_kernel is the shape-generic fallback.
 #pragma once
 
 #include "common.hpp"
@@ -23,13 +32,154 @@ namespace qasr {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+constexpr int kGemmK = 64;  // k per MFMA
+
+// ---------------------------------------------------------------------------
+// Main kernel
+// ---------------------------------------------------------------------------
+constexpr int kLdsBN = 192;           // W rows per workgroup
+constexpr int kLdsBM = 64;            // tokens per workgroup
+constexpr int kLdsWaveRows = 48;      // W rows per wave (3 MFMA row tiles)
+constexpr int kLdsMaxK = 2048;        // X tile must fit LDS: 64 x (2048 + 16) B
+constexpr int kLdsRowPad = 16;
+constexpr int kPrefetch = 8;          // k-steps of W in flight per wave
+constexpr int kNumXcd = 8;
+
+template <int KSTEPS>  // K / 64
+__global__ __launch_bounds__(256) void gemm_w8a8_swiglu_lds_kernel(
+    float* __restrict__ out, const int8_t* __restrict__ w, const float* __restrict__ scales,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, int batch, int inter,
+    int n_tiles, int m_tiles) {
+  constexpr int K = KSTEPS * kGemmK;
+  constexpr int LDS_STRIDE = K + kLdsRowPad;
+  extern __shared__ __align__(16) int8_t xlds[];  // [64][K + 16]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+
+  // XCD-aware tile order: consecutive blocks go to consecutive XCDs, so block
+  // b runs on XCD b % 8. Put the m_tiles blocks of one W tile on one XCD.
+  const int b = blockIdx.x;
+  const int xcd = b % kNumXcd;
+  const int slot = b / kNumXcd;
+  int tile_n, tile_m;
+  if (n_tiles % kNumXcd == 0) {
+    tile_m = slot % m_tiles;
+    tile_n = xcd + kNumXcd * (slot / m_tiles);
+  } else {
+    tile_m = b % m_tiles;
+    tile_n = b / m_tiles;
+  }
+  const int n_wave = tile_n * kLdsBN + wave * kLdsWaveRows;
+  const int m0 = tile_m * kLdsBM;
+
+  // W row pointers for this wave's three 16-row tiles (lane row r, group g).
+  const int8_t* wp[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) wp[i] = w + (size_t)(n_wave + 16 * i + r) * K + 16 * g;
+
+  // Stage Xq rows m0..m0+63 into LDS with direct global->LDS loads: each wave
+  // instruction moves 64 lanes x 16 bytes into 1 KiB of contiguous LDS (half or
+  // all of a K=2048 / K=1024 row), so the 128 KiB tile is in flight at once with
+  // no register round trip. Rows past the batch re-read row batch-1 (valid
+  // memory); their results are never stored.
+  {
+    constexpr int CHUNKS_PER_ROW = K / 1024;
+    constexpr int CHUNKS = kLdsBM * CHUNKS_PER_ROW;
+#pragma unroll 4
+    for (int c = wave; c < CHUNKS; c += 4) {
+      const int row = c / CHUNKS_PER_ROW, half = c - row * CHUNKS_PER_ROW;
+      const int src_row = m0 + row < batch ? m0 + row : batch - 1;
+      const int8_t* src = xq + (size_t)src_row * K + 1024 * half + 16 * lane;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)src,
+          (__attribute__((address_space(3))) void*)(xlds + row * LDS_STRIDE + 1024 * half), 16, 0, 0);
+    }
+  }
+
+  // Start the W stream; its HBM latency overlaps the LDS fill.
+  v4i wbuf[kPrefetch][3];
+#pragma unroll
+  for (int d = 0; d < kPrefetch; ++d)
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (d < KSTEPS) wbuf[d][i] = *reinterpret_cast<const v4i*>(wp[i] + d * kGemmK);
+
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0);  // the LDS fill (and the W prefetch) have landed
+  __syncthreads();
+
+  v4i acc[3][4];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  const int8_t* xl = xlds + r * LDS_STRIDE + 16 * g;
+#pragma unroll
+  for (int s0 = 0; s0 < KSTEPS; s0 += kPrefetch) {
+#pragma unroll
+    for (int d = 0; d < kPrefetch; ++d) {
+      const int s = s0 + d;
+      if (s < KSTEPS) {
+        v4i a[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          a[i] = wbuf[d][i];
+          if (s + kPrefetch < KSTEPS)
+            wbuf[d][i] = *reinterpret_cast<const v4i*>(wp[i] + (s + kPrefetch) * kGemmK);
+        }
+        // Keep the prefetch issue here: without this fence the scheduler sinks
+        // each load next to its use and the pipeline collapses to one load in
+        // flight per k-step.
+        __builtin_amdgcn_sched_barrier(0);
+        v4i bx[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bx[j] = *reinterpret_cast<const v4i*>(xl + 16 * j * LDS_STRIDE + s * kGemmK);
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bx[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // Epilogue: lane holds W rows n_wave + 16i + 4g + {0..3} for token m0 + 16j + r.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = m0 + 16 * j + r;
+    if (m >= batch) continue;
+    const float xsm = xs[m];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int n = n_wave + 16 * i + 4 * g;
+      const float4 sc = *reinterpret_cast<const float4*>(scales + n);
+      float2 o;
+      {
+        const float gg = ((float)acc[i][j][0] * xsm) * sc.x;
+        const float uu = ((float)acc[i][j][1] * xsm) * sc.y;
+        o.x = (gg / (1.0f + expf(-gg))) * uu;
+      }
+      {
+        const float gg = ((float)acc[i][j][2] * xsm) * sc.z;
+        const float uu = ((float)acc[i][j][3] * xsm) * sc.w;
+        o.y = (gg / (1.0f + expf(-gg))) * uu;
+      }
+      *reinterpret_cast<float2*>(out + (size_t)m * inter + (n >> 1)) = o;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Shape-generic fallback: 64 x 64 tiles, operands straight from global memory.
+// ---------------------------------------------------------------------------
 constexpr int kGemmBN = 64;  // W rows per workgroup (32 gate/up pairs)
 constexpr int kGemmBM = 64;  // tokens per workgroup
-constexpr int kGemmK = 64;   // k per MFMA
 
-// Workgroup = 4 waves in a 2x2 layout; each wave owns 32 W rows x 32 tokens =
-// 2 x 2 MFMA tiles. Operands come straight from global memory (the W slice is
-// shared with the neighbouring wave through L1/L2).
 __global__ __launch_bounds__(256) void gemm_w8a8_swiglu_kernel(
     float* __restrict__ out, const int8_t* __restrict__ w, const float* __restrict__ scales,
     const int8_t* __restrict__ xq, const float* __restrict__ xs, int batch, int K, int inter) {
@@ -73,7 +223,6 @@ __global__ __launch_bounds__(256) void gemm_w8a8_swiglu_kernel(
         acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
   }
 
-  // Epilogue: lane holds rows n0 + 16i + 4g + {0,1,2,3} for token m0 + 16j + r.
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int m = m0 + 16 * j + r;
@@ -103,6 +252,38 @@ inline bool gemm_w8a8_supported(size_t batch, size_t K, size_t inter) {
   return batch >= 1 && K % kGemmK == 0 && (2 * inter) % kGemmBN == 0;
 }
 
+inline bool gemm_w8a8_lds_shape(size_t K, size_t inter) {
+  return (K == 1024 || K == 2048) && (2 * inter) % kLdsBN == 0;
+}
+
+// Raises the dynamic-LDS limit of one kernel instance once (the default limit
+// is 64 KiB; the staged X tile needs up to 64 x 2064 bytes). Returns false if
+// the device cannot give a workgroup that much LDS.
+template <int KSTEPS>
+bool lds_kernel_ready(size_t lds) {
+  static const bool ok = [lds] {
+    int dev = 0, max_lds = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      return false;
+    if ((size_t)max_lds < (size_t)kLdsBM * (kLdsMaxK + kLdsRowPad)) return false;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_w8a8_swiglu_lds_kernel<KSTEPS>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, max_lds) == hipSuccess;
+  }();
+  (void)lds;
+  return ok;
+}
+
+template <int KSTEPS>
+bool launch_lds_gemm(float* out, const int8_t* w, const float* scales, const int8_t* xq,
+                     const float* xs, int batch, int inter, int n_tiles, int m_tiles,
+                     size_t lds, hipStream_t st) {
+  if (!lds_kernel_ready<KSTEPS>(lds)) return false;
+  gemm_w8a8_swiglu_lds_kernel<KSTEPS><<<(unsigned)(n_tiles * m_tiles), 256, lds, st>>>(
+      out, w, scales, xq, xs, batch, inter, n_tiles, m_tiles);
+  return true;
+}
+
 inline int gemm_w8a8_swiglu(float* out, const int8_t* w, const float* scales, const int8_t* xq,
                             const float* xs, size_t batch, size_t K, size_t inter,
                             hipStream_t st) {
@@ -110,6 +291,19 @@ inline int gemm_w8a8_swiglu(float* out, const int8_t* w, const float* scales, co
   // every row start 8-byte aligned once out is.
   if ((reinterpret_cast<uintptr_t>(out) & 7u) != 0) {
     return fail(QASR_ERR_INVALID_ARG, "gate_up_swiglu_w8a8: out must be 8-byte aligned");
+  }
+  if (gemm_w8a8_lds_shape(K, inter) && aligned16(scales) &&
+      (2 * inter / kLdsBN) * ((batch + kLdsBM - 1) / kLdsBM) <= 0x7fffffffu) {
+    const int n_tiles = (int)((2 * inter) / kLdsBN);
+    const int m_tiles = (int)((batch + kLdsBM - 1) / kLdsBM);
+    const size_t lds = (size_t)kLdsBM * (K + kLdsRowPad);
+    bool launched = false;
+    if (K == 1024) {
+      launched = launch_lds_gemm<16>(out, w, scales, xq, xs, (int)batch, (int)inter, n_tiles, m_tiles, lds, st);
+    } else {
+      launched = launch_lds_gemm<32>(out, w, scales, xq, xs, (int)batch, (int)inter, n_tiles, m_tiles, lds, st);
+    }
+    if (launched) return launch_status("gate_up_swiglu_w8a8 (mfma, lds)");
   }
   const size_t n_tiles = (2 * inter) / kGemmBN;
   const size_t m_tiles = (batch + kGemmBM - 1) / kGemmBM;

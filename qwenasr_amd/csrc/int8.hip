@@ -17,6 +17,44 @@ QASR_DEV float4 ld4(const float* p, size_t i) { return reinterpret_cast<const fl
 // ---------------------------------------------------------------------------
 // Per-row quantizer, quantize.rs:633-662.
 // ---------------------------------------------------------------------------
+// Register-resident variant: one workgroup per row, NV float4 per thread,
+// one read of x and one write of q.
+template <int NV>
+__global__ __launch_bounds__(256) void quantize_rows_vec_kernel(int8_t* q, float* scales,
+                                                                const float* x, int cols) {
+  __shared__ float red[256 / kWave];
+  const int c4 = cols >> 2;
+  const size_t base = (size_t)blockIdx.x * c4;
+  float4 v[NV];
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < c4) {
+      v[i] = ld4(x, base + c);
+      const float a0 = fabsf(v[i].x), a1 = fabsf(v[i].y), a2 = fabsf(v[i].z), a3 = fabsf(v[i].w);
+      if (a0 > m) m = a0;
+      if (a1 > m) m = a1;
+      if (a2 > m) m = a2;
+      if (a3 > m) m = a3;
+    }
+  }
+  m = block_max<256>(m, red);
+  const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+  if (threadIdx.x == 0) scales[blockIdx.x] = m / 127.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < c4) {
+      const uint32_t b = (uint32_t)(quant_i8(v[i].x, inv) & 0xff) |
+                         ((uint32_t)(quant_i8(v[i].y, inv) & 0xff) << 8) |
+                         ((uint32_t)(quant_i8(v[i].z, inv) & 0xff) << 16) |
+                         ((uint32_t)(quant_i8(v[i].w, inv) & 0xff) << 24);
+      reinterpret_cast<uint32_t*>(q)[base + c] = b;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void quantize_rows_kernel(int8_t* q, float* scales,
                                                             const float* x, int cols) {
   __shared__ float red[256 / kWave];
@@ -142,22 +180,15 @@ QASR_DEV int dot16(v4i a, v4i b, int acc) {
 // with the per-vector absmax of the whole input (wave-wide max), packing them
 // into int8x16 registers; returns the vector's scale.
 template <int KCH>
-QASR_DEV float quantize_lane_slices(const float* x, int lane, v4i* xq) {
-  float v[KCH][16];
+QASR_DEV float quantize_lane_values(const float (&v)[KCH][16], v4i* xq) {
   float m = 0.0f;
 #pragma unroll
-  for (int c = 0; c < KCH; ++c) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float4 f = ld4(x + c * 1024 + lane * 16 + 4 * t, 0);
-      v[c][4 * t] = f.x; v[c][4 * t + 1] = f.y; v[c][4 * t + 2] = f.z; v[c][4 * t + 3] = f.w;
-    }
+  for (int c = 0; c < KCH; ++c)
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
       const float a = fabsf(v[c][t]);
       if (a > m) m = a;
     }
-  }
   m = wave_max(m);
   const float inv = m > 0.0f ? 127.0f / m : 0.0f;
 #pragma unroll
@@ -184,7 +215,26 @@ __global__ __launch_bounds__(256) void gateup_matvec_kernel(float* out, const in
   const int pair0 = (blockIdx.x * (256 / kWave) + threadIdx.x / kWave) * NP;
   if (pair0 >= inter) return;
 
-  // Issue the weight stream first: NP pairs x 2 rows x KCH slices.
+  // Activations first: their loads (L2-resident) retire before the weight
+  // stream's, since a wave's vector loads complete in issue order.
+  v4i xq[KCH];
+  float xs = 0.0f;
+  float xv[F32IN ? KCH : 1][16];
+  if constexpr (F32IN) {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float4 f = ld4(xf + c * 1024 + lane * 16 + 4 * t, 0);
+        xv[c][4 * t] = f.x; xv[c][4 * t + 1] = f.y; xv[c][4 * t + 2] = f.z; xv[c][4 * t + 3] = f.w;
+      }
+  } else {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) xq[c] = reinterpret_cast<const v4i*>(xq8)[c * kWave + lane];
+    xs = xsc[0];
+  }
+
+  // Then the weight stream: NP pairs x 2 rows x KCH slices, all in flight.
   v4i wv[NP][2][KCH];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
@@ -196,15 +246,12 @@ __global__ __launch_bounds__(256) void gateup_matvec_kernel(float* out, const in
       for (int c = 0; c < KCH; ++c) wv[p][r][c] = __builtin_nontemporal_load(row + r * (K / 16) + c * kWave + lane);
   }
 
-  v4i xq[KCH];
-  float xs;
-  if constexpr (F32IN) {
-    xs = quantize_lane_slices<KCH>(xf, lane, xq);
-  } else {
-#pragma unroll
-    for (int c = 0; c < KCH; ++c) xq[c] = reinterpret_cast<const v4i*>(xq8)[c * kWave + lane];
-    xs = xsc[0];
-  }
+  // All weight loads stay issued before any use (the scheduler would otherwise
+  // sink them next to their dot products and serialise their latency).
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Per-vector quantization of x overlaps the weight stream.
+  if constexpr (F32IN) xs = quantize_lane_values<KCH>(xv, xq);
 
   int acc[NP][2];
 #pragma unroll
@@ -250,7 +297,7 @@ __global__ __launch_bounds__(256) void gateup_generic_kernel(float* out, const i
   if (lane == 0) out[(size_t)b * inter + j] = swiglu_w8a8(dg, du, xs[b], scales[2 * j], scales[2 * j + 1]);
 }
 
-constexpr int kMatvecPairs = 6;  // pairs per wave: 24 per 4-wave workgroup
+constexpr int kMatvecPairs = 3;  // pairs per wave: 12 per 4-wave workgroup
 
 template <bool F32IN>
 int launch_matvec(float* out, const int8_t* w, const float* scales, const int8_t* xq,
@@ -278,10 +325,20 @@ extern "C" int qasr_quantize_rows_i8(int8_t* q, float* scales, const float* x, s
                                      size_t cols, void* stream) {
   if (rows == 0) return QASR_OK;
   QASR_REQUIRE(q && scales && x, "quantize_rows_i8: null pointer");
-  QASR_REQUIRE(rows <= 0x7fffffffu && cols <= 0x7fffffffu, "quantize_rows_i8: size too large");
+  QASR_REQUIRE(rows <= kMaxRows && cols <= 0x7fffffffu, "quantize_rows_i8: size too large");
   size_t n;
   QASR_REQUIRE(mul_ok(rows, cols, &n), "quantize_rows_i8: rows * cols overflows");
-  quantize_rows_kernel<<<(unsigned)rows, 256, 0, as_stream(stream)>>>(q, scales, x, (int)cols);
+  hipStream_t st = as_stream(stream);
+  const int c = (int)cols;
+  if (cols % 4 == 0 && cols / 4 <= 8 * 256 && aligned16(x) && aligned4(q)) {
+    const size_t c4 = cols / 4;
+    if (c4 <= 256) quantize_rows_vec_kernel<1><<<(unsigned)rows, 256, 0, st>>>(q, scales, x, c);
+    else if (c4 <= 512) quantize_rows_vec_kernel<2><<<(unsigned)rows, 256, 0, st>>>(q, scales, x, c);
+    else if (c4 <= 1024) quantize_rows_vec_kernel<4><<<(unsigned)rows, 256, 0, st>>>(q, scales, x, c);
+    else quantize_rows_vec_kernel<8><<<(unsigned)rows, 256, 0, st>>>(q, scales, x, c);
+  } else {
+    quantize_rows_kernel<<<(unsigned)rows, 256, 0, st>>>(q, scales, x, c);
+  }
   return launch_status("quantize_rows_i8");
 }
 

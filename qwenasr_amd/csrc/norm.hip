@@ -17,10 +17,10 @@ QASR_DEV void st4(float* p, size_t i, float4 v) { reinterpret_cast<float4*>(p)[i
 // Arithmetic per row, as kernels/mod.rs:897-918 + avx.rs:374-415:
 //   rinv = 1 / sqrt(sum(x^2) / hidden + eps);  out = (x * rinv) * w
 // ---------------------------------------------------------------------------
-template <int BLOCK, int NV, bool ADD>
+template <int BLOCK, int NV, bool ADD, bool QUANT>
 __global__ __launch_bounds__(BLOCK) void rms_norm_vec_kernel(
-    float* x, const float* delta, const float* __restrict__ w, float* out,
-    int hidden, float eps) {
+    float* x, const float* delta, const float* __restrict__ w, float* out, int8_t* q,
+    float* q_scales, int hidden, float eps) {
   __shared__ float red[BLOCK / kWave];
   const int h4 = hidden >> 2;
   const size_t base = (size_t)blockIdx.x * (size_t)h4;
@@ -45,6 +45,7 @@ __global__ __launch_bounds__(BLOCK) void rms_norm_vec_kernel(
   }
   ss = block_sum<BLOCK>(ss, red);
   const float rinv = 1.0f / sqrtf(ss / (float)hidden + eps);
+  float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = threadIdx.x + i * BLOCK;
@@ -55,16 +56,42 @@ __global__ __launch_bounds__(BLOCK) void rms_norm_vec_kernel(
       o.y = (v[i].y * rinv) * wv.y;
       o.z = (v[i].z * rinv) * wv.z;
       o.w = (v[i].w * rinv) * wv.w;
-      st4(out, base + c, o);
+      if (out) st4(out, base + c, o);
+      v[i] = o;
+      if constexpr (QUANT) {
+        // absmax as quantize.rs:646-652 (`if abs > absmax`: NaN never wins)
+        const float a0 = fabsf(o.x), a1 = fabsf(o.y), a2 = fabsf(o.z), a3 = fabsf(o.w);
+        if (a0 > amax) amax = a0;
+        if (a1 > amax) amax = a1;
+        if (a2 > amax) amax = a2;
+        if (a3 > amax) amax = a3;
+      }
+    }
+  }
+  if constexpr (QUANT) {
+    // Per-row int8 quantization of the normalised row, quantize.rs:633-662.
+    amax = block_max<BLOCK>(amax, red);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    if (threadIdx.x == 0) q_scales[blockIdx.x] = amax / 127.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = threadIdx.x + i * BLOCK;
+      if (c < h4) {
+        const uint32_t b = (uint32_t)(quant_i8(v[i].x, inv) & 0xff) |
+                           ((uint32_t)(quant_i8(v[i].y, inv) & 0xff) << 8) |
+                           ((uint32_t)(quant_i8(v[i].z, inv) & 0xff) << 16) |
+                           ((uint32_t)(quant_i8(v[i].w, inv) & 0xff) << 24);
+        reinterpret_cast<uint32_t*>(q)[base + c] = b;
+      }
     }
   }
 }
 
-// Scalar fallback for any hidden / alignment: two sweeps over the row.
-template <bool ADD>
+// Scalar fallback for any hidden / alignment: sweeps over the row.
+template <bool ADD, bool QUANT>
 __global__ __launch_bounds__(256) void rms_norm_scalar_kernel(
-    float* x, const float* delta, const float* __restrict__ w, float* out,
-    int hidden, float eps) {
+    float* x, const float* delta, const float* __restrict__ w, float* out, int8_t* q,
+    float* q_scales, int hidden, float eps) {
   __shared__ float red[256 / kWave];
   const size_t base = (size_t)blockIdx.x * (size_t)hidden;
   float ss = 0.0f;
@@ -78,8 +105,22 @@ __global__ __launch_bounds__(256) void rms_norm_scalar_kernel(
   }
   ss = block_sum<256>(ss, red);
   const float rinv = 1.0f / sqrtf(ss / (float)hidden + eps);
+  float amax = 0.0f;
   for (int c = threadIdx.x; c < hidden; c += 256) {
-    out[base + c] = (x[base + c] * rinv) * w[c];
+    const float o = (x[base + c] * rinv) * w[c];
+    if (out) out[base + c] = o;
+    if constexpr (QUANT) {
+      const float a = fabsf(o);
+      if (a > amax) amax = a;
+    }
+  }
+  if constexpr (QUANT) {
+    amax = block_max<256>(amax, red);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    if (threadIdx.x == 0) q_scales[blockIdx.x] = amax / 127.0f;
+    for (int c = threadIdx.x; c < hidden; c += 256) {
+      q[base + c] = (int8_t)quant_i8((x[base + c] * rinv) * w[c], inv);
+    }
   }
 }
 
@@ -148,6 +189,64 @@ __global__ __launch_bounds__(BLOCK) void layer_norm_vec_kernel(
   }
 }
 
+// One wave per row (4 rows per workgroup): the row's NV float4 per lane stay
+// in registers and both statistics are wave reductions (no LDS, no barrier).
+template <int NV>
+__global__ __launch_bounds__(256) void layer_norm_wave_kernel(
+    float* out, const float* x, const float* __restrict__ w, const float* __restrict__ b,
+    int rows, int hidden, float eps) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (row >= rows) return;
+  const int h4 = hidden >> 2;
+  const int fused_end = hidden & ~7;
+  const size_t base = (size_t)row * (size_t)h4;
+  float4 v[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * kWave;
+    if (c < h4) {
+      v[i] = ld4(x, base + c);
+      s += v[i].x;
+      s += v[i].y;
+      s += v[i].z;
+      s += v[i].w;
+    }
+  }
+  s = wave_sum(s);
+  const float mean = s / (float)hidden;
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * kWave;
+    if (c < h4) {
+      float d;
+      d = v[i].x - mean; q += d * d;
+      d = v[i].y - mean; q += d * d;
+      d = v[i].z - mean; q += d * d;
+      d = v[i].w - mean; q += d * d;
+    }
+  }
+  q = wave_sum(q);
+  const float inv = 1.0f / sqrtf(q / (float)hidden + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + i * kWave;
+    if (c < h4) {
+      const float4 wv = ld4(w, c);
+      const float4 bv = ld4(b, c);
+      const bool f = 4 * c < fused_end;
+      float4 o;
+      o.x = ln_out(v[i].x, mean, inv, wv.x, bv.x, f);
+      o.y = ln_out(v[i].y, mean, inv, wv.y, bv.y, f);
+      o.z = ln_out(v[i].z, mean, inv, wv.z, bv.z, f);
+      o.w = ln_out(v[i].w, mean, inv, wv.w, bv.w, f);
+      st4(out, base + c, o);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void layer_norm_scalar_kernel(
     float* out, const float* x, const float* __restrict__ w,
     const float* __restrict__ b, int hidden, float eps) {
@@ -205,36 +304,37 @@ bool pick_row_shape(int h4, RowShape* s) {
   return false;
 }
 
-template <bool ADD>
-int launch_rms(float* x, const float* delta, const float* w, float* out,
-               size_t seq_len, size_t hidden, float eps, hipStream_t st) {
+template <bool ADD, bool QUANT>
+int launch_rms(float* x, const float* delta, const float* w, float* out, int8_t* q,
+               float* qs, size_t seq_len, size_t hidden, float eps, hipStream_t st) {
   const int h = (int)hidden;
   const dim3 grid((unsigned)seq_len);
   RowShape rs{};
   const bool vec = hidden % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(out) &&
-                   (!ADD || aligned16(delta)) && pick_row_shape(h / 4, &rs);
+                   (!ADD || aligned16(delta)) && (!QUANT || aligned4(q)) &&
+                   pick_row_shape(h / 4, &rs);
   if (!vec) {
-    rms_norm_scalar_kernel<ADD><<<grid, 256, 0, st>>>(x, delta, w, out, h, eps);
+    rms_norm_scalar_kernel<ADD, QUANT><<<grid, 256, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   } else if (rs.block == 64) {
-    rms_norm_vec_kernel<64, 1, ADD><<<grid, 64, 0, st>>>(x, delta, w, out, h, eps);
+    rms_norm_vec_kernel<64, 1, ADD, QUANT><<<grid, 64, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   } else if (rs.block == 128) {
-    rms_norm_vec_kernel<128, 1, ADD><<<grid, 128, 0, st>>>(x, delta, w, out, h, eps);
+    rms_norm_vec_kernel<128, 1, ADD, QUANT><<<grid, 128, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   } else if (rs.nv == 1) {
-    rms_norm_vec_kernel<256, 1, ADD><<<grid, 256, 0, st>>>(x, delta, w, out, h, eps);
+    rms_norm_vec_kernel<256, 1, ADD, QUANT><<<grid, 256, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   } else if (rs.nv == 2) {
-    rms_norm_vec_kernel<256, 2, ADD><<<grid, 256, 0, st>>>(x, delta, w, out, h, eps);
+    rms_norm_vec_kernel<256, 2, ADD, QUANT><<<grid, 256, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   } else if (rs.nv == 4) {
-    rms_norm_vec_kernel<256, 4, ADD><<<grid, 256, 0, st>>>(x, delta, w, out, h, eps);
+    rms_norm_vec_kernel<256, 4, ADD, QUANT><<<grid, 256, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   } else {
-    rms_norm_vec_kernel<256, 8, ADD><<<grid, 256, 0, st>>>(x, delta, w, out, h, eps);
+    rms_norm_vec_kernel<256, 8, ADD, QUANT><<<grid, 256, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   }
-  return launch_status(ADD ? "add_rms_norm" : "rms_norm");
+  return launch_status(QUANT ? "add_rms_norm_quant" : (ADD ? "add_rms_norm" : "rms_norm"));
 }
 
 int check_rows(size_t seq_len, size_t hidden) {
   size_t n;
   QASR_REQUIRE(mul_ok(seq_len, hidden, &n), "seq_len * hidden overflows");
-  QASR_REQUIRE(seq_len <= 0x7fffffffu, "seq_len exceeds the grid limit (2^31-1 rows)");
+  QASR_REQUIRE(seq_len <= kMaxRows, "seq_len exceeds the grid limit (2^24 rows per launch)");
   QASR_REQUIRE(hidden <= 0x7fffffffu, "hidden exceeds 2^31-1");
   return QASR_OK;
 }
@@ -265,8 +365,8 @@ extern "C" int qasr_rms_norm_f32(float* out, const float* x, const float* weight
   QASR_REQUIRE(out && x && weight, "rms_norm: null pointer");
   int rc = check_rows(seq_len, hidden);
   if (rc) return rc;
-  return launch_rms<false>(const_cast<float*>(x), nullptr, weight, out, seq_len, hidden, eps,
-                           as_stream(stream));
+  return launch_rms<false, false>(const_cast<float*>(x), nullptr, weight, out, nullptr, nullptr,
+                                  seq_len, hidden, eps, as_stream(stream));
 }
 
 extern "C" int qasr_add_rms_norm_f32(float* x, const float* delta, const float* weight,
@@ -277,7 +377,8 @@ extern "C" int qasr_add_rms_norm_f32(float* x, const float* delta, const float* 
   QASR_REQUIRE(out != x, "add_rms_norm: out must not alias the residual x");
   int rc = check_rows(seq_len, hidden);
   if (rc) return rc;
-  return launch_rms<true>(x, delta, weight, out, seq_len, hidden, eps, as_stream(stream));
+  return launch_rms<true, false>(x, delta, weight, out, nullptr, nullptr, seq_len, hidden, eps,
+                                 as_stream(stream));
 }
 
 extern "C" int qasr_layer_norm_f32(float* out, const float* x, const float* weight,
@@ -293,7 +394,15 @@ extern "C" int qasr_layer_norm_f32(float* out, const float* x, const float* weig
   RowShape rs{};
   const bool vec = hidden % 4 == 0 && aligned16(x) && aligned16(out) && aligned16(weight) &&
                    aligned16(bias) && pick_row_shape(h / 4, &rs);
-  if (!vec) {
+  const int h4 = h / 4;
+  if (vec && h4 <= 8 * kWave) {
+    const unsigned wgrid = (unsigned)((seq_len + 3) / 4);
+    const int r = (int)seq_len;
+    if (h4 <= kWave) layer_norm_wave_kernel<1><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps);
+    else if (h4 <= 2 * kWave) layer_norm_wave_kernel<2><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps);
+    else if (h4 <= 4 * kWave) layer_norm_wave_kernel<4><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps);
+    else layer_norm_wave_kernel<8><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps);
+  } else if (!vec) {
     layer_norm_scalar_kernel<<<grid, 256, 0, st>>>(out, x, weight, bias, h, eps);
   } else if (rs.block == 64) {
     layer_norm_vec_kernel<64, 1><<<grid, 64, 0, st>>>(out, x, weight, bias, h, eps);
@@ -309,4 +418,21 @@ extern "C" int qasr_layer_norm_f32(float* out, const float* x, const float* weig
     layer_norm_vec_kernel<256, 8><<<grid, 256, 0, st>>>(out, x, weight, bias, h, eps);
   }
   return launch_status("layer_norm");
+}
+
+extern "C" int qasr_add_rms_norm_quant_f32(float* x, const float* delta, const float* weight,
+                                           float* out, int8_t* q, float* q_scales,
+                                           size_t seq_len, size_t hidden, float eps,
+                                           void* stream) {
+  if (seq_len == 0 || hidden == 0) return QASR_OK;
+  QASR_REQUIRE(x && weight && q && q_scales, "add_rms_norm_quant: null pointer");
+  QASR_REQUIRE(out != x, "add_rms_norm_quant: out must not alias the residual x");
+  int rc = check_rows(seq_len, hidden);
+  if (rc) return rc;
+  if (delta) {
+    return launch_rms<true, true>(x, delta, weight, out, q, q_scales, seq_len, hidden, eps,
+                                  as_stream(stream));
+  }
+  return launch_rms<false, true>(x, nullptr, weight, out, q, q_scales, seq_len, hidden, eps,
+                                 as_stream(stream));
 }

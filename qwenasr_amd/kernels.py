@@ -24,7 +24,7 @@ from . import _lib
 from ._lib import QasrError  # noqa: F401  (re-export)
 
 __all__ = [
-    "add_inplace", "rms_norm", "add_rms_norm", "rms_norm_per_head", "apply_rope_neox",
+    "add_inplace", "rms_norm", "add_rms_norm", "add_rms_norm_quant", "rms_norm_per_head", "apply_rope_neox",
     "head_rms_norm_rope", "swiglu_multiply", "swiglu_multiply_inplace", "swiglu_split", "silu",
     "gelu", "gelu_erf", "layer_norm", "sinusoidal_pe", "pe_add", "tok_embed_f32_to_f32",
     "tok_embed_bf16_to_f32", "tok_embed_int8_to_f32", "embed_gather_f32", "embed_gather_bf16",
@@ -85,6 +85,24 @@ def add_rms_norm(x, delta, weight, out, seq_len: int, hidden: int, eps: float) -
     _need(out, F32, n, "out")
     _lib.call("qasr_add_rms_norm_f32", _ptr(x), _ptr(delta), _ptr(weight), _ptr(out), seq_len,
               hidden, eps, _stream())
+
+
+def add_rms_norm_quant(x, delta, weight, out, q, q_scales, seq_len: int, hidden: int,
+                       eps: float) -> None:
+    """Fused ``x += delta`` (skipped if delta is None), ``y = rms_norm(x)`` and
+    per-row int8 quantization of y into ``q``/``q_scales``; ``out`` (may be None)
+    receives y."""
+    n = seq_len * hidden
+    _need(x, F32, n, "x")
+    if delta is not None:
+        _need(delta, F32, n, "delta")
+    _need(weight, F32, hidden, "weight")
+    if out is not None:
+        _need(out, F32, n, "out")
+    _need(q, I8, n, "q")
+    _need(q_scales, F32, seq_len, "q_scales")
+    _lib.call("qasr_add_rms_norm_quant_f32", _ptr(x), _ptr(delta), _ptr(weight), _ptr(out),
+              _ptr(q), _ptr(q_scales), seq_len, hidden, eps, _stream())
 
 
 def layer_norm(out, x, weight, bias, seq_len: int, hidden: int, eps: float) -> None:
@@ -262,10 +280,6 @@ class QuantWeight:
     scales: torch.Tensor
     out_dim: int
     in_dim: int
-
-
-def _ids(ids) -> torch.Tensor:
-    return ids
 
 
 def embed_gather_f32(out, table, ids, n: int, dim: int) -> None:

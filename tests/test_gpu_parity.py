@@ -78,6 +78,43 @@ def test_rms_norm(dev, seq, hidden):
     assert_close(host(xt), oracle.rms_norm(x, w, seq, hidden, 1e-6), RTOL, ATOL, "rms_norm inplace")
 
 
+@pytest.mark.parametrize("seq,hidden", [(256, 2048), (1, 1024), (3, 1000), (5, 37)])
+@pytest.mark.parametrize("with_delta", [True, False])
+def test_add_rms_norm_quant(dev, seq, hidden, with_delta):
+    """x updated exactly; y within tolerance of the oracle; q/scales bit-exact to
+    quantize_rows_i8 applied to the kernel's own y (and within 1 of the oracle's)."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(24, seq, hidden)
+    x = normal(r, seq * hidden)
+    d = normal(r, seq * hidden)
+    w = normal(r, hidden, 0.1, 1.0)
+    xt, dt, wt = dev_t(x, dev), dev_t(d, dev), dev_t(w, dev)
+    out = torch.empty_like(xt)
+    q = torch.empty(seq * hidden, dtype=torch.int8, device=dev)
+    qs = torch.empty(seq, dtype=torch.float32, device=dev)
+    K.add_rms_norm_quant(xt, dt if with_delta else None, wt, out, q, qs, seq, hidden, 1e-6)
+    if with_delta:
+        x_ref, y_ref = oracle.add_rms_norm(x, d, w, seq, hidden, 1e-6)
+    else:
+        x_ref, y_ref = x, oracle.rms_norm(x, w, seq, hidden, 1e-6)
+    np.testing.assert_array_equal(host(xt), x_ref)
+    y = host(out)
+    assert_close(y, y_ref, RTOL, ATOL, "add_rms_norm_quant y")
+    q_self, s_self = oracle.quantize_f32_to_int8(y, seq, hidden)
+    np.testing.assert_array_equal(host(q), q_self)
+    np.testing.assert_array_equal(host(qs), s_self)
+    q_ref, _ = oracle.quantize_f32_to_int8(y_ref, seq, hidden)
+    assert np.abs(host(q).astype(np.int32) - q_ref.astype(np.int32)).max() <= 1
+    # without the fp32 output the int8 result is the same
+    xt2 = dev_t(x, dev)
+    q2 = torch.empty_like(q)
+    qs2 = torch.empty_like(qs)
+    K.add_rms_norm_quant(xt2, dt if with_delta else None, wt, None, q2, qs2, seq, hidden, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(q2, q) and torch.equal(qs2, qs)
+
+
 def test_rms_norm_misaligned_rows_take_scalar_path(dev):
     from qwenasr_amd import kernels as K
 
@@ -466,6 +503,8 @@ W8A8_CASES = [
     ("c4_matvec", 1, 2048, 6144),
     ("c4_0.6B", 1, 1024, 3072),
     ("c5_mfma", 256, 2048, 6144),
+    ("mfma_lds_k1024_ragged", 100, 1024, 3072),
+    ("mfma_lds_k512", 130, 512, 96),
     ("mfma_ragged_batch", 37, 2048, 96),
     ("mfma_small_k", 64, 512, 256),
     ("generic_path", 3, 400, 50),
