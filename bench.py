@@ -266,7 +266,9 @@ class C5BatchedDecode(Workload):
             w = self.randn(2 * I * H, 0.02)
             q, s = K.quantize_f32_to_int8(w, 2 * I, H)
             del w
-            self.layers.append(K.QuantWeight(q, s, 2 * I, H))
+            # weights are re-laid into MFMA tiles once, at load
+            self.layers.append(K.pack_w8a8_tiles(K.QuantWeight(q, s, 2 * I, H)))
+            del q
         S = L
         self.x = [self.randn(B * H) for _ in range(S)]
         self.d = [self.randn(B * H) for _ in range(S)]
@@ -289,7 +291,7 @@ class C5BatchedDecode(Workload):
                 self.q[i % S], self.k[i % S], self.qw, self.kw, self.rope.cos, self.rope.sin,
                 self.pos[i % S], B, nq, nk, hd, c["eps"]),
                 2 * B * (nq + nk) * hd * F + 2 * hd * F + 2 * B * hd * F + B * 4),
-            "gate_up_swiglu_w8a8_gemm": (lambda i: K.gate_up_swiglu_w8a8(
+            "gate_up_swiglu_w8a8_gemm": (lambda i: K.gate_up_swiglu_w8a8_packed(
                 self.o[i % S], self.layers[i % L], self.xq[i % S], self.xsc[i % S], B, H, I),
                 2 * I * H + 2 * I * F + B * H + B * F + B * I * F),
         }

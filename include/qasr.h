@@ -233,6 +233,27 @@ int qasr_gate_up_swiglu_w8a8(float* out, const int8_t* w, const float* scales,
                              size_t batch, size_t in_dim, size_t intermediate,
                              void* stream);
 
+/* Re-lays a row-major int8 weight matrix [rows, cols] into MFMA A-operand
+ * tiles (v_mfma_i32_16x16x64_i8): for each 16-row block rb and 64-byte k-step
+ * s one contiguous 1 KiB tile whose byte 16*l + b is
+ * W[16*rb + l%16][64*s + 16*(l/16) + b]; tiles are ordered [rb][s].
+ * rows % 16 == 0, cols % 64 == 0, out of place. A one-time
+ * load-time transform of the device weights, like the gate/up row interleave
+ * the decoder builds at load (decoder.rs:701-719); scales are unchanged.
+ * No reference counterpart (the reference reads .qint8 rows directly). */
+int qasr_pack_w8a8_tiles(int8_t* packed, const int8_t* w, size_t rows,
+                         size_t cols, void* stream);
+
+/* qasr_gate_up_swiglu_w8a8 on tile-packed weights: w_packed is
+ * qasr_pack_w8a8_tiles of the row-interleaved gate/up matrix. Same arithmetic
+ * and results. Needs in_dim 1024 or 2048 and (2*intermediate) % 192 == 0
+ * (QASR_ERR_UNSUPPORTED otherwise); out 8-byte aligned. */
+int qasr_gate_up_swiglu_w8a8_packed(float* out, const int8_t* w_packed,
+                                    const float* scales, const int8_t* xq,
+                                    const float* x_scales, size_t batch,
+                                    size_t in_dim, size_t intermediate,
+                                    void* stream);
+
 /* As qasr_gate_up_swiglu_w8a8 for batch == 1 with an fp32 input vector that
  * the kernel quantizes per-vector itself (qasr_quantize_rows_i8 arithmetic),
  * so one launch covers quantize + matvec + SwiGLU. */

@@ -64,6 +64,8 @@ SIGNATURES: dict[str, list] = {
     "qasr_interleave_gate_up_i8": [P, P, P, P, P, P, Z, Z, P],
     "qasr_gate_up_swiglu_w8a8": [P, P, P, P, P, Z, Z, Z, P],
     "qasr_gate_up_swiglu_w8a8_f32in": [P, P, P, P, Z, Z, P],
+    "qasr_pack_w8a8_tiles": [P, P, Z, Z, P],
+    "qasr_gate_up_swiglu_w8a8_packed": [P, P, P, P, P, Z, Z, Z, P],
 }
 
 _LIB = None

@@ -16,7 +16,7 @@
 // lane's four results are four consecutive W rows for one token -- two complete
 // gate/up pairs -- so the SwiGLU epilogue needs no data exchange.
 //
-// Main kernel (gemm_w8a8_swiglu_lds_kernel, K = 1024 or 2048): a workgroup
+// Row-major kernel (gemm_w8a8_swiglu_lds_kernel, K = 1024 or 2048): a workgroup
 // owns 192 W rows x 64 tokens. The 64 token rows of Xq (64 x K bytes) are
 // staged once in LDS by direct global->LDS loads, with a 16-byte row pad
 // (conflict-free b128 reads); each of the 4 waves owns 48 distinct W rows and
@@ -42,8 +42,21 @@ constexpr int kLdsBM = 64;            // tokens per workgroup
 constexpr int kLdsWaveRows = 48;      // W rows per wave (3 MFMA row tiles)
 constexpr int kLdsMaxK = 2048;        // X tile must fit LDS: 64 x (2048 + 16) B
 constexpr int kLdsRowPad = 16;
-constexpr int kPrefetch = 8;          // k-steps of W in flight per wave
+constexpr int kPrefetch = 12;         // k-steps of W in flight per wave
 constexpr int kNumXcd = 8;
+
+// MFMA tile layout of a weight matrix ("packed") for v_mfma_i32_16x16x64_i8:
+// for each block of 16 rows rb and each 64-byte k-step s, one contiguous 1 KiB
+// tile whose byte 16*lane + b is W[16*rb + lane % 16][64*s + 16*(lane / 16) + b],
+// i.e. exactly the A operand lane `lane` feeds the MFMA. Tiles are ordered
+// [rb][s], so a wave's operand load is one fully used 1 KiB span (8 cache
+// lines) instead of 16 row fragments of 64 bytes.
+constexpr int kPackRows = 16;
+constexpr int kPackK = 64;
+
+QASR_DEV size_t packed_tile_offset(int rb, int s, int ksteps) {
+  return ((size_t)rb * ksteps + s) * 1024;
+}
 
 template <int KSTEPS>  // K / 64
 __global__ __launch_bounds__(256) void gemm_w8a8_swiglu_lds_kernel(
@@ -75,8 +88,10 @@ __global__ __launch_bounds__(256) void gemm_w8a8_swiglu_lds_kernel(
   const int n_wave = tile_n * kLdsBN + wave * kLdsWaveRows;
   const int m0 = tile_m * kLdsBM;
 
-  // W row pointers for this wave's three 16-row tiles (lane row r, group g).
+  // W operand pointers for this wave's three 16-row tiles (lane row r, group
+  // g) and the byte step between consecutive k-steps.
   const int8_t* wp[3];
+  constexpr int WSTEP = kGemmK;
 #pragma unroll
   for (int i = 0; i < 3; ++i) wp[i] = w + (size_t)(n_wave + 16 * i + r) * K + 16 * g;
 
@@ -105,7 +120,7 @@ __global__ __launch_bounds__(256) void gemm_w8a8_swiglu_lds_kernel(
   for (int d = 0; d < kPrefetch; ++d)
 #pragma unroll
     for (int i = 0; i < 3; ++i)
-      if (d < KSTEPS) wbuf[d][i] = *reinterpret_cast<const v4i*>(wp[i] + d * kGemmK);
+      if (d < KSTEPS) wbuf[d][i] = *reinterpret_cast<const v4i*>(wp[i] + d * WSTEP);
 
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(0);  // the LDS fill (and the W prefetch) have landed
@@ -129,7 +144,7 @@ __global__ __launch_bounds__(256) void gemm_w8a8_swiglu_lds_kernel(
         for (int i = 0; i < 3; ++i) {
           a[i] = wbuf[d][i];
           if (s + kPrefetch < KSTEPS)
-            wbuf[d][i] = *reinterpret_cast<const v4i*>(wp[i] + (s + kPrefetch) * kGemmK);
+            wbuf[d][i] = *reinterpret_cast<const v4i*>(wp[i] + (s + kPrefetch) * WSTEP);
         }
         // Keep the prefetch issue here: without this fence the scheduler sinks
         // each load next to its use and the pipeline collapses to one load in
@@ -284,6 +299,25 @@ bool launch_lds_gemm(float* out, const int8_t* w, const float* scales, const int
   return true;
 }
 
+// Launches the LDS-staged kernel when the shape allows; returns false if it
+// did not launch (shape or device LDS), leaving the choice to the caller.
+inline bool try_lds_gemm(float* out, const int8_t* w, const float* scales, const int8_t* xq,
+                  const float* xs, size_t batch, size_t K, size_t inter, hipStream_t st) {
+  if (!gemm_w8a8_lds_shape(K, inter) || !aligned16(scales) ||
+      (2 * inter / kLdsBN) * ((batch + kLdsBM - 1) / kLdsBM) > 0x7fffffffu) {
+    return false;
+  }
+  const int n_tiles = (int)((2 * inter) / kLdsBN);
+  const int m_tiles = (int)((batch + kLdsBM - 1) / kLdsBM);
+  const size_t lds = (size_t)kLdsBM * (K + kLdsRowPad);
+  if (K == 1024) {
+    return launch_lds_gemm<16>(out, w, scales, xq, xs, (int)batch, (int)inter, n_tiles,
+                                       m_tiles, lds, st);
+  }
+  return launch_lds_gemm<32>(out, w, scales, xq, xs, (int)batch, (int)inter, n_tiles,
+                                     m_tiles, lds, st);
+}
+
 inline int gemm_w8a8_swiglu(float* out, const int8_t* w, const float* scales, const int8_t* xq,
                             const float* xs, size_t batch, size_t K, size_t inter,
                             hipStream_t st) {
@@ -292,18 +326,8 @@ inline int gemm_w8a8_swiglu(float* out, const int8_t* w, const float* scales, co
   if ((reinterpret_cast<uintptr_t>(out) & 7u) != 0) {
     return fail(QASR_ERR_INVALID_ARG, "gate_up_swiglu_w8a8: out must be 8-byte aligned");
   }
-  if (gemm_w8a8_lds_shape(K, inter) && aligned16(scales) &&
-      (2 * inter / kLdsBN) * ((batch + kLdsBM - 1) / kLdsBM) <= 0x7fffffffu) {
-    const int n_tiles = (int)((2 * inter) / kLdsBN);
-    const int m_tiles = (int)((batch + kLdsBM - 1) / kLdsBM);
-    const size_t lds = (size_t)kLdsBM * (K + kLdsRowPad);
-    bool launched = false;
-    if (K == 1024) {
-      launched = launch_lds_gemm<16>(out, w, scales, xq, xs, (int)batch, (int)inter, n_tiles, m_tiles, lds, st);
-    } else {
-      launched = launch_lds_gemm<32>(out, w, scales, xq, xs, (int)batch, (int)inter, n_tiles, m_tiles, lds, st);
-    }
-    if (launched) return launch_status("gate_up_swiglu_w8a8 (mfma, lds)");
+  if (try_lds_gemm(out, w, scales, xq, xs, batch, K, inter, st)) {
+    return launch_status("gate_up_swiglu_w8a8 (mfma, lds)");
   }
   const size_t n_tiles = (2 * inter) / kGemmBN;
   const size_t m_tiles = (batch + kGemmBM - 1) / kGemmBM;
@@ -312,6 +336,245 @@ inline int gemm_w8a8_swiglu(float* out, const int8_t* w, const float* scales, co
   gemm_w8a8_swiglu_kernel<<<(unsigned)grid, 256, 0, st>>>(out, w, scales, xq, xs, (int)batch,
                                                           (int)K, (int)inter);
   return launch_status("gate_up_swiglu_w8a8 (mfma)");
+}
+
+}  // namespace qasr
+
+namespace qasr {
+
+// Row-major [rows, cols] int8 -> MFMA tile layout (see packed_tile_offset).
+// One thread moves one 16-byte lane slice.
+__global__ __launch_bounds__(256) void pack_w8a8_tiles_kernel(int8_t* __restrict__ packed,
+                                                              const int8_t* __restrict__ w,
+                                                              size_t n_slices, int ksteps,
+                                                              size_t cols) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n_slices;
+       i += (size_t)gridDim.x * 256) {
+    const int lane = (int)(i & 63);
+    const size_t tile = i >> 6;
+    const size_t rb = tile / (size_t)ksteps;
+    const int s = (int)(tile - rb * ksteps);
+    const size_t row = rb * kPackRows + (lane & 15);
+    const size_t col = (size_t)s * kPackK + 16 * (lane >> 4);
+    *reinterpret_cast<v4i*>(packed + i * 16) = *reinterpret_cast<const v4i*>(w + row * cols + col);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Packed-weight kernel: one workgroup of 4*KSPLIT waves per CU, split-K.
+//
+// A workgroup owns 192 W rows x 64 tokens. Its 64 token rows of Xq are staged
+// once in LDS (direct global->LDS loads). Wave w = 4*kq + rg owns row group rg
+// (48 rows = 3 tiles of 16) for all 64 tokens (4 tiles) -- 12 accumulators --
+// over k-quarter kq of the K range, so every W tile and every X slice is read
+// once per workgroup, and 8 or 16 resident waves per CU keep the L2->L1 fill
+// path busy (one 4-wave workgroup per CU tops out near 40 GB/s per CU, 16
+// waves near 100 GB/s). After the K loop the waves with kq > 0 store their
+// partial sums in LDS (the X tile's space); the kq = 0 wave of each row group
+// adds them (exact int32) and finishes the SwiGLU epilogue.
+// ---------------------------------------------------------------------------
+constexpr int kKsBN = 192;
+constexpr int kKsBM = 64;
+constexpr int kKsPartialBytes = 12 * 4 * 64 * 4;  // one wave's 12 accumulators
+
+template <int KSPLIT>
+constexpr int ks_prefetch() { return KSPLIT == 4 ? 2 : 8; }
+
+template <int KS, int KSPLIT>  // KS = K / 64
+__global__ __launch_bounds__(64 * 4 * KSPLIT) void gemm_w8a8_swiglu_ksplit_kernel(
+    float* __restrict__ out, const int8_t* __restrict__ wpk, const float* __restrict__ scales,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, int batch, int inter,
+    int n_tiles, int m_tiles) {
+  constexpr int K = KS * kPackK;
+  constexpr int STRIDE = K + kLdsRowPad;
+  constexpr int KW = KS / KSPLIT;  // k-steps per wave
+  constexpr int PF = ks_prefetch<KSPLIT>();
+  constexpr int NWAVES = 4 * KSPLIT;
+  extern __shared__ __align__(16) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rg = wave & 3;
+  const int kq = wave >> 2;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+
+  const int b = blockIdx.x;
+  int tile_n, tile_m;
+  if (n_tiles % kNumXcd == 0) {
+    const int slot = b / kNumXcd;
+    tile_m = slot % m_tiles;
+    tile_n = b % kNumXcd + kNumXcd * (slot / m_tiles);
+  } else {
+    tile_m = b % m_tiles;
+    tile_n = b / m_tiles;
+  }
+  const int n_wave = tile_n * kKsBN + rg * 48;
+  const int m0 = tile_m * kKsBM;
+  const int k0 = kq * KW;
+
+  // X tile -> LDS, 1 KiB per wave instruction.
+  {
+    constexpr int CPR = K / 1024;
+    constexpr int CHUNKS = kKsBM * CPR;
+#pragma unroll 4
+    for (int c = wave; c < CHUNKS; c += NWAVES) {
+      const int row = c / CPR, part = c - row * CPR;
+      const int src_row = m0 + row < batch ? m0 + row : batch - 1;
+      const int8_t* src = xq + (size_t)src_row * K + 1024 * part + 16 * lane;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)src,
+          (__attribute__((address_space(3))) void*)(lds + row * STRIDE + 1024 * part), 16, 0, 0);
+    }
+  }
+
+  // W stream: 3 row tiles, k-steps k0 .. k0+KW-1.
+  const int8_t* wp = wpk + packed_tile_offset(n_wave / kPackRows, k0, KS) + 16 * lane;
+  constexpr size_t ROW_TILE = (size_t)KS * 1024;
+  v4i wbuf[PF][3];
+#pragma unroll
+  for (int d = 0; d < PF; ++d)
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (d < KW) wbuf[d][i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + i * ROW_TILE + d * 1024));
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  v4i acc[3][4];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  const int8_t* xl = lds + r * STRIDE + 16 * g + k0 * kPackK;
+#pragma unroll
+  for (int s0 = 0; s0 < KW; s0 += PF) {
+#pragma unroll
+    for (int d = 0; d < PF; ++d) {
+      const int s = s0 + d;
+      if (s < KW) {
+        v4i a[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          a[i] = wbuf[d][i];
+          if (s + PF < KW)
+            wbuf[d][i] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i*>(wp + i * ROW_TILE + (s + PF) * 1024));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        v4i bx[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bx[j] = *reinterpret_cast<const v4i*>(xl + 16 * j * STRIDE + s * kPackK);
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bx[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // Split-K reduction through LDS: partial set (kq - 1, rg) is 12 KiB laid out
+  // [tile][item][lane] int32, so lane-consecutive addresses.
+  int* red = reinterpret_cast<int*>(lds);
+  __syncthreads();  // all waves are done reading the X tile
+  if (kq > 0) {
+    int* dst = red + ((kq - 1) * 4 + rg) * (kKsPartialBytes / 4) + lane;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dst[((i * 4 + j) * 4 + q) * 64] = acc[i][j][q];
+  }
+  __syncthreads();
+  if (kq != 0) return;
+#pragma unroll
+  for (int p = 1; p < KSPLIT; ++p) {
+    const int* src = red + ((p - 1) * 4 + rg) * (kKsPartialBytes / 4) + lane;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[i][j][q] += src[((i * 4 + j) * 4 + q) * 64];
+  }
+
+  // Epilogue: lane holds W rows n_wave + 16i + 4g + {0..3} for token m0 + 16j + r.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = m0 + 16 * j + r;
+    if (m >= batch) continue;
+    const float xsm = xs[m];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int n = n_wave + 16 * i + 4 * g;
+      const float4 sc = *reinterpret_cast<const float4*>(scales + n);
+      float2 o;
+      {
+        const float gg = ((float)acc[i][j][0] * xsm) * sc.x;
+        const float uu = ((float)acc[i][j][1] * xsm) * sc.y;
+        o.x = (gg / (1.0f + expf(-gg))) * uu;
+      }
+      {
+        const float gg = ((float)acc[i][j][2] * xsm) * sc.z;
+        const float uu = ((float)acc[i][j][3] * xsm) * sc.w;
+        o.y = (gg / (1.0f + expf(-gg))) * uu;
+      }
+      *reinterpret_cast<float2*>(out + (size_t)m * inter + (n >> 1)) = o;
+    }
+  }
+}
+
+inline bool gemm_ksplit_shape(size_t K, size_t inter) {
+  return (K == 1024 || K == 2048) && (2 * inter) % kKsBN == 0;
+}
+
+template <int KS, int KSPLIT>
+bool ksplit_kernel_ready() {
+  static const bool ok = [] {
+    int dev = 0, max_lds = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      return false;
+    if ((size_t)max_lds < (size_t)kKsBM * (kLdsMaxK + kLdsRowPad)) return false;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_w8a8_swiglu_ksplit_kernel<KS, KSPLIT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, max_lds) == hipSuccess;
+  }();
+  return ok;
+}
+
+template <int KS, int KSPLIT>
+bool launch_ksplit(float* out, const int8_t* wpk, const float* scales, const int8_t* xq,
+                   const float* xs, int batch, int inter, int n_tiles, int m_tiles,
+                   hipStream_t st) {
+  if (!ksplit_kernel_ready<KS, KSPLIT>()) return false;
+  size_t lds = (size_t)kKsBM * (KS * kPackK + kLdsRowPad);
+  const size_t red = (size_t)(KSPLIT - 1) * 4 * kKsPartialBytes;
+  if (lds < red) lds = red;
+  gemm_w8a8_swiglu_ksplit_kernel<KS, KSPLIT><<<(unsigned)(n_tiles * m_tiles), 64 * 4 * KSPLIT, lds, st>>>(
+      out, wpk, scales, xq, xs, batch, inter, n_tiles, m_tiles);
+  return true;
+}
+
+constexpr int kDefaultKsplit = 1;
+
+// Launches the packed-weight kernel; returns false if the shape or the device
+// LDS does not allow it (nothing launched).
+template <int KSPLIT = kDefaultKsplit>
+bool try_packed_gemm(float* out, const int8_t* wpk, const float* scales, const int8_t* xq,
+                     const float* xs, size_t batch, size_t K, size_t inter, hipStream_t st) {
+  if (!gemm_ksplit_shape(K, inter)) return false;
+  const size_t n_tiles = 2 * inter / kKsBN, m_tiles = (batch + kKsBM - 1) / kKsBM;
+  if (n_tiles * m_tiles > 0x7fffffffu) return false;
+  if (K == 1024) {
+    return launch_ksplit<16, KSPLIT>(out, wpk, scales, xq, xs, (int)batch, (int)inter,
+                                     (int)n_tiles, (int)m_tiles, st);
+  }
+  return launch_ksplit<32, KSPLIT>(out, wpk, scales, xq, xs, (int)batch, (int)inter, (int)n_tiles,
+                                   (int)m_tiles, st);
 }
 
 }  // namespace qasr

@@ -441,3 +441,45 @@ extern "C" int qasr_gate_up_swiglu_w8a8_f32in(float* out, const int8_t* w, const
   return launch_matvec<true>(out, w, scales, nullptr, nullptr, x, in_dim, intermediate,
                              as_stream(stream));
 }
+
+extern "C" int qasr_pack_w8a8_tiles(int8_t* packed, const int8_t* w, size_t rows, size_t cols,
+                                    void* stream) {
+  if (rows == 0 || cols == 0) return QASR_OK;
+  QASR_REQUIRE(packed && w, "pack_w8a8_tiles: null pointer");
+  QASR_REQUIRE(packed != w, "pack_w8a8_tiles: packing is out of place");
+  QASR_REQUIRE(rows % kPackRows == 0 && cols % kPackK == 0,
+               "pack_w8a8_tiles: rows must be a multiple of 16 and cols of 64");
+  QASR_REQUIRE(aligned16(packed) && aligned16(w), "pack_w8a8_tiles: 16-byte alignment required");
+  size_t n;
+  QASR_REQUIRE(mul_ok(rows, cols, &n), "pack_w8a8_tiles: size overflows");
+  const size_t slices = n / 16;
+  pack_w8a8_tiles_kernel<<<grid_for(slices, 256), 256, 0, as_stream(stream)>>>(
+      packed, w, slices, (int)(cols / kPackK), cols);
+  return launch_status("pack_w8a8_tiles");
+}
+
+extern "C" int qasr_gate_up_swiglu_w8a8_packed(float* out, const int8_t* w_packed,
+                                               const float* scales, const int8_t* xq,
+                                               const float* x_scales, size_t batch,
+                                               size_t in_dim, size_t intermediate,
+                                               void* stream) {
+  if (batch == 0 || intermediate == 0) return QASR_OK;
+  QASR_REQUIRE(out && w_packed && scales && xq && x_scales,
+               "gate_up_swiglu_w8a8_packed: null pointer");
+  QASR_REQUIRE(aligned16(w_packed) && aligned16(xq) && aligned16(scales),
+               "gate_up_swiglu_w8a8_packed: w, xq and scales must be 16-byte aligned");
+  QASR_REQUIRE((reinterpret_cast<uintptr_t>(out) & 7u) == 0,
+               "gate_up_swiglu_w8a8_packed: out must be 8-byte aligned");
+  QASR_REQUIRE(batch <= 0x7fffffffu && intermediate <= 0x3fffffffu,
+               "gate_up_swiglu_w8a8_packed: size too large");
+  if (!gemm_ksplit_shape(in_dim, intermediate)) {
+    return fail(QASR_ERR_UNSUPPORTED,
+                "gate_up_swiglu_w8a8_packed: needs in_dim 1024 or 2048 and 2*intermediate % 192 == 0");
+  }
+  if (!try_packed_gemm(out, w_packed, scales, xq, x_scales, batch, in_dim, intermediate,
+                       as_stream(stream))) {
+    return fail(QASR_ERR_UNSUPPORTED,
+                "gate_up_swiglu_w8a8_packed: the device cannot give a workgroup 130 KiB of LDS");
+  }
+  return launch_status("gate_up_swiglu_w8a8_packed");
+}

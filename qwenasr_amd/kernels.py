@@ -30,7 +30,7 @@ __all__ = [
     "tok_embed_bf16_to_f32", "tok_embed_int8_to_f32", "embed_gather_f32", "embed_gather_bf16",
     "embed_gather_i8", "quantize_f32_to_int8", "quantize_rows_i8", "linear_nobias_int8",
     "linear_int8", "interleave_gate_up", "gate_up_swiglu_w8a8", "gate_up_swiglu_w8a8_f32in",
-    "RopeCache", "QuantWeight",
+    "pack_w8a8_tiles", "gate_up_swiglu_w8a8_packed", "RopeCache", "QuantWeight",
 ]
 
 
@@ -406,3 +406,24 @@ def gate_up_swiglu_w8a8_f32in(out, w: QuantWeight, x, in_dim: int, intermediate:
     _need(x, F32, in_dim, "x")
     _lib.call("qasr_gate_up_swiglu_w8a8_f32in", _ptr(out), _ptr(w.data), _ptr(w.scales), _ptr(x),
               in_dim, intermediate, _stream())
+
+
+def pack_w8a8_tiles(w: QuantWeight) -> QuantWeight:
+    """MFMA tile layout of an int8 weight (see include/qasr.h); scales are shared."""
+    _need(w.data, I8, w.out_dim * w.in_dim, "w.data")
+    packed = torch.empty(w.out_dim * w.in_dim, dtype=I8, device=w.data.device)
+    _lib.call("qasr_pack_w8a8_tiles", _ptr(packed), _ptr(w.data), w.out_dim, w.in_dim, _stream())
+    return QuantWeight(packed, w.scales, w.out_dim, w.in_dim)
+
+
+def gate_up_swiglu_w8a8_packed(out, w_packed: QuantWeight, xq, x_scales, batch: int, in_dim: int,
+                               intermediate: int) -> None:
+    """gate_up_swiglu_w8a8 on a pack_w8a8_tiles weight (same results)."""
+    _need(out, F32, batch * intermediate, "out")
+    _need(w_packed.data, I8, 2 * intermediate * in_dim, "w.data")
+    _need(w_packed.scales, F32, 2 * intermediate, "w.scales")
+    _need(xq, I8, batch * in_dim, "xq")
+    _need(x_scales, F32, batch, "x_scales")
+    _lib.call("qasr_gate_up_swiglu_w8a8_packed", _ptr(out), _ptr(w_packed.data),
+              _ptr(w_packed.scales), _ptr(xq), _ptr(x_scales), batch, in_dim, intermediate,
+              _stream())

@@ -576,3 +576,65 @@ def test_gate_up_swiglu_w8a8_f32_input(dev, in_dim, inter):
     out2 = torch.empty_like(out)
     K.gate_up_swiglu_w8a8(out2, w, q2, s2, 1, in_dim, inter)
     np.testing.assert_array_equal(host(out), host(out2))
+
+
+def pack_tiles_reference(w: np.ndarray) -> np.ndarray:
+    """The documented tile layout, built with numpy reshapes."""
+    rows, cols = w.shape
+    t = w.reshape(rows // 16, 16, cols // 64, 4, 16)      # [rb, r, s, g, b]
+    t = t.transpose(0, 2, 3, 1, 4)                        # [rb, s, g, r, b] -> lane = 16 g + r
+    return np.ascontiguousarray(t).reshape(-1)
+
+
+@pytest.mark.parametrize("rows,cols", [(192, 2048), (12288, 2048), (16, 64), (48, 192)])
+def test_pack_w8a8_tiles_layout(dev, rows, cols):
+    from qwenasr_amd import kernels as K
+
+    r = rng(25, rows, cols)
+    w = r.integers(-128, 128, (rows, cols), dtype=np.int8)
+    qw = K.QuantWeight(dev_t(w, dev), torch.ones(rows, device=dev), rows, cols)
+    p = K.pack_w8a8_tiles(qw)
+    np.testing.assert_array_equal(host(p.data), pack_tiles_reference(w))
+
+
+PACKED_CASES = [("c5", 256, 2048, 6144), ("ragged", 37, 2048, 96), ("k1024", 100, 1024, 3072),
+                ("b1", 1, 2048, 96)]
+
+
+@pytest.mark.parametrize("name,batch,in_dim,inter", PACKED_CASES)
+def test_gate_up_swiglu_w8a8_packed(dev, name, batch, in_dim, inter):
+    from qwenasr_amd import kernels as K
+
+    r = rng(26, batch, in_dim, inter)
+    wq, ws, _, xq, xs = gateup_inputs(r, batch, in_dim, inter)
+    w = K.QuantWeight(dev_t(wq, dev), dev_t(ws, dev), 2 * inter, in_dim)
+    wp = K.pack_w8a8_tiles(w)
+    out = torch.empty(batch * inter, dtype=torch.float32, device=dev)
+    K.gate_up_swiglu_w8a8_packed(out, wp, dev_t(xq, dev), dev_t(xs, dev), batch, in_dim, inter)
+    if batch * inter * in_dim <= 64 * 1024 * 1024:
+        ref, _ = oracle.gate_up_swiglu_w8a8(wq, ws, xq, xs, batch, in_dim, inter)
+    else:
+        ref = w8a8_reference_blas(wq, ws, xq, xs, batch, in_dim, inter)
+    assert_close(host(out), ref, RTOL, ATOL, name)
+    # identical to the row-major entry point, bit for bit
+    out2 = torch.empty_like(out)
+    K.gate_up_swiglu_w8a8(out2, w, dev_t(xq, dev), dev_t(xs, dev), batch, in_dim, inter)
+    np.testing.assert_array_equal(host(out), host(out2))
+
+
+def test_w8a8_packed_int32_dots_bit_exact(dev):
+    from qwenasr_amd import kernels as K
+
+    batch, in_dim, inter = 256, 2048, 6144
+    r = rng(27)
+    w = np.empty((2 * inter, in_dim), np.int8)
+    w[0::2] = r.integers(1, 128, (inter, in_dim), dtype=np.int8)
+    w[1::2] = r.integers(-128, 128, (inter, in_dim), dtype=np.int8)
+    xq = r.integers(1, 128, (batch, in_dim), dtype=np.int8)
+    qw = K.QuantWeight(dev_t(w, dev), torch.ones(2 * inter, device=dev), 2 * inter, in_dim)
+    out = torch.empty(batch * inter, dtype=torch.float32, device=dev)
+    K.gate_up_swiglu_w8a8_packed(out, K.pack_w8a8_tiles(qw), dev_t(xq, dev),
+                                 torch.ones(batch, device=dev), batch, in_dim, inter)
+    dots = xq.astype(np.float64) @ w.astype(np.float64).T
+    exp = (dots[:, 0::2].astype(np.float32) * dots[:, 1::2].astype(np.float32)).ravel()
+    np.testing.assert_array_equal(host(out), exp)
