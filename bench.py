@@ -448,6 +448,40 @@ def cpu_baseline(name: str, seconds: float) -> dict:
 
 
 # ---------------------------------------------------------------------------
+# Counter runs (rocprofv3 --pmc): one kernel at a time
+# ---------------------------------------------------------------------------
+COPY_BYTES = 64 << 20
+
+
+def profile_copy(torch, dev, n: int) -> int:
+    """A plain copy of known size: COPY_BYTES read + COPY_BYTES written per
+    launch. Its FETCH_SIZE / WRITE_SIZE readings calibrate those counters."""
+    src = [torch.ones(COPY_BYTES // 4, device=dev) for _ in range(8)]
+    dst = [torch.empty(COPY_BYTES // 4, device=dev) for _ in range(8)]
+    torch.cuda.synchronize()
+    for i in range(n):
+        dst[i % 8].copy_(src[i % 8])
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_kernel": "copy", "launches": n, "read_bytes": COPY_BYTES,
+                      "write_bytes": COPY_BYTES}), flush=True)
+    return 0
+
+
+def profile_kernel(torch, wl, name: str, n: int) -> int:
+    if name not in wl.kernels:
+        print(f"bench.py: workload {wl.name} has no kernel {name!r} (has {sorted(wl.kernels)})",
+              file=sys.stderr)
+        return 2
+    launch, nbytes = wl.kernels[name]
+    for i in range(n):
+        launch(i)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_kernel": name, "workload": wl.name, "launches": n,
+                      "algorithmic_bytes": nbytes}), flush=True)
+    return 0
+
+
+# ---------------------------------------------------------------------------
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -457,6 +491,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="launch from the host instead of graph replay")
+    ap.add_argument("--profile-kernel", metavar="NAME",
+                    help="for counter runs under rocprofv3: launch only this kernel of the workload "
+                         "--steps times (rotating buffers), eagerly, and print what ran; NAME 'copy' "
+                         "launches a plain 64 MiB device-to-device copy instead (the counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -476,8 +514,12 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.profile_kernel == "copy":
+        return profile_copy(torch, dev, args.steps)
     wl = WORKLOADS[args.workload](dev, torch)
     torch.cuda.synchronize()
+    if args.profile_kernel:
+        return profile_kernel(torch, wl, args.profile_kernel, args.steps)
     use_graph = not args.eager
     K, W = args.steps, args.warmup
     print(f"[bench] workload {wl.name}: {len(wl.kernels)} kernels, warmup {W}, steps {K}, "
@@ -524,8 +566,9 @@ def main() -> int:
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
         try:
-            traffic = json.loads(tfile.read_text()).get(wl.name, {}).get(dom_name)
-        except (ValueError, OSError):
+            entry = json.loads(tfile.read_text()).get(wl.name, {}).get(dom_name)
+            traffic = entry["hbm_bytes_per_launch"] if entry else None
+        except (ValueError, OSError, KeyError, TypeError):
             traffic = None
     roofline = {"bound": "hbm", "kernel": dom_name, "achieved": round(dom["GB/s"], 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["frac_hbm"], 4),

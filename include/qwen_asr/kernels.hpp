@@ -1,0 +1,339 @@
+// qwen_asr/kernels.hpp -- C++ host mirror of the Rust `qwen_asr::kernels`
+// module (crates/qwen-asr/src/kernels/mod.rs) over device memory, built on the
+// C-ABI in qasr.h.
+//
+// Every function keeps the reference's name and argument order; Rust slices
+// become DevSlice<T> views of device memory (pointer + element count). Where
+// the reference would panic on a slice that is too short, these throw Panic
+// before anything is launched; a non-zero qasr_status throws QasrError.
+// Calls enqueue on the thread's current stream (set_stream) and never
+// synchronise.
+//
+// Header-only; link libqasr_hip.so or libqasr_hip.a plus amdhip64.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <utility>
+
+#include "../qasr.h"
+
+namespace qwen_asr {
+namespace kernels {
+
+// The reference's panics (slice index out of range, dimension mismatch).
+struct Panic : std::out_of_range {
+  using std::out_of_range::out_of_range;
+};
+
+// A C-ABI call returned a non-zero status.
+struct QasrError : std::runtime_error {
+  int code;
+  QasrError(const std::string& fn, int c)
+      : std::runtime_error(fn + " failed (" + std::to_string(c) + "): " + qasr_last_error()),
+        code(c) {}
+};
+
+// Non-owning view of `len` elements of device memory.
+template <class T>
+struct DevSlice {
+  T* ptr = nullptr;
+  size_t len = 0;
+
+  DevSlice() = default;
+  DevSlice(T* p, size_t n) : ptr(p), len(n) {}
+  template <class U>
+  DevSlice(const DevSlice<U>& o) : ptr(o.ptr), len(o.len) {}  // T* <- U* (adds const)
+
+  // &s[start..start+n], panicking like a Rust range index.
+  DevSlice sub(size_t start, size_t n) const {
+    if (start > len || n > len - start) {
+      throw Panic("range end index " + std::to_string(start + n) +
+                  " out of range for slice of length " + std::to_string(len));
+    }
+    return DevSlice(ptr + start, n);
+  }
+};
+
+// Owning device buffer (hipMalloc/hipFree), used by RopeCache and tests.
+template <class T>
+class DeviceBuffer {
+ public:
+  DeviceBuffer() = default;
+  explicit DeviceBuffer(size_t n) : n_(n) {
+    if (n && hipMalloc(reinterpret_cast<void**>(&p_), n * sizeof(T)) != hipSuccess) {
+      throw std::bad_alloc();
+    }
+  }
+  ~DeviceBuffer() { reset(); }
+  DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), n_(o.n_) { o.p_ = nullptr; o.n_ = 0; }
+  DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
+    if (this != &o) {
+      reset();
+      p_ = o.p_;
+      n_ = o.n_;
+      o.p_ = nullptr;
+      o.n_ = 0;
+    }
+    return *this;
+  }
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+
+  T* data() const { return p_; }
+  size_t size() const { return n_; }
+  DevSlice<T> slice() const { return DevSlice<T>(p_, n_); }
+  operator DevSlice<T>() const { return slice(); }
+  operator DevSlice<const T>() const { return DevSlice<const T>(p_, n_); }
+
+ private:
+  void reset() {
+    if (p_) (void)hipFree(p_);
+    p_ = nullptr;
+    n_ = 0;
+  }
+  T* p_ = nullptr;
+  size_t n_ = 0;
+};
+
+namespace detail {
+inline hipStream_t& stream_ref() {
+  thread_local hipStream_t s = nullptr;
+  return s;
+}
+template <class T>
+void need(const DevSlice<T>& s, size_t n, const char* name) {
+  if (s.len < n) {
+    throw Panic(std::string(name) + ": range end index " + std::to_string(n) +
+                " out of range for slice of length " + std::to_string(s.len));
+  }
+}
+inline void check(int rc, const char* fn) {
+  if (rc != QASR_OK) throw QasrError(fn, rc);
+}
+inline void* st() { return reinterpret_cast<void*>(stream_ref()); }
+}  // namespace detail
+
+inline void set_stream(hipStream_t s) { detail::stream_ref() = s; }
+inline hipStream_t current_stream() { return detail::stream_ref(); }
+
+using F = DevSlice<float>;
+using CF = DevSlice<const float>;
+
+// ---- basic / normalisation (kernels/mod.rs:486-488, 866-935) -----------------
+inline void add_inplace(F a, CF b, size_t n) {
+  detail::need(a, n, "a");
+  detail::need(b, n, "b");
+  detail::check(qasr_add_inplace_f32(a.ptr, b.ptr, n, detail::st()), "add_inplace");
+}
+
+inline void rms_norm(F out, CF x, CF weight, size_t seq_len, size_t hidden, float eps) {
+  detail::need(out, seq_len * hidden, "out");
+  detail::need(x, seq_len * hidden, "x");
+  detail::need(weight, hidden, "weight");
+  detail::check(qasr_rms_norm_f32(out.ptr, x.ptr, weight.ptr, seq_len, hidden, eps, detail::st()),
+                "rms_norm");
+}
+
+// add_inplace(x, delta) followed by rms_norm(out, x) in one pass.
+inline void add_rms_norm(F x, CF delta, CF weight, F out, size_t seq_len, size_t hidden, float eps) {
+  detail::need(x, seq_len * hidden, "x");
+  detail::need(delta, seq_len * hidden, "delta");
+  detail::need(weight, hidden, "weight");
+  detail::need(out, seq_len * hidden, "out");
+  detail::check(qasr_add_rms_norm_f32(x.ptr, delta.ptr, weight.ptr, out.ptr, seq_len, hidden, eps,
+                                      detail::st()),
+                "add_rms_norm");
+}
+
+inline void layer_norm(F out, CF x, CF weight, CF bias, size_t seq_len, size_t hidden, float eps) {
+  detail::need(out, seq_len * hidden, "out");
+  detail::need(x, seq_len * hidden, "x");
+  detail::need(weight, hidden, "weight");
+  detail::need(bias, hidden, "bias");
+  detail::check(qasr_layer_norm_f32(out.ptr, x.ptr, weight.ptr, bias.ptr, seq_len, hidden, eps,
+                                    detail::st()),
+                "layer_norm");
+}
+
+inline void rms_norm_per_head(F x, CF weight, size_t seq_len, size_t n_heads, size_t head_dim,
+                              float eps) {
+  detail::need(x, seq_len * n_heads * head_dim, "x");
+  detail::need(weight, head_dim, "weight");
+  detail::check(qasr_rms_norm_per_head_f32(x.ptr, weight.ptr, seq_len, n_heads, head_dim, eps,
+                                           detail::st()),
+                "rms_norm_per_head");
+}
+
+// ---- RoPE (kernels/mod.rs:1247-1267, decoder.rs:234-306) --------------------------
+inline void apply_rope_neox(F x, CF cos_vals, CF sin_vals, size_t seq, size_t n_heads,
+                            size_t head_dim) {
+  detail::need(x, seq * n_heads * head_dim, "x");
+  detail::need(cos_vals, seq * head_dim, "cos_vals");
+  detail::need(sin_vals, seq * head_dim, "sin_vals");
+  detail::check(qasr_apply_rope_neox_f32(x.ptr, cos_vals.ptr, sin_vals.ptr, seq, n_heads, head_dim,
+                                         detail::st()),
+                "apply_rope_neox");
+}
+
+// Device RoPE table with the reference's growth rule: capacity doubles from
+// 1024; new rows are filled on the device. A change of head_dim or theta
+// rebuilds the table from row 0.
+class RopeCache {
+ public:
+  void ensure(size_t required_pos, size_t head_dim, float theta) {
+    if (head_dim != head_dim_ || theta != theta_) {
+      cos_ = DeviceBuffer<float>();
+      sin_ = DeviceBuffer<float>();
+      cap_ = 0;
+      head_dim_ = head_dim;
+      theta_ = theta;
+    }
+    if (required_pos <= cap_) return;
+    size_t new_cap = cap_ ? cap_ : 1024;
+    while (new_cap < required_pos) new_cap *= 2;
+    DeviceBuffer<float> c(new_cap * head_dim), s(new_cap * head_dim);
+    if (cap_) {
+      const size_t bytes = cap_ * head_dim * sizeof(float);
+      if (hipMemcpyAsync(c.data(), cos_.data(), bytes, hipMemcpyDeviceToDevice, current_stream()) != hipSuccess ||
+          hipMemcpyAsync(s.data(), sin_.data(), bytes, hipMemcpyDeviceToDevice, current_stream()) != hipSuccess) {
+        throw std::runtime_error("RopeCache::ensure: device copy failed");
+      }
+    }
+    detail::check(qasr_rope_table_fill_f32(c.data(), s.data(), cap_, new_cap, head_dim, theta,
+                                           detail::st()),
+                  "rope_table_fill");
+    cos_ = std::move(c);
+    sin_ = std::move(s);
+    cap_ = new_cap;
+  }
+  size_t cap() const { return cap_; }
+  size_t head_dim() const { return head_dim_; }
+  CF cos() const { return cos_; }
+  CF sin() const { return sin_; }
+  CF cos_at(size_t pos) const { return cos().sub(pos * head_dim_, head_dim_); }
+  CF sin_at(size_t pos) const { return sin().sub(pos * head_dim_, head_dim_); }
+  CF cos_range(size_t start, size_t len) const { return cos().sub(start * head_dim_, len * head_dim_); }
+  CF sin_range(size_t start, size_t len) const { return sin().sub(start * head_dim_, len * head_dim_); }
+
+ private:
+  DeviceBuffer<float> cos_, sin_;
+  size_t cap_ = 0, head_dim_ = 0;
+  float theta_ = 0.0f;
+};
+
+// q/k head RMSNorm + RoPE at per-row positions (positions.len == 0: row s at s).
+inline void head_rms_norm_rope(F q, F k, CF q_norm_w, CF k_norm_w, const RopeCache& rope,
+                               DevSlice<const int32_t> positions, size_t seq, size_t n_heads,
+                               size_t n_kv_heads, size_t head_dim, float eps) {
+  detail::need(q, seq * n_heads * head_dim, "q");
+  detail::need(k, seq * n_kv_heads * head_dim, "k");
+  detail::need(q_norm_w, head_dim, "q_norm_w");
+  detail::need(k_norm_w, head_dim, "k_norm_w");
+  if (positions.ptr) detail::need(positions, seq, "positions");
+  if (rope.head_dim() != head_dim) throw Panic("head_rms_norm_rope: RopeCache head_dim mismatch");
+  detail::check(qasr_head_rms_norm_rope_f32(q.ptr, k.ptr, q_norm_w.ptr, k_norm_w.ptr,
+                                            rope.cos().ptr, rope.sin().ptr, positions.ptr, seq,
+                                            n_heads, n_kv_heads, head_dim, rope.cap(), eps,
+                                            detail::st()),
+                "head_rms_norm_rope");
+}
+
+// ---- activations (kernels/mod.rs:941-994) ------------------------------------
+inline void silu(F x, size_t n) {
+  detail::need(x, n, "x");
+  detail::check(qasr_silu_f32(x.ptr, n, detail::st()), "silu");
+}
+
+inline void gelu(F x, size_t n) {  // tanh form, as the reference CPU path
+  detail::need(x, n, "x");
+  detail::check(qasr_gelu_tanh_f32(x.ptr, n, detail::st()), "gelu");
+}
+
+inline void gelu_erf(F x, size_t n) {  // exact erf form
+  detail::need(x, n, "x");
+  detail::check(qasr_gelu_erf_f32(x.ptr, n, detail::st()), "gelu_erf");
+}
+
+inline void swiglu_multiply(F out, CF gate_up, size_t seq_len, size_t intermediate) {
+  detail::need(out, seq_len * intermediate, "out");
+  detail::need(gate_up, seq_len * 2 * intermediate, "gate_up");
+  detail::check(qasr_swiglu_multiply_f32(out.ptr, gate_up.ptr, seq_len, intermediate, detail::st()),
+                "swiglu_multiply");
+}
+
+inline void swiglu_multiply_inplace(F gate, CF up) {
+  detail::need(up, gate.len, "up");
+  detail::check(qasr_swiglu_split_f32(gate.ptr, gate.ptr, up.ptr, gate.len, detail::st()),
+                "swiglu_multiply_inplace");
+}
+
+// ---- position embeddings (kernels/mod.rs:1213-1226) -------------------------------
+inline void sinusoidal_pe(F pe, size_t n_pos, size_t d_model) {
+  detail::need(pe, n_pos * d_model, "pe");
+  detail::check(qasr_sinusoidal_pe_f32(pe.ptr, n_pos, d_model, detail::st()), "sinusoidal_pe");
+}
+
+// ---- token embeddings (decoder.rs:631-646) ------------------------------------------
+inline void tok_embed_bf16_to_f32(F dst, DevSlice<const uint16_t> tok_emb_bf16,
+                                  DevSlice<const int32_t> token_id_on_device, size_t dim) {
+  detail::need(dst, dim, "dst");
+  detail::need(token_id_on_device, 1, "token_id");
+  detail::check(qasr_embed_gather_bf16(dst.ptr, tok_emb_bf16.ptr, token_id_on_device.ptr, 1, dim,
+                                       tok_emb_bf16.len / dim, detail::st()),
+                "tok_embed_bf16_to_f32");
+}
+
+// ---- INT8 (kernels/mod.rs:650-673, quantize.rs:633-662) --------------------------------
+inline void linear_nobias_int8(F y, CF x, DevSlice<const int8_t> w_int8, CF scales, size_t seq_len,
+                               size_t in_dim, size_t out_dim) {
+  detail::need(y, seq_len * out_dim, "y");
+  detail::need(x, seq_len * in_dim, "x");
+  detail::need(w_int8, out_dim * in_dim, "w_int8");
+  detail::need(scales, out_dim, "scales");
+  detail::check(qasr_linear_nobias_int8_f32(y.ptr, x.ptr, w_int8.ptr, scales.ptr, seq_len, in_dim,
+                                            out_dim, detail::st()),
+                "linear_nobias_int8");
+}
+
+inline void linear_int8(F y, CF x, DevSlice<const int8_t> w_int8, CF scales, CF bias,
+                        size_t seq_len, size_t in_dim, size_t out_dim) {
+  detail::need(y, seq_len * out_dim, "y");
+  detail::need(x, seq_len * in_dim, "x");
+  detail::need(w_int8, out_dim * in_dim, "w_int8");
+  detail::need(scales, out_dim, "scales");
+  if (bias.ptr) detail::need(bias, out_dim, "bias");
+  detail::check(qasr_linear_int8_f32(y.ptr, x.ptr, w_int8.ptr, scales.ptr, bias.ptr, seq_len,
+                                     in_dim, out_dim, detail::st()),
+                "linear_int8");
+}
+
+inline void quantize_f32_to_int8(DevSlice<int8_t> q, F scales, CF f32_data, size_t out_dim,
+                                 size_t in_dim) {
+  detail::need(q, out_dim * in_dim, "q");
+  detail::need(scales, out_dim, "scales");
+  detail::need(f32_data, out_dim * in_dim, "f32_data");
+  detail::check(qasr_quantize_rows_i8(q.ptr, scales.ptr, f32_data.ptr, out_dim, in_dim,
+                                      detail::st()),
+                "quantize_f32_to_int8");
+}
+
+inline void gate_up_swiglu_w8a8(F out, DevSlice<const int8_t> w_gate_up, CF scales,
+                                DevSlice<const int8_t> xq, CF x_scales, size_t batch,
+                                size_t in_dim, size_t intermediate) {
+  detail::need(out, batch * intermediate, "out");
+  detail::need(w_gate_up, 2 * intermediate * in_dim, "w_gate_up");
+  detail::need(scales, 2 * intermediate, "scales");
+  detail::need(xq, batch * in_dim, "xq");
+  detail::need(x_scales, batch, "x_scales");
+  detail::check(qasr_gate_up_swiglu_w8a8(out.ptr, w_gate_up.ptr, scales.ptr, xq.ptr, x_scales.ptr,
+                                         batch, in_dim, intermediate, detail::st()),
+                "gate_up_swiglu_w8a8");
+}
+
+}  // namespace kernels
+}  // namespace qwen_asr

@@ -89,7 +89,34 @@ def build(verbose: bool = False) -> Path:
     if ARCHIVE.exists():
         ARCHIVE.unlink()
     _run(["ar", "rcs", str(ARCHIVE), *map(str, objs)])
+    build_cpp_tests(hipcc, verbose)
     return SO
+
+
+ROOT = PKG.parent
+CPP_TESTS = ROOT / "tests" / "cpp"
+CPP_TEST_BIN = CPP_TESTS / "_build" / "test_kernels"
+
+
+def build_cpp_tests(hipcc: str | None = None, verbose: bool = False) -> Path:
+    """Builds the C++ host-mirror test against the static archive (so the
+    binary carries its own copy of the kernels: the static-link path a Rust
+    build.rs would use)."""
+    hipcc = hipcc or _hipcc()
+    CPP_TEST_BIN.parent.mkdir(exist_ok=True)
+    obj = CPP_TEST_BIN.with_suffix(".o")
+    tmp = CPP_TEST_BIN.with_suffix(".tmp")
+    # compile and link separately: hipcc applies ``-x hip`` to every input
+    # that follows a .cpp source, which would include the archive
+    cmds = [[hipcc, f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-Wall", "-I", str(ROOT / "include"),
+             "-c", str(CPP_TESTS / "test_kernels.cpp"), "-o", str(obj)],
+            [hipcc, f"--offload-arch={ARCH}", str(obj), str(ARCHIVE), "-o", str(tmp)]]
+    for cmd in cmds:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        _run(cmd)
+    os.replace(tmp, CPP_TEST_BIN)
+    return CPP_TEST_BIN
 
 
 if __name__ == "__main__":

@@ -1,0 +1,230 @@
+// The reference's kernel unit tests (crates/qwen-asr/tests/kernels.rs) restated
+// on the GPU through the C++ host mirror qwen_asr::kernels, plus drop-in
+// checks the reference cannot express (device tables, panics on short slices).
+//
+// Built by qwenasr_amd/build.py against the static archive libqasr_hip.a;
+// run by tests/test_gpu_cpp.py. Prints one line per test, exits non-zero on
+// any failure.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "qwen_asr/kernels.hpp"
+
+namespace K = qwen_asr::kernels;
+
+static int g_failed = 0;
+
+#define EXPECT(cond, ...)                                \
+  do {                                                   \
+    if (!(cond)) {                                       \
+      std::fprintf(stderr, "  expectation failed: " #cond " -- " __VA_ARGS__); \
+      std::fprintf(stderr, "\n");                        \
+      throw std::runtime_error("expectation failed");    \
+    }                                                    \
+  } while (0)
+
+template <class T>
+static K::DeviceBuffer<T> upload(const std::vector<T>& h) {
+  K::DeviceBuffer<T> d(h.size());
+  if (hipMemcpy(d.data(), h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+    throw std::runtime_error("hipMemcpy H2D failed");
+  return d;
+}
+
+template <class T>
+static std::vector<T> download(const K::DeviceBuffer<T>& d) {
+  std::vector<T> h(d.size());
+  if (hipDeviceSynchronize() != hipSuccess) throw std::runtime_error("device sync failed");
+  if (hipMemcpy(h.data(), d.data(), h.size() * sizeof(T), hipMemcpyDeviceToHost) != hipSuccess)
+    throw std::runtime_error("hipMemcpy D2H failed");
+  return h;
+}
+
+static void copy_row(std::vector<float>& h, const float* d) {
+  if (hipDeviceSynchronize() != hipSuccess ||
+      hipMemcpy(h.data(), d, h.size() * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess)
+    throw std::runtime_error("hipMemcpy D2H failed");
+}
+
+static float max_abs_err(const std::vector<float>& a, const std::vector<float>& b) {
+  float m = 0.0f;
+  for (size_t i = 0; i < a.size(); ++i) m = std::fmax(m, std::fabs(a[i] - b[i]));
+  return m;
+}
+
+static void run(const char* name, const std::function<void()>& fn) {
+  try {
+    fn();
+    std::printf("test %s ... ok\n", name);
+  } catch (const std::exception& e) {
+    ++g_failed;
+    std::printf("test %s ... FAILED (%s)\n", name, e.what());
+  }
+}
+
+// tests/kernels.rs:60-72
+static void test_rms_norm() {
+  const size_t dim = 128;
+  std::vector<float> x(dim), w(dim, 1.0f);
+  for (size_t i = 0; i < dim; ++i) x[i] = (float)i * 0.02f - 1.28f;
+  auto dx = upload(x), dw = upload(w);
+  K::DeviceBuffer<float> out(dim);
+  K::rms_norm(out, dx, dw, 1, dim, 1e-6f);
+  auto o = download(out);
+  double ss = 0;
+  for (float v : o) ss += (double)v * v;
+  const double rms = std::sqrt(ss / dim);
+  EXPECT(std::fabs(rms - 1.0) < 0.01, "RMS norm output should have RMS ~1.0, got %f", rms);
+}
+
+// tests/kernels.rs:74-89
+static void test_layer_norm() {
+  const size_t dim = 128;
+  std::vector<float> x(dim), w(dim, 1.0f), b(dim, 0.0f);
+  for (size_t i = 0; i < dim; ++i) x[i] = (float)i * 0.05f - 3.2f;
+  auto dx = upload(x), dw = upload(w), db = upload(b);
+  K::DeviceBuffer<float> out(dim);
+  K::layer_norm(out, dx, dw, db, 1, dim, 1e-5f);
+  auto o = download(out);
+  double mean = 0, var = 0;
+  for (float v : o) mean += v;
+  mean /= dim;
+  for (float v : o) var += (v - mean) * (v - mean);
+  var /= dim;
+  EXPECT(std::fabs(mean) < 0.01, "LayerNorm mean should be ~0, got %f", mean);
+  EXPECT(std::fabs(var - 1.0) < 0.02, "LayerNorm variance should be ~1, got %f", var);
+}
+
+// tests/kernels.rs:105-113, for both GELU forms
+static void test_gelu() {
+  for (int erf_form = 0; erf_form < 2; ++erf_form) {
+    std::vector<float> x = {0.0f, 1.0f, -1.0f, 2.0f, -0.5f};
+    auto d = upload(x);
+    if (erf_form) K::gelu_erf(d, x.size()); else K::gelu(d, x.size());
+    auto o = download(d);
+    EXPECT(std::fabs(o[0]) < 1e-5f, "GELU(0) should be ~0");
+    EXPECT(o[1] > 0.5f, "GELU(1) should be > 0.5");
+    EXPECT(o[2] < 0.0f, "GELU(-1) should be negative");
+  }
+}
+
+// tests/kernels.rs:115-124
+static void test_silu() {
+  std::vector<float> orig = {0.0f, 1.0f, -1.0f, 5.0f}, expected(4);
+  for (int i = 0; i < 4; ++i) expected[i] = orig[i] / (1.0f + std::exp(-orig[i]));
+  auto d = upload(orig);
+  K::silu(d, 4);
+  const float err = max_abs_err(download(d), expected);
+  EXPECT(err < 1e-5f, "SiLU mismatch, max_err=%g", err);
+}
+
+// tests/kernels.rs:126-152 (the vector ops on the path: add_inplace)
+static void test_vec_ops() {
+  const size_t n = 256;
+  std::vector<float> a(n), b(n);
+  for (size_t i = 0; i < n; ++i) {
+    a[i] = (float)i * 0.1f;
+    b[i] = (float)(n - i) * 0.1f;
+  }
+  auto da = upload(a), db = upload(b);
+  K::add_inplace(da, db, n);
+  auto o = download(da);
+  for (size_t i = 0; i < n; ++i) EXPECT(std::fabs(o[i] - (a[i] + b[i])) < 1e-5f, "add at %zu", i);
+}
+
+// RopeCache + apply_rope_neox: position 0 is the identity; the table grows by
+// doubling from 1024 and keeps its rows.
+static void test_rope_cache() {
+  K::RopeCache rope;
+  rope.ensure(10, 128, 1e6f);
+  EXPECT(rope.cap() == 1024, "initial capacity 1024, got %zu", rope.cap());
+  std::vector<float> x(2 * 128);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin((float)i);
+  auto dx = upload(x);
+  K::apply_rope_neox(dx, rope.cos_range(0, 1), rope.sin_range(0, 1), 1, 2, 128);
+  auto o = download(dx);
+  for (size_t i = 0; i < x.size(); ++i) EXPECT(o[i] == x[i], "pos 0 must be identity at %zu", i);
+  std::vector<float> row(128);
+  copy_row(row, rope.cos_at(700).ptr);
+  rope.ensure(3000, 128, 1e6f);
+  EXPECT(rope.cap() == 4096, "grown capacity 4096, got %zu", rope.cap());
+  std::vector<float> row2(128);
+  copy_row(row2, rope.cos_at(700).ptr);
+  EXPECT(row == row2, "growth must keep existing rows");
+  EXPECT(std::fabs(row2[0] - std::cos(700.0f)) < 1e-6f, "cos(700) column 0");
+}
+
+// linear_nobias_int8 with integer inputs and unit scales is exact.
+static void test_linear_int8_exact() {
+  const size_t in = 2048, out_dim = 64;
+  std::vector<int8_t> w(in * out_dim);
+  std::vector<float> x(in), s(out_dim, 1.0f);
+  for (size_t i = 0; i < w.size(); ++i) w[i] = (int8_t)((int)(i * 2654435761u >> 7) % 255 - 127);
+  for (size_t k = 0; k < in; ++k) x[k] = (float)((int)(k % 41) - 20);
+  auto dw = upload(w);
+  auto dx = upload(x), ds = upload(s);
+  K::DeviceBuffer<float> y(out_dim);
+  K::linear_nobias_int8(y, dx, dw, ds, 1, in, out_dim);
+  auto o = download(y);
+  for (size_t r = 0; r < out_dim; ++r) {
+    long long dot = 0;
+    for (size_t k = 0; k < in; ++k) dot += (long long)w[r * in + k] * (long long)x[k];
+    EXPECT((long long)o[r] == dot, "row %zu: %f vs %lld", r, o[r], dot);
+  }
+}
+
+// A short slice panics before anything is launched (the reference's slice
+// index panic).
+static void test_short_slice_panics() {
+  K::DeviceBuffer<float> out(100), x(128), w(128);
+  bool threw = false;
+  try {
+    K::rms_norm(out, x, w, 1, 128, 1e-6f);
+  } catch (const K::Panic&) {
+    threw = true;
+  }
+  EXPECT(threw, "rms_norm with a 100-element out slice must panic");
+  threw = false;
+  try {
+    K::DevSlice<float>(out.data(), 100).sub(90, 20);
+  } catch (const K::Panic&) {
+    threw = true;
+  }
+  EXPECT(threw, "sub-slice past the end must panic");
+}
+
+// A C-ABI contract breach surfaces as QasrError with the status code.
+static void test_status_errors() {
+  K::DeviceBuffer<float> x(2 * 4 * 127), c(2 * 127), s(2 * 127);
+  bool threw = false;
+  try {
+    K::apply_rope_neox(x, c, s, 2, 4, 127);  // odd head_dim
+  } catch (const K::QasrError& e) {
+    threw = e.code == QASR_ERR_INVALID_ARG;
+  }
+  EXPECT(threw, "odd head_dim must return QASR_ERR_INVALID_ARG");
+}
+
+int main() {
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+    std::printf("no GPU visible\n");
+    return 2;
+  }
+  run("test_rms_norm", test_rms_norm);
+  run("test_layer_norm", test_layer_norm);
+  run("test_gelu", test_gelu);
+  run("test_silu", test_silu);
+  run("test_vec_ops", test_vec_ops);
+  run("test_rope_cache", test_rope_cache);
+  run("test_linear_int8_exact", test_linear_int8_exact);
+  run("test_short_slice_panics", test_short_slice_panics);
+  run("test_status_errors", test_status_errors);
+  std::printf("%s: %d failed\n", g_failed ? "FAILED" : "ok", g_failed);
+  return g_failed ? 1 : 0;
+}

@@ -132,3 +132,13 @@ def test_qasr_error_carries_status_and_message():
         _lib.call("qasr_apply_rope_neox_f32", FAKE, FAKE, FAKE, 2, 4, 127, NULL)
     assert ei.value.code == _lib.QASR_ERR_INVALID_ARG
     assert "even" in ei.value.msg
+
+
+def test_cpp_mirror_binary_links_the_static_archive():
+    from qwenasr_amd import build
+
+    assert build.CPP_TEST_BIN.exists(), "C++ test not built"
+    ldd = subprocess.run(["ldd", str(build.CPP_TEST_BIN)], capture_output=True, text=True).stdout
+    assert "libqasr_hip.so" not in ldd  # kernels come from libqasr_hip.a
+    nm = subprocess.run(["nm", str(build.CPP_TEST_BIN)], capture_output=True, text=True).stdout
+    assert " T qasr_rms_norm_f32" in nm
