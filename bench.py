@@ -115,10 +115,10 @@ class C1DecodeChain(Workload):
             "head_rms_norm_rope": (lambda i: K.head_rms_norm_rope(
                 self.q[i % S], self.k[i % S], self.qw, self.kw, self.rope.cos, self.rope.sin,
                 self.pos[i % S], 1, nq, nk, hd, c["eps"]),
-                2 * (nq + nk) * hd * F + 2 * hd * F + 2 * hd * F * 2),
+                2 * (nq + nk) * hd * F + 2 * hd * F + 2 * hd * F + 4),
             "swiglu": (lambda i: K.swiglu_split(self.o[i % S], self.g[i % S], self.u[i % S], I), 3 * I * F),
         }
-        self.step_bytes = 83968
+        self.step_bytes = sum(b for _, b in self.kernels.values())
 
     def config(self):
         return {"batch": 1, "hidden": 1024, "heads": "16q/8kv x 128", "intermediate": 3072}
@@ -159,15 +159,15 @@ class C2PrefillChain(Workload):
             "embed_gather": (lambda i: K.embed_gather_f32(self.x[i % S], self.table, self.ids[i % S], T, H),
                              T * 4 + 2 * T * H * F),
             "add_rms_norm": (lambda i: K.add_rms_norm(self.x[i % S], self.d[i % S], self.w, self.y[i % S], T, H, c["eps"]),
-                             5 * T * H * F + H * F),
+                             4 * T * H * F + H * F),
             "head_rms_norm_rope": (lambda i: K.head_rms_norm_rope(
                 self.q[i % S], self.k[i % S], self.qw, self.kw, self.rope.cos, self.rope.sin, self.pos,
                 T, nq, nk, hd, c["eps"]),
-                2 * T * (nq + nk) * hd * F + 2 * hd * F + 2 * T * hd * F),
+                2 * T * (nq + nk) * hd * F + 2 * hd * F + 2 * T * hd * F + T * 4),
             "swiglu_multiply": (lambda i: K.swiglu_multiply(self.o[i % S], self.gu[i % S], T, I),
                                 3 * T * I * F),
         }
-        self.step_bytes = 46668800
+        self.step_bytes = sum(b for _, b in self.kernels.values())
 
     def config(self):
         return {"seq_len": 512, "hidden": 1024, "heads": "16q/8kv x 128", "intermediate": 3072,
@@ -195,12 +195,12 @@ class C3EncoderOps(Workload):
         self.pe = torch.empty(P * D, device=dev)
         K.sinusoidal_pe(self.pe, P, D)
         self.kernels = {
-            "pe_add": (lambda i: K.pe_add(self.x[i % S], self.pe, T, D, P), 2 * T * D * F),
+            "pe_add": (lambda i: K.pe_add(self.x[i % S], self.pe, T, D, P), 2 * T * D * F + P * D * F),
             "layer_norm": (lambda i: K.layer_norm(self.y[i % S], self.x[i % S], self.w, self.b, T, D, c["eps"]),
                            2 * T * D * F + 2 * D * F),
             "gelu_erf": (lambda i: K.gelu_erf(self.h[i % S], T * FF), 2 * T * FF * F),
         }
-        self.step_bytes = 129031168
+        self.step_bytes = sum(b for _, b in self.kernels.values())
 
     def config(self):
         return {"rows": 3000, "d_model": 896, "ffn": 3584, "pe_period": 13, "buffer_sets": self.S}
@@ -238,7 +238,7 @@ class C4Int8Matvec(Workload):
             self.outs[i % L], self.layers[i % L], self.xs[i % L], H, I), layer_bytes)}
         self.all_layers = all_layers
         self.layer_bytes = layer_bytes
-        self.step_bytes = L * 25247744
+        self.step_bytes = L * layer_bytes
 
     def step(self, i):
         self.all_layers(i)
@@ -295,7 +295,7 @@ class C5BatchedDecode(Workload):
                 self.o[i % S], self.layers[i % L], self.xq[i % S], self.xsc[i % S], B, H, I),
                 2 * I * H + 2 * I * F + B * H + B * F + B * I * F),
         }
-        self.step_bytes = 50653184
+        self.step_bytes = sum(b for _, b in self.kernels.values())
         self.gemm_ops = 2 * B * 2 * I * H
 
     def config(self):
@@ -347,7 +347,9 @@ def time_replay(torch, fn, n: int, use_graph: bool, reps: int = 1) -> float:
 # ---------------------------------------------------------------------------
 # CPU baseline (oracle, reference thread model)
 # ---------------------------------------------------------------------------
-def cpu_baseline(name: str, seconds: float) -> dict:
+def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
+    """The oracle timed on this host over a bounded sample of the same workload,
+    reported in the GPU step's unit (its algorithmic bytes per second)."""
     import numpy as np
 
     import oracle
@@ -403,10 +405,9 @@ def cpu_baseline(name: str, seconds: float) -> dict:
                 oracle.swiglu_multiply(gu, T, I)
 
         n, dt = run_until(step, seconds)
-        wl_bytes = {"c1": 83968, "c2": 46668800, "c5": 50653184}[name]
         per = dt / n
         threads = min(nproc, 16) if name == "c5" else 1
-        return {"value": wl_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
                 "ms_per_step": per * 1e3, "tokens_per_s": T / per if name != "c5" else T / (28 * per),
                 "sample": f"{n} full steps of the {name} chain (T={T}) on the oracle, "
                           f"{'single-threaded norms/RoPE/SwiGLU' + (', INT8 W8A32 matvec on ' + str(threads) + ' threads' if name == 'c5' else '')}"}
@@ -425,7 +426,7 @@ def cpu_baseline(name: str, seconds: float) -> dict:
 
         n, dt = run_until(step, seconds)
         per = dt / n
-        return {"value": 129031168 / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
                 "ms_per_step": per * 1e3,
                 "sample": f"{n} full c3 steps on the oracle, single-threaded; GELU is the reference's tanh form"}
     if name == "c4":
@@ -440,7 +441,7 @@ def cpu_baseline(name: str, seconds: float) -> dict:
 
         n, dt = run_until(step, seconds)
         per = dt / n
-        return {"value": 25247744 / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        return {"value": step_bytes / 28 / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
                 "ms_per_step": per * 1e3 * 28, "tokens_per_s": 1.0 / (28 * per),
                 "sample": f"{n} layer matvecs (W8A32, the reference's INT8 path) + SwiGLU on the oracle, "
                           f"{threads} threads; one weight matrix reused, so it is LLC-warm"}
@@ -559,8 +560,9 @@ def main() -> int:
     else:
         tokens_per_s = wl.unit_tokens / (ms_step * 1e-3)
 
-    # dominant kernel = largest share of the step time
-    dom_name = max(per_kernel, key=lambda k: per_kernel[k]["us"] * (28 if wl.name == "c4" else 1))
+    # dominant kernel = the one moving the most algorithmic bytes per step (a
+    # fixed choice per workload; by time the small c2 kernels tie within noise)
+    dom_name = max(per_kernel, key=lambda k: per_kernel[k]["bytes"])
     dom = per_kernel[dom_name]
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
@@ -582,7 +584,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         print(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s sample)...", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(wl.name, args.cpu_seconds)
+        cpu = cpu_baseline(wl.name, args.cpu_seconds, wl.step_bytes)
 
     out = {
         "metric": METRIC,
