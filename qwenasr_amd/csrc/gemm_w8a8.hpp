@@ -34,6 +34,18 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmK = 64;  // k per MFMA
 
+// SwiGLU epilogue of every W8A8 kernel (matvec and GEMM alike, so their
+// results agree bit for bit): g = (dg * xs) * sg, u = (du * xs) * su,
+// out = silu(g) * u. silu uses the hardware exp2 (__expf) and reciprocal:
+// a few ulp from g / (1 + expf(-g)), far inside the 1e-5 tolerance, at a third
+// of the VALU cost of the IEEE exp + divide. g >> 0 gives exactly g (exp
+// underflows to 0, rcp(1) = 1); g << 0 gives -0 (rcp(inf) = 0).
+QASR_DEV float swiglu_w8a8(int dg, int du, float xs, float sg, float su) {
+  const float g = ((float)dg * xs) * sg;
+  const float u = ((float)du * xs) * su;
+  return (g * __builtin_amdgcn_rcpf(1.0f + __expf(-g))) * u;
+}
+
 // ---------------------------------------------------------------------------
 // Main kernel
 // ---------------------------------------------------------------------------
@@ -174,16 +186,8 @@ __global__ __launch_bounds__(256) void gemm_w8a8_swiglu_lds_kernel(
       const int n = n_wave + 16 * i + 4 * g;
       const float4 sc = *reinterpret_cast<const float4*>(scales + n);
       float2 o;
-      {
-        const float gg = ((float)acc[i][j][0] * xsm) * sc.x;
-        const float uu = ((float)acc[i][j][1] * xsm) * sc.y;
-        o.x = (gg / (1.0f + expf(-gg))) * uu;
-      }
-      {
-        const float gg = ((float)acc[i][j][2] * xsm) * sc.z;
-        const float uu = ((float)acc[i][j][3] * xsm) * sc.w;
-        o.y = (gg / (1.0f + expf(-gg))) * uu;
-      }
+      o.x = swiglu_w8a8(acc[i][j][0], acc[i][j][1], xsm, sc.x, sc.y);
+      o.y = swiglu_w8a8(acc[i][j][2], acc[i][j][3], xsm, sc.z, sc.w);
       *reinterpret_cast<float2*>(out + (size_t)m * inter + (n >> 1)) = o;
     }
   }
@@ -248,16 +252,8 @@ __global__ __launch_bounds__(256) void gemm_w8a8_swiglu_kernel(
       const int n = n0 + 16 * i + 4 * g;
       const int p = n >> 1;
       float2 o;
-      {
-        const float gg = ((float)acc[i][j][0] * xsm) * scales[n];
-        const float uu = ((float)acc[i][j][1] * xsm) * scales[n + 1];
-        o.x = (gg / (1.0f + expf(-gg))) * uu;
-      }
-      {
-        const float gg = ((float)acc[i][j][2] * xsm) * scales[n + 2];
-        const float uu = ((float)acc[i][j][3] * xsm) * scales[n + 3];
-        o.y = (gg / (1.0f + expf(-gg))) * uu;
-      }
+      o.x = swiglu_w8a8(acc[i][j][0], acc[i][j][1], xsm, scales[n], scales[n + 1]);
+      o.y = swiglu_w8a8(acc[i][j][2], acc[i][j][3], xsm, scales[n + 2], scales[n + 3]);
       *reinterpret_cast<float2*>(out + (size_t)m * inter + p) = o;
     }
   }
@@ -361,44 +357,81 @@ __global__ __launch_bounds__(256) void pack_w8a8_tiles_kernel(int8_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// Packed-weight kernel: one workgroup of 4*KSPLIT waves per CU, split-K.
+// Packed-weight kernel: one 8-wave workgroup per CU, K split in two halves.
 //
-// A workgroup owns 192 W rows x 64 tokens. Its 64 token rows of Xq are staged
-// once in LDS (direct global->LDS loads). Wave w = 4*kq + rg owns row group rg
-// (48 rows = 3 tiles of 16) for all 64 tokens (4 tiles) -- 12 accumulators --
-// over k-quarter kq of the K range, so every W tile and every X slice is read
-// once per workgroup, and 8 or 16 resident waves per CU keep the L2->L1 fill
-// path busy (one 4-wave workgroup per CU tops out near 40 GB/s per CU, 16
-// waves near 100 GB/s). After the K loop the waves with kq > 0 store their
-// partial sums in LDS (the X tile's space); the kq = 0 wave of each row group
-// adds them (exact int32) and finishes the SwiGLU epilogue.
+// A workgroup owns 192 W rows x 64 tokens. Wave w = 4*kq + rg owns row group
+// rg (48 rows = 3 MFMA tiles of 16) for all 64 tokens (4 tiles, 12
+// accumulators) over K half kq, so every W tile and every Xq slice is read
+// once per workgroup, and two waves share each SIMD: a single wave cannot
+// issue v_mfma_i32_16x16x64_i8 back to back at full rate, two interleaved
+// waves can.
+//
+// Xq is staged in LDS by direct global->LDS loads in 32 KiB chunks of
+// [64 rows][512 bytes]; the 16-byte slot p of a row holds the row's logical
+// slot p ^ (row & 15), so the b128 fragment reads of 16 rows at one k offset
+// hit 16 distinct bank groups. The first chunk of each K half is waited for
+// before the loop, the second one when the loop reaches it. W streams from the
+// tile-packed layout straight into registers, PF k-steps ahead, with
+// non-temporal loads; the per-row and per-token scales of the epilogue are
+// loaded before the loop so their latency hides under it.
+//
+// After the loop the two waves of a row group exchange halves through LDS:
+// wave kq keeps token tiles 2kq, 2kq+1, adds its partner's partial sums for
+// them (exact int32) and runs the SwiGLU epilogue on them. The results are
+// staged as a [64][96] fp32 tile in LDS and written with 16-byte stores, each
+// token's 96 outputs (384 bytes) contiguous.
 // ---------------------------------------------------------------------------
-constexpr int kKsBN = 192;
-constexpr int kKsBM = 64;
-constexpr int kKsPartialBytes = 12 * 4 * 64 * 4;  // one wave's 12 accumulators
+constexpr int kPkBN = 192;       // W rows per workgroup
+constexpr int kPkBM = 64;        // tokens per workgroup
+constexpr int kPkWaves = 8;      // 4 row groups x 2 K halves
+constexpr int kPkChunk = 512;    // bytes of K per staged X chunk
+constexpr int kPkPrefetch = 4;   // k-steps of W in flight per wave
+constexpr size_t kPkLds = 131072;
 
-template <int KSPLIT>
-constexpr int ks_prefetch() { return KSPLIT == 4 ? 2 : 8; }
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+#define QASR_VMCNT(n) (((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 
-template <int KS, int KSPLIT>  // KS = K / 64
-__global__ __launch_bounds__(64 * 4 * KSPLIT) void gemm_w8a8_swiglu_ksplit_kernel(
+// X chunk c of the workgroup's 64 token rows: 32 DMA instructions of 1 KiB
+// (two rows each), 4 per wave. Rows past the batch re-read row batch - 1
+// (valid memory); their results are never stored.
+template <int K>
+QASR_DEV void stage_x_chunk(int8_t* lds, const int8_t* __restrict__ xq, int c, int wave, int lane,
+                            int m0, int batch) {
+#pragma unroll
+  for (int t = 0; t < 32 / kPkWaves; ++t) {
+    const int d = wave * (32 / kPkWaves) + t;
+    const int row = 2 * d + (lane >> 5);
+    const int slot = (lane & 31) ^ (row & 15);
+    const int src_row = m0 + row < batch ? m0 + row : batch - 1;
+    const int8_t* src = xq + (size_t)src_row * K + kPkChunk * c + 16 * slot;
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)(lds + c * 32768 + d * 1024),
+                                     16, 0, 0);
+  }
+}
+
+template <int KS, bool VEC_OUT>  // KS = K / 64 (16 or 32)
+__global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
     float* __restrict__ out, const int8_t* __restrict__ wpk, const float* __restrict__ scales,
     const int8_t* __restrict__ xq, const float* __restrict__ xs, int batch, int inter,
     int n_tiles, int m_tiles) {
   constexpr int K = KS * kPackK;
-  constexpr int STRIDE = K + kLdsRowPad;
-  constexpr int KW = KS / KSPLIT;  // k-steps per wave
-  constexpr int PF = ks_prefetch<KSPLIT>();
-  constexpr int NWAVES = 4 * KSPLIT;
+  constexpr int KW = KS / 2;                // k-steps per wave
+  constexpr int NCH = K / kPkChunk;         // X chunks (2 or 4)
+  constexpr int CH_HALF = NCH / 2;          // chunks per K half
+  constexpr int DMA_PER_CHUNK = 32 / kPkWaves;
+  constexpr int PF = kPkPrefetch;
+  constexpr int EPI_LOADS = 3 + 2;          // scale float4s + token scales
   extern __shared__ __align__(16) int8_t lds[];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int rg = wave & 3;
-  const int kq = wave >> 2;
-  const int r = lane & 15;
-  const int g = lane >> 4;
+  const int rg = wave & 3, kq = wave >> 2;
+  const int r = lane & 15, g = lane >> 4;
 
+  // XCD-aware order: block b runs on XCD b % 8; the m_tiles blocks that share
+  // a W tile go to the same XCD back to back, so 3 of 4 W reads hit its L2.
   const int b = blockIdx.x;
   int tile_n, tile_m;
   if (n_tiles % kNumXcd == 0) {
@@ -409,26 +442,20 @@ __global__ __launch_bounds__(64 * 4 * KSPLIT) void gemm_w8a8_swiglu_ksplit_kerne
     tile_m = b % m_tiles;
     tile_n = b / m_tiles;
   }
-  const int n_wave = tile_n * kKsBN + rg * 48;
-  const int m0 = tile_m * kKsBM;
+  const int n_wave = tile_n * kPkBN + rg * 48;
+  const int m0 = tile_m * kPkBM;
   const int k0 = kq * KW;
 
-  // X tile -> LDS, 1 KiB per wave instruction.
-  {
-    constexpr int CPR = K / 1024;
-    constexpr int CHUNKS = kKsBM * CPR;
-#pragma unroll 4
-    for (int c = wave; c < CHUNKS; c += NWAVES) {
-      const int row = c / CPR, part = c - row * CPR;
-      const int src_row = m0 + row < batch ? m0 + row : batch - 1;
-      const int8_t* src = xq + (size_t)src_row * K + 1024 * part + 16 * lane;
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)src,
-          (__attribute__((address_space(3))) void*)(lds + row * STRIDE + 1024 * part), 16, 0, 0);
-    }
+  // X: the first chunk of each K half, then the rest.
+  stage_x_chunk<K>(lds, xq, 0, wave, lane, m0, batch);
+  stage_x_chunk<K>(lds, xq, CH_HALF, wave, lane, m0, batch);
+#pragma unroll
+  for (int c = 1; c < CH_HALF; ++c) {
+    stage_x_chunk<K>(lds, xq, c, wave, lane, m0, batch);
+    stage_x_chunk<K>(lds, xq, CH_HALF + c, wave, lane, m0, batch);
   }
 
-  // W stream: 3 row tiles, k-steps k0 .. k0+KW-1.
+  // W window, then the epilogue operands (newest loads).
   const int8_t* wp = wpk + packed_tile_offset(n_wave / kPackRows, k0, KS) + 16 * lane;
   constexpr size_t ROW_TILE = (size_t)KS * 1024;
   v4i wbuf[PF][3];
@@ -436,9 +463,19 @@ __global__ __launch_bounds__(64 * 4 * KSPLIT) void gemm_w8a8_swiglu_ksplit_kerne
   for (int d = 0; d < PF; ++d)
 #pragma unroll
     for (int i = 0; i < 3; ++i)
-      if (d < KW) wbuf[d][i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + i * ROW_TILE + d * 1024));
+      wbuf[d][i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + i * ROW_TILE + d * 1024));
+  float4 sc[3];
+  float xsv[2];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) sc[i] = *reinterpret_cast<const float4*>(scales + n_wave + 16 * i + 4 * g);
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const int m = m0 + 16 * (2 * kq + jj) + r;
+    xsv[jj] = xs[m < batch ? m : batch - 1];
+  }
   __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(0);
+  // this wave's first-chunk DMAs are its oldest loads: allow everything newer
+  __builtin_amdgcn_s_waitcnt(QASR_VMCNT(2 * (CH_HALF - 1) * DMA_PER_CHUNK + 3 * PF + EPI_LOADS));
   __syncthreads();
 
   v4i acc[3][4];
@@ -447,13 +484,29 @@ __global__ __launch_bounds__(64 * 4 * KSPLIT) void gemm_w8a8_swiglu_ksplit_kerne
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-  const int8_t* xl = lds + r * STRIDE + 16 * g + k0 * kPackK;
+  // B fragment of token tile j at global k-step s
+  auto xfrag = [&](int s, int j) -> v4i {
+    const int c = s >> 3;
+    const int slot = 4 * (s & 7) + g;
+    return *reinterpret_cast<const v4i*>(lds + c * 32768 + (16 * j + r) * kPkChunk + 16 * (slot ^ r));
+  };
+  v4i bcur[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bcur[j] = xfrag(k0, j);
+
 #pragma unroll
   for (int s0 = 0; s0 < KW; s0 += PF) {
 #pragma unroll
     for (int d = 0; d < PF; ++d) {
       const int s = s0 + d;
       if (s < KW) {
+        if (CH_HALF > 1 && s % 8 == 7 && s + 1 < KW) {
+          // step s+1 reads the next chunk: every DMA is older than the W window
+          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_s_waitcnt(QASR_VMCNT(3 * PF));
+          __syncthreads();
+          __builtin_amdgcn_sched_barrier(0);
+        }
         v4i a[3];
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
@@ -462,119 +515,139 @@ __global__ __launch_bounds__(64 * 4 * KSPLIT) void gemm_w8a8_swiglu_ksplit_kerne
             wbuf[d][i] = __builtin_nontemporal_load(
                 reinterpret_cast<const v4i*>(wp + i * ROW_TILE + (s + PF) * 1024));
         }
+        // Keep the prefetch and the next B fragments issued here: without the
+        // fences the scheduler sinks each load next to its use.
         __builtin_amdgcn_sched_barrier(0);
-        v4i bx[4];
+        v4i bn[4];
+        if (s + 1 < KW) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          bx[j] = *reinterpret_cast<const v4i*>(xl + 16 * j * STRIDE + s * kPackK);
+          for (int j = 0; j < 4; ++j) bn[j] = xfrag(k0 + s + 1, j);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 3; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bx[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bcur[j], acc[i][j], 0, 0, 0);
+        if (s + 1 < KW) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bcur[j] = bn[j];
+        }
       }
     }
   }
 
-  // Split-K reduction through LDS: partial set (kq - 1, rg) is 12 KiB laid out
-  // [tile][item][lane] int32, so lane-consecutive addresses.
-  int* red = reinterpret_cast<int*>(lds);
-  __syncthreads();  // all waves are done reading the X tile
-  if (kq > 0) {
-    int* dst = red + ((kq - 1) * 4 + rg) * (kKsPartialBytes / 4) + lane;
+  // Exchange K-half partial sums. Register arrays take constant indices only
+  // (a runtime index would move acc to scratch memory).
+  __syncthreads();  // X no longer read
+  v4i give[3][2], mine[3][2];
+  if (kq == 0) {
 #pragma unroll
     for (int i = 0; i < 3; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int jj = 0; jj < 2; ++jj) { give[i][jj] = acc[i][2 + jj]; mine[i][jj] = acc[i][jj]; }
+  } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) dst[((i * 4 + j) * 4 + q) * 64] = acc[i][j][q];
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) { give[i][jj] = acc[i][jj]; mine[i][jj] = acc[i][2 + jj]; }
   }
+  v4i* ex = reinterpret_cast<v4i*>(lds);  // [rg][receiver kq][i][jj][lane]
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) ex[(((rg * 2 + (1 - kq)) * 3 + i) * 2 + jj) * 64 + lane] = give[i][jj];
   __syncthreads();
-  if (kq != 0) return;
 #pragma unroll
-  for (int p = 1; p < KSPLIT; ++p) {
-    const int* src = red + ((p - 1) * 4 + rg) * (kKsPartialBytes / 4) + lane;
+  for (int i = 0; i < 3; ++i)
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[i][j][q] += src[((i * 4 + j) * 4 + q) * 64];
-  }
+    for (int jj = 0; jj < 2; ++jj) mine[i][jj] += ex[(((rg * 2 + kq) * 3 + i) * 2 + jj) * 64 + lane];
 
-  // Epilogue: lane holds W rows n_wave + 16i + 4g + {0..3} for token m0 + 16j + r.
+  // Epilogue: lane holds W rows n_wave + 16i + 4g + {0..3} (two gate/up pairs)
+  // for token m0 + 16*(2kq + jj) + r.
+  if constexpr (VEC_OUT) {
+    __syncthreads();  // exchange area free
+    float* ot = reinterpret_cast<float*>(lds);  // [64 tokens][96 outputs]
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + 16 * j + r;
-    if (m >= batch) continue;
-    const float xsm = xs[m];
+    for (int jj = 0; jj < 2; ++jj) {
+      const int t = 16 * (2 * kq + jj) + r;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const int n = n_wave + 16 * i + 4 * g;
-      const float4 sc = *reinterpret_cast<const float4*>(scales + n);
-      float2 o;
-      {
-        const float gg = ((float)acc[i][j][0] * xsm) * sc.x;
-        const float uu = ((float)acc[i][j][1] * xsm) * sc.y;
-        o.x = (gg / (1.0f + expf(-gg))) * uu;
+      for (int i = 0; i < 3; ++i) {
+        float2 o;
+        o.x = swiglu_w8a8(mine[i][jj][0], mine[i][jj][1], xsv[jj], sc[i].x, sc[i].y);
+        o.y = swiglu_w8a8(mine[i][jj][2], mine[i][jj][3], xsv[jj], sc[i].z, sc[i].w);
+        *reinterpret_cast<float2*>(ot + t * 96 + rg * 24 + 8 * i + 2 * g) = o;
       }
-      {
-        const float gg = ((float)acc[i][j][2] * xsm) * sc.z;
-        const float uu = ((float)acc[i][j][3] * xsm) * sc.w;
-        o.y = (gg / (1.0f + expf(-gg))) * uu;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < kPkBM * 24 / (64 * kPkWaves); ++t) {
+      const int q = t * 64 * kPkWaves + threadIdx.x;
+      const int row = q / 24, c4 = q - row * 24;
+      const int m = m0 + row;
+      if (m < batch)
+        __builtin_nontemporal_store(*reinterpret_cast<const v4f*>(ot + row * 96 + 4 * c4),
+                                    reinterpret_cast<v4f*>(out + (size_t)m * inter + tile_n * 96 + 4 * c4));
+    }
+  } else {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int m = m0 + 16 * (2 * kq + jj) + r;
+      if (m >= batch) continue;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int n = n_wave + 16 * i + 4 * g;
+        float2 o;
+        o.x = swiglu_w8a8(mine[i][jj][0], mine[i][jj][1], xsv[jj], sc[i].x, sc[i].y);
+        o.y = swiglu_w8a8(mine[i][jj][2], mine[i][jj][3], xsv[jj], sc[i].z, sc[i].w);
+        *reinterpret_cast<float2*>(out + (size_t)m * inter + (n >> 1)) = o;
       }
-      *reinterpret_cast<float2*>(out + (size_t)m * inter + (n >> 1)) = o;
     }
   }
 }
 
-inline bool gemm_ksplit_shape(size_t K, size_t inter) {
-  return (K == 1024 || K == 2048) && (2 * inter) % kKsBN == 0;
+inline bool packed_gemm_shape(size_t K, size_t inter) {
+  return (K == 1024 || K == 2048) && (2 * inter) % kPkBN == 0;
 }
 
-template <int KS, int KSPLIT>
-bool ksplit_kernel_ready() {
+template <int KS, bool VEC_OUT>
+bool packed_kernel_ready() {
   static const bool ok = [] {
     int dev = 0, max_lds = 0;
     if (hipGetDevice(&dev) != hipSuccess) return false;
     if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
       return false;
-    if ((size_t)max_lds < (size_t)kKsBM * (kLdsMaxK + kLdsRowPad)) return false;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_w8a8_swiglu_ksplit_kernel<KS, KSPLIT>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, max_lds) == hipSuccess;
+    if ((size_t)max_lds < kPkLds) return false;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_w8a8_swiglu_packed_kernel<KS, VEC_OUT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPkLds) == hipSuccess;
   }();
   return ok;
 }
 
-template <int KS, int KSPLIT>
-bool launch_ksplit(float* out, const int8_t* wpk, const float* scales, const int8_t* xq,
-                   const float* xs, int batch, int inter, int n_tiles, int m_tiles,
-                   hipStream_t st) {
-  if (!ksplit_kernel_ready<KS, KSPLIT>()) return false;
-  size_t lds = (size_t)kKsBM * (KS * kPackK + kLdsRowPad);
-  const size_t red = (size_t)(KSPLIT - 1) * 4 * kKsPartialBytes;
-  if (lds < red) lds = red;
-  gemm_w8a8_swiglu_ksplit_kernel<KS, KSPLIT><<<(unsigned)(n_tiles * m_tiles), 64 * 4 * KSPLIT, lds, st>>>(
+template <int KS, bool VEC_OUT>
+bool launch_packed(float* out, const int8_t* wpk, const float* scales, const int8_t* xq,
+                   const float* xs, int batch, int inter, int n_tiles, int m_tiles, hipStream_t st) {
+  if (!packed_kernel_ready<KS, VEC_OUT>()) return false;
+  gemm_w8a8_swiglu_packed_kernel<KS, VEC_OUT><<<(unsigned)(n_tiles * m_tiles), 64 * kPkWaves, kPkLds, st>>>(
       out, wpk, scales, xq, xs, batch, inter, n_tiles, m_tiles);
   return true;
 }
 
-constexpr int kDefaultKsplit = 1;
-
 // Launches the packed-weight kernel; returns false if the shape or the device
-// LDS does not allow it (nothing launched).
-template <int KSPLIT = kDefaultKsplit>
-bool try_packed_gemm(float* out, const int8_t* wpk, const float* scales, const int8_t* xq,
-                     const float* xs, size_t batch, size_t K, size_t inter, hipStream_t st) {
-  if (!gemm_ksplit_shape(K, inter)) return false;
-  const size_t n_tiles = 2 * inter / kKsBN, m_tiles = (batch + kKsBM - 1) / kKsBM;
+// LDS does not allow it (nothing launched). 16-byte aligned outputs take the
+// LDS-staged 16-byte store path.
+inline bool try_packed_gemm(float* out, const int8_t* wpk, const float* scales, const int8_t* xq,
+                            const float* xs, size_t batch, size_t K, size_t inter, hipStream_t st) {
+  if (!packed_gemm_shape(K, inter)) return false;
+  const size_t n_tiles = 2 * inter / kPkBN, m_tiles = (batch + kPkBM - 1) / kPkBM;
   if (n_tiles * m_tiles > 0x7fffffffu) return false;
-  if (K == 1024) {
-    return launch_ksplit<16, KSPLIT>(out, wpk, scales, xq, xs, (int)batch, (int)inter,
-                                     (int)n_tiles, (int)m_tiles, st);
-  }
-  return launch_ksplit<32, KSPLIT>(out, wpk, scales, xq, xs, (int)batch, (int)inter, (int)n_tiles,
-                                   (int)m_tiles, st);
+  const bool vec = aligned16(out);
+  const int B = (int)batch, I = (int)inter, NT = (int)n_tiles, MT = (int)m_tiles;
+  if (K == 1024)
+    return vec ? launch_packed<16, true>(out, wpk, scales, xq, xs, B, I, NT, MT, st)
+               : launch_packed<16, false>(out, wpk, scales, xq, xs, B, I, NT, MT, st);
+  return vec ? launch_packed<32, true>(out, wpk, scales, xq, xs, B, I, NT, MT, st)
+             : launch_packed<32, false>(out, wpk, scales, xq, xs, B, I, NT, MT, st);
 }
 
 }  // namespace qasr

@@ -162,12 +162,6 @@ __global__ __launch_bounds__(256) void interleave_kernel(int8_t* wgu, float* sgu
 // loads are issued before the first v_dot4, then the 2*NP int32 sums are
 // reduced across the wave and NP lanes finish the SwiGLU epilogue.
 // ---------------------------------------------------------------------------
-QASR_DEV float swiglu_w8a8(int dg, int du, float xs, float sg, float su) {
-  const float g = ((float)dg * xs) * sg;
-  const float u = ((float)du * xs) * su;
-  return (g / (1.0f + expf(-g))) * u;
-}
-
 QASR_DEV int dot16(v4i a, v4i b, int acc) {
   acc = __builtin_amdgcn_sdot4(a[0], b[0], acc, false);
   acc = __builtin_amdgcn_sdot4(a[1], b[1], acc, false);
@@ -470,16 +464,17 @@ extern "C" int qasr_gate_up_swiglu_w8a8_packed(float* out, const int8_t* w_packe
                "gate_up_swiglu_w8a8_packed: w, xq and scales must be 16-byte aligned");
   QASR_REQUIRE((reinterpret_cast<uintptr_t>(out) & 7u) == 0,
                "gate_up_swiglu_w8a8_packed: out must be 8-byte aligned");
+  QASR_REQUIRE(batch <= 0x7fffffffu - 63, "gate_up_swiglu_w8a8_packed: batch too large");
   QASR_REQUIRE(batch <= 0x7fffffffu && intermediate <= 0x3fffffffu,
                "gate_up_swiglu_w8a8_packed: size too large");
-  if (!gemm_ksplit_shape(in_dim, intermediate)) {
+  if (!packed_gemm_shape(in_dim, intermediate)) {
     return fail(QASR_ERR_UNSUPPORTED,
                 "gate_up_swiglu_w8a8_packed: needs in_dim 1024 or 2048 and 2*intermediate % 192 == 0");
   }
   if (!try_packed_gemm(out, w_packed, scales, xq, x_scales, batch, in_dim, intermediate,
                        as_stream(stream))) {
     return fail(QASR_ERR_UNSUPPORTED,
-                "gate_up_swiglu_w8a8_packed: the device cannot give a workgroup 130 KiB of LDS");
+                "gate_up_swiglu_w8a8_packed: the device cannot give a workgroup 128 KiB of LDS");
   }
   return launch_status("gate_up_swiglu_w8a8_packed");
 }
