@@ -366,14 +366,21 @@ __global__ __launch_bounds__(256) void pack_w8a8_tiles_kernel(int8_t* __restrict
 // issue v_mfma_i32_16x16x64_i8 back to back at full rate, two interleaved
 // waves can.
 //
-// Xq is staged in LDS by direct global->LDS loads in 32 KiB chunks of
-// [64 rows][512 bytes]; the 16-byte slot p of a row holds the row's logical
-// slot p ^ (row & 15), so the b128 fragment reads of 16 rows at one k offset
-// hit 16 distinct bank groups. The first chunk of each K half is waited for
-// before the loop, the second one when the loop reaches it. W streams from the
-// tile-packed layout straight into registers, PF k-steps ahead, with
-// non-temporal loads; the per-row and per-token scales of the epilogue are
-// loaded before the loop so their latency hides under it.
+// Xq is staged in LDS in 32 KiB chunks of [64 rows][512 bytes]; the 16-byte
+// slot p of a row holds the row's logical slot p ^ (row & 15), so the b128
+// fragment reads of 16 rows at one k offset hit 16 distinct bank groups. Each
+// wave loads its share of the first chunk of both K halves into registers and
+// writes it to LDS before the loop; the second chunks (K = 2048) arrive in
+// registers during the first k-steps and are written at step 3, read from
+// step 8. Plain loads are used rather than the direct global->LDS form: the
+// compiler cannot tell which LDS bytes a pending direct load writes, so it
+// drains every outstanding load (the whole W window) at the first LDS read;
+// with register staging its per-load waits stay exact. The workgroup barriers
+// of the staging are bare s_barrier after lgkmcnt(0), since __syncthreads()
+// would also wait for the outstanding W loads. W streams from the tile-packed
+// layout straight into registers, PF k-steps ahead, with non-temporal loads;
+// the per-row and per-token scales of the epilogue are loaded before the loop
+// so their latency hides under it.
 //
 // After the loop the two waves of a row group exchange halves through LDS:
 // wave kq keeps token tiles 2kq, 2kq+1, adds its partner's partial sums for
@@ -385,30 +392,34 @@ constexpr int kPkBN = 192;       // W rows per workgroup
 constexpr int kPkBM = 64;        // tokens per workgroup
 constexpr int kPkWaves = 8;      // 4 row groups x 2 K halves
 constexpr int kPkChunk = 512;    // bytes of K per staged X chunk
-constexpr int kPkPrefetch = 4;   // k-steps of W in flight per wave
+constexpr int kPkPrefetch = 3;   // k-steps of W in flight per wave
 constexpr size_t kPkLds = 131072;
 
-// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
-// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
-#define QASR_VMCNT(n) (((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left at their maxima (gfx9
+// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+constexpr int kWaitLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
 
-// X chunk c of the workgroup's 64 token rows: 32 DMA instructions of 1 KiB
-// (two rows each), 4 per wave. Rows past the batch re-read row batch - 1
-// (valid memory); their results are never stored.
+// Workgroup barrier without a memory fence: the caller has made its own LDS
+// writes complete (lgkmcnt(0)); outstanding global loads keep flying.
+QASR_DEV void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// Wave `wave`'s share of X chunk c: 4 rows-pairs t, each lane one 16-byte slot.
+// Rows past the batch re-read row batch - 1 (valid memory); their results are
+// never stored.
 template <int K>
-QASR_DEV void stage_x_chunk(int8_t* lds, const int8_t* __restrict__ xq, int c, int wave, int lane,
-                            int m0, int batch) {
-#pragma unroll
-  for (int t = 0; t < 32 / kPkWaves; ++t) {
-    const int d = wave * (32 / kPkWaves) + t;
-    const int row = 2 * d + (lane >> 5);
-    const int slot = (lane & 31) ^ (row & 15);
-    const int src_row = m0 + row < batch ? m0 + row : batch - 1;
-    const int8_t* src = xq + (size_t)src_row * K + kPkChunk * c + 16 * slot;
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)(lds + c * 32768 + d * 1024),
-                                     16, 0, 0);
-  }
+QASR_DEV const v4i* x_chunk_src(const int8_t* __restrict__ xq, int c, int t, int wave, int lane,
+                                int m0, int batch) {
+  const int d = wave * 4 + t;
+  const int row = 2 * d + (lane >> 5);
+  const int slot = (lane & 31) ^ (row & 15);
+  const int src_row = m0 + row < batch ? m0 + row : batch - 1;
+  return reinterpret_cast<const v4i*>(xq + (size_t)src_row * K + kPkChunk * c + 16 * slot);
+}
+QASR_DEV v4i* x_chunk_dst(int8_t* lds, int c, int t, int wave, int lane) {
+  return reinterpret_cast<v4i*>(lds + c * 32768 + (wave * 4 + t) * 1024 + 16 * lane);
 }
 
 template <int KS, bool VEC_OUT>  // KS = K / 64 (16 or 32)
@@ -420,9 +431,8 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
   constexpr int KW = KS / 2;                // k-steps per wave
   constexpr int NCH = K / kPkChunk;         // X chunks (2 or 4)
   constexpr int CH_HALF = NCH / 2;          // chunks per K half
-  constexpr int DMA_PER_CHUNK = 32 / kPkWaves;
   constexpr int PF = kPkPrefetch;
-  constexpr int EPI_LOADS = 3 + 2;          // scale float4s + token scales
+  static_assert(kPkWaves * 4 * 2 == 64, "a chunk is 64 rows: 8 waves x 4 row pairs");
   extern __shared__ __align__(16) int8_t lds[];
 
   const int lane = threadIdx.x & 63;
@@ -446,16 +456,16 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
   const int m0 = tile_m * kPkBM;
   const int k0 = kq * KW;
 
-  // X: the first chunk of each K half, then the rest.
-  stage_x_chunk<K>(lds, xq, 0, wave, lane, m0, batch);
-  stage_x_chunk<K>(lds, xq, CH_HALF, wave, lane, m0, batch);
+  // Issue order: first X chunks, W window, epilogue operands, second X
+  // chunks; sched_barriers keep it (loads complete in issue order).
+  v4i xa[8], xb[8];
 #pragma unroll
-  for (int c = 1; c < CH_HALF; ++c) {
-    stage_x_chunk<K>(lds, xq, c, wave, lane, m0, batch);
-    stage_x_chunk<K>(lds, xq, CH_HALF + c, wave, lane, m0, batch);
+  for (int t = 0; t < 4; ++t) {
+    xa[t] = *x_chunk_src<K>(xq, 0, t, wave, lane, m0, batch);
+    xa[4 + t] = *x_chunk_src<K>(xq, CH_HALF, t, wave, lane, m0, batch);
   }
+  __builtin_amdgcn_sched_barrier(0);
 
-  // W window, then the epilogue operands (newest loads).
   const int8_t* wp = wpk + packed_tile_offset(n_wave / kPackRows, k0, KS) + 16 * lane;
   constexpr size_t ROW_TILE = (size_t)KS * 1024;
   v4i wbuf[PF][3];
@@ -464,6 +474,7 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
 #pragma unroll
     for (int i = 0; i < 3; ++i)
       wbuf[d][i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + i * ROW_TILE + d * 1024));
+  __builtin_amdgcn_sched_barrier(0);
   float4 sc[3];
   float xsv[2];
 #pragma unroll
@@ -474,9 +485,20 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
     xsv[jj] = xs[m < batch ? m : batch - 1];
   }
   __builtin_amdgcn_sched_barrier(0);
-  // this wave's first-chunk DMAs are its oldest loads: allow everything newer
-  __builtin_amdgcn_s_waitcnt(QASR_VMCNT(2 * (CH_HALF - 1) * DMA_PER_CHUNK + 3 * PF + EPI_LOADS));
-  __syncthreads();
+  if constexpr (CH_HALF > 1) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      xb[t] = *x_chunk_src<K>(xq, 1, t, wave, lane, m0, batch);
+      xb[4 + t] = *x_chunk_src<K>(xq, CH_HALF + 1, t, wave, lane, m0, batch);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    *x_chunk_dst(lds, 0, t, wave, lane) = xa[t];
+    *x_chunk_dst(lds, CH_HALF, t, wave, lane) = xa[4 + t];
+  }
+  lds_barrier();
 
   v4i acc[3][4];
 #pragma unroll
@@ -500,11 +522,18 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
     for (int d = 0; d < PF; ++d) {
       const int s = s0 + d;
       if (s < KW) {
-        if (CH_HALF > 1 && s % 8 == 7 && s + 1 < KW) {
-          // step s+1 reads the next chunk: every DMA is older than the W window
+        if (CH_HALF > 1 && s == 3) {  // second chunks into LDS
           __builtin_amdgcn_sched_barrier(0);
-          __builtin_amdgcn_s_waitcnt(QASR_VMCNT(3 * PF));
-          __syncthreads();
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            *x_chunk_dst(lds, 1, t, wave, lane) = xb[t];
+            *x_chunk_dst(lds, CH_HALF + 1, t, wave, lane) = xb[4 + t];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (CH_HALF > 1 && s == 7) {  // step 8 reads them (B fragments are loaded one step ahead)
+          __builtin_amdgcn_sched_barrier(0);
+          lds_barrier();
           __builtin_amdgcn_sched_barrier(0);
         }
         v4i a[3];
