@@ -102,7 +102,8 @@ int qasr_apply_rope_neox_f32(float* x, const float* cos_vals,
  *   k[s,h,:] = rope(rms_norm_head(k[s,h,:], k_norm_w), positions[s])
  * cos_tab/sin_tab are RopeCache tables of table_rows rows of head_dim floats
  * (decoder.rs:253-289). positions == NULL means row s uses position s.
- * A position outside [0, table_rows) poisons that row's q and k with NaN.
+ * table_rows must be at least 1; a position outside [0, table_rows) poisons
+ * that row's q and k with NaN.
  * Replaces rms_norm_per_head x2 + apply_rope_neox x2 at decoder.rs:455-459,
  * 543-547, 799-803, 888-892 (kernels/mod.rs:920-935, 1247-1267). k may be NULL
  * when n_kv_heads == 0. */

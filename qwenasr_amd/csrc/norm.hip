@@ -24,12 +24,14 @@ __global__ __launch_bounds__(BLOCK) void rms_norm_vec_kernel(
   __shared__ float red[BLOCK / kWave];
   const int h4 = hidden >> 2;
   const size_t base = (size_t)blockIdx.x * (size_t)h4;
-  float4 v[NV];
+  float4 v[NV], wv[NV];
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = threadIdx.x + i * BLOCK;
     if (c < h4) {
+      // the gain is independent of the row statistics: load it with the row
+      wv[i] = ld4(w, c);
       float4 a = ld4(x, base + c);
       if constexpr (ADD) {
         const float4 d = ld4(delta, base + c);
@@ -50,12 +52,11 @@ __global__ __launch_bounds__(BLOCK) void rms_norm_vec_kernel(
   for (int i = 0; i < NV; ++i) {
     const int c = threadIdx.x + i * BLOCK;
     if (c < h4) {
-      const float4 wv = ld4(w, c);
       float4 o;
-      o.x = (v[i].x * rinv) * wv.x;
-      o.y = (v[i].y * rinv) * wv.y;
-      o.z = (v[i].z * rinv) * wv.z;
-      o.w = (v[i].w * rinv) * wv.w;
+      o.x = (v[i].x * rinv) * wv[i].x;
+      o.y = (v[i].y * rinv) * wv[i].y;
+      o.z = (v[i].z * rinv) * wv[i].z;
+      o.w = (v[i].w * rinv) * wv[i].w;
       if (out) st4(out, base + c, o);
       v[i] = o;
       if constexpr (QUANT) {
@@ -143,12 +144,14 @@ __global__ __launch_bounds__(BLOCK) void layer_norm_vec_kernel(
   const int h4 = hidden >> 2;
   const int fused_end = hidden & ~7;
   const size_t base = (size_t)blockIdx.x * (size_t)h4;
-  float4 v[NV];
+  float4 v[NV], wv[NV], bv[NV];
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = threadIdx.x + i * BLOCK;
     if (c < h4) {
+      wv[i] = ld4(w, c);  // gain and bias: independent of the statistics
+      bv[i] = ld4(b, c);
       v[i] = ld4(x, base + c);
       s += v[i].x;
       s += v[i].y;
@@ -176,14 +179,12 @@ __global__ __launch_bounds__(BLOCK) void layer_norm_vec_kernel(
   for (int i = 0; i < NV; ++i) {
     const int c = threadIdx.x + i * BLOCK;
     if (c < h4) {
-      const float4 wv = ld4(w, c);
-      const float4 bv = ld4(b, c);
       const bool f = 4 * c < fused_end;  // 4-blocks never straddle an 8-block edge
       float4 o;
-      o.x = ln_out(v[i].x, mean, inv, wv.x, bv.x, f);
-      o.y = ln_out(v[i].y, mean, inv, wv.y, bv.y, f);
-      o.z = ln_out(v[i].z, mean, inv, wv.z, bv.z, f);
-      o.w = ln_out(v[i].w, mean, inv, wv.w, bv.w, f);
+      o.x = ln_out(v[i].x, mean, inv, wv[i].x, bv[i].x, f);
+      o.y = ln_out(v[i].y, mean, inv, wv[i].y, bv[i].y, f);
+      o.z = ln_out(v[i].z, mean, inv, wv[i].z, bv[i].z, f);
+      o.w = ln_out(v[i].w, mean, inv, wv[i].w, bv[i].w, f);
       st4(out, base + c, o);
     }
   }
@@ -201,12 +202,14 @@ __global__ __launch_bounds__(256) void layer_norm_wave_kernel(
   const int h4 = hidden >> 2;
   const int fused_end = hidden & ~7;
   const size_t base = (size_t)row * (size_t)h4;
-  float4 v[NV];
+  float4 v[NV], wv[NV], bv[NV];
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * kWave;
     if (c < h4) {
+      wv[i] = ld4(w, c);  // gain and bias: independent of the statistics
+      bv[i] = ld4(b, c);
       v[i] = ld4(x, base + c);
       s += v[i].x;
       s += v[i].y;
@@ -234,14 +237,12 @@ __global__ __launch_bounds__(256) void layer_norm_wave_kernel(
   for (int i = 0; i < NV; ++i) {
     const int c = lane + i * kWave;
     if (c < h4) {
-      const float4 wv = ld4(w, c);
-      const float4 bv = ld4(b, c);
       const bool f = 4 * c < fused_end;
       float4 o;
-      o.x = ln_out(v[i].x, mean, inv, wv.x, bv.x, f);
-      o.y = ln_out(v[i].y, mean, inv, wv.y, bv.y, f);
-      o.z = ln_out(v[i].z, mean, inv, wv.z, bv.z, f);
-      o.w = ln_out(v[i].w, mean, inv, wv.w, bv.w, f);
+      o.x = ln_out(v[i].x, mean, inv, wv[i].x, bv[i].x, f);
+      o.y = ln_out(v[i].y, mean, inv, wv[i].y, bv[i].y, f);
+      o.z = ln_out(v[i].z, mean, inv, wv[i].z, bv[i].z, f);
+      o.w = ln_out(v[i].w, mean, inv, wv[i].w, bv[i].w, f);
       st4(out, base + c, o);
     }
   }

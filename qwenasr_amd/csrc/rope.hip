@@ -63,6 +63,25 @@ __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
   long long row;
   head_of(a, gh, HD, &base, &w, &row);
 
+  // Every load that does not depend on the head's statistics is issued here,
+  // so the row, gains and table rows are in flight together.
+  float4 w1, w2;
+  if constexpr (NORM) {
+    w1 = ld4(w, sub);
+    w2 = ld4(w + HALF, sub);
+  }
+  long long pos = 0;
+  bool pos_ok = true;
+  float4 c1, c2, s1, s2;
+  if constexpr (ROPE) {
+    pos = a.positions ? (long long)a.positions[row] : row;
+    pos_ok = pos >= 0 && pos < a.table_rows;
+    const long long pr = pos_ok ? pos : 0;  // out-of-table rows read row 0, then become NaN
+    const float* cr = a.cos_tab + pr * HD;
+    const float* sr = a.sin_tab + pr * HD;
+    c1 = ld4(cr, sub); c2 = ld4(cr + HALF, sub);
+    s1 = ld4(sr, sub); s2 = ld4(sr + HALF, sub);
+  }
   float4 x1 = ld4(base, sub);
   float4 x2 = ld4(base + HALF, sub);
   if constexpr (NORM) {
@@ -77,25 +96,18 @@ __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
     ss += x2.w * x2.w;
     ss = group_sum<L>(ss);
     const float rinv = 1.0f / sqrtf(ss / (float)HD + a.eps);
-    const float4 w1 = ld4(w, sub);
-    const float4 w2 = ld4(w + HALF, sub);
     x1.x = (x1.x * rinv) * w1.x; x1.y = (x1.y * rinv) * w1.y;
     x1.z = (x1.z * rinv) * w1.z; x1.w = (x1.w * rinv) * w1.w;
     x2.x = (x2.x * rinv) * w2.x; x2.y = (x2.y * rinv) * w2.y;
     x2.z = (x2.z * rinv) * w2.z; x2.w = (x2.w * rinv) * w2.w;
   }
   if constexpr (ROPE) {
-    const long long pos = a.positions ? (long long)a.positions[row] : row;
-    if (pos < 0 || pos >= a.table_rows) {
+    if (!pos_ok) {
       const float n = qnan();
       x1 = make_float4(n, n, n, n);
       x2 = x1;
     } else {
       // kernels/mod.rs:1262-1263: v[d] = x1*c[d] + (-x2)*s[d]; v[d+h] = x2*c[d+h] + x1*s[d+h]
-      const float* cr = a.cos_tab + pos * HD;
-      const float* sr = a.sin_tab + pos * HD;
-      const float4 c1 = ld4(cr, sub), c2 = ld4(cr + HALF, sub);
-      const float4 s1 = ld4(sr, sub), s2 = ld4(sr + HALF, sub);
       float4 o1, o2;
       o1.x = x1.x * c1.x + (-x2.x) * s1.x; o2.x = x2.x * c2.x + x1.x * s2.x;
       o1.y = x1.y * c1.y + (-x2.y) * s1.y; o2.y = x2.y * c2.y + x1.y * s2.y;
@@ -262,6 +274,7 @@ extern "C" int qasr_head_rms_norm_rope_f32(float* q, float* k, const float* q_no
                                            void* stream) {
   if (seq == 0 || head_dim == 0 || n_heads + n_kv_heads == 0) return QASR_OK;
   QASR_REQUIRE(cos_tab && sin_tab, "head_rms_norm_rope: null table");
+  QASR_REQUIRE(table_rows > 0, "head_rms_norm_rope: the RoPE table has no rows");
   QASR_REQUIRE(n_heads == 0 || (q && q_norm_w), "head_rms_norm_rope: null q");
   QASR_REQUIRE(n_kv_heads == 0 || (k && k_norm_w), "head_rms_norm_rope: null k");
   int rc = check_heads(seq, n_heads, n_kv_heads, head_dim, true);

@@ -114,6 +114,10 @@ def test_shape_contracts():
     # overflowing products
     big = (1 << 62)
     assert rc("qasr_rms_norm_f32", FAKE, FAKE, FAKE, big, big, 1e-6, NULL) == _lib.QASR_ERR_INVALID_ARG
+    # a RoPE table needs at least one row (out-of-table positions read row 0, then become NaN)
+    assert rc("qasr_head_rms_norm_rope_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 1, 16, 8, 128, 0,
+              1e-6, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert "no rows" in last_error()
     # vocab must be positive
     assert rc("qasr_embed_gather_f32", FAKE, FAKE, FAKE, 1, 16, 0, NULL) == _lib.QASR_ERR_INVALID_ARG
 
