@@ -114,6 +114,28 @@ int qasr_head_rms_norm_rope_f32(float* q, float* k, const float* q_norm_w,
                                 size_t head_dim, size_t table_rows, float eps,
                                 void* stream);
 
+/* qasr_head_rms_norm_rope_f32 with the KV-cache store fused in (the step
+ * after q/k norm + RoPE in every decoder layer):
+ *   q[s,h,:]  = rope(rms_norm_head(q[s,h,:], q_norm_w), p)        (in place)
+ *   k_cache[row, h, :] = rope(rms_norm_head(k[s,h,:], k_norm_w), p)
+ *   v_cache[row, h, :] = v[s,h,:]
+ * with p = start_pos + s and row = p when positions == NULL (one sequence:
+ * k_cache/v_cache point at the layer's [cache_rows][n_kv_heads*head_dim]
+ * block, KvCache::k_at/v_at of decoder.rs:194-202), or p = positions[s] and
+ * row = s * cache_rows + p otherwise (row s is its own decode stream with its
+ * own [cache_rows][kv_dim] block). k and v are read, not modified.
+ * A row whose p lies outside the RoPE table or the cache gets a NaN q row and
+ * no cache write. Replaces rms_norm_per_head x2 + apply_rope_neox x2 + the
+ * k_at/v_at copies at decoder.rs:455-462, 543-550, 799-810, 888-895.
+ * head_dim 64/128/256/512 and 16-byte aligned buffers (else UNSUPPORTED). */
+int qasr_head_rms_norm_rope_kv_f32(float* q, const float* k, const float* v,
+                                   const float* q_norm_w, const float* k_norm_w,
+                                   const float* cos_tab, const float* sin_tab,
+                                   const int32_t* positions, size_t start_pos, size_t seq,
+                                   size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                   size_t table_rows, float eps, float* k_cache,
+                                   float* v_cache, size_t cache_rows, void* stream);
+
 /* Fill RoPE table rows [pos_begin, pos_end) for theta and head_dim:
  *   inv_freq[d] = 1 / theta^((2d)/head_dim)   (f32 powf, computed on the host
  *   once per call exactly as RopeCache::ensure does, decoder.rs:262-266)

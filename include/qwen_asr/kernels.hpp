@@ -243,6 +243,76 @@ inline void head_rms_norm_rope(F q, F k, CF q_norm_w, CF k_norm_w, const RopeCac
                 "head_rms_norm_rope");
 }
 
+// Device KV cache with the reference's layout [n_layers][max_seq][kv_dim] and
+// growth rule (decoder.rs:129-228): grow() doubles max_seq until it covers the
+// request and keeps the first len rows of every layer.
+class KvCache {
+ public:
+  KvCache(size_t n_layers, size_t max_seq, size_t kv_dim)
+      : n_layers_(n_layers), max_seq_(max_seq), kv_dim_(kv_dim),
+        k_(n_layers * max_seq * kv_dim), v_(n_layers * max_seq * kv_dim) {
+    zero(k_);
+    zero(v_);
+  }
+  size_t len = 0;
+  size_t max_seq() const { return max_seq_; }
+  size_t kv_dim() const { return kv_dim_; }
+  void grow(size_t required) {
+    if (required <= max_seq_) return;
+    size_t new_max = max_seq_;
+    while (new_max < required) new_max *= 2;
+    DeviceBuffer<float> k(n_layers_ * new_max * kv_dim_), v(n_layers_ * new_max * kv_dim_);
+    zero(k);
+    zero(v);
+    const size_t bytes = len * kv_dim_ * sizeof(float);
+    for (size_t l = 0; l < n_layers_ && bytes; ++l) {
+      const size_t src = l * max_seq_ * kv_dim_, dst = l * new_max * kv_dim_;
+      if (hipMemcpyAsync(k.data() + dst, k_.data() + src, bytes, hipMemcpyDeviceToDevice, current_stream()) != hipSuccess ||
+          hipMemcpyAsync(v.data() + dst, v_.data() + src, bytes, hipMemcpyDeviceToDevice, current_stream()) != hipSuccess) {
+        throw std::runtime_error("KvCache::grow: device copy failed");
+      }
+    }
+    k_ = std::move(k);
+    v_ = std::move(v);
+    max_seq_ = new_max;
+  }
+  // The layer's whole [max_seq][kv_dim] block (the store target) and its
+  // first len rows (what attention reads: k_layer / v_layer).
+  F k_block(size_t layer) const { return F(k_.data(), k_.size()).sub(layer * max_seq_ * kv_dim_, max_seq_ * kv_dim_); }
+  F v_block(size_t layer) const { return F(v_.data(), v_.size()).sub(layer * max_seq_ * kv_dim_, max_seq_ * kv_dim_); }
+  F k_layer(size_t layer) const { return k_block(layer).sub(0, len * kv_dim_); }
+  F v_layer(size_t layer) const { return v_block(layer).sub(0, len * kv_dim_); }
+
+ private:
+  static void zero(DeviceBuffer<float>& b) {
+    if (b.size() && hipMemsetAsync(b.data(), 0, b.size() * sizeof(float), current_stream()) != hipSuccess)
+      throw std::runtime_error("KvCache: device memset failed");
+  }
+  size_t n_layers_, max_seq_, kv_dim_;
+  DeviceBuffer<float> k_, v_;
+};
+
+// q/k head RMSNorm + RoPE with the KV store fused in: rows start_pos.. of one
+// sequence go to the layer blocks k_cache/v_cache (k and v are read only).
+inline void head_rms_norm_rope_kv(F q, CF k, CF v, CF q_norm_w, CF k_norm_w, const RopeCache& rope,
+                                  size_t start_pos, size_t seq, size_t n_heads, size_t n_kv_heads,
+                                  size_t head_dim, float eps, F k_cache, F v_cache, size_t cache_rows) {
+  const size_t kv_dim = n_kv_heads * head_dim;
+  detail::need(q, seq * n_heads * head_dim, "q");
+  detail::need(k, seq * kv_dim, "k");
+  detail::need(v, seq * kv_dim, "v");
+  detail::need(q_norm_w, head_dim, "q_norm_w");
+  detail::need(k_norm_w, head_dim, "k_norm_w");
+  detail::need(k_cache, cache_rows * kv_dim, "k_cache");
+  detail::need(v_cache, cache_rows * kv_dim, "v_cache");
+  if (rope.head_dim() != head_dim) throw Panic("head_rms_norm_rope_kv: RopeCache head_dim mismatch");
+  detail::check(qasr_head_rms_norm_rope_kv_f32(q.ptr, k.ptr, v.ptr, q_norm_w.ptr, k_norm_w.ptr,
+                                               rope.cos().ptr, rope.sin().ptr, nullptr, start_pos,
+                                               seq, n_heads, n_kv_heads, head_dim, rope.cap(), eps,
+                                               k_cache.ptr, v_cache.ptr, cache_rows, detail::st()),
+                "head_rms_norm_rope_kv");
+}
+
 // ---- activations (kernels/mod.rs:941-994) ------------------------------------
 inline void silu(F x, size_t n) {
   detail::need(x, n, "x");

@@ -31,6 +31,17 @@ struct HeadArgs {
   int nk;
   long long table_rows;
   float eps;
+  // KV-cache epilogue (head_rms_norm_rope_kv): k and v rows are read from
+  // k_src/v and written to the cache at row (stream * cache_rows + pos), with
+  // pos = positions[s] and stream = s when positions are given, else
+  // pos = start_pos + s and stream = 0 (the reference's single sequence).
+  const float* k_src;
+  const float* v;
+  float* k_cache;
+  float* v_cache;
+  long long kv_heads_end;  // q_heads + seq * n_kv_heads
+  long long start_pos;
+  long long cache_rows;
 };
 
 // Resolves global head index gh to its base pointer, norm weight and row.
@@ -48,7 +59,48 @@ QASR_DEV void head_of(const HeadArgs& a, long long gh, int hd, float** base, con
   }
 }
 
-template <int HD, bool NORM, bool ROPE>
+// KV mode: head gh is a q head (in place), a k head (read k_src, write the
+// cache) or a v head (copied to the cache). Returns the kind (0 q, 1 k, 2 v).
+QASR_DEV int head_kv_of(const HeadArgs& a, long long gh, int hd, const float** src, float** dst,
+                        const float** w, long long* row, long long* pos, bool* ok) {
+  int kind;
+  long long h = 0;
+  if (gh < a.q_heads) {
+    kind = 0;
+    *row = gh / a.nq;
+  } else if (gh < a.kv_heads_end) {
+    kind = 1;
+    const long long g = gh - a.q_heads;
+    *row = g / a.nk;
+    h = g - *row * a.nk;
+  } else {
+    kind = 2;
+    const long long g = gh - a.kv_heads_end;
+    *row = g / a.nk;
+    h = g - *row * a.nk;
+  }
+  const long long p = a.positions ? (long long)a.positions[*row] : a.start_pos + *row;
+  *pos = p;
+  *ok = p >= 0 && p < a.table_rows && p < a.cache_rows;
+  const long long stream = a.positions ? *row : 0;
+  const long long cache_off = ((stream * a.cache_rows + (*ok ? p : 0)) * a.nk + h) * hd;
+  if (kind == 0) {
+    *src = a.q + gh * hd;
+    *dst = a.q + gh * hd;
+    *w = a.qw;
+  } else if (kind == 1) {
+    *src = a.k_src + (gh - a.q_heads) * hd;
+    *dst = a.k_cache + cache_off;
+    *w = a.kw;
+  } else {
+    *src = a.v + (gh - a.kv_heads_end) * hd;
+    *dst = a.v_cache + cache_off;
+    *w = nullptr;
+  }
+  return kind;
+}
+
+template <int HD, bool NORM, bool ROPE, bool KV = false>
 __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
   constexpr int L = HD / 8;
   constexpr int HPW = kWave / L;
@@ -58,10 +110,25 @@ __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
   const long long gh =
       ((long long)blockIdx.x * (256 / kWave) + threadIdx.x / kWave) * HPW + lane / L;
   if (gh >= a.total_heads) return;  // whole lane groups leave together
-  float* base;
+  float* base;        // where the result goes
+  const float* src;   // where the head is read
   const float* w;
   long long row;
-  head_of(a, gh, HD, &base, &w, &row);
+  long long pos = 0;
+  bool pos_ok = true;
+  if constexpr (KV) {
+    const int kind = head_kv_of(a, gh, HD, &src, &base, &w, &row, &pos, &pos_ok);
+    if (kind == 2) {  // v: a plain copy into the cache (decoder.rs:550, 895)
+      if (pos_ok) {
+        st4(base, sub, ld4(src, sub));
+        st4(base + HALF, sub, ld4(src + HALF, sub));
+      }
+      return;  // the head's lane group leaves together
+    }
+  } else {
+    head_of(a, gh, HD, &base, &w, &row);
+    src = base;
+  }
 
   // Every load that does not depend on the head's statistics is issued here,
   // so the row, gains and table rows are in flight together.
@@ -70,20 +137,20 @@ __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
     w1 = ld4(w, sub);
     w2 = ld4(w + HALF, sub);
   }
-  long long pos = 0;
-  bool pos_ok = true;
   float4 c1, c2, s1, s2;
   if constexpr (ROPE) {
-    pos = a.positions ? (long long)a.positions[row] : row;
-    pos_ok = pos >= 0 && pos < a.table_rows;
+    if constexpr (!KV) {
+      pos = a.positions ? (long long)a.positions[row] : row;
+      pos_ok = pos >= 0 && pos < a.table_rows;
+    }
     const long long pr = pos_ok ? pos : 0;  // out-of-table rows read row 0, then become NaN
     const float* cr = a.cos_tab + pr * HD;
     const float* sr = a.sin_tab + pr * HD;
     c1 = ld4(cr, sub); c2 = ld4(cr + HALF, sub);
     s1 = ld4(sr, sub); s2 = ld4(sr + HALF, sub);
   }
-  float4 x1 = ld4(base, sub);
-  float4 x2 = ld4(base + HALF, sub);
+  float4 x1 = ld4(src, sub);
+  float4 x2 = ld4(src + HALF, sub);
   if constexpr (NORM) {
     // kernels/mod.rs:927-932: rms_inv = 1/sqrt(sum(v^2)/head_dim + eps); v = v*rms_inv*w
     float ss = x1.x * x1.x;
@@ -117,6 +184,7 @@ __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
       x2 = o2;
     }
   }
+  if (KV && !pos_ok && base != src) return;  // k head outside the cache: nothing written
   st4(base, sub, x1);
   st4(base + HALF, sub, x2);
 }
@@ -294,6 +362,70 @@ extern "C" int qasr_head_rms_norm_rope_f32(float* q, float* k, const float* q_no
   a.table_rows = (long long)table_rows;
   a.eps = eps;
   return launch_heads<true, true>(a, (int)head_dim, as_stream(stream));
+}
+
+extern "C" int qasr_head_rms_norm_rope_kv_f32(float* q, const float* k, const float* v,
+                                              const float* q_norm_w, const float* k_norm_w,
+                                              const float* cos_tab, const float* sin_tab,
+                                              const int32_t* positions, size_t start_pos,
+                                              size_t seq, size_t n_heads, size_t n_kv_heads,
+                                              size_t head_dim, size_t table_rows, float eps,
+                                              float* k_cache, float* v_cache, size_t cache_rows,
+                                              void* stream) {
+  if (seq == 0 || n_heads + n_kv_heads == 0) return QASR_OK;
+  QASR_REQUIRE(cos_tab && sin_tab, "head_rms_norm_rope_kv: null table");
+  QASR_REQUIRE(n_heads == 0 || (q && q_norm_w), "head_rms_norm_rope_kv: null q");
+  QASR_REQUIRE(n_kv_heads == 0 || (k && v && k_norm_w && k_cache && v_cache),
+               "head_rms_norm_rope_kv: null k, v or cache");
+  QASR_REQUIRE(table_rows > 0 && cache_rows > 0, "head_rms_norm_rope_kv: empty table or cache");
+  QASR_REQUIRE(positions || (start_pos <= cache_rows && seq <= cache_rows - start_pos &&
+                             start_pos + seq <= table_rows),
+               "head_rms_norm_rope_kv: rows start_pos..start_pos+seq exceed the cache or the RoPE table");
+  int rc = check_heads(seq, n_heads, 2 * n_kv_heads, head_dim, true);
+  if (rc) return rc;
+  size_t cache_elems;
+  QASR_REQUIRE(mul_ok(cache_rows, n_kv_heads * head_dim, &cache_elems) &&
+                   (!positions || mul_ok(cache_elems, seq, &cache_elems)),
+               "head_rms_norm_rope_kv: cache size overflows");
+  const bool vec = (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512) &&
+                   aligned16(q) && aligned16(k) && aligned16(v) && aligned16(q_norm_w) &&
+                   aligned16(k_norm_w) && aligned16(cos_tab) && aligned16(sin_tab) &&
+                   aligned16(k_cache) && aligned16(v_cache);
+  if (!vec) {
+    return fail(QASR_ERR_UNSUPPORTED,
+                "head_rms_norm_rope_kv: needs head_dim 64/128/256/512 and 16-byte aligned buffers");
+  }
+  HeadArgs a{};
+  a.q = q;
+  a.qw = q_norm_w;
+  a.kw = k_norm_w;
+  a.cos_tab = cos_tab;
+  a.sin_tab = sin_tab;
+  a.positions = positions;
+  a.q_heads = (long long)(seq * n_heads);
+  a.kv_heads_end = a.q_heads + (long long)(seq * n_kv_heads);
+  a.total_heads = a.kv_heads_end + (long long)(seq * n_kv_heads);
+  a.nq = n_heads ? (int)n_heads : 1;
+  a.nk = n_kv_heads ? (int)n_kv_heads : 1;
+  a.table_rows = (long long)table_rows;
+  a.eps = eps;
+  a.k_src = k;
+  a.v = v;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.start_pos = (long long)start_pos;
+  a.cache_rows = (long long)cache_rows;
+  const int hd = (int)head_dim;
+  const long long heads_per_block = (kWave / (hd / 8)) * (256 / kWave);
+  const unsigned grid = (unsigned)((a.total_heads + heads_per_block - 1) / heads_per_block);
+  hipStream_t st = as_stream(stream);
+  switch (hd) {
+    case 64: head_vec_kernel<64, true, true, true><<<grid, 256, 0, st>>>(a); break;
+    case 128: head_vec_kernel<128, true, true, true><<<grid, 256, 0, st>>>(a); break;
+    case 256: head_vec_kernel<256, true, true, true><<<grid, 256, 0, st>>>(a); break;
+    default: head_vec_kernel<512, true, true, true><<<grid, 256, 0, st>>>(a); break;
+  }
+  return launch_status("head_rms_norm_rope_kv");
 }
 
 extern "C" int qasr_rope_table_fill_f32(float* cos_tab, float* sin_tab, size_t pos_begin,

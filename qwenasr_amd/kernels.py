@@ -157,6 +157,80 @@ def head_rms_norm_rope(q, k, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, se
               _ptr(positions), seq, n_heads, n_kv_heads, head_dim, rows, eps, _stream())
 
 
+def head_rms_norm_rope_kv(q, k, v, q_norm_w, k_norm_w, rope: "RopeCache", positions, start_pos: int,
+                          seq: int, n_heads: int, n_kv_heads: int, head_dim: int, eps: float,
+                          k_cache, v_cache, cache_rows: int) -> None:
+    """q/k head RMSNorm + RoPE with the KV-cache store fused in
+    (decoder.rs:888-895: norm, rope, then ``k_at``/``v_at`` copies).
+
+    Without ``positions`` row s is position ``start_pos + s`` of one sequence
+    and ``k_cache``/``v_cache`` are that layer's ``[cache_rows, kv_dim]`` block
+    (``KvCache.k_layer_block``). With ``positions`` (int32, ``seq`` entries) row s
+    is its own decode stream and the caches are ``[seq, cache_rows, kv_dim]``.
+    k and v are read only; q is rotated in place.
+    """
+    kv_dim = n_kv_heads * head_dim
+    if n_heads:
+        _need(q, F32, seq * n_heads * head_dim, "q")
+        _need(q_norm_w, F32, head_dim, "q_norm_w")
+    if n_kv_heads:
+        _need(k, F32, seq * kv_dim, "k")
+        _need(v, F32, seq * kv_dim, "v")
+        _need(k_norm_w, F32, head_dim, "k_norm_w")
+        streams = seq if positions is not None else 1
+        _need(k_cache, F32, streams * cache_rows * kv_dim, "k_cache")
+        _need(v_cache, F32, streams * cache_rows * kv_dim, "v_cache")
+    if positions is not None:
+        _need(positions, I32, seq, "positions")
+    if rope.head_dim != head_dim:
+        raise ValueError("RopeCache head_dim does not match")
+    _lib.call("qasr_head_rms_norm_rope_kv_f32", _ptr(q if n_heads else None), _ptr(k), _ptr(v),
+              _ptr(q_norm_w if n_heads else None), _ptr(k_norm_w), _ptr(rope.cos), _ptr(rope.sin),
+              _ptr(positions), start_pos, seq, n_heads, n_kv_heads, head_dim, rope.cap, eps,
+              _ptr(k_cache), _ptr(v_cache), cache_rows, _stream())
+
+
+class KvCache:
+    """Device KV cache with the reference's layout and growth rule
+    (decoder.rs:129-228): ``k``/``v`` are ``[n_layers, max_seq, kv_dim]`` fp32,
+    ``grow`` doubles ``max_seq`` until it covers the request and copies the first
+    ``len`` rows of every layer."""
+
+    def __init__(self, n_layers: int, max_seq: int, kv_dim: int, device="cuda"):
+        self.n_layers, self.max_seq, self.kv_dim, self.len = n_layers, max_seq, kv_dim, 0
+        self.k = torch.zeros(n_layers * max_seq * kv_dim, dtype=F32, device=device)
+        self.v = torch.zeros_like(self.k)
+
+    def grow(self, required: int) -> None:
+        if required <= self.max_seq:
+            return
+        new_max = self.max_seq
+        while new_max < required:
+            new_max *= 2
+        k = torch.zeros(self.n_layers * new_max * self.kv_dim, dtype=F32, device=self.k.device)
+        v = torch.zeros_like(k)
+        n = self.len * self.kv_dim
+        for layer in range(self.n_layers):
+            src, dst = layer * self.max_seq * self.kv_dim, layer * new_max * self.kv_dim
+            k[dst:dst + n].copy_(self.k[src:src + n])
+            v[dst:dst + n].copy_(self.v[src:src + n])
+        self.k, self.v, self.max_seq = k, v, new_max
+
+    def k_layer_block(self, layer: int) -> torch.Tensor:
+        off = layer * self.max_seq * self.kv_dim
+        return self.k[off:off + self.max_seq * self.kv_dim]
+
+    def v_layer_block(self, layer: int) -> torch.Tensor:
+        off = layer * self.max_seq * self.kv_dim
+        return self.v[off:off + self.max_seq * self.kv_dim]
+
+    def k_layer(self, layer: int) -> torch.Tensor:
+        return self.k_layer_block(layer)[: self.len * self.kv_dim]
+
+    def v_layer(self, layer: int) -> torch.Tensor:
+        return self.v_layer_block(layer)[: self.len * self.kv_dim]
+
+
 class RopeCache:
     """Device RoPE table with the reference's growth rule (decoder.rs:234-306).
 

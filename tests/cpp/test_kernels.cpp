@@ -159,6 +159,46 @@ static void test_rope_cache() {
   EXPECT(std::fabs(row2[0] - std::cos(700.0f)) < 1e-6f, "cos(700) column 0");
 }
 
+// Decoder layer step with the KV store fused in: the cache rows equal the k/v
+// rows the separate norm + rope + copy produce, the rest of the cache stays 0,
+// and growing the cache keeps them.
+static void test_kv_store() {
+  const size_t seq = 3, nq = 2, nk = 1, hd = 128, start = 4, kv = nk * hd;
+  K::KvCache cache(2, 8, kv);
+  K::RopeCache rope;
+  rope.ensure(start + seq, hd, 1e6f);
+  std::vector<float> q(seq * nq * hd), k(seq * kv), v(seq * kv), w(hd, 1.0f);
+  for (size_t i = 0; i < q.size(); ++i) q[i] = std::sin(0.1f * (float)i);
+  for (size_t i = 0; i < k.size(); ++i) { k[i] = std::cos(0.07f * (float)i); v[i] = (float)i; }
+  auto dq = upload(q), dk = upload(k), dv = upload(v), dw = upload(w);
+  K::head_rms_norm_rope_kv(dq, dk, dv, dw, dw, rope, start, seq, nq, nk, hd, 1e-6f,
+                           cache.k_block(1), cache.v_block(1), cache.max_seq());
+  // reference path: per-head norm, rope on rows start.., copy
+  auto dk2 = upload(k);
+  K::rms_norm_per_head(dk2, dw, seq, nk, hd, 1e-6f);
+  K::apply_rope_neox(dk2, rope.cos_range(start, seq), rope.sin_range(start, seq), seq, nk, hd);
+  auto kref = download(dk2);
+  std::vector<float> kc(8 * kv), vc(8 * kv);
+  if (hipDeviceSynchronize() != hipSuccess ||
+      hipMemcpy(kc.data(), cache.k_block(1).ptr, kc.size() * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+      hipMemcpy(vc.data(), cache.v_block(1).ptr, vc.size() * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    throw std::runtime_error("copy back failed");
+  for (size_t s = 0; s < 8; ++s)
+    for (size_t d = 0; d < kv; ++d) {
+      const bool row = s >= start && s < start + seq;
+      const float ke = row ? kref[(s - start) * kv + d] : 0.0f, ve = row ? v[(s - start) * kv + d] : 0.0f;
+      EXPECT(kc[s * kv + d] == ke && vc[s * kv + d] == ve, "cache row %zu col %zu", s, d);
+    }
+  cache.len = start + seq;
+  cache.grow(20);
+  EXPECT(cache.max_seq() == 32, "grown to 32, got %zu", cache.max_seq());
+  std::vector<float> kc2(cache.len * kv);
+  if (hipDeviceSynchronize() != hipSuccess ||
+      hipMemcpy(kc2.data(), cache.k_layer(1).ptr, kc2.size() * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    throw std::runtime_error("copy back failed");
+  for (size_t i = 0; i < kc2.size(); ++i) EXPECT(kc2[i] == kc[i], "grow kept element %zu", i);
+}
+
 // linear_nobias_int8 with integer inputs and unit scales is exact.
 static void test_linear_int8_exact() {
   const size_t in = 2048, out_dim = 64;
@@ -222,6 +262,7 @@ int main() {
   run("test_silu", test_silu);
   run("test_vec_ops", test_vec_ops);
   run("test_rope_cache", test_rope_cache);
+  run("test_kv_store", test_kv_store);
   run("test_linear_int8_exact", test_linear_int8_exact);
   run("test_short_slice_panics", test_short_slice_panics);
   run("test_status_errors", test_status_errors);

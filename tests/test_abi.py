@@ -118,6 +118,10 @@ def test_shape_contracts():
     assert rc("qasr_head_rms_norm_rope_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 1, 16, 8, 128, 0,
               1e-6, NULL) == _lib.QASR_ERR_INVALID_ARG
     assert "no rows" in last_error()
+    # KV store: rows start_pos..start_pos+seq must fit the cache
+    assert rc("qasr_head_rms_norm_rope_kv_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 60, 8,
+              16, 8, 128, 2048, 1e-6, FAKE, FAKE, 64, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert "exceed" in last_error()
     # vocab must be positive
     assert rc("qasr_embed_gather_f32", FAKE, FAKE, FAKE, 1, 16, 0, NULL) == _lib.QASR_ERR_INVALID_ARG
 

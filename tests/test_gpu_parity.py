@@ -232,6 +232,112 @@ def test_head_rope_out_of_table_position_is_nan_row(dev):
     assert np.isfinite(qh[[0, 2]]).all() and np.isfinite(kh[[0, 2]]).all()
 
 
+def kv_reference(q, k, v, qw, kw, cos, sin, pos, seq, nq, nk, hd, eps):
+    """The reference's layer step (decoder.rs:543-550 / 888-895): per-head
+    RMSNorm of q and k, NeoX RoPE with the table rows of each row's position,
+    then the k/v rows copied into the cache. Returns q and the k/v rows."""
+    qn = oracle.rms_norm_per_head(q, qw, seq, nq, hd, eps)
+    kn = oracle.rms_norm_per_head(k, kw, seq, nk, hd, eps)
+    c = cos.reshape(-1, hd)[pos].ravel()
+    s = sin.reshape(-1, hd)[pos].ravel()
+    qr = oracle.apply_rope_neox(qn, c, s, seq, nq, hd)
+    kr = oracle.apply_rope_neox(kn, c, s, seq, nk, hd)
+    return qr, kr.reshape(seq, nk * hd), v.reshape(seq, nk * hd)
+
+
+@pytest.mark.parametrize("seq,start,nq,nk,hd,cache_rows", [
+    (7, 5, 16, 8, 128, 64),       # decode-ish: rows appended after 5 cached
+    (512, 0, 16, 8, 128, 1024),   # 0.6B prefill into a fresh layer block
+    (3, 61, 14, 2, 64, 64),       # last rows of the cache, head_dim 64
+])
+def test_head_rms_norm_rope_kv_single_sequence(dev, seq, start, nq, nk, hd, cache_rows):
+    from qwenasr_amd import kernels as K
+
+    r = rng(8, seq, start, hd)
+    q, k, v = normal(r, seq * nq * hd), normal(r, seq * nk * hd), normal(r, seq * nk * hd)
+    qw, kw = normal(r, hd, 0.1, 1.0), normal(r, hd, 0.1, 1.0)
+    rope = K.RopeCache(dev)
+    rope.ensure(start + seq, hd, 1e6)
+    cos, sin = oracle.rope_table(rope.cap, hd, 1e6)
+    kv_dim = nk * hd
+    kc = torch.full((cache_rows * kv_dim,), 7.0, device=dev)
+    vc = torch.full((cache_rows * kv_dim,), 7.0, device=dev)
+    qt = dev_t(q, dev)
+    kt, vt = dev_t(k, dev), dev_t(v, dev)
+    K.head_rms_norm_rope_kv(qt, kt, vt, dev_t(qw, dev), dev_t(kw, dev), rope, None, start, seq,
+                            nq, nk, hd, 1e-6, kc, vc, cache_rows)
+    pos = np.arange(start, start + seq)
+    q_ref, k_rows, v_rows = kv_reference(q, k, v, qw, kw, cos, sin, pos, seq, nq, nk, hd, 1e-6)
+    assert_close(host(qt), q_ref, RTOL, ATOL, "q")
+    kh, vh = host(kc).reshape(cache_rows, kv_dim), host(vc).reshape(cache_rows, kv_dim)
+    assert_close(kh[start:start + seq], k_rows, RTOL, ATOL, "k cache rows")
+    np.testing.assert_array_equal(vh[start:start + seq], v_rows)       # v is a copy
+    others = np.r_[0:start, start + seq:cache_rows]
+    assert (kh[others] == 7.0).all() and (vh[others] == 7.0).all()     # nothing else written
+    np.testing.assert_array_equal(host(kt), k)                          # k, v are read only
+    # same arithmetic as the fused norm+rope entry point, bit for bit
+    q2, k2 = dev_t(q, dev), dev_t(k, dev)
+    pos_t = dev_t(pos.astype(np.int32), dev)
+    K.head_rms_norm_rope(q2, k2, dev_t(qw, dev), dev_t(kw, dev), rope.cos, rope.sin, pos_t, seq,
+                         nq, nk, hd, 1e-6)
+    np.testing.assert_array_equal(host(qt), host(q2))
+    np.testing.assert_array_equal(kh[start:start + seq], host(k2).reshape(seq, kv_dim))
+
+
+def test_head_rms_norm_rope_kv_per_stream(dev):
+    """Batched decode: row s is stream s at its own position, each stream with
+    its own [cache_rows, kv_dim] block; a position past the cache leaves that
+    stream's cache untouched and its q row NaN."""
+    from qwenasr_amd import kernels as K
+
+    B, nq, nk, hd, cache_rows = 6, 16, 8, 128, 48
+    r = rng(9)
+    q, k, v = normal(r, B * nq * hd), normal(r, B * nk * hd), normal(r, B * nk * hd)
+    qw, kw = normal(r, hd, 0.1, 1.0), normal(r, hd, 0.1, 1.0)
+    pos = r.integers(0, cache_rows, B).astype(np.int32)
+    pos[4] = cache_rows  # past the end of stream 4's cache
+    rope = K.RopeCache(dev)
+    rope.ensure(cache_rows + 1, hd, 1e6)
+    cos, sin = oracle.rope_table(rope.cap, hd, 1e6)
+    kv_dim = nk * hd
+    kc = torch.full((B * cache_rows * kv_dim,), -3.0, device=dev)
+    vc = torch.full((B * cache_rows * kv_dim,), -3.0, device=dev)
+    qt = dev_t(q, dev)
+    K.head_rms_norm_rope_kv(qt, dev_t(k, dev), dev_t(v, dev), dev_t(qw, dev), dev_t(kw, dev), rope,
+                            dev_t(pos, dev), 0, B, nq, nk, hd, 1e-6, kc, vc, cache_rows)
+    ok = pos < cache_rows
+    q_ref, k_rows, v_rows = kv_reference(q, k, v, qw, kw, cos, sin, np.minimum(pos, cache_rows - 1),
+                                         B, nq, nk, hd, 1e-6)
+    qh = host(qt).reshape(B, nq * hd)
+    assert_close(qh[ok], q_ref.reshape(B, -1)[ok], RTOL, ATOL, "q")
+    assert np.isnan(qh[~ok]).all()
+    kh = host(kc).reshape(B, cache_rows, kv_dim)
+    vh = host(vc).reshape(B, cache_rows, kv_dim)
+    for b in range(B):
+        written = np.zeros(cache_rows, bool)
+        if ok[b]:
+            written[pos[b]] = True
+            assert_close(kh[b, pos[b]], k_rows[b], RTOL, ATOL, f"k stream {b}")
+            np.testing.assert_array_equal(vh[b, pos[b]], v_rows[b])
+        assert (kh[b][~written] == -3.0).all() and (vh[b][~written] == -3.0).all()
+
+
+def test_kv_cache_grow_keeps_rows(dev):
+    """KvCache.grow doubles max_seq and keeps each layer's first len rows
+    (decoder.rs:151-176)."""
+    from qwenasr_amd import kernels as K
+
+    cache = K.KvCache(3, 4, 16, dev)
+    cache.k.copy_(torch.arange(cache.k.numel(), dtype=torch.float32, device=dev))
+    before = [host(cache.k_layer_block(l))[:2 * 16].copy() for l in range(3)]
+    cache.len = 2
+    cache.grow(9)
+    assert cache.max_seq == 16
+    for l in range(3):
+        np.testing.assert_array_equal(host(cache.k_layer(l)), before[l])
+        assert (host(cache.k_layer_block(l))[2 * 16:] == 0).all()
+
+
 @pytest.mark.parametrize("seq,nh,hd", [(512, 16, 128), (3, 5, 64), (2, 3, 30)])
 def test_rms_norm_per_head_and_apply_rope(dev, seq, nh, hd):
     from qwenasr_amd import kernels as K
