@@ -285,6 +285,25 @@ int qasr_gate_up_swiglu_w8a8_f32in(float* out, const int8_t* w,
                                    size_t in_dim, size_t intermediate,
                                    void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* lm_head (decoder.rs:929-963)                                              */
+/* ------------------------------------------------------------------------ */
+
+/* idx[r] = index of the largest x[r, :] as the reference's greedy loop finds
+ * it (decoder.rs:941-949: start at element 0, replace on a strict `>`): the
+ * first maximum wins, NaN never wins, and a NaN in element 0 gives 0. */
+int qasr_argmax_rows_f32(int32_t* idx, const float* x, size_t rows, size_t cols,
+                         void* stream);
+
+/* INT8 lm_head + argmax for `rows` hidden states: logits[r, :] =
+ * linear_nobias_int8(x[r, :]) (qasr_linear_nobias_int8_f32 arithmetic, the
+ * reference's kernels::linear_nobias_int8 call at decoder.rs:939 and 954),
+ * then idx[r] = qasr_argmax_rows_f32(logits[r, :]). logits is caller-owned
+ * [rows, vocab] and keeps the logits. */
+int qasr_lm_head_int8_argmax_f32(int32_t* idx, float* logits, const float* x,
+                                 const int8_t* w, const float* scales, size_t rows,
+                                 size_t in_dim, size_t vocab, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -270,3 +270,12 @@ def gate_up_swiglu_w8a8(w, scales, xq, x_scales, batch, in_dim, inter):
                                   _p(_f32(scales)), _p(np.ascontiguousarray(xq, np.int8)),
                                   _p(_f32(x_scales)), batch, in_dim, inter)
     return out, dots
+
+
+def argmax_rows(x, rows, cols) -> np.ndarray:
+    """The lm_head argmax loop of decoder.rs:941-949 per row (first maximum
+    wins; a NaN never wins unless it is element 0)."""
+    x = _f32(x)
+    idx = np.empty(rows, np.int32)
+    lib().ref_argmax_rows(idx.ctypes.data_as(ctypes.c_void_p), _p(x), rows, cols)
+    return idx

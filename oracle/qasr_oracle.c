@@ -564,3 +564,24 @@ ORACLE_API void ref_gate_up_swiglu_w8a8(float* out, int32_t* dots, const int8_t*
     }
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* lm_head argmax, decoder.rs:941-949 (and 955-962):                         */
+/*   best = 0; best_val = logits[0];                                         */
+/*   for i in 1..n { if logits[i] > best_val { best_val = logits[i]; best = i } } */
+/* applied to each of `rows` rows.                                           */
+/* ------------------------------------------------------------------------ */
+ORACLE_API void ref_argmax_rows(int32_t* idx, const float* x, size_t rows, size_t cols) {
+  for (size_t r = 0; r < rows; ++r) {
+    const float* row = x + r * cols;
+    size_t best = 0;
+    float best_val = row[0];
+    for (size_t i = 1; i < cols; ++i) {
+      if (row[i] > best_val) {
+        best_val = row[i];
+        best = i;
+      }
+    }
+    idx[r] = (int32_t)best;
+  }
+}

@@ -10,8 +10,6 @@
 namespace qasr {
 namespace {
 
-QASR_DEV float4 ld4(const float* p, size_t i) { return reinterpret_cast<const float4*>(p)[i]; }
-QASR_DEV void st4(float* p, size_t i, float4 v) { reinterpret_cast<float4*>(p)[i] = v; }
 
 // ---------------------------------------------------------------------------
 // SwiGLU on the interleaved gate/up buffer, x86_64 reference arithmetic

@@ -98,6 +98,9 @@ QASR_DEV float block_max(float v, float* lds) {
 // ---------------------------------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+QASR_DEV float4 ld4(const float* p, size_t i) { return reinterpret_cast<const float4*>(p)[i]; }
+QASR_DEV void st4(float* p, size_t i, float4 v) { reinterpret_cast<float4*>(p)[i] = v; }
+
 QASR_DEV float4 ld4_nt(const float* p, size_t i) {
   const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p) + i);
   return make_float4(v[0], v[1], v[2], v[3]);

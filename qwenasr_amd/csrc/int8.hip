@@ -12,7 +12,6 @@
 namespace qasr {
 namespace {
 
-QASR_DEV float4 ld4(const float* p, size_t i) { return reinterpret_cast<const float4*>(p)[i]; }
 
 // ---------------------------------------------------------------------------
 // Per-row quantizer, quantize.rs:633-662.

@@ -190,6 +190,24 @@ def head_rms_norm_rope_kv(q, k, v, q_norm_w, k_norm_w, rope: "RopeCache", positi
               _ptr(k_cache), _ptr(v_cache), cache_rows, _stream())
 
 
+def argmax_rows(idx, x, rows: int, cols: int) -> None:
+    """Per-row argmax with the lm_head loop's semantics (decoder.rs:941-949)."""
+    _need(idx, I32, rows, "idx")
+    _need(x, F32, rows * cols, "x")
+    _lib.call("qasr_argmax_rows_f32", _ptr(idx), _ptr(x), rows, cols, _stream())
+
+
+def lm_head_int8_argmax(idx, logits, x, w: QuantWeight, rows: int, in_dim: int, vocab: int) -> None:
+    """INT8 lm_head logits + greedy argmax (decoder.rs:935-963)."""
+    _need(idx, I32, rows, "idx")
+    _need(logits, F32, rows * vocab, "logits")
+    _need(x, F32, rows * in_dim, "x")
+    _need(w.data, I8, vocab * in_dim, "w")
+    _need(w.scales, F32, vocab, "scales")
+    _lib.call("qasr_lm_head_int8_argmax_f32", _ptr(idx), _ptr(logits), _ptr(x), _ptr(w.data),
+              _ptr(w.scales), rows, in_dim, vocab, _stream())
+
+
 class KvCache:
     """Device KV cache with the reference's layout and growth rule
     (decoder.rs:129-228): ``k``/``v`` are ``[n_layers, max_seq, kv_dim]`` fp32,

@@ -744,3 +744,62 @@ def test_w8a8_packed_int32_dots_bit_exact(dev):
     dots = xq.astype(np.float64) @ w.astype(np.float64).T
     exp = (dots[:, 0::2].astype(np.float32) * dots[:, 1::2].astype(np.float32)).ravel()
     np.testing.assert_array_equal(host(out), exp)
+
+
+# ---------------------------------------------------------------------------
+# lm_head: INT8 logits + greedy argmax (decoder.rs:929-963)
+# ---------------------------------------------------------------------------
+def test_argmax_rows_matches_the_reference_loop(dev):
+    """Index work: bit-exact against the sequential loop, including ties (first
+    wins), NaN anywhere (never wins), NaN at element 0 (result 0), rows of -inf,
+    all-NaN rows and +inf ties; vectorised and scalar paths."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(40)
+    for cols in (151936, 1003, 4, 1):
+        rows = 12
+        x = normal(r, rows * cols).reshape(rows, cols)
+        x[1, :] = 2.5                                  # all equal: index 0
+        if cols > 3:
+            x[2, cols // 2] = x[2, cols - 1] = 9.0      # tie: first wins
+            x[3, 0] = np.nan                            # NaN at 0: index 0
+            x[4, ::7] = np.nan                          # scattered NaN
+            x[4, cols - 2] = 50.0
+            x[6, 1:3] = np.inf                          # +inf tie
+        x[5, :] = -np.inf                               # all -inf: index 0
+        x[7, :] = np.nan                                # all NaN: index 0
+        ref = oracle.argmax_rows(x.ravel(), rows, cols)
+        idx = torch.empty(rows, dtype=torch.int32, device=dev)
+        K.argmax_rows(idx, dev_t(x.ravel(), dev), rows, cols)
+        np.testing.assert_array_equal(host(idx), ref)
+        # misaligned start (scalar path)
+        xs = np.concatenate([[0.0], x.ravel()]).astype(np.float32)
+        xt = dev_t(xs, dev)[1:]
+        K.argmax_rows(idx, xt, rows, cols)
+        np.testing.assert_array_equal(host(idx), ref)
+
+
+@pytest.mark.parametrize("rows,in_dim,vocab", [(1, 1024, 151936), (3, 2048, 5000)])
+def test_lm_head_int8_argmax(dev, rows, in_dim, vocab):
+    """Logits within the W8A32 tolerance of the oracle; the token index equals
+    the reference loop's on the oracle logits whenever the top two logits are
+    further apart than twice the tolerance (checked), and always equals the
+    argmax of the returned logits."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(41, rows, vocab)
+    wq, ws = make_qweight(r, vocab, in_dim)
+    x = normal(r, rows * in_dim)
+    ref_logits = oracle.linear_nobias_int8(x, wq, ws, rows, in_dim, vocab, n_threads=8)
+    ref_idx = oracle.argmax_rows(ref_logits, rows, vocab)
+    idx = torch.empty(rows, dtype=torch.int32, device=dev)
+    logits = torch.empty(rows * vocab, device=dev)
+    w = K.QuantWeight(dev_t(wq, dev), dev_t(ws, dev), vocab, in_dim)
+    K.lm_head_int8_argmax(idx, logits, dev_t(x, dev), w, rows, in_dim, vocab)
+    lg = host(logits)
+    assert_close(lg, ref_logits, RTOL, ATOL, "logits")
+    np.testing.assert_array_equal(host(idx), oracle.argmax_rows(lg, rows, vocab))
+    top2 = np.sort(ref_logits.reshape(rows, vocab), axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 2 * (ATOL + RTOL * np.abs(top2[:, 1]))
+    assert clear.any()
+    np.testing.assert_array_equal(host(idx)[clear], ref_idx[clear])
