@@ -286,6 +286,24 @@ int qasr_gate_up_swiglu_w8a8_f32in(float* out, const int8_t* w,
                                    void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Attention (kernels/mod.rs:1124-1207)                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Causal grouped-query attention: for query row i (global position
+ * q_offset + i) and head h, keys j < min(q_offset + i + 1, seq_k) of kv head
+ * h / (n_heads / n_kv_heads):
+ *   out[i,h,:] = sum_j softmax_j(q[i,h,:] . k[j,kvh,:] * scale) * v[j,kvh,:]
+ * q, out: [seq_q, n_heads*head_dim]; k, v: [seq_k, n_kv_heads*head_dim]
+ * (a KvCache layer block, KvCache::k_layer_full of decoder.rs:212-222).
+ * A row with no keys gets zeros. Replaces kernels::causal_attention
+ * (kernels/mod.rs:1124-1207; calls decoder.rs:472-476, 561-564, 818-821,
+ * 900-903). head_dim 64 or 128, n_heads / n_kv_heads in {1, 2, 4, 8},
+ * 16-byte aligned buffers (else UNSUPPORTED). */
+int qasr_causal_attention_f32(float* out, const float* q, const float* k, const float* v,
+                              size_t seq_q, size_t seq_k, size_t n_heads, size_t n_kv_heads,
+                              size_t head_dim, float scale, size_t q_offset, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* lm_head (decoder.rs:929-963)                                              */
 /* ------------------------------------------------------------------------ */
 

@@ -47,6 +47,8 @@ _SIGS = {
     "ref_linear_int8": [_P, _P, _P, _P, _P, _Z, _Z, _Z, _I],
     "ref_interleave_gate_up": [_P, _P, _P, _P, _P, _P, _Z, _Z],
     "ref_gate_up_swiglu_w8a8": [_P, _P, _P, _P, _P, _P, _Z, _Z, _Z],
+    "ref_argmax_rows": [_P, _P, _Z, _Z],
+    "ref_causal_attention": [_P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _F, _Z],
 }
 
 _LIB = None
@@ -277,5 +279,13 @@ def argmax_rows(x, rows, cols) -> np.ndarray:
     wins; a NaN never wins unless it is element 0)."""
     x = _f32(x)
     idx = np.empty(rows, np.int32)
-    lib().ref_argmax_rows(idx.ctypes.data_as(ctypes.c_void_p), _p(x), rows, cols)
+    lib().ref_argmax_rows(_p(idx), _p(x), rows, cols)
     return idx
+
+
+def causal_attention(q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset):
+    """kernels/mod.rs:1124-1168 with the x86_64 vector helpers."""
+    out = np.empty(seq_q * n_heads * head_dim, np.float32)
+    lib().ref_causal_attention(_p(out), _p(_f32(q)), _p(_f32(k)), _p(_f32(v)), seq_q, seq_k,
+                               n_heads, n_kv_heads, head_dim, scale, q_offset)
+    return out

@@ -585,3 +585,89 @@ ORACLE_API void ref_argmax_rows(int32_t* idx, const float* x, size_t rows, size_
     idx[r] = (int32_t)best;
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* causal attention, kernels/mod.rs:1124-1168 (causal_attention_heads) with  */
+/* the x86_64 helpers: dot_f32 avx.rs:247-295 (four 8-lane FMA accumulators  */
+/* over 32-strides, an 8-stride tail into acc0, hsum of (acc0+acc1)+(acc2+acc3),*/
+/* scalar tail), vec_scale_add avx.rs:351-372 (dst = fma(dst, c, src)),      */
+/* vec_axpy_inplace avx.rs:326-349 (dst = fma(src, a, dst)),                 */
+/* vec_scale_inplace avx.rs:301-324 (dst *= s). Scalar tails as written.     */
+/* ------------------------------------------------------------------------ */
+static float dot_f32_avx(const float* a, const float* b, size_t n) {
+  float acc[4][8] = {{0}};
+  size_t i = 0;
+  while (i + 32 <= n) {
+    for (int r = 0; r < 4; ++r)
+      for (int l = 0; l < 8; ++l) acc[r][l] = fmaf(a[i + 8 * r + l], b[i + 8 * r + l], acc[r][l]);
+    i += 32;
+  }
+  while (i + 8 <= n) {
+    for (int l = 0; l < 8; ++l) acc[0][l] = fmaf(a[i + l], b[i + l], acc[0][l]);
+    i += 8;
+  }
+  float s01[8], s23[8], t[8];
+  for (int l = 0; l < 8; ++l) {
+    s01[l] = acc[0][l] + acc[1][l];
+    s23[l] = acc[2][l] + acc[3][l];
+    t[l] = s01[l] + s23[l];
+  }
+  float sum = hsum8(t);
+  while (i < n) {
+    sum += a[i] * b[i];
+    ++i;
+  }
+  return sum;
+}
+
+static void vec_scale_add_avx(float* dst, const float* src, float c, size_t n) {
+  size_t i = 0;
+  for (; i + 8 <= n; i += 8)
+    for (int l = 0; l < 8; ++l) dst[i + l] = fmaf(dst[i + l], c, src[i + l]);
+  for (; i < n; ++i) dst[i] = dst[i] * c + src[i];
+}
+
+static void vec_axpy_avx(float* dst, const float* src, float a, size_t n) {
+  size_t i = 0;
+  for (; i + 8 <= n; i += 8)
+    for (int l = 0; l < 8; ++l) dst[i + l] = fmaf(src[i + l], a, dst[i + l]);
+  for (; i < n; ++i) dst[i] += a * src[i];
+}
+
+ORACLE_API void ref_causal_attention(float* out, const float* q, const float* k, const float* v,
+                                     size_t seq_q, size_t seq_k, size_t n_heads,
+                                     size_t n_kv_heads, size_t head_dim, float scale,
+                                     size_t q_offset) {
+  const size_t heads_per_kv = n_heads / n_kv_heads;
+  const size_t q_hidden = n_heads * head_dim, kv_hidden = n_kv_heads * head_dim;
+  for (size_t h = 0; h < n_heads; ++h) {
+    const size_t kv_h = h / heads_per_kv;
+    for (size_t i = 0; i < seq_q; ++i) {
+      const float* q_row = q + i * q_hidden + h * head_dim;
+      float* o_row = out + i * q_hidden + h * head_dim;
+      const size_t global_pos = q_offset + i;
+      const size_t k_end = global_pos + 1 < seq_k ? global_pos + 1 : seq_k;
+      float max_score = -1e30f, sum_exp = 0.0f;
+      for (size_t d = 0; d < head_dim; ++d) o_row[d] = 0.0f;
+      for (size_t j = 0; j < k_end; ++j) {
+        const float* k_row = k + j * kv_hidden + kv_h * head_dim;
+        const float* v_row = v + j * kv_hidden + kv_h * head_dim;
+        const float score = dot_f32_avx(q_row, k_row, head_dim) * scale;
+        if (score > max_score) {
+          const float correction = expf(max_score - score);
+          sum_exp = sum_exp * correction + 1.0f;
+          vec_scale_add_avx(o_row, v_row, correction, head_dim);
+          max_score = score;
+        } else {
+          const float wt = expf(score - max_score);
+          sum_exp += wt;
+          vec_axpy_avx(o_row, v_row, wt, head_dim);
+        }
+      }
+      if (sum_exp > 0.0f) {
+        const float inv_sum = 1.0f / sum_exp;
+        for (size_t d = 0; d < head_dim; ++d) o_row[d] *= inv_sum;
+      }
+    }
+  }
+}

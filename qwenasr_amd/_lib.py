@@ -48,6 +48,7 @@ SIGNATURES: dict[str, list] = {
     "qasr_apply_rope_neox_f32": [P, P, P, Z, Z, Z, P],
     "qasr_head_rms_norm_rope_f32": [P, P, P, P, P, P, P, Z, Z, Z, Z, Z, F, P],
     "qasr_argmax_rows_f32": [P, P, Z, Z, P],
+    "qasr_causal_attention_f32": [P, P, P, P, Z, Z, Z, Z, Z, F, Z, P],
     "qasr_lm_head_int8_argmax_f32": [P, P, P, P, P, Z, Z, Z, P],
     "qasr_head_rms_norm_rope_kv_f32": [P, P, P, P, P, P, P, P, Z, Z, Z, Z, Z, Z, F, P, P, Z, P],
     "qasr_rope_table_fill_f32": [P, P, Z, Z, Z, F, P],

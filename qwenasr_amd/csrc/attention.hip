@@ -1,0 +1,226 @@
+// Causal grouped-query attention over a key/value block, the decoder's
+// attention step (kernels/mod.rs:1124-1207):
+//   for query row i (global position q_offset + i) and head h, with
+//   kv head h / (n_heads / n_kv_heads) and keys j < min(q_offset + i + 1, seq_k):
+//   out[i, h, :] = sum_j softmax_j(q[i,h,:] . k[j,kvh,:] * scale) v[j,kvh,:]
+// q, out: [seq_q, n_heads * head_dim]; k, v: [seq_k, n_kv_heads * head_dim]
+// (a KvCache layer block).
+//
+// The reference runs one online softmax per (row, head) over the keys in
+// order, starting from a running max of -1e30, and scales by 1/sum at the
+// end (no scaling when the sum is 0). Here keys are processed in tiles of 64:
+//   - QK: lane l owns key 64t + l and dots it with the q rows of all heads of
+//     the kv group (q broadcast from LDS), one 16-byte k load at a time;
+//   - the tile's max and sum come from wave reductions, and the running
+//     (max, sum, out) of each head is rescaled once per tile;
+//   - PV: lanes own head dimensions; the tile's keys are walked in order, each
+//     v row read with one coalesced wave load and its probability broadcast
+//     with readlane.
+// A workgroup holds R query rows of one kv head, S waves per row splitting the
+// key tiles; the S partial (max, sum, out) triples of a row are merged in LDS.
+// Prefill uses R = 4, S = 1 (the 4 rows' waves share k/v lines in L1); decode
+// uses R = 1, S = 8.
+#include "common.hpp"
+
+namespace qasr {
+namespace {
+
+QASR_DEV float bcast_lane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+template <int HD, int G, int R, int S>
+__global__ __launch_bounds__(64 * R * S) void causal_attention_kernel(
+    float* __restrict__ out, const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, int seq_q, int seq_k, int nk, float scale, int q_offset) {
+  constexpr int DPL = HD / 64;  // head dims per lane in the PV product
+  constexpr int NW = R * S;
+  __shared__ __align__(16) float qs[R][G][HD];
+  __shared__ float cm[NW][G];
+  __shared__ float cl[NW][G];
+  __shared__ __align__(16) float co[S > 1 ? NW : 1][G][HD];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rr = wave / S, sp = wave % S;
+  const int kh = blockIdx.y;
+  const int i = blockIdx.x * R + rr;
+  const bool row_ok = i < seq_q;
+  const int k_end = row_ok ? min(q_offset + i + 1, seq_k) : 0;
+  const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
+
+  if (sp == 0 && row_ok) {
+    const float* qr = q + (size_t)i * q_stride + (size_t)kh * G * HD;
+    for (int t = lane; t < G * HD; t += 64) qs[rr][t / HD][t % HD] = qr[t];
+  }
+  __syncthreads();
+
+  float m[G], l[G], o[G][DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -1e30f;  // the reference's initial running max
+    l[g] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o[g][d] = 0.0f;
+  }
+
+  const int ntiles = (k_end + 63) / 64;
+  for (int t = sp; t < ntiles; t += S) {
+    const int j = t * 64 + lane;
+    const bool kv = j < k_end;
+    // QK: this lane's key against every head of the group
+    float s[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) s[g] = 0.0f;
+    const float* kr = k + (size_t)(kv ? j : 0) * kv_stride + (size_t)kh * HD;
+#pragma unroll 8
+    for (int c = 0; c < HD / 4; ++c) {
+      const float4 kk = ld4(kr, c);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float4 qq = *reinterpret_cast<const float4*>(&qs[rr][g][4 * c]);
+        s[g] = __builtin_fmaf(qq.x, kk.x, s[g]);
+        s[g] = __builtin_fmaf(qq.y, kk.y, s[g]);
+        s[g] = __builtin_fmaf(qq.z, kk.z, s[g]);
+        s[g] = __builtin_fmaf(qq.w, kk.w, s[g]);
+      }
+    }
+    // online softmax update, one rescale per tile
+    float p[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float sc = kv ? s[g] * scale : -__builtin_inff();
+      const float mn = fmaxf(m[g], wave_max(sc));
+      const float corr = expf(m[g] - mn);
+      p[g] = kv ? expf(sc - mn) : 0.0f;
+      l[g] = l[g] * corr + wave_sum(p[g]);
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) o[g][d] *= corr;
+      m[g] = mn;
+    }
+    // PV: keys of the tile in order, lanes over head dims
+    const int nkeys = min(64, k_end - t * 64);
+    const float* vr = v + (size_t)(t * 64) * kv_stride + (size_t)kh * HD + lane * DPL;
+    for (int jj = 0; jj < nkeys; ++jj) {
+      float vv[DPL];
+      if constexpr (DPL == 2) {
+        const float2 t2 = *reinterpret_cast<const float2*>(vr + (size_t)jj * kv_stride);
+        vv[0] = t2.x;
+        vv[1] = t2.y;
+      } else {
+        vv[0] = vr[(size_t)jj * kv_stride];
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pj = bcast_lane(p[g], jj);
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o[g][d] = __builtin_fmaf(pj, vv[d], o[g][d]);
+      }
+    }
+  }
+
+  // merge the S key splits of a row
+  if constexpr (S > 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        cm[wave][g] = m[g];
+        cl[wave][g] = l[g];
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) co[wave][g][lane * DPL + d] = o[g][d];
+    __syncthreads();
+    if (sp == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float mx = cm[rr * S][g];
+        for (int w = 1; w < S; ++w) mx = fmaxf(mx, cm[rr * S + w][g]);
+        float lsum = 0.0f, acc[DPL];
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) acc[d] = 0.0f;
+        for (int w = 0; w < S; ++w) {
+          const float f = expf(cm[rr * S + w][g] - mx);
+          lsum = __builtin_fmaf(cl[rr * S + w][g], f, lsum);
+#pragma unroll
+          for (int d = 0; d < DPL; ++d) acc[d] = __builtin_fmaf(co[rr * S + w][g][lane * DPL + d], f, acc[d]);
+        }
+        l[g] = lsum;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o[g][d] = acc[d];
+      }
+    }
+  }
+  if (sp == 0 && row_ok) {
+    float* orow = out + (size_t)i * q_stride + (size_t)kh * G * HD;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float inv = l[g] > 0.0f ? 1.0f / l[g] : 1.0f;  // no scaling when the sum is 0
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) orow[g * HD + lane * DPL + d] = o[g][d] * inv;
+    }
+  }
+}
+
+template <int HD, int G>
+void launch_attention(float* out, const float* q, const float* k, const float* v, int seq_q,
+                      int seq_k, int nk, float scale, int q_offset, hipStream_t st) {
+  // enough (row, kv head) pairs to fill the chip: 4 rows per workgroup, one
+  // wave each; otherwise 8 waves split every row's keys
+  if ((long long)seq_q * nk >= 1024) {
+    const dim3 grid((unsigned)((seq_q + 3) / 4), (unsigned)nk);
+    causal_attention_kernel<HD, G, 4, 1><<<grid, 256, 0, st>>>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset);
+  } else {
+    const dim3 grid((unsigned)seq_q, (unsigned)nk);
+    causal_attention_kernel<HD, G, 1, 8><<<grid, 512, 0, st>>>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset);
+  }
+}
+
+template <int HD>
+bool dispatch_group(int G, float* out, const float* q, const float* k, const float* v, int seq_q,
+                    int seq_k, int nk, float scale, int q_offset, hipStream_t st) {
+  switch (G) {
+    case 1: launch_attention<HD, 1>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, st); return true;
+    case 2: launch_attention<HD, 2>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, st); return true;
+    case 4: launch_attention<HD, 4>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, st); return true;
+    case 8: launch_attention<HD, 8>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, st); return true;
+    default: return false;
+  }
+}
+
+}  // namespace
+}  // namespace qasr
+
+using namespace qasr;
+
+extern "C" int qasr_causal_attention_f32(float* out, const float* q, const float* k, const float* v,
+                                         size_t seq_q, size_t seq_k, size_t n_heads,
+                                         size_t n_kv_heads, size_t head_dim, float scale,
+                                         size_t q_offset, void* stream) {
+  if (seq_q == 0 || n_heads == 0) return QASR_OK;
+  QASR_REQUIRE(out && q, "causal_attention: null pointer");
+  QASR_REQUIRE(seq_k == 0 || (k && v), "causal_attention: null k or v");
+  QASR_REQUIRE(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+               "causal_attention: n_heads must be a multiple of n_kv_heads");
+  QASR_REQUIRE(seq_q < 0x40000000u && seq_k < 0x40000000u && q_offset < 0x40000000u &&
+                   n_heads <= 65536,
+               "causal_attention: size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(seq_q, n_heads * head_dim, &n) && mul_ok(seq_k, n_kv_heads * head_dim, &n),
+               "causal_attention: size overflows");
+  const size_t G = n_heads / n_kv_heads;
+  const bool ok_shape = (head_dim == 64 || head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8);
+  if (!ok_shape || !aligned16(q) || !aligned16(out) || (seq_k && (!aligned16(k) || !aligned16(v)))) {
+    return fail(QASR_ERR_UNSUPPORTED,
+                "causal_attention: needs head_dim 64 or 128, n_heads/n_kv_heads in {1,2,4,8} "
+                "and 16-byte aligned buffers");
+  }
+  hipStream_t st = as_stream(stream);
+  const int sq = (int)seq_q, sk = (int)seq_k, nk = (int)n_kv_heads, qo = (int)q_offset;
+  if (head_dim == 64)
+    dispatch_group<64>((int)G, out, q, k, v, sq, sk, nk, scale, qo, st);
+  else
+    dispatch_group<128>((int)G, out, q, k, v, sq, sk, nk, scale, qo, st);
+  return launch_status("causal_attention");
+}

@@ -190,6 +190,19 @@ def head_rms_norm_rope_kv(q, k, v, q_norm_w, k_norm_w, rope: "RopeCache", positi
               _ptr(k_cache), _ptr(v_cache), cache_rows, _stream())
 
 
+def causal_attention(out, q, k, v, seq_q: int, seq_k: int, n_heads: int, n_kv_heads: int,
+                     head_dim: int, scale: float, q_offset: int) -> None:
+    """Causal GQA attention over a KV block (kernels/mod.rs:1124-1207)."""
+    _need(out, F32, seq_q * n_heads * head_dim, "out")
+    _need(q, F32, seq_q * n_heads * head_dim, "q")
+    if seq_k:
+        _need(k, F32, seq_k * n_kv_heads * head_dim, "k")
+        _need(v, F32, seq_k * n_kv_heads * head_dim, "v")
+    _lib.call("qasr_causal_attention_f32", _ptr(out), _ptr(q), _ptr(k if seq_k else None),
+              _ptr(v if seq_k else None), seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale,
+              q_offset, _stream())
+
+
 def argmax_rows(idx, x, rows: int, cols: int) -> None:
     """Per-row argmax with the lm_head loop's semantics (decoder.rs:941-949)."""
     _need(idx, I32, rows, "idx")

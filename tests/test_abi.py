@@ -122,6 +122,11 @@ def test_shape_contracts():
     assert rc("qasr_head_rms_norm_rope_kv_f32", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 60, 8,
               16, 8, 128, 2048, 1e-6, FAKE, FAKE, 64, NULL) == _lib.QASR_ERR_INVALID_ARG
     assert "exceed" in last_error()
+    # attention: head groups must divide; unsupported head_dim
+    assert rc("qasr_causal_attention_f32", FAKE, FAKE, FAKE, FAKE, 1, 4, 6, 4, 128, 0.1, 3,
+              NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert rc("qasr_causal_attention_f32", FAKE, FAKE, FAKE, FAKE, 1, 4, 16, 8, 96, 0.1, 3,
+              NULL) == _lib.QASR_ERR_UNSUPPORTED
     # vocab must be positive
     assert rc("qasr_embed_gather_f32", FAKE, FAKE, FAKE, 1, 16, 0, NULL) == _lib.QASR_ERR_INVALID_ARG
 

@@ -803,3 +803,56 @@ def test_lm_head_int8_argmax(dev, rows, in_dim, vocab):
     clear = (top2[:, 1] - top2[:, 0]) > 2 * (ATOL + RTOL * np.abs(top2[:, 1]))
     assert clear.any()
     np.testing.assert_array_equal(host(idx)[clear], ref_idx[clear])
+
+
+# ---------------------------------------------------------------------------
+# Causal GQA attention over a KV block (kernels/mod.rs:1124-1207)
+# ---------------------------------------------------------------------------
+ATTN_CASES = [
+    ("decode_pos0", 1, 1, 16, 8, 128, 0),           # first token: a single key
+    ("decode_pos300", 1, 301, 16, 8, 128, 300),     # 1.7B/0.6B decode step
+    ("decode_pos2047", 1, 2048, 16, 8, 128, 2047),
+    ("prefill_512", 512, 512, 16, 8, 128, 0),       # 0.6B prefill, causal triangle
+    ("chunked_prefill", 37, 137, 16, 8, 128, 100),  # 37 new rows after 100 cached
+    ("keys_before_limit", 6, 3, 4, 4, 64, 10),      # seq_k below the causal limit, head_dim 64
+    ("gqa4_hd64", 9, 70, 8, 2, 64, 61),
+    ("mha_g1", 3, 65, 4, 4, 128, 62),
+    ("gqa8", 2, 129, 8, 1, 128, 127),
+    ("no_keys", 2, 0, 16, 8, 128, 0),
+]
+
+
+@pytest.mark.parametrize("name,seq_q,seq_k,nq,nk,hd,q_offset", ATTN_CASES)
+def test_causal_attention(dev, name, seq_q, seq_k, nq, nk, hd, q_offset):
+    from qwenasr_amd import kernels as K
+
+    r = rng(50, seq_q, seq_k, nq, hd)
+    q = normal(r, seq_q * nq * hd)
+    k = normal(r, max(seq_k, 1) * nk * hd)
+    v = normal(r, max(seq_k, 1) * nk * hd)
+    scale = hd ** -0.5
+    ref = oracle.causal_attention(q, k, v, seq_q, seq_k, nq, nk, hd, scale, q_offset)
+    out = torch.full((seq_q * nq * hd,), 5.0, device=dev)
+    K.causal_attention(out, dev_t(q, dev), dev_t(k, dev), dev_t(v, dev), seq_q, seq_k, nq, nk, hd,
+                       scale, q_offset)
+    assert_close(host(out), ref, RTOL, ATOL, name)
+
+
+def test_causal_attention_reads_a_cache_block(dev):
+    """k/v are the first seq_k rows of a larger KvCache layer block (the
+    reference passes k_layer_full): rows past seq_k are never read."""
+    from qwenasr_amd import kernels as K
+
+    nq, nk, hd, max_seq, seq_k = 16, 8, 128, 64, 20
+    r = rng(51)
+    q = normal(r, nq * hd)
+    kc = normal(r, max_seq * nk * hd)
+    vc = normal(r, max_seq * nk * hd)
+    kc[seq_k * nk * hd:] = np.nan
+    vc[seq_k * nk * hd:] = np.nan
+    ref = oracle.causal_attention(q, kc[: seq_k * nk * hd], vc[: seq_k * nk * hd], 1, seq_k, nq, nk,
+                                  hd, hd ** -0.5, seq_k - 1)
+    out = torch.empty(nq * hd, device=dev)
+    K.causal_attention(out, dev_t(q, dev), dev_t(kc, dev), dev_t(vc, dev), 1, seq_k, nq, nk, hd,
+                       hd ** -0.5, seq_k - 1)
+    assert_close(host(out), ref, RTOL, ATOL, "cache block")

@@ -270,3 +270,64 @@ def test_interleave_layout():
     np.testing.assert_array_equal(wgu[1::2], wu)
     np.testing.assert_array_equal(sgu[0::2], sg)
     np.testing.assert_array_equal(sgu[1::2], su)
+
+
+# --- causal attention (kernels/mod.rs:1124-1168) ---------------------------
+def attention_f64(q, k, v, seq_q, seq_k, nq, nk, hd, scale, q_offset):
+    """float64 softmax(q k^T * scale) v over keys 0..min(q_offset+i+1, seq_k)."""
+    Q = q.reshape(seq_q, nq, hd).astype(np.float64)
+    K = k[:seq_k * nk * hd].reshape(seq_k, nk, hd).astype(np.float64)
+    V = v[:seq_k * nk * hd].reshape(seq_k, nk, hd).astype(np.float64)
+    out = np.zeros((seq_q, nq, hd))
+    for i in range(seq_q):
+        ke = min(q_offset + i + 1, seq_k)
+        for h in range(nq):
+            if ke == 0:
+                continue
+            s = K[:ke, h // (nq // nk)] @ Q[i, h] * scale
+            p = np.exp(s - s.max())
+            out[i, h] = (p / p.sum()) @ V[:ke, h // (nq // nk)]
+    return out.ravel()
+
+
+@pytest.mark.parametrize("seq_q,seq_k,nq,nk,hd,q_offset", [
+    (1, 300, 16, 8, 128, 299),    # decode step at position 299
+    (7, 7, 4, 2, 128, 0),         # prefill, causal triangle
+    (5, 12, 14, 2, 64, 7),        # chunked prefill after 7 cached rows, head_dim 64
+    (3, 2, 2, 2, 36, 5),          # keys end before the causal limit; head_dim tail
+    (2, 0, 2, 1, 128, 0),         # no keys: zero output
+])
+def test_causal_attention_closed_form(seq_q, seq_k, nq, nk, hd, q_offset):
+    r = np.random.default_rng(seq_q * 1000 + seq_k)
+    q = r.standard_normal(seq_q * nq * hd).astype(np.float32)
+    k = r.standard_normal(max(seq_k, 1) * nk * hd).astype(np.float32)
+    v = r.standard_normal(max(seq_k, 1) * nk * hd).astype(np.float32)
+    o = oracle.causal_attention(q, k, v, seq_q, seq_k, nq, nk, hd, hd ** -0.5, q_offset)
+    ref = attention_f64(q, k, v, seq_q, seq_k, nq, nk, hd, hd ** -0.5, q_offset)
+    assert_close(o, ref, 2e-6, 1e-6, "attention")
+
+
+def test_causal_attention_single_key_is_v_and_gqa_sharing():
+    # one key: softmax weight 1, output = that v row exactly (x * (1/1))
+    hd = 128
+    r = np.random.default_rng(3)
+    q = r.standard_normal(4 * hd).astype(np.float32)
+    k = r.standard_normal(2 * hd).astype(np.float32)
+    v = r.standard_normal(2 * hd).astype(np.float32)
+    o = oracle.causal_attention(q, k, v, 1, 1, 4, 2, hd, 0.1, 0).reshape(4, hd)
+    np.testing.assert_array_equal(o[0], v[:hd])
+    np.testing.assert_array_equal(o[1], v[:hd])   # q heads 0,1 share kv head 0
+    np.testing.assert_array_equal(o[2], v[hd:])
+
+
+# --- lm_head argmax (decoder.rs:941-949) ------------------------------------
+def test_argmax_rows_semantics():
+    x = np.array([[1, np.nan, 5, 5],          # first maximum wins
+                  [np.nan, 3, 4, 1],          # NaN at 0 is never replaced
+                  [-np.inf] * 4,              # nothing beats element 0
+                  [2, 2, 1, np.inf],
+                  [0, -1, np.nan, 0.5]], np.float32)
+    np.testing.assert_array_equal(oracle.argmax_rows(x, 5, 4), [2, 0, 0, 3, 3])
+    r = np.random.default_rng(4)
+    y = r.standard_normal((6, 1000)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.argmax_rows(y, 6, 1000), y.argmax(axis=1))
