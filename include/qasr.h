@@ -303,6 +303,25 @@ int qasr_causal_attention_f32(float* out, const float* q, const float* k, const 
                               size_t seq_q, size_t seq_k, size_t n_heads, size_t n_kv_heads,
                               size_t head_dim, float scale, size_t q_offset, void* stream);
 
+/* qasr_causal_attention_f32 for decode-shaped calls (few query rows, long
+ * key ranges): the keys of each (row, kv head) are split over up to 64
+ * workgroups whose partial (max, sum, output) triples go to the caller's
+ * workspace and are merged by a second kernel, so a single decode stream
+ * uses the whole GPU. Same results within rounding (the merge reorders the
+ * softmax sums). workspace: 16-byte aligned, at least
+ * qasr_causal_attention_workspace_floats(seq_q, n_heads, head_dim) floats for
+ * the full split; with less (or NULL) it falls back to fewer or no splits.
+ * No reference counterpart: the reference threads over heads
+ * (kernels/mod.rs:1174-1203); this is its single-stream GPU shape. */
+int qasr_causal_attention_split_f32(float* out, const float* q, const float* k, const float* v,
+                                    size_t seq_q, size_t seq_k, size_t n_heads,
+                                    size_t n_kv_heads, size_t head_dim, float scale,
+                                    size_t q_offset, float* workspace, size_t workspace_floats,
+                                    void* stream);
+
+/* Workspace floats qasr_causal_attention_split_f32 can use for these sizes. */
+size_t qasr_causal_attention_workspace_floats(size_t seq_q, size_t n_heads, size_t head_dim);
+
 /* ------------------------------------------------------------------------ */
 /* lm_head (decoder.rs:929-963)                                              */
 /* ------------------------------------------------------------------------ */

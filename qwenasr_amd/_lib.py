@@ -49,6 +49,7 @@ SIGNATURES: dict[str, list] = {
     "qasr_head_rms_norm_rope_f32": [P, P, P, P, P, P, P, Z, Z, Z, Z, Z, F, P],
     "qasr_argmax_rows_f32": [P, P, Z, Z, P],
     "qasr_causal_attention_f32": [P, P, P, P, Z, Z, Z, Z, Z, F, Z, P],
+    "qasr_causal_attention_split_f32": [P, P, P, P, Z, Z, Z, Z, Z, F, Z, P, Z, P],
     "qasr_lm_head_int8_argmax_f32": [P, P, P, P, P, Z, Z, Z, P],
     "qasr_head_rms_norm_rope_kv_f32": [P, P, P, P, P, P, P, P, Z, Z, Z, Z, Z, Z, F, P, P, Z, P],
     "qasr_rope_table_fill_f32": [P, P, Z, Z, Z, F, P],
@@ -72,6 +73,11 @@ SIGNATURES: dict[str, list] = {
     "qasr_gate_up_swiglu_w8a8_packed": [P, P, P, P, P, Z, Z, Z, P],
 }
 
+# entry points that return a size instead of a status
+SIZE_QUERIES = {
+    "qasr_causal_attention_workspace_floats": [ctypes.c_size_t] * 3,
+}
+
 _LIB = None
 
 
@@ -88,6 +94,9 @@ def lib() -> ctypes.CDLL:
         so.qasr_version.argtypes = []
         so.qasr_last_error.restype = c_char_p
         so.qasr_last_error.argtypes = []
+        for name in SIZE_QUERIES:
+            getattr(so, name).restype = ctypes.c_size_t
+            getattr(so, name).argtypes = SIZE_QUERIES[name]
         for name, args in SIGNATURES.items():
             fn = getattr(so, name)
             fn.argtypes = args

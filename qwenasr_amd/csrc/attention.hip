@@ -29,10 +29,14 @@ QASR_DEV float bcast_lane(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-template <int HD, int G, int R, int S>
+// PARTIAL: workgroup z covers keys [z * keys_per_split, (z + 1) * keys_per_split)
+// and writes its unnormalised (max, sum, out) per head to the workspace
+// (ws_o [seq_q][n_heads][nsplit][HD], ws_ml [seq_q][n_heads][nsplit][2]).
+template <int HD, int G, int R, int S, bool PARTIAL = false>
 __global__ __launch_bounds__(64 * R * S) void causal_attention_kernel(
     float* __restrict__ out, const float* __restrict__ q, const float* __restrict__ k,
-    const float* __restrict__ v, int seq_q, int seq_k, int nk, float scale, int q_offset) {
+    const float* __restrict__ v, int seq_q, int seq_k, int nk, float scale, int q_offset,
+    int keys_per_split = 0, float* __restrict__ ws_o = nullptr, float* __restrict__ ws_ml = nullptr) {
   constexpr int DPL = HD / 64;  // head dims per lane in the PV product
   constexpr int NW = R * S;
   __shared__ __align__(16) float qs[R][G][HD];
@@ -45,7 +49,12 @@ __global__ __launch_bounds__(64 * R * S) void causal_attention_kernel(
   const int kh = blockIdx.y;
   const int i = blockIdx.x * R + rr;
   const bool row_ok = i < seq_q;
-  const int k_end = row_ok ? min(q_offset + i + 1, seq_k) : 0;
+  int k_end = row_ok ? min(q_offset + i + 1, seq_k) : 0;
+  int k_begin = 0;
+  if constexpr (PARTIAL) {
+    k_begin = min(k_end, (int)blockIdx.z * keys_per_split);
+    k_end = min(k_end, k_begin + keys_per_split);
+  }
   const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
 
   if (sp == 0 && row_ok) {
@@ -63,9 +72,9 @@ __global__ __launch_bounds__(64 * R * S) void causal_attention_kernel(
     for (int d = 0; d < DPL; ++d) o[g][d] = 0.0f;
   }
 
-  const int ntiles = (k_end + 63) / 64;
+  const int ntiles = (k_end - k_begin + 63) / 64;
   for (int t = sp; t < ntiles; t += S) {
-    const int j = t * 64 + lane;
+    const int j = k_begin + t * 64 + lane;
     const bool kv = j < k_end;
     // QK: this lane's key against every head of the group
     float s[G];
@@ -98,8 +107,8 @@ __global__ __launch_bounds__(64 * R * S) void causal_attention_kernel(
       m[g] = mn;
     }
     // PV: keys of the tile in order, lanes over head dims
-    const int nkeys = min(64, k_end - t * 64);
-    const float* vr = v + (size_t)(t * 64) * kv_stride + (size_t)kh * HD + lane * DPL;
+    const int nkeys = min(64, k_end - (k_begin + t * 64));
+    const float* vr = v + (size_t)(k_begin + t * 64) * kv_stride + (size_t)kh * HD + lane * DPL;
     for (int jj = 0; jj < nkeys; ++jj) {
       float vv[DPL];
       if constexpr (DPL == 2) {
@@ -146,11 +155,28 @@ __global__ __launch_bounds__(64 * R * S) void causal_attention_kernel(
 #pragma unroll
           for (int d = 0; d < DPL; ++d) acc[d] = __builtin_fmaf(co[rr * S + w][g][lane * DPL + d], f, acc[d]);
         }
+        m[g] = mx;  // the merged triple is relative to the row's overall max
         l[g] = lsum;
 #pragma unroll
         for (int d = 0; d < DPL; ++d) o[g][d] = acc[d];
       }
     }
+  }
+  if constexpr (PARTIAL) {
+    if (sp == 0 && row_ok) {
+      const int nsplit = gridDim.z;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const size_t slot = ((size_t)i * nk * G + (size_t)kh * G + g) * nsplit + blockIdx.z;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) ws_o[slot * HD + lane * DPL + d] = o[g][d];
+        if (lane == 0) {
+          ws_ml[2 * slot] = m[g];
+          ws_ml[2 * slot + 1] = l[g];
+        }
+      }
+    }
+    return;
   }
   if (sp == 0 && row_ok) {
     float* orow = out + (size_t)i * q_stride + (size_t)kh * G * HD;
@@ -161,6 +187,47 @@ __global__ __launch_bounds__(64 * R * S) void causal_attention_kernel(
       for (int d = 0; d < DPL; ++d) orow[g * HD + lane * DPL + d] = o[g][d] * inv;
     }
   }
+}
+
+// Merges the nsplit partials of each (row, head): one wave per (row, head),
+// lanes over head dims; splits with no keys carry sum 0 and max -1e30.
+template <int HD>
+__global__ __launch_bounds__(256) void attention_combine_kernel(float* __restrict__ out,
+                                                                const float* __restrict__ ws_o,
+                                                                const float* __restrict__ ws_ml,
+                                                                long long rows_heads, int nsplit) {
+  constexpr int DPL = HD / 64;
+  const int lane = threadIdx.x & 63;
+  const long long rh = (long long)blockIdx.x * 4 + threadIdx.x / 64;  // row * n_heads + head
+  if (rh >= rows_heads) return;
+  const float* ml = ws_ml + (size_t)rh * nsplit * 2;
+  float mx = ml[0];
+  for (int z = 1; z < nsplit; ++z) mx = fmaxf(mx, ml[2 * z]);
+  float lsum = 0.0f, acc[DPL];
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) acc[d] = 0.0f;
+  for (int z = 0; z < nsplit; ++z) {
+    const float f = expf(ml[2 * z] - mx);
+    lsum = __builtin_fmaf(ml[2 * z + 1], f, lsum);
+    const float* oz = ws_o + ((size_t)rh * nsplit + z) * HD + lane * DPL;
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) acc[d] = __builtin_fmaf(oz[d], f, acc[d]);
+  }
+  const float inv = lsum > 0.0f ? 1.0f / lsum : 1.0f;
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) out[(size_t)rh * HD + lane * DPL + d] = acc[d] * inv;
+}
+
+template <int HD, int G>
+void launch_attention_split(float* out, const float* q, const float* k, const float* v, int seq_q,
+                            int seq_k, int nk, float scale, int q_offset, int nsplit,
+                            int keys_per_split, float* ws_o, float* ws_ml, hipStream_t st) {
+  const dim3 grid((unsigned)seq_q, (unsigned)nk, (unsigned)nsplit);
+  causal_attention_kernel<HD, G, 1, 4, true><<<grid, 256, 0, st>>>(
+      out, q, k, v, seq_q, seq_k, nk, scale, q_offset, keys_per_split, ws_o, ws_ml);
+  const long long rows_heads = (long long)seq_q * nk * G;
+  attention_combine_kernel<HD><<<(unsigned)((rows_heads + 3) / 4), 256, 0, st>>>(out, ws_o, ws_ml,
+                                                                               rows_heads, nsplit);
 }
 
 template <int HD, int G>
@@ -177,16 +244,57 @@ void launch_attention(float* out, const float* q, const float* k, const float* v
   }
 }
 
+struct SplitPlan {
+  int nsplit = 0, keys_per_split = 0;
+  float* ws_o = nullptr;
+  float* ws_ml = nullptr;
+};
+
 template <int HD>
 bool dispatch_group(int G, float* out, const float* q, const float* k, const float* v, int seq_q,
-                    int seq_k, int nk, float scale, int q_offset, hipStream_t st) {
+                    int seq_k, int nk, float scale, int q_offset, const SplitPlan& sp,
+                    hipStream_t st) {
+#define QASR_ATTN_CASE(GG)                                                                       \
+  case GG:                                                                                       \
+    if (sp.nsplit > 1)                                                                           \
+      launch_attention_split<HD, GG>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, sp.nsplit, \
+                                     sp.keys_per_split, sp.ws_o, sp.ws_ml, st);                 \
+    else                                                                                         \
+      launch_attention<HD, GG>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, st);            \
+    return true;
   switch (G) {
-    case 1: launch_attention<HD, 1>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, st); return true;
-    case 2: launch_attention<HD, 2>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, st); return true;
-    case 4: launch_attention<HD, 4>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, st); return true;
-    case 8: launch_attention<HD, 8>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset, st); return true;
+    QASR_ATTN_CASE(1)
+    QASR_ATTN_CASE(2)
+    QASR_ATTN_CASE(4)
+    QASR_ATTN_CASE(8)
     default: return false;
   }
+#undef QASR_ATTN_CASE
+}
+
+// Key-split plan: aim for about 2 workgroups per CU, splits of at least 256
+// keys, at most kMaxSplits; nothing to gain when the causal range is short.
+constexpr int kMaxSplits = 64;
+
+SplitPlan plan_split(size_t seq_q, size_t seq_k, size_t nk, size_t q_offset, size_t head_dim,
+                     size_t n_heads, float* workspace, size_t workspace_floats) {
+  SplitPlan p;
+  const size_t k_max = seq_k < q_offset + seq_q ? seq_k : q_offset + seq_q;
+  const size_t pairs = seq_q * nk;
+  if (!workspace || pairs >= 512 || k_max < 512) return p;
+  size_t want = (512 + pairs - 1) / pairs;
+  const size_t by_len = k_max / 256;
+  if (want > by_len) want = by_len;
+  if (want > (size_t)kMaxSplits) want = kMaxSplits;
+  if (want < 2) return p;
+  const size_t need = seq_q * n_heads * want * (head_dim + 2);
+  if (need > workspace_floats) return p;
+  p.nsplit = (int)want;
+  p.keys_per_split = (int)(((k_max + want - 1) / want + 63) / 64 * 64);
+  p.nsplit = (int)((k_max + p.keys_per_split - 1) / p.keys_per_split);
+  p.ws_o = workspace;
+  p.ws_ml = workspace + seq_q * n_heads * (size_t)p.nsplit * head_dim;
+  return p;
 }
 
 }  // namespace
@@ -194,10 +302,10 @@ bool dispatch_group(int G, float* out, const float* q, const float* k, const flo
 
 using namespace qasr;
 
-extern "C" int qasr_causal_attention_f32(float* out, const float* q, const float* k, const float* v,
-                                         size_t seq_q, size_t seq_k, size_t n_heads,
-                                         size_t n_kv_heads, size_t head_dim, float scale,
-                                         size_t q_offset, void* stream) {
+static int attention_impl(float* out, const float* q, const float* k, const float* v, size_t seq_q,
+                          size_t seq_k, size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                          float scale, size_t q_offset, float* workspace, size_t workspace_floats,
+                          void* stream) {
   if (seq_q == 0 || n_heads == 0) return QASR_OK;
   QASR_REQUIRE(out && q, "causal_attention: null pointer");
   QASR_REQUIRE(seq_k == 0 || (k && v), "causal_attention: null k or v");
@@ -216,11 +324,36 @@ extern "C" int qasr_causal_attention_f32(float* out, const float* q, const float
                 "causal_attention: needs head_dim 64 or 128, n_heads/n_kv_heads in {1,2,4,8} "
                 "and 16-byte aligned buffers");
   }
+  QASR_REQUIRE(!workspace || aligned16(workspace), "causal_attention: workspace must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
   const int sq = (int)seq_q, sk = (int)seq_k, nk = (int)n_kv_heads, qo = (int)q_offset;
+  const SplitPlan sp = plan_split(seq_q, seq_k, n_kv_heads, q_offset, head_dim, n_heads, workspace,
+                                  workspace_floats);
   if (head_dim == 64)
-    dispatch_group<64>((int)G, out, q, k, v, sq, sk, nk, scale, qo, st);
+    dispatch_group<64>((int)G, out, q, k, v, sq, sk, nk, scale, qo, sp, st);
   else
-    dispatch_group<128>((int)G, out, q, k, v, sq, sk, nk, scale, qo, st);
+    dispatch_group<128>((int)G, out, q, k, v, sq, sk, nk, scale, qo, sp, st);
   return launch_status("causal_attention");
+}
+
+extern "C" int qasr_causal_attention_f32(float* out, const float* q, const float* k, const float* v,
+                                         size_t seq_q, size_t seq_k, size_t n_heads,
+                                         size_t n_kv_heads, size_t head_dim, float scale,
+                                         size_t q_offset, void* stream) {
+  return attention_impl(out, q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset,
+                        nullptr, 0, stream);
+}
+
+extern "C" size_t qasr_causal_attention_workspace_floats(size_t seq_q, size_t n_heads,
+                                                         size_t head_dim) {
+  return seq_q * n_heads * (size_t)kMaxSplits * (head_dim + 2);
+}
+
+extern "C" int qasr_causal_attention_split_f32(float* out, const float* q, const float* k,
+                                               const float* v, size_t seq_q, size_t seq_k,
+                                               size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                               float scale, size_t q_offset, float* workspace,
+                                               size_t workspace_floats, void* stream) {
+  return attention_impl(out, q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset,
+                        workspace, workspace_floats, stream);
 }

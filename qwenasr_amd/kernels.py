@@ -203,6 +203,27 @@ def causal_attention(out, q, k, v, seq_q: int, seq_k: int, n_heads: int, n_kv_he
               q_offset, _stream())
 
 
+def attention_workspace(seq_q: int, n_heads: int, head_dim: int, device="cuda") -> torch.Tensor:
+    """Workspace for causal_attention_split (allocate once, reuse per call)."""
+    n = _lib.lib().qasr_causal_attention_workspace_floats(seq_q, n_heads, head_dim)
+    return torch.empty(n, dtype=F32, device=device)
+
+
+def causal_attention_split(out, q, k, v, seq_q: int, seq_k: int, n_heads: int, n_kv_heads: int,
+                           head_dim: int, scale: float, q_offset: int, workspace) -> None:
+    """causal_attention with the keys split over workgroups (decode shape);
+    partials go to ``workspace`` (see attention_workspace)."""
+    _need(out, F32, seq_q * n_heads * head_dim, "out")
+    _need(q, F32, seq_q * n_heads * head_dim, "q")
+    if seq_k:
+        _need(k, F32, seq_k * n_kv_heads * head_dim, "k")
+        _need(v, F32, seq_k * n_kv_heads * head_dim, "v")
+    _need(workspace, F32, 0, "workspace")
+    _lib.call("qasr_causal_attention_split_f32", _ptr(out), _ptr(q), _ptr(k if seq_k else None),
+              _ptr(v if seq_k else None), seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale,
+              q_offset, _ptr(workspace), workspace.numel(), _stream())
+
+
 def argmax_rows(idx, x, rows: int, cols: int) -> None:
     """Per-row argmax with the lm_head loop's semantics (decoder.rs:941-949)."""
     _need(idx, I32, rows, "idx")

@@ -52,7 +52,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_ctypes_table_matches_header():
-    declared = declared_functions() - {"qasr_version", "qasr_last_error"}
+    declared = declared_functions() - {"qasr_version", "qasr_last_error"} - set(_lib.SIZE_QUERIES)
     assert set(_lib.SIGNATURES) == declared
 
 
@@ -155,3 +155,8 @@ def test_cpp_mirror_binary_links_the_static_archive():
     assert "libqasr_hip.so" not in ldd  # kernels come from libqasr_hip.a
     nm = subprocess.run(["nm", str(build.CPP_TEST_BIN)], capture_output=True, text=True).stdout
     assert " T qasr_rms_norm_f32" in nm
+
+
+def test_attention_workspace_size_query():
+    # seq_q * n_heads * 64 splits * (head_dim + 2) floats
+    assert _lib.lib().qasr_causal_attention_workspace_floats(1, 16, 128) == 16 * 64 * 130

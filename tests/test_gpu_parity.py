@@ -856,3 +856,31 @@ def test_causal_attention_reads_a_cache_block(dev):
     K.causal_attention(out, dev_t(q, dev), dev_t(kc, dev), dev_t(vc, dev), 1, seq_k, nq, nk, hd,
                        hd ** -0.5, seq_k - 1)
     assert_close(host(out), ref, RTOL, ATOL, "cache block")
+
+
+@pytest.mark.parametrize("name,seq_q,seq_k,nq,nk,hd,q_offset", [
+    ("decode_1.7b_pos2047", 1, 2048, 16, 8, 128, 2047),
+    ("decode_pos700", 1, 701, 16, 8, 128, 700),
+    ("decode_3rows", 3, 4000, 16, 8, 128, 3997),
+    ("decode_hd64_g4", 1, 1500, 8, 2, 64, 1499),
+    ("short_no_split", 1, 200, 16, 8, 128, 199),
+    ("rows_end_early", 2, 3000, 16, 8, 128, 700),   # causal limit far below seq_k: empty splits
+])
+def test_causal_attention_split(dev, name, seq_q, seq_k, nq, nk, hd, q_offset):
+    from qwenasr_amd import kernels as K
+
+    r = rng(52, seq_q, seq_k, hd)
+    q = normal(r, seq_q * nq * hd)
+    k = normal(r, seq_k * nk * hd)
+    v = normal(r, seq_k * nk * hd)
+    ref = oracle.causal_attention(q, k, v, seq_q, seq_k, nq, nk, hd, hd ** -0.5, q_offset)
+    out = torch.empty(seq_q * nq * hd, device=dev)
+    ws = K.attention_workspace(seq_q, nq, hd, dev)
+    K.causal_attention_split(out, dev_t(q, dev), dev_t(k, dev), dev_t(v, dev), seq_q, seq_k, nq, nk,
+                             hd, hd ** -0.5, q_offset, ws)
+    assert_close(host(out), ref, RTOL, ATOL, name)
+    # a too-small workspace falls back to fewer or no splits, same results
+    out2 = torch.empty_like(out)
+    K.causal_attention_split(out2, dev_t(q, dev), dev_t(k, dev), dev_t(v, dev), seq_q, seq_k, nq, nk,
+                             hd, hd ** -0.5, q_offset, ws[:100])
+    assert_close(host(out2), ref, RTOL, ATOL, name + " fallback")
