@@ -10,6 +10,10 @@ random-init weights -- no checkpoints):
   c3  audio-encoder ops: PE add + LayerNorm on [3000,896], erf-GELU on [3000,3584]
   c4  1.7B INT8 decode gate/up matvec + SwiGLU, B=1, 28 distinct layers per step
   c5  1.7B batched decode, B=256: add+RMSNorm + q/k norm+RoPE + quantize + INT8 MFMA gate/up GEMM+SwiGLU
+  w8a32_decode  1.7B INT8 decode projections via the W8A32 drop-in (q/k/v/o, gate/up, down), 28 layers
+  attn_decode   1.7B decode attention at position 2047 (keys split over workgroups), 28 layers
+  attn_prefill  0.6B causal prefill attention, T=512
+  lm_head       0.6B INT8 lm_head [151936,1024] logits + greedy argmax, B=1
 
 A step is one pass of the workload's kernel chain over one buffer set; sets
 rotate so the working set exceeds the 256 MB last-level cache. Steps are
@@ -36,6 +40,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "fused-layer-kernel GB/s (% MI355X HBM peak) + decode tokens/s, 0.6B/1.7B shapes"
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 LLC_BYTES = 256 << 20
 ROTATE_BYTES = 2 * LLC_BYTES  # each kernel's rotating footprint must exceed 2x the LLC
 
@@ -57,7 +62,9 @@ class Workload:
     name = ""
     description = ""
     unit_tokens = 1  # tokens per step (for tokens/s)
-    step_bytes = 0   # algorithmic bytes per step (SURVEY per-unit figure)
+    tokens_per_step = 1.0  # tokens a step advances (28 layers make one decode token)
+    step_bytes = 0   # algorithmic bytes per step
+    dtype = "f32"    # arithmetic type of the path
 
     def __init__(self, dev, torch):
         self.dev = dev
@@ -74,8 +81,8 @@ class Workload:
         return t
 
     def step(self, i: int) -> None:
-        for launch, _ in self.kernels.values():
-            launch(i)
+        for spec in self.kernels.values():
+            spec[0](i)
 
     def config(self) -> dict:
         return {}
@@ -119,6 +126,7 @@ class C1DecodeChain(Workload):
             "swiglu": (lambda i: K.swiglu_split(self.o[i % S], self.g[i % S], self.u[i % S], I), 3 * I * F),
         }
         self.step_bytes = sum(b for _, b in self.kernels.values())
+        self.tokens_per_step = 1.0 / 28  # one layer's chain; 28 layers make a token
 
     def config(self):
         return {"batch": 1, "hidden": 1024, "heads": "16q/8kv x 128", "intermediate": 3072}
@@ -168,6 +176,7 @@ class C2PrefillChain(Workload):
                                 3 * T * I * F),
         }
         self.step_bytes = sum(b for _, b in self.kernels.values())
+        self.tokens_per_step = 512.0
 
     def config(self):
         return {"seq_len": 512, "hidden": 1024, "heads": "16q/8kv x 128", "intermediate": 3072,
@@ -201,6 +210,7 @@ class C3EncoderOps(Workload):
             "gelu_erf": (lambda i: K.gelu_erf(self.h[i % S], T * FF), 2 * T * FF * F),
         }
         self.step_bytes = sum(b for _, b in self.kernels.values())
+        self.tokens_per_step = 3000.0
 
     def config(self):
         return {"rows": 3000, "d_model": 896, "ffn": 3584, "pe_period": 13, "buffer_sets": self.S}
@@ -239,6 +249,8 @@ class C4Int8Matvec(Workload):
         self.all_layers = all_layers
         self.layer_bytes = layer_bytes
         self.step_bytes = L * layer_bytes
+        self.tokens_per_step = 1.0  # a step is 28 layers: one token
+        self.dtype = "int8/int32->f32"
 
     def step(self, i):
         self.all_layers(i)
@@ -296,6 +308,8 @@ class C5BatchedDecode(Workload):
                 2 * I * H + 2 * I * F + B * H + B * F + B * I * F),
         }
         self.step_bytes = sum(b for _, b in self.kernels.values())
+        self.tokens_per_step = 256.0 / 28  # one layer for 256 streams
+        self.dtype = "int8/int32->f32"
         self.gemm_ops = 2 * B * 2 * I * H
 
     def config(self):
@@ -303,8 +317,155 @@ class C5BatchedDecode(Workload):
                 "layers_rotated": 28}
 
 
+class W8A32Decode(Workload):
+    name = "w8a32_decode"
+    description = ("qwen3-asr-1.7b INT8 decode projections as the reference runs them (W8A32 "
+                   "linear_nobias_int8, B=1): q/k/v/o, fused gate/up and down per layer, 28 distinct layers")
+    unit_tokens = 1
+    dtype = "int8/f32"
+
+    SHAPES = {"wq": (2048, 2048), "wk": (1024, 2048), "wv": (1024, 2048), "wo": (2048, 2048),
+              "gate_up": (12288, 2048), "down": (2048, 6144)}
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        L = 28
+        self.L = L
+        self.w = {n: [] for n in self.SHAPES}
+        for n, (o, i) in self.SHAPES.items():
+            for _ in range(L):
+                # int8 weights and per-row scales with the quantizer's value range
+                q = torch.randint(-127, 128, (o * i,), generator=self.gen, device=dev, dtype=torch.int8)
+                self.w[n].append((q, self.randn(o, 1e-4, 1e-3).abs_()))
+        self.x = {n: [self.randn(i) for _ in range(L)] for n, (o, i) in self.SHAPES.items()}
+        self.y = {n: [torch.empty(o, device=dev) for _ in range(L)] for n, (o, i) in self.SHAPES.items()}
+
+        def mk(n):
+            o, i = self.SHAPES[n]
+            return (lambda j: K.linear_nobias_int8(self.y[n][j % L], self.x[n][j % L], self.w[n][j % L][0],
+                                                   self.w[n][j % L][1], 1, i, o),
+                    o * i + o * F + i * F + o * F)
+
+        self.kernels = {n: mk(n) for n in self.SHAPES}
+        self.step_bytes = L * sum(b for _, b in self.kernels.values())
+        self.tokens_per_step = 1.0
+
+    def step(self, i):
+        for l in range(self.L):
+            for spec in self.kernels.values():
+                spec[0](l)
+
+    def config(self):
+        return {"batch": 1, "hidden": 2048, "intermediate": 6144, "layers": 28,
+                "projections": {n: f"[{o},{i}]" for n, (o, i) in self.SHAPES.items()}}
+
+
+class AttnDecode(Workload):
+    name = "attn_decode"
+    description = ("qwen3-asr-1.7b decode attention at position 2047: q[16,128] against a 2048-row "
+                   "KV block [2048, 8x128] per layer, keys split over workgroups; 28 distinct layers per step")
+    unit_tokens = 1
+    dtype = "f32"
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        nq, nk, hd, L, seq_k = 16, 8, 128, 28, 2048
+        self.k = [self.randn(seq_k * nk * hd) for _ in range(L)]
+        self.v = [self.randn(seq_k * nk * hd) for _ in range(L)]
+        self.q = [self.randn(nq * hd) for _ in range(L)]
+        self.o = [torch.empty(nq * hd, device=dev) for _ in range(L)]
+        self.ws = K.attention_workspace(1, nq, hd, dev)
+        scale = hd ** -0.5
+
+        def one(i):
+            l = i % L
+            K.causal_attention_split(self.o[l], self.q[l], self.k[l], self.v[l], 1, seq_k, nq, nk, hd,
+                                     scale, seq_k - 1, self.ws)
+
+        self.one, self.L = one, L
+        layer_bytes = 2 * seq_k * nk * hd * F + 2 * nq * hd * F
+        self.kernels = {"causal_attention_split": (one, layer_bytes)}
+        self.step_bytes = L * layer_bytes
+        self.tokens_per_step = 1.0
+
+    def step(self, i):
+        for l in range(self.L):
+            self.one(l)
+
+    def config(self):
+        return {"batch": 1, "position": 2047, "heads": "16q/8kv x 128", "layers": 28}
+
+
+class AttnPrefill(Workload):
+    name = "attn_prefill"
+    description = ("qwen3-asr-0.6b causal prefill attention T=512: q[512,16x128] over k/v[512,8x128], "
+                   "fp32 (VALU)")
+    unit_tokens = 512
+    dtype = "f32"
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        T, nq, nk, hd = 512, 16, 8, 128
+        per_set = (2 * T * nq * hd + 2 * T * nk * hd) * F
+        self.S = sets_for(per_set)
+        S = self.S
+        self.q = [self.randn(T * nq * hd) for _ in range(S)]
+        self.k = [self.randn(T * nk * hd) for _ in range(S)]
+        self.v = [self.randn(T * nk * hd) for _ in range(S)]
+        self.o = [torch.empty(T * nq * hd, device=dev) for _ in range(S)]
+        scale = hd ** -0.5
+        flops = 2 * 2 * nq * hd * (T * (T + 1) // 2)
+        self.kernels = {"causal_attention": (
+            lambda i: K.causal_attention(self.o[i % S], self.q[i % S], self.k[i % S], self.v[i % S],
+                                         T, T, nq, nk, hd, scale, 0), per_set, flops)}
+        self.step_bytes = per_set
+        self.tokens_per_step = float(T)
+
+    def config(self):
+        return {"seq_len": 512, "heads": "16q/8kv x 128", "buffer_sets": self.S}
+
+
+class LmHead(Workload):
+    name = "lm_head"
+    description = ("qwen3-asr-0.6b INT8 lm_head [151936,1024] logits + greedy argmax, B=1 "
+                   "(W8A32 as the reference), 4 weight copies rotate")
+    unit_tokens = 1
+    dtype = "int8/f32"
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        V, H, C = VOCAB, 1024, 4
+        self.w = []
+        for _ in range(C):
+            w = self.randn(V * H, 0.02)
+            q, sc = K.quantize_f32_to_int8(w, V, H)
+            del w
+            self.w.append(K.QuantWeight(q, sc, V, H))
+        self.x = [self.randn(H) for _ in range(C)]
+        self.logits = [torch.empty(V, device=dev) for _ in range(C)]
+        self.idx = [torch.empty(1, dtype=torch.int32, device=dev) for _ in range(C)]
+        nbytes = V * H + V * F + H * F + 2 * V * F + 4
+        self.kernels = {"lm_head_int8_argmax": (
+            lambda i: K.lm_head_int8_argmax(self.idx[i % C], self.logits[i % C], self.x[i % C],
+                                            self.w[i % C], 1, H, V), nbytes)}
+        self.step_bytes = nbytes
+        self.tokens_per_step = 1.0
+
+    def config(self):
+        return {"batch": 1, "hidden": 1024, "vocab": VOCAB, "weight_copies": 4}
+
+
 WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c4": C4Int8Matvec,
-             "c5": C5BatchedDecode}
+             "c5": C5BatchedDecode, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
+             "lm_head": LmHead}
 
 
 # ---------------------------------------------------------------------------
@@ -445,6 +606,61 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
                 "ms_per_step": per * 1e3 * 28, "tokens_per_s": 1.0 / (28 * per),
                 "sample": f"{n} layer matvecs (W8A32, the reference's INT8 path) + SwiGLU on the oracle, "
                           f"{threads} threads; one weight matrix reused, so it is LLC-warm"}
+    if name == "w8a32_decode":
+        shapes = W8A32Decode.SHAPES
+        ws = {n: (r.integers(-127, 128, o * i, dtype=np.int8), (1e-3 + 1e-4 * r.random(o)).astype(np.float32))
+              for n, (o, i) in shapes.items()}
+        xs = {n: r.standard_normal(i, dtype=np.float32) for n, (o, i) in shapes.items()}
+        threads = min(nproc, 16)
+
+        def layer():
+            for n, (o, i) in shapes.items():
+                oracle.linear_nobias_int8(xs[n], ws[n][0], ws[n][1], 1, i, o, n_threads=threads)
+
+        n, dt = run_until(layer, seconds)
+        per = dt / n
+        return {"value": step_bytes / 28 / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "ms_per_step": per * 1e3 * 28, "tokens_per_s": 1.0 / (28 * per),
+                "sample": f"{n} layers of the six W8A32 projections on the oracle, {threads} threads "
+                          "(one layer's weights reused, so LLC-warm)"}
+    if name == "attn_decode":
+        nq, nk, hd, seq_k = 16, 8, 128, 2048
+        q = r.standard_normal(nq * hd, dtype=np.float32)
+        k = r.standard_normal(seq_k * nk * hd, dtype=np.float32)
+        v = r.standard_normal(seq_k * nk * hd, dtype=np.float32)
+        n, dt = run_until(lambda: oracle.causal_attention(q, k, v, 1, seq_k, nq, nk, hd, hd ** -0.5,
+                                                          seq_k - 1), seconds)
+        per = dt / n
+        return {"value": step_bytes / 28 / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "ms_per_step": per * 1e3 * 28, "tokens_per_s": 1.0 / (28 * per),
+                "sample": f"{n} single-layer decode attentions at position 2047 on the oracle, one thread "
+                          "(the reference threads over heads)"}
+    if name == "attn_prefill":
+        T, nq, nk, hd = 512, 16, 8, 128
+        q = r.standard_normal(T * nq * hd, dtype=np.float32)
+        k = r.standard_normal(T * nk * hd, dtype=np.float32)
+        v = r.standard_normal(T * nk * hd, dtype=np.float32)
+        n, dt = run_until(lambda: oracle.causal_attention(q, k, v, T, T, nq, nk, hd, hd ** -0.5, 0),
+                          seconds)
+        per = dt / n
+        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "ms_per_step": per * 1e3, "tokens_per_s": T / per,
+                "sample": f"{n} T=512 prefill attentions on the oracle, one thread"}
+    if name == "lm_head":
+        V, H = VOCAB, 1024
+        wq, ws = oracle.quantize_f32_to_int8(0.02 * r.standard_normal(V * H, dtype=np.float32), V, H)
+        x = r.standard_normal(H, dtype=np.float32)
+        threads = min(nproc, 16)
+
+        def step():
+            lg = oracle.linear_nobias_int8(x, wq, ws, 1, H, V, n_threads=threads)
+            oracle.argmax_rows(lg, 1, V)
+
+        n, dt = run_until(step, seconds)
+        per = dt / n
+        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "ms_per_step": per * 1e3, "tokens_per_s": 1.0 / per,
+                "sample": f"{n} INT8 lm_head matvecs + argmax on the oracle, {threads} threads"}
     raise ValueError(name)
 
 
@@ -543,22 +759,19 @@ def main() -> int:
     print(f"[bench] step {ms_step * 1e3:.2f} us", file=sys.stderr, flush=True)
 
     per_kernel = {}
-    for kname, (launch, nbytes) in wl.kernels.items():
+    for kname, spec in wl.kernels.items():
+        launch, nbytes = spec[0], spec[1]
         ms = time_replay(torch, launch, K, use_graph, reps)
         per_kernel[kname] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / (ms * 1e-3) / 1e9,
                              "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        if len(spec) > 2:
+            per_kernel[kname]["flops"] = spec[2]
+            per_kernel[kname]["TFLOP/s"] = spec[2] / (ms * 1e-3) / 1e12
         print(f"[bench] {kname}: {ms * 1e3:.2f} us, {per_kernel[kname]['GB/s']:.0f} GB/s",
               file=sys.stderr, flush=True)
 
     value = wl.step_bytes / (ms_step * 1e-3) / 1e9
-    if wl.name == "c4":
-        tokens_per_s = 1.0 / (ms_step * 1e-3)  # one step = one token through 28 layers
-    elif wl.name == "c5":
-        tokens_per_s = wl.unit_tokens / (28 * ms_step * 1e-3)
-    elif wl.name == "c1":
-        tokens_per_s = 1.0 / (28 * ms_step * 1e-3)
-    else:
-        tokens_per_s = wl.unit_tokens / (ms_step * 1e-3)
+    tokens_per_s = wl.tokens_per_step / (ms_step * 1e-3)
 
     # dominant kernel = the one moving the most algorithmic bytes per step (a
     # fixed choice per workload; by time the small c2 kernels tie within noise)
@@ -572,10 +785,18 @@ def main() -> int:
             traffic = entry["hbm_bytes_per_launch"] if entry else None
         except (ValueError, OSError, KeyError, TypeError):
             traffic = None
-    roofline = {"bound": "hbm", "kernel": dom_name, "achieved": round(dom["GB/s"], 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["frac_hbm"], 4),
-                "traffic": traffic, "avg_us": round(dom["us"], 3),
-                "algorithmic_bytes": dom["bytes"]}
+    if "flops" in dom and dom["flops"] / dom["bytes"] > FP32_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+        # compute-bound (arithmetic intensity above the fp32 ridge)
+        roofline = {"bound": "mfma", "kernel": dom_name, "achieved": round(dom["TFLOP/s"], 2),
+                    "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(dom["TFLOP/s"] / FP32_PEAK_TFLOPS, 4), "traffic": traffic,
+                    "avg_us": round(dom["us"], 3), "algorithmic_flops": dom["flops"],
+                    "algorithmic_bytes": dom["bytes"]}
+    else:
+        roofline = {"bound": "hbm", "kernel": dom_name, "achieved": round(dom["GB/s"], 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["frac_hbm"], 4),
+                    "traffic": traffic, "avg_us": round(dom["us"], 3),
+                    "algorithmic_bytes": dom["bytes"]}
     if wl.name == "c5":
         g = per_kernel["gate_up_swiglu_w8a8_gemm"]
         roofline["gemm_mfma_int8_TOPS"] = round(wl.gemm_ops / (g["us"] * 1e-6) / 1e12, 1)
@@ -597,7 +818,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if wl.name in ("c1", "c2", "c3") else "int8/int32->f32",
+        "dtype": wl.dtype,
         "data": "synthetic (seeded torch.randn inputs, random-init weights; no checkpoints)",
         "config": {"workload": wl.description, **wl.config(),
                    "timing": "hipGraph replay of K steps, HIP events" if use_graph else "eager launches, HIP events"},

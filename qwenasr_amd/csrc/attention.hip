@@ -25,6 +25,8 @@
 namespace qasr {
 namespace {
 
+constexpr int kPvBatch = 16;  // v rows in flight per lane in the PV product
+
 QASR_DEV float bcast_lane(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
@@ -106,23 +108,34 @@ __global__ __launch_bounds__(64 * R * S) void causal_attention_kernel(
       for (int d = 0; d < DPL; ++d) o[g][d] *= corr;
       m[g] = mn;
     }
-    // PV: keys of the tile in order, lanes over head dims
+    // PV: keys of the tile in order, lanes over head dims. The v rows of 16
+    // keys are loaded before their FMAs so their latencies overlap (past the
+    // tile's last key the loads repeat that key and are not accumulated).
     const int nkeys = min(64, k_end - (k_begin + t * 64));
     const float* vr = v + (size_t)(k_begin + t * 64) * kv_stride + (size_t)kh * HD + lane * DPL;
-    for (int jj = 0; jj < nkeys; ++jj) {
-      float vv[DPL];
-      if constexpr (DPL == 2) {
-        const float2 t2 = *reinterpret_cast<const float2*>(vr + (size_t)jj * kv_stride);
-        vv[0] = t2.x;
-        vv[1] = t2.y;
-      } else {
-        vv[0] = vr[(size_t)jj * kv_stride];
+    for (int j0 = 0; j0 < nkeys; j0 += kPvBatch) {
+      float vv[kPvBatch][DPL];
+#pragma unroll
+      for (int u = 0; u < kPvBatch; ++u) {
+        const size_t jj = (size_t)min(j0 + u, nkeys - 1);
+        if constexpr (DPL == 2) {
+          const float2 t2 = *reinterpret_cast<const float2*>(vr + jj * kv_stride);
+          vv[u][0] = t2.x;
+          vv[u][1] = t2.y;
+        } else {
+          vv[u][0] = vr[jj * kv_stride];
+        }
       }
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pj = bcast_lane(p[g], jj);
+      for (int u = 0; u < kPvBatch; ++u) {
+        if (j0 + u < nkeys) {  // uniform across the wave
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) o[g][d] = __builtin_fmaf(pj, vv[d], o[g][d]);
+          for (int g = 0; g < G; ++g) {
+            const float pj = bcast_lane(p[g], j0 + u);
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) o[g][d] = __builtin_fmaf(pj, vv[u][d], o[g][d]);
+          }
+        }
       }
     }
   }
@@ -223,7 +236,7 @@ void launch_attention_split(float* out, const float* q, const float* k, const fl
                             int seq_k, int nk, float scale, int q_offset, int nsplit,
                             int keys_per_split, float* ws_o, float* ws_ml, hipStream_t st) {
   const dim3 grid((unsigned)seq_q, (unsigned)nk, (unsigned)nsplit);
-  causal_attention_kernel<HD, G, 1, 4, true><<<grid, 256, 0, st>>>(
+  causal_attention_kernel<HD, G, 1, 1, true><<<grid, 64, 0, st>>>(
       out, q, k, v, seq_q, seq_k, nk, scale, q_offset, keys_per_split, ws_o, ws_ml);
   const long long rows_heads = (long long)seq_q * nk * G;
   attention_combine_kernel<HD><<<(unsigned)((rows_heads + 3) / 4), 256, 0, st>>>(out, ws_o, ws_ml,
@@ -272,8 +285,9 @@ bool dispatch_group(int G, float* out, const float* q, const float* k, const flo
 #undef QASR_ATTN_CASE
 }
 
-// Key-split plan: aim for about 2 workgroups per CU, splits of at least 256
-// keys, at most kMaxSplits; nothing to gain when the causal range is short.
+// Key-split plan: one-wave workgroups of whole 64-key tiles, aiming at about
+// 4 waves per CU (1024 workgroups), at most kMaxSplits splits; nothing to
+// gain when there are already many (row, kv head) pairs or few keys.
 constexpr int kMaxSplits = 64;
 
 SplitPlan plan_split(size_t seq_q, size_t seq_k, size_t nk, size_t q_offset, size_t head_dim,
@@ -281,9 +295,9 @@ SplitPlan plan_split(size_t seq_q, size_t seq_k, size_t nk, size_t q_offset, siz
   SplitPlan p;
   const size_t k_max = seq_k < q_offset + seq_q ? seq_k : q_offset + seq_q;
   const size_t pairs = seq_q * nk;
-  if (!workspace || pairs >= 512 || k_max < 512) return p;
-  size_t want = (512 + pairs - 1) / pairs;
-  const size_t by_len = k_max / 256;
+  if (!workspace || pairs >= 512 || k_max < 256) return p;
+  size_t want = (1024 + pairs - 1) / pairs;
+  const size_t by_len = k_max / 64;
   if (want > by_len) want = by_len;
   if (want > (size_t)kMaxSplits) want = kMaxSplits;
   if (want < 2) return p;

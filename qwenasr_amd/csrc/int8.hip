@@ -112,6 +112,59 @@ __global__ __launch_bounds__(256) void w8a32_vec_kernel(float* y, const float* x
   }
 }
 
+// Decode shape (one token): each wave owns R consecutive output rows, issues
+// all R x KCH weight loads before the first FMA (so R KiB per chunk are in
+// flight per wave instead of one), and keeps x in registers across its rows.
+template <int KCH, int R>
+__global__ __launch_bounds__(256) void w8a32_rows_kernel(float* y, const float* x, const int8_t* w,
+                                                         const float* scales, const float* bias,
+                                                         int in_dim, int out_dim) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int o0 = (blockIdx.x * (256 / kWave) + threadIdx.x / kWave) * R;
+  if (o0 >= out_dim) return;
+  v4i wv[R][KCH];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int o = o0 + r < out_dim ? o0 + r : out_dim - 1;  // tail rows recompute the last row
+    const v4i* wr = reinterpret_cast<const v4i*>(w + (size_t)o * in_dim);
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) wv[r][c] = __builtin_nontemporal_load(wr + c * kWave + lane);
+  }
+  float4 xv[KCH][4];
+#pragma unroll
+  for (int c = 0; c < KCH; ++c)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xv[c][t] = ld4(x + (c * kWave + lane) * 16 + 4 * t, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int wq[4] = {wv[r][c][0], wv[r][c][1], wv[r][c][2], wv[r][c][3]};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        a = __builtin_fmaf((float)(int8_t)(wq[t] & 0xff), xv[c][t].x, a);
+        a = __builtin_fmaf((float)(int8_t)((wq[t] >> 8) & 0xff), xv[c][t].y, a);
+        a = __builtin_fmaf((float)(int8_t)((wq[t] >> 16) & 0xff), xv[c][t].z, a);
+        a = __builtin_fmaf((float)(int8_t)((wq[t] >> 24) & 0xff), xv[c][t].w, a);
+      }
+    }
+    acc[r] = wave_sum(a);
+  }
+  if (lane < R && o0 + lane < out_dim) {
+    float a = acc[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r)
+      if (lane == r) a = acc[r];
+    const int o = o0 + lane;
+    float res = a * scales[o];
+    if (bias) res += bias[o];
+    y[o] = res;
+  }
+}
+
 __global__ __launch_bounds__(256) void w8a32_scalar_kernel(float* y, const float* x, const int8_t* w,
                                                            const float* scales, const float* bias,
                                                            int seq, int in_dim, int out_dim) {
@@ -351,7 +404,19 @@ static int launch_w8a32(float* y, const float* x, const int8_t* w, const float* 
   const int s = (int)seq_len, k = (int)in_dim, o = (int)out_dim;
   const bool vec = in_dim >= 1024 && in_dim % 1024 == 0 && in_dim <= 8192 && aligned16(w) &&
                    aligned16(x);
-  if (vec) {
+  if (vec && seq_len == 1) {
+    // rows per wave: 6-8 KiB of weights in flight per wave
+    switch (in_dim / 1024) {
+      case 1: w8a32_rows_kernel<1, 8><<<(unsigned)((out_dim + 31) / 32), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
+      case 2: w8a32_rows_kernel<2, 4><<<(unsigned)((out_dim + 15) / 16), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
+      case 3: w8a32_rows_kernel<3, 2><<<(unsigned)((out_dim + 7) / 8), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
+      case 4: w8a32_rows_kernel<4, 2><<<(unsigned)((out_dim + 7) / 8), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
+      case 5: w8a32_rows_kernel<5, 1><<<(unsigned)((out_dim + 3) / 4), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
+      case 6: w8a32_rows_kernel<6, 1><<<(unsigned)((out_dim + 3) / 4), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
+      case 7: w8a32_rows_kernel<7, 1><<<(unsigned)((out_dim + 3) / 4), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
+      default: w8a32_rows_kernel<8, 1><<<(unsigned)((out_dim + 3) / 4), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
+    }
+  } else if (vec) {
     switch (in_dim / 1024) {
       case 1: w8a32_vec_kernel<1><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
       case 2: w8a32_vec_kernel<2><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;

@@ -553,7 +553,10 @@ def make_qweight(r, rows, cols):
 
 
 @pytest.mark.parametrize("seq,in_dim,out_dim", [(1, 2048, 12288), (4, 1024, 3072), (3, 2048, 2048),
-                                                (2, 100, 33)])
+                                                (2, 100, 33),
+                                                # one token: R rows per wave, ragged row tails
+                                                (1, 1024, 1001), (1, 3072, 2047), (1, 4096, 33),
+                                                (1, 6144, 2048), (1, 2048, 1)])
 def test_linear_nobias_int8_w8a32(dev, seq, in_dim, out_dim):
     from qwenasr_amd import kernels as K
 
