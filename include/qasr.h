@@ -311,6 +311,7 @@ int qasr_causal_attention_f32(float* out, const float* q, const float* k, const 
  * softmax sums). workspace: 16-byte aligned, at least
  * qasr_causal_attention_workspace_floats(seq_q, n_heads, head_dim) floats for
  * the full split; with less (or NULL) it falls back to fewer or no splits.
+ * Calls that share a workspace must not run concurrently (one stream).
  * No reference counterpart: the reference threads over heads
  * (kernels/mod.rs:1174-1203); this is its single-stream GPU shape. */
 int qasr_causal_attention_split_f32(float* out, const float* q, const float* k, const float* v,

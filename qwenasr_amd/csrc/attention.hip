@@ -202,33 +202,202 @@ __global__ __launch_bounds__(64 * R * S) void causal_attention_kernel(
   }
 }
 
-// Merges the nsplit partials of each (row, head): one wave per (row, head),
-// lanes over head dims; splits with no keys carry sum 0 and max -1e30.
+// Sum over the 4 lanes of a quad (lanes 4a..4a+3), every lane gets it.
+QASR_DEV float quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));  // lane ^ 1
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));  // lane ^ 2
+  return v;
+}
+
+// Merges the nsplit (<= 64) partials of one (row, head) with one wave: lane z
+// reads split z's (max, sum) so the overall max and the rescaled sum are wave
+// reductions; the outputs are then summed with lanes over head dims, 16
+// splits' rows in flight at a time. Splits with no keys carry sum 0 and max
+// -1e30 and drop out. `o` points at the (row, head) output row.
+template <int HD>
+QASR_DEV void merge_splits(float* o, const float* ws_o, const float* ml, int nsplit, int lane) {
+  constexpr int DPL = HD / 64;
+  constexpr int B = 16;
+  const bool has = lane < nsplit;
+  const float mz = has ? ml[2 * lane] : -__builtin_inff();
+  const float lz = has ? ml[2 * lane + 1] : 0.0f;
+  const float mx = wave_max(mz);
+  const float f = has ? expf(mz - mx) : 0.0f;
+  const float lsum = wave_sum(lz * f);
+  float acc[DPL];
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) acc[d] = 0.0f;
+  const float* ob = ws_o + lane * DPL;
+  for (int z0 = 0; z0 < nsplit; z0 += B) {
+    float ov[B][DPL];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const size_t z = (size_t)min(z0 + u, nsplit - 1);
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) ov[u][d] = ob[z * HD + d];
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      if (z0 + u < nsplit) {  // uniform
+        const float fz = bcast_lane(f, z0 + u);
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) acc[d] = __builtin_fmaf(ov[u][d], fz, acc[d]);
+      }
+    }
+  }
+  const float inv = lsum > 0.0f ? 1.0f / lsum : 1.0f;
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) o[lane * DPL + d] = acc[d] * inv;
+}
+
+// Decode-shaped split: one 4-wave workgroup per (row, kv head, key split)
+// walks whole 64-key tiles; wave w owns keys 16w .. 16w+15 of each tile, so
+// every SIMD of the CU has its own loads in flight. Each wave issues all k and
+// v loads of its 16 keys before using any (one memory round trip per tile).
+// QK: a quad of lanes owns a key (lane l covers head dims 32*(l%4) .. +31 of
+// key l/4), so each load instruction reads 16 keys x 64 contiguous bytes and
+// the quad's partial dots meet with two DPP adds. PV: lanes over head dims,
+// probabilities broadcast with readlane. The 4 waves' (max, sum, out) merge in
+// LDS; the workgroup writes its unnormalised partial to the workspace.
+template <int HD, int G>
+__global__ __launch_bounds__(256) void attention_decode_split_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    int seq_q, int seq_k, int nk, float scale, int q_offset, int keys_per_split,
+    float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  constexpr int DPL = HD / 64;
+  constexpr int DQ = HD / 4;   // head dims per lane of a quad
+  constexpr int C4 = DQ / 4;   // float4 loads per key per lane
+  __shared__ float cm[4][G], cl[4][G];
+  __shared__ __align__(16) float co[4][G][HD];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int quarter = lane & 3, kq = lane >> 2;  // dim quarter, key within the wave's 16
+  const int i = blockIdx.x, kh = blockIdx.y;
+  const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
+  float4 qv[G][C4];
+  const float* qr = q + (size_t)i * q_stride + (size_t)kh * G * HD + quarter * DQ;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int c = 0; c < C4; ++c) qv[g][c] = ld4(qr + g * HD, c);
+
+  const int k_lim = min(q_offset + i + 1, seq_k);
+  const int k_begin = min(k_lim, (int)blockIdx.z * keys_per_split);
+  const int k_end = min(k_lim, k_begin + keys_per_split);
+  float m[G], l[G], o[G][DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -1e30f;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o[g][d] = 0.0f;
+  }
+  for (int t0 = k_begin + 16 * wave; t0 < k_end; t0 += 64) {
+    const int nkeys = min(16, k_end - t0);  // this wave's keys in the tile (>= 1)
+    const int j = min(kq, nkeys - 1);       // past them: repeat the last key, masked below
+    const float* kr = k + (size_t)(t0 + j) * kv_stride + (size_t)kh * HD + quarter * DQ;
+    float4 kk[C4];
+#pragma unroll
+    for (int c = 0; c < C4; ++c) kk[c] = ld4(kr, c);
+    const float* vr = v + (size_t)t0 * kv_stride + (size_t)kh * HD + lane * DPL;
+    float vv[16][DPL];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const size_t jj = (size_t)min(u, nkeys - 1);
+      if constexpr (DPL == 2) {
+        const float2 t2 = *reinterpret_cast<const float2*>(vr + jj * kv_stride);
+        vv[u][0] = t2.x;
+        vv[u][1] = t2.y;
+      } else {
+        vv[u][0] = vr[jj * kv_stride];
+      }
+    }
+    // every load issued before the first use (the scheduler would otherwise
+    // sink the v loads below the QK arithmetic: two round trips)
+    __builtin_amdgcn_sched_barrier(0);
+    const bool key_ok = kq < nkeys;
+    float p[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float a = 0.0f;
+#pragma unroll
+      for (int c = 0; c < C4; ++c) {
+        a = __builtin_fmaf(qv[g][c].x, kk[c].x, a);
+        a = __builtin_fmaf(qv[g][c].y, kk[c].y, a);
+        a = __builtin_fmaf(qv[g][c].z, kk[c].z, a);
+        a = __builtin_fmaf(qv[g][c].w, kk[c].w, a);
+      }
+      a = quad_sum(a);
+      const float sc = key_ok ? a * scale : -__builtin_inff();
+      const float mn = fmaxf(m[g], wave_max(sc));
+      const float corr = expf(m[g] - mn);
+      p[g] = key_ok ? expf(sc - mn) : 0.0f;
+      l[g] = l[g] * corr + wave_sum(quarter == 0 ? p[g] : 0.0f);  // one copy of each key per quad
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) o[g][d] *= corr;
+      m[g] = mn;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (u < nkeys) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float pj = bcast_lane(p[g], 4 * u);
+#pragma unroll
+          for (int d = 0; d < DPL; ++d) o[g][d] = __builtin_fmaf(pj, vv[u][d], o[g][d]);
+        }
+      }
+    }
+  }
+  // merge the 4 waves
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      cm[wave][g] = m[g];
+      cl[wave][g] = l[g];
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) co[wave][g][lane * DPL + d] = o[g][d];
+  __syncthreads();
+  const int nsplit = gridDim.z;
+  if (wave == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mx = fmaxf(fmaxf(cm[0][g], cm[1][g]), fmaxf(cm[2][g], cm[3][g]));
+      float lsum = 0.0f, acc[DPL];
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) acc[d] = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = expf(cm[w][g] - mx);
+        lsum = __builtin_fmaf(cl[w][g], f, lsum);
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) acc[d] = __builtin_fmaf(co[w][g][lane * DPL + d], f, acc[d]);
+      }
+      const size_t slot = ((size_t)i * nk * G + (size_t)kh * G + g) * nsplit + blockIdx.z;
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) ws_o[slot * HD + lane * DPL + d] = acc[d];
+      if (lane == 0) {
+        ws_ml[2 * slot] = mx;
+        ws_ml[2 * slot + 1] = lsum;
+      }
+    }
+  }
+}
+
+// Merges the partials of every (row, head), one wave each.
 template <int HD>
 __global__ __launch_bounds__(256) void attention_combine_kernel(float* __restrict__ out,
                                                                 const float* __restrict__ ws_o,
                                                                 const float* __restrict__ ws_ml,
                                                                 long long rows_heads, int nsplit) {
-  constexpr int DPL = HD / 64;
   const int lane = threadIdx.x & 63;
   const long long rh = (long long)blockIdx.x * 4 + threadIdx.x / 64;  // row * n_heads + head
   if (rh >= rows_heads) return;
-  const float* ml = ws_ml + (size_t)rh * nsplit * 2;
-  float mx = ml[0];
-  for (int z = 1; z < nsplit; ++z) mx = fmaxf(mx, ml[2 * z]);
-  float lsum = 0.0f, acc[DPL];
-#pragma unroll
-  for (int d = 0; d < DPL; ++d) acc[d] = 0.0f;
-  for (int z = 0; z < nsplit; ++z) {
-    const float f = expf(ml[2 * z] - mx);
-    lsum = __builtin_fmaf(ml[2 * z + 1], f, lsum);
-    const float* oz = ws_o + ((size_t)rh * nsplit + z) * HD + lane * DPL;
-#pragma unroll
-    for (int d = 0; d < DPL; ++d) acc[d] = __builtin_fmaf(oz[d], f, acc[d]);
-  }
-  const float inv = lsum > 0.0f ? 1.0f / lsum : 1.0f;
-#pragma unroll
-  for (int d = 0; d < DPL; ++d) out[(size_t)rh * HD + lane * DPL + d] = acc[d] * inv;
+  merge_splits<HD>(out + (size_t)rh * HD, ws_o + (size_t)rh * nsplit * HD, ws_ml + (size_t)rh * nsplit * 2,
+                   nsplit, lane);
 }
 
 template <int HD, int G>
@@ -236,8 +405,13 @@ void launch_attention_split(float* out, const float* q, const float* k, const fl
                             int seq_k, int nk, float scale, int q_offset, int nsplit,
                             int keys_per_split, float* ws_o, float* ws_ml, hipStream_t st) {
   const dim3 grid((unsigned)seq_q, (unsigned)nk, (unsigned)nsplit);
-  causal_attention_kernel<HD, G, 1, 1, true><<<grid, 64, 0, st>>>(
-      out, q, k, v, seq_q, seq_k, nk, scale, q_offset, keys_per_split, ws_o, ws_ml);
+  if constexpr (G * HD <= 256) {  // the wave's loads fit the register file
+    attention_decode_split_kernel<HD, G><<<grid, 256, 0, st>>>(q, k, v, seq_q, seq_k, nk, scale,
+                                                              q_offset, keys_per_split, ws_o, ws_ml);
+  } else {
+    causal_attention_kernel<HD, G, 1, 1, true><<<grid, 64, 0, st>>>(
+        out, q, k, v, seq_q, seq_k, nk, scale, q_offset, keys_per_split, ws_o, ws_ml);
+  }
   const long long rows_heads = (long long)seq_q * nk * G;
   attention_combine_kernel<HD><<<(unsigned)((rows_heads + 3) / 4), 256, 0, st>>>(out, ws_o, ws_ml,
                                                                                rows_heads, nsplit);
@@ -285,9 +459,13 @@ bool dispatch_group(int G, float* out, const float* q, const float* k, const flo
 #undef QASR_ATTN_CASE
 }
 
-// Key-split plan: one-wave workgroups of whole 64-key tiles, aiming at about
-// 4 waves per CU (1024 workgroups), at most kMaxSplits splits; nothing to
-// gain when there are already many (row, kv head) pairs or few keys.
+// Key-split plan: workgroups of whole 64-key tiles, aiming at about 1024
+// workgroups, at most kMaxSplits splits; nothing to gain when there are
+// already many (row, kv head) pairs or few keys. Workspace layout: the
+// partial outputs [seq_q][n_heads][nsplit][head_dim], then the (max, sum)
+// pairs [seq_q][n_heads][nsplit][2]. (Merging in the last-finishing
+// workgroup instead of a second kernel needs an agent-scope fence per
+// workgroup -- a whole-L2 writeback and invalidate -- and measured 2x slower.)
 constexpr int kMaxSplits = 64;
 
 SplitPlan plan_split(size_t seq_q, size_t seq_k, size_t nk, size_t q_offset, size_t head_dim,
@@ -307,7 +485,7 @@ SplitPlan plan_split(size_t seq_q, size_t seq_k, size_t nk, size_t q_offset, siz
   p.keys_per_split = (int)(((k_max + want - 1) / want + 63) / 64 * 64);
   p.nsplit = (int)((k_max + p.keys_per_split - 1) / p.keys_per_split);
   p.ws_o = workspace;
-  p.ws_ml = workspace + seq_q * n_heads * (size_t)p.nsplit * head_dim;
+  p.ws_ml = p.ws_o + seq_q * n_heads * (size_t)p.nsplit * head_dim;
   return p;
 }
 

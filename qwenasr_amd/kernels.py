@@ -204,7 +204,8 @@ def causal_attention(out, q, k, v, seq_q: int, seq_k: int, n_heads: int, n_kv_he
 
 
 def attention_workspace(seq_q: int, n_heads: int, head_dim: int, device="cuda") -> torch.Tensor:
-    """Workspace for causal_attention_split (allocate once, reuse per call)."""
+    """Workspace for causal_attention_split: allocate once, reuse per call on
+    one stream."""
     n = _lib.lib().qasr_causal_attention_workspace_floats(seq_q, n_heads, head_dim)
     return torch.empty(n, dtype=F32, device=device)
 

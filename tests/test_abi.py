@@ -158,5 +158,6 @@ def test_cpp_mirror_binary_links_the_static_archive():
 
 
 def test_attention_workspace_size_query():
-    # seq_q * n_heads * 64 splits * (head_dim + 2) floats
+    # seq_q * n_heads * 64 splits * (head_dim + 2)
     assert _lib.lib().qasr_causal_attention_workspace_floats(1, 16, 128) == 16 * 64 * 130
+    assert _lib.lib().qasr_causal_attention_workspace_floats(3, 2, 64) == 6 * 64 * 66

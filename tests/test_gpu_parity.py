@@ -887,3 +887,27 @@ def test_causal_attention_split(dev, name, seq_q, seq_k, nq, nk, hd, q_offset):
     K.causal_attention_split(out2, dev_t(q, dev), dev_t(k, dev), dev_t(v, dev), seq_q, seq_k, nq, nk,
                              hd, hd ** -0.5, q_offset, ws[:100])
     assert_close(host(out2), ref, RTOL, ATOL, name + " fallback")
+
+
+def test_causal_attention_split_repeated_calls_share_the_workspace(dev):
+    """64 calls in a row on one workspace, with alternating inputs, each equal
+    to the oracle."""
+    from qwenasr_amd import kernels as K
+
+    nq, nk, hd, seq_k = 16, 8, 128, 2048
+    r = rng(53)
+    cases = []
+    for c in range(2):
+        q = normal(r, nq * hd)
+        k = normal(r, seq_k * nk * hd)
+        v = normal(r, seq_k * nk * hd)
+        pos = seq_k - 1 - 517 * c
+        ref = oracle.causal_attention(q, k, v, 1, seq_k, nq, nk, hd, hd ** -0.5, pos)
+        cases.append((dev_t(q, dev), dev_t(k, dev), dev_t(v, dev), pos, ref))
+    ws = K.attention_workspace(1, nq, hd, dev)
+    outs = [torch.empty(nq * hd, device=dev) for _ in range(64)]
+    for it in range(64):
+        q, k, v, pos, _ = cases[it % 2]
+        K.causal_attention_split(outs[it], q, k, v, 1, seq_k, nq, nk, hd, hd ** -0.5, pos, ws)
+    for it in range(64):
+        assert_close(host(outs[it]), cases[it % 2][4], RTOL, ATOL, f"call {it}")
