@@ -452,10 +452,12 @@ class LmHead(Workload):
         self.x = [self.randn(H) for _ in range(C)]
         self.logits = [torch.empty(V, device=dev) for _ in range(C)]
         self.idx = [torch.empty(1, dtype=torch.int32, device=dev) for _ in range(C)]
-        nbytes = V * H + V * F + H * F + 2 * V * F + 4
+        # weights, scales, x, the logits written once, the token index
+        nbytes = V * H + V * F + H * F + V * F + 4
+        self.ws = K.lm_head_workspace(V, dev)
         self.kernels = {"lm_head_int8_argmax": (
             lambda i: K.lm_head_int8_argmax(self.idx[i % C], self.logits[i % C], self.x[i % C],
-                                            self.w[i % C], 1, H, V), nbytes)}
+                                            self.w[i % C], 1, H, V, self.ws), nbytes)}
         self.step_bytes = nbytes
         self.tokens_per_step = 1.0
 
@@ -689,7 +691,7 @@ def profile_kernel(torch, wl, name: str, n: int) -> int:
         print(f"bench.py: workload {wl.name} has no kernel {name!r} (has {sorted(wl.kernels)})",
               file=sys.stderr)
         return 2
-    launch, nbytes = wl.kernels[name]
+    launch, nbytes = wl.kernels[name][0], wl.kernels[name][1]
     for i in range(n):
         launch(i)
     torch.cuda.synchronize()

@@ -336,11 +336,71 @@ int qasr_argmax_rows_f32(int32_t* idx, const float* x, size_t rows, size_t cols,
 /* INT8 lm_head + argmax for `rows` hidden states: logits[r, :] =
  * linear_nobias_int8(x[r, :]) (qasr_linear_nobias_int8_f32 arithmetic, the
  * reference's kernels::linear_nobias_int8 call at decoder.rs:939 and 954),
- * then idx[r] = qasr_argmax_rows_f32(logits[r, :]). logits is caller-owned
- * [rows, vocab] and keeps the logits. */
+ * then idx[r] = the qasr_argmax_rows_f32 index of logits[r, :]. logits is
+ * caller-owned [rows, vocab] and keeps the logits.
+ *
+ * workspace (8-byte aligned, may be NULL): with rows == 1 and at least
+ * qasr_lm_head_argmax_workspace_bytes(vocab) bytes, the matvec reduces its
+ * rows to per-workgroup candidates there and one small kernel merges them
+ * (no second pass over the logits). Without it, or for rows > 1, the logits
+ * are scanned after the matvec. Same idx either way. Calls that share a
+ * workspace must be ordered on one stream. */
 int qasr_lm_head_int8_argmax_f32(int32_t* idx, float* logits, const float* x,
                                  const int8_t* w, const float* scales, size_t rows,
-                                 size_t in_dim, size_t vocab, void* stream);
+                                 size_t in_dim, size_t vocab, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* Workspace bytes qasr_lm_head_int8_argmax_f32 can use for this vocab. */
+size_t qasr_lm_head_argmax_workspace_bytes(size_t vocab);
+
+/* ------------------------------------------------------------------------ */
+/* .qint8 weight files (quantize.rs:1-34, QuantFile quantize.rs:114-300)     */
+/* ------------------------------------------------------------------------ */
+
+/* Tensor dtypes of a .qint8 file (the V2 dtype byte; V1 infers them). */
+enum { QASR_QINT8_INT8 = 0, QASR_QINT8_F32 = 1, QASR_QINT8_BF16 = 2 };
+
+typedef struct qasr_qint8_file qasr_qint8_file;
+
+/* Maps `path` read-only and parses its tensor table as QuantFile::open does
+ * (quantize.rs:122-245): V1 or V2 magic, V1 dtype from scale_offset, unknown
+ * V2 dtype as INT8, a table cut short by the end of the file ends there.
+ * Host-side setup call (no device work). */
+int qasr_qint8_open(const char* path, qasr_qint8_file** out);
+/* Unmaps the file. If any upload was queued from it, first waits for the
+ * device (copies from the mapping may still be in flight). NULL is a no-op. */
+int qasr_qint8_close(qasr_qint8_file* f);
+
+/* Format version (1 or 2) and number of tensors parsed. */
+int qasr_qint8_info(const qasr_qint8_file* f, int* version, size_t* n_tensors);
+
+/* Index of the tensor named `name` (QuantFile::find, quantize.rs:247-249). */
+int qasr_qint8_find(const qasr_qint8_file* f, const char* name, size_t* index);
+
+/* Table entry of tensor `index`: name (not NUL-terminated; valid until close),
+ * dtype, shape (shape_cap entries available), offsets into the data section.
+ * Any output pointer may be NULL. */
+int qasr_qint8_tensor(const qasr_qint8_file* f, size_t index, const char** name,
+                      size_t* name_len, int* dtype, size_t* n_dims, uint64_t* shape,
+                      size_t shape_cap, uint64_t* data_offset, uint64_t* scale_offset);
+
+/* Copies tensor `index` to device memory: its data (numel bytes for INT8,
+ * 4*numel for F32, 2*numel for BF16) to dev_data and, for INT8, its shape[0]
+ * row scales to dev_scales (the mapping of QuantFile::get_quant_weight,
+ * quantize.rs:252-268). Fails if the tensor extends past the file. Load-time
+ * call: the copy is from pageable memory and may not be asynchronous. */
+int qasr_qint8_upload(const qasr_qint8_file* f, size_t index, void* dev_data,
+                      float* dev_scales, void* stream);
+
+/* Uploads INT8 gate [inter, hidden] and up [inter, hidden] as the fused
+ * row-interleaved matrix dev_w [2*inter, hidden] (g0, u0, g1, u1, ...) with
+ * interleaved scales dev_scales [2*inter], directly by strided copies: the
+ * fusion DecoderInt8::load does on the host (decoder.rs:697-719), which takes
+ * inter and hidden from the model config. Both tensors must be INT8 and
+ * exactly [inter, hidden]; the reference does not check this. */
+int qasr_qint8_upload_gate_up(const qasr_qint8_file* f, const char* gate_name,
+                              const char* up_name, size_t inter, size_t hidden,
+                              int8_t* dev_w, float* dev_scales, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

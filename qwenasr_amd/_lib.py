@@ -50,7 +50,7 @@ SIGNATURES: dict[str, list] = {
     "qasr_argmax_rows_f32": [P, P, Z, Z, P],
     "qasr_causal_attention_f32": [P, P, P, P, Z, Z, Z, Z, Z, F, Z, P],
     "qasr_causal_attention_split_f32": [P, P, P, P, Z, Z, Z, Z, Z, F, Z, P, Z, P],
-    "qasr_lm_head_int8_argmax_f32": [P, P, P, P, P, Z, Z, Z, P],
+    "qasr_lm_head_int8_argmax_f32": [P, P, P, P, P, Z, Z, Z, P, Z, P],
     "qasr_head_rms_norm_rope_kv_f32": [P, P, P, P, P, P, P, P, Z, Z, Z, Z, Z, Z, F, P, P, Z, P],
     "qasr_rope_table_fill_f32": [P, P, Z, Z, Z, F, P],
     "qasr_swiglu_multiply_f32": [P, P, Z, Z, P],
@@ -71,11 +71,20 @@ SIGNATURES: dict[str, list] = {
     "qasr_gate_up_swiglu_w8a8_f32in": [P, P, P, P, Z, Z, P],
     "qasr_pack_w8a8_tiles": [P, P, Z, Z, P],
     "qasr_gate_up_swiglu_w8a8_packed": [P, P, P, P, P, Z, Z, Z, P],
+    # .qint8 files: host-side handle calls (out-parameters are host pointers)
+    "qasr_qint8_open": [c_char_p, P],
+    "qasr_qint8_close": [P],
+    "qasr_qint8_info": [P, P, P],
+    "qasr_qint8_find": [P, c_char_p, P],
+    "qasr_qint8_tensor": [P, Z, P, P, P, P, P, Z, P, P],
+    "qasr_qint8_upload": [P, Z, P, P, P],
+    "qasr_qint8_upload_gate_up": [P, c_char_p, c_char_p, Z, Z, P, P, P],
 }
 
 # entry points that return a size instead of a status
 SIZE_QUERIES = {
     "qasr_causal_attention_workspace_floats": [ctypes.c_size_t] * 3,
+    "qasr_lm_head_argmax_workspace_bytes": [ctypes.c_size_t],
 }
 
 _LIB = None

@@ -189,6 +189,28 @@ inline bool mul_ok(size_t a, size_t b, size_t* out) {
   return true;
 }
 
+// Argmax order of the reference's lm_head scan (decoder.rs:941-949): a larger
+// value wins, equal values go to the lower index, a NaN never wins.
+QASR_DEV bool argmax_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+QASR_DEV void argmax_consider(float v, int i, float& bv, int& bi) {
+  if (v == v && argmax_better(v, i, bv, bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+// Logits of one token through the W8A32 decode kernel, which also writes one
+// (best value, index bits) pair per workgroup to `part` (int8.hip). Returns
+// false, launching nothing, when the shape has no such kernel; *n_part is the
+// number of pairs written.
+bool launch_w8a32_argmax_partials(float* y, const float* x, const int8_t* w, const float* scales,
+                                  size_t in_dim, size_t out_dim, float2* part, size_t part_cap,
+                                  hipStream_t st, unsigned* n_part);
+// Most pairs any shape writes: one per 4 output rows.
+inline size_t lm_head_partials_max(size_t vocab) { return (vocab + 3) / 4; }
+
 }  // namespace qasr
 
 #define QASR_REQUIRE(cond, msg)                                   \

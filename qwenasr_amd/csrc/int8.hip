@@ -7,6 +7,8 @@
 // 2*in_dim contiguous bytes and its SwiGLU output needs no cross-wave exchange.
 #include "common.hpp"
 
+#include <climits>
+
 #include "gemm_w8a8.hpp"
 
 namespace qasr {
@@ -115,13 +117,20 @@ __global__ __launch_bounds__(256) void w8a32_vec_kernel(float* y, const float* x
 // Decode shape (one token): each wave owns R consecutive output rows, issues
 // all R x KCH weight loads before the first FMA (so R KiB per chunk are in
 // flight per wave instead of one), and keeps x in registers across its rows.
-template <int KCH, int R>
+// With PART, the workgroup also reduces its rows' results to the best
+// (value, index) in the lm_head argmax order and writes it to part[blockIdx.x];
+// waves past the last row then stay to the end (their loads clamp to the last
+// row and they offer no candidate).
+template <int KCH, int R, bool PART = false>
 __global__ __launch_bounds__(256) void w8a32_rows_kernel(float* y, const float* x, const int8_t* w,
                                                          const float* scales, const float* bias,
-                                                         int in_dim, int out_dim) {
+                                                         int in_dim, int out_dim,
+                                                         float2* part = nullptr) {
   const int lane = threadIdx.x & (kWave - 1);
   const int o0 = (blockIdx.x * (256 / kWave) + threadIdx.x / kWave) * R;
-  if (o0 >= out_dim) return;
+  if constexpr (!PART) {
+    if (o0 >= out_dim) return;
+  }
   v4i wv[R][KCH];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -153,15 +162,47 @@ __global__ __launch_bounds__(256) void w8a32_rows_kernel(float* y, const float* 
     }
     acc[r] = wave_sum(a);
   }
-  if (lane < R && o0 + lane < out_dim) {
+  const bool mine = lane < R && o0 + lane < out_dim;
+  float res = 0.0f;
+  if (mine) {
     float a = acc[0];
 #pragma unroll
     for (int r = 1; r < R; ++r)
       if (lane == r) a = acc[r];
     const int o = o0 + lane;
-    float res = a * scales[o];
+    res = a * scales[o];
     if (bias) res += bias[o];
     y[o] = res;
+  }
+  if constexpr (PART) {
+    __shared__ float sv[256 / kWave];
+    __shared__ int si[256 / kWave];
+    float bv = -__builtin_inff();
+    int bi = INT_MAX;
+    if (mine) argmax_consider(res, o0 + lane, bv, bi);
+#pragma unroll
+    for (int m = R / 2; m >= 1; m >>= 1) {  // candidates sit in lanes 0..R-1
+      const float ov = __shfl_xor(bv, m, kWave);
+      const int oi = __shfl_xor(bi, m, kWave);
+      if (argmax_better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      sv[threadIdx.x / kWave] = bv;
+      si[threadIdx.x / kWave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int k = 1; k < 256 / kWave; ++k)
+        if (argmax_better(sv[k], si[k], bv, bi)) {
+          bv = sv[k];
+          bi = si[k];
+        }
+      part[blockIdx.x] = make_float2(bv, __int_as_float(bi));
+    }
   }
 }
 
@@ -432,6 +473,34 @@ static int launch_w8a32(float* y, const float* x, const int8_t* w, const float* 
   }
   return launch_status("linear_int8");
 }
+
+namespace qasr {
+bool launch_w8a32_argmax_partials(float* y, const float* x, const int8_t* w, const float* scales,
+                                  size_t in_dim, size_t out_dim, float2* part, size_t part_cap,
+                                  hipStream_t st, unsigned* n_part) {
+  if (!(in_dim >= 1024 && in_dim % 1024 == 0 && in_dim <= 8192 && aligned16(w) && aligned16(x)))
+    return false;
+  if (out_dim == 0 || out_dim > 0x7fffffffu - 64) return false;
+  const int kc = (int)(in_dim / 1024);
+  const int rows_per_wg = 4 * (kc == 1 ? 8 : kc == 2 ? 4 : kc <= 4 ? 2 : 1);
+  const size_t grid = (out_dim + rows_per_wg - 1) / rows_per_wg;
+  if (grid > part_cap) return false;
+  const int k = (int)in_dim, o = (int)out_dim;
+  const unsigned g = (unsigned)grid;
+  switch (kc) {
+    case 1: w8a32_rows_kernel<1, 8, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
+    case 2: w8a32_rows_kernel<2, 4, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
+    case 3: w8a32_rows_kernel<3, 2, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
+    case 4: w8a32_rows_kernel<4, 2, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
+    case 5: w8a32_rows_kernel<5, 1, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
+    case 6: w8a32_rows_kernel<6, 1, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
+    case 7: w8a32_rows_kernel<7, 1, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
+    default: w8a32_rows_kernel<8, 1, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
+  }
+  *n_part = g;
+  return true;
+}
+}  // namespace qasr
 
 extern "C" int qasr_linear_nobias_int8_f32(float* y, const float* x, const int8_t* w,
                                            const float* scales, size_t seq_len, size_t in_dim,

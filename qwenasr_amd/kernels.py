@@ -232,15 +232,24 @@ def argmax_rows(idx, x, rows: int, cols: int) -> None:
     _lib.call("qasr_argmax_rows_f32", _ptr(idx), _ptr(x), rows, cols, _stream())
 
 
-def lm_head_int8_argmax(idx, logits, x, w: QuantWeight, rows: int, in_dim: int, vocab: int) -> None:
-    """INT8 lm_head logits + greedy argmax (decoder.rs:935-963)."""
+def lm_head_workspace(vocab: int, device="cuda") -> torch.Tensor:
+    """Workspace for the one-token lm_head argmax (bytes as a uint8 tensor)."""
+    n = _lib.lib().qasr_lm_head_argmax_workspace_bytes(vocab)
+    return torch.empty(max(n, 8), dtype=torch.uint8, device=device)
+
+
+def lm_head_int8_argmax(idx, logits, x, w: QuantWeight, rows: int, in_dim: int, vocab: int,
+                        workspace: torch.Tensor | None = None) -> None:
+    """INT8 lm_head logits + greedy argmax (decoder.rs:935-963). With a
+    ``lm_head_workspace`` and one row the argmax is reduced inside the matvec."""
     _need(idx, I32, rows, "idx")
     _need(logits, F32, rows * vocab, "logits")
     _need(x, F32, rows * in_dim, "x")
     _need(w.data, I8, vocab * in_dim, "w")
     _need(w.scales, F32, vocab, "scales")
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _lib.call("qasr_lm_head_int8_argmax_f32", _ptr(idx), _ptr(logits), _ptr(x), _ptr(w.data),
-              _ptr(w.scales), rows, in_dim, vocab, _stream())
+              _ptr(w.scales), rows, in_dim, vocab, _ptr(workspace), ws_bytes, _stream())
 
 
 class KvCache:

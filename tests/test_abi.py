@@ -161,3 +161,10 @@ def test_attention_workspace_size_query():
     # seq_q * n_heads * 64 splits * (head_dim + 2)
     assert _lib.lib().qasr_causal_attention_workspace_floats(1, 16, 128) == 16 * 64 * 130
     assert _lib.lib().qasr_causal_attention_workspace_floats(3, 2, 64) == 6 * 64 * 66
+
+
+def test_lm_head_workspace_size_query():
+    # one (value, index) pair of 8 bytes per 4 logits at most
+    assert _lib.lib().qasr_lm_head_argmax_workspace_bytes(151936) == 8 * 37984
+    assert _lib.lib().qasr_lm_head_argmax_workspace_bytes(5) == 16
+    assert _lib.lib().qasr_lm_head_argmax_workspace_bytes(0) == 0

@@ -782,12 +782,15 @@ def test_argmax_rows_matches_the_reference_loop(dev):
         np.testing.assert_array_equal(host(idx), ref)
 
 
-@pytest.mark.parametrize("rows,in_dim,vocab", [(1, 1024, 151936), (3, 2048, 5000)])
-def test_lm_head_int8_argmax(dev, rows, in_dim, vocab):
+@pytest.mark.parametrize("rows,in_dim,vocab,use_ws", [
+    (1, 1024, 151936, True), (1, 1024, 151936, False), (3, 2048, 5000, True),
+    (1, 2048, 5001, True), (1, 3072, 4099, True), (1, 6144, 997, True), (1, 1000, 300, True)])
+def test_lm_head_int8_argmax(dev, rows, in_dim, vocab, use_ws):
     """Logits within the W8A32 tolerance of the oracle; the token index equals
     the reference loop's on the oracle logits whenever the top two logits are
     further apart than twice the tolerance (checked), and always equals the
-    argmax of the returned logits."""
+    argmax of the returned logits. ``use_ws``: with the workspace (one row: argmax
+    reduced inside the matvec) or without (logits scanned afterwards)."""
     from qwenasr_amd import kernels as K
 
     r = rng(41, rows, vocab)
@@ -798,7 +801,8 @@ def test_lm_head_int8_argmax(dev, rows, in_dim, vocab):
     idx = torch.empty(rows, dtype=torch.int32, device=dev)
     logits = torch.empty(rows * vocab, device=dev)
     w = K.QuantWeight(dev_t(wq, dev), dev_t(ws, dev), vocab, in_dim)
-    K.lm_head_int8_argmax(idx, logits, dev_t(x, dev), w, rows, in_dim, vocab)
+    wsp = K.lm_head_workspace(vocab, dev) if use_ws else None
+    K.lm_head_int8_argmax(idx, logits, dev_t(x, dev), w, rows, in_dim, vocab, wsp)
     lg = host(logits)
     assert_close(lg, ref_logits, RTOL, ATOL, "logits")
     np.testing.assert_array_equal(host(idx), oracle.argmax_rows(lg, rows, vocab))
@@ -806,6 +810,59 @@ def test_lm_head_int8_argmax(dev, rows, in_dim, vocab):
     clear = (top2[:, 1] - top2[:, 0]) > 2 * (ATOL + RTOL * np.abs(top2[:, 1]))
     assert clear.any()
     np.testing.assert_array_equal(host(idx)[clear], ref_idx[clear])
+
+
+@pytest.mark.parametrize("in_dim,vocab", [(1024, 151936), (2048, 5003), (5120, 999)])
+def test_lm_head_fused_argmax_ties_nan_and_tails(dev, in_dim, vocab):
+    """The in-matvec reduction keeps the reference loop's order across
+    workgroups: equal maxima in rows far apart go to the lower index, a NaN
+    logit never wins, a NaN logit at index 0 gives 0, a -inf-only candidate set
+    still has an index; the last partial workgroup counts."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(42, in_dim, vocab)
+    wq = r.integers(-3, 4, size=(vocab, in_dim), dtype=np.int8)
+    ws = np.full(vocab, 1e-3, np.float32)
+    x = np.ones(in_dim, np.float32)
+    idx = torch.empty(1, dtype=torch.int32, device=dev)
+    logits = torch.empty(vocab, device=dev)
+    wsp = K.lm_head_workspace(vocab, dev)
+
+    def run(wq, ws):
+        w = K.QuantWeight(dev_t(wq, dev), dev_t(ws, dev), vocab, in_dim)
+        K.lm_head_int8_argmax(idx, logits, dev_t(x, dev), w, 1, in_dim, vocab, wsp)
+        lg = host(logits)
+        return int(host(idx)[0]), lg
+
+    top = [vocab // 2 + 1, 7, vocab - 1]
+    w2 = wq.copy()
+    for t in top:
+        w2[t, :] = 127                                    # identical maxima
+    w2s = ws.copy()
+    w2s[top] = 1.0
+    got, lg = run(w2, w2s)
+    assert got == 7 == int(oracle.argmax_rows(lg, 1, vocab)[0])
+    w2s[7] = np.nan                                       # NaN never wins
+    got, lg = run(w2, w2s)
+    assert np.isnan(lg[7]) and got == min(top[0], top[2]) == int(oracle.argmax_rows(lg, 1, vocab)[0])
+    w3s = ws.copy()
+    w3s[vocab - 1] = 1.0                                  # the max in the last (partial) workgroup
+    w3 = wq.copy()
+    w3[vocab - 1, :] = 127
+    got, lg = run(w3, w3s)
+    assert got == vocab - 1
+    w3s[0] = np.nan                                       # NaN at index 0: result 0
+    got, lg = run(w3, w3s)
+    assert got == 0 == int(oracle.argmax_rows(lg, 1, vocab)[0])
+    w4s = np.full(vocab, -np.inf, np.float32)             # -inf and NaN, one finite logit
+    w4 = np.ones_like(wq)
+    w4s[1: vocab // 3] = np.nan
+    w4s[vocab - 2] = -1.0
+    got, lg = run(w4, w4s)
+    assert np.isneginf(lg[0]) and got == vocab - 2 == int(oracle.argmax_rows(lg, 1, vocab)[0])
+    w4s[vocab - 2] = -np.inf                              # all -inf or NaN: the first -inf
+    got, lg = run(w4, w4s)
+    assert got == 0 == int(oracle.argmax_rows(lg, 1, vocab)[0])
 
 
 # ---------------------------------------------------------------------------
