@@ -17,8 +17,10 @@
 #include <cstddef>
 #include <cstdint>
 #include <stdexcept>
+#include <optional>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "../qasr.h"
 
@@ -404,6 +406,145 @@ inline void gate_up_swiglu_w8a8(F out, DevSlice<const int8_t> w_gate_up, CF scal
                                          batch, in_dim, intermediate, detail::st()),
                 "gate_up_swiglu_w8a8");
 }
+
+// ---- attention (kernels/mod.rs:1124-1207) ---------------------------------------------
+inline size_t attention_workspace_floats(size_t seq_q, size_t n_heads, size_t head_dim) {
+  return qasr_causal_attention_workspace_floats(seq_q, n_heads, head_dim);
+}
+
+// kernels::causal_attention: q [seq_q, n_heads*hd], k/v [seq_k, n_kv_heads*hd] (a KvCache
+// layer block), out [seq_q, n_heads*hd]; query i sees keys 0..=q_offset+i.
+inline void causal_attention(F out, CF q, CF k, CF v, size_t seq_q, size_t seq_k, size_t n_heads,
+                             size_t n_kv_heads, size_t head_dim, float scale, size_t q_offset) {
+  detail::need(out, seq_q * n_heads * head_dim, "out");
+  detail::need(q, seq_q * n_heads * head_dim, "q");
+  detail::need(k, seq_k * n_kv_heads * head_dim, "k");
+  detail::need(v, seq_k * n_kv_heads * head_dim, "v");
+  detail::check(qasr_causal_attention_f32(out.ptr, q.ptr, k.ptr, v.ptr, seq_q, seq_k, n_heads,
+                                          n_kv_heads, head_dim, scale, q_offset, detail::st()),
+                "causal_attention");
+}
+
+// Same result with the keys split over workgroups (decode); workspace of
+// attention_workspace_floats(seq_q, n_heads, head_dim) floats, reused across calls.
+inline void causal_attention(F out, CF q, CF k, CF v, size_t seq_q, size_t seq_k, size_t n_heads,
+                             size_t n_kv_heads, size_t head_dim, float scale, size_t q_offset,
+                             F workspace) {
+  detail::need(out, seq_q * n_heads * head_dim, "out");
+  detail::need(q, seq_q * n_heads * head_dim, "q");
+  detail::need(k, seq_k * n_kv_heads * head_dim, "k");
+  detail::need(v, seq_k * n_kv_heads * head_dim, "v");
+  detail::check(qasr_causal_attention_split_f32(out.ptr, q.ptr, k.ptr, v.ptr, seq_q, seq_k, n_heads,
+                                                n_kv_heads, head_dim, scale, q_offset,
+                                                workspace.ptr, workspace.len, detail::st()),
+                "causal_attention");
+}
+
+// ---- lm_head (decoder.rs:929-963) ---------------------------------------------------
+inline void argmax_rows(DevSlice<int32_t> idx, CF x, size_t rows, size_t cols) {
+  detail::need(idx, rows, "idx");
+  detail::need(x, rows * cols, "x");
+  detail::check(qasr_argmax_rows_f32(idx.ptr, x.ptr, rows, cols, detail::st()), "argmax_rows");
+}
+
+inline size_t lm_head_workspace_bytes(size_t vocab) {
+  return qasr_lm_head_argmax_workspace_bytes(vocab);
+}
+
+inline void lm_head_int8_argmax(DevSlice<int32_t> idx, F logits, CF x, DevSlice<const int8_t> w,
+                                CF scales, size_t rows, size_t in_dim, size_t vocab,
+                                DevSlice<uint8_t> workspace = {}) {
+  detail::need(idx, rows, "idx");
+  detail::need(logits, rows * vocab, "logits");
+  detail::need(x, rows * in_dim, "x");
+  detail::need(w, vocab * in_dim, "w");
+  detail::need(scales, vocab, "scales");
+  detail::check(qasr_lm_head_int8_argmax_f32(idx.ptr, logits.ptr, x.ptr, w.ptr, scales.ptr, rows,
+                                             in_dim, vocab, workspace.ptr, workspace.len,
+                                             detail::st()),
+                "lm_head_int8_argmax");
+}
+
+// ---- .qint8 files (QuantFile, quantize.rs:108-330) ----------------------------------------
+struct QuantTensorMeta {
+  std::string name;
+  int dtype = QASR_QINT8_INT8;
+  std::vector<uint64_t> shape;
+  uint64_t data_offset = 0, scale_offset = 0;
+  size_t numel() const {
+    size_t n = 1;
+    for (uint64_t d : shape) n *= (size_t)d;
+    return n;
+  }
+  size_t out_dim() const { return shape.empty() ? 0 : (size_t)shape[0]; }
+  size_t in_dim() const { return shape.size() < 2 ? 0 : numel() / out_dim(); }
+};
+
+class QuantFile {
+ public:
+  // QuantFile::open: empty for a missing or malformed file.
+  static std::optional<QuantFile> open(const std::string& path) {
+    qasr_qint8_file* h = nullptr;
+    if (qasr_qint8_open(path.c_str(), &h) != QASR_OK) return std::nullopt;
+    return QuantFile(h);
+  }
+  QuantFile(QuantFile&& o) noexcept : h_(o.h_), tensors_(std::move(o.tensors_)) { o.h_ = nullptr; }
+  QuantFile(const QuantFile&) = delete;
+  QuantFile& operator=(const QuantFile&) = delete;
+  ~QuantFile() { qasr_qint8_close(h_); }
+
+  int version() const {
+    int v = 0;
+    detail::check(qasr_qint8_info(h_, &v, nullptr), "qint8_info");
+    return v;
+  }
+  const std::vector<QuantTensorMeta>& tensors() const { return tensors_; }
+  const QuantTensorMeta* find(const std::string& name) const {
+    size_t i = 0;
+    if (qasr_qint8_find(h_, name.c_str(), &i) != QASR_OK) return nullptr;
+    return &tensors_[i];
+  }
+  // Copies a tensor's data (and INT8 row scales) to device memory.
+  void upload(const std::string& name, void* data, size_t data_bytes, F scales = {}) const {
+    const QuantTensorMeta* m = find(name);
+    if (!m) throw Panic("qint8_upload: no tensor " + name);
+    const size_t es = m->dtype == QASR_QINT8_F32 ? 4 : m->dtype == QASR_QINT8_BF16 ? 2 : 1;
+    if (data_bytes < m->numel() * es) throw Panic("qint8_upload: data slice too short for " + name);
+    if (m->dtype == QASR_QINT8_INT8) detail::need(scales, m->out_dim(), "scales");
+    size_t i = 0;
+    detail::check(qasr_qint8_find(h_, name.c_str(), &i), "qint8_find");
+    detail::check(qasr_qint8_upload(h_, i, data, scales.ptr, detail::st()), "qint8_upload");
+  }
+  // DecoderInt8::load's fused gate/up (decoder.rs:697-719), built by the copy itself.
+  void upload_gate_up(const std::string& gate, const std::string& up, size_t inter, size_t hidden,
+                      DevSlice<int8_t> w, F scales) const {
+    detail::need(w, 2 * inter * hidden, "w");
+    detail::need(scales, 2 * inter, "scales");
+    detail::check(qasr_qint8_upload_gate_up(h_, gate.c_str(), up.c_str(), inter, hidden, w.ptr,
+                                            scales.ptr, detail::st()),
+                  "qint8_upload_gate_up");
+  }
+
+ private:
+  explicit QuantFile(qasr_qint8_file* h) : h_(h) {
+    size_t n = 0;
+    detail::check(qasr_qint8_info(h_, nullptr, &n), "qint8_info");
+    for (size_t i = 0; i < n; ++i) {
+      QuantTensorMeta m;
+      const char* name = nullptr;
+      size_t name_len = 0, n_dims = 0;
+      uint64_t shape[256];
+      detail::check(qasr_qint8_tensor(h_, i, &name, &name_len, &m.dtype, &n_dims, shape, 256,
+                                      &m.data_offset, &m.scale_offset),
+                    "qint8_tensor");
+      m.name.assign(name, name_len);
+      m.shape.assign(shape, shape + n_dims);
+      tensors_.push_back(std::move(m));
+    }
+  }
+  qasr_qint8_file* h_ = nullptr;
+  std::vector<QuantTensorMeta> tensors_;
+};
 
 }  // namespace kernels
 }  // namespace qwen_asr

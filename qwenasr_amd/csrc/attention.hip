@@ -417,9 +417,217 @@ void launch_attention_split(float* out, const float* q, const float* k, const fl
                                                                                rows_heads, nsplit);
 }
 
+// Prefill attention on the fp32 matrix cores (v_mfma_f32_16x16x4f32), for
+// head_dim 128 and 1 or 2 q heads per kv head. Products and sums stay fp32;
+// only the order of the terms of each dot product and of the key sum differ
+// from the reference's sequential loops.
+//
+// A workgroup takes 16 query rows x the G heads of one kv head with 8 waves:
+// group z (waves 4z..4z+3) walks the 64-key tiles z, z+2, ... of the rows'
+// causal range, and the two groups' (max, sum, out) are merged at the end.
+// Within a group, wave w owns keys 16w..16w+15 of a tile in the QK product and
+// head dims 32w..32w+31 in the PV product.
+//   QK, as S^T = K Q^T: A[i][k] (lane i+16k) = K[key i][dim 32k+s] and
+//     B[k][j] (lane j+16k) = Q[query j][dim 32k+s] at step s = 0..31, so each
+//     lane reads 32 contiguous floats of its key and of its query. The result
+//     sits at lane j+16c, register r = S[query j][key 16w+4c+r].
+//   softmax per query row over the tile: the wave's max/sum over its 16 keys
+//     (registers, then lanes j, j+16, j+32, j+48), the tile's across the 4
+//     waves through LDS; the running (max, sum, out) are rescaled once per tile
+//     from the reference's initial max -1e30.
+//   PV, as O = P V: step (kb, r) consumes keys 16kb+4c+r (c = the lane group),
+//     A[i][c] = P[query i][that key] (one float4 LDS read covers r = 0..3) and
+//     B[c][j] = V[that key][dim 32w+2j+jt]; the result sits at lane j+16c,
+//     register r = O[query 4c+r][dim 32w+2j+jt].
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kPfStride = 68;  // LDS row of the P tile in floats (64 keys + pad)
+
+QASR_DEV void ld_row32(float (&dst)[32], const float* p) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const float4 t = ld4(p, c);
+    dst[4 * c] = t.x;
+    dst[4 * c + 1] = t.y;
+    dst[4 * c + 2] = t.z;
+    dst[4 * c + 3] = t.w;
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(512) void attention_prefill_mfma_kernel(
+    float* __restrict__ out, const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, int seq_q, int seq_k, int nk, float scale, int q_offset) {
+  constexpr int HD = 128;
+  __shared__ float red_max[2][4][G][16];
+  __shared__ float red_sum[2][4][G][16];
+  __shared__ float corr_l[2][G][16];
+  __shared__ __align__(16) float pl[2][G][16][kPfStride];
+  __shared__ float ml[2][G][16][2];
+  __shared__ __align__(16) float ol[G][16][HD];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = wave >> 2, w = wave & 3;
+  const int lo = lane & 15, hi = lane >> 4;
+  const int i0 = ((int)gridDim.x - 1 - (int)blockIdx.x) * 16;  // longest rows first
+  const int kh = blockIdx.y;
+  const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
+
+  // keys [0, k_hi) cover every row of the block; tiles alternate between groups
+  const int k_hi = min(q_offset + min(i0 + 16, seq_q), seq_k);
+  const int ntiles = (k_hi + 63) / 64;
+  const int nit = (ntiles + 1) / 2;
+  const int k_lim = min(q_offset + i0 + lo + 1, seq_k);  // keys of this lane's query (QK side)
+
+  float qf[G][32];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    ld_row32(qf[g], q + (size_t)min(i0 + lo, seq_q - 1) * q_stride + (size_t)(kh * G + g) * HD + 32 * hi);
+
+  float m_run[G], l_run[G];
+  v4f o[G][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m_run[g] = -1e30f;  // the reference's initial running max
+    l_run[g] = 0.0f;
+    o[g][0] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    o[g][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  const int last_key = seq_k > 0 ? seq_k - 1 : 0;
+  const float* kbase = k + (size_t)kh * HD + 32 * hi;
+  const float* vbase = v + (size_t)kh * HD + 32 * w + 2 * lo;
+  float kf[32];
+  if (nit > 0) ld_row32(kf, kbase + (size_t)min(min(grp, ntiles - 1) * 64 + 16 * w + lo, last_key) * kv_stride);
+
+  for (int it = 0; it < nit; ++it) {
+    const int t = 2 * it + grp;
+    const bool tile_ok = t < ntiles;  // the odd group's last turn may have no tile
+    const int tc = tile_ok ? t : ntiles - 1;
+    float2 vf[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {  // u = 4 kb + r: key 16kb + 4hi + r of the tile
+      const int key = min(tc * 64 + 16 * (u >> 2) + 4 * hi + (u & 3), last_key);
+      vf[u] = *reinterpret_cast<const float2*>(vbase + (size_t)key * kv_stride);
+    }
+    v4f sacc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) sacc[g] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < 32; ++st)
+#pragma unroll
+      for (int g = 0; g < G; ++g) sacc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[g][st], sacc[g], 0, 0, 0);
+    if (it + 1 < nit)  // next tile's keys while the softmax and PV run
+      ld_row32(kf, kbase + (size_t)min(min(t + 2, ntiles - 1) * 64 + 16 * w + lo, last_key) * kv_stride);
+
+    float sv[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = t * 64 + 16 * w + 4 * hi + r;
+        sv[g][r] = (tile_ok && key < k_lim) ? sacc[g][r] * scale : -__builtin_inff();
+        mx = fmaxf(mx, sv[g][r]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (hi == 0) red_max[grp][w][g][lo] = mx;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float tmax = red_max[grp][0][g][lo];
+#pragma unroll
+      for (int ww = 1; ww < 4; ++ww) tmax = fmaxf(tmax, red_max[grp][ww][g][lo]);
+      const float m_new = fmaxf(m_run[g], tmax);
+      const float corr = expf(m_run[g] - m_new);
+      float p[4], sum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = sv[g][r] == -__builtin_inff() ? 0.0f : expf(sv[g][r] - m_new);
+        sum += p[r];
+      }
+      sum += __shfl_xor(sum, 16, 64);
+      sum += __shfl_xor(sum, 32, 64);
+      if (hi == 0) red_sum[grp][w][g][lo] = sum;
+      *reinterpret_cast<float4*>(&pl[grp][g][lo][16 * w + 4 * hi]) = make_float4(p[0], p[1], p[2], p[3]);
+      if (w == 0 && hi == 0) corr_l[grp][g][lo] = corr;
+      m_run[g] = m_new;
+      l_run[g] *= corr;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) l_run[g] += red_sum[grp][ww][g][lo];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float c = corr_l[grp][g][4 * hi + r];
+        o[g][0][r] *= c;
+        o[g][1][r] *= c;
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&pl[grp][g][lo][16 * kb + 4 * hi]);
+        const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          o[g][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], vf[4 * kb + r].x, o[g][0], 0, 0, 0);
+          o[g][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], vf[4 * kb + r].y, o[g][1], 0, 0, 0);
+        }
+      }
+  }
+
+  // merge the two groups: group 1 hands its (max, sum) and outputs to group 0
+  if (w == 0 && hi == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      ml[grp][g][lo][0] = m_run[g];
+      ml[grp][g][lo][1] = l_run[g];
+    }
+  }
+  if (grp == 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<float2*>(&ol[g][4 * hi + r][32 * w + 2 * lo]) = make_float2(o[g][0][r], o[g][1][r]);
+  }
+  __syncthreads();
+  if (grp == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * hi + r;
+        const float m0 = ml[0][g][row][0], l0 = ml[0][g][row][1];
+        const float m1 = ml[1][g][row][0], l1 = ml[1][g][row][1];
+        const float mx = fmaxf(m0, m1);
+        const float f0 = expf(m0 - mx), f1 = expf(m1 - mx);
+        const float lsum = __builtin_fmaf(l1, f1, l0 * f0);
+        const float inv = lsum > 0.0f ? 1.0f / lsum : 1.0f;  // no scaling when the sum is 0
+        const float2 o1 = *reinterpret_cast<const float2*>(&ol[g][row][32 * w + 2 * lo]);
+        const float a0 = __builtin_fmaf(o1.x, f1, o[g][0][r] * f0) * inv;
+        const float a1 = __builtin_fmaf(o1.y, f1, o[g][1][r] * f0) * inv;
+        if (i0 + row < seq_q)
+          *reinterpret_cast<float2*>(out + (size_t)(i0 + row) * q_stride + (size_t)(kh * G + g) * HD +
+                                     32 * w + 2 * lo) = make_float2(a0, a1);
+      }
+  }
+}
+
 template <int HD, int G>
 void launch_attention(float* out, const float* q, const float* k, const float* v, int seq_q,
                       int seq_k, int nk, float scale, int q_offset, hipStream_t st) {
+  if constexpr (HD == 128 && (G == 1 || G == 2)) {
+    if (seq_q >= 16) {  // prefill: the matrix-core kernel
+      const dim3 grid((unsigned)((seq_q + 15) / 16), (unsigned)nk);
+      attention_prefill_mfma_kernel<G><<<grid, 512, 0, st>>>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset);
+      return;
+    }
+  }
   // enough (row, kv head) pairs to fill the chip: 4 rows per workgroup, one
   // wave each; otherwise 8 waves split every row's keys
   if ((long long)seq_q * nk >= 1024) {

@@ -7,8 +7,11 @@
 // any failure.
 #include <hip/hip_runtime.h>
 
+#include <unistd.h>
+
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <functional>
 #include <string>
 #include <vector>
@@ -218,6 +221,120 @@ static void test_linear_int8_exact() {
   }
 }
 
+// Attention over one key returns that key's value row exactly (softmax weight
+// exp(0)/1); two identical keys average their values; the key-split form
+// agrees with the single-pass form.
+static void test_causal_attention() {
+  const size_t nh = 16, nk = 8, hd = 128;
+  std::vector<float> q(nh * hd), k(300 * nk * hd), v(300 * nk * hd);
+  for (size_t i = 0; i < q.size(); ++i) q[i] = std::sin(0.37f * (float)i);
+  for (size_t i = 0; i < k.size(); ++i) k[i] = std::cos(0.11f * (float)i) * 0.5f;
+  for (size_t i = 0; i < v.size(); ++i) v[i] = std::sin(0.05f * (float)i + 1.0f);
+  auto dq = upload(q), dk = upload(k), dv = upload(v);
+  K::DeviceBuffer<float> out(nh * hd), out2(nh * hd);
+  const float scale = 1.0f / std::sqrt((float)hd);
+  K::causal_attention(out, dq, dk, dv, 1, 1, nh, nk, hd, scale, 0);
+  auto o = download(out);
+  for (size_t h = 0; h < nh; ++h)
+    for (size_t d = 0; d < hd; ++d)
+      EXPECT(o[h * hd + d] == v[(h / (nh / nk)) * hd + d], "head %zu dim %zu", h, d);
+  std::vector<float> k2(k.begin(), k.begin() + 2 * nk * hd);
+  for (size_t i = 0; i < nk * hd; ++i) k2[nk * hd + i] = k2[i];  // key 1 == key 0
+  auto dk2 = upload(k2);
+  K::causal_attention(out, dq, dk2, dv, 1, 2, nh, nk, hd, scale, 1);
+  o = download(out);
+  for (size_t h = 0; h < nh; ++h)
+    for (size_t d = 0; d < hd; ++d) {
+      const size_t c = (h / (nh / nk)) * hd + d;
+      const float want = 0.5f * (v[c] + v[nk * hd + c]);
+      EXPECT(std::fabs(o[h * hd + d] - want) <= 1e-6f, "head %zu dim %zu", h, d);
+    }
+  K::DeviceBuffer<float> ws(K::attention_workspace_floats(1, nh, hd));
+  K::causal_attention(out, dq, dk, dv, 1, 300, nh, nk, hd, scale, 299);
+  K::causal_attention(out2, dq, dk, dv, 1, 300, nh, nk, hd, scale, 299, ws);
+  const auto a = download(out), b = download(out2);
+  for (size_t i = 0; i < a.size(); ++i)
+    EXPECT(std::fabs(a[i] - b[i]) <= 1e-5f + 1e-5f * std::fabs(a[i]), "elem %zu: %f vs %f", i, a[i], b[i]);
+}
+
+// lm_head: equal maxima go to the lower index, with and without the workspace.
+static void test_lm_head_argmax() {
+  const size_t in = 1024, vocab = 5000;
+  std::vector<int8_t> w(vocab * in);
+  for (size_t i = 0; i < w.size(); ++i) w[i] = (int8_t)((int)(i * 2654435761u >> 9) % 7 - 3);
+  for (size_t r : {4321u, 3u, 777u})
+    for (size_t c = 0; c < in; ++c) w[r * in + c] = 127;
+  std::vector<float> x(in, 1.0f), sc(vocab, 1e-3f);
+  sc[4321] = sc[3] = sc[777] = 1.0f;
+  auto dw = upload(w);
+  auto dx = upload(x), ds = upload(sc);
+  K::DeviceBuffer<float> logits(vocab);
+  K::DeviceBuffer<int32_t> idx(1);
+  K::DeviceBuffer<uint8_t> ws(K::lm_head_workspace_bytes(vocab));
+  K::lm_head_int8_argmax(idx, logits, dx, dw, ds, 1, in, vocab, ws);
+  EXPECT(download(idx)[0] == 3, "fused: %d", download(idx)[0]);
+  K::lm_head_int8_argmax(idx, logits, dx, dw, ds, 1, in, vocab);
+  EXPECT(download(idx)[0] == 3, "unfused: %d", download(idx)[0]);
+}
+
+// .qint8: a V2 file written byte by byte (quantize.rs:1-34) reads back, uploads
+// bit-exactly, and the gate/up pair lands row-interleaved.
+static void test_qint8_file() {
+  std::string bytes = std::string("QINT8\x02\x00\x00", 8);
+  auto u16 = [&](uint16_t v) { bytes.append(reinterpret_cast<const char*>(&v), 2); };
+  auto u32 = [&](uint32_t v) { bytes.append(reinterpret_cast<const char*>(&v), 4); };
+  auto u64 = [&](uint64_t v) { bytes.append(reinterpret_cast<const char*>(&v), 8); };
+  auto entry = [&](const std::string& n, uint8_t dt, std::vector<uint32_t> shape, uint64_t d, uint64_t s) {
+    u16((uint16_t)n.size());
+    bytes += n;
+    bytes.push_back((char)dt);
+    bytes.push_back((char)shape.size());
+    for (uint32_t x : shape) u32(x);
+    u64(d);
+    u64(s);
+  };
+  u32(3);
+  u32(0);
+  entry("g", 0, {2, 4}, 0, 8);
+  entry("u", 0, {2, 4}, 16, 24);
+  entry("n", 1, {3}, 32, 0);
+  const int8_t g[8] = {1, 2, 3, 4, -1, -2, -3, -4}, u[8] = {5, 6, 7, 8, -5, -6, -7, -8};
+  const float gs[2] = {0.5f, 0.25f}, us[2] = {2.0f, 4.0f}, n[3] = {1.5f, -2.5f, 3.25f};
+  bytes.append(reinterpret_cast<const char*>(g), 8);
+  bytes.append(reinterpret_cast<const char*>(gs), 8);
+  bytes.append(reinterpret_cast<const char*>(u), 8);
+  bytes.append(reinterpret_cast<const char*>(us), 8);
+  bytes.append(reinterpret_cast<const char*>(n), 12);
+  const char* tmp = std::getenv("TMPDIR");
+  const std::string path = std::string(tmp ? tmp : "/tmp") + "/qasr_cpp_test_" +
+                           std::to_string((long)getpid()) + ".qint8";
+  FILE* f = std::fopen(path.c_str(), "wb");
+  EXPECT(f, "cannot write %s", path.c_str());
+  std::fwrite(bytes.data(), 1, bytes.size(), f);
+  std::fclose(f);
+  {
+    auto qf = K::QuantFile::open(path);
+    EXPECT(qf.has_value(), "open failed");
+    EXPECT(qf->version() == 2 && qf->tensors().size() == 3, "table");
+    const auto* m = qf->find("n");
+    EXPECT(m && m->dtype == QASR_QINT8_F32 && m->numel() == 3, "n meta");
+    EXPECT(qf->find("missing") == nullptr, "find missing");
+    K::DeviceBuffer<float> dn(3), dsc(4);
+    qf->upload("n", dn.data(), 12);
+    const auto hn = download(dn);
+    EXPECT(hn[0] == n[0] && hn[1] == n[1] && hn[2] == n[2], "f32 upload");
+    K::DeviceBuffer<int8_t> dw(16);
+    qf->upload_gate_up("g", "u", 2, 4, dw, dsc);
+    const auto hw = download(dw);
+    const auto hs = download(dsc);
+    const int8_t want[16] = {1, 2, 3, 4, 5, 6, 7, 8, -1, -2, -3, -4, -5, -6, -7, -8};
+    for (int i = 0; i < 16; ++i) EXPECT(hw[i] == want[i], "fused byte %d", i);
+    EXPECT(hs[0] == 0.5f && hs[1] == 2.0f && hs[2] == 0.25f && hs[3] == 4.0f, "fused scales");
+  }
+  std::remove(path.c_str());
+  EXPECT(!K::QuantFile::open(path).has_value(), "a missing file opens as nothing");
+}
+
 // A short slice panics before anything is launched (the reference's slice
 // index panic).
 static void test_short_slice_panics() {
@@ -264,6 +381,9 @@ int main() {
   run("test_rope_cache", test_rope_cache);
   run("test_kv_store", test_kv_store);
   run("test_linear_int8_exact", test_linear_int8_exact);
+  run("test_causal_attention", test_causal_attention);
+  run("test_lm_head_argmax", test_lm_head_argmax);
+  run("test_qint8_file", test_qint8_file);
   run("test_short_slice_panics", test_short_slice_panics);
   run("test_status_errors", test_status_errors);
   std::printf("%s: %d failed\n", g_failed ? "FAILED" : "ok", g_failed);

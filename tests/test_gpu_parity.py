@@ -879,6 +879,14 @@ ATTN_CASES = [
     ("mha_g1", 3, 65, 4, 4, 128, 62),
     ("gqa8", 2, 129, 8, 1, 128, 127),
     ("no_keys", 2, 0, 16, 8, 128, 0),
+    # prefill on the matrix cores (16 rows per workgroup, tiles alternate between 2 wave groups)
+    ("mfma_16_rows", 16, 16, 16, 8, 128, 0),
+    ("mfma_ragged_17", 17, 17, 16, 8, 128, 0),
+    ("mfma_mha_g1", 40, 90, 8, 8, 128, 50),
+    ("mfma_keys_below_limit", 33, 20, 16, 8, 128, 40),
+    ("mfma_one_key", 16, 1, 16, 8, 128, 0),
+    ("mfma_chunk_700", 700, 1000, 16, 8, 128, 300),
+    ("mfma_no_keys", 20, 0, 16, 8, 128, 0),
 ]
 
 
