@@ -418,34 +418,41 @@ void launch_attention_split(float* out, const float* q, const float* k, const fl
 }
 
 // Prefill attention on the fp32 matrix cores (v_mfma_f32_16x16x4f32), for
-// head_dim 128 and 1 or 2 q heads per kv head. Products and sums stay fp32;
-// only the order of the terms of each dot product and of the key sum differ
-// from the reference's sequential loops.
+// head_dim 128. Products and sums stay fp32; only the order of the terms of
+// each dot product and of the key sum differ from the reference's sequential
+// loops.
 //
-// A workgroup takes 16 query rows x the G heads of one kv head with 8 waves:
-// group z (waves 4z..4z+3) walks the 64-key tiles z, z+2, ... of the rows'
-// causal range, and the two groups' (max, sum, out) are merged at the end.
-// Within a group, wave w owns keys 16w..16w+15 of a tile in the QK product and
-// head dims 32w..32w+31 in the PV product.
-//   QK, as S^T = K Q^T: A[i][k] (lane i+16k) = K[key i][dim 32k+s] and
-//     B[k][j] (lane j+16k) = Q[query j][dim 32k+s] at step s = 0..31, so each
-//     lane reads 32 contiguous floats of its key and of its query. The result
-//     sits at lane j+16c, register r = S[query j][key 16w+4c+r].
-//   softmax per query row over the tile: the wave's max/sum over its 16 keys
-//     (registers, then lanes j, j+16, j+32, j+48), the tile's across the 4
-//     waves through LDS; the running (max, sum, out) are rescaled once per tile
-//     from the reference's initial max -1e30.
-//   PV, as O = P V: step (kb, r) consumes keys 16kb+4c+r (c = the lane group),
-//     A[i][c] = P[query i][that key] (one float4 LDS read covers r = 0..3) and
-//     B[c][j] = V[that key][dim 32w+2j+jt]; the result sits at lane j+16c,
-//     register r = O[query 4c+r][dim 32w+2j+jt].
+// The 16 columns of the products are (query row, head) pairs: R = 16 / G
+// consecutive rows x the G q heads of one kv head, column c = g * R + i, so
+// the heads sharing a kv head share every k and v load. A workgroup of NW
+// waves takes one such block; wave w walks the 64-key tiles w, w + NW, ... of
+// the block's causal range as a complete online softmax of its own, and the
+// NW (max, sum, out) triples are merged at the end. Per tile and wave:
+//   QK, as S^T = K Q^T, one 16-key block kb at a time: A[i][k] (lane i+16k) =
+//     K[key 16kb+i][dim d] and B[k][c] (lane c+16k) = Q[column c][dim d] at
+//     step s = 0..31 with d = 16(s/4) + 4k + s%4 (a bijection of the 128
+//     dims; each load instruction reads 64 contiguous bytes of a row). The
+//     result sits at lane c+16h, register r = S[column c][key 16kb+4h+r].
+//   softmax per column over the tile: 16 scores per lane, then lanes c, c+16,
+//     c+32, c+48; the running (max, sum, out) are rescaled once per tile from
+//     the reference's initial max -1e30.
+//   PV, as O = P V: step (kb, r) consumes keys 16kb+4h+r (h = the lane
+//     group), so A[c][h] = P[column c][that key] is the probability the lane
+//     already holds, and B[h][j] = V[that key][dim 4j + jt%4 + 64(jt/4)] for
+//     the 8 output tiles jt (whole 128-byte lines per load instruction); the
+//     result sits at lane j+16h, register r = O[column 4h+r][that dim].
 typedef float v4f __attribute__((ext_vector_type(4)));
-constexpr int kPfStride = 68;  // LDS row of the P tile in floats (64 keys + pad)
+// Key-tile streams per workgroup. About 200 registers per wave allow two
+// waves per SIMD, so a CU holds two 4-wave workgroups (measured at T=512,
+// 0.6B: 30.5 us; 8 waves per workgroup, one workgroup per CU: 47.7 us).
+constexpr int kPrefillWaves = 4;
 
+// dims 16c + 4h .. 16c + 4h + 3 (c = 0..7) of a row, for lane group h (p points
+// at dim 4h): one load instruction reads 64 contiguous bytes per row
 QASR_DEV void ld_row32(float (&dst)[32], const float* p) {
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
-    const float4 t = ld4(p, c);
+    const float4 t = ld4(p, 4 * c);
     dst[4 * c] = t.x;
     dst[4 * c + 1] = t.y;
     dst[4 * c + 2] = t.z;
@@ -453,178 +460,211 @@ QASR_DEV void ld_row32(float (&dst)[32], const float* p) {
   }
 }
 
-template <int G>
-__global__ __launch_bounds__(512) void attention_prefill_mfma_kernel(
+// v rows of keys key0 + r (r = 0..3), dims 4j..4j+3 and 64+4j..64+4j+3 for
+// lane j (vbase points at dim 4j): dst[8r + jt]
+QASR_DEV void ld_v_block(float (&dst)[32], const float* vbase, size_t kv_stride, int key0,
+                         int last_key) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float* p = vbase + (size_t)min(key0 + r, last_key) * kv_stride;
+    const float4 a = ld4(p, 0), b = ld4(p, 16);
+    dst[8 * r] = a.x;
+    dst[8 * r + 1] = a.y;
+    dst[8 * r + 2] = a.z;
+    dst[8 * r + 3] = a.w;
+    dst[8 * r + 4] = b.x;
+    dst[8 * r + 5] = b.y;
+    dst[8 * r + 6] = b.z;
+    dst[8 * r + 7] = b.w;
+  }
+}
+
+template <int G, int NW>
+__global__ __launch_bounds__(64 * NW) void attention_prefill_mfma_kernel(
     float* __restrict__ out, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, int seq_q, int seq_k, int nk, float scale, int q_offset) {
   constexpr int HD = 128;
-  __shared__ float red_max[2][4][G][16];
-  __shared__ float red_sum[2][4][G][16];
-  __shared__ float corr_l[2][G][16];
-  __shared__ __align__(16) float pl[2][G][16][kPfStride];
-  __shared__ float ml[2][G][16][2];
-  __shared__ __align__(16) float ol[G][16][HD];
+  constexpr int R = 16 / G;  // query rows per block
+  __shared__ float ml[NW][16][2];
+  __shared__ __align__(16) float ol[NW - 1][16][HD];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int grp = wave >> 2, w = wave & 3;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int lo = lane & 15, hi = lane >> 4;
-  const int i0 = ((int)gridDim.x - 1 - (int)blockIdx.x) * 16;  // longest rows first
-  const int kh = blockIdx.y;
+  // Items (row block, kv head) ranked heaviest first; workgroups i and i + n/2
+  // take ranks i and n-1-i, so the two workgroups a CU holds at once pair a
+  // long causal range with a short one.
+  const int n_items = (int)gridDim.x, half = (n_items + 1) / 2, wid = (int)blockIdx.x;
+  const int rank = wid < half ? wid : n_items - 1 - (wid - half);
+  const int nblk = n_items / nk;
+  const int i0 = (nblk - 1 - rank / nk) * R;
+  const int kh = rank % nk;
   const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
 
-  // keys [0, k_hi) cover every row of the block; tiles alternate between groups
-  const int k_hi = min(q_offset + min(i0 + 16, seq_q), seq_k);
+  // keys [0, k_hi) cover every row of the block
+  const int k_hi = min(q_offset + min(i0 + R, seq_q), seq_k);
   const int ntiles = (k_hi + 63) / 64;
-  const int nit = (ntiles + 1) / 2;
-  const int k_lim = min(q_offset + i0 + lo + 1, seq_k);  // keys of this lane's query (QK side)
-
-  float qf[G][32];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-    ld_row32(qf[g], q + (size_t)min(i0 + lo, seq_q - 1) * q_stride + (size_t)(kh * G + g) * HD + 32 * hi);
-
-  float m_run[G], l_run[G];
-  v4f o[G][2];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m_run[g] = -1e30f;  // the reference's initial running max
-    l_run[g] = 0.0f;
-    o[g][0] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    o[g][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  }
+  // this lane's QK column: row i0 + lo % R, head lo / R
+  const int k_lim = min(q_offset + i0 + lo % R + 1, seq_k);
   const int last_key = seq_k > 0 ? seq_k - 1 : 0;
-  const float* kbase = k + (size_t)kh * HD + 32 * hi;
-  const float* vbase = v + (size_t)kh * HD + 32 * w + 2 * lo;
-  float kf[32];
-  if (nit > 0) ld_row32(kf, kbase + (size_t)min(min(grp, ntiles - 1) * 64 + 16 * w + lo, last_key) * kv_stride);
 
-  for (int it = 0; it < nit; ++it) {
-    const int t = 2 * it + grp;
-    const bool tile_ok = t < ntiles;  // the odd group's last turn may have no tile
-    const int tc = tile_ok ? t : ntiles - 1;
-    float2 vf[16];
+  float m_run = -1e30f;  // the reference's initial running max
+  float l_run = 0.0f;
+  v4f o[8];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {  // u = 4 kb + r: key 16kb + 4hi + r of the tile
-      const int key = min(tc * 64 + 16 * (u >> 2) + 4 * hi + (u & 3), last_key);
-      vf[u] = *reinterpret_cast<const float2*>(vbase + (size_t)key * kv_stride);
-    }
-    v4f sacc[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) sacc[g] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int st = 0; st < 32; ++st)
-#pragma unroll
-      for (int g = 0; g < G; ++g) sacc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[g][st], sacc[g], 0, 0, 0);
-    if (it + 1 < nit)  // next tile's keys while the softmax and PV run
-      ld_row32(kf, kbase + (size_t)min(min(t + 2, ntiles - 1) * 64 + 16 * w + lo, last_key) * kv_stride);
+  for (int jt = 0; jt < 8; ++jt) o[jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    float sv[G][4];
+  if (w < ntiles) {
+    float qf[32];
+    ld_row32(qf, q + (size_t)min(i0 + lo % R, seq_q - 1) * q_stride + (size_t)(kh * G + lo / R) * HD + 4 * hi);
+    const float* kbase = k + (size_t)kh * HD + 4 * hi;
+    const float* vbase = v + (size_t)kh * HD + 4 * lo;
+    float ka[32], kb1[32];
+    ld_row32(ka, kbase + (size_t)min(w * 64 + lo, last_key) * kv_stride);
+    ld_row32(kb1, kbase + (size_t)min(w * 64 + 16 + lo, last_key) * kv_stride);
+    for (int t = w; t < ntiles; t += NW) {
+      const int key0 = t * 64;
+      // QK: key blocks 0 and 1 from the prefetched rows, 2 and 3 loaded meanwhile
+      float kc[32], kd[32];
+      ld_row32(kc, kbase + (size_t)min(key0 + 32 + lo, last_key) * kv_stride);
+      ld_row32(kd, kbase + (size_t)min(key0 + 48 + lo, last_key) * kv_stride);
+      v4f sacc[4];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+      for (int b = 0; b < 4; ++b) sacc[b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < 32; ++st) {
+        sacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[st], qf[st], sacc[0], 0, 0, 0);
+        sacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb1[st], qf[st], sacc[1], 0, 0, 0);
+      }
+      float va[32], vb[32];
+      ld_v_block(va, vbase, kv_stride, key0 + 4 * hi, last_key);
+      ld_v_block(vb, vbase, kv_stride, key0 + 16 + 4 * hi, last_key);
+#pragma unroll
+      for (int st = 0; st < 32; ++st) {
+        sacc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc[st], qf[st], sacc[2], 0, 0, 0);
+        sacc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(kd[st], qf[st], sacc[3], 0, 0, 0);
+      }
+      float vc[32], vd[32];
+      ld_v_block(vc, vbase, kv_stride, key0 + 32 + 4 * hi, last_key);
+      ld_v_block(vd, vbase, kv_stride, key0 + 48 + 4 * hi, last_key);
+
+      // online softmax over the tile's 64 keys, per column
+      float sv[4][4];
       float mx = -__builtin_inff();
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = t * 64 + 16 * w + 4 * hi + r;
-        sv[g][r] = (tile_ok && key < k_lim) ? sacc[g][r] * scale : -__builtin_inff();
-        mx = fmaxf(mx, sv[g][r]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      if (hi == 0) red_max[grp][w][g][lo] = mx;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float tmax = red_max[grp][0][g][lo];
-#pragma unroll
-      for (int ww = 1; ww < 4; ++ww) tmax = fmaxf(tmax, red_max[grp][ww][g][lo]);
-      const float m_new = fmaxf(m_run[g], tmax);
-      const float corr = expf(m_run[g] - m_new);
-      float p[4], sum = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = sv[g][r] == -__builtin_inff() ? 0.0f : expf(sv[g][r] - m_new);
-        sum += p[r];
-      }
-      sum += __shfl_xor(sum, 16, 64);
-      sum += __shfl_xor(sum, 32, 64);
-      if (hi == 0) red_sum[grp][w][g][lo] = sum;
-      *reinterpret_cast<float4*>(&pl[grp][g][lo][16 * w + 4 * hi]) = make_float4(p[0], p[1], p[2], p[3]);
-      if (w == 0 && hi == 0) corr_l[grp][g][lo] = corr;
-      m_run[g] = m_new;
-      l_run[g] *= corr;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int ww = 0; ww < 4; ++ww) l_run[g] += red_sum[grp][ww][g][lo];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float c = corr_l[grp][g][4 * hi + r];
-        o[g][0][r] *= c;
-        o[g][1][r] *= c;
-      }
-    }
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float4 a4 = *reinterpret_cast<const float4*>(&pl[grp][g][lo][16 * kb + 4 * hi]);
-        const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+      for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          o[g][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], vf[4 * kb + r].x, o[g][0], 0, 0, 0);
-          o[g][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], vf[4 * kb + r].y, o[g][1], 0, 0, 0);
+          const int key = key0 + 16 * b + 4 * hi + r;
+          sv[b][r] = key < k_lim ? sacc[b][r] * scale : -__builtin_inff();
+          mx = fmaxf(mx, sv[b][r]);
         }
-      }
-  }
-
-  // merge the two groups: group 1 hands its (max, sum) and outputs to group 0
-  if (w == 0 && hi == 0) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      const float corr = expf(m_run - m_new);
+      float sum = 0.0f;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      ml[grp][g][lo][0] = m_run[g];
-      ml[grp][g][lo][1] = l_run[g];
-    }
-  }
-  if (grp == 1) {
+      for (int b = 0; b < 4; ++b)
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<float2*>(&ol[g][4 * hi + r][32 * w + 2 * lo]) = make_float2(o[g][0][r], o[g][1][r]);
-  }
-  __syncthreads();
-  if (grp == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int r = 0; r < 4; ++r) {
+          sv[b][r] = sv[b][r] == -__builtin_inff() ? 0.0f : expf(sv[b][r] - m_new);
+          sum += sv[b][r];
+        }
+      sum += __shfl_xor(sum, 16, 64);
+      sum += __shfl_xor(sum, 32, 64);
+      l_run = __builtin_fmaf(l_run, corr, sum);
+      m_run = m_new;
+      // the O rows of this lane are columns 4hi + r: their corrections
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 4 * hi + r;
-        const float m0 = ml[0][g][row][0], l0 = ml[0][g][row][1];
-        const float m1 = ml[1][g][row][0], l1 = ml[1][g][row][1];
-        const float mx = fmaxf(m0, m1);
-        const float f0 = expf(m0 - mx), f1 = expf(m1 - mx);
-        const float lsum = __builtin_fmaf(l1, f1, l0 * f0);
-        const float inv = lsum > 0.0f ? 1.0f / lsum : 1.0f;  // no scaling when the sum is 0
-        const float2 o1 = *reinterpret_cast<const float2*>(&ol[g][row][32 * w + 2 * lo]);
-        const float a0 = __builtin_fmaf(o1.x, f1, o[g][0][r] * f0) * inv;
-        const float a1 = __builtin_fmaf(o1.y, f1, o[g][1][r] * f0) * inv;
-        if (i0 + row < seq_q)
-          *reinterpret_cast<float2*>(out + (size_t)(i0 + row) * q_stride + (size_t)(kh * G + g) * HD +
-                                     32 * w + 2 * lo) = make_float2(a0, a1);
+        const float c = __shfl(corr, 4 * hi + r, 64);
+#pragma unroll
+        for (int jt = 0; jt < 8; ++jt) o[jt][r] *= c;
       }
+      // next tile's first two key blocks while PV runs
+      const int tn = t + NW < ntiles ? t + NW : t;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int jt = 0; jt < 8; ++jt) o[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[0][r], va[8 * r + jt], o[jt], 0, 0, 0);
+      ld_row32(ka, kbase + (size_t)min(tn * 64 + lo, last_key) * kv_stride);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int jt = 0; jt < 8; ++jt) o[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[1][r], vb[8 * r + jt], o[jt], 0, 0, 0);
+      ld_row32(kb1, kbase + (size_t)min(tn * 64 + 16 + lo, last_key) * kv_stride);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int jt = 0; jt < 8; ++jt) o[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[2][r], vc[8 * r + jt], o[jt], 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int jt = 0; jt < 8; ++jt) o[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[3][r], vd[8 * r + jt], o[jt], 0, 0, 0);
+    }
+  }
+
+  // merge the NW waves' (max, sum, out) in wave 0; a wave without tiles
+  // carries max -1e30 and sum 0 and drops out
+  if (hi == 0) {
+    ml[w][lo][0] = m_run;
+    ml[w][lo][1] = l_run;
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float* dst = &ol[w - 1][4 * hi + r][4 * lo];
+      *reinterpret_cast<float4*>(dst) = make_float4(o[0][r], o[1][r], o[2][r], o[3][r]);
+      *reinterpret_cast<float4*>(dst + 64) = make_float4(o[4][r], o[5][r], o[6][r], o[7][r]);
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int col = 4 * hi + r;
+      float mx = ml[0][col][0];
+#pragma unroll
+      for (int u = 1; u < NW; ++u) mx = fmaxf(mx, ml[u][col][0]);
+      const float f0 = expf(ml[0][col][0] - mx);
+      float lsum = ml[0][col][1] * f0;
+      float acc[8];
+#pragma unroll
+      for (int jt = 0; jt < 8; ++jt) acc[jt] = o[jt][r] * f0;
+#pragma unroll
+      for (int u = 1; u < NW; ++u) {
+        const float f = expf(ml[u][col][0] - mx);
+        lsum = __builtin_fmaf(ml[u][col][1], f, lsum);
+        const float4 a = *reinterpret_cast<const float4*>(&ol[u - 1][col][4 * lo]);
+        const float4 b = *reinterpret_cast<const float4*>(&ol[u - 1][col][4 * lo + 64]);
+        acc[0] = __builtin_fmaf(a.x, f, acc[0]);
+        acc[1] = __builtin_fmaf(a.y, f, acc[1]);
+        acc[2] = __builtin_fmaf(a.z, f, acc[2]);
+        acc[3] = __builtin_fmaf(a.w, f, acc[3]);
+        acc[4] = __builtin_fmaf(b.x, f, acc[4]);
+        acc[5] = __builtin_fmaf(b.y, f, acc[5]);
+        acc[6] = __builtin_fmaf(b.z, f, acc[6]);
+        acc[7] = __builtin_fmaf(b.w, f, acc[7]);
+      }
+      const float inv = lsum > 0.0f ? 1.0f / lsum : 1.0f;  // no scaling when the sum is 0
+      const int row = i0 + col % R, head = kh * G + col / R;
+      if (row < seq_q) {
+        float* dst = out + (size_t)row * q_stride + (size_t)head * HD + 4 * lo;
+        st4(dst, 0, make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv));
+        st4(dst, 16, make_float4(acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv));
+      }
+    }
   }
 }
 
 template <int HD, int G>
 void launch_attention(float* out, const float* q, const float* k, const float* v, int seq_q,
                       int seq_k, int nk, float scale, int q_offset, hipStream_t st) {
-  if constexpr (HD == 128 && (G == 1 || G == 2)) {
-    if (seq_q >= 16) {  // prefill: the matrix-core kernel
-      const dim3 grid((unsigned)((seq_q + 15) / 16), (unsigned)nk);
-      attention_prefill_mfma_kernel<G><<<grid, 512, 0, st>>>(out, q, k, v, seq_q, seq_k, nk, scale, q_offset);
+  if constexpr (HD == 128) {
+    if (seq_q >= 16 / G) {  // prefill: the matrix-core kernel, 16 / G rows per workgroup
+      const unsigned items = (unsigned)((seq_q + 16 / G - 1) / (16 / G)) * (unsigned)nk;
+      attention_prefill_mfma_kernel<G, kPrefillWaves><<<items, 64 * kPrefillWaves, 0, st>>>(
+          out, q, k, v, seq_q, seq_k, nk, scale, q_offset);
       return;
     }
   }

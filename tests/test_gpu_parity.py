@@ -887,6 +887,9 @@ ATTN_CASES = [
     ("mfma_one_key", 16, 1, 16, 8, 128, 0),
     ("mfma_chunk_700", 700, 1000, 16, 8, 128, 300),
     ("mfma_no_keys", 20, 0, 16, 8, 128, 0),
+    ("mfma_g4", 25, 60, 16, 4, 128, 35),
+    ("mfma_g8", 9, 40, 8, 1, 128, 31),
+    ("mfma_g2_8_rows", 8, 8, 16, 8, 128, 0),
 ]
 
 
