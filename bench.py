@@ -320,7 +320,8 @@ class C5BatchedDecode(Workload):
 class W8A32Decode(Workload):
     name = "w8a32_decode"
     description = ("qwen3-asr-1.7b INT8 decode projections as the reference runs them (W8A32 "
-                   "linear_nobias_int8, B=1): q/k/v/o, fused gate/up and down per layer, 28 distinct layers")
+                   "linear_nobias_int8, B=1): q/k/v in one launch, o, fused gate/up and down per layer, "
+                   "28 distinct layers")
     unit_tokens = 1
     dtype = "int8/f32"
 
@@ -348,8 +349,17 @@ class W8A32Decode(Workload):
                                                    self.w[n][j % L][1], 1, i, o),
                     o * i + o * F + i * F + o * F)
 
-        self.kernels = {n: mk(n) for n in self.SHAPES}
-        self.step_bytes = L * sum(b for _, b in self.kernels.values())
+        def qkv(j):
+            names = ("wq", "wk", "wv")
+            ws = [K.QuantWeight(self.w[n][j % L][0], self.w[n][j % L][1], self.SHAPES[n][0], 2048)
+                  for n in names]
+            K.linear_nobias_int8_multi([self.y[n][j % L] for n in names], ws, self.x["wq"][j % L], 1, 2048)
+
+        qkv_rows = sum(self.SHAPES[n][0] for n in ("wq", "wk", "wv"))
+        # q/k/v read one x: weights, scales and outputs of the three, x once
+        self.kernels = {"qkv": (qkv, qkv_rows * 2048 + 2 * qkv_rows * F + 2048 * F)}
+        self.kernels.update({n: mk(n) for n in ("wo", "gate_up", "down")})
+        self.step_bytes = L * sum(spec[1] for spec in self.kernels.values())
         self.tokens_per_step = 1.0
 
     def step(self, i):

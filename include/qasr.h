@@ -226,6 +226,16 @@ int qasr_linear_nobias_int8_f32(float* y, const float* x, const int8_t* w,
                                 const float* scales, size_t seq_len,
                                 size_t in_dim, size_t out_dim, void* stream);
 
+/* Up to 4 W8A32 projections of the same input in one launch: for m < n_mats,
+ * ys[m][s, :] = qasr_linear_nobias_int8_f32(x[s, :], ws[m], scales[m]) with
+ * out_dims[m] rows (the q/k/v calls of one decode step share x:
+ * decoder.rs:881-886). Same results as the separate calls, bit for bit. ys, ws,
+ * scales and out_dims are host arrays of n_mats device pointers / sizes. */
+int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,
+                                      const int8_t* const* ws, const float* const* scales,
+                                      const size_t* out_dims, const float* x, size_t seq_len,
+                                      size_t in_dim, void* stream);
+
 /* W8A32 linear with optional bias (bias may be NULL): y = linear_nobias + bias.
  * Replaces kernels::linear_int8 (kernels/mod.rs:664-673). */
 int qasr_linear_int8_f32(float* y, const float* x, const int8_t* w,

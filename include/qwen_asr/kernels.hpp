@@ -372,6 +372,34 @@ inline void linear_nobias_int8(F y, CF x, DevSlice<const int8_t> w_int8, CF scal
                 "linear_nobias_int8");
 }
 
+// Several projections of the same x in one launch (decoder.rs:881-886's q/k/v):
+// ys[m] = linear_nobias_int8(x, ws[m], scales[m]) with out_dims[m] rows.
+inline void linear_nobias_int8_multi(const std::vector<F>& ys,
+                                     const std::vector<DevSlice<const int8_t>>& ws,
+                                     const std::vector<CF>& scales,
+                                     const std::vector<size_t>& out_dims, CF x, size_t seq_len,
+                                     size_t in_dim) {
+  const size_t n = out_dims.size();
+  if (ys.size() != n || ws.size() != n || scales.size() != n)
+    throw Panic("linear_nobias_int8_multi: one output, weight and scale slice per matrix");
+  std::vector<float*> yp(n);
+  std::vector<const int8_t*> wp(n);
+  std::vector<const float*> sp(n);
+  for (size_t m = 0; m < n; ++m) {
+    detail::need(ys[m], seq_len * out_dims[m], "y");
+    detail::need(ws[m], out_dims[m] * in_dim, "w_int8");
+    detail::need(scales[m], out_dims[m], "scales");
+    yp[m] = ys[m].ptr;
+    wp[m] = ws[m].ptr;
+    sp[m] = scales[m].ptr;
+  }
+  detail::need(x, seq_len * in_dim, "x");
+  detail::check(qasr_linear_nobias_int8_multi_f32(n, yp.data(), wp.data(), sp.data(),
+                                                  out_dims.data(), x.ptr, seq_len, in_dim,
+                                                  detail::st()),
+                "linear_nobias_int8_multi");
+}
+
 inline void linear_int8(F y, CF x, DevSlice<const int8_t> w_int8, CF scales, CF bias,
                         size_t seq_len, size_t in_dim, size_t out_dim) {
   detail::need(y, seq_len * out_dim, "y");

@@ -121,13 +121,12 @@ __global__ __launch_bounds__(256) void w8a32_vec_kernel(float* y, const float* x
 // (value, index) in the lm_head argmax order and writes it to part[blockIdx.x];
 // waves past the last row then stay to the end (their loads clamp to the last
 // row and they offer no candidate).
-template <int KCH, int R, bool PART = false>
-__global__ __launch_bounds__(256) void w8a32_rows_kernel(float* y, const float* x, const int8_t* w,
-                                                         const float* scales, const float* bias,
-                                                         int in_dim, int out_dim,
-                                                         float2* part = nullptr) {
+template <int KCH, int R, bool PART>
+QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const float* scales,
+                              const float* bias, int in_dim, int out_dim, unsigned block,
+                              float2* part) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int o0 = (blockIdx.x * (256 / kWave) + threadIdx.x / kWave) * R;
+  const int o0 = (int)(block * (256 / kWave) + threadIdx.x / kWave) * R;
   if constexpr (!PART) {
     if (o0 >= out_dim) return;
   }
@@ -201,9 +200,97 @@ __global__ __launch_bounds__(256) void w8a32_rows_kernel(float* y, const float* 
           bv = sv[k];
           bi = si[k];
         }
-      part[blockIdx.x] = make_float2(bv, __int_as_float(bi));
+      part[block] = make_float2(bv, __int_as_float(bi));
     }
   }
+}
+
+template <int KCH, int R, bool PART = false>
+__global__ __launch_bounds__(256) void w8a32_rows_kernel(float* y, const float* x, const int8_t* w,
+                                                         const float* scales, const float* bias,
+                                                         int in_dim, int out_dim,
+                                                         float2* part = nullptr) {
+  w8a32_rows_body<KCH, R, PART>(y, x, w, scales, bias, in_dim, out_dim, blockIdx.x, part);
+}
+
+// Several matrices of the same input in one launch (the q/k/v projections):
+// workgroups [wg_begin[m], wg_begin[m + 1]) compute matrix m.
+constexpr int kMaxMats = 4;
+struct MatSet {
+  float* y[kMaxMats];
+  const int8_t* w[kMaxMats];
+  const float* s[kMaxMats];
+  int out[kMaxMats];
+  unsigned wg_begin[kMaxMats + 1];
+  int n;
+};
+
+template <int KCH, int R>
+__global__ __launch_bounds__(256) void w8a32_rows_multi_kernel(MatSet ms, const float* x,
+                                                               int in_dim) {
+  float* y = ms.y[0];
+  const int8_t* w = ms.w[0];
+  const float* sc = ms.s[0];
+  int out = ms.out[0];
+  unsigned b0 = 0;
+#pragma unroll
+  for (int m = 1; m < kMaxMats; ++m)
+    if (m < ms.n && blockIdx.x >= ms.wg_begin[m]) {
+      y = ms.y[m];
+      w = ms.w[m];
+      sc = ms.s[m];
+      out = ms.out[m];
+      b0 = ms.wg_begin[m];
+    }
+  w8a32_rows_body<KCH, R, false>(y, x, w, sc, nullptr, in_dim, out, blockIdx.x - b0, nullptr);
+}
+
+// Rows per wave of a one-token matvec: the largest power of two that leaves
+// at least 1024 waves (an even spread over the 1024 SIMDs) and keeps the
+// weight registers of a wave at most 8-16 KiB in flight.
+int rows_per_wave(size_t in_dim, size_t out_rows) {
+  const size_t kch = in_dim / 1024;
+  const int cap = kch == 1 ? 8 : kch == 2 ? 4 : 2;
+  int r = 1;
+  while (r < cap && out_rows / (2 * (size_t)r) >= 1024) r *= 2;
+  return r;
+}
+
+bool w8a32_rows_shape(size_t in_dim, const void* w, const void* x) {
+  return in_dim >= 1024 && in_dim % 1024 == 0 && in_dim <= 8192 && aligned16(w) && aligned16(x);
+}
+
+// Launches the one-token kernel for (in_dim / 1024, r) on `grid` workgroups.
+template <bool PART>
+void launch_rows(int kch, int r, unsigned grid, hipStream_t st, float* y, const float* x,
+                 const int8_t* w, const float* scales, const float* bias, int k, int o,
+                 float2* part) {
+#define QASR_ROWS(KCH, R)                                                                        \
+  if (kch == KCH && r == R) {                                                                    \
+    w8a32_rows_kernel<KCH, R, PART><<<grid, 256, 0, st>>>(y, x, w, scales, bias, k, o, part);    \
+    return;                                                                                      \
+  }
+  QASR_ROWS(1, 1) QASR_ROWS(1, 2) QASR_ROWS(1, 4) QASR_ROWS(1, 8)
+  QASR_ROWS(2, 1) QASR_ROWS(2, 2) QASR_ROWS(2, 4)
+  QASR_ROWS(3, 1) QASR_ROWS(3, 2) QASR_ROWS(4, 1) QASR_ROWS(4, 2)
+  QASR_ROWS(5, 1) QASR_ROWS(5, 2) QASR_ROWS(6, 1) QASR_ROWS(6, 2)
+  QASR_ROWS(7, 1) QASR_ROWS(7, 2) QASR_ROWS(8, 1) QASR_ROWS(8, 2)
+#undef QASR_ROWS
+}
+
+void launch_rows_multi(int kch, int r, unsigned grid, hipStream_t st, const MatSet& ms,
+                       const float* x, int k) {
+#define QASR_ROWS(KCH, R)                                                      \
+  if (kch == KCH && r == R) {                                                  \
+    w8a32_rows_multi_kernel<KCH, R><<<grid, 256, 0, st>>>(ms, x, k);           \
+    return;                                                                    \
+  }
+  QASR_ROWS(1, 1) QASR_ROWS(1, 2) QASR_ROWS(1, 4) QASR_ROWS(1, 8)
+  QASR_ROWS(2, 1) QASR_ROWS(2, 2) QASR_ROWS(2, 4)
+  QASR_ROWS(3, 1) QASR_ROWS(3, 2) QASR_ROWS(4, 1) QASR_ROWS(4, 2)
+  QASR_ROWS(5, 1) QASR_ROWS(5, 2) QASR_ROWS(6, 1) QASR_ROWS(6, 2)
+  QASR_ROWS(7, 1) QASR_ROWS(7, 2) QASR_ROWS(8, 1) QASR_ROWS(8, 2)
+#undef QASR_ROWS
 }
 
 __global__ __launch_bounds__(256) void w8a32_scalar_kernel(float* y, const float* x, const int8_t* w,
@@ -443,20 +530,11 @@ static int launch_w8a32(float* y, const float* x, const int8_t* w, const float* 
   hipStream_t st = as_stream(stream);
   const unsigned grid = (unsigned)((out_dim + 3) / 4);
   const int s = (int)seq_len, k = (int)in_dim, o = (int)out_dim;
-  const bool vec = in_dim >= 1024 && in_dim % 1024 == 0 && in_dim <= 8192 && aligned16(w) &&
-                   aligned16(x);
+  const bool vec = w8a32_rows_shape(in_dim, w, x);
   if (vec && seq_len == 1) {
-    // rows per wave: 6-8 KiB of weights in flight per wave
-    switch (in_dim / 1024) {
-      case 1: w8a32_rows_kernel<1, 8><<<(unsigned)((out_dim + 31) / 32), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
-      case 2: w8a32_rows_kernel<2, 4><<<(unsigned)((out_dim + 15) / 16), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
-      case 3: w8a32_rows_kernel<3, 2><<<(unsigned)((out_dim + 7) / 8), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
-      case 4: w8a32_rows_kernel<4, 2><<<(unsigned)((out_dim + 7) / 8), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
-      case 5: w8a32_rows_kernel<5, 1><<<(unsigned)((out_dim + 3) / 4), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
-      case 6: w8a32_rows_kernel<6, 1><<<(unsigned)((out_dim + 3) / 4), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
-      case 7: w8a32_rows_kernel<7, 1><<<(unsigned)((out_dim + 3) / 4), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
-      default: w8a32_rows_kernel<8, 1><<<(unsigned)((out_dim + 3) / 4), 256, 0, st>>>(y, x, w, scales, bias, k, o); break;
-    }
+    const int r = rows_per_wave(in_dim, out_dim);
+    launch_rows<false>((int)(in_dim / 1024), r, (unsigned)((out_dim + 4 * r - 1) / (4 * r)), st, y, x,
+                       w, scales, bias, k, o, nullptr);
   } else if (vec) {
     switch (in_dim / 1024) {
       case 1: w8a32_vec_kernel<1><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
@@ -478,26 +556,14 @@ namespace qasr {
 bool launch_w8a32_argmax_partials(float* y, const float* x, const int8_t* w, const float* scales,
                                   size_t in_dim, size_t out_dim, float2* part, size_t part_cap,
                                   hipStream_t st, unsigned* n_part) {
-  if (!(in_dim >= 1024 && in_dim % 1024 == 0 && in_dim <= 8192 && aligned16(w) && aligned16(x)))
-    return false;
+  if (!w8a32_rows_shape(in_dim, w, x)) return false;
   if (out_dim == 0 || out_dim > 0x7fffffffu - 64) return false;
-  const int kc = (int)(in_dim / 1024);
-  const int rows_per_wg = 4 * (kc == 1 ? 8 : kc == 2 ? 4 : kc <= 4 ? 2 : 1);
-  const size_t grid = (out_dim + rows_per_wg - 1) / rows_per_wg;
+  const int r = rows_per_wave(in_dim, out_dim);
+  const size_t grid = (out_dim + 4 * r - 1) / (4 * r);
   if (grid > part_cap) return false;
-  const int k = (int)in_dim, o = (int)out_dim;
-  const unsigned g = (unsigned)grid;
-  switch (kc) {
-    case 1: w8a32_rows_kernel<1, 8, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
-    case 2: w8a32_rows_kernel<2, 4, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
-    case 3: w8a32_rows_kernel<3, 2, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
-    case 4: w8a32_rows_kernel<4, 2, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
-    case 5: w8a32_rows_kernel<5, 1, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
-    case 6: w8a32_rows_kernel<6, 1, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
-    case 7: w8a32_rows_kernel<7, 1, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
-    default: w8a32_rows_kernel<8, 1, true><<<g, 256, 0, st>>>(y, x, w, scales, nullptr, k, o, part); break;
-  }
-  *n_part = g;
+  launch_rows<true>((int)(in_dim / 1024), r, (unsigned)grid, st, y, x, w, scales, nullptr,
+                    (int)in_dim, (int)out_dim, part);
+  *n_part = (unsigned)grid;
   return true;
 }
 }  // namespace qasr
@@ -506,6 +572,54 @@ extern "C" int qasr_linear_nobias_int8_f32(float* y, const float* x, const int8_
                                            const float* scales, size_t seq_len, size_t in_dim,
                                            size_t out_dim, void* stream) {
   return launch_w8a32(y, x, w, scales, nullptr, seq_len, in_dim, out_dim, stream);
+}
+
+extern "C" int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,
+                                                 const int8_t* const* ws,
+                                                 const float* const* scales,
+                                                 const size_t* out_dims, const float* x,
+                                                 size_t seq_len, size_t in_dim, void* stream) {
+  if (n_mats == 0 || seq_len == 0) return QASR_OK;
+  QASR_REQUIRE(ys && ws && scales && out_dims && x, "linear_nobias_int8_multi: null pointer");
+  QASR_REQUIRE(n_mats <= (size_t)kMaxMats, "linear_nobias_int8_multi: at most 4 matrices");
+  bool one_launch = seq_len == 1;
+  size_t total = 0;
+  for (size_t m = 0; m < n_mats; ++m) {
+    QASR_REQUIRE(ys[m] && ws[m] && scales[m], "linear_nobias_int8_multi: null pointer");
+    QASR_REQUIRE(out_dims[m] <= 0x7fffffffu - 64 && in_dim <= 0x7fffffffu,
+                 "linear_nobias_int8_multi: size too large");
+    size_t n;
+    QASR_REQUIRE(mul_ok(in_dim, out_dims[m], &n) && mul_ok(seq_len, in_dim, &n) &&
+                     mul_ok(seq_len, out_dims[m], &n),
+                 "linear_nobias_int8_multi: size overflows");
+    one_launch = one_launch && w8a32_rows_shape(in_dim, ws[m], x);
+    total += out_dims[m];
+  }
+  QASR_REQUIRE(total <= 0x7fffffffu, "linear_nobias_int8_multi: size too large");
+  if (total == 0) return QASR_OK;
+  if (!one_launch) {
+    for (size_t m = 0; m < n_mats; ++m) {
+      const int rc = launch_w8a32(ys[m], x, ws[m], scales[m], nullptr, seq_len, in_dim, out_dims[m],
+                                  stream);
+      if (rc != QASR_OK) return rc;
+    }
+    return QASR_OK;
+  }
+  const int r = rows_per_wave(in_dim, total);
+  MatSet ms{};
+  unsigned wg = 0;
+  for (size_t m = 0; m < n_mats; ++m) {
+    ms.y[m] = ys[m];
+    ms.w[m] = ws[m];
+    ms.s[m] = scales[m];
+    ms.out[m] = (int)out_dims[m];
+    ms.wg_begin[m] = wg;
+    wg += (unsigned)((out_dims[m] + 4 * r - 1) / (4 * r));
+  }
+  for (size_t m = n_mats; m <= (size_t)kMaxMats; ++m) ms.wg_begin[m] = wg;
+  ms.n = (int)n_mats;
+  launch_rows_multi((int)(in_dim / 1024), r, wg, as_stream(stream), ms, x, (int)in_dim);
+  return launch_status("linear_nobias_int8_multi");
 }
 
 extern "C" int qasr_linear_int8_f32(float* y, const float* x, const int8_t* w, const float* scales,

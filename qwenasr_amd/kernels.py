@@ -494,6 +494,24 @@ def linear_nobias_int8(y, x, w_int8, scales, seq_len: int, in_dim: int, out_dim:
               seq_len, in_dim, out_dim, _stream())
 
 
+def linear_nobias_int8_multi(ys, ws: list, x, seq_len: int, in_dim: int) -> None:
+    """Several W8A32 projections of the same x in one launch (q/k/v, decoder.rs:881-886);
+    ``ws`` are QuantWeights, ``ys[m]`` gets ``seq_len * ws[m].out_dim`` floats."""
+    if len(ys) != len(ws):
+        raise ValueError("one output per weight")
+    for y, w in zip(ys, ws):
+        _need(y, F32, seq_len * w.out_dim, "y")
+        _need(w.data, I8, w.out_dim * in_dim, "w")
+        _need(w.scales, F32, w.out_dim, "scales")
+    _need(x, F32, seq_len * in_dim, "x")
+    n = len(ws)
+    arr = ctypes.c_void_p * max(n, 1)
+    _lib.call("qasr_linear_nobias_int8_multi_f32", n, arr(*[y.data_ptr() for y in ys]),
+              arr(*[w.data.data_ptr() for w in ws]), arr(*[w.scales.data_ptr() for w in ws]),
+              (ctypes.c_size_t * max(n, 1))(*[w.out_dim for w in ws]), _ptr(x), seq_len, in_dim,
+              _stream())
+
+
 def linear_int8(y, x, w_int8, scales, bias, seq_len: int, in_dim: int, out_dim: int) -> None:
     """W8A32 linear with optional bias (kernels/mod.rs:664-673)."""
     _need(y, F32, seq_len * out_dim, "y")

@@ -168,3 +168,18 @@ def test_lm_head_workspace_size_query():
     assert _lib.lib().qasr_lm_head_argmax_workspace_bytes(151936) == 8 * 37984
     assert _lib.lib().qasr_lm_head_argmax_workspace_bytes(5) == 16
     assert _lib.lib().qasr_lm_head_argmax_workspace_bytes(0) == 0
+
+
+def test_linear_multi_validation():
+    so = _lib.lib()
+    arr = ctypes.c_void_p * 5
+    sz = ctypes.c_size_t * 5
+    ptrs = arr(*([FAKE.value] * 5))
+    dims = sz(*([16] * 5))
+    assert so.qasr_linear_nobias_int8_multi_f32(5, ptrs, ptrs, ptrs, dims, FAKE, 1, 1024, NULL) == \
+        _lib.QASR_ERR_INVALID_ARG
+    assert "at most 4" in last_error()
+    nul = arr(FAKE.value, 0, FAKE.value, FAKE.value, FAKE.value)
+    assert so.qasr_linear_nobias_int8_multi_f32(2, nul, ptrs, ptrs, dims, FAKE, 1, 1024, NULL) == \
+        _lib.QASR_ERR_INVALID_ARG
+    assert so.qasr_linear_nobias_int8_multi_f32(0, None, None, None, None, None, 1, 1024, NULL) == 0

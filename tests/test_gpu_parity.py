@@ -552,11 +552,45 @@ def make_qweight(r, rows, cols):
     return oracle.quantize_f32_to_int8(w, rows, cols)
 
 
+@pytest.mark.parametrize("seq,in_dim,outs", [
+    (1, 2048, (2048, 1024, 1024)),       # 1.7B q/k/v
+    (1, 1024, (2048, 1024, 1024)),       # 0.6B q/k/v
+    (1, 2048, (1, 5, 4096, 7)),          # four matrices, ragged row tails
+    (1, 6144, (2048, 3)),
+    (3, 2048, (2048, 1024)),             # several tokens: one launch per matrix
+    (1, 1000, (17, 33)),                 # in_dim off the vector path
+])
+def test_linear_nobias_int8_multi(dev, seq, in_dim, outs):
+    """One launch over several matrices of the same x equals the separate
+    linear_nobias_int8 calls bit for bit (each row's dot is computed the same
+    way whichever wave owns it), and the oracle within the fp32 tolerance."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(29, seq, in_dim, len(outs))
+    x = normal(r, seq * in_dim)
+    xt = dev_t(x, dev)
+    ws, refs = [], []
+    for o in outs:
+        wq, sc = make_qweight(r, o, in_dim)
+        ws.append(K.QuantWeight(dev_t(wq, dev), dev_t(sc, dev), o, in_dim))
+        refs.append(oracle.linear_nobias_int8(x, wq, sc, seq, in_dim, o))
+    ys = [torch.full((seq * o,), 7.0, device=dev) for o in outs]
+    K.linear_nobias_int8_multi(ys, ws, xt, seq, in_dim)
+    for o, y, w, ref in zip(outs, ys, ws, refs):
+        z = torch.empty(seq * o, device=dev)
+        K.linear_nobias_int8(z, xt, w.data, w.scales, seq, in_dim, o)
+        np.testing.assert_array_equal(host(y), host(z))
+        assert_close(host(y), ref, RTOL, ATOL, f"multi out={o}")
+
+
 @pytest.mark.parametrize("seq,in_dim,out_dim", [(1, 2048, 12288), (4, 1024, 3072), (3, 2048, 2048),
                                                 (2, 100, 33),
                                                 # one token: R rows per wave, ragged row tails
                                                 (1, 1024, 1001), (1, 3072, 2047), (1, 4096, 33),
-                                                (1, 6144, 2048), (1, 2048, 1)])
+                                                (1, 6144, 2048), (1, 2048, 1),
+                                                # rows per wave 1, 2 and 8 by output rows
+                                                (1, 2048, 1024), (1, 2048, 4096), (1, 8192, 64),
+                                                (1, 1024, 40000)])
 def test_linear_nobias_int8_w8a32(dev, seq, in_dim, out_dim):
     from qwenasr_amd import kernels as K
 
