@@ -14,6 +14,7 @@ random-init weights -- no checkpoints):
   attn_decode   1.7B decode attention at position 2047 (keys split over workgroups), 28 layers
   attn_prefill  0.6B causal prefill attention, T=512
   lm_head       0.6B INT8 lm_head [151936,1024] logits + greedy argmax, B=1
+  decode_step   1.7B INT8 decode of one token, all 28 layers + lm_head argmax on the device (tokens/s)
 
 A step is one pass of the workload's kernel chain over one buffer set; sets
 rotate so the working set exceeds the 256 MB last-level cache. Steps are
@@ -372,6 +373,58 @@ class W8A32Decode(Workload):
                 "projections": {n: f"[{o},{i}]" for n, (o, i) in self.SHAPES.items()}}
 
 
+class DecodeStep(Workload):
+    name = "decode_step"
+    description = ("qwen3-asr-1.7b INT8 decode of one token at position 1023, B=1, fully on the device: "
+                   "28 layers of input RMSNorm, q/k/v (one launch), q/k norm+RoPE+KV store, split "
+                   "attention over 1024 cached rows, o, add+RMSNorm, gate/up+SwiGLU, down; final norm and "
+                   "INT8 lm_head [151936,2048] greedy argmax")
+    unit_tokens = 1
+    dtype = "int8/f32"
+    POS = 1023
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+        from qwenasr_amd.decoder import DecoderInt8
+
+        c = DEC_1_7B
+        H, I, nq, nk, hd, L = c["hidden"], c["inter"], c["n_heads"], c["n_kv_heads"], c["head_dim"], 28
+
+        def qw(o, i):  # int8 weights and per-row scales with the quantizer's value range
+            q = torch.randint(-127, 128, (o * i,), generator=self.gen, device=dev, dtype=torch.int8)
+            return K.QuantWeight(q, self.randn(o, 1e-4, 1e-3).abs_(), o, i)
+
+        def gain(n):
+            return self.randn(n, 0.1, 1.0)
+
+        layers = [{"wq": qw(nq * hd, H), "wk": qw(nk * hd, H), "wv": qw(nk * hd, H), "wo": qw(H, nq * hd),
+                   "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": gain(hd), "k_norm": gain(hd),
+                   "input_norm": gain(H), "post_attn_norm": gain(H)} for _ in range(L)]
+        weights = {"layers": layers, "norm": gain(H), "lm_head": qw(VOCAB, H)}
+        self.dec = DecoderInt8(weights, H, I, L, nq, nk, hd, c["eps"], c["theta"], max_seq=2048, device=dev)
+        self.dec.kv.k.normal_(generator=self.gen)  # rows 0..1022: an earlier context
+        self.dec.kv.v.normal_(generator=self.gen)
+        self.dec.kv.len = self.POS
+        self.dec.prepare(self.POS)
+        self.embed = [self.randn(H) for _ in range(4)]
+        kv = nk * hd
+        layer_bytes = (sum(w.out_dim * w.in_dim + w.out_dim * F for k, w in layers[0].items()
+                           if isinstance(w, K.QuantWeight))
+                       + (2 * hd + 2 * H) * F                      # norm gains
+                       + 2 * (self.POS + 1) * kv * F              # k/v rows read by attention
+                       + 2 * kv * F)                              # the new k/v rows
+        head_bytes = VOCAB * H + 2 * VOCAB * F + H * F + 4       # lm_head weights, scales, logits, token
+        step_bytes = L * layer_bytes + head_bytes
+        self.kernels = {"decode_token": (lambda i: self.dec.decode(self.embed[i % 4], self.POS), step_bytes)}
+        self.step_bytes = step_bytes
+        self.tokens_per_step = 1.0
+
+    def config(self):
+        return {"batch": 1, "position": self.POS, "hidden": 2048, "intermediate": 6144,
+                "heads": "16q/8kv x 128", "layers": 28, "vocab": VOCAB}
+
+
 class AttnDecode(Workload):
     name = "attn_decode"
     description = ("qwen3-asr-1.7b decode attention at position 2047: q[16,128] against a 2048-row "
@@ -477,7 +530,7 @@ class LmHead(Workload):
 
 WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c4": C4Int8Matvec,
              "c5": C5BatchedDecode, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
-             "lm_head": LmHead}
+             "lm_head": LmHead, "decode_step": DecodeStep}
 
 
 # ---------------------------------------------------------------------------
@@ -658,6 +711,35 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
         return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
                 "ms_per_step": per * 1e3, "tokens_per_s": T / per,
                 "sample": f"{n} T=512 prefill attentions on the oracle, one thread"}
+    if name == "decode_step":
+        from oracle.decoder import decode_int8_step
+
+        c = DEC_1_7B
+        H, I, nq, nk, hd = c["hidden"], c["inter"], c["n_heads"], c["n_kv_heads"], c["head_dim"]
+        pos = DecodeStep.POS
+
+        def qw(o, i):
+            return (r.integers(-127, 128, (o, i), dtype=np.int8), (1e-3 + 1e-4 * r.random(o)).astype(np.float32))
+
+        def gain(n):
+            return (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+
+        layer = {"wq": qw(nq * hd, H), "wk": qw(nk * hd, H), "wv": qw(nk * hd, H), "wo": qw(H, nq * hd),
+                 "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": gain(hd), "k_norm": gain(hd),
+                 "input_norm": gain(H), "post_attn_norm": gain(H)}
+        w = {"layers": [layer] * 28, "norm": gain(H), "lm_head": qw(VOCAB, H)}
+        kc = r.standard_normal((28, pos + 1, nk * hd), dtype=np.float32)
+        vc = r.standard_normal((28, pos + 1, nk * hd), dtype=np.float32)
+        x = r.standard_normal(H, dtype=np.float32)
+        threads = min(nproc, 16)
+        n, dt = run_until(lambda: decode_int8_step(w, kc, vc, pos, x, nq, nk, hd, c["eps"], c["theta"],
+                                                   threads), seconds)
+        per = dt / n
+        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "ms_per_step": per * 1e3, "tokens_per_s": 1.0 / per,
+                "sample": f"{n} decode tokens at position {pos} on the oracle's restated decode step "
+                          f"(decoder.rs:848-965): INT8 matvecs on {threads} threads, attention on one, "
+                          "one layer's weights shared by the 28 layers (LLC-warm)"}
     if name == "lm_head":
         V, H = VOCAB, 1024
         wq, ws = oracle.quantize_f32_to_int8(0.02 * r.standard_normal(V * H, dtype=np.float32), V, H)

@@ -226,6 +226,16 @@ int qasr_linear_nobias_int8_f32(float* y, const float* x, const int8_t* w,
                                 const float* scales, size_t seq_len,
                                 size_t in_dim, size_t out_dim, void* stream);
 
+/* The INT8 decode step's gate/up projection and SwiGLU in one call
+ * (decoder.rs:912-921): gate_up = linear_nobias_int8(x, w_gate_up) on the
+ * row-interleaved fused weight [2*intermediate, in_dim] (g0, u0, g1, u1, ...,
+ * with interleaved scales), then out[s, j] = g / (1 + expf(-g)) * u with
+ * g = gate_up[s, 2j], u = gate_up[s, 2j + 1] -- the decode loop's libm SwiGLU,
+ * not the prefill fast_exp form. The gate_up values are never written. */
+int qasr_gate_up_swiglu_int8_f32(float* out, const float* x, const int8_t* w_gate_up,
+                                 const float* scales_gate_up, size_t seq_len, size_t in_dim,
+                                 size_t intermediate, void* stream);
+
 /* Up to 4 W8A32 projections of the same input in one launch: for m < n_mats,
  * ys[m][s, :] = qasr_linear_nobias_int8_f32(x[s, :], ws[m], scales[m]) with
  * out_dims[m] rows (the q/k/v calls of one decode step share x:

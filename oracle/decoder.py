@@ -1,0 +1,64 @@
+"""CPU restatement of the reference's INT8 decode step -- TEST INFRASTRUCTURE ONLY.
+
+``decode_int8_step`` follows ``decoder.rs:848-965`` op by op with the oracle's
+kernel restatements (oracle/qasr_oracle.c): input RMSNorm, the three
+``linear_nobias_int8`` projections, per-head RMSNorm + NeoX RoPE at ``pos``,
+the K/V row copies into the cache, ``causal_attention`` over rows 0..pos, the
+o projection and residual add, post-attention RMSNorm, the fused gate/up
+projection with the loop's libm SwiGLU (decoder.rs:916-921), the down
+projection and residual add; then the final RMSNorm, the lm_head logits and
+the greedy argmax (decoder.rs:929-963). Only tests/ and bench.py's
+cpu_baseline leg use it.
+
+Pinned by its parts: every primitive it calls is pinned in tests/test_oracle.py;
+the composition is checked against a float64 numpy evaluation of the same
+formulas in tests/test_oracle.py::test_decode_step_composition.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import (add_inplace, apply_rope_neox, argmax_rows, causal_attention, linear_nobias_int8,
+               rms_norm, rms_norm_per_head, rope_table, swiglu_split)
+
+
+def decode_int8_step(w: dict, k_cache: np.ndarray, v_cache: np.ndarray, pos: int,
+                     embed: np.ndarray, n_heads: int, n_kv_heads: int, head_dim: int,
+                     eps: float = 1e-6, theta: float = 1e6, threads: int = 1):
+    """One token. ``w``: {"layers": [{"wq": (int8 [out,in], scales), ..., "gate_up": fused
+    interleaved (w, s), "down", "q_norm", "k_norm", "input_norm", "post_attn_norm"}], "norm",
+    "lm_head": (w, s)}. ``k_cache``/``v_cache``: [layers, max_seq, kv_dim] float32, row ``pos``
+    is written. Returns (token, final normed hidden, logits)."""
+    H = embed.size
+    q_dim, kv_dim = n_heads * head_dim, n_kv_heads * head_dim
+    cos, sin = rope_table(pos + 1, head_dim, theta)
+    c, s = cos[pos * head_dim:(pos + 1) * head_dim], sin[pos * head_dim:(pos + 1) * head_dim]
+    scale = 1.0 / math.sqrt(head_dim)
+    x = np.array(embed, np.float32)
+    for l, lw in enumerate(w["layers"]):
+        xn = rms_norm(x, lw["input_norm"], 1, H, eps)
+        q = linear_nobias_int8(xn, *lw["wq"], 1, H, q_dim, threads)
+        k = linear_nobias_int8(xn, *lw["wk"], 1, H, kv_dim, threads)
+        v = linear_nobias_int8(xn, *lw["wv"], 1, H, kv_dim, threads)
+        q = rms_norm_per_head(q, lw["q_norm"], 1, n_heads, head_dim, eps)
+        k = rms_norm_per_head(k, lw["k_norm"], 1, n_kv_heads, head_dim, eps)
+        q = apply_rope_neox(q, c, s, 1, n_heads, head_dim)
+        k = apply_rope_neox(k, c, s, 1, n_kv_heads, head_dim)
+        k_cache[l, pos] = k
+        v_cache[l, pos] = v
+        attn = causal_attention(q, k_cache[l, :pos + 1].ravel(), v_cache[l, :pos + 1].ravel(), 1, pos + 1,
+                                n_heads, n_kv_heads, head_dim, scale, pos)
+        proj = linear_nobias_int8(attn, *lw["wo"], 1, q_dim, H, threads)
+        add_inplace(x, proj)
+        xn = rms_norm(x, lw["post_attn_norm"], 1, H, eps)
+        inter = lw["gate_up"][1].size // 2
+        gu = linear_nobias_int8(xn, *lw["gate_up"], 1, H, 2 * inter, threads)
+        ffn = swiglu_split(gu[0::2].copy(), gu[1::2].copy())
+        down = linear_nobias_int8(ffn, *lw["down"], 1, inter, H, threads)
+        add_inplace(x, down)
+    xn = rms_norm(x, w["norm"], 1, H, eps)
+    vocab = w["lm_head"][1].size
+    logits = linear_nobias_int8(xn, *w["lm_head"], 1, H, vocab, threads)
+    return int(argmax_rows(logits, 1, vocab)[0]), xn, logits

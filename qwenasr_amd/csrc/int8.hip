@@ -121,10 +121,16 @@ __global__ __launch_bounds__(256) void w8a32_vec_kernel(float* y, const float* x
 // (value, index) in the lm_head argmax order and writes it to part[blockIdx.x];
 // waves past the last row then stay to the end (their loads clamp to the last
 // row and they offer no candidate).
-template <int KCH, int R, bool PART>
+// Epilogues of the one-token matvec: plain rows, rows + per-workgroup argmax
+// candidate (lm_head), or the decode loop's SwiGLU on interleaved gate/up rows.
+enum RowsEpi { kEpiRows = 0, kEpiArgmax = 1, kEpiSwiglu = 2 };
+
+template <int KCH, int R, int EPI>
 QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const float* scales,
                               const float* bias, int in_dim, int out_dim, unsigned block,
                               float2* part) {
+  constexpr bool PART = EPI == kEpiArgmax;
+  static_assert(EPI != kEpiSwiglu || R % 2 == 0, "SwiGLU pairs sit in one wave");
   const int lane = threadIdx.x & (kWave - 1);
   const int o0 = (int)(block * (256 / kWave) + threadIdx.x / kWave) * R;
   if constexpr (!PART) {
@@ -171,7 +177,13 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
     const int o = o0 + lane;
     res = a * scales[o];
     if (bias) res += bias[o];
-    y[o] = res;
+    if constexpr (EPI != kEpiSwiglu) y[o] = res;
+  }
+  if constexpr (EPI == kEpiSwiglu) {
+    // rows o0 + 2i and o0 + 2i + 1 are gate_i and up_i (decoder.rs:916-921):
+    // out[(o0 + lane) / 2] = g / (1 + expf(-g)) * u
+    const float u = __shfl_down(res, 1, kWave);
+    if (mine && (lane & 1) == 0) y[(o0 + lane) >> 1] = silu_expf(res) * u;
   }
   if constexpr (PART) {
     __shared__ float sv[256 / kWave];
@@ -205,12 +217,12 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
   }
 }
 
-template <int KCH, int R, bool PART = false>
+template <int KCH, int R, int EPI = kEpiRows>
 __global__ __launch_bounds__(256) void w8a32_rows_kernel(float* y, const float* x, const int8_t* w,
                                                          const float* scales, const float* bias,
                                                          int in_dim, int out_dim,
                                                          float2* part = nullptr) {
-  w8a32_rows_body<KCH, R, PART>(y, x, w, scales, bias, in_dim, out_dim, blockIdx.x, part);
+  w8a32_rows_body<KCH, R, EPI>(y, x, w, scales, bias, in_dim, out_dim, blockIdx.x, part);
 }
 
 // Several matrices of the same input in one launch (the q/k/v projections):
@@ -242,7 +254,32 @@ __global__ __launch_bounds__(256) void w8a32_rows_multi_kernel(MatSet ms, const 
       out = ms.out[m];
       b0 = ms.wg_begin[m];
     }
-  w8a32_rows_body<KCH, R, false>(y, x, w, sc, nullptr, in_dim, out, blockIdx.x - b0, nullptr);
+  w8a32_rows_body<KCH, R, kEpiRows>(y, x, w, sc, nullptr, in_dim, out, blockIdx.x - b0, nullptr);
+}
+
+// Gate/up pairs for any shape: one wave per (token, output j) takes the dots
+// of interleaved rows 2j (gate) and 2j + 1 (up) and applies the decode SwiGLU.
+__global__ __launch_bounds__(256) void gate_up_swiglu_w8a32_pairs_kernel(
+    float* out, const float* x, const int8_t* w, const float* scales, int seq, int in_dim,
+    int inter) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long item = (long long)blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (item >= (long long)seq * inter) return;
+  const int s = (int)(item / inter), j = (int)(item % inter);
+  const int8_t* wg = w + (size_t)(2 * j) * in_dim;
+  const int8_t* wu = wg + in_dim;
+  const float* xs = x + (size_t)s * in_dim;
+  float ag = 0.0f, au = 0.0f;
+  for (int k = lane; k < in_dim; k += kWave) {
+    ag = __builtin_fmaf((float)wg[k], xs[k], ag);
+    au = __builtin_fmaf((float)wu[k], xs[k], au);
+  }
+  ag = wave_sum(ag);
+  au = wave_sum(au);
+  if (lane == 0) {
+    const float g = ag * scales[2 * j], u = au * scales[2 * j + 1];
+    out[(size_t)s * inter + j] = silu_expf(g) * u;
+  }
 }
 
 // Rows per wave of a one-token matvec: the largest power of two that leaves
@@ -261,20 +298,24 @@ bool w8a32_rows_shape(size_t in_dim, const void* w, const void* x) {
 }
 
 // Launches the one-token kernel for (in_dim / 1024, r) on `grid` workgroups.
-template <bool PART>
+template <int EPI>
 void launch_rows(int kch, int r, unsigned grid, hipStream_t st, float* y, const float* x,
                  const int8_t* w, const float* scales, const float* bias, int k, int o,
                  float2* part) {
 #define QASR_ROWS(KCH, R)                                                                        \
   if (kch == KCH && r == R) {                                                                    \
-    w8a32_rows_kernel<KCH, R, PART><<<grid, 256, 0, st>>>(y, x, w, scales, bias, k, o, part);    \
+    w8a32_rows_kernel<KCH, R, EPI><<<grid, 256, 0, st>>>(y, x, w, scales, bias, k, o, part);     \
     return;                                                                                      \
   }
-  QASR_ROWS(1, 1) QASR_ROWS(1, 2) QASR_ROWS(1, 4) QASR_ROWS(1, 8)
-  QASR_ROWS(2, 1) QASR_ROWS(2, 2) QASR_ROWS(2, 4)
-  QASR_ROWS(3, 1) QASR_ROWS(3, 2) QASR_ROWS(4, 1) QASR_ROWS(4, 2)
-  QASR_ROWS(5, 1) QASR_ROWS(5, 2) QASR_ROWS(6, 1) QASR_ROWS(6, 2)
-  QASR_ROWS(7, 1) QASR_ROWS(7, 2) QASR_ROWS(8, 1) QASR_ROWS(8, 2)
+  if constexpr (EPI != kEpiSwiglu) {
+    QASR_ROWS(1, 1) QASR_ROWS(2, 1) QASR_ROWS(3, 1) QASR_ROWS(4, 1)
+    QASR_ROWS(5, 1) QASR_ROWS(6, 1) QASR_ROWS(7, 1) QASR_ROWS(8, 1)
+  }
+  QASR_ROWS(1, 2) QASR_ROWS(1, 4) QASR_ROWS(1, 8)
+  QASR_ROWS(2, 2) QASR_ROWS(2, 4)
+  QASR_ROWS(3, 2) QASR_ROWS(4, 2)
+  QASR_ROWS(5, 2) QASR_ROWS(6, 2)
+  QASR_ROWS(7, 2) QASR_ROWS(8, 2)
 #undef QASR_ROWS
 }
 
@@ -533,8 +574,8 @@ static int launch_w8a32(float* y, const float* x, const int8_t* w, const float* 
   const bool vec = w8a32_rows_shape(in_dim, w, x);
   if (vec && seq_len == 1) {
     const int r = rows_per_wave(in_dim, out_dim);
-    launch_rows<false>((int)(in_dim / 1024), r, (unsigned)((out_dim + 4 * r - 1) / (4 * r)), st, y, x,
-                       w, scales, bias, k, o, nullptr);
+    launch_rows<kEpiRows>((int)(in_dim / 1024), r, (unsigned)((out_dim + 4 * r - 1) / (4 * r)), st,
+                          y, x, w, scales, bias, k, o, nullptr);
   } else if (vec) {
     switch (in_dim / 1024) {
       case 1: w8a32_vec_kernel<1><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
@@ -561,8 +602,8 @@ bool launch_w8a32_argmax_partials(float* y, const float* x, const int8_t* w, con
   const int r = rows_per_wave(in_dim, out_dim);
   const size_t grid = (out_dim + 4 * r - 1) / (4 * r);
   if (grid > part_cap) return false;
-  launch_rows<true>((int)(in_dim / 1024), r, (unsigned)grid, st, y, x, w, scales, nullptr,
-                    (int)in_dim, (int)out_dim, part);
+  launch_rows<kEpiArgmax>((int)(in_dim / 1024), r, (unsigned)grid, st, y, x, w, scales, nullptr,
+                         (int)in_dim, (int)out_dim, part);
   *n_part = (unsigned)grid;
   return true;
 }
@@ -572,6 +613,33 @@ extern "C" int qasr_linear_nobias_int8_f32(float* y, const float* x, const int8_
                                            const float* scales, size_t seq_len, size_t in_dim,
                                            size_t out_dim, void* stream) {
   return launch_w8a32(y, x, w, scales, nullptr, seq_len, in_dim, out_dim, stream);
+}
+
+extern "C" int qasr_gate_up_swiglu_int8_f32(float* out, const float* x, const int8_t* w_gate_up,
+                                            const float* scales_gate_up, size_t seq_len,
+                                            size_t in_dim, size_t intermediate, void* stream) {
+  if (seq_len == 0 || intermediate == 0) return QASR_OK;
+  QASR_REQUIRE(out && x && w_gate_up && scales_gate_up, "gate_up_swiglu_int8: null pointer");
+  QASR_REQUIRE(in_dim > 0 && in_dim <= 0x7fffffffu && seq_len <= 0x7fffffffu &&
+                   intermediate <= 0x3fffffffu - 64,
+               "gate_up_swiglu_int8: size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(2 * intermediate, in_dim, &n) && mul_ok(seq_len, in_dim, &n) &&
+                   mul_ok(seq_len, intermediate, &n) && n < ((size_t)1 << 33),
+               "gate_up_swiglu_int8: size overflows");
+  hipStream_t st = as_stream(stream);
+  const size_t rows = 2 * intermediate;
+  if (seq_len == 1 && w8a32_rows_shape(in_dim, w_gate_up, x)) {
+    const int r = rows_per_wave(in_dim, rows) < 2 ? 2 : rows_per_wave(in_dim, rows);
+    launch_rows<kEpiSwiglu>((int)(in_dim / 1024), r, (unsigned)((rows + 4 * r - 1) / (4 * r)), st,
+                            out, x, w_gate_up, scales_gate_up, nullptr, (int)in_dim, (int)rows,
+                            nullptr);
+  } else {
+    const long long items = (long long)seq_len * (long long)intermediate;
+    gate_up_swiglu_w8a32_pairs_kernel<<<(unsigned)((items + 3) / 4), 256, 0, st>>>(
+        out, x, w_gate_up, scales_gate_up, (int)seq_len, (int)in_dim, (int)intermediate);
+  }
+  return launch_status("gate_up_swiglu_int8");
 }
 
 extern "C" int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,

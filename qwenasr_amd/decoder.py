@@ -1,0 +1,96 @@
+"""Device-resident INT8 decoder step: the reference's ``DecoderInt8`` decode
+(crates/qwen-asr/src/decoder.rs:848-965) over the C-ABI kernels.
+
+Per layer, in the reference's order:
+  input RMSNorm (fused with the previous layer's residual add), q/k/v
+  projections (one launch), q/k head RMSNorm + RoPE with the K/V rows written
+  into the cache (one launch), causal attention over the layer's cache block
+  (keys split over workgroups), o projection, residual add + post-attention
+  RMSNorm (one launch), gate/up projection + SwiGLU (one launch), down
+  projection.
+Then the last residual add + final RMSNorm and the INT8 lm_head with the greedy
+argmax (decoder.rs:929-963). Everything stays on the device: the token id is
+written to a device int32, and the hidden state, KV cache and RoPE tables
+never leave HBM.
+
+Weights come from ``qint8.load_decoder_int8`` (or any dict of the same
+layout); ``DecoderInt8.decode`` runs one token and can be captured in a HIP
+graph (no host synchronisation, no allocation after construction for a fixed
+position).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import kernels as K
+
+
+class DecoderInt8:
+    def __init__(self, weights: dict, hidden: int, intermediate: int, n_layers: int, n_heads: int = 16,
+                 n_kv_heads: int = 8, head_dim: int = 128, eps: float = 1e-6, theta: float = 1e6,
+                 vocab: int | None = None, max_seq: int = 256, device="cuda"):
+        self.w = weights
+        self.H, self.I, self.L = hidden, intermediate, n_layers
+        self.nq, self.nk, self.hd = n_heads, n_kv_heads, head_dim
+        self.eps, self.theta = eps, theta
+        lm = weights.get("lm_head") or weights["tok_embeddings"]  # tied weights: decoder.rs:951-954
+        self.lm = lm
+        self.vocab = vocab if vocab is not None else lm.out_dim
+        dev = device
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.x = torch.zeros(hidden, **f32)
+        self.x_norm = torch.empty(hidden, **f32)
+        self.q = torch.empty(n_heads * head_dim, **f32)
+        self.k = torch.empty(n_kv_heads * head_dim, **f32)
+        self.v = torch.empty(n_kv_heads * head_dim, **f32)
+        self.attn = torch.empty(n_heads * head_dim, **f32)
+        self.proj = torch.empty(hidden, **f32)
+        self.ffn = torch.empty(intermediate, **f32)
+        self.down = torch.empty(hidden, **f32)
+        self.logits = torch.empty(self.vocab, **f32)
+        self.token = torch.empty(1, dtype=torch.int32, device=dev)
+        self.kv = K.KvCache(n_layers, max_seq, n_kv_heads * head_dim, dev)
+        self.rope = K.RopeCache(dev)
+        self.attn_ws = K.attention_workspace(1, n_heads, head_dim, dev)
+        self.lm_ws = K.lm_head_workspace(self.vocab, dev)
+        self.scale = 1.0 / math.sqrt(head_dim)
+
+    def prepare(self, pos: int) -> None:
+        """Host-side growth before a decode at ``pos`` (decoder.rs:866-872):
+        cache capacity and RoPE rows. Nothing here runs in the timed step."""
+        if pos >= self.kv.max_seq:
+            self.kv.grow(pos + 1024)
+        self.rope.ensure(pos + 1, self.hd, self.theta)
+
+    def decode(self, embed: torch.Tensor, pos: int) -> None:
+        """One token at position ``pos`` (the cache holds rows 0..pos-1):
+        ``self.token`` receives the greedy next token, ``self.x_norm`` the final
+        normed hidden state. Call ``prepare(pos)`` first."""
+        H, I, nq, nk, hd, eps = self.H, self.I, self.nq, self.nk, self.hd, self.eps
+        self.x.copy_(embed)
+        for l, lw in enumerate(self.w["layers"]):
+            if l == 0:
+                K.rms_norm(self.x_norm, self.x, lw["input_norm"], 1, H, eps)
+            else:  # previous layer's residual add fused with this layer's input norm
+                K.add_rms_norm(self.x, self.down, lw["input_norm"], self.x_norm, 1, H, eps)
+            K.linear_nobias_int8_multi([self.q, self.k, self.v], [lw["wq"], lw["wk"], lw["wv"]],
+                                       self.x_norm, 1, H)
+            K.head_rms_norm_rope_kv(self.q, self.k, self.v, lw["q_norm"], lw["k_norm"], self.rope, None,
+                                    pos, 1, nq, nk, hd, eps, self.kv.k_layer_block(l),
+                                    self.kv.v_layer_block(l), self.kv.max_seq)
+            K.causal_attention_split(self.attn, self.q, self.kv.k_layer_block(l), self.kv.v_layer_block(l),
+                                     1, pos + 1, nq, nk, hd, self.scale, pos, self.attn_ws)
+            wo = lw["wo"]
+            K.linear_nobias_int8(self.proj, self.attn, wo.data, wo.scales, 1, nq * hd, H)
+            K.add_rms_norm(self.x, self.proj, lw["post_attn_norm"], self.x_norm, 1, H, eps)
+            K.gate_up_swiglu_int8(self.ffn, self.x_norm, lw["gate_up"], 1, H, I)
+            dn = lw["down"]
+            K.linear_nobias_int8(self.down, self.ffn, dn.data, dn.scales, 1, I, H)
+        K.add_rms_norm(self.x, self.down, self.w["norm"], self.x_norm, 1, H, eps)
+        K.lm_head_int8_argmax(self.token, self.logits, self.x_norm, self.lm, 1, H, self.vocab, self.lm_ws)
+
+    def finish(self, pos: int) -> None:
+        """The cache now holds rows 0..pos (decoder.rs:926)."""
+        self.kv.len = pos + 1

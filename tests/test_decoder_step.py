@@ -1,0 +1,104 @@
+"""The whole INT8 decode step on the device (qwenasr_amd/decoder.py) against
+the oracle's restatement of decoder.rs:848-965, with the weights going through
+a .qint8 V2 file, the C-ABI reader, the device upload and the gate/up
+interleave on the way.
+
+Tolerance: each kernel holds rel/abs 1e-5; the step chains ~10 of them per
+layer, each feeding the next, so the final hidden state, the logits and the
+cache rows are compared at rel/abs 1e-4 (measured error is printed on
+failure). The token must equal the oracle's whenever the oracle's top two
+logits are further apart than the logit tolerance.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import qint8_format as fmt
+from oracle.decoder import decode_int8_step
+from tests.test_oracle import small_decoder
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def write_model(path, w, L):
+    quant, f32 = [], []
+    for i, lw in enumerate(w["layers"]):
+        lp = f"thinker.model.layers.{i}"
+        for n, key in (("self_attn.q_proj", "wq"), ("self_attn.k_proj", "wk"), ("self_attn.v_proj", "wv"),
+                       ("self_attn.o_proj", "wo"), ("mlp.gate_proj", "gate"), ("mlp.up_proj", "up"),
+                       ("mlp.down_proj", "down")):
+            q, s = lw[key]
+            quant.append((f"{lp}.{n}.weight", list(q.shape), q, s))
+        for n, key in (("self_attn.q_norm", "q_norm"), ("self_attn.k_norm", "k_norm"),
+                       ("input_layernorm", "input_norm"), ("post_attention_layernorm", "post_attn_norm")):
+            f32.append((f"{lp}.{n}.weight", [lw[key].size], lw[key]))
+    q, s = w["lm_head"]
+    quant.append(("thinker.lm_head.weight", list(q.shape), q, s))
+    quant.append(("thinker.model.embed_tokens.weight", list(q.shape), q, s))
+    f32.append(("thinker.model.norm.weight", [w["norm"].size], w["norm"]))
+    path.write_bytes(fmt.write_v2(quant, f32, []))
+
+
+@pytest.mark.parametrize("H,I,vocab", [(1024, 3072, 3000), (2048, 6144, 1000)])
+def test_decode_steps_match_the_oracle(tmp_path, dev, H, I, vocab):
+    from qwenasr_amd import qint8
+    from qwenasr_amd.decoder import DecoderInt8
+
+    L, nq, nk, hd, n_pos = 2, 16, 8, 128, 5
+    r = np.random.default_rng([31, H])
+    w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
+    p = tmp_path / "model.qint8"
+    write_model(p, w, L)
+    with qint8.QuantFile.open(str(p)) as qf:
+        dims = qint8.detect_decoder_dims(qf)
+        assert (dims.hidden, dims.intermediate, dims.lm_head_dim) == (H, I, vocab)
+        dims.n_layers = L
+        weights = qint8.load_decoder_int8(qf, dims, dev)
+    dec = DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=4, device=dev)
+    kc = np.zeros((L, 16, nk * hd), np.float32)
+    vc = np.zeros_like(kc)
+    for pos in range(n_pos):  # the cache grows past its first 4 rows at pos 4
+        x = r.standard_normal(H).astype(np.float32)
+        tok, xn, logits = decode_int8_step(w, kc, vc, pos, x, nq, nk, hd, threads=8)
+        dec.prepare(pos)
+        dec.decode(torch.from_numpy(x).to(dev), pos)
+        dec.finish(pos)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(dec.x_norm.cpu().numpy(), xn, rtol=TOL, atol=TOL)
+        np.testing.assert_allclose(dec.logits.cpu().numpy(), logits, rtol=TOL, atol=TOL)
+        kv = nk * hd
+        for l in range(L):
+            kg = dec.kv.k_layer(l).cpu().numpy().reshape(pos + 1, kv)
+            vg = dec.kv.v_layer(l).cpu().numpy().reshape(pos + 1, kv)
+            np.testing.assert_allclose(kg, kc[l, :pos + 1], rtol=TOL, atol=TOL)
+            np.testing.assert_allclose(vg, vc[l, :pos + 1], rtol=TOL, atol=TOL)
+        top2 = np.sort(logits)[-2:]
+        got = int(dec.token.cpu().numpy()[0])
+        assert got == int(oracle.argmax_rows(dec.logits.cpu().numpy(), 1, vocab)[0])
+        if top2[1] - top2[0] > 2 * TOL * (1 + abs(top2[1])):
+            assert got == tok, (pos, got, tok)
+
+
+def test_gate_up_swiglu_int8_matches_linear_plus_loop(dev):
+    """The fused gate/up + SwiGLU entry against linear_nobias_int8 + the
+    decode loop's SwiGLU on the oracle, one token (fused epilogue) and several
+    tokens / off-vector shapes (pair kernel)."""
+    from qwenasr_amd import kernels as K
+
+    r = np.random.default_rng(32)
+    for seq, H, I in ((1, 2048, 6144), (1, 1024, 3072), (1, 3072, 100), (3, 1024, 64), (1, 1000, 77)):
+        wf = (0.02 * r.standard_normal((2 * I, H))).astype(np.float32)
+        q, s = oracle.quantize_f32_to_int8(wf, 2 * I, H)
+        x = r.standard_normal(seq * H).astype(np.float32)
+        gu = oracle.linear_nobias_int8(x, q, s, seq, H, 2 * I).reshape(seq, 2 * I)
+        ref = oracle.swiglu_split(gu[:, 0::2].ravel().copy(), gu[:, 1::2].ravel().copy())
+        out = torch.full((seq * I,), 9.0, device=dev)
+        w = K.QuantWeight(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), 2 * I, H)
+        K.gate_up_swiglu_int8(out, torch.from_numpy(x).to(dev), w, seq, H, I)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5, err_msg=f"{seq},{H},{I}")

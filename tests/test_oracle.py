@@ -331,3 +331,95 @@ def test_argmax_rows_semantics():
     r = np.random.default_rng(4)
     y = r.standard_normal((6, 1000)).astype(np.float32)
     np.testing.assert_array_equal(oracle.argmax_rows(y, 6, 1000), y.argmax(axis=1))
+
+
+# --- the INT8 decode step composition (decoder.rs:848-965) -------------------------
+def _f64_decode(w, kc, vc, pos, x, nq, nk, hd, eps=1e-6, theta=1e6):
+    """float64 numpy evaluation of the decode step's formulas (no oracle kernels)."""
+    H = x.size
+    half = hd // 2
+    inv = theta ** (-(2.0 * np.arange(half)) / hd)
+    ang = pos * inv
+    cos, sin = np.cos(ang), np.sin(ang)
+
+    def rms(v, g):
+        return v / np.sqrt(np.mean(v * v) + eps) * g
+
+    def lin(v, ws):
+        return (ws[0].astype(np.float64) @ v) * ws[1]
+
+    def heads(v, n, g):
+        v = v.reshape(n, hd)
+        v = v / np.sqrt(np.mean(v * v, axis=1, keepdims=True) + eps) * g
+        a, b = v[:, :half], v[:, half:]
+        return np.concatenate([a * cos - b * sin, b * cos + a * sin], axis=1)
+
+    x = x.astype(np.float64)
+    for l, lw in enumerate(w["layers"]):
+        xn = rms(x, lw["input_norm"])
+        q = heads(lin(xn, lw["wq"]), nq, lw["q_norm"])
+        k = heads(lin(xn, lw["wk"]), nk, lw["k_norm"])
+        kc[l, pos] = k.ravel()
+        vc[l, pos] = lin(xn, lw["wv"])
+        K = kc[l, :pos + 1].reshape(pos + 1, nk, hd)
+        V = vc[l, :pos + 1].reshape(pos + 1, nk, hd)
+        att = np.empty((nq, hd))
+        for h in range(nq):
+            s = K[:, h // (nq // nk)] @ q[h] / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            att[h] = (p / p.sum()) @ V[:, h // (nq // nk)]
+        x = x + lin(att.ravel(), lw["wo"])
+        xn = rms(x, lw["post_attn_norm"])
+        gu = lin(xn, lw["gate_up"])
+        g, u = gu[0::2], gu[1::2]
+        x = x + lin(g / (1 + np.exp(-g)) * u, lw["down"])
+    xn = rms(x, w["norm"])
+    logits = lin(xn, w["lm_head"])
+    return int(np.argmax(logits)), xn, logits
+
+
+def small_decoder(r, H, I, L, nq, nk, hd, vocab):
+    def qw(o, i):
+        wf = (0.02 * r.standard_normal((o, i))).astype(np.float32)
+        q, s = oracle.quantize_f32_to_int8(wf, o, i)
+        return q.reshape(o, i), s
+
+    def gain(n):
+        return (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+
+    layers = []
+    for _ in range(L):
+        gq, gs = qw(I, H)
+        uq, us = qw(I, H)
+        wgu, sgu = oracle.interleave_gate_up(gq, gs, uq, us, I, H)
+        layers.append({"wq": qw(nq * hd, H), "wk": qw(nk * hd, H), "wv": qw(nk * hd, H),
+                       "wo": qw(H, nq * hd), "gate_up": (wgu.reshape(2 * I, H), sgu),
+                       "down": qw(H, I), "q_norm": gain(hd), "k_norm": gain(hd),
+                       "input_norm": gain(H), "post_attn_norm": gain(H),
+                       "gate": (gq, gs), "up": (uq, us)})
+    return {"layers": layers, "norm": gain(H), "lm_head": qw(vocab, H)}
+
+
+def test_decode_step_composition():
+    """The restated decode step equals a float64 evaluation of decoder.rs's
+    formulas (a dropped residual, a swapped gate/up, a wrong norm gain or RoPE
+    position would not) over three positions, cache rows included."""
+    from oracle.decoder import decode_int8_step
+
+    r = np.random.default_rng(77)
+    H, I, L, nq, nk, hd, vocab = 64, 96, 2, 4, 2, 16, 50
+    w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
+    kc = np.zeros((L, 8, nk * hd), np.float32)
+    vc = np.zeros_like(kc)
+    kc64, vc64 = np.zeros(kc.shape), np.zeros(vc.shape)
+    for pos in range(3):
+        x = r.standard_normal(H).astype(np.float32)
+        tok, xn, logits = decode_int8_step(w, kc, vc, pos, x, nq, nk, hd)
+        tok64, xn64, logits64 = _f64_decode(w, kc64, vc64, pos, x, nq, nk, hd)
+        np.testing.assert_allclose(xn, xn64, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(logits, logits64, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(kc[:, :pos + 1], kc64[:, :pos + 1], rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(vc[:, :pos + 1], vc64[:, :pos + 1], rtol=1e-4, atol=1e-5)
+        top2 = np.sort(logits64)[-2:]
+        if top2[1] - top2[0] > 1e-3:
+            assert tok == tok64
