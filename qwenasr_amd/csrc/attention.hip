@@ -218,23 +218,34 @@ template <int HD>
 QASR_DEV void merge_splits(float* o, const float* ws_o, const float* ml, int nsplit, int lane) {
   constexpr int DPL = HD / 64;
   constexpr int B = 16;
+  const float* ob = ws_o + lane * DPL;
+  // the first B splits' output rows do not depend on the maxima: their loads
+  // go out with the (max, sum) loads, one memory round trip for both
+  float ov[B][DPL];
+#pragma unroll
+  for (int u = 0; u < B; ++u) {
+    const size_t z = (size_t)min(u, nsplit - 1);
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) ov[u][d] = ob[z * HD + d];
+  }
   const bool has = lane < nsplit;
   const float mz = has ? ml[2 * lane] : -__builtin_inff();
   const float lz = has ? ml[2 * lane + 1] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
   const float mx = wave_max(mz);
   const float f = has ? expf(mz - mx) : 0.0f;
   const float lsum = wave_sum(lz * f);
   float acc[DPL];
 #pragma unroll
   for (int d = 0; d < DPL; ++d) acc[d] = 0.0f;
-  const float* ob = ws_o + lane * DPL;
   for (int z0 = 0; z0 < nsplit; z0 += B) {
-    float ov[B][DPL];
+    if (z0 > 0) {
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const size_t z = (size_t)min(z0 + u, nsplit - 1);
+      for (int u = 0; u < B; ++u) {
+        const size_t z = (size_t)min(z0 + u, nsplit - 1);
 #pragma unroll
-      for (int d = 0; d < DPL; ++d) ov[u][d] = ob[z * HD + d];
+        for (int d = 0; d < DPL; ++d) ov[u][d] = ob[z * HD + d];
+      }
     }
 #pragma unroll
     for (int u = 0; u < B; ++u) {
