@@ -262,6 +262,7 @@ class C4Int8Matvec(Workload):
 
 class C5BatchedDecode(Workload):
     name = "c5"
+    B = 256
     description = ("qwen3-asr-1.7b batched decode B=256 (positions U[0,2047]): add+RMSNorm[256,2048] "
                    "fused with per-row int8 quantization + q/k head-RMSNorm+RoPE + W8A8 MFMA gate/up "
                    "GEMM [256,2048]x[2048,12288] + SwiGLU; 28 distinct layers rotate")
@@ -272,7 +273,7 @@ class C5BatchedDecode(Workload):
         from qwenasr_amd import kernels as K
 
         c = DEC_1_7B
-        B, L = 256, 28
+        B, L = self.B, 28
         H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
         self.layers = []
         for _ in range(L):
@@ -309,13 +310,23 @@ class C5BatchedDecode(Workload):
                 2 * I * H + 2 * I * F + B * H + B * F + B * I * F),
         }
         self.step_bytes = sum(b for _, b in self.kernels.values())
-        self.tokens_per_step = 256.0 / 28  # one layer for 256 streams
+        self.tokens_per_step = B / 28.0  # one layer for B streams
         self.dtype = "int8/int32->f32"
         self.gemm_ops = 2 * B * 2 * I * H
 
     def config(self):
-        return {"batch": 256, "hidden": 2048, "heads": "16q/8kv x 128", "intermediate": 6144,
+        return {"batch": self.B, "hidden": 2048, "heads": "16q/8kv x 128", "intermediate": 6144,
                 "layers_rotated": 28}
+
+
+class C5Share(C5BatchedDecode):
+    """c5 at one GPU's data-parallel share of a 256-stream batch over 8 GPUs."""
+    name = "c5_b32"
+    B = 32
+    description = ("qwen3-asr-1.7b batched decode B=32 (one GPU's share of 256 streams over 8): "
+                   "add+RMSNorm[32,2048]+int8 quant, q/k head-RMSNorm+RoPE, W8A8 gate/up + SwiGLU "
+                   "[32,2048]x[2048,12288]; 28 distinct layers rotate")
+    unit_tokens = 32
 
 
 class W8A32Decode(Workload):
@@ -529,7 +540,7 @@ class LmHead(Workload):
 
 
 WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c4": C4Int8Matvec,
-             "c5": C5BatchedDecode, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
+             "c5": C5BatchedDecode, "c5_b32": C5Share, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
              "lm_head": LmHead, "decode_step": DecodeStep}
 
 
@@ -592,9 +603,9 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
                 return n, dt
 
     nproc = os.cpu_count() or 1
-    if name in ("c1", "c2", "c5"):
-        c = DEC_0_6B if name != "c5" else DEC_1_7B
-        T = {"c1": 1, "c2": 512, "c5": 256}[name]
+    if name in ("c1", "c2", "c5", "c5_b32"):
+        c = DEC_0_6B if not name.startswith("c5") else DEC_1_7B
+        T = {"c1": 1, "c2": 512, "c5": 256, "c5_b32": 32}[name]
         H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
         x = r.standard_normal(T * H, dtype=np.float32)
         d = r.standard_normal(T * H, dtype=np.float32)
@@ -604,14 +615,15 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
         qw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
         kw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
         cos, sin = oracle.rope_table(2048, hd, c["theta"])
-        pos = (np.arange(T) if name == "c2" else r.integers(0, 2048 if name == "c5" else 512, T)).astype(np.int32)
+        c5 = name.startswith("c5")
+        pos = (np.arange(T) if name == "c2" else r.integers(0, 2048 if c5 else 512, T)).astype(np.int32)
         gu = r.standard_normal(T * 2 * I, dtype=np.float32)
         table = ids = None
         if name == "c2":
             table = (0.02 * r.standard_normal((VOCAB, H), dtype=np.float32))
             ids = r.integers(0, VOCAB, T).astype(np.int32)
         wq = ws = None
-        if name == "c5":
+        if c5:
             wq, ws = oracle.quantize_f32_to_int8((0.02 * r.standard_normal(2 * I * H, dtype=np.float32)), 2 * I, H)
 
         def step():
@@ -621,7 +633,7 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
                 xx = x
             oracle.add_rms_norm(xx, d, w, T, H, c["eps"])
             oracle.head_rms_norm_rope(q, k, qw, kw, cos, sin, pos, T, nq, nk, hd, c["eps"])
-            if name == "c5":
+            if c5:
                 # the reference's INT8 path: W8A32 matvec per token, then swiglu_multiply
                 gate_up = oracle.linear_nobias_int8(x, wq, ws, T, H, 2 * I, n_threads=min(nproc, 16))
                 oracle.swiglu_multiply(gate_up, T, I)
@@ -632,11 +644,11 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
 
         n, dt = run_until(step, seconds)
         per = dt / n
-        threads = min(nproc, 16) if name == "c5" else 1
+        threads = min(nproc, 16) if c5 else 1
         return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-                "ms_per_step": per * 1e3, "tokens_per_s": T / per if name != "c5" else T / (28 * per),
+                "ms_per_step": per * 1e3, "tokens_per_s": T / per if not c5 else T / (28 * per),
                 "sample": f"{n} full steps of the {name} chain (T={T}) on the oracle, "
-                          f"{'single-threaded norms/RoPE/SwiGLU' + (', INT8 W8A32 matvec on ' + str(threads) + ' threads' if name == 'c5' else '')}"}
+                          f"{'single-threaded norms/RoPE/SwiGLU' + (', INT8 W8A32 matvec on ' + str(threads) + ' threads' if c5 else '')}"}
     if name == "c3":
         T, D, FF = 3000, 896, 3584
         x = r.standard_normal(T * D, dtype=np.float32)
