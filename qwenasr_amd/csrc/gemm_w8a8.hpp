@@ -635,6 +635,111 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small-batch packed kernel (batch <= 64): one 8-wave workgroup per 48 W rows.
+//
+// With a single 64-token tile the 192-row kernel launches only 2*inter/192
+// workgroups (64 at the 1.7B shape, a quarter of the CUs). Here a workgroup
+// owns 48 rows x all tokens and wave w owns k-steps [w*KW, (w+1)*KW) (KW =
+// K/64/8): its W tiles and X fragments go straight to registers (every W and
+// X byte is loaded once per workgroup, no LDS staging), its 12 accumulators
+// are int32 partial sums over its K slice, and the 8 partials of each
+// accumulator tile are added in LDS (exact) by the wave that runs that tile's
+// SwiGLU epilogue -- the same epilogue, so the outputs equal the 192-row
+// kernel's bit for bit.
+// ---------------------------------------------------------------------------
+constexpr int kSbRows = 48;
+constexpr int kSbWaves = 8;
+constexpr size_t kSbLds = (size_t)kSbWaves * 12 * 64 * 16;  // 96 KiB of partial sums
+
+template <int KS>
+__global__ __launch_bounds__(64 * kSbWaves) void gemm_w8a8_swiglu_small_kernel(
+    float* __restrict__ out, const int8_t* __restrict__ wpk, const float* __restrict__ scales,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, int batch, int inter) {
+  constexpr int KW = KS / kSbWaves;
+  constexpr int K = KS * kPackK;
+  extern __shared__ __align__(16) int8_t lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * kSbRows;
+  const int s0 = wave * KW;
+
+  v4i wv[KW][3], xv[KW][4];
+  const int8_t* wp = wpk + 16 * lane;
+#pragma unroll
+  for (int s = 0; s < KW; ++s)
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      wv[s][i] = __builtin_nontemporal_load(
+          reinterpret_cast<const v4i*>(wp + packed_tile_offset(n0 / kPackRows + i, s0 + s, KS)));
+  // token tiles past the batch are neither loaded nor multiplied (uniform tests)
+#pragma unroll
+  for (int s = 0; s < KW; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = 16 * j + r;
+      const int row = m < batch ? m : batch - 1;  // rows past the batch: valid memory, dropped
+      xv[s][j] = v4i{0, 0, 0, 0};
+      if (16 * j < batch)
+        xv[s][j] = *reinterpret_cast<const v4i*>(xq + (size_t)row * K + kPackK * (s0 + s) + 16 * g);
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  v4i acc[3][4];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < KW; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (16 * j < batch) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[s][i], xv[s][j], acc[i][j], 0, 0, 0);
+      }
+
+  v4i* part = reinterpret_cast<v4i*>(lds);  // [wave][tile 4i + j][lane]
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[(wave * 12 + 4 * i + j) * 64 + lane] = acc[i][j];
+  __syncthreads();
+  // wave w finishes accumulator tiles w and w + 8: lane holds W rows
+  // n0 + 16i + 4g + {0..3} (two gate/up pairs) for token 16j + r
+  for (int t = wave; t < 12; t += kSbWaves) {
+    const int i = t >> 2, j = t & 3;
+    if (16 * j >= batch) continue;
+    v4i sum = part[t * 64 + lane];
+#pragma unroll
+    for (int u = 1; u < kSbWaves; ++u) sum += part[(u * 12 + t) * 64 + lane];
+    const int m = 16 * j + r;
+    if (m < batch) {
+      const float xsv = xs[m];
+      const int n = n0 + 16 * i + 4 * g;
+      const float4 sc = *reinterpret_cast<const float4*>(scales + n);
+      float2 o;
+      o.x = swiglu_w8a8(sum[0], sum[1], xsv, sc.x, sc.y);
+      o.y = swiglu_w8a8(sum[2], sum[3], xsv, sc.z, sc.w);
+      *reinterpret_cast<float2*>(out + (size_t)m * inter + (n >> 1)) = o;
+    }
+  }
+}
+
+template <int KS>
+bool small_kernel_ready() {
+  static const bool ok = [] {
+    int dev = 0, max_lds = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      return false;
+    if ((size_t)max_lds < kSbLds) return false;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_w8a8_swiglu_small_kernel<KS>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSbLds) == hipSuccess;
+  }();
+  return ok;
+}
+
 inline bool packed_gemm_shape(size_t K, size_t inter) {
   return (K == 1024 || K == 2048) && (2 * inter) % kPkBN == 0;
 }
@@ -672,6 +777,17 @@ inline bool try_packed_gemm(float* out, const int8_t* wpk, const float* scales, 
   if (n_tiles * m_tiles > 0x7fffffffu) return false;
   const bool vec = aligned16(out);
   const int B = (int)batch, I = (int)inter, NT = (int)n_tiles, MT = (int)m_tiles;
+  if (batch <= 64 && (2 * inter) % kSbRows == 0) {  // one token tile: 48-row workgroups
+    const unsigned grid = (unsigned)(2 * inter / kSbRows);
+    if (K == 1024 && small_kernel_ready<16>()) {
+      gemm_w8a8_swiglu_small_kernel<16><<<grid, 64 * kSbWaves, kSbLds, st>>>(out, wpk, scales, xq, xs, B, I);
+      return true;
+    }
+    if (K == 2048 && small_kernel_ready<32>()) {
+      gemm_w8a8_swiglu_small_kernel<32><<<grid, 64 * kSbWaves, kSbLds, st>>>(out, wpk, scales, xq, xs, B, I);
+      return true;
+    }
+  }
   if (K == 1024)
     return vec ? launch_packed<16, true>(out, wpk, scales, xq, xs, B, I, NT, MT, st)
                : launch_packed<16, false>(out, wpk, scales, xq, xs, B, I, NT, MT, st);
