@@ -28,6 +28,8 @@
 
 #include "common.hpp"
 
+#include <atomic>
+
 namespace qasr {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -267,22 +269,34 @@ inline bool gemm_w8a8_lds_shape(size_t K, size_t inter) {
   return (K == 1024 || K == 2048) && (2 * inter) % kLdsBN == 0;
 }
 
-// Raises the dynamic-LDS limit of one kernel instance once (the default limit
-// is 64 KiB; the staged X tile needs up to 64 x 2064 bytes). Returns false if
-// the device cannot give a workgroup that much LDS.
+// Raises kernel Fn's dynamic-LDS limit (64 KiB by default) to `bytes` on the
+// current device. The attribute is per device, so the outcome is remembered
+// per device (0 unknown, 1 set, -1 unavailable); concurrent first calls may
+// both set it, which is harmless. Returns false if the device cannot give a
+// workgroup that much LDS.
+template <auto Fn>
+bool raise_lds_limit(size_t bytes) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<signed char> state[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  const signed char known = state[dev].load(std::memory_order_acquire);
+  if (known != 0) return known > 0;
+  int max_lds = 0;
+  const bool ok =
+      hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+      (size_t)max_lds >= bytes &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(Fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)bytes) == hipSuccess;
+  state[dev].store(ok ? 1 : -1, std::memory_order_release);
+  return ok;
+}
+
+// The staged X tile needs up to 64 x 2064 bytes.
 template <int KSTEPS>
 bool lds_kernel_ready(size_t lds) {
-  static const bool ok = [lds] {
-    int dev = 0, max_lds = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-      return false;
-    if ((size_t)max_lds < (size_t)kLdsBM * (kLdsMaxK + kLdsRowPad)) return false;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_w8a8_swiglu_lds_kernel<KSTEPS>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, max_lds) == hipSuccess;
-  }();
   (void)lds;
-  return ok;
+  return raise_lds_limit<&gemm_w8a8_swiglu_lds_kernel<KSTEPS>>((size_t)kLdsBM * (kLdsMaxK + kLdsRowPad));
 }
 
 template <int KSTEPS>
@@ -728,16 +742,7 @@ __global__ __launch_bounds__(64 * kSbWaves) void gemm_w8a8_swiglu_small_kernel(
 
 template <int KS>
 bool small_kernel_ready() {
-  static const bool ok = [] {
-    int dev = 0, max_lds = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-      return false;
-    if ((size_t)max_lds < kSbLds) return false;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_w8a8_swiglu_small_kernel<KS>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSbLds) == hipSuccess;
-  }();
-  return ok;
+  return raise_lds_limit<&gemm_w8a8_swiglu_small_kernel<KS>>(kSbLds);
 }
 
 inline bool packed_gemm_shape(size_t K, size_t inter) {
@@ -746,16 +751,7 @@ inline bool packed_gemm_shape(size_t K, size_t inter) {
 
 template <int KS, bool VEC_OUT>
 bool packed_kernel_ready() {
-  static const bool ok = [] {
-    int dev = 0, max_lds = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-      return false;
-    if ((size_t)max_lds < kPkLds) return false;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_w8a8_swiglu_packed_kernel<KS, VEC_OUT>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPkLds) == hipSuccess;
-  }();
-  return ok;
+  return raise_lds_limit<&gemm_w8a8_swiglu_packed_kernel<KS, VEC_OUT>>(kPkLds);
 }
 
 template <int KS, bool VEC_OUT>

@@ -71,7 +71,6 @@ class QuantFile:
 
     def __init__(self, handle: ctypes.c_void_p):
         self._h = handle
-        so = _lib.lib()
         ver = ctypes.c_int()
         n = ctypes.c_size_t()
         _lib.call("qasr_qint8_info", self._h, ctypes.byref(ver), ctypes.byref(n))
@@ -90,7 +89,6 @@ class QuantFile:
             self.tensors.append(QuantTensorMeta(nm, dtype.value, tuple(shape[:n_dims.value]),
                                                 doff.value, soff.value))
             self._index[nm] = i  # a repeated name maps to its last entry, as in the C table
-        del so
 
     @classmethod
     def open(cls, path: str) -> "QuantFile | None":
