@@ -384,6 +384,50 @@ class W8A32Decode(Workload):
                 "projections": {n: f"[{o},{i}]" for n, (o, i) in self.SHAPES.items()}}
 
 
+class W8A32Prefill(Workload):
+    name = "w8a32_prefill"
+    description = ("qwen3-asr-0.6b INT8 prefill projections, T=512 (W8A32 linear_nobias_int8 with "
+                   "seq_len 512, as the reference runs them): q/k/v in one call, o, fused gate/up, down; "
+                   "28 distinct layers rotate")
+    unit_tokens = 512
+    dtype = "int8/f32"
+    T = 512
+    SHAPES = {"wq": (2048, 1024), "wk": (1024, 1024), "wv": (1024, 1024), "wo": (1024, 2048),
+              "gate_up": (6144, 1024), "down": (1024, 3072)}
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        L, T = 28, self.T
+        self.L = L
+        self.w = {n: [K.QuantWeight(torch.randint(-127, 128, (o * i,), generator=self.gen, device=dev,
+                                                  dtype=torch.int8), self.randn(o, 1e-4, 1e-3).abs_(), o, i)
+                      for _ in range(L)] for n, (o, i) in self.SHAPES.items()}
+        self.x = {i: [self.randn(T * i) for _ in range(2)] for i in (1024, 2048, 3072)}
+        self.y = {n: torch.empty(T * o, device=dev) for n, (o, i) in self.SHAPES.items()}
+
+        def mk(n):
+            o, i = self.SHAPES[n]
+            return (lambda j: K.linear_nobias_int8(self.y[n], self.x[i][j % 2], self.w[n][j % L].data,
+                                                   self.w[n][j % L].scales, T, i, o),
+                    o * i + o * F + T * i * F + T * o * F, 2 * T * o * i)
+
+        def qkv(j):
+            K.linear_nobias_int8_multi([self.y[n] for n in ("wq", "wk", "wv")],
+                                       [self.w[n][j % L] for n in ("wq", "wk", "wv")], self.x[1024][j % 2], T, 1024)
+
+        rows = 2048 + 1024 + 1024
+        self.kernels = {"qkv": (qkv, rows * 1024 + rows * F + T * 1024 * F + T * rows * F, 2 * T * rows * 1024)}
+        self.kernels.update({n: mk(n) for n in ("wo", "gate_up", "down")})
+        self.step_bytes = sum(spec[1] for spec in self.kernels.values())
+        self.tokens_per_step = T / 28.0  # one layer of a 512-token prefill
+
+    def config(self):
+        return {"seq_len": self.T, "hidden": 1024, "intermediate": 3072, "layers_rotated": 28,
+                "projections": {n: f"[{o},{i}]" for n, (o, i) in self.SHAPES.items()}}
+
+
 class DecodeStep(Workload):
     name = "decode_step"
     description = ("qwen3-asr-1.7b INT8 decode of one token at position 1023, B=1, fully on the device: "
@@ -541,7 +585,8 @@ class LmHead(Workload):
 
 WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c4": C4Int8Matvec,
              "c5": C5BatchedDecode, "c5_b32": C5Share, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
-             "lm_head": LmHead, "decode_step": DecodeStep}
+             "lm_head": LmHead, "decode_step": DecodeStep,
+             "w8a32_prefill": W8A32Prefill}
 
 
 # ---------------------------------------------------------------------------

@@ -221,7 +221,13 @@ int qasr_quantize_rows_i8(int8_t* q, float* scales, const float* x,
 
 /* W8A32 linear, no bias: y[s,o] = (sum_k (f32)w[o,k] * x[s,k]) * scales[o].
  * Replaces kernels::linear_nobias_int8 (kernels/mod.rs:650-661,
- * generic.rs:37-49). */
+ * generic.rs:37-49). Products are exact and summed in fp32 on every path (the
+ * reference's arithmetic, another summation order). From 8 tokens up (with
+ * in_dim % 64 == 0 and 16-byte aligned w and x) the call is one matrix-core
+ * GEMM instead of the reference's per-token matvecs: x is split exactly into
+ * three bf16 terms and int8 weights are exact in bf16. On that path a
+ * non-finite activation turns its output row to NaN (the reference may give
+ * +-inf there); finite inputs give the same results as the other paths. */
 int qasr_linear_nobias_int8_f32(float* y, const float* x, const int8_t* w,
                                 const float* scales, size_t seq_len,
                                 size_t in_dim, size_t out_dim, void* stream);

@@ -531,6 +531,192 @@ int launch_matvec(float* out, const int8_t* w, const float* scales, const int8_t
 
 bool matvec_shape(size_t in_dim) { return in_dim % 1024 == 0 && in_dim >= 1024 && in_dim <= 4096; }
 
+// ---------------------------------------------------------------------------
+// W8A32 linear for many tokens (prefill) on the bf16 matrix cores, fp32-exact
+// products: the reference's T matvecs (kernels/mod.rs:655-660) as one GEMM
+//   y[t, n] = (sum_k (f32)w[n, k] * x[t, k]) * scales[n] (+ bias[n]).
+// An int8 weight is exact in bf16, and an fp32 activation is exactly
+// hi + mid + lo with three bf16 terms (truncation: 8 + 8 + 8 mantissa bits),
+// so every product w * x = w*hi + w*mid + w*lo is formed exactly and summed in
+// fp32 by v_mfma_f32_16x16x32_bf16 -- the same fp32-sum arithmetic as the
+// reference, only in another order.
+// A workgroup owns 128 weight rows x 64 tokens and walks K in chunks of 64:
+// the chunk's weights (as bf16) and activations (as the three bf16 terms) are
+// staged in LDS, then each of the 4 waves (64 rows x 32 tokens) runs 2 k-steps
+// x 3 terms x 4 x 2 MFMA tiles. MFMA operands: A[i][k] (lane i + 16*(k/8),
+// element k%8) = weight row i, B[k][j] = token j; the result lane l holds rows
+// 4*(l/16)+v of token l%16.
+// ---------------------------------------------------------------------------
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+constexpr int kGmBK = 64;           // K per staged chunk
+constexpr int kGmRow = kGmBK + 8;   // LDS row in bf16 (16-byte pad)
+
+QASR_DEV unsigned short bf16_bits_trunc(float v) { return (unsigned short)(__float_as_uint(v) >> 16); }
+QASR_DEV float bf16_trunc(float v) { return __uint_as_float(__float_as_uint(v) & 0xffff0000u); }
+
+// BN weight rows x BT tokens per workgroup (BN in {64, 128}, BT in {32, 64});
+// the 4 waves form a 2 x 2 grid of (BN/2) x (BT/2) tiles.
+// Up to 4 weight matrices of the same activations (q/k/v) in one launch:
+// column-of-workgroups ranges [bx_begin[m], bx_begin[m + 1]) compute matrix m.
+struct GemmSet {
+  float* y[4];
+  const int8_t* w[4];
+  const float* s[4];
+  const float* b[4];
+  int N[4];
+  unsigned bx_begin[5];
+  int n;
+};
+
+template <int BN, int BT, bool BIAS>
+__global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, const float* __restrict__ x,
+                                                                int T, int K) {
+  float* y = set.y[0];
+  const int8_t* w = set.w[0];
+  const float* scales = set.s[0];
+  const float* bias = set.b[0];
+  int N = set.N[0];
+  unsigned bx0 = 0;
+#pragma unroll
+  for (int m = 1; m < 4; ++m)
+    if (m < set.n && blockIdx.x >= set.bx_begin[m]) {
+      y = set.y[m];
+      w = set.w[m];
+      scales = set.s[m];
+      bias = set.b[m];
+      N = set.N[m];
+      bx0 = set.bx_begin[m];
+    }
+  constexpr int MI = BN / 32, MJ = BT / 32;          // 16x16 tiles per wave
+  constexpr int TPW = 256 / BN, WB = kGmBK / TPW;    // weight staging: threads per row, bytes each
+  constexpr int TPX = 256 / BT, XF = kGmBK / TPX;    // activation staging: threads per token, floats each
+  __shared__ __align__(16) unsigned short wl[BN][kGmRow];
+  __shared__ __align__(16) unsigned short xl[3][BT][kGmRow];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave & 1, wc = wave >> 1;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = (int)(blockIdx.x - bx0) * BN, t0 = blockIdx.y * BT;
+  v4f acc[MI][MJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // rows and tokens past the end re-read the last one (valid memory; not stored)
+  const int w_row = tid / TPW, w_part = tid % TPW;
+  const int8_t* wsrc = w + (size_t)min(n0 + w_row, N - 1) * K + WB * w_part;
+  const int x_tok = tid / TPX, x_part = tid % TPX;
+  const float* xsrc = x + (size_t)min(t0 + x_tok, T - 1) * K + XF * x_part;
+
+  for (int k0 = 0; k0 < K; k0 += kGmBK) {
+    v4i wv[WB / 16];
+#pragma unroll
+    for (int c = 0; c < WB / 16; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc + k0 + 16 * c);
+    float4 xv[XF / 4];
+#pragma unroll
+    for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc + k0, c);
+#pragma unroll
+    for (int c = 0; c < WB / 16; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int v = wv[c][q];
+        ushort4 h;  // int8 -> bf16 is exact (at most 8 significant bits)
+        h.x = bf16_bits_trunc((float)(int8_t)(v & 0xff));
+        h.y = bf16_bits_trunc((float)(int8_t)((v >> 8) & 0xff));
+        h.z = bf16_bits_trunc((float)(int8_t)((v >> 16) & 0xff));
+        h.w = bf16_bits_trunc((float)(int8_t)((v >> 24) & 0xff));
+        *reinterpret_cast<ushort4*>(&wl[w_row][WB * w_part + 16 * c + 4 * q]) = h;
+      }
+#pragma unroll
+    for (int c = 0; c < XF / 4; ++c) {
+      const float e[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+      ushort4 th, tm, tl;
+      unsigned short* ph = reinterpret_cast<unsigned short*>(&th);
+      unsigned short* pm = reinterpret_cast<unsigned short*>(&tm);
+      unsigned short* pl = reinterpret_cast<unsigned short*>(&tl);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {  // x = hi + mid + lo exactly
+        const float hi = bf16_trunc(e[q]);
+        const float r1 = e[q] - hi;
+        const float mid = bf16_trunc(r1);
+        const float r2 = r1 - mid;  // at most 8 significant bits
+        ph[q] = bf16_bits_trunc(hi);
+        pm[q] = bf16_bits_trunc(mid);
+        pl[q] = bf16_bits_trunc(r2);
+      }
+      const int col = XF * x_part + 4 * c;
+      *reinterpret_cast<ushort4*>(&xl[0][x_tok][col]) = th;
+      *reinterpret_cast<ushort4*>(&xl[1][x_tok][col]) = tm;
+      *reinterpret_cast<ushort4*>(&xl[2][x_tok][col]) = tl;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kGmBK; kk += 32) {
+      v8bf a[MI], b[3][MJ];
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+        a[i] = *reinterpret_cast<const v8bf*>(&wl[(BN / 2) * wr + 16 * i + r][kk + 8 * g]);
+#pragma unroll
+      for (int term = 0; term < 3; ++term)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          b[term][j] = *reinterpret_cast<const v8bf*>(&xl[term][(BT / 2) * wc + 16 * j + r][kk + 8 * g]);
+#pragma unroll
+      for (int term = 0; term < 3; ++term)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < MJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[term][j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  // lane holds rows n0 + (BN/2)wr + 16i + 4g + v (v = 0..3) of token t0 + (BT/2)wc + 16j + r
+#pragma unroll
+  for (int j = 0; j < MJ; ++j) {
+    const int t = t0 + (BT / 2) * wc + 16 * j + r;
+    if (t >= T) continue;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int n = n0 + (BN / 2) * wr + 16 * i + 4 * g;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (n + v < N) {
+          float res = acc[i][j][v] * scales[n + v];
+          if constexpr (BIAS) res += bias[n + v];
+          y[(size_t)t * N + n + v] = res;
+        }
+      }
+    }
+  }
+}
+
+// Tile shape: the largest that still gives at least 256 workgroups.
+template <bool BIAS>
+void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st) {
+  auto cols = [&](int bn) {
+    unsigned c = 0;
+    for (int m = 0; m < set.n; ++m) {
+      set.bx_begin[m] = c;
+      c += (unsigned)((set.N[m] + bn - 1) / bn);
+    }
+    for (int m = set.n; m <= 4; ++m) set.bx_begin[m] = c;
+    return c;
+  };
+  unsigned c = cols(128);
+  if ((long long)c * ((T + 63) / 64) >= 256) {
+    w8a32_gemm_bf16x3_kernel<128, 64, BIAS><<<dim3(c, (unsigned)((T + 63) / 64)), 256, 0, st>>>(set, x, T, K);
+    return;
+  }
+  c = cols(64);
+  if ((long long)c * ((T + 63) / 64) >= 256) {
+    w8a32_gemm_bf16x3_kernel<64, 64, BIAS><<<dim3(c, (unsigned)((T + 63) / 64)), 256, 0, st>>>(set, x, T, K);
+    return;
+  }
+  w8a32_gemm_bf16x3_kernel<64, 32, BIAS><<<dim3(c, (unsigned)((T + 31) / 32)), 256, 0, st>>>(set, x, T, K);
+}
+
 }  // namespace
 }  // namespace qasr
 
@@ -557,6 +743,14 @@ extern "C" int qasr_quantize_rows_i8(int8_t* q, float* scales, const float* x, s
   return launch_status("quantize_rows_i8");
 }
 
+// From this many tokens the linear runs as one matrix-core GEMM instead of
+// per-token matvecs.
+constexpr size_t kGemmMinTokens = 8;
+
+static bool w8a32_gemm_shape(size_t seq_len, size_t in_dim, const void* w, const void* x) {
+  return seq_len >= kGemmMinTokens && in_dim % kGmBK == 0 && aligned16(w) && aligned16(x);
+}
+
 static int launch_w8a32(float* y, const float* x, const int8_t* w, const float* scales,
                         const float* bias, size_t seq_len, size_t in_dim, size_t out_dim,
                         void* stream) {
@@ -576,6 +770,18 @@ static int launch_w8a32(float* y, const float* x, const int8_t* w, const float* 
     const int r = rows_per_wave(in_dim, out_dim);
     launch_rows<kEpiRows>((int)(in_dim / 1024), r, (unsigned)((out_dim + 4 * r - 1) / (4 * r)), st,
                           y, x, w, scales, bias, k, o, nullptr);
+  } else if (w8a32_gemm_shape(seq_len, in_dim, w, x)) {
+    GemmSet set{};
+    set.y[0] = y;
+    set.w[0] = w;
+    set.s[0] = scales;
+    set.b[0] = bias;
+    set.N[0] = o;
+    set.n = 1;
+    if (bias)
+      launch_w8a32_gemm<true>(set, x, s, k, st);
+    else
+      launch_w8a32_gemm<false>(set, x, s, k, st);
   } else if (vec) {
     switch (in_dim / 1024) {
       case 1: w8a32_vec_kernel<1><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
@@ -665,6 +871,21 @@ extern "C" int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys
   }
   QASR_REQUIRE(total <= 0x7fffffffu, "linear_nobias_int8_multi: size too large");
   if (total == 0) return QASR_OK;
+  bool gemm = !one_launch;
+  for (size_t m = 0; m < n_mats; ++m) gemm = gemm && w8a32_gemm_shape(seq_len, in_dim, ws[m], x);
+  if (gemm) {
+    GemmSet set{};
+    for (size_t m = 0; m < n_mats; ++m) {
+      set.y[m] = ys[m];
+      set.w[m] = ws[m];
+      set.s[m] = scales[m];
+      set.b[m] = nullptr;
+      set.N[m] = (int)out_dims[m];
+    }
+    set.n = (int)n_mats;
+    launch_w8a32_gemm<false>(set, x, (int)seq_len, (int)in_dim, as_stream(stream));
+    return launch_status("linear_nobias_int8_multi");
+  }
   if (!one_launch) {
     for (size_t m = 0; m < n_mats; ++m) {
       const int rc = launch_w8a32(ys[m], x, ws[m], scales[m], nullptr, seq_len, in_dim, out_dims[m],

@@ -559,6 +559,8 @@ def make_qweight(r, rows, cols):
     (1, 6144, (2048, 3)),
     (3, 2048, (2048, 1024)),             # several tokens: one launch per matrix
     (1, 1000, (17, 33)),                 # in_dim off the vector path
+    (512, 1024, (2048, 1024, 1024)),     # prefill q/k/v: one matrix-core GEMM launch
+    (17, 2048, (1, 5, 300, 7)),
 ])
 def test_linear_nobias_int8_multi(dev, seq, in_dim, outs):
     """One launch over several matrices of the same x equals the separate
@@ -590,7 +592,11 @@ def test_linear_nobias_int8_multi(dev, seq, in_dim, outs):
                                                 (1, 6144, 2048), (1, 2048, 1),
                                                 # rows per wave 1, 2 and 8 by output rows
                                                 (1, 2048, 1024), (1, 2048, 4096), (1, 8192, 64),
-                                                (1, 1024, 40000)])
+                                                (1, 1024, 40000),
+                                                # 8+ tokens: the bf16x3 matrix-core GEMM
+                                                (8, 1024, 33), (64, 2048, 2048), (512, 1024, 6144),
+                                                (100, 3072, 1000), (17, 1024, 130), (70, 6144, 257),
+                                                (9, 1088, 200)])
 def test_linear_nobias_int8_w8a32(dev, seq, in_dim, out_dim):
     from qwenasr_amd import kernels as K
 
@@ -619,6 +625,28 @@ def test_linear_int8_integer_inputs_exact(dev):
                          in_dim, out_dim)
     exact = wq.astype(np.int64) @ x.astype(np.int64)
     np.testing.assert_array_equal(host(y).astype(np.int64), exact)
+
+
+@pytest.mark.parametrize("seq", [1, 64])
+def test_linear_int8_integer_inputs_exact_many_tokens(dev, seq):
+    """Integer activations with unit scales: every path (one-token rows kernel,
+    matrix-core GEMM) returns the exact integer dots -- the three-term bf16
+    split of an integer is exact and the fp32 sums stay below 2^24."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(21, seq)
+    in_dim, out_dim = 2048, 300
+    wq = r.integers(-128, 128, (out_dim, in_dim), dtype=np.int8)
+    x = r.integers(-20, 21, (seq, in_dim)).astype(np.float32)
+    x[0, :5] = [1e-3, -2.5e-2, 3.75, 1 / 3, 65.0]  # non-integers: compared to float64 below
+    y = torch.empty(seq * out_dim, dtype=torch.float32, device=dev)
+    K.linear_nobias_int8(y, dev_t(x.ravel(), dev), dev_t(wq, dev), torch.ones(out_dim, device=dev), seq,
+                         in_dim, out_dim)
+    got = host(y).reshape(seq, out_dim)
+    exact = x[1:].astype(np.int64) @ wq.astype(np.int64).T
+    np.testing.assert_array_equal(got[1:].astype(np.int64), exact)
+    ref0 = wq.astype(np.float64) @ x[0].astype(np.float64)
+    assert_close(got[0], ref0, RTOL, ATOL, "non-integer row")
 
 
 def test_interleave_gate_up(dev):
