@@ -548,8 +548,7 @@ bool matvec_shape(size_t in_dim) { return in_dim % 1024 == 0 && in_dim >= 1024 &
 // 4*(l/16)+v of token l%16.
 // ---------------------------------------------------------------------------
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-constexpr int kGmBK = 64;           // K per staged chunk
-constexpr int kGmRow = kGmBK + 8;   // LDS row in bf16 (16-byte pad)
+constexpr int kGmBK = 64;           // K granularity of the GEMM path (chunks are 64 or 128)
 
 QASR_DEV unsigned short bf16_bits_trunc(float v) { return (unsigned short)(__float_as_uint(v) >> 16); }
 QASR_DEV float bf16_trunc(float v) { return __uint_as_float(__float_as_uint(v) & 0xffff0000u); }
@@ -568,9 +567,10 @@ struct GemmSet {
   int n;
 };
 
-template <int BN, int BT, bool BIAS>
+template <int BN, int BT, int BK, bool BIAS>
 __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, const float* __restrict__ x,
                                                                 int T, int K) {
+  constexpr int kGmRow = BK + 8;  // LDS row in bf16 (16-byte pad)
   float* y = set.y[0];
   const int8_t* w = set.w[0];
   const float* scales = set.s[0];
@@ -588,8 +588,8 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, con
       bx0 = set.bx_begin[m];
     }
   constexpr int MI = BN / 32, MJ = BT / 32;          // 16x16 tiles per wave
-  constexpr int TPW = 256 / BN, WB = kGmBK / TPW;    // weight staging: threads per row, bytes each
-  constexpr int TPX = 256 / BT, XF = kGmBK / TPX;    // activation staging: threads per token, floats each
+  constexpr int TPW = 256 / BN, WB = BK / TPW;       // weight staging: threads per row, bytes each
+  constexpr int TPX = 256 / BT, XF = BK / TPX;       // activation staging: threads per token, floats each
   __shared__ __align__(16) unsigned short wl[BN][kGmRow];
   __shared__ __align__(16) unsigned short xl[3][BT][kGmRow];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -608,13 +608,14 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, con
   const int x_tok = tid / TPX, x_part = tid % TPX;
   const float* xsrc = x + (size_t)min(t0 + x_tok, T - 1) * K + XF * x_part;
 
-  for (int k0 = 0; k0 < K; k0 += kGmBK) {
-    v4i wv[WB / 16];
+  // the next chunk's loads are issued before the current chunk's MFMAs
+  v4i wv[WB / 16];
+  float4 xv[XF / 4];
 #pragma unroll
-    for (int c = 0; c < WB / 16; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc + k0 + 16 * c);
-    float4 xv[XF / 4];
+  for (int c = 0; c < WB / 16; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc + 16 * c);
 #pragma unroll
-    for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc + k0, c);
+  for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc, c);
+  for (int k0 = 0; k0 < K; k0 += BK) {
 #pragma unroll
     for (int c = 0; c < WB / 16; ++c)
 #pragma unroll
@@ -650,8 +651,14 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, con
       *reinterpret_cast<ushort4*>(&xl[2][x_tok][col]) = tl;
     }
     __syncthreads();
+    if (k0 + BK < K) {
 #pragma unroll
-    for (int kk = 0; kk < kGmBK; kk += 32) {
+      for (int c = 0; c < WB / 16; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc + k0 + BK + 16 * c);
+#pragma unroll
+      for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc + k0 + BK, c);
+    }
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 32) {
       v8bf a[MI], b[3][MJ];
 #pragma unroll
       for (int i = 0; i < MI; ++i)
@@ -706,15 +713,18 @@ void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
   };
   unsigned c = cols(128);
   if ((long long)c * ((T + 63) / 64) >= 256) {
-    w8a32_gemm_bf16x3_kernel<128, 64, BIAS><<<dim3(c, (unsigned)((T + 63) / 64)), 256, 0, st>>>(set, x, T, K);
+    w8a32_gemm_bf16x3_kernel<128, 64, 64, BIAS><<<dim3(c, (unsigned)((T + 63) / 64)), 256, 0, st>>>(set, x, T, K);
     return;
   }
   c = cols(64);
   if ((long long)c * ((T + 63) / 64) >= 256) {
-    w8a32_gemm_bf16x3_kernel<64, 64, BIAS><<<dim3(c, (unsigned)((T + 63) / 64)), 256, 0, st>>>(set, x, T, K);
+    w8a32_gemm_bf16x3_kernel<64, 64, 64, BIAS><<<dim3(c, (unsigned)((T + 63) / 64)), 256, 0, st>>>(set, x, T, K);
     return;
   }
-  w8a32_gemm_bf16x3_kernel<64, 32, BIAS><<<dim3(c, (unsigned)((T + 31) / 32)), 256, 0, st>>>(set, x, T, K);
+  if (K % 128 == 0)
+    w8a32_gemm_bf16x3_kernel<64, 32, 128, BIAS><<<dim3(c, (unsigned)((T + 31) / 32)), 256, 0, st>>>(set, x, T, K);
+  else
+    w8a32_gemm_bf16x3_kernel<64, 32, 64, BIAS><<<dim3(c, (unsigned)((T + 31) / 32)), 256, 0, st>>>(set, x, T, K);
 }
 
 }  // namespace
