@@ -571,6 +571,7 @@ template <int BN, int BT, int BK, bool BIAS>
 __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, const float* __restrict__ x,
                                                                 int T, int K) {
   constexpr int kGmRow = BK + 8;  // LDS row in bf16 (16-byte pad)
+  extern __shared__ __align__(16) unsigned short gm_lds[];  // [BN][kGmRow] weights, [3][BT][kGmRow] terms
   float* y = set.y[0];
   const int8_t* w = set.w[0];
   const float* scales = set.s[0];
@@ -590,8 +591,8 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, con
   constexpr int MI = BN / 32, MJ = BT / 32;          // 16x16 tiles per wave
   constexpr int TPW = 256 / BN, WB = BK / TPW;       // weight staging: threads per row, bytes each
   constexpr int TPX = 256 / BT, XF = BK / TPX;       // activation staging: threads per token, floats each
-  __shared__ __align__(16) unsigned short wl[BN][kGmRow];
-  __shared__ __align__(16) unsigned short xl[3][BT][kGmRow];
+  auto wl = reinterpret_cast<unsigned short (*)[kGmRow]>(gm_lds);
+  auto xl = reinterpret_cast<unsigned short (*)[BT][kGmRow]>(gm_lds + BN * kGmRow);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave & 1, wc = wave >> 1;
   const int r = lane & 15, g = lane >> 4;
@@ -699,7 +700,24 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, con
   }
 }
 
-// Tile shape: the largest that still gives at least 256 workgroups.
+template <int BN, int BT, int BK>
+constexpr size_t gemm_lds_bytes() {
+  return (size_t)(BN + 3 * BT) * (BK + 8) * 2;
+}
+
+template <int BN, int BT, int BK, bool BIAS>
+bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
+  constexpr size_t lds = gemm_lds_bytes<BN, BT, BK>();
+  if (K % BK != 0) return false;
+  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_kernel<BN, BT, BK, BIAS>>(lds)) return false;
+  w8a32_gemm_bf16x3_kernel<BN, BT, BK, BIAS><<<dim3(cols, (unsigned)((T + BT - 1) / BT)), 256, lds, st>>>(
+      set, x, T, K);
+  return true;
+}
+
+// Tile shape: the largest that still gives at least 256 workgroups; 128-wide
+// K chunks where K allows and two workgroups still fit a CU's LDS (half the
+// barriers per K).
 template <bool BIAS>
 void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st) {
   auto cols = [&](int bn) {
@@ -713,18 +731,17 @@ void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
   };
   unsigned c = cols(128);
   if ((long long)c * ((T + 63) / 64) >= 256) {
-    w8a32_gemm_bf16x3_kernel<128, 64, 64, BIAS><<<dim3(c, (unsigned)((T + 63) / 64)), 256, 0, st>>>(set, x, T, K);
+    try_gemm<128, 64, 64, BIAS>(set, c, x, T, K, st);  // 128-wide chunks: 87 KB LDS, one workgroup per CU
     return;
   }
   c = cols(64);
   if ((long long)c * ((T + 63) / 64) >= 256) {
-    w8a32_gemm_bf16x3_kernel<64, 64, 64, BIAS><<<dim3(c, (unsigned)((T + 63) / 64)), 256, 0, st>>>(set, x, T, K);
+    if (try_gemm<64, 64, 128, BIAS>(set, c, x, T, K, st)) return;
+    try_gemm<64, 64, 64, BIAS>(set, c, x, T, K, st);
     return;
   }
-  if (K % 128 == 0)
-    w8a32_gemm_bf16x3_kernel<64, 32, 128, BIAS><<<dim3(c, (unsigned)((T + 31) / 32)), 256, 0, st>>>(set, x, T, K);
-  else
-    w8a32_gemm_bf16x3_kernel<64, 32, 64, BIAS><<<dim3(c, (unsigned)((T + 31) / 32)), 256, 0, st>>>(set, x, T, K);
+  if (try_gemm<64, 32, 128, BIAS>(set, c, x, T, K, st)) return;
+  try_gemm<64, 32, 64, BIAS>(set, c, x, T, K, st);
 }
 
 }  // namespace

@@ -596,7 +596,9 @@ def test_linear_nobias_int8_multi(dev, seq, in_dim, outs):
                                                 # 8+ tokens: the bf16x3 matrix-core GEMM
                                                 (8, 1024, 33), (64, 2048, 2048), (512, 1024, 6144),
                                                 (100, 3072, 1000), (17, 1024, 130), (70, 6144, 257),
-                                                (9, 1088, 200)])
+                                                (9, 1088, 200),
+                                                # 64x64 tiles: 128-wide K chunks, 64-wide, ragged
+                                                (512, 1024, 2048), (512, 1088, 2048), (520, 1024, 2000)])
 def test_linear_nobias_int8_w8a32(dev, seq, in_dim, out_dim):
     from qwenasr_amd import kernels as K
 
