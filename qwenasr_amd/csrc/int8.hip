@@ -540,15 +540,21 @@ bool matvec_shape(size_t in_dim) { return in_dim % 1024 == 0 && in_dim >= 1024 &
 // so every product w * x = w*hi + w*mid + w*lo is formed exactly and summed in
 // fp32 by v_mfma_f32_16x16x32_bf16 -- the same fp32-sum arithmetic as the
 // reference, only in another order.
-// A workgroup owns 128 weight rows x 64 tokens and walks K in chunks of 64:
-// the chunk's weights (as bf16) and activations (as the three bf16 terms) are
-// staged in LDS, then each of the 4 waves (64 rows x 32 tokens) runs 2 k-steps
-// x 3 terms x 4 x 2 MFMA tiles. MFMA operands: A[i][k] (lane i + 16*(k/8),
-// element k%8) = weight row i, B[k][j] = token j; the result lane l holds rows
-// 4*(l/16)+v of token l%16.
+// Two kernels. The LDS-staged one: a workgroup owns 128 weight rows x 64
+// tokens and walks K in chunks of 64; the chunk's weights (as bf16) and
+// activations (as the three bf16 terms) are staged in LDS, then each of the 4
+// waves (64 rows x 32 tokens) runs 2 k-steps x 3 terms x 4 x 2 MFMA tiles. The
+// split-K one (smaller grids): the 4 waves share a smaller tile, split K
+// between them and load their fragments straight into registers.
+// MFMA operands: A[i][k] (lane i + 16*(k/8), element k%8) = weight row i,
+// B[k][j] = token j; the result lane l holds rows 4*(l/16)+v of token l%16.
 // ---------------------------------------------------------------------------
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-constexpr int kGmBK = 64;           // K granularity of the GEMM path (chunks are 64 or 128)
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+constexpr int kGmBK = 64;           // K granularity of the GEMM path
+// K chunks in flight per thread in the LDS-staged kernel (2 and 3 measured
+// slower: the extra registers cost more than the latency they hide)
+constexpr int kGemmPrefetch = 1;
 
 QASR_DEV unsigned short bf16_bits_trunc(float v) { return (unsigned short)(__float_as_uint(v) >> 16); }
 QASR_DEV float bf16_trunc(float v) { return __uint_as_float(__float_as_uint(v) & 0xffff0000u); }
@@ -567,11 +573,36 @@ struct GemmSet {
   int n;
 };
 
-template <int BN, int BT, int BK, bool BIAS>
-__global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, const float* __restrict__ x,
-                                                                int T, int K) {
+// Workgroup -> tile map. The grid is one-dimensional over cols x rows tiles
+// and workgroup b runs on XCD b % 8. With split_cols = a > 0, XCD c owns the
+// rectangle of cols/a column blocks x rows/(8/a) token blocks at (c % a, c / a),
+// so the weights and activations it reads fit its own L2; split_cols = 0 keeps
+// the row-major order (column block fastest).
+struct TileMap {
+  unsigned cols, rows, split_cols;
+};
+
+QASR_DEV void tile_of(const TileMap& m, unsigned b, unsigned& bx, unsigned& by) {
+  if (m.split_cols == 0) {
+    bx = b % m.cols;
+    by = b / m.cols;
+    return;
+  }
+  const unsigned xcd = b % 8, slot = b / 8;
+  const unsigned ca = m.cols / m.split_cols, rb = m.rows / (8 / m.split_cols);
+  bx = (xcd % m.split_cols) * ca + slot % ca;
+  by = (xcd / m.split_cols) * rb + slot / ca;
+}
+
+// NPF chunks of weights and activations are in flight in registers: the loads
+// of chunk c + NPF are issued right after chunk c is staged into LDS.
+template <int BN, int BT, int BK, int NPF, bool BIAS>
+__global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, TileMap map,
+                                                                const float* __restrict__ x, int T, int K) {
   constexpr int kGmRow = BK + 8;  // LDS row in bf16 (16-byte pad)
   extern __shared__ __align__(16) unsigned short gm_lds[];  // [BN][kGmRow] weights, [3][BT][kGmRow] terms
+  unsigned bx, by;
+  tile_of(map, blockIdx.x, bx, by);
   float* y = set.y[0];
   const int8_t* w = set.w[0];
   const float* scales = set.s[0];
@@ -580,7 +611,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, con
   unsigned bx0 = 0;
 #pragma unroll
   for (int m = 1; m < 4; ++m)
-    if (m < set.n && blockIdx.x >= set.bx_begin[m]) {
+    if (m < set.n && bx >= set.bx_begin[m]) {
       y = set.y[m];
       w = set.w[m];
       scales = set.s[m];
@@ -596,7 +627,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, con
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave & 1, wc = wave >> 1;
   const int r = lane & 15, g = lane >> 4;
-  const int n0 = (int)(blockIdx.x - bx0) * BN, t0 = blockIdx.y * BT;
+  const int n0 = (int)(bx - bx0) * BN, t0 = (int)by * BT;
   v4f acc[MI][MJ];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
@@ -609,78 +640,88 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, con
   const int x_tok = tid / TPX, x_part = tid % TPX;
   const float* xsrc = x + (size_t)min(t0 + x_tok, T - 1) * K + XF * x_part;
 
-  // the next chunk's loads are issued before the current chunk's MFMAs
-  v4i wv[WB / 16];
-  float4 xv[XF / 4];
+  v4i wv[NPF][WB / 16];
+  float4 xv[NPF][XF / 4];
 #pragma unroll
-  for (int c = 0; c < WB / 16; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc + 16 * c);
+  for (int q = 0; q < NPF; ++q)
+    if (q * BK < K) {
 #pragma unroll
-  for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc, c);
-  for (int k0 = 0; k0 < K; k0 += BK) {
+      for (int c = 0; c < WB / 16; ++c) wv[q][c] = *reinterpret_cast<const v4i*>(wsrc + q * BK + 16 * c);
 #pragma unroll
-    for (int c = 0; c < WB / 16; ++c)
+      for (int c = 0; c < XF / 4; ++c) xv[q][c] = ld4(xsrc + q * BK, c);
+    }
+  for (int kb = 0; kb < K; kb += NPF * BK) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int v = wv[c][q];
-        ushort4 h;  // int8 -> bf16 is exact (at most 8 significant bits)
-        h.x = bf16_bits_trunc((float)(int8_t)(v & 0xff));
-        h.y = bf16_bits_trunc((float)(int8_t)((v >> 8) & 0xff));
-        h.z = bf16_bits_trunc((float)(int8_t)((v >> 16) & 0xff));
-        h.w = bf16_bits_trunc((float)(int8_t)((v >> 24) & 0xff));
-        *reinterpret_cast<ushort4*>(&wl[w_row][WB * w_part + 16 * c + 4 * q]) = h;
+    for (int q = 0; q < NPF; ++q) {
+      const int k0 = kb + q * BK;
+      if (k0 >= K) break;
+#pragma unroll
+      for (int c = 0; c < WB / 16; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = wv[q][c][e];
+          ushort4 h;  // int8 -> bf16 is exact (at most 8 significant bits)
+          h.x = bf16_bits_trunc((float)(int8_t)(v & 0xff));
+          h.y = bf16_bits_trunc((float)(int8_t)((v >> 8) & 0xff));
+          h.z = bf16_bits_trunc((float)(int8_t)((v >> 16) & 0xff));
+          h.w = bf16_bits_trunc((float)(int8_t)((v >> 24) & 0xff));
+          *reinterpret_cast<ushort4*>(&wl[w_row][WB * w_part + 16 * c + 4 * e]) = h;
+        }
+#pragma unroll
+      for (int c = 0; c < XF / 4; ++c) {
+        const float ev[4] = {xv[q][c].x, xv[q][c].y, xv[q][c].z, xv[q][c].w};
+        ushort4 th, tm, tl;
+        unsigned short* ph = reinterpret_cast<unsigned short*>(&th);
+        unsigned short* pm = reinterpret_cast<unsigned short*>(&tm);
+        unsigned short* pl = reinterpret_cast<unsigned short*>(&tl);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {  // x = hi + mid + lo exactly
+          const float hi = bf16_trunc(ev[e]);
+          const float r1 = ev[e] - hi;
+          const float mid = bf16_trunc(r1);
+          const float r2 = r1 - mid;  // at most 8 significant bits
+          ph[e] = bf16_bits_trunc(hi);
+          pm[e] = bf16_bits_trunc(mid);
+          pl[e] = bf16_bits_trunc(r2);
+        }
+        const int col = XF * x_part + 4 * c;
+        *reinterpret_cast<ushort4*>(&xl[0][x_tok][col]) = th;
+        *reinterpret_cast<ushort4*>(&xl[1][x_tok][col]) = tm;
+        *reinterpret_cast<ushort4*>(&xl[2][x_tok][col]) = tl;
+      }
+      __syncthreads();
+      if (k0 + NPF * BK < K) {
+#pragma unroll
+        for (int c = 0; c < WB / 16; ++c)
+          wv[q][c] = *reinterpret_cast<const v4i*>(wsrc + k0 + NPF * BK + 16 * c);
+#pragma unroll
+        for (int c = 0; c < XF / 4; ++c) xv[q][c] = ld4(xsrc + k0 + NPF * BK, c);
       }
 #pragma unroll
-    for (int c = 0; c < XF / 4; ++c) {
-      const float e[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
-      ushort4 th, tm, tl;
-      unsigned short* ph = reinterpret_cast<unsigned short*>(&th);
-      unsigned short* pm = reinterpret_cast<unsigned short*>(&tm);
-      unsigned short* pl = reinterpret_cast<unsigned short*>(&tl);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {  // x = hi + mid + lo exactly
-        const float hi = bf16_trunc(e[q]);
-        const float r1 = e[q] - hi;
-        const float mid = bf16_trunc(r1);
-        const float r2 = r1 - mid;  // at most 8 significant bits
-        ph[q] = bf16_bits_trunc(hi);
-        pm[q] = bf16_bits_trunc(mid);
-        pl[q] = bf16_bits_trunc(r2);
-      }
-      const int col = XF * x_part + 4 * c;
-      *reinterpret_cast<ushort4*>(&xl[0][x_tok][col]) = th;
-      *reinterpret_cast<ushort4*>(&xl[1][x_tok][col]) = tm;
-      *reinterpret_cast<ushort4*>(&xl[2][x_tok][col]) = tl;
-    }
-    __syncthreads();
-    if (k0 + BK < K) {
-#pragma unroll
-      for (int c = 0; c < WB / 16; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc + k0 + BK + 16 * c);
-#pragma unroll
-      for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc + k0 + BK, c);
-    }
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 32) {
-      v8bf a[MI], b[3][MJ];
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-        a[i] = *reinterpret_cast<const v8bf*>(&wl[(BN / 2) * wr + 16 * i + r][kk + 8 * g]);
-#pragma unroll
-      for (int term = 0; term < 3; ++term)
-#pragma unroll
-        for (int j = 0; j < MJ; ++j)
-          b[term][j] = *reinterpret_cast<const v8bf*>(&xl[term][(BT / 2) * wc + 16 * j + r][kk + 8 * g]);
-#pragma unroll
-      for (int term = 0; term < 3; ++term)
+      for (int kk = 0; kk < BK; kk += 32) {
+        v8bf a[MI], b[3][MJ];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
+          a[i] = *reinterpret_cast<const v8bf*>(&wl[(BN / 2) * wr + 16 * i + r][kk + 8 * g]);
+#pragma unroll
+        for (int term = 0; term < 3; ++term)
 #pragma unroll
           for (int j = 0; j < MJ; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[term][j], acc[i][j], 0, 0, 0);
+            b[term][j] = *reinterpret_cast<const v8bf*>(&xl[term][(BT / 2) * wc + 16 * j + r][kk + 8 * g]);
+#pragma unroll
+        for (int term = 0; term < 3; ++term)
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < MJ; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[term][j], acc[i][j], 0, 0, 0);
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 
   // lane holds rows n0 + (BN/2)wr + 16i + 4g + v (v = 0..3) of token t0 + (BT/2)wc + 16j + r
+  const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
 #pragma unroll
   for (int j = 0; j < MJ; ++j) {
     const int t = t0 + (BT / 2) * wc + 16 * j + r;
@@ -688,13 +729,19 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, con
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const int n = n0 + (BN / 2) * wr + 16 * i + 4 * g;
+      float res[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        if (n + v < N) {
-          float res = acc[i][j][v] * scales[n + v];
-          if constexpr (BIAS) res += bias[n + v];
-          y[(size_t)t * N + n + v] = res;
-        }
+        const int nv = min(n + v, N - 1);
+        res[v] = acc[i][j][v] * scales[nv];
+        if constexpr (BIAS) res[v] += bias[nv];
+      }
+      if (vec_out && n + 3 < N) {
+        *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (n + v < N) y[(size_t)t * N + n + v] = res[v];
       }
     }
   }
@@ -705,19 +752,228 @@ constexpr size_t gemm_lds_bytes() {
   return (size_t)(BN + 3 * BT) * (BK + 8) * 2;
 }
 
-template <int BN, int BT, int BK, bool BIAS>
-bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
-  constexpr size_t lds = gemm_lds_bytes<BN, BT, BK>();
-  if (K % BK != 0) return false;
-  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_kernel<BN, BT, BK, BIAS>>(lds)) return false;
-  w8a32_gemm_bf16x3_kernel<BN, BT, BK, BIAS><<<dim3(cols, (unsigned)((T + BT - 1) / BT)), 256, lds, st>>>(
-      set, x, T, K);
+// Column split of the XCD map that minimises the bytes one XCD reads
+// (cols/a weight blocks of BN x K int8 + rows/(8/a) token blocks of BT x K fp32);
+// 0 when no split divides the tile grid evenly.
+inline unsigned xcd_split_cols(unsigned cols, unsigned rows, int BN, int BT) {
+  unsigned best = 0;
+  double best_cost = 0;
+  for (unsigned a = 1; a <= 8; a *= 2) {
+    const unsigned b = 8 / a;
+    if (cols % a || rows % b) continue;
+    const double cost = (double)(cols / a) * BN + (double)(rows / b) * BT * 4;
+    if (best == 0 || cost < best_cost) {
+      best = a;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+// Split-K variant: the KW waves of a workgroup share one BN x BT output tile
+// and take interleaved 64-wide K steps (wave w: steps w, w + KW, ...). Each
+// wave loads its weight and activation fragments straight into registers in
+// the MFMA operand layout, so the main loop has no LDS traffic and no
+// barriers; each weight and activation element is converted once per
+// workgroup, as in the LDS-staged kernel. Within a 64-wide step, lane group g
+// (lanes 16g..16g+15) covers k = 16g..16g+15: the first 8 feed MFMA slots
+// 8g..8g+7 of the first 32-slot product and the next 8 those of the second
+// (the same permutation of k for both operands, so the dot product is
+// unchanged). The KW partial tiles are added in LDS in wave order.
+QASR_DEV unsigned bf16_pair(float lo_elem, float hi_elem) {  // upper halves of two floats
+  return __builtin_amdgcn_perm(__float_as_uint(hi_elem), __float_as_uint(lo_elem), 0x07060302u);
+}
+
+template <int MI, int MJ>
+struct KsplitRaw {
+  v4i w[MI];          // 16 int8 of one weight row
+  float4 x[MJ][4];    // 16 floats of one token
+};
+
+// The KW waves' partial tiles are added in LDS in wave order (deterministic),
+// the tile pairs (i, j) split over the waves; epilogue y = sum * scale (+ bias).
+// Lane (r, g) of pair (i, j) holds rows n0 + 16i + 4g + v of token t0 + 16j + r.
+template <int MI, int MJ, int KW, bool BIAS>
+QASR_DEV void ksplit_reduce_store(const v4f (&acc)[MI][MJ], float* red, int wave, int lane, float* y,
+                                  const float* scales, const float* bias, int N, int T, int n0, int t0) {
+  const int r = lane & 15, g = lane >> 4;
+  float* mine = red + (size_t)wave * (MI * MJ * 4 * 64);
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < MJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) mine[((i * MJ + j) * 4 + v) * 64 + lane] = acc[i][j][v];
+  __syncthreads();
+  const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  for (int p = wave; p < MI * MJ; p += KW) {
+    const int i = p / MJ, j = p % MJ;
+    const int t = t0 + 16 * j + r;
+    const int n = n0 + 16 * i + 4 * g;
+    float res[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float sum = red[(p * 4 + v) * 64 + lane];
+#pragma unroll
+      for (int ww = 1; ww < KW; ++ww) sum += red[(size_t)ww * (MI * MJ * 4 * 64) + (p * 4 + v) * 64 + lane];
+      const int nv = min(n + v, N - 1);
+      res[v] = sum * scales[nv];
+      if constexpr (BIAS) res[v] += bias[nv];
+    }
+    if (t >= T) continue;
+    if (vec_out && n + 3 < N) {
+      *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+    }
+  }
+}
+
+template <int BN, int BT, int KW, bool BIAS>
+__global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set, TileMap map,
+                                                                    const float* __restrict__ x, int T, int K) {
+  constexpr int MI = BN / 16, MJ = BT / 16;
+  extern __shared__ __align__(16) float gk_red[];  // [KW][MI * MJ * 4][64] partial tiles
+  unsigned bx, by;
+  tile_of(map, blockIdx.x, bx, by);
+  float* y = set.y[0];
+  const int8_t* w = set.w[0];
+  const float* scales = set.s[0];
+  const float* bias = set.b[0];
+  int N = set.N[0];
+  unsigned bx0 = 0;
+#pragma unroll
+  for (int m = 1; m < 4; ++m)
+    if (m < set.n && bx >= set.bx_begin[m]) {
+      y = set.y[m];
+      w = set.w[m];
+      scales = set.s[m];
+      bias = set.b[m];
+      N = set.N[m];
+      bx0 = set.bx_begin[m];
+    }
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = (int)(bx - bx0) * BN, t0 = (int)by * BT;
+  // rows and tokens past the end re-read the last one (valid memory; not stored)
+  const int8_t* wp[MI];
+  const float* xp[MJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) wp[i] = w + (size_t)min(n0 + 16 * i + r, N - 1) * K + 16 * g;
+#pragma unroll
+  for (int j = 0; j < MJ; ++j) xp[j] = x + (size_t)min(t0 + 16 * j + r, T - 1) * K + 16 * g;
+
+  v4f acc[MI][MJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto load = [&](KsplitRaw<MI, MJ>& raw, int step) {
+    const int k = step * 64;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) raw.w[i] = *reinterpret_cast<const v4i*>(wp[i] + k);
+#pragma unroll
+    for (int j = 0; j < MJ; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) raw.x[j][c] = ld4(xp[j] + k, c);
+  };
+  auto compute = [&](const KsplitRaw<MI, MJ>& raw) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {  // k = 16g + 8h + (0..7): MFMA slots 8g..8g+7
+      // weights: int8 -> bf16 is exact (at most 8 significant bits)
+      v4u a[MI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int v = raw.w[i][2 * h + q];
+          a[i][2 * q] = bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff));
+          a[i][2 * q + 1] = bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff));
+        }
+      // activations: x = hi + mid + lo exactly (three truncated bf16 terms)
+      v4u b[3][MJ];
+#pragma unroll
+      for (int j = 0; j < MJ; ++j)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const float4 xv = raw.x[j][2 * h + c];
+          const float e[4] = {xv.x, xv.y, xv.z, xv.w};
+          float r1[4], r2[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            r1[q] = e[q] - bf16_trunc(e[q]);
+            r2[q] = r1[q] - bf16_trunc(r1[q]);  // at most 8 significant bits
+          }
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            b[0][j][2 * c + q] = bf16_pair(e[2 * q], e[2 * q + 1]);
+            b[1][j][2 * c + q] = bf16_pair(r1[2 * q], r1[2 * q + 1]);
+            b[2][j][2 * c + q] = bf16_pair(r2[2 * q], r2[2 * q + 1]);
+          }
+        }
+#pragma unroll
+      for (int term = 0; term < 3; ++term)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < MJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a[i]),
+                                                                __builtin_bit_cast(v8bf, b[term][j]),
+                                                                acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // two register sets in turn: the loads of step s + KW are in flight while
+  // step s is converted and multiplied
+  const int steps = K / 64;
+  KsplitRaw<MI, MJ> ra, rb;
+  if (wave < steps) load(ra, wave);
+  for (int s = wave; s < steps; s += 2 * KW) {
+    if (s + KW < steps) load(rb, s + KW);
+    compute(ra);
+    if (s + KW >= steps) break;
+    if (s + 2 * KW < steps) load(ra, s + 2 * KW);
+    compute(rb);
+  }
+
+  ksplit_reduce_store<MI, MJ, KW, BIAS>(acc, gk_red, wave, lane, y, scales, bias, N, T, n0, t0);
+}
+
+template <int BN, int BT, int KW, bool BIAS>
+bool try_gemm_ksplit(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
+  constexpr size_t lds = (size_t)KW * BN * BT * sizeof(float);
+  if (K % 64 != 0) return false;
+  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_ksplit_kernel<BN, BT, KW, BIAS>>(lds)) return false;
+  TileMap map;
+  map.cols = cols;
+  map.rows = (unsigned)((T + BT - 1) / BT);
+  map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
+  w8a32_gemm_ksplit_kernel<BN, BT, KW, BIAS><<<map.cols * map.rows, 64 * KW, lds, st>>>(set, map, x, T, K);
   return true;
 }
 
-// Tile shape: the largest that still gives at least 256 workgroups; 128-wide
-// K chunks where K allows and two workgroups still fit a CU's LDS (half the
-// barriers per K).
+template <int BN, int BT, int BK, int NPF, bool BIAS>
+bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
+  constexpr size_t lds = gemm_lds_bytes<BN, BT, BK>();
+  if (K % BK != 0) return false;
+  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, BIAS>>(lds)) return false;
+  TileMap map;
+  map.cols = cols;
+  map.rows = (unsigned)((T + BT - 1) / BT);
+  map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
+  w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, BIAS><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K);
+  return true;
+}
+
+// Kernel and tile: the LDS-staged 128 x 64 tile where it still gives at least
+// 256 workgroups (its staged operands are shared by 4 waves: 128 B loaded per
+// MFMA); otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
+// 32 x 32 that fills the chip (measured at T = 512: o [1024, 2048] 20.0 ->
+// 16.7 us, down [1024, 3072] 27.4 -> 20.9 us against the LDS-staged 64 x 32).
 template <bool BIAS>
 void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st) {
   auto cols = [&](int bn) {
@@ -729,19 +985,22 @@ void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
     for (int m = set.n; m <= 4; ++m) set.bx_begin[m] = c;
     return c;
   };
+  const long long rows64 = (T + 63) / 64, rows32 = (T + 31) / 32;
   unsigned c = cols(128);
-  if ((long long)c * ((T + 63) / 64) >= 256) {
-    try_gemm<128, 64, 64, BIAS>(set, c, x, T, K, st);  // 128-wide chunks: 87 KB LDS, one workgroup per CU
+  if (c * rows64 >= 256) {
+    try_gemm<128, 64, 64, kGemmPrefetch, BIAS>(set, c, x, T, K, st);
     return;
   }
   c = cols(64);
-  if ((long long)c * ((T + 63) / 64) >= 256) {
-    if (try_gemm<64, 64, 128, BIAS>(set, c, x, T, K, st)) return;
-    try_gemm<64, 64, 64, BIAS>(set, c, x, T, K, st);
+  if (c * rows64 >= 256) {
+    try_gemm_ksplit<64, 64, 4, BIAS>(set, c, x, T, K, st);
     return;
   }
-  if (try_gemm<64, 32, 128, BIAS>(set, c, x, T, K, st)) return;
-  try_gemm<64, 32, 64, BIAS>(set, c, x, T, K, st);
+  if (c * rows32 >= 256) {
+    try_gemm_ksplit<64, 32, 4, BIAS>(set, c, x, T, K, st);
+    return;
+  }
+  try_gemm_ksplit<32, 32, 4, BIAS>(set, cols(32), x, T, K, st);
 }
 
 }  // namespace

@@ -563,9 +563,12 @@ def make_qweight(r, rows, cols):
     (17, 2048, (1, 5, 300, 7)),
 ])
 def test_linear_nobias_int8_multi(dev, seq, in_dim, outs):
-    """One launch over several matrices of the same x equals the separate
-    linear_nobias_int8 calls bit for bit (each row's dot is computed the same
-    way whichever wave owns it), and the oracle within the fp32 tolerance."""
+    """One launch over several matrices of the same x matches the separate
+    linear_nobias_int8 calls and the oracle. Up to 7 tokens every row's dot is
+    computed the same way whichever wave owns it, so the results are equal bit
+    for bit; from 8 tokens (the matrix-core GEMM) the tile follows the total
+    width, and a wider launch may use a tile that sums k in another order, so
+    there both agree within the fp32 tolerance."""
     from qwenasr_amd import kernels as K
 
     r = rng(29, seq, in_dim, len(outs))
@@ -581,7 +584,10 @@ def test_linear_nobias_int8_multi(dev, seq, in_dim, outs):
     for o, y, w, ref in zip(outs, ys, ws, refs):
         z = torch.empty(seq * o, device=dev)
         K.linear_nobias_int8(z, xt, w.data, w.scales, seq, in_dim, o)
-        np.testing.assert_array_equal(host(y), host(z))
+        if seq < 8:
+            np.testing.assert_array_equal(host(y), host(z))
+        else:
+            assert_close(host(y), host(z).astype(np.float64), RTOL, ATOL, f"multi vs single out={o}")
         assert_close(host(y), ref, RTOL, ATOL, f"multi out={o}")
 
 
@@ -597,8 +603,9 @@ def test_linear_nobias_int8_multi(dev, seq, in_dim, outs):
                                                 (8, 1024, 33), (64, 2048, 2048), (512, 1024, 6144),
                                                 (100, 3072, 1000), (17, 1024, 130), (70, 6144, 257),
                                                 (9, 1088, 200),
-                                                # 64x64 tiles: 128-wide K chunks, 64-wide, ragged
-                                                (512, 1024, 2048), (512, 1088, 2048), (520, 1024, 2000)])
+                                                # split-K 64x64, 64x32 tiles (32x32 above), ragged
+                                                (512, 1024, 2048), (512, 1088, 2048), (520, 1024, 2000),
+                                                (512, 2048, 1024), (500, 1024, 1000)])
 def test_linear_nobias_int8_w8a32(dev, seq, in_dim, out_dim):
     from qwenasr_amd import kernels as K
 
