@@ -252,6 +252,36 @@ int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,
                                       const size_t* out_dims, const float* x, size_t seq_len,
                                       size_t in_dim, void* stream);
 
+/* One decode token's layer-input residual add + RMSNorm and the projections
+ * that read it, in one launch: h = x + delta (delta may be NULL: h = x),
+ * xn = rms_norm(h) * norm_w, ys[m] = linear_nobias_int8(xn, ws[m], scales[m]).
+ * Replaces the pairs add_inplace + rms_norm (decoder.rs:924->878, 908+910,
+ * kernels/mod.rs:486-488, 897-918) followed by the projections that consume
+ * the normalised row (q/k/v decoder.rs:881-886). Every workgroup normalises
+ * the row itself, in the element order of qasr_add_rms_norm_f32, so ys equal
+ * qasr_add_rms_norm_f32 + qasr_linear_nobias_int8_multi_f32 at one token bit
+ * for bit. h is written to h_out (NULL: not written), which must not overlap x
+ * or delta: the residual stream alternates between two buffers. One token;
+ * in_dim 1024..8192 in steps of 1024 (QASR_ERR_UNSUPPORTED otherwise). */
+int qasr_add_rms_norm_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,
+                                                   const int8_t* const* ws,
+                                                   const float* const* scales,
+                                                   const size_t* out_dims, float* h_out,
+                                                   const float* x, const float* delta,
+                                                   const float* norm_w, size_t in_dim,
+                                                   float eps, void* stream);
+
+/* The post-attention residual add + RMSNorm and the gate/up projection +
+ * SwiGLU of one decode token in one launch (decoder.rs:908-921): as
+ * qasr_add_rms_norm_linear_nobias_int8_multi_f32, with the output of
+ * qasr_gate_up_swiglu_int8_f32 on the normalised row; equal bit for bit to
+ * qasr_add_rms_norm_f32 followed by qasr_gate_up_swiglu_int8_f32. */
+int qasr_add_rms_norm_gate_up_swiglu_int8_f32(float* out, float* h_out, const float* x,
+                                              const float* delta, const float* norm_w,
+                                              const int8_t* w_gate_up,
+                                              const float* scales_gate_up, size_t in_dim,
+                                              size_t intermediate, float eps, void* stream);
+
 /* W8A32 linear with optional bias (bias may be NULL): y = linear_nobias + bias.
  * Replaces kernels::linear_int8 (kernels/mod.rs:664-673). */
 int qasr_linear_int8_f32(float* y, const float* x, const int8_t* w,

@@ -125,16 +125,42 @@ __global__ __launch_bounds__(256) void w8a32_vec_kernel(float* y, const float* x
 // candidate (lm_head), or the decode loop's SwiGLU on interleaved gate/up rows.
 enum RowsEpi { kEpiRows = 0, kEpiArgmax = 1, kEpiSwiglu = 2 };
 
-template <int KCH, int R, int EPI>
+// With NORM the input row is not read as given: every workgroup first forms
+// h = x (+ delta) and the RMSNorm h * rinv * gain of it in LDS, with the same
+// element assignment (thread t: float4s t, t + 256, ...) and the same block
+// reduction as rms_norm_vec_kernel<256, KCH>, so the row equals that kernel's
+// output bit for bit; workgroup 0 also writes h to h_out.
+struct RowNorm {
+  const float* x;
+  const float* delta;  // nullable: plain RMSNorm of x
+  const float* gain;
+  float* h_out;        // nullable; never x or delta (other workgroups still read them)
+  float eps;
+};
+
+template <int KCH, int R, int EPI, bool NORM = false>
 QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const float* scales,
                               const float* bias, int in_dim, int out_dim, unsigned block,
-                              float2* part) {
+                              float2* part, const RowNorm& rn = RowNorm{}) {
   constexpr bool PART = EPI == kEpiArgmax;
   static_assert(EPI != kEpiSwiglu || R % 2 == 0, "SwiGLU pairs sit in one wave");
+  static_assert(!(NORM && PART), "no normalised input on the argmax path");
   const int lane = threadIdx.x & (kWave - 1);
   const int o0 = (int)(block * (256 / kWave) + threadIdx.x / kWave) * R;
-  if constexpr (!PART) {
+  if constexpr (!PART && !NORM) {
     if (o0 >= out_dim) return;
+  }
+  // the row statistics' inputs are loaded before the weights: the wait for
+  // them then leaves the weight loads in flight
+  float4 nx[NORM ? KCH : 1], nd[NORM ? KCH : 1], ng[NORM ? KCH : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      ng[i] = ld4(rn.gain, c);
+      nx[i] = ld4(rn.x, c);
+      if (rn.delta) nd[i] = ld4(rn.delta, c);
+    }
   }
   v4i wv[R][KCH];
 #pragma unroll
@@ -145,10 +171,47 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
     for (int c = 0; c < KCH; ++c) wv[r][c] = __builtin_nontemporal_load(wr + c * kWave + lane);
   }
   float4 xv[KCH][4];
+  if constexpr (NORM) {
+    __shared__ float4 xs[256 * KCH];
+    __shared__ float red[256 / kWave];
+    float ss = 0.0f;
 #pragma unroll
-  for (int c = 0; c < KCH; ++c)
+    for (int i = 0; i < KCH; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      float4 a = nx[i];
+      if (rn.delta) {
+        a.x += nd[i].x; a.y += nd[i].y; a.z += nd[i].z; a.w += nd[i].w;
+      }
+      if (rn.h_out && blockIdx.x == 0) st4(rn.h_out, c, a);
+      nx[i] = a;
+      ss += a.x * a.x;
+      ss += a.y * a.y;
+      ss += a.z * a.z;
+      ss += a.w * a.w;
+    }
+    ss = block_sum<256>(ss, red);
+    const float rinv = 1.0f / sqrtf(ss / (float)in_dim + rn.eps);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) xv[c][t] = ld4(x + (c * kWave + lane) * 16 + 4 * t, 0);
+    for (int i = 0; i < KCH; ++i) {
+      float4 o;
+      o.x = (nx[i].x * rinv) * ng[i].x;
+      o.y = (nx[i].y * rinv) * ng[i].y;
+      o.z = (nx[i].z * rinv) * ng[i].z;
+      o.w = (nx[i].w * rinv) * ng[i].w;
+      xs[threadIdx.x + 256 * i] = o;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < KCH; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xv[c][t] = xs[(c * kWave + lane) * 4 + t];
+    if (o0 >= out_dim) return;  // after the workgroup's barrier
+  } else {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xv[c][t] = ld4(x + (c * kWave + lane) * 16 + 4 * t, 0);
+  }
   __builtin_amdgcn_sched_barrier(0);
   float acc[R];
 #pragma unroll
@@ -217,12 +280,12 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
   }
 }
 
-template <int KCH, int R, int EPI = kEpiRows>
+template <int KCH, int R, int EPI = kEpiRows, bool NORM = false>
 __global__ __launch_bounds__(256) void w8a32_rows_kernel(float* y, const float* x, const int8_t* w,
                                                          const float* scales, const float* bias,
                                                          int in_dim, int out_dim,
-                                                         float2* part = nullptr) {
-  w8a32_rows_body<KCH, R, EPI>(y, x, w, scales, bias, in_dim, out_dim, blockIdx.x, part);
+                                                         float2* part = nullptr, RowNorm rn = RowNorm{}) {
+  w8a32_rows_body<KCH, R, EPI, NORM>(y, x, w, scales, bias, in_dim, out_dim, blockIdx.x, part, rn);
 }
 
 // Several matrices of the same input in one launch (the q/k/v projections):
@@ -237,9 +300,9 @@ struct MatSet {
   int n;
 };
 
-template <int KCH, int R>
+template <int KCH, int R, bool NORM = false>
 __global__ __launch_bounds__(256) void w8a32_rows_multi_kernel(MatSet ms, const float* x,
-                                                               int in_dim) {
+                                                               int in_dim, RowNorm rn = RowNorm{}) {
   float* y = ms.y[0];
   const int8_t* w = ms.w[0];
   const float* sc = ms.s[0];
@@ -254,7 +317,7 @@ __global__ __launch_bounds__(256) void w8a32_rows_multi_kernel(MatSet ms, const 
       out = ms.out[m];
       b0 = ms.wg_begin[m];
     }
-  w8a32_rows_body<KCH, R, kEpiRows>(y, x, w, sc, nullptr, in_dim, out, blockIdx.x - b0, nullptr);
+  w8a32_rows_body<KCH, R, kEpiRows, NORM>(y, x, w, sc, nullptr, in_dim, out, blockIdx.x - b0, nullptr, rn);
 }
 
 // Gate/up pairs for any shape: one wave per (token, output j) takes the dots
@@ -297,15 +360,16 @@ bool w8a32_rows_shape(size_t in_dim, const void* w, const void* x) {
   return in_dim >= 1024 && in_dim % 1024 == 0 && in_dim <= 8192 && aligned16(w) && aligned16(x);
 }
 
-// Launches the one-token kernel for (in_dim / 1024, r) on `grid` workgroups.
-template <int EPI>
+// Launches the one-token kernel for (in_dim / 1024, r) on `grid` workgroups
+// (with NORM, the input row is rn's normalised h and x is not read).
+template <int EPI, bool NORM = false>
 void launch_rows(int kch, int r, unsigned grid, hipStream_t st, float* y, const float* x,
                  const int8_t* w, const float* scales, const float* bias, int k, int o,
-                 float2* part) {
-#define QASR_ROWS(KCH, R)                                                                        \
-  if (kch == KCH && r == R) {                                                                    \
-    w8a32_rows_kernel<KCH, R, EPI><<<grid, 256, 0, st>>>(y, x, w, scales, bias, k, o, part);     \
-    return;                                                                                      \
+                 float2* part, const RowNorm& rn = RowNorm{}) {
+#define QASR_ROWS(KCH, R)                                                                            \
+  if (kch == KCH && r == R) {                                                                        \
+    w8a32_rows_kernel<KCH, R, EPI, NORM><<<grid, 256, 0, st>>>(y, x, w, scales, bias, k, o, part, rn); \
+    return;                                                                                          \
   }
   if constexpr (EPI != kEpiSwiglu) {
     QASR_ROWS(1, 1) QASR_ROWS(2, 1) QASR_ROWS(3, 1) QASR_ROWS(4, 1)
@@ -319,11 +383,12 @@ void launch_rows(int kch, int r, unsigned grid, hipStream_t st, float* y, const 
 #undef QASR_ROWS
 }
 
+template <bool NORM = false>
 void launch_rows_multi(int kch, int r, unsigned grid, hipStream_t st, const MatSet& ms,
-                       const float* x, int k) {
+                       const float* x, int k, const RowNorm& rn = RowNorm{}) {
 #define QASR_ROWS(KCH, R)                                                      \
   if (kch == KCH && r == R) {                                                  \
-    w8a32_rows_multi_kernel<KCH, R><<<grid, 256, 0, st>>>(ms, x, k);           \
+    w8a32_rows_multi_kernel<KCH, R, NORM><<<grid, 256, 0, st>>>(ms, x, k, rn); \
     return;                                                                    \
   }
   QASR_ROWS(1, 1) QASR_ROWS(1, 2) QASR_ROWS(1, 4) QASR_ROWS(1, 8)
@@ -1195,6 +1260,100 @@ extern "C" int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys
   ms.n = (int)n_mats;
   launch_rows_multi((int)(in_dim / 1024), r, wg, as_stream(stream), ms, x, (int)in_dim);
   return launch_status("linear_nobias_int8_multi");
+}
+
+// [a, a + an) and [b, b + bn) share a byte (null never overlaps)
+static bool bytes_overlap(const void* a, size_t an, const void* b, size_t bn) {
+  if (!a || !b) return false;
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + bn && pb < pa + an;
+}
+
+// Checks shared by the fused add + RMSNorm + projection entry points: the row
+// is in_dim floats on the one-token vector path, h_out overlaps neither input.
+static int check_row_norm(const char* what, float* h_out, const float* x, const float* delta,
+                          const float* norm_w, size_t in_dim, float eps) {
+  QASR_REQUIRE(x && norm_w, std::string(what) + ": null pointer");
+  if (!(in_dim >= 1024 && in_dim % 1024 == 0 && in_dim <= 8192))
+    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": in_dim must be 1024..8192 in steps of 1024");
+  if (!(aligned16(x) && aligned16(norm_w) && aligned16(delta) && aligned16(h_out)))
+    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": rows must be 16-byte aligned");
+  const size_t nb = in_dim * sizeof(float);
+  QASR_REQUIRE(!bytes_overlap(h_out, nb, x, nb) && !bytes_overlap(h_out, nb, delta, nb),
+               std::string(what) + ": h_out must not overlap x or delta");
+  QASR_REQUIRE(eps >= 0.0f, std::string(what) + ": eps must be non-negative");
+  return QASR_OK;
+}
+
+extern "C" int qasr_add_rms_norm_linear_nobias_int8_multi_f32(
+    size_t n_mats, float* const* ys, const int8_t* const* ws, const float* const* scales,
+    const size_t* out_dims, float* h_out, const float* x, const float* delta, const float* norm_w,
+    size_t in_dim, float eps, void* stream) {
+  const char* what = "add_rms_norm_linear_nobias_int8_multi";
+  if (n_mats == 0) return QASR_OK;
+  QASR_REQUIRE(ys && ws && scales && out_dims, std::string(what) + ": null pointer");
+  QASR_REQUIRE(n_mats <= (size_t)kMaxMats, std::string(what) + ": at most 4 matrices");
+  int rc = check_row_norm(what, h_out, x, delta, norm_w, in_dim, eps);
+  if (rc != QASR_OK) return rc;
+  size_t total = 0;
+  for (size_t m = 0; m < n_mats; ++m) {
+    QASR_REQUIRE(ys[m] && ws[m] && scales[m], std::string(what) + ": null pointer");
+    QASR_REQUIRE(out_dims[m] <= 0x7fffffffu - 64, std::string(what) + ": size too large");
+    size_t n;
+    QASR_REQUIRE(mul_ok(in_dim, out_dims[m], &n), std::string(what) + ": size overflows");
+    if (!aligned16(ws[m])) return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": weights must be 16-byte aligned");
+    const size_t yb = out_dims[m] * sizeof(float), nb = in_dim * sizeof(float);
+    QASR_REQUIRE(!bytes_overlap(ys[m], yb, x, nb) && !bytes_overlap(ys[m], yb, delta, nb) &&
+                     !bytes_overlap(ys[m], yb, h_out, nb),
+                 std::string(what) + ": outputs must not overlap the row");
+    total += out_dims[m];
+  }
+  QASR_REQUIRE(total <= 0x7fffffffu, std::string(what) + ": size too large");
+  const int r = rows_per_wave(in_dim, total);
+  MatSet ms{};
+  unsigned wg = 0;
+  for (size_t m = 0; m < n_mats; ++m) {
+    ms.y[m] = ys[m];
+    ms.w[m] = ws[m];
+    ms.s[m] = scales[m];
+    ms.out[m] = (int)out_dims[m];
+    ms.wg_begin[m] = wg;
+    wg += (unsigned)((out_dims[m] + 4 * r - 1) / (4 * r));
+  }
+  for (size_t m = n_mats; m <= (size_t)kMaxMats; ++m) ms.wg_begin[m] = wg;
+  ms.n = (int)n_mats;
+  if (wg == 0) return QASR_OK;
+  const RowNorm rn{x, delta, norm_w, h_out, eps};
+  launch_rows_multi<true>((int)(in_dim / 1024), r, wg, as_stream(stream), ms, x, (int)in_dim, rn);
+  return launch_status(what);
+}
+
+extern "C" int qasr_add_rms_norm_gate_up_swiglu_int8_f32(float* out, float* h_out, const float* x,
+                                                         const float* delta, const float* norm_w,
+                                                         const int8_t* w_gate_up,
+                                                         const float* scales_gate_up, size_t in_dim,
+                                                         size_t intermediate, float eps,
+                                                         void* stream) {
+  const char* what = "add_rms_norm_gate_up_swiglu_int8";
+  if (intermediate == 0) return QASR_OK;
+  QASR_REQUIRE(out && w_gate_up && scales_gate_up, std::string(what) + ": null pointer");
+  int rc = check_row_norm(what, h_out, x, delta, norm_w, in_dim, eps);
+  if (rc != QASR_OK) return rc;
+  QASR_REQUIRE(intermediate <= 0x3fffffffu - 64, std::string(what) + ": size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(2 * intermediate, in_dim, &n), std::string(what) + ": size overflows");
+  if (!aligned16(w_gate_up)) return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": weights must be 16-byte aligned");
+  const size_t ob = intermediate * sizeof(float), nb = in_dim * sizeof(float);
+  QASR_REQUIRE(!bytes_overlap(out, ob, x, nb) && !bytes_overlap(out, ob, delta, nb) &&
+                   !bytes_overlap(out, ob, h_out, nb),
+               std::string(what) + ": out must not overlap the row");
+  const size_t rows = 2 * intermediate;
+  const int r = rows_per_wave(in_dim, rows) < 2 ? 2 : rows_per_wave(in_dim, rows);
+  const RowNorm rn{x, delta, norm_w, h_out, eps};
+  launch_rows<kEpiSwiglu, true>((int)(in_dim / 1024), r, (unsigned)((rows + 4 * r - 1) / (4 * r)),
+                                as_stream(stream), out, x, w_gate_up, scales_gate_up, nullptr,
+                                (int)in_dim, (int)rows, nullptr, rn);
+  return launch_status(what);
 }
 
 extern "C" int qasr_linear_int8_f32(float* y, const float* x, const int8_t* w, const float* scales,

@@ -2,12 +2,16 @@
 (crates/qwen-asr/src/decoder.rs:848-965) over the C-ABI kernels.
 
 Per layer, in the reference's order:
-  input RMSNorm (fused with the previous layer's residual add), q/k/v
-  projections (one launch), q/k head RMSNorm + RoPE with the K/V rows written
-  into the cache (one launch), causal attention over the layer's cache block
-  (keys split over workgroups), o projection, residual add + post-attention
-  RMSNorm (one launch), gate/up projection + SwiGLU (one launch), down
-  projection.
+  the previous layer's residual add + input RMSNorm + q/k/v projections (one
+  launch), q/k head RMSNorm + RoPE with the K/V rows written into the cache
+  (one launch), causal attention over the layer's cache block (keys split over
+  workgroups, then merged), o projection, residual add + post-attention RMSNorm
+  + gate/up projection + SwiGLU (one launch), down projection: 7 launches.
+The fused add + RMSNorm + projection launches normalise the row inside every
+workgroup, in the element order of the standalone add_rms_norm kernel, so the
+results equal the unfused sequence (``fuse_norms=False``: add_rms_norm, then
+the projection) bit for bit. The residual stream alternates between two
+buffers, since no workgroup may write the row the others still read.
 Then the last residual add + final RMSNorm and the INT8 lm_head with the greedy
 argmax (decoder.rs:929-963). Everything stays on the device: the token id is
 written to a device int32, and the hidden state, KV cache and RoPE tables
@@ -30,7 +34,8 @@ from . import kernels as K
 class DecoderInt8:
     def __init__(self, weights: dict, hidden: int, intermediate: int, n_layers: int, n_heads: int = 16,
                  n_kv_heads: int = 8, head_dim: int = 128, eps: float = 1e-6, theta: float = 1e6,
-                 vocab: int | None = None, max_seq: int = 256, device="cuda"):
+                 vocab: int | None = None, max_seq: int = 256, device="cuda",
+                 fuse_norms: bool | None = None):
         self.w = weights
         self.H, self.I, self.L = hidden, intermediate, n_layers
         self.nq, self.nk, self.hd = n_heads, n_kv_heads, head_dim
@@ -40,7 +45,11 @@ class DecoderInt8:
         self.vocab = vocab if vocab is not None else lm.out_dim
         dev = device
         f32 = dict(dtype=torch.float32, device=dev)
+        # the fused launches take rows of 1024..8192 floats in steps of 1024
+        ok = hidden % 1024 == 0 and 1024 <= hidden <= 8192
+        self.fuse_norms = ok if fuse_norms is None else (fuse_norms and ok)
         self.x = torch.zeros(hidden, **f32)
+        self.x2 = torch.zeros(hidden, **f32)  # the residual's other buffer (fused path)
         self.x_norm = torch.empty(hidden, **f32)
         self.q = torch.empty(n_heads * head_dim, **f32)
         self.k = torch.empty(n_kv_heads * head_dim, **f32)
@@ -68,6 +77,9 @@ class DecoderInt8:
         """One token at position ``pos`` (the cache holds rows 0..pos-1):
         ``self.token`` receives the greedy next token, ``self.x_norm`` the final
         normed hidden state. Call ``prepare(pos)`` first."""
+        if self.fuse_norms:
+            self._decode_fused(embed, pos)
+            return
         H, I, nq, nk, hd, eps = self.H, self.I, self.nq, self.nk, self.hd, self.eps
         self.x.copy_(embed)
         for l, lw in enumerate(self.w["layers"]):
@@ -89,6 +101,34 @@ class DecoderInt8:
             dn = lw["down"]
             K.linear_nobias_int8(self.down, self.ffn, dn.data, dn.scales, 1, I, H)
         K.add_rms_norm(self.x, self.down, self.w["norm"], self.x_norm, 1, H, eps)
+        K.lm_head_int8_argmax(self.token, self.logits, self.x_norm, self.lm, 1, H, self.vocab, self.lm_ws)
+
+    def _decode_fused(self, embed: torch.Tensor, pos: int) -> None:
+        H, I, nq, nk, hd, eps = self.H, self.I, self.nq, self.nk, self.hd, self.eps
+        h, h2 = self.x, self.x2
+        h.copy_(embed)
+        for l, lw in enumerate(self.w["layers"]):
+            qkv_w = [lw["wq"], lw["wk"], lw["wv"]]
+            if l == 0:
+                K.add_rms_norm_linear_nobias_int8_multi([self.q, self.k, self.v], qkv_w, None, h, None,
+                                                        lw["input_norm"], H, eps)
+            else:  # previous layer's residual add + this layer's input norm + q/k/v
+                K.add_rms_norm_linear_nobias_int8_multi([self.q, self.k, self.v], qkv_w, h2, h, self.down,
+                                                        lw["input_norm"], H, eps)
+                h, h2 = h2, h
+            K.head_rms_norm_rope_kv(self.q, self.k, self.v, lw["q_norm"], lw["k_norm"], self.rope, None,
+                                    pos, 1, nq, nk, hd, eps, self.kv.k_layer_block(l),
+                                    self.kv.v_layer_block(l), self.kv.max_seq)
+            K.causal_attention_split(self.attn, self.q, self.kv.k_layer_block(l), self.kv.v_layer_block(l),
+                                     1, pos + 1, nq, nk, hd, self.scale, pos, self.attn_ws)
+            wo = lw["wo"]
+            K.linear_nobias_int8(self.proj, self.attn, wo.data, wo.scales, 1, nq * hd, H)
+            K.add_rms_norm_gate_up_swiglu_int8(self.ffn, h2, h, self.proj, lw["post_attn_norm"], lw["gate_up"],
+                                               H, I, eps)
+            h, h2 = h2, h
+            dn = lw["down"]
+            K.linear_nobias_int8(self.down, self.ffn, dn.data, dn.scales, 1, I, H)
+        K.add_rms_norm(h, self.down, self.w["norm"], self.x_norm, 1, H, eps)
         K.lm_head_int8_argmax(self.token, self.logits, self.x_norm, self.lm, 1, H, self.vocab, self.lm_ws)
 
     def finish(self, pos: int) -> None:

@@ -523,6 +523,51 @@ def gate_up_swiglu_int8(out, x, w: QuantWeight, seq_len: int, in_dim: int, inter
               seq_len, in_dim, intermediate, _stream())
 
 
+def add_rms_norm_linear_nobias_int8_multi(ys, ws: list, h_out, x, delta, norm_w, in_dim: int,
+                                          eps: float) -> None:
+    """One decode token: h = x + delta (``delta`` None: h = x), the RMSNorm of h,
+    and the projections of the normalised row in one launch (decoder.rs:924->878
+    then 881-886). ``h_out`` (None: not written) gets h and must be a different
+    buffer from x and delta; ``ys[m]`` equals add_rms_norm + linear_nobias_int8_multi
+    bit for bit."""
+    if len(ys) != len(ws):
+        raise ValueError("one output per weight")
+    for y, w in zip(ys, ws):
+        _need(y, F32, w.out_dim, "y")
+        _need(w.data, I8, w.out_dim * in_dim, "w")
+        _need(w.scales, F32, w.out_dim, "scales")
+    _need(x, F32, in_dim, "x")
+    _need(norm_w, F32, in_dim, "norm_w")
+    if delta is not None:
+        _need(delta, F32, in_dim, "delta")
+    if h_out is not None:
+        _need(h_out, F32, in_dim, "h_out")
+    n = len(ws)
+    arr = ctypes.c_void_p * max(n, 1)
+    _lib.call("qasr_add_rms_norm_linear_nobias_int8_multi_f32", n, arr(*[y.data_ptr() for y in ys]),
+              arr(*[w.data.data_ptr() for w in ws]), arr(*[w.scales.data_ptr() for w in ws]),
+              (ctypes.c_size_t * max(n, 1))(*[w.out_dim for w in ws]), _ptr(h_out), _ptr(x),
+              _ptr(delta), _ptr(norm_w), in_dim, eps, _stream())
+
+
+def add_rms_norm_gate_up_swiglu_int8(out, h_out, x, delta, norm_w, w: QuantWeight, in_dim: int,
+                                     intermediate: int, eps: float) -> None:
+    """One decode token: the post-attention add + RMSNorm, the gate/up projection
+    and the decode SwiGLU in one launch (decoder.rs:908-921); equals add_rms_norm
+    followed by gate_up_swiglu_int8 bit for bit."""
+    _need(out, F32, intermediate, "out")
+    _need(x, F32, in_dim, "x")
+    _need(norm_w, F32, in_dim, "norm_w")
+    if delta is not None:
+        _need(delta, F32, in_dim, "delta")
+    if h_out is not None:
+        _need(h_out, F32, in_dim, "h_out")
+    _need(w.data, I8, 2 * intermediate * in_dim, "w")
+    _need(w.scales, F32, 2 * intermediate, "scales")
+    _lib.call("qasr_add_rms_norm_gate_up_swiglu_int8_f32", _ptr(out), _ptr(h_out), _ptr(x), _ptr(delta),
+              _ptr(norm_w), _ptr(w.data), _ptr(w.scales), in_dim, intermediate, eps, _stream())
+
+
 def linear_int8(y, x, w_int8, scales, bias, seq_len: int, in_dim: int, out_dim: int) -> None:
     """W8A32 linear with optional bias (kernels/mod.rs:664-673)."""
     _need(y, F32, seq_len * out_dim, "y")

@@ -183,3 +183,42 @@ def test_linear_multi_validation():
     assert so.qasr_linear_nobias_int8_multi_f32(2, nul, ptrs, ptrs, dims, FAKE, 1, 1024, NULL) == \
         _lib.QASR_ERR_INVALID_ARG
     assert so.qasr_linear_nobias_int8_multi_f32(0, None, None, None, None, None, 1, 1024, NULL) == 0
+
+
+def test_fused_norm_projection_validation():
+    """The fused add + RMSNorm + projection entry points reject, before any
+    launch: an h_out that overlaps x or delta (other workgroups still read the
+    row), outputs that overlap the row, rows off the one-token vector path,
+    misaligned rows, more than 4 matrices and null pointers."""
+    so = _lib.lib()
+    X, D, G, H, Y, W, S = (ctypes.c_void_p(a) for a in
+                           (0x100000, 0x200000, 0x300000, 0x400000, 0x500000, 0x600000, 0x700000))
+    arr = ctypes.c_void_p * 3
+    sz = ctypes.c_size_t * 3
+    ys, ws, ss, dims = arr(Y.value, Y.value + 0x10000, Y.value + 0x20000), arr(W.value, W.value, W.value), \
+        arr(S.value, S.value, S.value), sz(2048, 1024, 1024)
+    multi = so.qasr_add_rms_norm_linear_nobias_int8_multi_f32
+    gu = so.qasr_add_rms_norm_gate_up_swiglu_int8_f32
+    inv, uns = _lib.QASR_ERR_INVALID_ARG, _lib.QASR_ERR_UNSUPPORTED
+    # h_out aliasing x, or overlapping delta's 8 KiB row
+    assert multi(3, ys, ws, ss, dims, X, X, D, G, 2048, 1e-6, NULL) == inv
+    assert "overlap" in last_error()
+    assert multi(3, ys, ws, ss, dims, ctypes.c_void_p(D.value + 4096), X, D, G, 2048, 1e-6, NULL) == inv
+    assert gu(Y, ctypes.c_void_p(X.value + 16), X, D, G, W, S, 2048, 6144, 1e-6, NULL) == inv
+    # an output over the row
+    assert multi(3, arr(X.value, Y.value, Y.value + 0x10000), ws, ss, dims, H, X, D, G, 2048, 1e-6, NULL) == inv
+    assert gu(ctypes.c_void_p(D.value - 64), H, X, D, G, W, S, 2048, 6144, 1e-6, NULL) == inv
+    # off the vector path / misaligned
+    assert multi(3, ys, ws, ss, dims, H, X, D, G, 1000, 1e-6, NULL) == uns
+    assert gu(Y, H, ctypes.c_void_p(X.value + 4), D, G, W, S, 2048, 6144, 1e-6, NULL) == uns
+    assert gu(Y, H, X, D, G, W, S, 9216, 6144, 1e-6, NULL) == uns
+    # counts and nulls
+    arr5 = ctypes.c_void_p * 5
+    p5 = arr5(*([Y.value] * 5))
+    assert multi(5, p5, p5, p5, (ctypes.c_size_t * 5)(*([16] * 5)), H, X, D, G, 2048, 1e-6, NULL) == inv
+    assert multi(3, ys, ws, ss, dims, H, NULL, D, G, 2048, 1e-6, NULL) == inv
+    assert gu(NULL, H, X, D, G, W, S, 2048, 6144, 1e-6, NULL) == inv
+    assert multi(3, ys, ws, ss, dims, H, X, D, G, 2048, -1.0, NULL) == inv
+    # empty calls succeed without touching the device
+    assert multi(0, None, None, None, None, NULL, NULL, NULL, NULL, 2048, 1e-6, NULL) == _lib.QASR_OK
+    assert gu(Y, H, X, D, G, W, S, 2048, 0, 1e-6, NULL) == _lib.QASR_OK

@@ -102,3 +102,37 @@ def test_gate_up_swiglu_int8_matches_linear_plus_loop(dev):
         K.gate_up_swiglu_int8(out, torch.from_numpy(x).to(dev), w, seq, H, I)
         torch.cuda.synchronize()
         np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5, err_msg=f"{seq},{H},{I}")
+
+
+def test_fused_norm_decode_equals_unfused(tmp_path, dev):
+    """The decode step with the add + RMSNorm folded into the projections
+    (fuse_norms=True, 7 launches per layer) equals the unfused sequence
+    (add_rms_norm, then the projection) bit for bit: hidden state, logits,
+    token and cache rows, over several positions."""
+    from qwenasr_amd import qint8
+    from qwenasr_amd.decoder import DecoderInt8
+
+    H, I, L, nq, nk, hd, vocab = 2048, 6144, 2, 16, 8, 128, 1000
+    r = np.random.default_rng([33, H])
+    w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
+    p = tmp_path / "model.qint8"
+    write_model(p, w, L)
+    with qint8.QuantFile.open(str(p)) as qf:
+        dims = qint8.detect_decoder_dims(qf)
+        dims.n_layers = L
+        weights = qint8.load_decoder_int8(qf, dims, dev)
+    decs = [DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=8, device=dev, fuse_norms=f) for f in (True, False)]
+    assert decs[0].fuse_norms and not decs[1].fuse_norms
+    for pos in range(3):
+        x = torch.from_numpy(r.standard_normal(H).astype(np.float32)).to(dev)
+        for d in decs:
+            d.prepare(pos)
+            d.decode(x, pos)
+            d.finish(pos)
+        torch.cuda.synchronize()
+        for name in ("x_norm", "logits", "token"):
+            np.testing.assert_array_equal(getattr(decs[0], name).cpu().numpy(),
+                                          getattr(decs[1], name).cpu().numpy(), err_msg=f"{name} pos {pos}")
+        for l in range(L):
+            np.testing.assert_array_equal(decs[0].kv.k_layer(l).cpu().numpy(), decs[1].kv.k_layer(l).cpu().numpy())
+            np.testing.assert_array_equal(decs[0].kv.v_layer(l).cpu().numpy(), decs[1].kv.v_layer(l).cpu().numpy())

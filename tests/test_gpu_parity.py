@@ -591,6 +591,92 @@ def test_linear_nobias_int8_multi(dev, seq, in_dim, outs):
         assert_close(host(y), ref, RTOL, ATOL, f"multi out={o}")
 
 
+def _norm_inputs(r, H, dev):
+    x, d, g = normal(r, H), normal(r, H), normal(r, H, 0.1, 1.0)
+    return x, d, g, dev_t(x, dev), dev_t(d, dev), dev_t(g, dev)
+
+
+def _unfused_norm(K, xt, dt, gt, H, eps, dev):
+    """add_rms_norm (or rms_norm without delta) on copies: (residual, normalised row)."""
+    xa, xn = xt.clone(), torch.empty(H, device=dev)
+    if dt is not None:
+        K.add_rms_norm(xa, dt, gt, xn, 1, H, eps)
+    else:
+        K.rms_norm(xn, xa, gt, 1, H, eps)
+    return xa, xn
+
+
+@pytest.mark.parametrize("H,outs,with_delta", [
+    (2048, (2048, 1024, 1024), True),    # 1.7B q/k/v after the previous layer's down projection
+    (2048, (2048, 1024, 1024), False),   # layer 0: plain RMSNorm of the embedding
+    (1024, (2048, 1024, 1024), True),    # 0.6B
+    (3072, (100, 7), True),              # three float4 per thread, ragged row tails
+    (6144, (4096,), True),               # six float4 per thread
+    (4096, (5, 33, 1000, 64), True),     # four matrices
+])
+def test_add_rms_norm_linear_multi_equals_unfused(dev, H, outs, with_delta):
+    """The fused add + RMSNorm + projections launch equals add_rms_norm followed
+    by linear_nobias_int8_multi bit for bit (every workgroup normalises the row
+    in the standalone kernel's element order), writes h to h_out, leaves x and
+    delta untouched, and matches the oracle's add + RMSNorm + matvecs."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(41, H, len(outs), int(with_delta))
+    eps = 1e-6
+    x, d, g, xt, dt, gt = _norm_inputs(r, H, dev)
+    dt = dt if with_delta else None
+    qws, ws = [], []
+    for o in outs:
+        wq, sc = make_qweight(r, o, H)
+        qws.append((wq, sc))
+        ws.append(K.QuantWeight(dev_t(wq, dev), dev_t(sc, dev), o, H))
+    xa, xn = _unfused_norm(K, xt, dt, gt, H, eps, dev)
+    ref_ys = [torch.empty(o, device=dev) for o in outs]
+    K.linear_nobias_int8_multi(ref_ys, ws, xn, 1, H)
+    ys = [torch.full((o,), 7.0, device=dev) for o in outs]
+    h_out = torch.full((H,), 5.0, device=dev)
+    K.add_rms_norm_linear_nobias_int8_multi(ys, ws, h_out, xt, dt, gt, H, eps)
+    for y, z in zip(ys, ref_ys):
+        np.testing.assert_array_equal(host(y), host(z))
+    np.testing.assert_array_equal(host(h_out), host(xa))
+    np.testing.assert_array_equal(host(xt), x)
+    if with_delta:
+        np.testing.assert_array_equal(host(dt), d)
+        xn_ref = oracle.add_rms_norm(x, d, g, 1, H, eps)[1]
+    else:
+        xn_ref = oracle.rms_norm(x, g, 1, H, eps)
+    for y, (wq, sc), o in zip(ys, qws, outs):
+        assert_close(host(y), oracle.linear_nobias_int8(xn_ref, wq, sc, 1, H, o), RTOL, ATOL, f"out={o}")
+
+
+@pytest.mark.parametrize("H,I,with_delta", [(2048, 6144, True), (1024, 3072, True), (1024, 3072, False),
+                                            (3072, 100, True), (6144, 2048, True)])
+def test_add_rms_norm_gate_up_swiglu_equals_unfused(dev, H, I, with_delta):
+    """The fused post-attention add + RMSNorm + gate/up + SwiGLU launch equals
+    add_rms_norm followed by gate_up_swiglu_int8 bit for bit, and the oracle's
+    add + RMSNorm + matvec + decode SwiGLU within the fp32 tolerance."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(42, H, I, int(with_delta))
+    eps = 1e-6
+    x, d, g, xt, dt, gt = _norm_inputs(r, H, dev)
+    dt = dt if with_delta else None
+    wq, sc = make_qweight(r, 2 * I, H)
+    w = K.QuantWeight(dev_t(wq, dev), dev_t(sc, dev), 2 * I, H)
+    xa, xn = _unfused_norm(K, xt, dt, gt, H, eps, dev)
+    ref = torch.empty(I, device=dev)
+    K.gate_up_swiglu_int8(ref, xn, w, 1, H, I)
+    out = torch.full((I,), 7.0, device=dev)
+    h_out = torch.full((H,), 5.0, device=dev)
+    K.add_rms_norm_gate_up_swiglu_int8(out, h_out, xt, dt, gt, w, H, I, eps)
+    np.testing.assert_array_equal(host(out), host(ref))
+    np.testing.assert_array_equal(host(h_out), host(xa))
+    np.testing.assert_array_equal(host(xt), x)
+    xn_ref = oracle.add_rms_norm(x, d, g, 1, H, eps)[1] if with_delta else oracle.rms_norm(x, g, 1, H, eps)
+    gu = oracle.linear_nobias_int8(xn_ref, wq, sc, 1, H, 2 * I)
+    assert_close(host(out), oracle.swiglu_split(gu[0::2].copy(), gu[1::2].copy()), RTOL, ATOL, "swiglu")
+
+
 @pytest.mark.parametrize("seq,in_dim,out_dim", [(1, 2048, 12288), (4, 1024, 3072), (3, 2048, 2048),
                                                 (2, 100, 33),
                                                 # one token: R rows per wave, ragged row tails
