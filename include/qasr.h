@@ -376,6 +376,29 @@ int qasr_causal_attention_split_f32(float* out, const float* q, const float* k, 
                                     size_t q_offset, float* workspace, size_t workspace_floats,
                                     void* stream);
 
+/* One decode token's attention block after the q/k/v projections, the
+ * layer's steps of decoder.rs:888-903 in one call: q/k head RMSNorm + RoPE at
+ * position pos, the K/V rows stored into the layer's cache block, and causal
+ * attention of the token over cache rows 0..pos. Same results, bit for bit,
+ * as qasr_head_rms_norm_rope_kv_f32(q, k, v, ..., positions = NULL,
+ * start_pos = pos, seq = 1, ...) followed by
+ * qasr_causal_attention_split_f32(out, q, k_cache, v_cache, 1, pos + 1, ...,
+ * q_offset = pos, workspace, ...). When the keys are split over workgroups
+ * (workspace large enough, pos >= 255, head_dim 128 with n_heads/n_kv_heads
+ * <= 2 or head_dim 64 with <= 4) it is a single attention launch (+ merge):
+ * every workgroup normalises and rotates its q heads itself and the one
+ * holding key pos writes the cache rows; q is then left as given. Otherwise
+ * it runs the two calls, and q holds its normalised, rotated rows: treat q
+ * as scratch. pos must lie inside the RoPE table and the cache (INVALID_ARG
+ * otherwise; the two-call form writes NaN rows instead). No reference
+ * counterpart as one call. */
+int qasr_decode_attention_f32(float* out, float* q, const float* k, const float* v,
+                              const float* q_norm_w, const float* k_norm_w, const float* cos_tab,
+                              const float* sin_tab, size_t table_rows, size_t pos, size_t n_heads,
+                              size_t n_kv_heads, size_t head_dim, float eps, float scale,
+                              float* k_cache, float* v_cache, size_t cache_rows, float* workspace,
+                              size_t workspace_floats, void* stream);
+
 /* Workspace floats qasr_causal_attention_split_f32 can use for these sizes. */
 size_t qasr_causal_attention_workspace_floats(size_t seq_q, size_t n_heads, size_t head_dim);
 

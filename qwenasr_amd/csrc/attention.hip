@@ -270,11 +270,27 @@ QASR_DEV void merge_splits(float* o, const float* ws_o, const float* ml, int nsp
 // the quad's partial dots meet with two DPP adds. PV: lanes over head dims,
 // probabilities broadcast with readlane. The 4 waves' (max, sum, out) merge in
 // LDS; the workgroup writes its unnormalised partial to the workspace.
-template <int HD, int G>
+// The decode step's q/k head RMSNorm + RoPE and KV-cache store, done inside
+// the split kernel (PRE): q, k, v are the raw projection outputs of the one
+// token at position pos; cos_row/sin_row the RoPE table rows of pos; k_row,
+// v_row the layer's cache rows of pos.
+struct DecodePre {
+  const float* k;
+  const float* v;
+  const float* q_norm_w;
+  const float* k_norm_w;
+  const float* cos_row;
+  const float* sin_row;
+  float* k_row;
+  float* v_row;
+  float eps;
+};
+
+template <int HD, int G, bool PRE = false>
 __global__ __launch_bounds__(256) void attention_decode_split_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     int seq_q, int seq_k, int nk, float scale, int q_offset, int keys_per_split,
-    float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+    float* __restrict__ ws_o, float* __restrict__ ws_ml, DecodePre pre = DecodePre{}) {
   constexpr int DPL = HD / 64;
   constexpr int DQ = HD / 4;   // head dims per lane of a quad
   constexpr int C4 = DQ / 4;   // float4 loads per key per lane
@@ -285,11 +301,48 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
   const int i = blockIdx.x, kh = blockIdx.y;
   const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
   float4 qv[G][C4];
-  const float* qr = q + (size_t)i * q_stride + (size_t)kh * G * HD + quarter * DQ;
+  if constexpr (PRE) {
+    // One token (i == 0). Groups of HD/8 lanes, in the layout of the head
+    // kernel: groups 0..G-1 normalise and rotate this kv head's q heads into
+    // LDS; in the split that holds key pos (the last), group G writes the
+    // normalised, rotated k row into the cache and group G+1 the v row. The
+    // barrier then makes the row visible to the workgroup's key loop (no
+    // other workgroup reads it).
+    constexpr int L = HD / 8, HALF = HD / 2;
+    static_assert((G + 2) * L <= 256, "prologue groups fit the workgroup");
+    __shared__ __align__(16) float qs[G][HD];
+    const int grp = threadIdx.x / L, sub = threadIdx.x % L;
+    const bool last = blockIdx.z == gridDim.z - 1;
+    if (grp < G || (last && grp == G)) {
+      const bool is_q = grp < G;
+      const float* src = is_q ? q + (size_t)(kh * G + grp) * HD : pre.k + (size_t)kh * HD;
+      const float* w = is_q ? pre.q_norm_w : pre.k_norm_w;
+      const float4 w1 = ld4(w, sub), w2 = ld4(w + HALF, sub);
+      const float4 c1 = ld4(pre.cos_row, sub), c2 = ld4(pre.cos_row + HALF, sub);
+      const float4 s1 = ld4(pre.sin_row, sub), s2 = ld4(pre.sin_row + HALF, sub);
+      float4 x1 = ld4(src, sub), x2 = ld4(src + HALF, sub);
+      head_norm_rope<HD, true, true>(x1, x2, w1, w2, c1, c2, s1, s2, true, pre.eps);
+      float* dst = is_q ? &qs[grp][0] : pre.k_row + (size_t)kh * HD;
+      st4(dst, sub, x1);
+      st4(dst + HALF, sub, x2);
+    } else if (last && grp == G + 1) {
+      const float* src = pre.v + (size_t)kh * HD;
+      float* dst = pre.v_row + (size_t)kh * HD;
+      st4(dst, sub, ld4(src, sub));
+      st4(dst + HALF, sub, ld4(src + HALF, sub));
+    }
+    __syncthreads();
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int c = 0; c < C4; ++c) qv[g][c] = ld4(qr + g * HD, c);
+      for (int c = 0; c < C4; ++c) qv[g][c] = *reinterpret_cast<const float4*>(&qs[g][quarter * DQ + 4 * c]);
+  } else {
+    const float* qr = q + (size_t)i * q_stride + (size_t)kh * G * HD + quarter * DQ;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int c = 0; c < C4; ++c) qv[g][c] = ld4(qr + g * HD, c);
+  }
 
   const int k_lim = min(q_offset + i + 1, seq_k);
   const int k_begin = min(k_lim, (int)blockIdx.z * keys_per_split);
@@ -414,11 +467,16 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(float* __restric
 template <int HD, int G>
 void launch_attention_split(float* out, const float* q, const float* k, const float* v, int seq_q,
                             int seq_k, int nk, float scale, int q_offset, int nsplit,
-                            int keys_per_split, float* ws_o, float* ws_ml, hipStream_t st) {
+                            int keys_per_split, float* ws_o, float* ws_ml, hipStream_t st,
+                            const DecodePre* pre = nullptr) {
   const dim3 grid((unsigned)seq_q, (unsigned)nk, (unsigned)nsplit);
   if constexpr (G * HD <= 256) {  // the wave's loads fit the register file
-    attention_decode_split_kernel<HD, G><<<grid, 256, 0, st>>>(q, k, v, seq_q, seq_k, nk, scale,
-                                                              q_offset, keys_per_split, ws_o, ws_ml);
+    if (pre)
+      attention_decode_split_kernel<HD, G, true><<<grid, 256, 0, st>>>(
+          q, k, v, seq_q, seq_k, nk, scale, q_offset, keys_per_split, ws_o, ws_ml, *pre);
+    else
+      attention_decode_split_kernel<HD, G><<<grid, 256, 0, st>>>(q, k, v, seq_q, seq_k, nk, scale,
+                                                                q_offset, keys_per_split, ws_o, ws_ml);
   } else {
     causal_attention_kernel<HD, G, 1, 1, true><<<grid, 64, 0, st>>>(
         out, q, k, v, seq_q, seq_k, nk, scale, q_offset, keys_per_split, ws_o, ws_ml);
@@ -793,6 +851,56 @@ extern "C" int qasr_causal_attention_f32(float* out, const float* q, const float
                                          size_t q_offset, void* stream) {
   return attention_impl(out, q, k, v, seq_q, seq_k, n_heads, n_kv_heads, head_dim, scale, q_offset,
                         nullptr, 0, stream);
+}
+
+extern "C" int qasr_decode_attention_f32(float* out, float* q, const float* k, const float* v,
+                                         const float* q_norm_w, const float* k_norm_w,
+                                         const float* cos_tab, const float* sin_tab,
+                                         size_t table_rows, size_t pos, size_t n_heads,
+                                         size_t n_kv_heads, size_t head_dim, float eps, float scale,
+                                         float* k_cache, float* v_cache, size_t cache_rows,
+                                         float* workspace, size_t workspace_floats, void* stream) {
+  if (n_heads == 0) return QASR_OK;
+  QASR_REQUIRE(out && q && k && v && q_norm_w && k_norm_w && cos_tab && sin_tab && k_cache && v_cache,
+               "decode_attention: null pointer");
+  QASR_REQUIRE(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+               "decode_attention: n_heads must be a multiple of n_kv_heads");
+  QASR_REQUIRE(pos < table_rows && pos < cache_rows,
+               "decode_attention: pos must lie inside the RoPE table and the cache");
+  QASR_REQUIRE(pos < 0x40000000u && n_heads <= 65536 && head_dim <= 4096,
+               "decode_attention: size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(cache_rows, n_kv_heads * head_dim, &n), "decode_attention: size overflows");
+  const size_t G = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim;
+  const SplitPlan sp = plan_split(1, pos + 1, n_kv_heads, pos, head_dim, n_heads, workspace,
+                                  workspace_floats);
+  const bool fused_shape = (head_dim == 128 && (G == 1 || G == 2)) ||
+                           (head_dim == 64 && (G == 1 || G == 2 || G == 4));
+  const bool aligned = aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v) &&
+                       aligned16(q_norm_w) && aligned16(k_norm_w) && aligned16(cos_tab) &&
+                       aligned16(sin_tab) && aligned16(k_cache) && aligned16(v_cache) &&
+                       (!workspace || aligned16(workspace));
+  if (sp.nsplit > 1 && fused_shape && aligned) {
+    DecodePre pre{k, v, q_norm_w, k_norm_w, cos_tab + pos * head_dim, sin_tab + pos * head_dim,
+                  k_cache + pos * kv_dim, v_cache + pos * kv_dim, eps};
+    hipStream_t st = as_stream(stream);
+    const int nk = (int)n_kv_heads, sk = (int)pos + 1, qo = (int)pos;
+#define QASR_PRE(HD, GG)                                                                         \
+  if (head_dim == HD && G == GG) {                                                               \
+    launch_attention_split<HD, GG>(out, q, k_cache, v_cache, 1, sk, nk, scale, qo, sp.nsplit,    \
+                                   sp.keys_per_split, sp.ws_o, sp.ws_ml, st, &pre);             \
+    return launch_status("decode_attention");                                                    \
+  }
+    QASR_PRE(128, 1) QASR_PRE(128, 2) QASR_PRE(64, 1) QASR_PRE(64, 2) QASR_PRE(64, 4)
+#undef QASR_PRE
+  }
+  // short contexts and other shapes: the two calls this one stands for
+  int rc = qasr_head_rms_norm_rope_kv_f32(q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, nullptr, pos, 1,
+                                          n_heads, n_kv_heads, head_dim, table_rows, eps, k_cache,
+                                          v_cache, cache_rows, stream);
+  if (rc != QASR_OK) return rc;
+  return attention_impl(out, q, k_cache, v_cache, 1, pos + 1, n_heads, n_kv_heads, head_dim, scale, pos,
+                        workspace, workspace_floats, stream);
 }
 
 extern "C" size_t qasr_causal_attention_workspace_floats(size_t seq_q, size_t n_heads,

@@ -140,6 +140,51 @@ QASR_DEV float ref_fast_exp(float x) {
 
 QASR_DEV float qnan() { return __int_as_float(0x7fc00000); }
 
+// Per-head RMSNorm (NORM) and NeoX RoPE (ROPE) of one head held by a group of
+// HD/8 consecutive lanes: lane `sub` holds dims 4sub..4sub+3 in x1 and
+// HD/2 + 4sub..4sub+3 in x2, with the gains (w1, w2) and the position's table
+// entries (c1, c2, s1, s2) for the same dims.
+//   kernels/mod.rs:927-932: rms_inv = 1/sqrt(sum(v^2)/head_dim + eps); v = v*rms_inv*w
+//   kernels/mod.rs:1262-1263: v[d] = x1*c[d] + (-x2)*s[d]; v[d+h] = x2*c[d+h] + x1*s[d+h]
+// A position outside the table (pos_ok false) turns the head to NaN. Every
+// kernel that normalises or rotates heads calls this, so they agree bit for bit.
+template <int HD, bool NORM, bool ROPE>
+QASR_DEV void head_norm_rope(float4& x1, float4& x2, const float4& w1, const float4& w2,
+                             const float4& c1, const float4& c2, const float4& s1,
+                             const float4& s2, bool pos_ok, float eps) {
+  if constexpr (NORM) {
+    float ss = x1.x * x1.x;
+    ss += x1.y * x1.y;
+    ss += x1.z * x1.z;
+    ss += x1.w * x1.w;
+    ss += x2.x * x2.x;
+    ss += x2.y * x2.y;
+    ss += x2.z * x2.z;
+    ss += x2.w * x2.w;
+    ss = group_sum<HD / 8>(ss);
+    const float rinv = 1.0f / sqrtf(ss / (float)HD + eps);
+    x1.x = (x1.x * rinv) * w1.x; x1.y = (x1.y * rinv) * w1.y;
+    x1.z = (x1.z * rinv) * w1.z; x1.w = (x1.w * rinv) * w1.w;
+    x2.x = (x2.x * rinv) * w2.x; x2.y = (x2.y * rinv) * w2.y;
+    x2.z = (x2.z * rinv) * w2.z; x2.w = (x2.w * rinv) * w2.w;
+  }
+  if constexpr (ROPE) {
+    if (!pos_ok) {
+      const float n = qnan();
+      x1 = make_float4(n, n, n, n);
+      x2 = x1;
+    } else {
+      float4 o1, o2;
+      o1.x = x1.x * c1.x + (-x2.x) * s1.x; o2.x = x2.x * c2.x + x1.x * s2.x;
+      o1.y = x1.y * c1.y + (-x2.y) * s1.y; o2.y = x2.y * c2.y + x1.y * s2.y;
+      o1.z = x1.z * c1.z + (-x2.z) * s1.z; o2.z = x2.z * c2.z + x1.z * s2.z;
+      o1.w = x1.w * c1.w + (-x2.w) * s1.w; o2.w = x2.w * c2.w + x1.w * s2.w;
+      x1 = o1;
+      x2 = o2;
+    }
+  }
+}
+
 // Round half away from zero, then clamp to int8 (NaN -> 0), the arithmetic of
 // quantize.rs:657-658: `(v * inv).round().clamp(-128, 127) as i8`.
 QASR_DEV int quant_i8(float v, float inv) {

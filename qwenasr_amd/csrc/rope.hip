@@ -149,39 +149,7 @@ __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
   }
   float4 x1 = ld4(src, sub);
   float4 x2 = ld4(src + HALF, sub);
-  if constexpr (NORM) {
-    // kernels/mod.rs:927-932: rms_inv = 1/sqrt(sum(v^2)/head_dim + eps); v = v*rms_inv*w
-    float ss = x1.x * x1.x;
-    ss += x1.y * x1.y;
-    ss += x1.z * x1.z;
-    ss += x1.w * x1.w;
-    ss += x2.x * x2.x;
-    ss += x2.y * x2.y;
-    ss += x2.z * x2.z;
-    ss += x2.w * x2.w;
-    ss = group_sum<L>(ss);
-    const float rinv = 1.0f / sqrtf(ss / (float)HD + a.eps);
-    x1.x = (x1.x * rinv) * w1.x; x1.y = (x1.y * rinv) * w1.y;
-    x1.z = (x1.z * rinv) * w1.z; x1.w = (x1.w * rinv) * w1.w;
-    x2.x = (x2.x * rinv) * w2.x; x2.y = (x2.y * rinv) * w2.y;
-    x2.z = (x2.z * rinv) * w2.z; x2.w = (x2.w * rinv) * w2.w;
-  }
-  if constexpr (ROPE) {
-    if (!pos_ok) {
-      const float n = qnan();
-      x1 = make_float4(n, n, n, n);
-      x2 = x1;
-    } else {
-      // kernels/mod.rs:1262-1263: v[d] = x1*c[d] + (-x2)*s[d]; v[d+h] = x2*c[d+h] + x1*s[d+h]
-      float4 o1, o2;
-      o1.x = x1.x * c1.x + (-x2.x) * s1.x; o2.x = x2.x * c2.x + x1.x * s2.x;
-      o1.y = x1.y * c1.y + (-x2.y) * s1.y; o2.y = x2.y * c2.y + x1.y * s2.y;
-      o1.z = x1.z * c1.z + (-x2.z) * s1.z; o2.z = x2.z * c2.z + x1.z * s2.z;
-      o1.w = x1.w * c1.w + (-x2.w) * s1.w; o2.w = x2.w * c2.w + x1.w * s2.w;
-      x1 = o1;
-      x2 = o2;
-    }
-  }
+  head_norm_rope<HD, NORM, ROPE>(x1, x2, w1, w2, c1, c2, s1, s2, pos_ok, a.eps);
   if (KV && !pos_ok && base != src) return;  // k head outside the cache: nothing written
   st4(base, sub, x1);
   st4(base + HALF, sub, x2);

@@ -3,14 +3,16 @@
 
 Per layer, in the reference's order:
   the previous layer's residual add + input RMSNorm + q/k/v projections (one
-  launch), q/k head RMSNorm + RoPE with the K/V rows written into the cache
-  (one launch), causal attention over the layer's cache block (keys split over
-  workgroups, then merged), o projection, residual add + post-attention RMSNorm
-  + gate/up projection + SwiGLU (one launch), down projection: 7 launches.
+  launch), q/k head RMSNorm + RoPE, the K/V rows written into the cache and
+  causal attention over the layer's cache block (one launch with the keys
+  split over workgroups, then the merge), o projection, residual add +
+  post-attention RMSNorm + gate/up projection + SwiGLU (one launch), down
+  projection: 6 launches (7 below 256 cached keys, where attention does not
+  split and the head norm runs as its own launch).
 The fused add + RMSNorm + projection launches normalise the row inside every
 workgroup, in the element order of the standalone add_rms_norm kernel, so the
 results equal the unfused sequence (``fuse_norms=False``: add_rms_norm, then
-the projection) bit for bit. The residual stream alternates between two
+the projection; the head norm kernel, then attention) bit for bit. The residual stream alternates between two
 buffers, since no workgroup may write the row the others still read.
 Then the last residual add + final RMSNorm and the INT8 lm_head with the greedy
 argmax (decoder.rs:929-963). Everything stays on the device: the token id is
@@ -116,11 +118,9 @@ class DecoderInt8:
                 K.add_rms_norm_linear_nobias_int8_multi([self.q, self.k, self.v], qkv_w, h2, h, self.down,
                                                         lw["input_norm"], H, eps)
                 h, h2 = h2, h
-            K.head_rms_norm_rope_kv(self.q, self.k, self.v, lw["q_norm"], lw["k_norm"], self.rope, None,
-                                    pos, 1, nq, nk, hd, eps, self.kv.k_layer_block(l),
-                                    self.kv.v_layer_block(l), self.kv.max_seq)
-            K.causal_attention_split(self.attn, self.q, self.kv.k_layer_block(l), self.kv.v_layer_block(l),
-                                     1, pos + 1, nq, nk, hd, self.scale, pos, self.attn_ws)
+            K.decode_attention(self.attn, self.q, self.k, self.v, lw["q_norm"], lw["k_norm"], self.rope, pos,
+                               nq, nk, hd, eps, self.scale, self.kv.k_layer_block(l), self.kv.v_layer_block(l),
+                               self.kv.max_seq, self.attn_ws)
             wo = lw["wo"]
             K.linear_nobias_int8(self.proj, self.attn, wo.data, wo.scales, 1, nq * hd, H)
             K.add_rms_norm_gate_up_swiglu_int8(self.ffn, h2, h, self.proj, lw["post_attn_norm"], lw["gate_up"],

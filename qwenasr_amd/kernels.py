@@ -225,6 +225,32 @@ def causal_attention_split(out, q, k, v, seq_q: int, seq_k: int, n_heads: int, n
               q_offset, _ptr(workspace), workspace.numel(), _stream())
 
 
+def decode_attention(out, q, k, v, q_norm_w, k_norm_w, rope: "RopeCache", pos: int, n_heads: int,
+                     n_kv_heads: int, head_dim: int, eps: float, scale: float, k_cache, v_cache,
+                     cache_rows: int, workspace) -> None:
+    """One decode token: q/k head RMSNorm + RoPE at ``pos``, the K/V rows into the
+    layer's cache block and causal attention over rows 0..pos, equal bit for bit
+    to head_rms_norm_rope_kv + causal_attention_split (decoder.rs:888-903). With
+    the keys split over workgroups it is one attention launch; ``q`` is scratch
+    (it may come back normalised and rotated)."""
+    kv_dim = n_kv_heads * head_dim
+    _need(out, F32, n_heads * head_dim, "out")
+    _need(q, F32, n_heads * head_dim, "q")
+    _need(k, F32, kv_dim, "k")
+    _need(v, F32, kv_dim, "v")
+    _need(q_norm_w, F32, head_dim, "q_norm_w")
+    _need(k_norm_w, F32, head_dim, "k_norm_w")
+    _need(k_cache, F32, cache_rows * kv_dim, "k_cache")
+    _need(v_cache, F32, cache_rows * kv_dim, "v_cache")
+    _need(workspace, F32, 0, "workspace")
+    if rope.head_dim != head_dim:
+        raise ValueError("RopeCache head_dim does not match")
+    _lib.call("qasr_decode_attention_f32", _ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm_w),
+              _ptr(k_norm_w), _ptr(rope.cos), _ptr(rope.sin), rope.cap, pos, n_heads, n_kv_heads,
+              head_dim, eps, scale, _ptr(k_cache), _ptr(v_cache), cache_rows, _ptr(workspace),
+              workspace.numel(), _stream())
+
+
 def argmax_rows(idx, x, rows: int, cols: int) -> None:
     """Per-row argmax with the lm_head loop's semantics (decoder.rs:941-949)."""
     _need(idx, I32, rows, "idx")

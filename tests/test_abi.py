@@ -222,3 +222,21 @@ def test_fused_norm_projection_validation():
     # empty calls succeed without touching the device
     assert multi(0, None, None, None, None, NULL, NULL, NULL, NULL, 2048, 1e-6, NULL) == _lib.QASR_OK
     assert gu(Y, H, X, D, G, W, S, 2048, 0, 1e-6, NULL) == _lib.QASR_OK
+
+
+def test_decode_attention_validation():
+    """pos outside the RoPE table or the cache, null pointers and a head count
+    that is not a multiple of the kv heads are rejected before any launch."""
+    so = _lib.lib()
+    f = so.qasr_decode_attention_f32
+    P = [ctypes.c_void_p(0x100000 * (i + 1)) for i in range(10)]
+    out, q, k, v, qw, kw, cs, sn, kc, vc = P
+    inv = _lib.QASR_ERR_INVALID_ARG
+    # (..., table_rows, pos, n_heads, n_kv_heads, head_dim, eps, scale, k_cache, v_cache, cache_rows, ws, n, stream)
+    assert f(out, q, k, v, qw, kw, cs, sn, 1024, 1024, 16, 8, 128, 1e-6, 0.088, kc, vc, 2048, NULL, 0, NULL) == inv
+    assert "inside the RoPE table" in last_error()
+    assert f(out, q, k, v, qw, kw, cs, sn, 4096, 2048, 16, 8, 128, 1e-6, 0.088, kc, vc, 2048, NULL, 0, NULL) == inv
+    assert f(out, q, k, v, qw, kw, cs, sn, 4096, 10, 16, 5, 128, 1e-6, 0.088, kc, vc, 2048, NULL, 0, NULL) == inv
+    assert f(out, NULL, k, v, qw, kw, cs, sn, 4096, 10, 16, 8, 128, 1e-6, 0.088, kc, vc, 2048, NULL, 0, NULL) == inv
+    assert f(out, q, k, v, qw, kw, cs, sn, 4096, 10, 0, 8, 128, 1e-6, 0.088, kc, vc, 2048, NULL, 0, NULL) == \
+        _lib.QASR_OK

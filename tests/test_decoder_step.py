@@ -105,10 +105,11 @@ def test_gate_up_swiglu_int8_matches_linear_plus_loop(dev):
 
 
 def test_fused_norm_decode_equals_unfused(tmp_path, dev):
-    """The decode step with the add + RMSNorm folded into the projections
-    (fuse_norms=True, 7 launches per layer) equals the unfused sequence
-    (add_rms_norm, then the projection) bit for bit: hidden state, logits,
-    token and cache rows, over several positions."""
+    """The decode step with the add + RMSNorm folded into the projections and
+    the head norm + cache store folded into attention (fuse_norms=True)
+    equals the unfused sequence bit for bit: hidden state, logits, token and
+    cache rows, at positions where attention runs unsplit (0, 1) and split
+    (300-302)."""
     from qwenasr_amd import qint8
     from qwenasr_amd.decoder import DecoderInt8
 
@@ -121,9 +122,15 @@ def test_fused_norm_decode_equals_unfused(tmp_path, dev):
         dims = qint8.detect_decoder_dims(qf)
         dims.n_layers = L
         weights = qint8.load_decoder_int8(qf, dims, dev)
-    decs = [DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=8, device=dev, fuse_norms=f) for f in (True, False)]
+    decs = [DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=512, device=dev, fuse_norms=f)
+            for f in (True, False)]
     assert decs[0].fuse_norms and not decs[1].fuse_norms
-    for pos in range(3):
+    # an earlier context of 300 rows, so attention splits its keys (one fused launch)
+    decs[0].kv.k.normal_()
+    decs[0].kv.v.normal_()
+    decs[1].kv.k.copy_(decs[0].kv.k)
+    decs[1].kv.v.copy_(decs[0].kv.v)
+    for pos in (0, 1, 300, 301, 302):
         x = torch.from_numpy(r.standard_normal(H).astype(np.float32)).to(dev)
         for d in decs:
             d.prepare(pos)

@@ -1114,6 +1114,61 @@ def test_causal_attention_split(dev, name, seq_q, seq_k, nq, nk, hd, q_offset):
     assert_close(host(out2), ref, RTOL, ATOL, name + " fallback")
 
 
+@pytest.mark.parametrize("pos,nq,nk,hd,cache_rows", [
+    (1023, 16, 8, 128, 2048),   # 1.7B / 0.6B decode: one attention launch
+    (2047, 16, 8, 128, 2048),   # last cache row
+    (300, 16, 16, 128, 512),    # one q head per kv head
+    (1499, 8, 2, 64, 1600),     # head_dim 64, 4 q heads per kv head
+    (700, 4, 2, 64, 701),
+    (200, 16, 8, 128, 256),     # too few keys to split: the two-call form
+    (0, 16, 8, 128, 8),         # first token
+])
+def test_decode_attention_equals_unfused(dev, pos, nq, nk, hd, cache_rows):
+    """The one-token attention block in one call equals head_rms_norm_rope_kv
+    followed by causal_attention_split bit for bit: the output and every cache
+    row (the workgroup holding key pos writes the cache rows itself)."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(54, pos, nq, hd)
+    kv_dim = nk * hd
+    q, k, v = normal(r, nq * hd), normal(r, kv_dim), normal(r, kv_dim)
+    qw, kw = normal(r, hd, 0.1, 1.0), normal(r, hd, 0.1, 1.0)
+    cache_k, cache_v = normal(r, cache_rows * kv_dim), normal(r, cache_rows * kv_dim)
+    rope = K.RopeCache(dev)
+    rope.ensure(pos + 1, hd, 1e6)
+    scale = hd ** -0.5
+    outs, caches = [], []
+    for fused in (True, False):
+        kc, vc = dev_t(cache_k, dev), dev_t(cache_v, dev)
+        qt, kt, vt = dev_t(q, dev), dev_t(k, dev), dev_t(v, dev)
+        out = torch.full((nq * hd,), 9.0, device=dev)
+        ws = K.attention_workspace(1, nq, hd, dev)
+        if fused:
+            K.decode_attention(out, qt, kt, vt, dev_t(qw, dev), dev_t(kw, dev), rope, pos, nq, nk, hd, 1e-6,
+                               scale, kc, vc, cache_rows, ws)
+        else:
+            K.head_rms_norm_rope_kv(qt, kt, vt, dev_t(qw, dev), dev_t(kw, dev), rope, None, pos, 1, nq, nk,
+                                    hd, 1e-6, kc, vc, cache_rows)
+            K.causal_attention_split(out, qt, kc, vc, 1, pos + 1, nq, nk, hd, scale, pos, ws)
+        outs.append(host(out))
+        caches.append((host(kc), host(vc)))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    np.testing.assert_array_equal(caches[0][0], caches[1][0])
+    np.testing.assert_array_equal(caches[0][1], caches[1][1])
+    # rows other than pos are untouched
+    others = np.r_[0:pos * kv_dim, (pos + 1) * kv_dim:cache_rows * kv_dim]
+    np.testing.assert_array_equal(caches[0][0][others], cache_k[others])
+    # and the oracle: norm + RoPE + cache store, then attention over rows 0..pos
+    cos, sin = oracle.rope_table(rope.cap, hd, 1e6)
+    q_ref, k_rows, v_rows = kv_reference(q, k, v, qw, kw, cos, sin, np.array([pos]), 1, nq, nk, hd, 1e-6)
+    kref = cache_k.reshape(cache_rows, kv_dim)[:pos + 1].copy()
+    vref = cache_v.reshape(cache_rows, kv_dim)[:pos + 1].copy()
+    kref[pos], vref[pos] = k_rows[0], v_rows[0]
+    ref = oracle.causal_attention(q_ref.astype(np.float32), kref.ravel(), vref.ravel(), 1, pos + 1, nq, nk,
+                                  hd, scale, pos)
+    assert_close(outs[0], ref, RTOL, ATOL, "decode attention")
+
+
 def test_causal_attention_split_repeated_calls_share_the_workspace(dev):
     """64 calls in a row on one workspace, with alternating inputs, each equal
     to the oracle."""
