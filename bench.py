@@ -436,9 +436,9 @@ class W8A32Prefill(Workload):
 class DecodeStep(Workload):
     name = "decode_step"
     description = ("qwen3-asr-1.7b INT8 decode of one token at position 1023, B=1, fully on the device: "
-                   "28 layers of input RMSNorm, q/k/v (one launch), q/k norm+RoPE+KV store, split "
-                   "attention over 1024 cached rows, o, add+RMSNorm, gate/up+SwiGLU, down; final norm and "
-                   "INT8 lm_head [151936,2048] greedy argmax")
+                   "28 layers of residual add+input RMSNorm+q/k/v (one launch), q/k norm+RoPE+KV store+"
+                   "split attention over 1024 cached rows (one launch) + merge, o, add+RMSNorm+gate/up+"
+                   "SwiGLU (one launch), down; final norm and INT8 lm_head [151936,2048] greedy argmax")
     unit_tokens = 1
     dtype = "int8/f32"
     POS = 1023
