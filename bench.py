@@ -485,6 +485,64 @@ class DecodeStep(Workload):
                 "heads": "16q/8kv x 128", "layers": 28, "vocab": VOCAB}
 
 
+class PrefillStep(Workload):
+    name = "prefill_step"
+    description = ("qwen3-asr-0.6b INT8 prefill of a 512-token chunk at position 0, fully on the device "
+                   "(decoder.rs:751-847): 28 layers of RMSNorm (fused with the residual add), q/k/v "
+                   "(one bf16x3 matrix-core GEMM), q/k norm+RoPE+KV store of 512 rows, causal attention "
+                   "(fp32 matrix cores), o, add+RMSNorm, gate/up, prefill SwiGLU, down; last residual add")
+    unit_tokens = 512
+    dtype = "int8/f32"
+    T = 512
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+        from qwenasr_amd.decoder import DecoderInt8
+
+        c = DEC_0_6B
+        H, I, nq, nk, hd, L, T = c["hidden"], c["inter"], c["n_heads"], c["n_kv_heads"], c["head_dim"], 28, self.T
+
+        def qw(o, i):
+            q = torch.randint(-127, 128, (o * i,), generator=self.gen, device=dev, dtype=torch.int8)
+            return K.QuantWeight(q, self.randn(o, 1e-4, 1e-3).abs_(), o, i)
+
+        def gain(n):
+            return self.randn(n, 0.1, 1.0)
+
+        layers = [{"wq": qw(nq * hd, H), "wk": qw(nk * hd, H), "wv": qw(nk * hd, H), "wo": qw(H, nq * hd),
+                   "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": gain(hd), "k_norm": gain(hd),
+                   "input_norm": gain(H), "post_attn_norm": gain(H)} for _ in range(L)]
+        weights = {"layers": layers, "norm": gain(H), "lm_head": qw(1000, H)}
+        self.dec = DecoderInt8(weights, H, I, L, nq, nk, hd, c["eps"], c["theta"], max_seq=T, device=dev)
+        self.dec.prepare_prefill(0, T)
+        self.embeds = [self.randn(T * H) for _ in range(2)]
+        kv, q_dim = nk * hd, nq * hd
+        proj = sum(w.out_dim * w.in_dim for k, w in layers[0].items() if isinstance(w, K.QuantWeight))
+        layer_bytes = (sum(w.out_dim * w.in_dim + w.out_dim * F for k, w in layers[0].items()
+                           if isinstance(w, K.QuantWeight))
+                       + (2 * hd + 2 * H) * F                      # norm gains
+                       + 2 * T * kv * F)                          # the chunk's k/v rows written
+        step_bytes = L * layer_bytes + 2 * T * H * F              # embeddings in, residual out
+        gemm_flops = 2 * T * proj
+        attn_flops = 2 * 2 * hd * nq * (T * (T + 1) // 2)         # QK and PV over the causal triangle
+        self.step_flops = L * (gemm_flops + attn_flops)
+        # ceiling: GEMM flops at the bf16x3 rate (three bf16 products per fp32
+        # multiply-add), attention flops at the fp32 matrix-core rate
+        floor_s = L * (gemm_flops / (BF16_PEAK_TFLOPS / 3 * 1e12) + attn_flops / (FP32_PEAK_TFLOPS * 1e12))
+        self.mfma_peak_tflops = self.step_flops / floor_s / 1e12
+        self.mfma_peak_basis = ("projections at bf16 MFMA 2500/3 TFLOP/s (bf16x3), attention at fp32 MFMA "
+                                "157.3 TFLOP/s, weighted by their flops")
+        self.kernels = {"prefill": (lambda i: self.dec.prefill(self.embeds[i % 2], T, 0), step_bytes,
+                                    self.step_flops)}
+        self.step_bytes = step_bytes
+        self.tokens_per_step = float(T)
+
+    def config(self):
+        return {"seq_len": self.T, "start_pos": 0, "hidden": 1024, "intermediate": 3072,
+                "heads": "16q/8kv x 128", "layers": 28}
+
+
 class AttnDecode(Workload):
     name = "attn_decode"
     description = ("qwen3-asr-1.7b decode attention at position 2047: q[16,128] against a 2048-row "
@@ -591,7 +649,7 @@ class LmHead(Workload):
 WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c4": C4Int8Matvec,
              "c5": C5BatchedDecode, "c5_b32": C5Share, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
              "lm_head": LmHead, "decode_step": DecodeStep,
-             "w8a32_prefill": W8A32Prefill}
+             "w8a32_prefill": W8A32Prefill, "prefill_step": PrefillStep}
 
 
 # ---------------------------------------------------------------------------
@@ -802,6 +860,34 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
                 "sample": f"{n} decode tokens at position {pos} on the oracle's restated decode step "
                           f"(decoder.rs:848-965): INT8 matvecs on {threads} threads, attention on one, "
                           "one layer's weights shared by the 28 layers (LLC-warm)"}
+    if name == "prefill_step":
+        from oracle.decoder import prefill_int8
+
+        c = DEC_0_6B
+        H, I, nq, nk, hd, T = c["hidden"], c["inter"], c["n_heads"], c["n_kv_heads"], c["head_dim"], PrefillStep.T
+
+        def qw(o, i):
+            return (r.integers(-127, 128, (o, i), dtype=np.int8), (1e-3 + 1e-4 * r.random(o)).astype(np.float32))
+
+        def gain(n):
+            return (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+
+        layer = {"wq": qw(nq * hd, H), "wk": qw(nk * hd, H), "wv": qw(nk * hd, H), "wo": qw(H, nq * hd),
+                 "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": gain(hd), "k_norm": gain(hd),
+                 "input_norm": gain(H), "post_attn_norm": gain(H)}
+        kc = np.zeros((1, T, nk * hd), np.float32)
+        vc = np.zeros_like(kc)
+        x = r.standard_normal(T * H, dtype=np.float32)
+        threads = min(nproc, 16)
+        # whole layers of the 512-token prefill, one at a time; the step is 28 of them
+        n, dt = run_until(lambda: prefill_int8({"layers": [layer]}, kc, vc, 0, x, T, nq, nk, hd, c["eps"],
+                                               c["theta"], threads), seconds)
+        per = dt / n * 28
+        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "ms_per_step": per * 1e3, "tokens_per_s": T / per,
+                "sample": f"{n} layers of a {T}-token prefill on the oracle's restated prefill "
+                          f"(decoder.rs:751-847; INT8 linears on {threads} threads, attention and norms on "
+                          "one), timed per layer and scaled to the 28 layers"}
     if name == "lm_head":
         V, H = VOCAB, 1024
         wq, ws = oracle.quantize_f32_to_int8(0.02 * r.standard_normal(V * H, dtype=np.float32), V, H)

@@ -1,4 +1,5 @@
-"""CPU restatement of the reference's INT8 decode step -- TEST INFRASTRUCTURE ONLY.
+"""CPU restatement of the reference's INT8 decode step and prefill -- TEST
+INFRASTRUCTURE ONLY.
 
 ``decode_int8_step`` follows ``decoder.rs:848-965`` op by op with the oracle's
 kernel restatements (oracle/qasr_oracle.c): input RMSNorm, the three
@@ -7,12 +8,16 @@ the K/V row copies into the cache, ``causal_attention`` over rows 0..pos, the
 o projection and residual add, post-attention RMSNorm, the fused gate/up
 projection with the loop's libm SwiGLU (decoder.rs:916-921), the down
 projection and residual add; then the final RMSNorm, the lm_head logits and
-the greedy argmax (decoder.rs:929-963). Only tests/ and bench.py's
-cpu_baseline leg use it.
+the greedy argmax (decoder.rs:929-963). ``prefill_int8`` follows
+``decoder.rs:751-847``: the same layer for seq_len rows at positions
+start_pos.., with the prefill's fast_exp SwiGLU (kernels::swiglu_multiply)
+and no final norm or lm_head. Only tests/ and bench.py's cpu_baseline leg use
+it.
 
 Pinned by its parts: every primitive it calls is pinned in tests/test_oracle.py;
-the composition is checked against a float64 numpy evaluation of the same
-formulas in tests/test_oracle.py::test_decode_step_composition.
+the compositions are checked against float64 numpy evaluations of the same
+formulas in tests/test_oracle.py::test_decode_step_composition and
+::test_prefill_composition.
 """
 from __future__ import annotations
 
@@ -21,7 +26,7 @@ import math
 import numpy as np
 
 from . import (add_inplace, apply_rope_neox, argmax_rows, causal_attention, linear_nobias_int8,
-               rms_norm, rms_norm_per_head, rope_table, swiglu_split)
+               rms_norm, rms_norm_per_head, rope_table, swiglu_multiply, swiglu_split)
 
 
 def decode_int8_step(w: dict, k_cache: np.ndarray, v_cache: np.ndarray, pos: int,
@@ -62,3 +67,43 @@ def decode_int8_step(w: dict, k_cache: np.ndarray, v_cache: np.ndarray, pos: int
     vocab = w["lm_head"][1].size
     logits = linear_nobias_int8(xn, *w["lm_head"], 1, H, vocab, threads)
     return int(argmax_rows(logits, 1, vocab)[0]), xn, logits
+
+
+def prefill_int8(w: dict, k_cache: np.ndarray, v_cache: np.ndarray, start_pos: int,
+                 embeds: np.ndarray, seq_len: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                 eps: float = 1e-6, theta: float = 1e6, threads: int = 1, layers=None) -> np.ndarray:
+    """``seq_len`` tokens at positions start_pos.. (decoder.rs:751-847). Cache rows
+    start_pos..start_pos+seq_len-1 of every layer are written; returns the
+    residual stream x [seq_len * hidden] after the last layer. ``layers`` (an
+    iterable of layer dicts) replaces w["layers"] when given."""
+    T = seq_len
+    H = embeds.size // T
+    q_dim, kv_dim = n_heads * head_dim, n_kv_heads * head_dim
+    cos, sin = rope_table(start_pos + T, head_dim, theta)
+    c = cos[start_pos * head_dim:(start_pos + T) * head_dim]
+    s = sin[start_pos * head_dim:(start_pos + T) * head_dim]
+    scale = 1.0 / math.sqrt(head_dim)
+    total = start_pos + T
+    x = np.array(embeds, np.float32).ravel()
+    for l, lw in enumerate(w["layers"] if layers is None else layers):
+        xn = rms_norm(x, lw["input_norm"], T, H, eps)
+        q = linear_nobias_int8(xn, *lw["wq"], T, H, q_dim, threads)
+        k = linear_nobias_int8(xn, *lw["wk"], T, H, kv_dim, threads)
+        v = linear_nobias_int8(xn, *lw["wv"], T, H, kv_dim, threads)
+        q = rms_norm_per_head(q, lw["q_norm"], T, n_heads, head_dim, eps)
+        k = rms_norm_per_head(k, lw["k_norm"], T, n_kv_heads, head_dim, eps)
+        q = apply_rope_neox(q, c, s, T, n_heads, head_dim)
+        k = apply_rope_neox(k, c, s, T, n_kv_heads, head_dim)
+        k_cache[l, start_pos:total] = k.reshape(T, kv_dim)
+        v_cache[l, start_pos:total] = v.reshape(T, kv_dim)
+        attn = causal_attention(q, k_cache[l, :total].ravel(), v_cache[l, :total].ravel(), T, total,
+                                n_heads, n_kv_heads, head_dim, scale, start_pos)
+        proj = linear_nobias_int8(attn, *lw["wo"], T, q_dim, H, threads)
+        add_inplace(x, proj)
+        xn = rms_norm(x, lw["post_attn_norm"], T, H, eps)
+        inter = lw["gate_up"][1].size // 2
+        gu = linear_nobias_int8(xn, *lw["gate_up"], T, H, 2 * inter, threads)
+        gate = swiglu_multiply(gu, T, inter)
+        ffn = linear_nobias_int8(gate, *lw["down"], T, inter, H, threads)
+        add_inplace(x, ffn)
+    return x

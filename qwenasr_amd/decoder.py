@@ -19,6 +19,14 @@ argmax (decoder.rs:929-963). Everything stays on the device: the token id is
 written to a device int32, and the hidden state, KV cache and RoPE tables
 never leave HBM.
 
+``DecoderInt8.prefill`` runs the reference's INT8 prefill
+(decoder.rs:751-847) for a chunk of tokens: per layer RMSNorm (fused with the
+previous layer's residual add), q/k/v (one matrix-core GEMM launch), q/k head
+RMSNorm + RoPE with the chunk's K/V rows written into the cache, causal
+attention over the cache (matrix cores), o, residual add + post-attention
+RMSNorm, gate/up, the prefill SwiGLU (fast_exp form), down: 9 launches per
+layer, then the last residual add.
+
 Weights come from ``qint8.load_decoder_int8`` (or any dict of the same
 layout); ``DecoderInt8.decode`` runs one token and can be captured in a HIP
 graph (no host synchronisation, no allocation after construction for a fixed
@@ -67,6 +75,62 @@ class DecoderInt8:
         self.attn_ws = K.attention_workspace(1, n_heads, head_dim, dev)
         self.lm_ws = K.lm_head_workspace(self.vocab, dev)
         self.scale = 1.0 / math.sqrt(head_dim)
+
+    def _ensure_prefill(self, T: int) -> None:
+        if getattr(self, "_pcap", 0) >= T:
+            return
+        f32 = dict(dtype=torch.float32, device=self.x.device)
+        H, I, q_dim, kv_dim = self.H, self.I, self.nq * self.hd, self.nk * self.hd
+        self.px = torch.empty(T * H, **f32)
+        self.pxn = torch.empty(T * H, **f32)
+        self.pq = torch.empty(T * q_dim, **f32)
+        self.pk = torch.empty(T * kv_dim, **f32)
+        self.pv = torch.empty(T * kv_dim, **f32)
+        self.pattn = torch.empty(T * q_dim, **f32)
+        self.pproj = torch.empty(T * H, **f32)
+        self.pgu = torch.empty(T * 2 * I, **f32)
+        self.pgate = torch.empty(T * I, **f32)
+        self.pffn = torch.empty(T * H, **f32)
+        self._pcap = T
+
+    def prepare_prefill(self, start_pos: int, T: int) -> None:
+        """Host-side growth before a prefill of T tokens at start_pos
+        (decoder.rs:770-781): cache capacity, RoPE rows, the chunk's buffers."""
+        if start_pos + T > self.kv.max_seq:
+            self.kv.grow(start_pos + T + 1024)
+        self.rope.ensure(start_pos + T, self.hd, self.theta)
+        self._ensure_prefill(T)
+
+    def prefill(self, embeds: torch.Tensor, T: int, start_pos: int) -> None:
+        """T tokens at positions start_pos.. (decoder.rs:751-847): writes cache rows
+        start_pos..start_pos+T-1 of every layer; ``self.px[:T*H]`` receives the
+        residual stream after the last layer. Call ``prepare_prefill`` first."""
+        H, I, nq, nk, hd, eps = self.H, self.I, self.nq, self.nk, self.hd, self.eps
+        q_dim = nq * hd
+        total = start_pos + T
+        x = self.px
+        x[:T * H].copy_(embeds[:T * H])
+        for l, lw in enumerate(self.w["layers"]):
+            if l == 0:
+                K.rms_norm(self.pxn, x, lw["input_norm"], T, H, eps)
+            else:  # previous layer's residual add (decoder.rs:843) + this layer's input norm
+                K.add_rms_norm(x, self.pffn, lw["input_norm"], self.pxn, T, H, eps)
+            K.linear_nobias_int8_multi([self.pq, self.pk, self.pv], [lw["wq"], lw["wk"], lw["wv"]],
+                                       self.pxn, T, H)
+            kb, vb = self.kv.k_layer_block(l), self.kv.v_layer_block(l)
+            K.head_rms_norm_rope_kv(self.pq, self.pk, self.pv, lw["q_norm"], lw["k_norm"], self.rope, None,
+                                    start_pos, T, nq, nk, hd, eps, kb, vb, self.kv.max_seq)
+            K.causal_attention(self.pattn, self.pq, kb, vb, T, total, nq, nk, hd, self.scale, start_pos)
+            wo = lw["wo"]
+            K.linear_nobias_int8(self.pproj, self.pattn, wo.data, wo.scales, T, q_dim, H)
+            K.add_rms_norm(x, self.pproj, lw["post_attn_norm"], self.pxn, T, H, eps)
+            gu = lw["gate_up"]
+            K.linear_nobias_int8(self.pgu, self.pxn, gu.data, gu.scales, T, H, 2 * I)
+            K.swiglu_multiply(self.pgate, self.pgu, T, I)
+            dn = lw["down"]
+            K.linear_nobias_int8(self.pffn, self.pgate, dn.data, dn.scales, T, I, H)
+        K.add_inplace(x, self.pffn, T * H)
+        self.kv.len = total
 
     def prepare(self, pos: int) -> None:
         """Host-side growth before a decode at ``pos`` (decoder.rs:866-872):

@@ -16,7 +16,7 @@ import pytest
 
 import oracle
 from oracle import qint8_format as fmt
-from oracle.decoder import decode_int8_step
+from oracle.decoder import decode_int8_step, prefill_int8
 from tests.test_oracle import small_decoder
 
 torch = pytest.importorskip("torch")
@@ -143,3 +143,59 @@ def test_fused_norm_decode_equals_unfused(tmp_path, dev):
         for l in range(L):
             np.testing.assert_array_equal(decs[0].kv.k_layer(l).cpu().numpy(), decs[1].kv.k_layer(l).cpu().numpy())
             np.testing.assert_array_equal(decs[0].kv.v_layer(l).cpu().numpy(), decs[1].kv.v_layer(l).cpu().numpy())
+
+
+def _load(tmp_path, w, L, dev):
+    from qwenasr_amd import qint8
+
+    p = tmp_path / "model.qint8"
+    write_model(p, w, L)
+    with qint8.QuantFile.open(str(p)) as qf:
+        dims = qint8.detect_decoder_dims(qf)
+        dims.n_layers = L
+        return qint8.load_decoder_int8(qf, dims, dev)
+
+
+@pytest.mark.parametrize("H,I", [(1024, 3072), (2048, 6144)])
+def test_prefill_then_decode_matches_the_oracle(tmp_path, dev, H, I):
+    """The device prefill (decoder.rs:751-847) of two chunks -- 37 rows at
+    position 0 (ragged matrix-core GEMM tiles), then 20 rows at 37 -- against
+    the oracle's restatement: the residual stream after the last layer and
+    every cache row, then a decode step over the prefilled cache (token,
+    logits). Tolerance as for the decode step (chained kernels, 1e-4)."""
+    from qwenasr_amd.decoder import DecoderInt8
+
+    L, nq, nk, hd, vocab = 2, 16, 8, 128, 1000
+    r = np.random.default_rng([35, H])
+    w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
+    dec = DecoderInt8(_load(tmp_path, w, L, dev), H, I, L, nq, nk, hd, max_seq=64, device=dev)
+    kv = nk * hd
+    kc = np.zeros((L, 128, kv), np.float32)
+    vc = np.zeros_like(kc)
+    start = 0
+    for T in (37, 20):
+        X = r.standard_normal((T, H)).astype(np.float32)
+        x_ref = prefill_int8(w, kc, vc, start, X.ravel(), T, nq, nk, hd, threads=8)
+        dec.prepare_prefill(start, T)
+        dec.prefill(torch.from_numpy(X.ravel()).to(dev), T, start)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(dec.px[:T * H].cpu().numpy(), x_ref, rtol=TOL, atol=TOL,
+                                   err_msg=f"residual after chunk at {start}")
+        start += T
+        assert dec.kv.len == start
+        for l in range(L):
+            np.testing.assert_allclose(dec.kv.k_layer(l).cpu().numpy().reshape(start, kv), kc[l, :start],
+                                       rtol=TOL, atol=TOL, err_msg=f"k rows layer {l}")
+            np.testing.assert_allclose(dec.kv.v_layer(l).cpu().numpy().reshape(start, kv), vc[l, :start],
+                                       rtol=TOL, atol=TOL, err_msg=f"v rows layer {l}")
+    e = r.standard_normal(H).astype(np.float32)
+    tok, xn, logits = decode_int8_step(w, kc, vc, start, e, nq, nk, hd, threads=8)
+    dec.prepare(start)
+    dec.decode(torch.from_numpy(e).to(dev), start)
+    dec.finish(start)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(dec.x_norm.cpu().numpy(), xn, rtol=TOL, atol=TOL)
+    np.testing.assert_allclose(dec.logits.cpu().numpy(), logits, rtol=TOL, atol=TOL)
+    top2 = np.sort(logits)[-2:]
+    if top2[1] - top2[0] > 10 * TOL * max(1.0, abs(top2[1])):
+        assert int(dec.token.cpu()[0]) == tok

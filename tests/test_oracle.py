@@ -423,3 +423,76 @@ def test_decode_step_composition():
         top2 = np.sort(logits64)[-2:]
         if top2[1] - top2[0] > 1e-3:
             assert tok == tok64
+
+
+def _f64_prefill(w, kc, vc, start, X, nq, nk, hd, eps=1e-6, theta=1e6):
+    """float64 numpy evaluation of the prefill's formulas (no oracle kernels)."""
+    T, H = X.shape
+    half = hd // 2
+    inv = theta ** (-(2.0 * np.arange(half)) / hd)
+    ang = (start + np.arange(T))[:, None] * inv[None, :]
+    cos, sin = np.cos(ang), np.sin(ang)
+
+    def rms(v, g):
+        return v / np.sqrt(np.mean(v * v, axis=1, keepdims=True) + eps) * g
+
+    def lin(v, ws):
+        return (v @ ws[0].astype(np.float64).T) * ws[1]
+
+    def heads(v, n, g):
+        v = v.reshape(T, n, hd)
+        v = v / np.sqrt(np.mean(v * v, axis=2, keepdims=True) + eps) * g
+        a, b = v[..., :half], v[..., half:]
+        c, s = cos[:, None, :], sin[:, None, :]
+        return np.concatenate([a * c - b * s, b * c + a * s], axis=2).reshape(T, n * hd)
+
+    x = X.astype(np.float64)
+    total = start + T
+    for l, lw in enumerate(w["layers"]):
+        xn = rms(x, lw["input_norm"])
+        q = heads(lin(xn, lw["wq"]), nq, lw["q_norm"])
+        kc[l, start:total] = heads(lin(xn, lw["wk"]), nk, lw["k_norm"])
+        vc[l, start:total] = lin(xn, lw["wv"])
+        K = kc[l, :total].reshape(total, nk, hd)
+        V = vc[l, :total].reshape(total, nk, hd)
+        att = np.empty((T, nq, hd))
+        for i in range(T):
+            for h in range(nq):
+                sc = K[:start + i + 1, h // (nq // nk)] @ q[i].reshape(nq, hd)[h] / np.sqrt(hd)
+                p = np.exp(sc - sc.max())
+                att[i, h] = (p / p.sum()) @ V[:start + i + 1, h // (nq // nk)]
+        x = x + lin(att.reshape(T, nq * hd), lw["wo"])
+        xn = rms(x, lw["post_attn_norm"])
+        gu = lin(xn, lw["gate_up"])
+        g, u = gu[:, 0::2], gu[:, 1::2]
+        x = x + lin(g / (1 + np.exp(-g)) * u, lw["down"])
+    return x
+
+
+def test_prefill_composition():
+    """The restated prefill equals a float64 evaluation of decoder.rs:751-847's
+    formulas (a missing residual, a row using another row's RoPE position, a
+    causal mask off by one or a cache row written at the wrong offset would
+    not) over two chunks: 5 rows at position 0, then 3 more at position 5; a
+    decode step after them sees the same cache."""
+    from oracle.decoder import decode_int8_step, prefill_int8
+
+    r = np.random.default_rng(78)
+    H, I, L, nq, nk, hd, vocab = 64, 96, 2, 4, 2, 16, 50
+    w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
+    kc = np.zeros((L, 16, nk * hd), np.float32)
+    vc = np.zeros_like(kc)
+    kc64, vc64 = np.zeros(kc.shape), np.zeros(vc.shape)
+    start = 0
+    for T in (5, 3):
+        X = r.standard_normal((T, H)).astype(np.float32)
+        x = prefill_int8(w, kc, vc, start, X.ravel(), T, nq, nk, hd)
+        x64 = _f64_prefill(w, kc64, vc64, start, X, nq, nk, hd)
+        np.testing.assert_allclose(x.reshape(T, H), x64, rtol=1e-4, atol=1e-4)
+        np.testing.assert_allclose(kc[:, :start + T], kc64[:, :start + T], rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(vc[:, :start + T], vc64[:, :start + T], rtol=1e-4, atol=1e-5)
+        start += T
+    e = r.standard_normal(H).astype(np.float32)
+    _, xn, _ = decode_int8_step(w, kc, vc, start, e, nq, nk, hd)
+    _, xn64, _ = _f64_decode(w, kc64, vc64, start, e, nq, nk, hd)
+    np.testing.assert_allclose(xn, xn64, rtol=1e-4, atol=1e-4)
