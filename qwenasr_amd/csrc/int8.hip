@@ -616,6 +616,7 @@ bool matvec_shape(size_t in_dim) { return in_dim % 1024 == 0 && in_dim >= 1024 &
 // ---------------------------------------------------------------------------
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kGmBK = 64;           // K granularity of the GEMM path
 // K chunks in flight per thread in the LDS-staged kernel (2 and 3 measured
 // slower: the extra registers cost more than the latency they hide)
@@ -623,6 +624,10 @@ constexpr int kGemmPrefetch = 1;
 
 QASR_DEV unsigned short bf16_bits_trunc(float v) { return (unsigned short)(__float_as_uint(v) >> 16); }
 QASR_DEV float bf16_trunc(float v) { return __uint_as_float(__float_as_uint(v) & 0xffff0000u); }
+// bf16 bits of two floats, truncated, packed low element first
+QASR_DEV unsigned bf16_pair(float lo_elem, float hi_elem) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi_elem), __float_as_uint(lo_elem), 0x07060302u);
+}
 
 // BN weight rows x BT tokens per workgroup (BN in {64, 128}, BT in {32, 64});
 // the 4 waves form a 2 x 2 grid of (BN/2) x (BT/2) tiles.
@@ -684,20 +689,24 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
       N = set.N[m];
       bx0 = set.bx_begin[m];
     }
-  constexpr int MI = BN / 32, MJ = BT / 32;          // 16x16 tiles per wave
+  // 32x32x16 products: a wave's (BN/2) x (BT/2) tile is MI x MJ blocks of 32 x 32
+  // (the 16x16x32 form needs twice the independent accumulators to keep the
+  // matrix pipe full at one wave per SIMD)
+  constexpr int MI = BN / 64, MJ = BT / 64;
+  static_assert(BN % 64 == 0 && BT % 64 == 0, "32 x 32 blocks per wave");
   constexpr int TPW = 256 / BN, WB = BK / TPW;       // weight staging: threads per row, bytes each
   constexpr int TPX = 256 / BT, XF = BK / TPX;       // activation staging: threads per token, floats each
   auto wl = reinterpret_cast<unsigned short (*)[kGmRow]>(gm_lds);
   auto xl = reinterpret_cast<unsigned short (*)[BT][kGmRow]>(gm_lds + BN * kGmRow);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave & 1, wc = wave >> 1;
-  const int r = lane & 15, g = lane >> 4;
+  const int r = lane & 31, g = lane >> 5;
   const int n0 = (int)(bx - bx0) * BN, t0 = (int)by * BT;
-  v4f acc[MI][MJ];
+  v16f acc[MI][MJ];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < MJ; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < MJ; ++j) acc[i][j] = v16f{};
 
   // rows and tokens past the end re-read the last one (valid memory; not stored)
   const int w_row = tid / TPW, w_part = tid % TPW;
@@ -723,36 +732,25 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
 #pragma unroll
       for (int c = 0; c < WB / 16; ++c)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < 4; ++e) {  // int8 -> bf16 is exact (at most 8 significant bits)
           const int v = wv[q][c][e];
-          ushort4 h;  // int8 -> bf16 is exact (at most 8 significant bits)
-          h.x = bf16_bits_trunc((float)(int8_t)(v & 0xff));
-          h.y = bf16_bits_trunc((float)(int8_t)((v >> 8) & 0xff));
-          h.z = bf16_bits_trunc((float)(int8_t)((v >> 16) & 0xff));
-          h.w = bf16_bits_trunc((float)(int8_t)((v >> 24) & 0xff));
-          *reinterpret_cast<ushort4*>(&wl[w_row][WB * w_part + 16 * c + 4 * e]) = h;
+          const uint2 h = make_uint2(bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff)),
+                                     bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff)));
+          *reinterpret_cast<uint2*>(&wl[w_row][WB * w_part + 16 * c + 4 * e]) = h;
         }
 #pragma unroll
-      for (int c = 0; c < XF / 4; ++c) {
+      for (int c = 0; c < XF / 4; ++c) {  // x = hi + mid + lo exactly
         const float ev[4] = {xv[q][c].x, xv[q][c].y, xv[q][c].z, xv[q][c].w};
-        ushort4 th, tm, tl;
-        unsigned short* ph = reinterpret_cast<unsigned short*>(&th);
-        unsigned short* pm = reinterpret_cast<unsigned short*>(&tm);
-        unsigned short* pl = reinterpret_cast<unsigned short*>(&tl);
+        float r1[4], r2[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {  // x = hi + mid + lo exactly
-          const float hi = bf16_trunc(ev[e]);
-          const float r1 = ev[e] - hi;
-          const float mid = bf16_trunc(r1);
-          const float r2 = r1 - mid;  // at most 8 significant bits
-          ph[e] = bf16_bits_trunc(hi);
-          pm[e] = bf16_bits_trunc(mid);
-          pl[e] = bf16_bits_trunc(r2);
+        for (int e = 0; e < 4; ++e) {
+          r1[e] = ev[e] - bf16_trunc(ev[e]);
+          r2[e] = r1[e] - bf16_trunc(r1[e]);  // at most 8 significant bits
         }
         const int col = XF * x_part + 4 * c;
-        *reinterpret_cast<ushort4*>(&xl[0][x_tok][col]) = th;
-        *reinterpret_cast<ushort4*>(&xl[1][x_tok][col]) = tm;
-        *reinterpret_cast<ushort4*>(&xl[2][x_tok][col]) = tl;
+        *reinterpret_cast<uint2*>(&xl[0][x_tok][col]) = make_uint2(bf16_pair(ev[0], ev[1]), bf16_pair(ev[2], ev[3]));
+        *reinterpret_cast<uint2*>(&xl[1][x_tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
+        *reinterpret_cast<uint2*>(&xl[2][x_tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
       }
       __syncthreads();
       if (k0 + NPF * BK < K) {
@@ -763,26 +761,165 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
         for (int c = 0; c < XF / 4; ++c) xv[q][c] = ld4(xsrc + k0 + NPF * BK, c);
       }
 #pragma unroll
-      for (int kk = 0; kk < BK; kk += 32) {
+      for (int kk = 0; kk < BK; kk += 16) {
         v8bf a[MI], b[3][MJ];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
-          a[i] = *reinterpret_cast<const v8bf*>(&wl[(BN / 2) * wr + 16 * i + r][kk + 8 * g]);
+          a[i] = *reinterpret_cast<const v8bf*>(&wl[(BN / 2) * wr + 32 * i + r][kk + 8 * g]);
 #pragma unroll
         for (int term = 0; term < 3; ++term)
 #pragma unroll
           for (int j = 0; j < MJ; ++j)
-            b[term][j] = *reinterpret_cast<const v8bf*>(&xl[term][(BT / 2) * wc + 16 * j + r][kk + 8 * g]);
+            b[term][j] = *reinterpret_cast<const v8bf*>(&xl[term][(BT / 2) * wc + 32 * j + r][kk + 8 * g]);
 #pragma unroll
         for (int term = 0; term < 3; ++term)
 #pragma unroll
           for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int j = 0; j < MJ; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[term][j], acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[term][j], acc[i][j], 0, 0, 0);
       }
       __syncthreads();
     }
+  }
+
+  // lane l, register 4q + v of block (i, j) holds row n0 + (BN/2)wr + 32i + 8q + 4(l/32) + v
+  // of token t0 + (BT/2)wc + 32j + l%32
+  const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+  for (int j = 0; j < MJ; ++j) {
+    const int t = t0 + (BT / 2) * wc + 32 * j + r;
+    if (t >= T) continue;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + (BN / 2) * wr + 32 * i + 8 * q + 4 * g;
+        float res[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int nv = min(n + v, N - 1);
+          res[v] = acc[i][j][4 * q + v] * scales[nv];
+          if constexpr (BIAS) res[v] += bias[nv];
+        }
+        if (vec_out && n + 3 < N) {
+          *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+        }
+      }
+  }
+}
+
+// Variant of the LDS-staged kernel: only the activations (split once per
+// workgroup into the three bf16 terms) go through LDS; each wave loads its own
+// weight fragments straight into registers in the MFMA layout (16 contiguous
+// bytes of a row per lane: lane group g covers k = 16g..16g+15 of a 64-wide
+// chunk, the first 8 feeding one 32-slot product and the next 8 the other --
+// the B fragments are read from LDS with the same k order). A workgroup owns
+// BN weight rows x BT tokens, the 4 waves a 2 x 2 grid of (BN/2) x (BT/2).
+template <int BN, int BT, bool BIAS>
+__global__ __launch_bounds__(256) void w8a32_gemm_xlds_kernel(GemmSet set, TileMap map,
+                                                              const float* __restrict__ x, int T, int K) {
+  constexpr int BK = 64;
+  constexpr int kRow = BK + 8;                  // LDS row in bf16 (16-byte pad)
+  __shared__ __align__(16) unsigned short xl[3][BT][kRow];
+  unsigned bx, by;
+  tile_of(map, blockIdx.x, bx, by);
+  float* y = set.y[0];
+  const int8_t* w = set.w[0];
+  const float* scales = set.s[0];
+  const float* bias = set.b[0];
+  int N = set.N[0];
+  unsigned bx0 = 0;
+#pragma unroll
+  for (int m = 1; m < 4; ++m)
+    if (m < set.n && bx >= set.bx_begin[m]) {
+      y = set.y[m];
+      w = set.w[m];
+      scales = set.s[m];
+      bias = set.b[m];
+      N = set.N[m];
+      bx0 = set.bx_begin[m];
+    }
+  constexpr int MI = BN / 32, MJ = BT / 32;     // 16x16 tiles per wave
+  constexpr int TPX = 256 / BT, XF = BK / TPX;   // activation staging: threads per token, floats each
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave & 1, wc = wave >> 1;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = (int)(bx - bx0) * BN, t0 = (int)by * BT;
+  v4f acc[MI][MJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // rows and tokens past the end re-read the last one (valid memory; not stored)
+  const int8_t* wp[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) wp[i] = w + (size_t)min(n0 + (BN / 2) * wr + 16 * i + r, N - 1) * K + 16 * g;
+  const int x_tok = tid / TPX, x_part = tid % TPX;
+  const float* xsrc = x + (size_t)min(t0 + x_tok, T - 1) * K + XF * x_part;
+
+  v4i wv[MI];
+  float4 xv[XF / 4];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) wv[i] = *reinterpret_cast<const v4i*>(wp[i]);
+#pragma unroll
+  for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc, c);
+  for (int k0 = 0; k0 < K; k0 += BK) {
+#pragma unroll
+    for (int c = 0; c < XF / 4; ++c) {  // x = hi + mid + lo exactly
+      const float ev[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+      float r1[4], r2[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r1[e] = ev[e] - bf16_trunc(ev[e]);
+        r2[e] = r1[e] - bf16_trunc(r1[e]);  // at most 8 significant bits
+      }
+      const int col = XF * x_part + 4 * c;
+      *reinterpret_cast<uint2*>(&xl[0][x_tok][col]) = make_uint2(bf16_pair(ev[0], ev[1]), bf16_pair(ev[2], ev[3]));
+      *reinterpret_cast<uint2*>(&xl[1][x_tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
+      *reinterpret_cast<uint2*>(&xl[2][x_tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
+    }
+    // this chunk's weights: int8 -> bf16 (exact), k = 16g + 8h + e
+    v4u a[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int v = wv[i][q];
+        a[i][q >> 1][2 * (q & 1)] = bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff));
+        a[i][q >> 1][2 * (q & 1) + 1] =
+            bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff));
+      }
+    __syncthreads();
+    if (k0 + BK < K) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) wv[i] = *reinterpret_cast<const v4i*>(wp[i] + k0 + BK);
+#pragma unroll
+      for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc + k0 + BK, c);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v8bf b[3][MJ];
+#pragma unroll
+      for (int term = 0; term < 3; ++term)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          b[term][j] = *reinterpret_cast<const v8bf*>(&xl[term][(BT / 2) * wc + 16 * j + r][16 * g + 8 * h]);
+#pragma unroll
+      for (int term = 0; term < 3; ++term)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < MJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a[i][h]), b[term][j],
+                                                                acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
   }
 
   // lane holds rows n0 + (BN/2)wr + 16i + 4g + v (v = 0..3) of token t0 + (BT/2)wc + 16j + r
@@ -812,6 +949,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
   }
 }
 
+
 template <int BN, int BT, int BK>
 constexpr size_t gemm_lds_bytes() {
   return (size_t)(BN + 3 * BT) * (BK + 8) * 2;
@@ -838,49 +976,56 @@ inline unsigned xcd_split_cols(unsigned cols, unsigned rows, int BN, int BT) {
 // Split-K variant: the KW waves of a workgroup share one BN x BT output tile
 // and take interleaved 64-wide K steps (wave w: steps w, w + KW, ...). Each
 // wave loads its weight and activation fragments straight into registers in
-// the MFMA operand layout, so the main loop has no LDS traffic and no
-// barriers; each weight and activation element is converted once per
-// workgroup, as in the LDS-staged kernel. Within a 64-wide step, lane group g
-// (lanes 16g..16g+15) covers k = 16g..16g+15: the first 8 feed MFMA slots
-// 8g..8g+7 of the first 32-slot product and the next 8 those of the second
-// (the same permutation of k for both operands, so the dot product is
-// unchanged). The KW partial tiles are added in LDS in wave order.
-QASR_DEV unsigned bf16_pair(float lo_elem, float hi_elem) {  // upper halves of two floats
-  return __builtin_amdgcn_perm(__float_as_uint(hi_elem), __float_as_uint(lo_elem), 0x07060302u);
+// the operand layout of v_mfma_f32_32x32x16_bf16 (A[i][k] in lane i + 32(k/8),
+// element k%8; B alike), so the main loop has no LDS traffic and no barriers;
+// each weight and activation element is converted once per workgroup. Within
+// a 32-wide K chunk, lane group g (lanes 32g..32g+31) covers k = 16g..16g+15:
+// the first 8 feed MFMA slots 8g..8g+7 of one 16-slot product and the next 8
+// those of the other (the same permutation of k for both operands, so the dot
+// product is unchanged). With a single 32 x 32 block per wave each bf16 term
+// gets its own accumulator (three independent chains for the matrix pipe),
+// added hi + mid + lo at the end. The KW partial tiles are added in LDS in
+// wave order.
+QASR_DEV unsigned bf16_pair_i8(int v, int byte) {  // bytes byte, byte + 1 of v as two bf16
+  return bf16_pair((float)(int8_t)((v >> (8 * byte)) & 0xff), (float)(int8_t)((v >> (8 * byte + 8)) & 0xff));
 }
 
 template <int MI, int MJ>
 struct KsplitRaw {
-  v4i w[MI];          // 16 int8 of one weight row
-  float4 x[MJ][4];    // 16 floats of one token
+  v4i w[MI][2];          // per 32-wide chunk: 16 int8 of one weight row
+  float4 x[MJ][2][4];    // per 32-wide chunk: 16 floats of one token
 };
 
-// The KW waves' partial tiles are added in LDS in wave order (deterministic),
-// the tile pairs (i, j) split over the waves; epilogue y = sum * scale (+ bias).
-// Lane (r, g) of pair (i, j) holds rows n0 + 16i + 4g + v of token t0 + 16j + r.
+// Lane l, register 4q + v of block (i, j) holds row n0 + 32i + 8q + 4(l/32) + v
+// of token t0 + 32j + l%32; the KW waves' partial tiles are added in LDS in
+// wave order (deterministic), the blocks split over the waves; epilogue
+// y = sum * scale (+ bias).
 template <int MI, int MJ, int KW, bool BIAS>
-QASR_DEV void ksplit_reduce_store(const v4f (&acc)[MI][MJ], float* red, int wave, int lane, float* y,
+QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wave, int lane, float* y,
                                   const float* scales, const float* bias, int N, int T, int n0, int t0) {
-  const int r = lane & 15, g = lane >> 4;
-  float* mine = red + (size_t)wave * (MI * MJ * 4 * 64);
+  const int r = lane & 31, g = lane >> 5;
+  constexpr int PER_WAVE = MI * MJ * 16 * 64;  // floats
+  float* mine = red + (size_t)wave * PER_WAVE;
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < MJ; ++j)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) mine[((i * MJ + j) * 4 + v) * 64 + lane] = acc[i][j][v];
+      for (int e = 0; e < 16; ++e) mine[((i * MJ + j) * 16 + e) * 64 + lane] = acc[i][j][e];
   __syncthreads();
   const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
-  for (int p = wave; p < MI * MJ; p += KW) {
-    const int i = p / MJ, j = p % MJ;
-    const int t = t0 + 16 * j + r;
-    const int n = n0 + 16 * i + 4 * g;
+  for (int p = wave; p < MI * MJ * 4; p += KW) {  // (block, register quad) items
+    const int blk = p >> 2, q = p & 3;
+    const int i = blk / MJ, j = blk % MJ;
+    const int t = t0 + 32 * j + r;
+    const int n = n0 + 32 * i + 8 * q + 4 * g;
     float res[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      float sum = red[(p * 4 + v) * 64 + lane];
+      const int e = (blk * 16 + 4 * q + v) * 64 + lane;
+      float sum = red[e];
 #pragma unroll
-      for (int ww = 1; ww < KW; ++ww) sum += red[(size_t)ww * (MI * MJ * 4 * 64) + (p * 4 + v) * 64 + lane];
+      for (int ww = 1; ww < KW; ++ww) sum += red[(size_t)ww * PER_WAVE + e];
       const int nv = min(n + v, N - 1);
       res[v] = sum * scales[nv];
       if constexpr (BIAS) res[v] += bias[nv];
@@ -899,8 +1044,10 @@ QASR_DEV void ksplit_reduce_store(const v4f (&acc)[MI][MJ], float* red, int wave
 template <int BN, int BT, int KW, bool BIAS>
 __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set, TileMap map,
                                                                     const float* __restrict__ x, int T, int K) {
-  constexpr int MI = BN / 16, MJ = BT / 16;
-  extern __shared__ __align__(16) float gk_red[];  // [KW][MI * MJ * 4][64] partial tiles
+  constexpr int MI = BN / 32, MJ = BT / 32;
+  constexpr int NT = MI * MJ == 1 ? 3 : 1;  // accumulators per block: one per term for a single block
+  static_assert(BN % 32 == 0 && BT % 32 == 0, "32 x 32 blocks");
+  extern __shared__ __align__(16) float gk_red[];  // [KW][MI * MJ * 16][64] partial tiles
   unsigned bx, by;
   tile_of(map, blockIdx.x, bx, by);
   float* y = set.y[0];
@@ -921,75 +1068,80 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
     }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches
-  const int r = lane & 15, g = lane >> 4;
+  const int r = lane & 31, g = lane >> 5;
   const int n0 = (int)(bx - bx0) * BN, t0 = (int)by * BT;
   // rows and tokens past the end re-read the last one (valid memory; not stored)
   const int8_t* wp[MI];
   const float* xp[MJ];
 #pragma unroll
-  for (int i = 0; i < MI; ++i) wp[i] = w + (size_t)min(n0 + 16 * i + r, N - 1) * K + 16 * g;
+  for (int i = 0; i < MI; ++i) wp[i] = w + (size_t)min(n0 + 32 * i + r, N - 1) * K + 16 * g;
 #pragma unroll
-  for (int j = 0; j < MJ; ++j) xp[j] = x + (size_t)min(t0 + 16 * j + r, T - 1) * K + 16 * g;
+  for (int j = 0; j < MJ; ++j) xp[j] = x + (size_t)min(t0 + 32 * j + r, T - 1) * K + 16 * g;
 
-  v4f acc[MI][MJ];
+  v16f acc[NT][MI][MJ];
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+  for (int u = 0; u < NT; ++u)
 #pragma unroll
-    for (int j = 0; j < MJ; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < MJ; ++j) acc[u][i][j] = v16f{};
 
   auto load = [&](KsplitRaw<MI, MJ>& raw, int step) {
-    const int k = step * 64;
 #pragma unroll
-    for (int i = 0; i < MI; ++i) raw.w[i] = *reinterpret_cast<const v4i*>(wp[i] + k);
+    for (int c = 0; c < 2; ++c) {
+      const int k = step * 64 + 32 * c;
 #pragma unroll
-    for (int j = 0; j < MJ; ++j)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) raw.x[j][c] = ld4(xp[j] + k, c);
-  };
-  auto compute = [&](const KsplitRaw<MI, MJ>& raw) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {  // k = 16g + 8h + (0..7): MFMA slots 8g..8g+7
-      // weights: int8 -> bf16 is exact (at most 8 significant bits)
-      v4u a[MI];
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int v = raw.w[i][2 * h + q];
-          a[i][2 * q] = bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff));
-          a[i][2 * q + 1] = bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff));
-        }
-      // activations: x = hi + mid + lo exactly (three truncated bf16 terms)
-      v4u b[3][MJ];
+      for (int i = 0; i < MI; ++i) raw.w[i][c] = *reinterpret_cast<const v4i*>(wp[i] + k);
 #pragma unroll
       for (int j = 0; j < MJ; ++j)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const float4 xv = raw.x[j][2 * h + c];
-          const float e[4] = {xv.x, xv.y, xv.z, xv.w};
-          float r1[4], r2[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            r1[q] = e[q] - bf16_trunc(e[q]);
-            r2[q] = r1[q] - bf16_trunc(r1[q]);  // at most 8 significant bits
-          }
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            b[0][j][2 * c + q] = bf16_pair(e[2 * q], e[2 * q + 1]);
-            b[1][j][2 * c + q] = bf16_pair(r1[2 * q], r1[2 * q + 1]);
-            b[2][j][2 * c + q] = bf16_pair(r2[2 * q], r2[2 * q + 1]);
-          }
-        }
-#pragma unroll
-      for (int term = 0; term < 3; ++term)
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-          for (int j = 0; j < MJ; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a[i]),
-                                                                __builtin_bit_cast(v8bf, b[term][j]),
-                                                                acc[i][j], 0, 0, 0);
+        for (int f = 0; f < 4; ++f) raw.x[j][c][f] = ld4(xp[j] + k, f);
     }
+  };
+  auto compute = [&](const KsplitRaw<MI, MJ>& raw) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // k = 32c + 16g + 8h + (0..7): MFMA slots 8g..8g+7
+        // weights: int8 -> bf16 is exact (at most 8 significant bits)
+        v4u a[MI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int v0 = raw.w[i][c][2 * h], v1 = raw.w[i][c][2 * h + 1];
+          a[i] = v4u{bf16_pair_i8(v0, 0), bf16_pair_i8(v0, 2), bf16_pair_i8(v1, 0), bf16_pair_i8(v1, 2)};
+        }
+        // activations: x = hi + mid + lo exactly (three truncated bf16 terms)
+        v4u b[3][MJ];
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            const float4 xv = raw.x[j][c][2 * h + f];
+            const float e[4] = {xv.x, xv.y, xv.z, xv.w};
+            float r1[4], r2[4];
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+              r1[qq] = e[qq] - bf16_trunc(e[qq]);
+              r2[qq] = r1[qq] - bf16_trunc(r1[qq]);  // at most 8 significant bits
+            }
+            b[0][j][2 * f] = bf16_pair(e[0], e[1]);
+            b[0][j][2 * f + 1] = bf16_pair(e[2], e[3]);
+            b[1][j][2 * f] = bf16_pair(r1[0], r1[1]);
+            b[1][j][2 * f + 1] = bf16_pair(r1[2], r1[3]);
+            b[2][j][2 * f] = bf16_pair(r2[0], r2[1]);
+            b[2][j][2 * f + 1] = bf16_pair(r2[2], r2[3]);
+          }
+#pragma unroll
+        for (int term = 0; term < 3; ++term)
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < MJ; ++j) {
+              v16f& d = acc[NT == 3 ? term : 0][i][j];
+              d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a[i]),
+                                                          __builtin_bit_cast(v8bf, b[term][j]), d, 0, 0, 0);
+            }
+      }
   };
 
   // two register sets in turn: the loads of step s + KW are in flight while
@@ -1004,8 +1156,11 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
     if (s + 2 * KW < steps) load(ra, s + 2 * KW);
     compute(rb);
   }
-
-  ksplit_reduce_store<MI, MJ, KW, BIAS>(acc, gk_red, wave, lane, y, scales, bias, N, T, n0, t0);
+  if constexpr (NT == 3) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[0][0][0][e] = (acc[0][0][0][e] + acc[1][0][0][e]) + acc[2][0][0][e];
+  }
+  ksplit_reduce_store<MI, MJ, KW, BIAS>(acc[0], gk_red, wave, lane, y, scales, bias, N, T, n0, t0);
 }
 
 template <int BN, int BT, int KW, bool BIAS>
@@ -1018,6 +1173,17 @@ bool try_gemm_ksplit(const GemmSet& set, unsigned cols, const float* x, int T, i
   map.rows = (unsigned)((T + BT - 1) / BT);
   map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
   w8a32_gemm_ksplit_kernel<BN, BT, KW, BIAS><<<map.cols * map.rows, 64 * KW, lds, st>>>(set, map, x, T, K);
+  return true;
+}
+
+template <int BN, int BT, bool BIAS>
+bool try_gemm_xlds(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
+  if (K % 64 != 0) return false;
+  TileMap map;
+  map.cols = cols;
+  map.rows = (unsigned)((T + BT - 1) / BT);
+  map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
+  w8a32_gemm_xlds_kernel<BN, BT, BIAS><<<map.cols * map.rows, 256, 0, st>>>(set, map, x, T, K);
   return true;
 }
 
@@ -1053,10 +1219,26 @@ void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
   const long long rows64 = (T + 63) / 64, rows32 = (T + 31) / 32;
   unsigned c = cols(128);
   if (c * rows64 >= 256) {
+#ifdef QASR_XLDS
+    try_gemm_xlds<128, 64, BIAS>(set, c, x, T, K, st);
+#else
     try_gemm<128, 64, 64, kGemmPrefetch, BIAS>(set, c, x, T, K, st);
+#endif
     return;
   }
   c = cols(64);
+#ifdef QASR_XLDS_SMALL
+  if (c * rows64 >= 256) {
+    try_gemm_xlds<64, 64, BIAS>(set, c, x, T, K, st);
+    return;
+  }
+  if (c * rows32 >= 256) {
+    try_gemm_xlds<64, 32, BIAS>(set, c, x, T, K, st);
+    return;
+  }
+  try_gemm_xlds<32, 32, BIAS>(set, cols(32), x, T, K, st);
+  return;
+#endif
   if (c * rows64 >= 256) {
     try_gemm_ksplit<64, 64, 4, BIAS>(set, c, x, T, K, st);
     return;
