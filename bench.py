@@ -519,11 +519,22 @@ class PrefillStep(Workload):
         self.embeds = [self.randn(T * H) for _ in range(2)]
         kv, q_dim = nk * hd, nq * hd
         proj = sum(w.out_dim * w.in_dim for k, w in layers[0].items() if isinstance(w, K.QuantWeight))
-        layer_bytes = (sum(w.out_dim * w.in_dim + w.out_dim * F for k, w in layers[0].items()
-                           if isinstance(w, K.QuantWeight))
-                       + (2 * hd + 2 * H) * F                      # norm gains
-                       + 2 * T * kv * F)                          # the chunk's k/v rows written
-        step_bytes = L * layer_bytes + 2 * T * H * F              # embeddings in, residual out
+        # algorithmic bytes of the 9 kernels of a layer: each one's inputs read and
+        # outputs written once (the reference's op sequence moves every activation
+        # between its ops through memory)
+        row = T * F
+        qkv_out = q_dim + 2 * kv
+        layer_bytes = (
+            4 * row * H + H * F                                          # add + RMSNorm: x, delta in; x, norm out
+            + qkv_out * H + qkv_out * F + row * H + row * qkv_out        # q/k/v GEMM
+            + 2 * row * q_dim + 4 * row * kv + 2 * hd * F + 2 * T * hd * F  # head norm+RoPE+KV store (+ gains, tables)
+            + 2 * row * q_dim + 2 * row * kv                             # attention: q, k, v rows in, out
+            + H * q_dim + H * F + row * q_dim + row * H                  # o GEMM
+            + 4 * row * H + H * F                                        # add + post-attention RMSNorm
+            + 2 * I * H + 2 * I * F + row * H + row * 2 * I              # gate/up GEMM
+            + row * 2 * I + row * I                                      # SwiGLU
+            + H * I + H * F + row * I + row * H)                         # down GEMM
+        step_bytes = L * layer_bytes + 3 * row * H                       # + the last residual add
         gemm_flops = 2 * T * proj
         attn_flops = 2 * 2 * hd * nq * (T * (T + 1) // 2)         # QK and PV over the causal triangle
         self.step_flops = L * (gemm_flops + attn_flops)
