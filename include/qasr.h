@@ -242,6 +242,19 @@ int qasr_gate_up_swiglu_int8_f32(float* out, const float* x, const int8_t* w_gat
                                  const float* scales_gate_up, size_t seq_len, size_t in_dim,
                                  size_t intermediate, void* stream);
 
+/* The prefill's gate/up projection and SwiGLU in one call (decoder.rs:831-834):
+ * gate_up = linear_nobias_int8(x, w_gate_up) on the row-interleaved fused
+ * weight, then kernels::swiglu_multiply (kernels/mod.rs:965-985, the
+ * fast_exp form of avx.rs:565-599: out[s, j] = silu(gate_up[s, 2j]) *
+ * gate_up[s, 2j + 1]). The gate_up values are never written. From 8 tokens
+ * (the matrix-core GEMM path of qasr_linear_nobias_int8_f32) equal bit for
+ * bit to qasr_linear_nobias_int8_f32 followed by qasr_swiglu_multiply_f32;
+ * below, one wave per (token, output) takes the two dots (fp32, another
+ * order). No reference counterpart as one call. */
+int qasr_gate_up_swiglu_multiply_int8_f32(float* out, const float* x, const int8_t* w_gate_up,
+                                          const float* scales_gate_up, size_t seq_len,
+                                          size_t in_dim, size_t intermediate, void* stream);
+
 /* Up to 4 W8A32 projections of the same input in one launch: for m < n_mats,
  * ys[m][s, :] = qasr_linear_nobias_int8_f32(x[s, :], ws[m], scales[m]) with
  * out_dims[m] rows (the q/k/v calls of one decode step share x:

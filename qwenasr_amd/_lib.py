@@ -69,6 +69,7 @@ SIGNATURES: dict[str, list] = {
     "qasr_linear_int8_f32": [P, P, P, P, P, Z, Z, Z, P],
     "qasr_linear_nobias_int8_multi_f32": [Z, P, P, P, P, P, Z, Z, P],
     "qasr_gate_up_swiglu_int8_f32": [P, P, P, P, Z, Z, Z, P],
+    "qasr_gate_up_swiglu_multiply_int8_f32": [P, P, P, P, Z, Z, Z, P],
     "qasr_add_rms_norm_linear_nobias_int8_multi_f32": [Z, P, P, P, P, P, P, P, P, Z, F, P],
     "qasr_add_rms_norm_gate_up_swiglu_int8_f32": [P, P, P, P, P, P, P, Z, Z, F, P],
     "qasr_interleave_gate_up_i8": [P, P, P, P, P, P, Z, Z, P],

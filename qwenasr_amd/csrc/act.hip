@@ -16,10 +16,7 @@ namespace {
 // (avx.rs:565-599): columns j < (inter & ~7) use g / (1 + fast_exp(0 - g)),
 // the row tail uses g / (1 + expf(-g)); out = silu * u.
 // ---------------------------------------------------------------------------
-QASR_DEV float swiglu_ref(float g, float u, bool fast) {
-  const float s = fast ? g / (1.0f + ref_fast_exp(0.0f - g)) : g / (1.0f + expf(-g));
-  return s * u;
-}
+
 
 // One output float4 per thread over an exact grid. Without a row tail
 // (inter % 8 == 0) every column takes the fast_exp path and no row index is

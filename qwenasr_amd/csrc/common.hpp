@@ -138,6 +138,15 @@ QASR_DEV float ref_fast_exp(float x) {
   return e * p;
 }
 
+// One output of the prefill SwiGLU (kernels::swiglu_multiply, x86 arithmetic
+// avx.rs:565-599): silu(g) * u with silu from fast_exp for columns below
+// inter & ~7 (fast) and from expf for the row tail. Shared by the SwiGLU
+// kernel and the gate/up GEMM's SwiGLU epilogue, which agree bit for bit.
+QASR_DEV float swiglu_ref(float g, float u, bool fast) {
+  const float s = fast ? g / (1.0f + ref_fast_exp(0.0f - g)) : g / (1.0f + expf(-g));
+  return s * u;
+}
+
 QASR_DEV float qnan() { return __int_as_float(0x7fc00000); }
 
 // Per-head RMSNorm (NORM) and NeoX RoPE (ROPE) of one head held by a group of

@@ -321,7 +321,9 @@ __global__ __launch_bounds__(256) void w8a32_rows_multi_kernel(MatSet ms, const 
 }
 
 // Gate/up pairs for any shape: one wave per (token, output j) takes the dots
-// of interleaved rows 2j (gate) and 2j + 1 (up) and applies the decode SwiGLU.
+// of interleaved rows 2j (gate) and 2j + 1 (up) and applies the decode SwiGLU
+// (libm expf) or, with PREFILL, the prefill one (swiglu_ref).
+template <bool PREFILL = false>
 __global__ __launch_bounds__(256) void gate_up_swiglu_w8a32_pairs_kernel(
     float* out, const float* x, const int8_t* w, const float* scales, int seq, int in_dim,
     int inter) {
@@ -341,7 +343,10 @@ __global__ __launch_bounds__(256) void gate_up_swiglu_w8a32_pairs_kernel(
   au = wave_sum(au);
   if (lane == 0) {
     const float g = ag * scales[2 * j], u = au * scales[2 * j + 1];
-    out[(size_t)s * inter + j] = silu_expf(g) * u;
+    if constexpr (PREFILL)
+      out[(size_t)s * inter + j] = swiglu_ref(g, u, j < (inter & ~7));
+    else
+      out[(size_t)s * inter + j] = silu_expf(g) * u;
   }
 }
 
@@ -618,6 +623,10 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kGmBK = 64;           // K granularity of the GEMM path
+// GEMM epilogues: y = acc * scale; + bias; or the prefill SwiGLU of each
+// interleaved (gate, up) row pair, y[t, n/2] = swiglu(y[t, n], y[t, n + 1]),
+// an output row of N/2 (kernels::swiglu_multiply after the gate/up projection)
+enum GemmEpi { kGemmRows = 0, kGemmBias = 1, kGemmSwiglu = 2 };
 // K chunks in flight per thread in the LDS-staged kernel (2 and 3 measured
 // slower: the extra registers cost more than the latency they hide)
 constexpr int kGemmPrefetch = 1;
@@ -666,7 +675,16 @@ QASR_DEV void tile_of(const TileMap& m, unsigned b, unsigned& bx, unsigned& by) 
 
 // NPF chunks of weights and activations are in flight in registers: the loads
 // of chunk c + NPF are issued right after chunk c is staged into LDS.
-template <int BN, int BT, int BK, int NPF, bool BIAS>
+// Rows n..n+3 (n a multiple of 4) of token t are the interleaved pairs of
+// outputs n/2 and n/2 + 1 of the SwiGLU row (N/2 wide).
+QASR_DEV void swiglu_store(float* y, const float (&res)[4], int t, int n, int N) {
+  const int inter = N >> 1, j = n >> 1, fast_end = inter & ~7;
+  float* row = y + (size_t)t * inter;
+  if (n + 1 < N) row[j] = swiglu_ref(res[0], res[1], j < fast_end);
+  if (n + 3 < N) row[j + 1] = swiglu_ref(res[2], res[3], j + 1 < fast_end);
+}
+
+template <int BN, int BT, int BK, int NPF, int EPI>
 __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, TileMap map,
                                                                 const float* __restrict__ x, int T, int K) {
   constexpr int kGmRow = BK + 8;  // LDS row in bf16 (16-byte pad)
@@ -800,9 +818,11 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
         for (int v = 0; v < 4; ++v) {
           const int nv = min(n + v, N - 1);
           res[v] = acc[i][j][4 * q + v] * scales[nv];
-          if constexpr (BIAS) res[v] += bias[nv];
+          if constexpr (EPI == kGemmBias) res[v] += bias[nv];
         }
-        if (vec_out && n + 3 < N) {
+        if constexpr (EPI == kGemmSwiglu) {
+          swiglu_store(y, res, t, n, N);
+        } else if (vec_out && n + 3 < N) {
           *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
         } else {
 #pragma unroll
@@ -812,143 +832,6 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
       }
   }
 }
-
-// Variant of the LDS-staged kernel: only the activations (split once per
-// workgroup into the three bf16 terms) go through LDS; each wave loads its own
-// weight fragments straight into registers in the MFMA layout (16 contiguous
-// bytes of a row per lane: lane group g covers k = 16g..16g+15 of a 64-wide
-// chunk, the first 8 feeding one 32-slot product and the next 8 the other --
-// the B fragments are read from LDS with the same k order). A workgroup owns
-// BN weight rows x BT tokens, the 4 waves a 2 x 2 grid of (BN/2) x (BT/2).
-template <int BN, int BT, bool BIAS>
-__global__ __launch_bounds__(256) void w8a32_gemm_xlds_kernel(GemmSet set, TileMap map,
-                                                              const float* __restrict__ x, int T, int K) {
-  constexpr int BK = 64;
-  constexpr int kRow = BK + 8;                  // LDS row in bf16 (16-byte pad)
-  __shared__ __align__(16) unsigned short xl[3][BT][kRow];
-  unsigned bx, by;
-  tile_of(map, blockIdx.x, bx, by);
-  float* y = set.y[0];
-  const int8_t* w = set.w[0];
-  const float* scales = set.s[0];
-  const float* bias = set.b[0];
-  int N = set.N[0];
-  unsigned bx0 = 0;
-#pragma unroll
-  for (int m = 1; m < 4; ++m)
-    if (m < set.n && bx >= set.bx_begin[m]) {
-      y = set.y[m];
-      w = set.w[m];
-      scales = set.s[m];
-      bias = set.b[m];
-      N = set.N[m];
-      bx0 = set.bx_begin[m];
-    }
-  constexpr int MI = BN / 32, MJ = BT / 32;     // 16x16 tiles per wave
-  constexpr int TPX = 256 / BT, XF = BK / TPX;   // activation staging: threads per token, floats each
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave & 1, wc = wave >> 1;
-  const int r = lane & 15, g = lane >> 4;
-  const int n0 = (int)(bx - bx0) * BN, t0 = (int)by * BT;
-  v4f acc[MI][MJ];
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < MJ; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // rows and tokens past the end re-read the last one (valid memory; not stored)
-  const int8_t* wp[MI];
-#pragma unroll
-  for (int i = 0; i < MI; ++i) wp[i] = w + (size_t)min(n0 + (BN / 2) * wr + 16 * i + r, N - 1) * K + 16 * g;
-  const int x_tok = tid / TPX, x_part = tid % TPX;
-  const float* xsrc = x + (size_t)min(t0 + x_tok, T - 1) * K + XF * x_part;
-
-  v4i wv[MI];
-  float4 xv[XF / 4];
-#pragma unroll
-  for (int i = 0; i < MI; ++i) wv[i] = *reinterpret_cast<const v4i*>(wp[i]);
-#pragma unroll
-  for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc, c);
-  for (int k0 = 0; k0 < K; k0 += BK) {
-#pragma unroll
-    for (int c = 0; c < XF / 4; ++c) {  // x = hi + mid + lo exactly
-      const float ev[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
-      float r1[4], r2[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        r1[e] = ev[e] - bf16_trunc(ev[e]);
-        r2[e] = r1[e] - bf16_trunc(r1[e]);  // at most 8 significant bits
-      }
-      const int col = XF * x_part + 4 * c;
-      *reinterpret_cast<uint2*>(&xl[0][x_tok][col]) = make_uint2(bf16_pair(ev[0], ev[1]), bf16_pair(ev[2], ev[3]));
-      *reinterpret_cast<uint2*>(&xl[1][x_tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
-      *reinterpret_cast<uint2*>(&xl[2][x_tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
-    }
-    // this chunk's weights: int8 -> bf16 (exact), k = 16g + 8h + e
-    v4u a[MI][2];
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int v = wv[i][q];
-        a[i][q >> 1][2 * (q & 1)] = bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff));
-        a[i][q >> 1][2 * (q & 1) + 1] =
-            bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff));
-      }
-    __syncthreads();
-    if (k0 + BK < K) {
-#pragma unroll
-      for (int i = 0; i < MI; ++i) wv[i] = *reinterpret_cast<const v4i*>(wp[i] + k0 + BK);
-#pragma unroll
-      for (int c = 0; c < XF / 4; ++c) xv[c] = ld4(xsrc + k0 + BK, c);
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      v8bf b[3][MJ];
-#pragma unroll
-      for (int term = 0; term < 3; ++term)
-#pragma unroll
-        for (int j = 0; j < MJ; ++j)
-          b[term][j] = *reinterpret_cast<const v8bf*>(&xl[term][(BT / 2) * wc + 16 * j + r][16 * g + 8 * h]);
-#pragma unroll
-      for (int term = 0; term < 3; ++term)
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-          for (int j = 0; j < MJ; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a[i][h]), b[term][j],
-                                                                acc[i][j], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-
-  // lane holds rows n0 + (BN/2)wr + 16i + 4g + v (v = 0..3) of token t0 + (BT/2)wc + 16j + r
-  const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
-#pragma unroll
-  for (int j = 0; j < MJ; ++j) {
-    const int t = t0 + (BT / 2) * wc + 16 * j + r;
-    if (t >= T) continue;
-#pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const int n = n0 + (BN / 2) * wr + 16 * i + 4 * g;
-      float res[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int nv = min(n + v, N - 1);
-        res[v] = acc[i][j][v] * scales[nv];
-        if constexpr (BIAS) res[v] += bias[nv];
-      }
-      if (vec_out && n + 3 < N) {
-        *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
-      } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (n + v < N) y[(size_t)t * N + n + v] = res[v];
-      }
-    }
-  }
-}
-
 
 template <int BN, int BT, int BK>
 constexpr size_t gemm_lds_bytes() {
@@ -1000,7 +883,7 @@ struct KsplitRaw {
 // of token t0 + 32j + l%32; the KW waves' partial tiles are added in LDS in
 // wave order (deterministic), the blocks split over the waves; epilogue
 // y = sum * scale (+ bias).
-template <int MI, int MJ, int KW, bool BIAS>
+template <int MI, int MJ, int KW, int EPI>
 QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wave, int lane, float* y,
                                   const float* scales, const float* bias, int N, int T, int n0, int t0) {
   const int r = lane & 31, g = lane >> 5;
@@ -1028,10 +911,12 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
       for (int ww = 1; ww < KW; ++ww) sum += red[(size_t)ww * PER_WAVE + e];
       const int nv = min(n + v, N - 1);
       res[v] = sum * scales[nv];
-      if constexpr (BIAS) res[v] += bias[nv];
+      if constexpr (EPI == kGemmBias) res[v] += bias[nv];
     }
     if (t >= T) continue;
-    if (vec_out && n + 3 < N) {
+    if constexpr (EPI == kGemmSwiglu) {
+      swiglu_store(y, res, t, n, N);
+    } else if (vec_out && n + 3 < N) {
       *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
     } else {
 #pragma unroll
@@ -1041,7 +926,7 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
   }
 }
 
-template <int BN, int BT, int KW, bool BIAS>
+template <int BN, int BT, int KW, int EPI>
 __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set, TileMap map,
                                                                     const float* __restrict__ x, int T, int K) {
   constexpr int MI = BN / 32, MJ = BT / 32;
@@ -1160,43 +1045,32 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[0][0][0][e] = (acc[0][0][0][e] + acc[1][0][0][e]) + acc[2][0][0][e];
   }
-  ksplit_reduce_store<MI, MJ, KW, BIAS>(acc[0], gk_red, wave, lane, y, scales, bias, N, T, n0, t0);
+  ksplit_reduce_store<MI, MJ, KW, EPI>(acc[0], gk_red, wave, lane, y, scales, bias, N, T, n0, t0);
 }
 
-template <int BN, int BT, int KW, bool BIAS>
+template <int BN, int BT, int KW, int EPI>
 bool try_gemm_ksplit(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
   constexpr size_t lds = (size_t)KW * BN * BT * sizeof(float);
   if (K % 64 != 0) return false;
-  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_ksplit_kernel<BN, BT, KW, BIAS>>(lds)) return false;
+  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_ksplit_kernel<BN, BT, KW, EPI>>(lds)) return false;
   TileMap map;
   map.cols = cols;
   map.rows = (unsigned)((T + BT - 1) / BT);
   map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
-  w8a32_gemm_ksplit_kernel<BN, BT, KW, BIAS><<<map.cols * map.rows, 64 * KW, lds, st>>>(set, map, x, T, K);
+  w8a32_gemm_ksplit_kernel<BN, BT, KW, EPI><<<map.cols * map.rows, 64 * KW, lds, st>>>(set, map, x, T, K);
   return true;
 }
 
-template <int BN, int BT, bool BIAS>
-bool try_gemm_xlds(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
-  if (K % 64 != 0) return false;
-  TileMap map;
-  map.cols = cols;
-  map.rows = (unsigned)((T + BT - 1) / BT);
-  map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
-  w8a32_gemm_xlds_kernel<BN, BT, BIAS><<<map.cols * map.rows, 256, 0, st>>>(set, map, x, T, K);
-  return true;
-}
-
-template <int BN, int BT, int BK, int NPF, bool BIAS>
+template <int BN, int BT, int BK, int NPF, int EPI>
 bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
   constexpr size_t lds = gemm_lds_bytes<BN, BT, BK>();
   if (K % BK != 0) return false;
-  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, BIAS>>(lds)) return false;
+  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, EPI>>(lds)) return false;
   TileMap map;
   map.cols = cols;
   map.rows = (unsigned)((T + BT - 1) / BT);
   map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
-  w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, BIAS><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K);
+  w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K);
   return true;
 }
 
@@ -1205,7 +1079,7 @@ bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, h
 // MFMA); otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
 // 32 x 32 that fills the chip (measured at T = 512: o [1024, 2048] 20.0 ->
 // 16.7 us, down [1024, 3072] 27.4 -> 20.9 us against the LDS-staged 64 x 32).
-template <bool BIAS>
+template <int EPI>
 void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st) {
   auto cols = [&](int bn) {
     unsigned c = 0;
@@ -1219,35 +1093,19 @@ void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
   const long long rows64 = (T + 63) / 64, rows32 = (T + 31) / 32;
   unsigned c = cols(128);
   if (c * rows64 >= 256) {
-#ifdef QASR_XLDS
-    try_gemm_xlds<128, 64, BIAS>(set, c, x, T, K, st);
-#else
-    try_gemm<128, 64, 64, kGemmPrefetch, BIAS>(set, c, x, T, K, st);
-#endif
+    try_gemm<128, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
     return;
   }
   c = cols(64);
-#ifdef QASR_XLDS_SMALL
   if (c * rows64 >= 256) {
-    try_gemm_xlds<64, 64, BIAS>(set, c, x, T, K, st);
+    try_gemm_ksplit<64, 64, 4, EPI>(set, c, x, T, K, st);
     return;
   }
   if (c * rows32 >= 256) {
-    try_gemm_xlds<64, 32, BIAS>(set, c, x, T, K, st);
+    try_gemm_ksplit<64, 32, 4, EPI>(set, c, x, T, K, st);
     return;
   }
-  try_gemm_xlds<32, 32, BIAS>(set, cols(32), x, T, K, st);
-  return;
-#endif
-  if (c * rows64 >= 256) {
-    try_gemm_ksplit<64, 64, 4, BIAS>(set, c, x, T, K, st);
-    return;
-  }
-  if (c * rows32 >= 256) {
-    try_gemm_ksplit<64, 32, 4, BIAS>(set, c, x, T, K, st);
-    return;
-  }
-  try_gemm_ksplit<32, 32, 4, BIAS>(set, cols(32), x, T, K, st);
+  try_gemm_ksplit<32, 32, 4, EPI>(set, cols(32), x, T, K, st);
 }
 
 }  // namespace
@@ -1312,9 +1170,9 @@ static int launch_w8a32(float* y, const float* x, const int8_t* w, const float* 
     set.N[0] = o;
     set.n = 1;
     if (bias)
-      launch_w8a32_gemm<true>(set, x, s, k, st);
+      launch_w8a32_gemm<kGemmBias>(set, x, s, k, st);
     else
-      launch_w8a32_gemm<false>(set, x, s, k, st);
+      launch_w8a32_gemm<kGemmRows>(set, x, s, k, st);
   } else if (vec) {
     switch (in_dim / 1024) {
       case 1: w8a32_vec_kernel<1><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
@@ -1375,10 +1233,40 @@ extern "C" int qasr_gate_up_swiglu_int8_f32(float* out, const float* x, const in
                             nullptr);
   } else {
     const long long items = (long long)seq_len * (long long)intermediate;
-    gate_up_swiglu_w8a32_pairs_kernel<<<(unsigned)((items + 3) / 4), 256, 0, st>>>(
+    gate_up_swiglu_w8a32_pairs_kernel<false><<<(unsigned)((items + 3) / 4), 256, 0, st>>>(
         out, x, w_gate_up, scales_gate_up, (int)seq_len, (int)in_dim, (int)intermediate);
   }
   return launch_status("gate_up_swiglu_int8");
+}
+
+extern "C" int qasr_gate_up_swiglu_multiply_int8_f32(float* out, const float* x, const int8_t* w_gate_up,
+                                                     const float* scales_gate_up, size_t seq_len,
+                                                     size_t in_dim, size_t intermediate, void* stream) {
+  if (seq_len == 0 || intermediate == 0) return QASR_OK;
+  QASR_REQUIRE(out && x && w_gate_up && scales_gate_up, "gate_up_swiglu_multiply_int8: null pointer");
+  QASR_REQUIRE(in_dim > 0 && in_dim <= 0x7fffffffu && seq_len <= 0x7fffffffu &&
+                   intermediate <= 0x3fffffffu - 64,
+               "gate_up_swiglu_multiply_int8: size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(2 * intermediate, in_dim, &n) && mul_ok(seq_len, in_dim, &n) &&
+                   mul_ok(seq_len, 2 * intermediate, &n) && n < ((size_t)1 << 33),
+               "gate_up_swiglu_multiply_int8: size overflows");
+  hipStream_t st = as_stream(stream);
+  if (w8a32_gemm_shape(seq_len, in_dim, w_gate_up, x)) {
+    GemmSet set{};
+    set.y[0] = out;
+    set.w[0] = w_gate_up;
+    set.s[0] = scales_gate_up;
+    set.b[0] = nullptr;
+    set.N[0] = (int)(2 * intermediate);
+    set.n = 1;
+    launch_w8a32_gemm<kGemmSwiglu>(set, x, (int)seq_len, (int)in_dim, st);
+  } else {
+    const long long items = (long long)seq_len * (long long)intermediate;
+    gate_up_swiglu_w8a32_pairs_kernel<true><<<(unsigned)((items + 3) / 4), 256, 0, st>>>(
+        out, x, w_gate_up, scales_gate_up, (int)seq_len, (int)in_dim, (int)intermediate);
+  }
+  return launch_status("gate_up_swiglu_multiply_int8");
 }
 
 extern "C" int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,
@@ -1416,7 +1304,7 @@ extern "C" int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys
       set.N[m] = (int)out_dims[m];
     }
     set.n = (int)n_mats;
-    launch_w8a32_gemm<false>(set, x, (int)seq_len, (int)in_dim, as_stream(stream));
+    launch_w8a32_gemm<kGemmRows>(set, x, (int)seq_len, (int)in_dim, as_stream(stream));
     return launch_status("linear_nobias_int8_multi");
   }
   if (!one_launch) {

@@ -24,8 +24,8 @@ never leave HBM.
 previous layer's residual add), q/k/v (one matrix-core GEMM launch), q/k head
 RMSNorm + RoPE with the chunk's K/V rows written into the cache, causal
 attention over the cache (matrix cores), o, residual add + post-attention
-RMSNorm, gate/up, the prefill SwiGLU (fast_exp form), down: 9 launches per
-layer, then the last residual add.
+RMSNorm, gate/up with the prefill SwiGLU (fast_exp form) in its epilogue,
+down: 8 launches per layer, then the last residual add.
 
 Weights come from ``qint8.load_decoder_int8`` (or any dict of the same
 layout); ``DecoderInt8.decode`` runs one token and can be captured in a HIP
@@ -88,7 +88,6 @@ class DecoderInt8:
         self.pv = torch.empty(T * kv_dim, **f32)
         self.pattn = torch.empty(T * q_dim, **f32)
         self.pproj = torch.empty(T * H, **f32)
-        self.pgu = torch.empty(T * 2 * I, **f32)
         self.pgate = torch.empty(T * I, **f32)
         self.pffn = torch.empty(T * H, **f32)
         self._pcap = T
@@ -124,9 +123,7 @@ class DecoderInt8:
             wo = lw["wo"]
             K.linear_nobias_int8(self.pproj, self.pattn, wo.data, wo.scales, T, q_dim, H)
             K.add_rms_norm(x, self.pproj, lw["post_attn_norm"], self.pxn, T, H, eps)
-            gu = lw["gate_up"]
-            K.linear_nobias_int8(self.pgu, self.pxn, gu.data, gu.scales, T, H, 2 * I)
-            K.swiglu_multiply(self.pgate, self.pgu, T, I)
+            K.gate_up_swiglu_multiply_int8(self.pgate, self.pxn, lw["gate_up"], T, H, I)
             dn = lw["down"]
             K.linear_nobias_int8(self.pffn, self.pgate, dn.data, dn.scales, T, I, H)
         K.add_inplace(x, self.pffn, T * H)

@@ -594,6 +594,17 @@ def add_rms_norm_gate_up_swiglu_int8(out, h_out, x, delta, norm_w, w: QuantWeigh
               _ptr(norm_w), _ptr(w.data), _ptr(w.scales), in_dim, intermediate, eps, _stream())
 
 
+def gate_up_swiglu_multiply_int8(out, x, w: QuantWeight, seq_len: int, in_dim: int, intermediate: int) -> None:
+    """The prefill's W8A32 gate/up projection on the interleaved weight + swiglu_multiply
+    (decoder.rs:831-834; the fast_exp SwiGLU), one launch; gate/up values are not stored."""
+    _need(out, F32, seq_len * intermediate, "out")
+    _need(x, F32, seq_len * in_dim, "x")
+    _need(w.data, I8, 2 * intermediate * in_dim, "w")
+    _need(w.scales, F32, 2 * intermediate, "scales")
+    _lib.call("qasr_gate_up_swiglu_multiply_int8_f32", _ptr(out), _ptr(x), _ptr(w.data), _ptr(w.scales),
+              seq_len, in_dim, intermediate, _stream())
+
+
 def linear_int8(y, x, w_int8, scales, bias, seq_len: int, in_dim: int, out_dim: int) -> None:
     """W8A32 linear with optional bias (kernels/mod.rs:664-673)."""
     _need(y, F32, seq_len * out_dim, "y")

@@ -145,6 +145,35 @@ def test_fused_norm_decode_equals_unfused(tmp_path, dev):
             np.testing.assert_array_equal(decs[0].kv.v_layer(l).cpu().numpy(), decs[1].kv.v_layer(l).cpu().numpy())
 
 
+@pytest.mark.parametrize("seq,H,I", [(512, 1024, 3072), (37, 1024, 3072), (100, 2048, 1000), (8, 1024, 100),
+                                     (3, 1024, 64), (1, 1000, 77)])
+def test_gate_up_swiglu_multiply_int8(dev, seq, H, I):
+    """The prefill gate/up projection with the SwiGLU in its epilogue: from 8
+    tokens (matrix-core GEMM; the 128x64 tile, a split-K tile, a row tail of
+    the fast_exp columns) equal bit for bit to linear_nobias_int8 followed by
+    swiglu_multiply; at every size within the fp32 tolerance of the oracle's
+    linear + swiglu_multiply (kernels/mod.rs:965-985)."""
+    from qwenasr_amd import kernels as K
+
+    r = np.random.default_rng([36, seq, H, I])
+    wf = (0.02 * r.standard_normal((2 * I, H))).astype(np.float32)
+    q, s = oracle.quantize_f32_to_int8(wf, 2 * I, H)
+    x = r.standard_normal(seq * H).astype(np.float32)
+    w = K.QuantWeight(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), 2 * I, H)
+    xt = torch.from_numpy(x).to(dev)
+    gu = torch.empty(seq * 2 * I, device=dev)
+    ref = torch.empty(seq * I, device=dev)
+    K.linear_nobias_int8(gu, xt, w.data, w.scales, seq, H, 2 * I)
+    K.swiglu_multiply(ref, gu, seq, I)
+    out = torch.full((seq * I,), 9.0, device=dev)
+    K.gate_up_swiglu_multiply_int8(out, xt, w, seq, H, I)
+    torch.cuda.synchronize()
+    if seq >= 8 and H % 64 == 0:
+        np.testing.assert_array_equal(out.cpu().numpy(), ref.cpu().numpy())
+    gu_ref = oracle.linear_nobias_int8(x, q, s, seq, H, 2 * I, n_threads=8)
+    np.testing.assert_allclose(out.cpu().numpy(), oracle.swiglu_multiply(gu_ref, seq, I), rtol=1e-5, atol=1e-5)
+
+
 def _load(tmp_path, w, L, dev):
     from qwenasr_amd import qint8
 
