@@ -301,49 +301,6 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
   const int i = blockIdx.x, kh = blockIdx.y;
   const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
   float4 qv[G][C4];
-  if constexpr (PRE) {
-    // One token (i == 0). Groups of HD/8 lanes, in the layout of the head
-    // kernel: groups 0..G-1 normalise and rotate this kv head's q heads into
-    // LDS; in the split that holds key pos (the last), group G writes the
-    // normalised, rotated k row into the cache and group G+1 the v row. The
-    // barrier then makes the row visible to the workgroup's key loop (no
-    // other workgroup reads it).
-    constexpr int L = HD / 8, HALF = HD / 2;
-    static_assert((G + 2) * L <= 256, "prologue groups fit the workgroup");
-    __shared__ __align__(16) float qs[G][HD];
-    const int grp = threadIdx.x / L, sub = threadIdx.x % L;
-    const bool last = blockIdx.z == gridDim.z - 1;
-    if (grp < G || (last && grp == G)) {
-      const bool is_q = grp < G;
-      const float* src = is_q ? q + (size_t)(kh * G + grp) * HD : pre.k + (size_t)kh * HD;
-      const float* w = is_q ? pre.q_norm_w : pre.k_norm_w;
-      const float4 w1 = ld4(w, sub), w2 = ld4(w + HALF, sub);
-      const float4 c1 = ld4(pre.cos_row, sub), c2 = ld4(pre.cos_row + HALF, sub);
-      const float4 s1 = ld4(pre.sin_row, sub), s2 = ld4(pre.sin_row + HALF, sub);
-      float4 x1 = ld4(src, sub), x2 = ld4(src + HALF, sub);
-      head_norm_rope<HD, true, true>(x1, x2, w1, w2, c1, c2, s1, s2, true, pre.eps);
-      float* dst = is_q ? &qs[grp][0] : pre.k_row + (size_t)kh * HD;
-      st4(dst, sub, x1);
-      st4(dst + HALF, sub, x2);
-    } else if (last && grp == G + 1) {
-      const float* src = pre.v + (size_t)kh * HD;
-      float* dst = pre.v_row + (size_t)kh * HD;
-      st4(dst, sub, ld4(src, sub));
-      st4(dst + HALF, sub, ld4(src + HALF, sub));
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int c = 0; c < C4; ++c) qv[g][c] = *reinterpret_cast<const float4*>(&qs[g][quarter * DQ + 4 * c]);
-  } else {
-    const float* qr = q + (size_t)i * q_stride + (size_t)kh * G * HD + quarter * DQ;
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int c = 0; c < C4; ++c) qv[g][c] = ld4(qr + g * HD, c);
-  }
-
   const int k_lim = min(q_offset + i + 1, seq_k);
   const int k_begin = min(k_lim, (int)blockIdx.z * keys_per_split);
   const int k_end = min(k_lim, k_begin + keys_per_split);
@@ -355,15 +312,16 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
 #pragma unroll
     for (int d = 0; d < DPL; ++d) o[g][d] = 0.0f;
   }
-  for (int t0 = k_begin + 16 * wave; t0 < k_end; t0 += 64) {
-    const int nkeys = min(16, k_end - t0);  // this wave's keys in the tile (>= 1)
-    const int j = min(kq, nkeys - 1);       // past them: repeat the last key, masked below
+
+  // A tile: this wave's keys t0 .. t0 + 15 (past k_end: repeat the last key,
+  // masked in process_tile).
+  auto load_tile = [&](int t0, float4 (&kk)[C4], float (&vv)[16][DPL]) {
+    const int nkeys = min(16, k_end - t0);
+    const int j = min(kq, nkeys - 1);
     const float* kr = k + (size_t)(t0 + j) * kv_stride + (size_t)kh * HD + quarter * DQ;
-    float4 kk[C4];
 #pragma unroll
     for (int c = 0; c < C4; ++c) kk[c] = ld4(kr, c);
     const float* vr = v + (size_t)t0 * kv_stride + (size_t)kh * HD + lane * DPL;
-    float vv[16][DPL];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const size_t jj = (size_t)min(u, nkeys - 1);
@@ -375,9 +333,11 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
         vv[u][0] = vr[jj * kv_stride];
       }
     }
-    // every load issued before the first use (the scheduler would otherwise
-    // sink the v loads below the QK arithmetic: two round trips)
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  // with use_vlast, the tile's last key takes its v row from vlast
+  auto process_tile = [&](int t0, const float4 (&kk)[C4], const float (&vv)[16][DPL], bool use_vlast,
+                          const float (&vlast)[DPL]) {
+    const int nkeys = min(16, k_end - t0);
     const bool key_ok = kq < nkeys;
     float p[G];
 #pragma unroll
@@ -407,10 +367,113 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
         for (int g = 0; g < G; ++g) {
           const float pj = bcast_lane(p[g], 4 * u);
 #pragma unroll
-          for (int d = 0; d < DPL; ++d) o[g][d] = __builtin_fmaf(pj, vv[u][d], o[g][d]);
+          for (int d = 0; d < DPL; ++d) {
+            const float vx = (use_vlast && u == nkeys - 1) ? vlast[d] : vv[u][d];
+            o[g][d] = __builtin_fmaf(pj, vx, o[g][d]);
+          }
         }
       }
     }
+  };
+
+  int t0 = k_begin + 16 * wave;
+  [[maybe_unused]] const int pos = k_lim - 1;  // PRE: the new key, the last of the last split
+  [[maybe_unused]] const bool last = blockIdx.z == gridDim.z - 1;
+  // PRE: the tile holding key pos takes that row from LDS (kpos, vpos). Key
+  // pos is the last of the last split, so it is the last key of its tile:
+  // the lanes whose key it is get kpos, and the PV sum takes vpos (vlast)
+  // for the tile's last key. Returns whether the tile holds key pos.
+  auto patch = [&](int t, float4 (&kk)[C4], float (&vlast)[DPL], const float* kpos, const float* vpos) {
+    if (!(last && pos >= t && pos < t + 16)) return false;  // uniform
+    const int nkeys = min(16, k_end - t);
+    if (min(kq, nkeys - 1) == nkeys - 1) {
+#pragma unroll
+      for (int c = 0; c < C4; ++c) kk[c] = *reinterpret_cast<const float4*>(&kpos[quarter * DQ + 4 * c]);
+    }
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) vlast[d] = vpos[lane * DPL + d];
+    return true;
+  };
+  [[maybe_unused]] const float* kpos_p = nullptr;
+  [[maybe_unused]] const float* vpos_p = nullptr;
+  if constexpr (PRE) {
+    // One token (i == 0). The wave's first tile is loaded before the
+    // prologue (it does not depend on it). Groups of HD/8 lanes, in the
+    // layout of the head kernel: groups 0..G-1 normalise and rotate this kv
+    // head's q heads into LDS; in the split that holds key pos (the last),
+    // group G writes the normalised, rotated k row into the cache and group
+    // G+1 the v row, both also into LDS. The tile holding key pos takes that
+    // row from LDS (its loads may predate the cache writes), so nothing in
+    // this launch reads the new cache rows (no other workgroup reads them
+    // either) and the barrier waits for LDS only, not for the global loads
+    // and stores in flight.
+    constexpr int L = HD / 8, HALF = HD / 2;
+    static_assert((G + 2) * L <= 256, "prologue groups fit the workgroup");
+    __shared__ __align__(16) float qs[G][HD];
+    __shared__ __align__(16) float kpos[HD], vpos[HD];
+    float4 kk0[C4];
+    float vv0[16][DPL];
+    const bool first = t0 < k_end;  // uniform per wave
+    if (first) load_tile(t0, kk0, vv0);
+    __builtin_amdgcn_sched_barrier(0);
+    const int grp = threadIdx.x / L, sub = threadIdx.x % L;
+    kpos_p = kpos;
+    vpos_p = vpos;
+    if (grp < G || (last && grp == G)) {
+      const bool is_q = grp < G;
+      const float* src = is_q ? q + (size_t)(kh * G + grp) * HD : pre.k + (size_t)kh * HD;
+      const float* w = is_q ? pre.q_norm_w : pre.k_norm_w;
+      const float4 w1 = ld4(w, sub), w2 = ld4(w + HALF, sub);
+      const float4 c1 = ld4(pre.cos_row, sub), c2 = ld4(pre.cos_row + HALF, sub);
+      const float4 s1 = ld4(pre.sin_row, sub), s2 = ld4(pre.sin_row + HALF, sub);
+      float4 x1 = ld4(src, sub), x2 = ld4(src + HALF, sub);
+      head_norm_rope<HD, true, true>(x1, x2, w1, w2, c1, c2, s1, s2, true, pre.eps);
+      float* dst = is_q ? &qs[grp][0] : kpos;
+      st4(dst, sub, x1);
+      st4(dst + HALF, sub, x2);
+      if (!is_q) {
+        float* kr = pre.k_row + (size_t)kh * HD;
+        st4(kr, sub, x1);
+        st4(kr + HALF, sub, x2);
+      }
+    } else if (last && grp == G + 1) {
+      const float* src = pre.v + (size_t)kh * HD;
+      float* dst = pre.v_row + (size_t)kh * HD;
+      const float4 v1 = ld4(src, sub), v2 = ld4(src + HALF, sub);
+      st4(dst, sub, v1);
+      st4(dst + HALF, sub, v2);
+      st4(vpos, sub, v1);
+      st4(vpos + HALF, sub, v2);
+    }
+    lds_barrier();
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int c = 0; c < C4; ++c) qv[g][c] = *reinterpret_cast<const float4*>(&qs[g][quarter * DQ + 4 * c]);
+    if (first) {
+      float vlast[DPL];
+      const bool hit = patch(t0, kk0, vlast, kpos, vpos);
+      process_tile(t0, kk0, vv0, hit, vlast);
+      t0 += 64;
+    }
+  } else {
+    const float* qr = q + (size_t)i * q_stride + (size_t)kh * G * HD + quarter * DQ;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int c = 0; c < C4; ++c) qv[g][c] = ld4(qr + g * HD, c);
+  }
+  for (; t0 < k_end; t0 += 64) {
+    float4 kk[C4];
+    float vv[16][DPL];
+    load_tile(t0, kk, vv);
+    // every load issued before the first use (the scheduler would otherwise
+    // sink the v loads below the QK arithmetic: two round trips)
+    __builtin_amdgcn_sched_barrier(0);
+    float vlast[DPL];
+    bool hit = false;
+    if constexpr (PRE) hit = patch(t0, kk, vlast, kpos_p, vpos_p);
+    process_tile(t0, kk, vv, hit, vlast);
   }
   // merge the 4 waves
   if (lane == 0) {

@@ -149,6 +149,19 @@ QASR_DEV float swiglu_ref(float g, float u, bool fast) {
 
 QASR_DEV float qnan() { return __int_as_float(0x7fc00000); }
 
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left at their maxima (gfx9
+// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+constexpr int kWaitLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
+
+// Workgroup barrier without a global-memory fence: the workgroup's LDS writes
+// are complete (lgkmcnt(0)) and visible after it; outstanding global loads and
+// stores keep flying (__syncthreads would wait for them: gfx9 counts both in
+// vmcnt).
+QASR_DEV void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // Per-head RMSNorm (NORM) and NeoX RoPE (ROPE) of one head held by a group of
 // HD/8 consecutive lanes: lane `sub` holds dims 4sub..4sub+3 in x1 and
 // HD/2 + 4sub..4sub+3 in x2, with the gains (w1, w2) and the position's table

@@ -409,16 +409,6 @@ constexpr int kPkChunk = 512;    // bytes of K per staged X chunk
 constexpr int kPkPrefetch = 3;   // k-steps of W in flight per wave
 constexpr size_t kPkLds = 131072;
 
-// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left at their maxima (gfx9
-// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
-constexpr int kWaitLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
-
-// Workgroup barrier without a memory fence: the caller has made its own LDS
-// writes complete (lgkmcnt(0)); outstanding global loads keep flying.
-QASR_DEV void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-  asm volatile("s_barrier" ::: "memory");
-}
 
 // Wave `wave`'s share of X chunk c: 4 rows-pairs t, each lane one 16-byte slot.
 // Rows past the batch re-read row batch - 1 (valid memory); their results are
