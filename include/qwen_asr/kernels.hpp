@@ -435,6 +435,80 @@ inline void gate_up_swiglu_w8a8(F out, DevSlice<const int8_t> w_gate_up, CF scal
                 "gate_up_swiglu_w8a8");
 }
 
+// The decode loop's gate/up projection + SwiGLU (decoder.rs:912-921): out = silu(g) * u on the
+// row-interleaved fused weight, gate/up values never stored.
+inline void gate_up_swiglu_int8(F out, CF x, DevSlice<const int8_t> w_gate_up, CF scales,
+                                size_t seq_len, size_t in_dim, size_t intermediate) {
+  detail::need(out, seq_len * intermediate, "out");
+  detail::need(x, seq_len * in_dim, "x");
+  detail::need(w_gate_up, 2 * intermediate * in_dim, "w_gate_up");
+  detail::need(scales, 2 * intermediate, "scales");
+  detail::check(qasr_gate_up_swiglu_int8_f32(out.ptr, x.ptr, w_gate_up.ptr, scales.ptr, seq_len,
+                                             in_dim, intermediate, detail::st()),
+                "gate_up_swiglu_int8");
+}
+
+// The prefill's gate/up projection + swiglu_multiply (decoder.rs:831-834, the fast_exp SwiGLU).
+inline void gate_up_swiglu_multiply_int8(F out, CF x, DevSlice<const int8_t> w_gate_up, CF scales,
+                                         size_t seq_len, size_t in_dim, size_t intermediate) {
+  detail::need(out, seq_len * intermediate, "out");
+  detail::need(x, seq_len * in_dim, "x");
+  detail::need(w_gate_up, 2 * intermediate * in_dim, "w_gate_up");
+  detail::need(scales, 2 * intermediate, "scales");
+  detail::check(qasr_gate_up_swiglu_multiply_int8_f32(out.ptr, x.ptr, w_gate_up.ptr, scales.ptr,
+                                                      seq_len, in_dim, intermediate, detail::st()),
+                "gate_up_swiglu_multiply_int8");
+}
+
+// Decode folds (one token): h = x + delta (delta empty: h = x), the RMSNorm of h and the
+// projections of the normalised row in one launch, equal bit for bit to add_rms_norm followed by
+// the projection; h goes to h_out (empty: not written), which must not overlap x or delta.
+inline void add_rms_norm_linear_nobias_int8_multi(const std::vector<F>& ys,
+                                                  const std::vector<DevSlice<const int8_t>>& ws,
+                                                  const std::vector<CF>& scales,
+                                                  const std::vector<size_t>& out_dims, F h_out, CF x,
+                                                  CF delta, CF norm_w, size_t in_dim, float eps) {
+  const size_t n = out_dims.size();
+  if (ys.size() != n || ws.size() != n || scales.size() != n)
+    throw Panic("add_rms_norm_linear_nobias_int8_multi: one output, weight and scale slice per matrix");
+  std::vector<float*> yp(n);
+  std::vector<const int8_t*> wp(n);
+  std::vector<const float*> sp(n);
+  for (size_t m = 0; m < n; ++m) {
+    detail::need(ys[m], out_dims[m], "y");
+    detail::need(ws[m], out_dims[m] * in_dim, "w_int8");
+    detail::need(scales[m], out_dims[m], "scales");
+    yp[m] = ys[m].ptr;
+    wp[m] = ws[m].ptr;
+    sp[m] = scales[m].ptr;
+  }
+  detail::need(x, in_dim, "x");
+  detail::need(norm_w, in_dim, "norm_w");
+  if (delta.ptr) detail::need(delta, in_dim, "delta");
+  if (h_out.ptr) detail::need(h_out, in_dim, "h_out");
+  detail::check(qasr_add_rms_norm_linear_nobias_int8_multi_f32(n, yp.data(), wp.data(), sp.data(),
+                                                               out_dims.data(), h_out.ptr, x.ptr,
+                                                               delta.ptr, norm_w.ptr, in_dim, eps,
+                                                               detail::st()),
+                "add_rms_norm_linear_nobias_int8_multi");
+}
+
+inline void add_rms_norm_gate_up_swiglu_int8(F out, F h_out, CF x, CF delta, CF norm_w,
+                                             DevSlice<const int8_t> w_gate_up, CF scales,
+                                             size_t in_dim, size_t intermediate, float eps) {
+  detail::need(out, intermediate, "out");
+  detail::need(x, in_dim, "x");
+  detail::need(norm_w, in_dim, "norm_w");
+  if (delta.ptr) detail::need(delta, in_dim, "delta");
+  if (h_out.ptr) detail::need(h_out, in_dim, "h_out");
+  detail::need(w_gate_up, 2 * intermediate * in_dim, "w_gate_up");
+  detail::need(scales, 2 * intermediate, "scales");
+  detail::check(qasr_add_rms_norm_gate_up_swiglu_int8_f32(out.ptr, h_out.ptr, x.ptr, delta.ptr,
+                                                          norm_w.ptr, w_gate_up.ptr, scales.ptr,
+                                                          in_dim, intermediate, eps, detail::st()),
+                "add_rms_norm_gate_up_swiglu_int8");
+}
+
 // ---- attention (kernels/mod.rs:1124-1207) ---------------------------------------------
 inline size_t attention_workspace_floats(size_t seq_q, size_t n_heads, size_t head_dim) {
   return qasr_causal_attention_workspace_floats(seq_q, n_heads, head_dim);
@@ -466,6 +540,29 @@ inline void causal_attention(F out, CF q, CF k, CF v, size_t seq_q, size_t seq_k
                                                 n_kv_heads, head_dim, scale, q_offset,
                                                 workspace.ptr, workspace.len, detail::st()),
                 "causal_attention");
+}
+
+// One decode token: q/k head RMSNorm + RoPE at pos, the K/V rows into the layer's cache block
+// and causal attention over rows 0..pos (decoder.rs:888-903), equal bit for bit to
+// head_rms_norm_rope_kv + causal_attention with a workspace; q is scratch.
+inline void decode_attention(F out, F q, CF k, CF v, CF q_norm_w, CF k_norm_w, const RopeCache& rope,
+                             size_t pos, size_t n_heads, size_t n_kv_heads, size_t head_dim, float eps,
+                             float scale, F k_cache, F v_cache, size_t cache_rows, F workspace) {
+  const size_t kv_dim = n_kv_heads * head_dim;
+  detail::need(out, n_heads * head_dim, "out");
+  detail::need(q, n_heads * head_dim, "q");
+  detail::need(k, kv_dim, "k");
+  detail::need(v, kv_dim, "v");
+  detail::need(q_norm_w, head_dim, "q_norm_w");
+  detail::need(k_norm_w, head_dim, "k_norm_w");
+  detail::need(k_cache, cache_rows * kv_dim, "k_cache");
+  detail::need(v_cache, cache_rows * kv_dim, "v_cache");
+  if (rope.head_dim() != head_dim) throw Panic("decode_attention: RopeCache head_dim mismatch");
+  detail::check(qasr_decode_attention_f32(out.ptr, q.ptr, k.ptr, v.ptr, q_norm_w.ptr, k_norm_w.ptr,
+                                          rope.cos().ptr, rope.sin().ptr, rope.cap(), pos, n_heads,
+                                          n_kv_heads, head_dim, eps, scale, k_cache.ptr, v_cache.ptr,
+                                          cache_rows, workspace.ptr, workspace.len, detail::st()),
+                "decode_attention");
 }
 
 // ---- lm_head (decoder.rs:929-963) ---------------------------------------------------

@@ -221,6 +221,50 @@ static void test_linear_int8_exact() {
   }
 }
 
+// The decode-step folds through the C++ mirror equal the unfused calls bit for bit:
+// add + RMSNorm + q/k/v, add + RMSNorm + gate/up + SwiGLU, the prefill gate/up + SwiGLU.
+static void test_decode_folds() {
+  const size_t H = 2048, I = 512, qo = 2048, kvo = 1024, T = 24;
+  auto pseudo = [](size_t i, int span) { return (int)((i * 2654435761u) >> 9) % span - span / 2; };
+  std::vector<float> x(H), d(H), g(H), xt(T * H);
+  for (size_t k = 0; k < H; ++k) {
+    x[k] = pseudo(k, 2001) / 1000.0f;
+    d[k] = pseudo(k + 7, 2001) / 1000.0f;
+    g[k] = 1.0f + pseudo(k + 13, 201) / 1000.0f;
+  }
+  for (size_t k = 0; k < T * H; ++k) xt[k] = pseudo(k + 29, 2001) / 1000.0f;
+  auto mk_w = [&](size_t rows, size_t salt) {
+    std::vector<int8_t> w(rows * H);
+    for (size_t i = 0; i < w.size(); ++i) w[i] = (int8_t)pseudo(i + salt, 255);
+    return w;
+  };
+  auto mk_s = [&](size_t rows) { return std::vector<float>(rows, 1.0f / 4096.0f); };
+  auto wq = upload(mk_w(qo, 1)), wk = upload(mk_w(kvo, 2)), wv = upload(mk_w(kvo, 3)), wgu = upload(mk_w(2 * I, 4));
+  auto sq = upload(mk_s(qo)), sk = upload(mk_s(kvo)), sv = upload(mk_s(kvo)), sgu = upload(mk_s(2 * I));
+  auto dx = upload(x), dd = upload(d), dg = upload(g), dxt = upload(xt);
+  const float eps = 1e-6f;
+  // unfused: add_rms_norm on a copy, then the projections
+  auto xa = upload(x);
+  K::DeviceBuffer<float> xn(H), q0(qo), k0(kvo), v0(kvo), q1(qo), k1(kvo), v1(kvo), h(H);
+  K::add_rms_norm(xa, dd, dg, xn, 1, H, eps);
+  K::linear_nobias_int8_multi({q0, k0, v0}, {wq, wk, wv}, {sq, sk, sv}, {qo, kvo, kvo}, xn, 1, H);
+  K::add_rms_norm_linear_nobias_int8_multi({q1, k1, v1}, {wq, wk, wv}, {sq, sk, sv}, {qo, kvo, kvo}, h, dx, dd,
+                                           dg, H, eps);
+  EXPECT(download(q0) == download(q1) && download(k0) == download(k1) && download(v0) == download(v1),
+         "q/k/v differ");
+  EXPECT(download(h) == download(xa), "residual differs");
+  K::DeviceBuffer<float> o0(I), o1(I);
+  K::gate_up_swiglu_int8(o0, xn, wgu, sgu, 1, H, I);
+  K::add_rms_norm_gate_up_swiglu_int8(o1, h, dx, dd, dg, wgu, sgu, H, I, eps);
+  EXPECT(download(o0) == download(o1), "gate/up SwiGLU differs");
+  // prefill: GEMM + swiglu_multiply vs the fused epilogue (24 tokens: the matrix-core path)
+  K::DeviceBuffer<float> gu(T * 2 * I), p0(T * I), p1(T * I);
+  K::linear_nobias_int8(gu, dxt, wgu, sgu, T, H, 2 * I);
+  K::swiglu_multiply(p0, gu, T, I);
+  K::gate_up_swiglu_multiply_int8(p1, dxt, wgu, sgu, T, H, I);
+  EXPECT(download(p0) == download(p1), "prefill gate/up SwiGLU differs");
+}
+
 // Attention over one key returns that key's value row exactly (softmax weight
 // exp(0)/1); two identical keys average their values; the key-split form
 // agrees with the single-pass form.
@@ -381,6 +425,7 @@ int main() {
   run("test_rope_cache", test_rope_cache);
   run("test_kv_store", test_kv_store);
   run("test_linear_int8_exact", test_linear_int8_exact);
+  run("test_decode_folds", test_decode_folds);
   run("test_causal_attention", test_causal_attention);
   run("test_lm_head_argmax", test_lm_head_argmax);
   run("test_qint8_file", test_qint8_file);
