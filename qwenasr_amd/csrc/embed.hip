@@ -18,11 +18,11 @@ __global__ __launch_bounds__(256) void gather_vec_kernel(float* out, const void*
   float* dst = out + (size_t)blockIdx.x * dim;
   const bool bad = id < 0 || id >= vocab;
   if constexpr (MODE == 0) {
-    const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(table) + (bad ? 0 : id) * dim);
+    const float* src = static_cast<const float*>(table) + (bad ? 0 : id) * dim;
     for (int c = threadIdx.x; c < dim / 4; c += 256) {
-      float4 v = src[c];
+      float4 v = ld4_nt(src, c);
       if (bad) v = make_float4(qnan(), qnan(), qnan(), qnan());
-      reinterpret_cast<float4*>(dst)[c] = v;
+      st4_nt(dst, c, v);
     }
   } else if constexpr (MODE == 1) {
     const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(table) + (bad ? 0 : id) * dim);
@@ -34,8 +34,8 @@ __global__ __launch_bounds__(256) void gather_vec_kernel(float* out, const void*
       hi.x = __uint_as_float(r.z << 16); hi.y = __uint_as_float(r.z & 0xffff0000u);
       hi.z = __uint_as_float(r.w << 16); hi.w = __uint_as_float(r.w & 0xffff0000u);
       if (bad) { lo = make_float4(qnan(), qnan(), qnan(), qnan()); hi = lo; }
-      reinterpret_cast<float4*>(dst)[2 * c] = lo;
-      reinterpret_cast<float4*>(dst)[2 * c + 1] = hi;
+      st4_nt(dst, 2 * c, lo);
+      st4_nt(dst, 2 * c + 1, hi);
     }
   } else {
     const int4* src = reinterpret_cast<const int4*>(static_cast<const int8_t*>(table) + (bad ? 0 : id) * dim);
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void gather_vec_kernel(float* out, const void*
         o.y = (float)(int8_t)((w[k] >> 8) & 0xff) * s;
         o.z = (float)(int8_t)((w[k] >> 16) & 0xff) * s;
         o.w = (float)(int8_t)((w[k] >> 24) & 0xff) * s;
-        reinterpret_cast<float4*>(dst)[4 * c + k] = o;
+        st4_nt(dst, 4 * c + k, o);
       }
     }
   }

@@ -4,6 +4,10 @@
 // thread keeps NV float4 of the row in registers, so a row crosses HBM exactly
 // once in each direction (read x [+ delta], write [x and] out). The sum of
 // squares (or mean/variance) is reduced with wave shuffles and one LDS step.
+// Row data moves with nontemporal 16-byte accesses (the LayerNorm at
+// [3000,896] measured 7.1 us with cached accesses, 6.0 us with these), except
+// in the add+RMSNorm+quantize kernel, where they measured slower ([256,2048]:
+// 4.1 -> 4.6 us); gains and biases, read by every row, stay cached.
 #include "common.hpp"
 
 namespace qasr {
@@ -30,11 +34,11 @@ __global__ __launch_bounds__(BLOCK) void rms_norm_vec_kernel(
     if (c < h4) {
       // the gain is independent of the row statistics: load it with the row
       wv[i] = ld4(w, c);
-      float4 a = ld4(x, base + c);
+      float4 a = QUANT ? ld4(x, base + c) : ld4_nt(x, base + c);
       if constexpr (ADD) {
-        const float4 d = ld4(delta, base + c);
+        const float4 d = QUANT ? ld4(delta, base + c) : ld4_nt(delta, base + c);
         a.x += d.x; a.y += d.y; a.z += d.z; a.w += d.w;
-        st4(x, base + c, a);
+        if constexpr (QUANT) st4(x, base + c, a); else st4_nt(x, base + c, a);
       }
       v[i] = a;
       ss += a.x * a.x;
@@ -55,7 +59,9 @@ __global__ __launch_bounds__(BLOCK) void rms_norm_vec_kernel(
       o.y = (v[i].y * rinv) * wv[i].y;
       o.z = (v[i].z * rinv) * wv[i].z;
       o.w = (v[i].w * rinv) * wv[i].w;
-      if (out) st4(out, base + c, o);
+      if (out) {
+        if constexpr (QUANT) st4(out, base + c, o); else st4_nt(out, base + c, o);
+      }
       v[i] = o;
       if constexpr (QUANT) {
         // absmax as quantize.rs:646-652 (`if abs > absmax`: NaN never wins)
@@ -150,7 +156,7 @@ __global__ __launch_bounds__(BLOCK) void layer_norm_vec_kernel(
     if (c < h4) {
       wv[i] = ld4(w, c);  // gain and bias: independent of the statistics
       bv[i] = ld4(b, c);
-      v[i] = ld4(x, base + c);
+      v[i] = ld4_nt(x, base + c);
       s += v[i].x;
       s += v[i].y;
       s += v[i].z;
@@ -183,7 +189,7 @@ __global__ __launch_bounds__(BLOCK) void layer_norm_vec_kernel(
       o.y = ln_out(v[i].y, mean, inv, wv[i].y, bv[i].y, f);
       o.z = ln_out(v[i].z, mean, inv, wv[i].z, bv[i].z, f);
       o.w = ln_out(v[i].w, mean, inv, wv[i].w, bv[i].w, f);
-      st4(out, base + c, o);
+      st4_nt(out, base + c, o);
     }
   }
 }
@@ -208,7 +214,7 @@ __global__ __launch_bounds__(256) void layer_norm_wave_kernel(
     if (c < h4) {
       wv[i] = ld4(w, c);  // gain and bias: independent of the statistics
       bv[i] = ld4(b, c);
-      v[i] = ld4(x, base + c);
+      v[i] = ld4_nt(x, base + c);
       s += v[i].x;
       s += v[i].y;
       s += v[i].z;
@@ -241,7 +247,7 @@ __global__ __launch_bounds__(256) void layer_norm_wave_kernel(
       o.y = ln_out(v[i].y, mean, inv, wv[i].y, bv[i].y, f);
       o.z = ln_out(v[i].z, mean, inv, wv[i].z, bv[i].z, f);
       o.w = ln_out(v[i].w, mean, inv, wv[i].w, bv[i].w, f);
-      st4(out, base + c, o);
+      st4_nt(out, base + c, o);
     }
   }
 }

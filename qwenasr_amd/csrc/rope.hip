@@ -118,8 +118,8 @@ __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
     const int kind = head_kv_of(a, gh, HD, &src, &base, &w, &row, &pos, &pos_ok);
     if (kind == 2) {  // v: a plain copy into the cache (decoder.rs:550, 895)
       if (pos_ok) {
-        st4(base, sub, ld4(src, sub));
-        st4(base + HALF, sub, ld4(src + HALF, sub));
+        st4_nt(base, sub, ld4_nt(src, sub));
+        st4_nt(base + HALF, sub, ld4_nt(src + HALF, sub));
       }
       return;  // the head's lane group leaves together
     }
@@ -147,12 +147,12 @@ __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
     c1 = ld4(cr, sub); c2 = ld4(cr + HALF, sub);
     s1 = ld4(sr, sub); s2 = ld4(sr + HALF, sub);
   }
-  float4 x1 = ld4(src, sub);
-  float4 x2 = ld4(src + HALF, sub);
+  float4 x1 = ld4_nt(src, sub);
+  float4 x2 = ld4_nt(src + HALF, sub);
   head_norm_rope<HD, NORM, ROPE>(x1, x2, w1, w2, c1, c2, s1, s2, pos_ok, a.eps);
   if (KV && !pos_ok && base != src) return;  // k head outside the cache: nothing written
-  st4(base, sub, x1);
-  st4(base + HALF, sub, x2);
+  st4_nt(base, sub, x1);
+  st4_nt(base + HALF, sub, x2);
 }
 
 // Any head_dim (even when ROPE), any alignment: one wave per head.
