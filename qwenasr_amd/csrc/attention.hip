@@ -315,6 +315,10 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
 
   // A tile: this wave's keys t0 .. t0 + 15 (past k_end: repeat the last key,
   // masked in process_tile).
+  // Cached loads: the K/V rows of all layers (235 MB at 28 layers x 1024
+  // positions of the 1.7B shape) stay in the last-level cache from one decode
+  // step to the next while the weights stream past it nontemporally;
+  // nontemporal K/V loads measured 895 -> 956 us per decoded token.
   auto load_tile = [&](int t0, float4 (&kk)[C4], float (&vv)[16][DPL]) {
     const int nkeys = min(16, k_end - t0);
     const int j = min(kq, nkeys - 1);
