@@ -228,3 +228,65 @@ def test_prefill_then_decode_matches_the_oracle(tmp_path, dev, H, I):
     top2 = np.sort(logits)[-2:]
     if top2[1] - top2[0] > 10 * TOL * max(1.0, abs(top2[1])):
         assert int(dec.token.cpu()[0]) == tok
+
+
+def test_graph_replays_equal_the_eager_calls(tmp_path, dev):
+    """bench.py times the decode step and the prefill as captured HIP graphs.
+    Each of three replays, with the outputs overwritten by eager fills and the
+    device synchronised in between, must give the eager call's results bit for
+    bit: decode (fused and unfused, key splits at position 300) and a 64-token
+    prefill (matrix-core GEMMs, cache rows of every layer)."""
+    from qwenasr_amd.decoder import DecoderInt8
+
+    H, I, L, nq, nk, hd, vocab = 2048, 6144, 2, 16, 8, 128, 1000
+    r = np.random.default_rng([37, H])
+    w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
+    weights = _load(tmp_path, w, L, dev)
+    gen = torch.Generator(device=dev).manual_seed(37)
+
+    def snapshot(d, names, rows):
+        got = {n: getattr(d, n).clone() for n in names}
+        for l in range(L):
+            got[f"k{l}"] = d.kv.k_layer_block(l).view(d.kv.max_seq, -1)[rows].clone()
+            got[f"v{l}"] = d.kv.v_layer_block(l).view(d.kv.max_seq, -1)[rows].clone()
+        return got
+
+    def scribble(d, names, rows):
+        for n in names:
+            t = getattr(d, n)
+            t.fill_(-1) if t.dtype == torch.int32 else t.fill_(float("nan"))
+        for l in range(L):
+            d.kv.k_layer_block(l).view(d.kv.max_seq, -1)[rows] = float("nan")
+            d.kv.v_layer_block(l).view(d.kv.max_seq, -1)[rows] = float("nan")
+
+    def check(d, fn, names, rows, what):
+        fn()
+        torch.cuda.synchronize()
+        ref = snapshot(d, names, rows)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        for rep in range(3):
+            scribble(d, names, rows)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = snapshot(d, names, rows)
+            for n, t in ref.items():
+                assert torch.equal(got[n], t), f"{what}: replay {rep} differs in {n}"
+
+    pos = 300
+    for fuse in (True, False):
+        d = DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=512, device=dev, fuse_norms=fuse)
+        d.kv.k.normal_(generator=gen)
+        d.kv.v.normal_(generator=gen)
+        d.prepare(pos)
+        x = torch.randn(H, device=dev, generator=gen)
+        check(d, lambda: d.decode(x, pos), ("x_norm", "logits", "token"), pos,
+              f"decode fuse_norms={fuse}")
+
+    T = 64
+    d = DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=512, device=dev)
+    d.prepare_prefill(0, T)
+    e = torch.randn(T * H, device=dev, generator=gen)
+    check(d, lambda: d.prefill(e, T, 0), ("px",), slice(0, T), "prefill")

@@ -1191,3 +1191,102 @@ def test_causal_attention_split_repeated_calls_share_the_workspace(dev):
         K.causal_attention_split(outs[it], q, k, v, 1, seq_k, nq, nk, hd, hd ** -0.5, pos, ws)
     for it in range(64):
         assert_close(host(outs[it]), cases[it % 2][4], RTOL, ATOL, f"call {it}")
+
+
+def test_config_chains_replay_in_graphs(dev):
+    """bench.py times the c2-c5 chains as captured HIP graphs. For each chain,
+    three replays -- inputs restored and outputs overwritten by eager work,
+    the device synchronised in between -- give the eager call's results bit
+    for bit (the W8A8 GEMM at B=256, the packed kernel, and at B=32, the
+    small-batch kernel)."""
+    from qwenasr_amd import kernels as K
+
+    gen = torch.Generator(device=dev).manual_seed(41)
+
+    def rnd(*n):
+        return torch.randn(*n, device=dev, generator=gen)
+
+    def run_chain(name, inputs, outputs, fn):
+        pristine = {k: v.clone() for k, v in inputs.items()}
+
+        def restore():
+            for k, v in inputs.items():
+                v.copy_(pristine[k])
+            for t in outputs.values():
+                t.fill_(-1) if t.dtype in (torch.int8, torch.int32) else t.fill_(float("nan"))
+
+        restore()
+        fn()
+        torch.cuda.synchronize()
+        ref = {k: v.clone() for k, v in {**inputs, **outputs}.items()}
+        restore()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        for rep in range(3):
+            restore()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            for k, v in {**inputs, **outputs}.items():
+                assert torch.equal(v, ref[k]), f"{name}: replay {rep} differs in {k}"
+
+    rope = K.RopeCache(dev)
+    rope.ensure(2048, 128, 1e6)
+
+    # c2 at 64 tokens: gather, add+RMSNorm, q/k norm+RoPE, SwiGLU
+    T, H, I, V = 64, 1024, 3072, 4096
+    table = rnd(V * H)
+    ids = torch.randint(0, V, (T,), device=dev, generator=gen, dtype=torch.int32)
+    gin = {"x": rnd(T * H), "q": rnd(T * 16 * 128), "k": rnd(T * 8 * 128)}
+    gout = {"emb": torch.empty(T * H, device=dev), "y": torch.empty(T * H, device=dev),
+            "o": torch.empty(T * I, device=dev)}
+    d, gu, w = rnd(T * H), rnd(T * 2 * I), rnd(H)
+    qw, kw = rnd(128), rnd(128)
+
+    def c2():
+        K.embed_gather_f32(gout["emb"], table, ids, T, H)
+        K.add_rms_norm(gin["x"], d, w, gout["y"], T, H, 1e-6)
+        K.head_rms_norm_rope(gin["q"], gin["k"], qw, kw, rope.cos, rope.sin, None, T, 16, 8, 128, 1e-6)
+        K.swiglu_multiply(gout["o"], gu, T, I)
+
+    run_chain("c2", gin, gout, c2)
+
+    # c3 at 300 rows: PE add, LayerNorm, erf-GELU
+    R, D, F_ = 300, 896, 3584
+    pe = torch.empty(13 * D, device=dev)
+    K.sinusoidal_pe(pe, 13, D)
+    ein = {"x": rnd(R * D), "h": rnd(R * F_)}
+    eout = {"ln": torch.empty(R * D, device=dev)}
+    lw, lb = rnd(D), rnd(D)
+
+    def c3():
+        K.pe_add(ein["x"], pe, R, D, 13)
+        K.layer_norm(eout["ln"], ein["x"], lw, lb, R, D, 1e-5)
+        K.gelu_erf(ein["h"], R * F_)
+
+    run_chain("c3", ein, eout, c3)
+
+    # c4: W8A8 matvec + SwiGLU with the activation quantized in the kernel
+    Hc, Ic = 2048, 6144
+    wq, ws = K.quantize_f32_to_int8(rnd(2 * Ic * Hc) * 0.02, 2 * Ic, Hc)
+    wgu = K.QuantWeight(wq, ws, 2 * Ic, Hc)
+    xin = rnd(Hc)
+    c4out = {"o": torch.empty(Ic, device=dev)}
+    run_chain("c4", {}, c4out, lambda: K.gate_up_swiglu_w8a8_f32in(c4out["o"], wgu, xin, Hc, Ic))
+
+    # c5 at B=256 and B=32: add+RMSNorm+quant, q/k norm+RoPE at per-row positions, GEMM
+    wpk = K.pack_w8a8_tiles(wgu)
+    for B in (256, 32):
+        bin_ = {"x": rnd(B * Hc), "q": rnd(B * 16 * 128), "k": rnd(B * 8 * 128)}
+        bout = {"xq": torch.empty(B * Hc, dtype=torch.int8, device=dev), "xs": torch.empty(B, device=dev),
+                "o": torch.empty(B * Ic, device=dev)}
+        bd, bw = rnd(B * Hc), rnd(Hc)
+        pos = torch.randint(0, 2048, (B,), device=dev, generator=gen, dtype=torch.int32)
+
+        def c5():
+            K.add_rms_norm_quant(bin_["x"], bd, bw, None, bout["xq"], bout["xs"], B, Hc, 1e-6)
+            K.head_rms_norm_rope(bin_["q"], bin_["k"], qw, kw, rope.cos, rope.sin, pos, B, 16, 8, 128, 1e-6)
+            K.gate_up_swiglu_w8a8_packed(bout["o"], wpk, bout["xq"], bout["xs"], B, Hc, Ic)
+
+        run_chain(f"c5 B={B}", bin_, bout, c5)
