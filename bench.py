@@ -218,6 +218,30 @@ class C3EncoderOps(Workload):
         return {"rows": 3000, "d_model": 896, "ffn": 3584, "pe_period": 13, "buffer_sets": self.S}
 
 
+class C3Fused(C3EncoderOps):
+    """c3 with the PE add and the LayerNorm that reads its rows (layer 0's
+    attention norm, encoder.rs:341-343 then 370-371) in one pass."""
+    name = "c3_fused"
+    description = ("qwen3-asr-0.6b audio-encoder ops with the PE add fused into layer 0's LayerNorm: "
+                   "x[3000,896] += pe (13-row table), LayerNorm(eps 1e-5) of it, one pass; exact erf-GELU "
+                   "on [3000,3584]")
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        c = ENC_0_6B
+        T, D, FF, P, S = 3000, c["d_model"], c["ffn"], c["pe_rows"], self.S
+        gelu = self.kernels["gelu_erf"]
+        self.kernels = {
+            "pe_add_layer_norm": (lambda i: K.pe_add_layer_norm(
+                self.x[i % S], self.pe, self.y[i % S], self.w, self.b, T, D, P, c["eps"]),
+                3 * T * D * F + P * D * F + 2 * D * F),
+            "gelu_erf": gelu,
+        }
+        self.step_bytes = sum(b for _, b in self.kernels.values())
+
+
 class C4Int8Matvec(Workload):
     name = "c4"
     description = ("qwen3-asr-1.7b INT8 W8A8 gate/up matvec [12288,2048] + SwiGLU, B=1, 28 distinct "
@@ -657,7 +681,8 @@ class LmHead(Workload):
         return {"batch": 1, "hidden": 1024, "vocab": VOCAB, "weight_copies": 4}
 
 
-WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c4": C4Int8Matvec,
+WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c3_fused": C3Fused,
+             "c4": C4Int8Matvec,
              "c5": C5BatchedDecode, "c5_b32": C5Share, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
              "lm_head": LmHead, "decode_step": DecodeStep,
              "w8a32_prefill": W8A32Prefill, "prefill_step": PrefillStep}

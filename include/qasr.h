@@ -186,6 +186,16 @@ int qasr_sinusoidal_pe_f32(float* pe, size_t n_pos, size_t d_model, void* stream
 int qasr_pe_add_f32(float* x, const float* pe, size_t rows, size_t d_model,
                     size_t n_pos, void* stream);
 
+/* x[r,:] += pe[r mod n_pos, :], then out = layer_norm(x) (the arithmetic of
+ * qasr_layer_norm_f32), in one pass over the rows. Replaces the encoder's PE
+ * add (encoder.rs:341-343, 599-601) together with layer 0's attention
+ * LayerNorm of the same rows (encoder.rs:370-371, 625-626; kernels/mod.rs:866-895).
+ * x and out equal those of qasr_pe_add_f32 followed by qasr_layer_norm_f32 bit
+ * for bit. out and pe must not overlap x. */
+int qasr_pe_add_layer_norm_f32(float* x, const float* pe, float* out, const float* weight,
+                               const float* bias, size_t rows, size_t d_model, size_t n_pos,
+                               float eps, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Token-embedding gather (decoder.rs:631-646, context.rs:115-124)           */
 /* ------------------------------------------------------------------------ */

@@ -350,6 +350,26 @@ inline void sinusoidal_pe(F pe, size_t n_pos, size_t d_model) {
   detail::check(qasr_sinusoidal_pe_f32(pe.ptr, n_pos, d_model, detail::st()), "sinusoidal_pe");
 }
 
+// x[r] += pe[r mod n_pos] (the per-chunk add of encoder.rs:341-343 over all rows)
+inline void pe_add(F x, CF pe, size_t rows, size_t d_model, size_t n_pos) {
+  detail::need(x, rows * d_model, "x");
+  detail::need(pe, n_pos * d_model, "pe");
+  detail::check(qasr_pe_add_f32(x.ptr, pe.ptr, rows, d_model, n_pos, detail::st()), "pe_add");
+}
+
+// pe_add + layer 0's LayerNorm of the same rows (encoder.rs:341-343, 370-371) in one pass
+inline void pe_add_layer_norm(F x, CF pe, F out, CF weight, CF bias, size_t rows, size_t d_model,
+                              size_t n_pos, float eps) {
+  detail::need(x, rows * d_model, "x");
+  detail::need(pe, n_pos * d_model, "pe");
+  detail::need(out, rows * d_model, "out");
+  detail::need(weight, d_model, "weight");
+  detail::need(bias, d_model, "bias");
+  detail::check(qasr_pe_add_layer_norm_f32(x.ptr, pe.ptr, out.ptr, weight.ptr, bias.ptr, rows, d_model,
+                                           n_pos, eps, detail::st()),
+                "pe_add_layer_norm");
+}
+
 // ---- token embeddings (decoder.rs:631-646) ------------------------------------------
 inline void tok_embed_bf16_to_f32(F dst, DevSlice<const uint16_t> tok_emb_bf16,
                                   DevSlice<const int32_t> token_id_on_device, size_t dim) {

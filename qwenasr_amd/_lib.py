@@ -61,6 +61,7 @@ SIGNATURES: dict[str, list] = {
     "qasr_gelu_erf_f32": [P, Z, P],
     "qasr_sinusoidal_pe_f32": [P, Z, Z, P],
     "qasr_pe_add_f32": [P, P, Z, Z, Z, P],
+    "qasr_pe_add_layer_norm_f32": [P, P, P, P, P, Z, Z, Z, F, P],
     "qasr_embed_gather_f32": [P, P, P, Z, Z, Z, P],
     "qasr_embed_gather_bf16": [P, P, P, Z, Z, Z, P],
     "qasr_embed_gather_i8": [P, P, P, P, Z, Z, Z, P],

@@ -196,16 +196,22 @@ __global__ __launch_bounds__(BLOCK) void layer_norm_vec_kernel(
 
 // One wave per row (4 rows per workgroup): the row's NV float4 per lane stay
 // in registers and both statistics are wave reductions (no LDS, no barrier).
-template <int NV>
+// With PE the row first takes the position-embedding add of pe_add_vec_kernel
+// (x[r] += pe[r mod n_pos], the same fp32 adds) and is written back to x_out
+// before it is normalised: the encoder's PE add (encoder.rs:341-343) and layer
+// 0's LayerNorm of the same rows (encoder.rs:370-371) in one pass.
+template <int NV, bool PE = false>
 __global__ __launch_bounds__(256) void layer_norm_wave_kernel(
     float* out, const float* x, const float* __restrict__ w, const float* __restrict__ b,
-    int rows, int hidden, float eps) {
+    int rows, int hidden, float eps, float* x_out = nullptr, const float* pe = nullptr,
+    int n_pos = 1) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
   if (row >= rows) return;
   const int h4 = hidden >> 2;
   const int fused_end = hidden & ~7;
   const size_t base = (size_t)row * (size_t)h4;
+  const size_t pbase = PE ? (size_t)(row % n_pos) * (size_t)h4 : 0;
   float4 v[NV], wv[NV], bv[NV];
   float s = 0.0f;
 #pragma unroll
@@ -215,6 +221,11 @@ __global__ __launch_bounds__(256) void layer_norm_wave_kernel(
       wv[i] = ld4(w, c);  // gain and bias: independent of the statistics
       bv[i] = ld4(b, c);
       v[i] = ld4_nt(x, base + c);
+      if constexpr (PE) {
+        const float4 p = ld4(pe, pbase + c);  // 13 table rows shared by all rows: cached
+        v[i].x += p.x; v[i].y += p.y; v[i].z += p.z; v[i].w += p.w;
+        st4_nt(x_out, base + c, v[i]);
+      }
       s += v[i].x;
       s += v[i].y;
       s += v[i].z;
@@ -423,6 +434,44 @@ extern "C" int qasr_layer_norm_f32(float* out, const float* x, const float* weig
     layer_norm_vec_kernel<256, 8><<<grid, 256, 0, st>>>(out, x, weight, bias, h, eps);
   }
   return launch_status("layer_norm");
+}
+
+static bool spans_overlap(const void* a, size_t an, const void* b, size_t bn) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + bn && pb < pa + an;
+}
+
+extern "C" int qasr_pe_add_layer_norm_f32(float* x, const float* pe, float* out,
+                                          const float* weight, const float* bias, size_t rows,
+                                          size_t d_model, size_t n_pos, float eps, void* stream) {
+  if (rows == 0 || d_model == 0) return QASR_OK;
+  QASR_REQUIRE(x && pe && out && weight && bias, "pe_add_layer_norm: null pointer");
+  QASR_REQUIRE(n_pos > 0 && n_pos < 0x7fffffffu, "pe_add_layer_norm: n_pos must be in [1, 2^31)");
+  int rc = check_rows(rows, d_model);
+  if (rc) return rc;
+  const size_t xb = rows * d_model * sizeof(float), pb = n_pos * d_model * sizeof(float);
+  QASR_REQUIRE(!spans_overlap(out, xb, x, xb) && !spans_overlap(pe, pb, x, xb),
+               "pe_add_layer_norm: out and pe must not overlap x");
+  const int h = (int)d_model, h4 = h / 4;
+  const bool vec = d_model % 4 == 0 && h4 <= 8 * kWave && aligned16(x) && aligned16(out) &&
+                   aligned16(pe) && aligned16(weight) && aligned16(bias);
+  if (!vec) {  // any other shape: the two passes, with the same results
+    rc = qasr_pe_add_f32(x, pe, rows, d_model, n_pos, stream);
+    if (rc != QASR_OK) return rc;
+    return qasr_layer_norm_f32(out, x, weight, bias, rows, d_model, eps, stream);
+  }
+  hipStream_t st = as_stream(stream);
+  const unsigned wgrid = (unsigned)((rows + 3) / 4);
+  const int r = (int)rows, np = (int)n_pos;
+  if (h4 <= kWave)
+    layer_norm_wave_kernel<1, true><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
+  else if (h4 <= 2 * kWave)
+    layer_norm_wave_kernel<2, true><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
+  else if (h4 <= 4 * kWave)
+    layer_norm_wave_kernel<4, true><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
+  else
+    layer_norm_wave_kernel<8, true><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
+  return launch_status("pe_add_layer_norm");
 }
 
 extern "C" int qasr_add_rms_norm_quant_f32(float* x, const float* delta, const float* weight,

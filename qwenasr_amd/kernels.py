@@ -431,6 +431,20 @@ def pe_add(x, pe, rows: int, d_model: int, n_pos: int) -> None:
     _lib.call("qasr_pe_add_f32", _ptr(x), _ptr(pe), rows, d_model, n_pos, _stream())
 
 
+def pe_add_layer_norm(x, pe, out, weight, bias, rows: int, d_model: int, n_pos: int,
+                      eps: float) -> None:
+    """``x[r] += pe[r % n_pos]`` then ``out = layer_norm(x)`` in one pass: the
+    encoder's PE add (encoder.rs:341-343) and layer 0's LayerNorm of the same
+    rows (encoder.rs:370-371); equal to ``pe_add`` + ``layer_norm`` bit for bit."""
+    _need(x, F32, rows * d_model, "x")
+    _need(pe, F32, n_pos * d_model, "pe")
+    _need(out, F32, rows * d_model, "out")
+    _need(weight, F32, d_model, "weight")
+    _need(bias, F32, d_model, "bias")
+    _lib.call("qasr_pe_add_layer_norm_f32", _ptr(x), _ptr(pe), _ptr(out), _ptr(weight), _ptr(bias),
+              rows, d_model, n_pos, eps, _stream())
+
+
 # ---------------------------------------------------------------------------
 # Token embeddings (decoder.rs:631-646)
 # ---------------------------------------------------------------------------

@@ -81,6 +81,8 @@ def test_null_pointers_are_invalid_arg():
     assert "null" in last_error()
     assert rc("qasr_add_rms_norm_f32", FAKE, NULL, FAKE, FAKE, 4, 64, 1e-6, NULL) == _lib.QASR_ERR_INVALID_ARG
     assert rc("qasr_layer_norm_f32", FAKE, FAKE, FAKE, NULL, 1, 8, 1e-5, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert rc("qasr_pe_add_layer_norm_f32", FAKE, NULL, ctypes.c_void_p(0x100000), FAKE, FAKE, 1, 8, 1,
+              1e-5, NULL) == _lib.QASR_ERR_INVALID_ARG
     assert rc("qasr_embed_gather_i8", FAKE, FAKE, NULL, FAKE, 1, 16, 10, NULL) == _lib.QASR_ERR_INVALID_ARG
     assert rc("qasr_gate_up_swiglu_w8a8", FAKE, FAKE, FAKE, NULL, FAKE, 1, 64, 32, NULL) == _lib.QASR_ERR_INVALID_ARG
 
@@ -240,3 +242,16 @@ def test_decode_attention_validation():
     assert f(out, NULL, k, v, qw, kw, cs, sn, 4096, 10, 16, 8, 128, 1e-6, 0.088, kc, vc, 2048, NULL, 0, NULL) == inv
     assert f(out, q, k, v, qw, kw, cs, sn, 4096, 10, 0, 8, 128, 1e-6, 0.088, kc, vc, 2048, NULL, 0, NULL) == \
         _lib.QASR_OK
+
+
+def test_pe_add_layer_norm_validation():
+    """out or pe overlapping x, and n_pos = 0, are rejected before any launch."""
+    x, other = FAKE, ctypes.c_void_p(0x100000)
+    assert rc("qasr_pe_add_layer_norm_f32", x, other, ctypes.c_void_p(0x10000 + 16), other, other, 4, 8,
+              1, 1e-5, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert "overlap" in last_error()
+    assert rc("qasr_pe_add_layer_norm_f32", x, ctypes.c_void_p(0x10000 + 64), other, other, other, 4, 8,
+              1, 1e-5, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert rc("qasr_pe_add_layer_norm_f32", x, other, ctypes.c_void_p(0x200000), other, other, 4, 8, 0,
+              1e-5, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert "n_pos" in last_error()

@@ -456,6 +456,33 @@ def test_pe_add(dev, rows, dm, n_pos):
     np.testing.assert_array_equal(host(xt), oracle.pe_add(x, pe, rows, dm, n_pos))
 
 
+@pytest.mark.parametrize("rows,dm,n_pos", [(3000, 896, 13), (64, 1024, 13), (50, 256, 7), (10, 2048, 13),
+                                          (7, 30, 3), (5, 4096, 13)])
+def test_pe_add_layer_norm_equals_the_two_passes(dev, rows, dm, n_pos):
+    """The fused PE add + layer 0 LayerNorm equals pe_add followed by
+    layer_norm bit for bit (x and out), on the one-wave-per-row path (hidden
+    256..2048) and on the two-pass fallbacks (hidden 30, 4096); out against the
+    oracle's LayerNorm of the oracle's x + pe at the LayerNorm tolerance."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(14, rows, dm)
+    x = normal(r, rows * dm)
+    w = normal(r, dm, 0.1, 1.0)
+    b = normal(r, dm, 0.02)
+    pe = dev_t(oracle.sinusoidal_pe(n_pos, dm), dev)
+    wt, bt = dev_t(w, dev), dev_t(b, dev)
+    xa, xb = dev_t(x, dev), dev_t(x, dev)
+    oa, ob = torch.empty_like(xa), torch.empty_like(xb)
+    K.pe_add_layer_norm(xa, pe, oa, wt, bt, rows, dm, n_pos, 1e-5)
+    K.pe_add(xb, pe, rows, dm, n_pos)
+    K.layer_norm(ob, xb, wt, bt, rows, dm, 1e-5)
+    np.testing.assert_array_equal(host(xa), host(xb))
+    np.testing.assert_array_equal(host(oa), host(ob))
+    xs = oracle.pe_add(x, host(pe), rows, dm, n_pos)
+    np.testing.assert_array_equal(host(xa), xs)
+    assert_close(host(oa), oracle.layer_norm(xs, w, b, rows, dm, 1e-5), RTOL, ATOL, "pe_add_layer_norm")
+
+
 # ---------------------------------------------------------------------------
 # Embedding gathers
 # ---------------------------------------------------------------------------
@@ -1194,7 +1221,8 @@ def test_causal_attention_split_repeated_calls_share_the_workspace(dev):
 
 
 def test_config_chains_replay_in_graphs(dev):
-    """bench.py times the c2-c5 chains as captured HIP graphs. For each chain,
+    """bench.py times the c2-c5 chains (and c3 with the fused PE add + LayerNorm)
+    as captured HIP graphs. For each chain,
     three replays -- inputs restored and outputs overwritten by eager work,
     the device synchronised in between -- give the eager call's results bit
     for bit (the W8A8 GEMM at B=256, the packed kernel, and at B=32, the
@@ -1266,6 +1294,12 @@ def test_config_chains_replay_in_graphs(dev):
         K.gelu_erf(ein["h"], R * F_)
 
     run_chain("c3", ein, eout, c3)
+
+    def c3_fused():
+        K.pe_add_layer_norm(ein["x"], pe, eout["ln"], lw, lb, R, D, 13, 1e-5)
+        K.gelu_erf(ein["h"], R * F_)
+
+    run_chain("c3 fused", ein, eout, c3_fused)
 
     # c4: W8A8 matvec + SwiGLU with the activation quantized in the kernel
     Hc, Ic = 2048, 6144
