@@ -10,6 +10,7 @@
 #include <unistd.h>
 
 #include <cmath>
+#include <cstring>
 #include <cstdio>
 #include <cstdlib>
 #include <functional>
@@ -101,6 +102,28 @@ static void test_layer_norm() {
   var /= dim;
   EXPECT(std::fabs(mean) < 0.01, "LayerNorm mean should be ~0, got %f", mean);
   EXPECT(std::fabs(var - 1.0) < 0.02, "LayerNorm variance should be ~1, got %f", var);
+}
+
+// The encoder's PE add fused into layer 0's LayerNorm equals the two passes
+// (encoder.rs:341-343, 370-371), x and the normalised rows alike, bit for bit.
+static void test_pe_add_layer_norm() {
+  const size_t rows = 40, dim = 896, n_pos = 13;
+  std::vector<float> x(rows * dim), w(dim), b(dim);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin(0.37f * (float)i) * 2.0f;
+  for (size_t i = 0; i < dim; ++i) {
+    w[i] = 1.0f + 0.1f * std::cos((float)i);
+    b[i] = 0.02f * std::sin(3.0f * (float)i);
+  }
+  K::DeviceBuffer<float> pe(n_pos * dim);
+  K::sinusoidal_pe(pe, n_pos, dim);
+  auto xa = upload(x), xb = upload(x), dw = upload(w), db = upload(b);
+  K::DeviceBuffer<float> oa(rows * dim), ob(rows * dim);
+  K::pe_add_layer_norm(xa, pe, oa, dw, db, rows, dim, n_pos, 1e-5f);
+  K::pe_add(xb, pe, rows, dim, n_pos);
+  K::layer_norm(ob, xb, dw, db, rows, dim, 1e-5f);
+  const auto hxa = download(xa), hxb = download(xb), hoa = download(oa), hob = download(ob);
+  EXPECT(std::memcmp(hxa.data(), hxb.data(), hxa.size() * 4) == 0, "x differs from pe_add");
+  EXPECT(std::memcmp(hoa.data(), hob.data(), hoa.size() * 4) == 0, "out differs from layer_norm");
 }
 
 // tests/kernels.rs:105-113, for both GELU forms
@@ -419,6 +442,7 @@ int main() {
   }
   run("test_rms_norm", test_rms_norm);
   run("test_layer_norm", test_layer_norm);
+  run("test_pe_add_layer_norm", test_pe_add_layer_norm);
   run("test_gelu", test_gelu);
   run("test_silu", test_silu);
   run("test_vec_ops", test_vec_ops);
