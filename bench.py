@@ -242,6 +242,28 @@ class C3Fused(C3EncoderOps):
         self.step_bytes = sum(b for _, b in self.kernels.values())
 
 
+class EncAddLayerNorm(C3EncoderOps):
+    """An encoder residual add and the LayerNorm that reads its rows next
+    (encoder.rs:386 + 389-390) at the c3 shape, one pass."""
+    name = "enc_add_ln"
+    description = ("qwen3-asr-0.6b encoder residual add + LayerNorm(eps 1e-5) in one pass on [3000,896] "
+                   "(x += delta; out = LayerNorm(x))")
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        c = ENC_0_6B
+        T, D, S = 3000, c["d_model"], self.S
+        self.d = [self.randn(T * D) for _ in range(S)]
+        self.kernels = {
+            "add_layer_norm": (lambda i: K.add_layer_norm(
+                self.x[i % S], self.d[i % S], self.w, self.b, self.y[i % S], T, D, c["eps"]),
+                4 * T * D * F + 2 * D * F),
+        }
+        self.step_bytes = sum(b for _, b in self.kernels.values())
+
+
 class C4Int8Matvec(Workload):
     name = "c4"
     description = ("qwen3-asr-1.7b INT8 W8A8 gate/up matvec [12288,2048] + SwiGLU, B=1, 28 distinct "
@@ -682,6 +704,7 @@ class LmHead(Workload):
 
 
 WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c3_fused": C3Fused,
+             "enc_add_ln": EncAddLayerNorm,
              "c4": C4Int8Matvec,
              "c5": C5BatchedDecode, "c5_b32": C5Share, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
              "lm_head": LmHead, "decode_step": DecodeStep,

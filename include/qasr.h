@@ -196,6 +196,16 @@ int qasr_pe_add_layer_norm_f32(float* x, const float* pe, float* out, const floa
                                const float* bias, size_t rows, size_t d_model, size_t n_pos,
                                float eps, void* stream);
 
+/* x += delta, then out = layer_norm(x) (the arithmetic of qasr_add_inplace_f32
+ * and qasr_layer_norm_f32) in one pass over the rows. Replaces each encoder
+ * residual add together with the LayerNorm that reads its rows next:
+ * add_inplace (encoder.rs:386, 397; kernels/mod.rs:486-488) + layer_norm
+ * (encoder.rs:389-390 and the next layer's 370-371, or the final 401-402;
+ * kernels/mod.rs:866-895). x and out equal those of the two calls bit for bit.
+ * x, delta and out must not overlap. */
+int qasr_add_layer_norm_f32(float* x, const float* delta, const float* weight, const float* bias,
+                            float* out, size_t seq_len, size_t hidden, float eps, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Token-embedding gather (decoder.rs:631-646, context.rs:115-124)           */
 /* ------------------------------------------------------------------------ */

@@ -344,6 +344,19 @@ inline void swiglu_multiply_inplace(F gate, CF up) {
                 "swiglu_multiply_inplace");
 }
 
+// residual add + the LayerNorm that reads its rows (encoder.rs:386 + 389-390, 397 + 370-371)
+inline void add_layer_norm(F x, CF delta, CF weight, CF bias, F out, size_t seq_len, size_t hidden,
+                           float eps) {
+  detail::need(x, seq_len * hidden, "x");
+  detail::need(delta, seq_len * hidden, "delta");
+  detail::need(weight, hidden, "weight");
+  detail::need(bias, hidden, "bias");
+  detail::need(out, seq_len * hidden, "out");
+  detail::check(qasr_add_layer_norm_f32(x.ptr, delta.ptr, weight.ptr, bias.ptr, out.ptr, seq_len,
+                                        hidden, eps, detail::st()),
+                "add_layer_norm");
+}
+
 // ---- position embeddings (kernels/mod.rs:1213-1226) -------------------------------
 inline void sinusoidal_pe(F pe, size_t n_pos, size_t d_model) {
   detail::need(pe, n_pos * d_model, "pe");

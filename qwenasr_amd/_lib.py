@@ -44,6 +44,7 @@ SIGNATURES: dict[str, list] = {
     "qasr_add_rms_norm_f32": [P, P, P, P, Z, Z, F, P],
     "qasr_add_rms_norm_quant_f32": [P, P, P, P, P, P, Z, Z, F, P],
     "qasr_layer_norm_f32": [P, P, P, P, Z, Z, F, P],
+    "qasr_add_layer_norm_f32": [P, P, P, P, P, Z, Z, F, P],
     "qasr_rms_norm_per_head_f32": [P, P, Z, Z, Z, F, P],
     "qasr_apply_rope_neox_f32": [P, P, P, Z, Z, Z, P],
     "qasr_head_rms_norm_rope_f32": [P, P, P, P, P, P, P, Z, Z, Z, Z, Z, F, P],

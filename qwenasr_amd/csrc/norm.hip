@@ -196,14 +196,20 @@ __global__ __launch_bounds__(BLOCK) void layer_norm_vec_kernel(
 
 // One wave per row (4 rows per workgroup): the row's NV float4 per lane stay
 // in registers and both statistics are wave reductions (no LDS, no barrier).
-// With PE the row first takes the position-embedding add of pe_add_vec_kernel
-// (x[r] += pe[r mod n_pos], the same fp32 adds) and is written back to x_out
-// before it is normalised: the encoder's PE add (encoder.rs:341-343) and layer
-// 0's LayerNorm of the same rows (encoder.rs:370-371) in one pass.
-template <int NV, bool PE = false>
+// With a pre-add the row first takes an addition and is written back to x_out
+// before it is normalised, with the fp32 adds of the standalone kernels:
+//   kLnAddPe:    x[r] += pe[r mod n_pos] (pe_add_vec_kernel): the encoder's PE
+//                add (encoder.rs:341-343) and layer 0's LayerNorm of the same
+//                rows (encoder.rs:370-371) in one pass;
+//   kLnAddDelta: x[r] += delta[r] (add_vec_kernel): each residual add of the
+//                encoder layer and the LayerNorm that reads its rows next
+//                (encoder.rs:386 + 389-390, 397 + 370-371, 397 + 401-402).
+enum LnAdd { kLnPlain = 0, kLnAddPe = 1, kLnAddDelta = 2 };
+
+template <int NV, int ADD = kLnPlain>
 __global__ __launch_bounds__(256) void layer_norm_wave_kernel(
     float* out, const float* x, const float* __restrict__ w, const float* __restrict__ b,
-    int rows, int hidden, float eps, float* x_out = nullptr, const float* pe = nullptr,
+    int rows, int hidden, float eps, float* x_out = nullptr, const float* add = nullptr,
     int n_pos = 1) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
@@ -211,7 +217,7 @@ __global__ __launch_bounds__(256) void layer_norm_wave_kernel(
   const int h4 = hidden >> 2;
   const int fused_end = hidden & ~7;
   const size_t base = (size_t)row * (size_t)h4;
-  const size_t pbase = PE ? (size_t)(row % n_pos) * (size_t)h4 : 0;
+  const size_t abase = ADD == kLnAddPe ? (size_t)(row % n_pos) * (size_t)h4 : base;
   float4 v[NV], wv[NV], bv[NV];
   float s = 0.0f;
 #pragma unroll
@@ -221,8 +227,9 @@ __global__ __launch_bounds__(256) void layer_norm_wave_kernel(
       wv[i] = ld4(w, c);  // gain and bias: independent of the statistics
       bv[i] = ld4(b, c);
       v[i] = ld4_nt(x, base + c);
-      if constexpr (PE) {
-        const float4 p = ld4(pe, pbase + c);  // 13 table rows shared by all rows: cached
+      if constexpr (ADD != kLnPlain) {
+        // the 13 PE table rows are shared by all rows (cached); delta streams
+        const float4 p = ADD == kLnAddPe ? ld4(add, abase + c) : ld4_nt(add, abase + c);
         v[i].x += p.x; v[i].y += p.y; v[i].z += p.z; v[i].w += p.w;
         st4_nt(x_out, base + c, v[i]);
       }
@@ -464,14 +471,47 @@ extern "C" int qasr_pe_add_layer_norm_f32(float* x, const float* pe, float* out,
   const unsigned wgrid = (unsigned)((rows + 3) / 4);
   const int r = (int)rows, np = (int)n_pos;
   if (h4 <= kWave)
-    layer_norm_wave_kernel<1, true><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
+    layer_norm_wave_kernel<1, kLnAddPe><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
   else if (h4 <= 2 * kWave)
-    layer_norm_wave_kernel<2, true><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
+    layer_norm_wave_kernel<2, kLnAddPe><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
   else if (h4 <= 4 * kWave)
-    layer_norm_wave_kernel<4, true><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
+    layer_norm_wave_kernel<4, kLnAddPe><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
   else
-    layer_norm_wave_kernel<8, true><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
+    layer_norm_wave_kernel<8, kLnAddPe><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, pe, np);
   return launch_status("pe_add_layer_norm");
+}
+
+extern "C" int qasr_add_layer_norm_f32(float* x, const float* delta, const float* weight,
+                                       const float* bias, float* out, size_t seq_len,
+                                       size_t hidden, float eps, void* stream) {
+  if (seq_len == 0 || hidden == 0) return QASR_OK;
+  QASR_REQUIRE(x && delta && weight && bias && out, "add_layer_norm: null pointer");
+  int rc = check_rows(seq_len, hidden);
+  if (rc) return rc;
+  const size_t xb = seq_len * hidden * sizeof(float);
+  QASR_REQUIRE(!spans_overlap(out, xb, x, xb) && !spans_overlap(delta, xb, x, xb) &&
+                   !spans_overlap(delta, xb, out, xb),
+               "add_layer_norm: x, delta and out must not overlap");
+  const int h = (int)hidden, h4 = h / 4;
+  const bool vec = hidden % 4 == 0 && h4 <= 8 * kWave && aligned16(x) && aligned16(out) &&
+                   aligned16(delta) && aligned16(weight) && aligned16(bias);
+  if (!vec) {  // any other shape: the two passes, with the same results
+    rc = qasr_add_inplace_f32(x, delta, seq_len * hidden, stream);
+    if (rc != QASR_OK) return rc;
+    return qasr_layer_norm_f32(out, x, weight, bias, seq_len, hidden, eps, stream);
+  }
+  hipStream_t st = as_stream(stream);
+  const unsigned wgrid = (unsigned)((seq_len + 3) / 4);
+  const int r = (int)seq_len;
+  if (h4 <= kWave)
+    layer_norm_wave_kernel<1, kLnAddDelta><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, delta);
+  else if (h4 <= 2 * kWave)
+    layer_norm_wave_kernel<2, kLnAddDelta><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, delta);
+  else if (h4 <= 4 * kWave)
+    layer_norm_wave_kernel<4, kLnAddDelta><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, delta);
+  else
+    layer_norm_wave_kernel<8, kLnAddDelta><<<wgrid, 256, 0, st>>>(out, x, weight, bias, r, h, eps, x, delta);
+  return launch_status("add_layer_norm");
 }
 
 extern "C" int qasr_add_rms_norm_quant_f32(float* x, const float* delta, const float* weight,

@@ -115,6 +115,22 @@ def layer_norm(out, x, weight, bias, seq_len: int, hidden: int, eps: float) -> N
               hidden, eps, _stream())
 
 
+
+def add_layer_norm(x, delta, weight, bias, out, seq_len: int, hidden: int, eps: float) -> None:
+    """``x += delta`` then ``out = layer_norm(x)`` in one pass: an encoder
+    residual add (encoder.rs:386, 397) and the LayerNorm that reads its rows
+    next (encoder.rs:389-390, 370-371, 401-402); equal to ``add_inplace`` +
+    ``layer_norm`` bit for bit."""
+    n = seq_len * hidden
+    _need(x, F32, n, "x")
+    _need(delta, F32, n, "delta")
+    _need(weight, F32, hidden, "weight")
+    _need(bias, F32, hidden, "bias")
+    _need(out, F32, n, "out")
+    _lib.call("qasr_add_layer_norm_f32", _ptr(x), _ptr(delta), _ptr(weight), _ptr(bias), _ptr(out),
+              seq_len, hidden, eps, _stream())
+
+
 def rms_norm_per_head(x, weight, seq_len: int, n_heads: int, head_dim: int, eps: float) -> None:
     """In-place per-head RMSNorm (kernels/mod.rs:920-935)."""
     _need(x, F32, seq_len * n_heads * head_dim, "x")

@@ -126,6 +126,29 @@ static void test_pe_add_layer_norm() {
   EXPECT(std::memcmp(hoa.data(), hob.data(), hoa.size() * 4) == 0, "out differs from layer_norm");
 }
 
+// An encoder residual add fused into the LayerNorm that reads its rows equals
+// add_inplace + layer_norm bit for bit (encoder.rs:386 + 389-390).
+static void test_add_layer_norm() {
+  const size_t rows = 40, dim = 1024;
+  std::vector<float> x(rows * dim), d(rows * dim), w(dim), b(dim);
+  for (size_t i = 0; i < x.size(); ++i) {
+    x[i] = std::sin(0.37f * (float)i) * 2.0f;
+    d[i] = std::cos(0.11f * (float)i);
+  }
+  for (size_t i = 0; i < dim; ++i) {
+    w[i] = 1.0f + 0.1f * std::cos((float)i);
+    b[i] = 0.02f * std::sin(3.0f * (float)i);
+  }
+  auto xa = upload(x), xb = upload(x), dd = upload(d), dw = upload(w), db = upload(b);
+  K::DeviceBuffer<float> oa(rows * dim), ob(rows * dim);
+  K::add_layer_norm(xa, dd, dw, db, oa, rows, dim, 1e-5f);
+  K::add_inplace(xb, dd, rows * dim);
+  K::layer_norm(ob, xb, dw, db, rows, dim, 1e-5f);
+  const auto hxa = download(xa), hxb = download(xb), hoa = download(oa), hob = download(ob);
+  EXPECT(std::memcmp(hxa.data(), hxb.data(), hxa.size() * 4) == 0, "x differs from add_inplace");
+  EXPECT(std::memcmp(hoa.data(), hob.data(), hoa.size() * 4) == 0, "out differs from layer_norm");
+}
+
 // tests/kernels.rs:105-113, for both GELU forms
 static void test_gelu() {
   for (int erf_form = 0; erf_form < 2; ++erf_form) {
@@ -443,6 +466,7 @@ int main() {
   run("test_rms_norm", test_rms_norm);
   run("test_layer_norm", test_layer_norm);
   run("test_pe_add_layer_norm", test_pe_add_layer_norm);
+  run("test_add_layer_norm", test_add_layer_norm);
   run("test_gelu", test_gelu);
   run("test_silu", test_silu);
   run("test_vec_ops", test_vec_ops);

@@ -255,3 +255,16 @@ def test_pe_add_layer_norm_validation():
     assert rc("qasr_pe_add_layer_norm_f32", x, other, ctypes.c_void_p(0x200000), other, other, 4, 8, 0,
               1e-5, NULL) == _lib.QASR_ERR_INVALID_ARG
     assert "n_pos" in last_error()
+
+
+def test_add_layer_norm_validation():
+    """Overlapping x, delta and out, and null pointers, are rejected before any launch."""
+    x, other = FAKE, ctypes.c_void_p(0x100000)
+    assert rc("qasr_add_layer_norm_f32", x, other, other, other, ctypes.c_void_p(0x10000 + 16), 4, 8, 1e-5,
+              NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert "overlap" in last_error()
+    assert rc("qasr_add_layer_norm_f32", x, ctypes.c_void_p(0x10000 + 64), other, other,
+              ctypes.c_void_p(0x200000), 4, 8, 1e-5, NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert rc("qasr_add_layer_norm_f32", x, NULL, other, other, ctypes.c_void_p(0x200000), 4, 8, 1e-5,
+              NULL) == _lib.QASR_ERR_INVALID_ARG
+    assert "null" in last_error()

@@ -19,4 +19,4 @@ def test_cpp_kernel_tests_pass():
     print(r.stderr)
     assert r.returncode == 0, r.stdout + r.stderr
     lines = [l for l in r.stdout.splitlines() if l.startswith("test ")]
-    assert len(lines) == 15 and all(l.endswith("ok") for l in lines)
+    assert len(lines) == 16 and all(l.endswith("ok") for l in lines)

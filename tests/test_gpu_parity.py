@@ -483,6 +483,29 @@ def test_pe_add_layer_norm_equals_the_two_passes(dev, rows, dm, n_pos):
     assert_close(host(oa), oracle.layer_norm(xs, w, b, rows, dm, 1e-5), RTOL, ATOL, "pe_add_layer_norm")
 
 
+@pytest.mark.parametrize("rows,dm", [(3000, 896), (64, 1024), (50, 256), (10, 2048), (7, 30), (5, 4096)])
+def test_add_layer_norm_equals_the_two_passes(dev, rows, dm):
+    """The fused residual add + LayerNorm equals add_inplace followed by
+    layer_norm bit for bit (x and out) on the one-wave-per-row path and on the
+    two-pass fallbacks; out against the oracle's LayerNorm of x + delta."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(15, rows, dm)
+    x, d = normal(r, rows * dm), normal(r, rows * dm)
+    w, b = normal(r, dm, 0.1, 1.0), normal(r, dm, 0.02)
+    wt, bt, dt = dev_t(w, dev), dev_t(b, dev), dev_t(d, dev)
+    xa, xb = dev_t(x, dev), dev_t(x, dev)
+    oa, ob = torch.empty_like(xa), torch.empty_like(xb)
+    K.add_layer_norm(xa, dt, wt, bt, oa, rows, dm, 1e-5)
+    K.add_inplace(xb, dt, rows * dm)
+    K.layer_norm(ob, xb, wt, bt, rows, dm, 1e-5)
+    np.testing.assert_array_equal(host(xa), host(xb))
+    np.testing.assert_array_equal(host(oa), host(ob))
+    xs = (x + d).astype(np.float32)
+    np.testing.assert_array_equal(host(xa), xs)
+    assert_close(host(oa), oracle.layer_norm(xs, w, b, rows, dm, 1e-5), RTOL, ATOL, "add_layer_norm")
+
+
 # ---------------------------------------------------------------------------
 # Embedding gathers
 # ---------------------------------------------------------------------------
@@ -1300,6 +1323,8 @@ def test_config_chains_replay_in_graphs(dev):
         K.gelu_erf(ein["h"], R * F_)
 
     run_chain("c3 fused", ein, eout, c3_fused)
+    dres = rnd(R * D)
+    run_chain("add + LayerNorm", ein, eout, lambda: K.add_layer_norm(ein["x"], dres, lw, lb, eout["ln"], R, D, 1e-5))
 
     # c4: W8A8 matvec + SwiGLU with the activation quantized in the kernel
     Hc, Ic = 2048, 6144
