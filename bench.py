@@ -1016,8 +1016,8 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards as pure data parallelism with no exchange; see the design notes)",
+        print(f"bench.py: measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards as pure data parallelism with no exchange between GPUs)",
               file=sys.stderr)
         return 2
 

@@ -1,7 +1,7 @@
 """CPU restatement of the .qint8 weight-file format (test infrastructure only).
 
-Only tests/ may import this module: it is the checker for the C-ABI reader in
-qwenasr_amd/csrc/qint8_file.hip, never part of the product path.
+Only tests/ may import this module: the tests check the C-ABI reader in
+qwenasr_amd/csrc/qint8_file.hip against it; it is never part of the product path.
 
 * ``write_v1`` restates ``write_qint8_file`` (crates/qwen-asr/src/quantize.rs:385-478):
   INT8 tensors first (data, zero pad to 4, f32 scales), then F32 tensors

@@ -2,7 +2,7 @@
 
 Markers:
   gpu -- needs an MI355X (gfx950) and the built libqasr_hip.so; these are the
-         parity tests proper and run on the GPU box. Everything else runs on CPU.
+         parity tests proper and run on a GPU. Everything else runs on CPU.
 """
 from __future__ import annotations
 

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/qasr_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/qasr_oracle.c) before the GPU tests compare against it.
 
 Each check compares the oracle with something it does not share code with:
 the known-answer properties of the reference's own tests
