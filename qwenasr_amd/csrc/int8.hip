@@ -770,7 +770,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
         *reinterpret_cast<uint2*>(&xl[1][x_tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
         *reinterpret_cast<uint2*>(&xl[2][x_tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
       }
-      __syncthreads();
+      lds_barrier();  // the staged chunk is visible to every wave
       if (k0 + NPF * BK < K) {
 #pragma unroll
         for (int c = 0; c < WB / 16; ++c)
@@ -797,7 +797,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
             for (int j = 0; j < MJ; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[term][j], acc[i][j], 0, 0, 0);
       }
-      __syncthreads();
+      lds_barrier();  // LDS only: the prefetched chunk's global loads stay in flight
     }
   }
 
