@@ -1,30 +1,40 @@
 #!/usr/bin/env python3
 """Benchmark of the fused-layer kernel path on one MI355X.
 
-    python bench.py [--workload c2] [--steps K] [--warmup W] [--gpus 1]
+    python bench.py [--workload c5] [--configs c1,c1_cold,...] [--steps K] [--warmup W] [--gpus 1]
 
 Workloads (shapes of the Qwen3-ASR decoder/encoder; synthetic seeded data,
 random-init weights -- no checkpoints):
-  c1  0.6B decode-token chain, B=1: add+RMSNorm[1,1024] + q/k head-norm+RoPE + SwiGLU[3072]
-  c2  0.6B prefill chain, T=512: embed gather + add+RMSNorm + q/k norm+RoPE + SwiGLU  (default)
-  c3  audio-encoder ops: PE add + LayerNorm on [3000,896], erf-GELU on [3000,3584]
-  c4  1.7B INT8 decode gate/up matvec + SwiGLU, B=1, 28 distinct layers per step
-  c5  1.7B batched decode, B=256: add+RMSNorm + q/k norm+RoPE + quantize + INT8 MFMA gate/up GEMM+SwiGLU
+  c1       0.6B decode-token chain, B=1: add+RMSNorm[1,1024] + q/k head-norm+RoPE + SwiGLU[3072] (LLC-hot)
+  c1_cold  c1 with every step's inputs read from HBM (caches flushed between timed replays)
+  c2       0.6B prefill chain, T=512: embed gather + add+RMSNorm + q/k norm+RoPE + SwiGLU
+  c3       audio-encoder ops: PE add + LayerNorm on [3000,896], erf-GELU on [3000,3584]
+  c3_fused c3 with the PE add folded into the LayerNorm that reads its rows
+  c4       1.7B INT8 decode gate/up matvec + SwiGLU, B=1, 28 distinct layers per step
+  c5       1.7B batched decode, B=256: add+RMSNorm+quantize, q/k norm+RoPE, INT8 MFMA gate/up GEMM+SwiGLU
+           (the default, headline workload)
+  c5_b32   c5 at B=32 (one GPU's data-parallel share of 256 streams over 8)
   w8a32_decode  1.7B INT8 decode projections via the W8A32 drop-in (q/k/v/o, gate/up, down), 28 layers
   attn_decode   1.7B decode attention at position 2047 (keys split over workgroups), 28 layers
   attn_prefill  0.6B causal prefill attention, T=512
   lm_head       0.6B INT8 lm_head [151936,1024] logits + greedy argmax, B=1
   decode_step   1.7B INT8 decode of one token, all 28 layers + lm_head argmax on the device (tokens/s)
+  prefill_step  0.6B INT8 prefill of 512 tokens through all 28 layers (tokens/s)
 
 A step is one pass of the workload's kernel chain over one buffer set; sets
 rotate so the working set exceeds the 256 MB last-level cache. Steps are
-captured once into a HIP graph and replayed; the K timed steps are bracketed by
-synchronisation and HIP events on the launch stream. Each kernel's average
-duration is measured the same way (its launches alone, K of them, graph
-replay), and its algorithmic bytes per launch give roofline.achieved.
+captured once into a HIP graph; the graph of K steps is replayed at least 5
+times (and for at least 100 steps), each replay bracketed by synchronisation
+and HIP events on the launch stream, and the median per step is reported with
+p10/p90/min. Each kernel's duration is measured the same way (its launches
+alone, K of them), and its algorithmic bytes per launch give
+roofline.achieved.
 
-Prints ONE JSON line. The CPU baseline is the oracle (a C restatement of the
-reference Rust kernels) timed on this host for a bounded sample.
+Prints ONE JSON line: the headline workload's value, roofline and CPU
+baseline, and under "configs" the other workloads measured in the same run,
+each with its per-kernel figures and its own CPU baseline. The CPU baseline is
+the oracle (a C restatement of the reference Rust kernels, compiled here with
+-march=native) timed on this host for a bounded sample.
 """
 from __future__ import annotations
 
@@ -67,6 +77,7 @@ class Workload:
     tokens_per_step = 1.0  # tokens a step advances (28 layers make one decode token)
     step_bytes = 0   # algorithmic bytes per step
     dtype = "f32"    # arithmetic type of the path
+    steps_hint = 200  # K of the timed region (a cold workload rotates at least K buffer sets)
 
     def __init__(self, dev, torch):
         self.dev = dev
@@ -102,7 +113,7 @@ class C1DecodeChain(Workload):
 
         c = DEC_0_6B
         H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
-        self.S = 64
+        self.S = self.n_sets()
         self.x = [self.randn(H) for _ in range(self.S)]
         self.d = [self.randn(H) for _ in range(self.S)]
         self.y = [torch.empty(H, device=dev) for _ in range(self.S)]
@@ -130,8 +141,35 @@ class C1DecodeChain(Workload):
         self.step_bytes = sum(b for _, b in self.kernels.values())
         self.tokens_per_step = 1.0 / 28  # one layer's chain; 28 layers make a token
 
+    def n_sets(self) -> int:
+        return 64  # 5.4 MB of inputs: the rotation stays in the last-level cache (hot)
+
     def config(self):
-        return {"batch": 1, "hidden": 1024, "heads": "16q/8kv x 128", "intermediate": 3072}
+        return {"batch": 1, "hidden": 1024, "heads": "16q/8kv x 128", "intermediate": 3072,
+                "buffer_sets": self.S, "cache": "hot (64 sets, 5.4 MB, resident in the last-level cache)"}
+
+
+class C1Cold(C1DecodeChain):
+    """c1 with every step on input buffers not touched since the caches were
+    flushed: at least K sets rotate, and 1 GiB is written between timed
+    replays (the last-level cache is 256 MB), so each step reads its
+    activations from HBM. The gains and the RoPE table are shared by the
+    steps (as one layer's are across decode tokens)."""
+    name = "c1_cold"
+    description = C1DecodeChain.description + " -- cold: inputs read from HBM"
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        self.flush_buf = torch.empty(1 << 28, device=dev)  # 1 GiB
+
+    def n_sets(self) -> int:
+        return max(64, self.steps_hint)
+
+    def between(self) -> None:
+        self.flush_buf.fill_(1.0)
+
+    def config(self):
+        return {**super().config(), "cache": f"cold ({self.S} sets, 1 GiB written between timed replays)"}
 
 
 class C2PrefillChain(Workload):
@@ -590,8 +628,11 @@ class PrefillStep(Workload):
         self.mfma_peak_tflops = self.step_flops / floor_s / 1e12
         self.mfma_peak_basis = ("projections at bf16 MFMA 2500/3 TFLOP/s (bf16x3), attention at fp32 MFMA "
                                 "157.3 TFLOP/s, weighted by their flops")
-        self.kernels = {"prefill": (lambda i: self.dec.prefill(self.embeds[i % 2], T, 0), step_bytes,
-                                    self.step_flops)}
+        def prefill_at_0(i):
+            self.dec.kv.len = 0  # every step prefills a chunk at position 0
+            self.dec.prefill(self.embeds[i % 2], T, 0)
+
+        self.kernels = {"prefill": (prefill_at_0, step_bytes, self.step_flops)}
         self.step_bytes = step_bytes
         self.tokens_per_step = float(T)
 
@@ -703,7 +744,8 @@ class LmHead(Workload):
         return {"batch": 1, "hidden": 1024, "vocab": VOCAB, "weight_copies": 4}
 
 
-WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c3_fused": C3Fused,
+WORKLOADS = {"c1": C1DecodeChain, "c1_cold": C1Cold, "c2": C2PrefillChain, "c3": C3EncoderOps,
+             "c3_fused": C3Fused,
              "enc_add_ln": EncAddLayerNorm,
              "c4": C4Int8Matvec,
              "c5": C5BatchedDecode, "c5_b32": C5Share, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
@@ -714,10 +756,21 @@ WORKLOADS = {"c1": C1DecodeChain, "c2": C2PrefillChain, "c3": C3EncoderOps, "c3_
 # ---------------------------------------------------------------------------
 # Timing
 # ---------------------------------------------------------------------------
-def time_replay(torch, fn, n: int, use_graph: bool, reps: int = 1) -> float:
-    """Average ms per call of fn(i), i = 0..n-1, measured with HIP events on the
-    current stream. With use_graph, the n calls are captured once and replayed."""
+def replays_for(steps: int) -> int:
+    """Timed replays of the K-step region: at least 5, and at least 100 steps."""
+    return max(5, math.ceil(100 / max(1, steps)))
+
+
+def time_stats(torch, fn, n: int, use_graph: bool, reps: int, between=None) -> dict:
+    """ms per call of fn(i), i = 0..n-1: the n calls are captured once into a HIP
+    graph (or launched eagerly) and timed ``reps`` times with HIP events on the
+    launch stream, each replay bracketed by device synchronisation; ``between``
+    runs untimed before each replay (the cache flush of a cold workload).
+    Returns the median, p10, p90 and minimum over the replays."""
+    import numpy as np
+
     stream = torch.cuda.current_stream()
+    g = None
     if use_graph:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
@@ -725,171 +778,205 @@ def time_replay(torch, fn, n: int, use_graph: bool, reps: int = 1) -> float:
                 fn(i)
         g.replay()  # warm the graph once
         torch.cuda.synchronize()
-        best = float("inf")
-        for _ in range(reps):
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record(stream)
-            g.replay()
-            e.record(stream)
-            torch.cuda.synchronize()
-            best = min(best, s.elapsed_time(e))
-        del g
-        return best / n
-    best = float("inf")
+    per = []
     for _ in range(reps):
+        if between is not None:
+            between()
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record(stream)
-        for i in range(n):
-            fn(i)
+        if g is not None:
+            g.replay()
+        else:
+            for i in range(n):
+                fn(i)
         e.record(stream)
         torch.cuda.synchronize()
-        best = min(best, s.elapsed_time(e))
-    return best / n
+        per.append(s.elapsed_time(e) / n)
+    del g
+    a = np.asarray(per)
+    return {"median": float(np.median(a)), "p10": float(np.percentile(a, 10)),
+            "p90": float(np.percentile(a, 90)), "min": float(a.min()), "replays": reps}
 
 
 # ---------------------------------------------------------------------------
 # CPU baseline (oracle, reference thread model)
 # ---------------------------------------------------------------------------
+def host_info(threads: int, build: str) -> dict:
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        nproc = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": nproc, "cpu_count": os.cpu_count(), "cpu_model": model, "threads": threads,
+            "oracle_build": build}
+
+
+def cpu_threads() -> int:
+    """The reference pool: min(available cores, MAX_THREADS = 16) (kernels/mod.rs:177, 288-302)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def _run_until(fn, budget):
+    fn()  # untimed: first touch of the outputs, thread and frequency ramp
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget:
+            return n, dt
+
+
 def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
-    """The oracle timed on this host over a bounded sample of the same workload,
-    reported in the GPU step's unit (its algorithmic bytes per second)."""
+    """The oracle (a C restatement of the reference's kernels, compiled here
+    with -march=native) timed on this host over a bounded sample of the same
+    workload, with the reference's thread model: norms, RoPE, SwiGLU,
+    LayerNorm, GELU, PE and attention on one thread; the INT8 matvec on
+    min(cores, 16) threads in contiguous row chunks, one matvec per token.
+    The C functions are called directly on preallocated buffers (no wrapper
+    allocation or copy per call). Reported in the GPU step's unit."""
+    from ctypes import c_void_p
+
     import numpy as np
 
     import oracle
 
+    build = oracle.use_native()
+    L = oracle.lib()
+    P = lambda a: c_void_p(a.ctypes.data)  # noqa: E731
     r = np.random.default_rng(99)
+    nt = cpu_threads()
 
-    def run_until(fn, budget):
-        n, t0 = 0, time.perf_counter()
-        while True:
-            fn()
-            n += 1
-            dt = time.perf_counter() - t0
-            if dt >= budget:
-                return n, dt
+    def f32(*shape, sc=1.0, m=0.0):
+        return (m + sc * r.standard_normal(shape, dtype=np.float32)).astype(np.float32)
 
-    nproc = os.cpu_count() or 1
-    if name in ("c1", "c2", "c5", "c5_b32"):
-        c = DEC_0_6B if not name.startswith("c5") else DEC_1_7B
-        T = {"c1": 1, "c2": 512, "c5": 256, "c5_b32": 32}[name]
+    def qweights(o, i, n=1):
+        """n distinct int8 weight matrices [o, i] with row scales of the quantizer's range."""
+        return [(np.frombuffer(r.bytes(o * i), np.int8).reshape(o, i),
+                 (1e-3 + 1e-4 * r.random(o)).astype(np.float32)) for _ in range(n)]
+
+    def qk_gains(hd):
+        # q/k head norms run in place, and a step repeats them on the same
+        # buffers: a non-unit gain applied hundreds of times drives the smaller
+        # components into denormals (slow on x86). Unit gains keep the values
+        # bounded; the arithmetic is the same for any gain.
+        return np.ones(hd, np.float32), np.ones(hd, np.float32)
+
+    def result(per, threads, sample, tokens_per_step=None):
+        out = {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+               "ms_per_step": per * 1e3, "sample": sample, "host": host_info(threads, build)}
+        if tokens_per_step is not None:
+            out["tokens_per_s"] = tokens_per_step / per
+        return out
+
+    if name in ("c1", "c1_cold"):
+        c = DEC_0_6B
         H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
-        x = r.standard_normal(T * H, dtype=np.float32)
-        d = r.standard_normal(T * H, dtype=np.float32)
-        w = (1 + 0.1 * r.standard_normal(H)).astype(np.float32)
-        q = r.standard_normal(T * nq * hd, dtype=np.float32)
-        k = r.standard_normal(T * nk * hd, dtype=np.float32)
-        qw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
-        kw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
-        cos, sin = oracle.rope_table(2048, hd, c["theta"])
-        c5 = name.startswith("c5")
-        pos = (np.arange(T) if name == "c2" else r.integers(0, 2048 if c5 else 512, T)).astype(np.int32)
-        gu = r.standard_normal(T * 2 * I, dtype=np.float32)
-        table = ids = None
-        if name == "c2":
-            table = (0.02 * r.standard_normal((VOCAB, H), dtype=np.float32))
-            ids = r.integers(0, VOCAB, T).astype(np.int32)
-        wq = ws = None
-        if c5:
-            wq, ws = oracle.quantize_f32_to_int8((0.02 * r.standard_normal(2 * I * H, dtype=np.float32)), 2 * I, H)
+        S = 64 if name == "c1" else 8192  # 8192 x 84 KB = 688 MB rotates through the host caches
+        x, d, y = f32(S, H), f32(S, H), np.empty((S, H), np.float32)
+        q, k = f32(S, nq * hd), f32(S, nk * hd)
+        g, u, o = f32(S, I), f32(S, I), np.empty((S, I), np.float32)
+        (w, (qw, kw)) = f32(H, sc=0.1, m=1.0), qk_gains(hd)
+        cos, sin = oracle.rope_table(512, hd, c["theta"])
+        pos = r.integers(0, 512, S).astype(np.int32)
+        iters = 20000
+        args = (P(x), P(d), P(w), P(y), P(q), P(k), P(qw), P(kw), P(cos), P(sin), P(pos), P(o), P(g), P(u),
+                H, nq, nk, hd, I, c["eps"])
+        n, dt = _run_until(lambda: L.ref_decode_chain_repeat(iters, S, *args), seconds)
+        per = dt / (n * iters)
+        return result(per, 1, f"{n * iters} decode chains (one layer: add+RMSNorm, q/k head norm+RoPE, "
+                              f"SwiGLU) over {S} rotating input sets, one thread, repeated in C",
+                      1.0 / 28)
+    if name in ("c2",):
+        c = DEC_0_6B
+        T = 512
+        H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
+        table = f32(VOCAB, H, sc=0.02)
+        ids = r.integers(0, VOCAB, T).astype(np.int32)
+        x, d, y = np.empty((T, H), np.float32), f32(T, H), np.empty((T, H), np.float32)
+        q, k = f32(T, nq * hd), f32(T, nk * hd)
+        gu, o = f32(T, 2 * I), np.empty((T, I), np.float32)
+        (w, (qw, kw)) = f32(H, sc=0.1, m=1.0), qk_gains(hd)
+        cos, sin = oracle.rope_table(T, hd, c["theta"])
+        pos = np.arange(T, dtype=np.int32)
 
         def step():
-            if table is not None:
-                xx = oracle.embed_gather_f32(table, ids, H)
-            else:
-                xx = x
-            oracle.add_rms_norm(xx, d, w, T, H, c["eps"])
-            oracle.head_rms_norm_rope(q, k, qw, kw, cos, sin, pos, T, nq, nk, hd, c["eps"])
-            if c5:
-                # the reference's INT8 path: W8A32 matvec per token, then swiglu_multiply
-                gate_up = oracle.linear_nobias_int8(x, wq, ws, T, H, 2 * I, n_threads=min(nproc, 16))
-                oracle.swiglu_multiply(gate_up, T, I)
-            elif name == "c1":
-                oracle.swiglu_split(gu[:I], gu[I:2 * I])
-            else:
-                oracle.swiglu_multiply(gu, T, I)
+            L.ref_embed_gather_f32(P(x), P(table), P(ids), T, H)
+            L.ref_add_rms_norm(P(x), P(d), P(w), P(y), T, H, c["eps"])
+            L.ref_head_rms_norm_rope(P(q), P(k), P(qw), P(kw), P(cos), P(sin), P(pos), T, nq, nk, hd, c["eps"])
+            L.ref_swiglu_multiply(P(o), P(gu), T, I)
 
-        n, dt = run_until(step, seconds)
-        per = dt / n
-        threads = min(nproc, 16) if c5 else 1
-        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-                "ms_per_step": per * 1e3, "tokens_per_s": T / per if not c5 else T / (28 * per),
-                "sample": f"{n} full steps of the {name} chain (T={T}) on the oracle, "
-                          f"{'single-threaded norms/RoPE/SwiGLU' + (', INT8 W8A32 matvec on ' + str(threads) + ' threads' if c5 else '')}"}
-    if name == "c3":
+        n, dt = _run_until(step, seconds)
+        return result(dt / n, 1, f"{n} full c2 steps (T=512) on the oracle, one thread", float(T))
+    if name in ("c3", "c3_fused"):
         T, D, FF = 3000, 896, 3584
-        x = r.standard_normal(T * D, dtype=np.float32)
-        h = r.standard_normal(T * FF, dtype=np.float32)
-        w = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
-        b = (0.02 * r.standard_normal(D)).astype(np.float32)
+        x, h, y = f32(T, D), f32(T, FF), np.empty((T, D), np.float32)
+        w, bb = f32(D, sc=0.1, m=1.0), f32(D, sc=0.02)
         pe = oracle.sinusoidal_pe(13, D)
 
         def step():
-            xx = oracle.pe_add(x, pe, T, D, 13)
-            oracle.layer_norm(xx, w, b, T, D, 1e-5)
-            oracle.gelu_tanh(h)  # the reference CPU path's GELU (tanh form)
+            L.ref_pe_add(P(x), P(pe), T, D, 13)
+            L.ref_layer_norm(P(y), P(x), P(w), P(bb), T, D, 1e-5)
+            L.ref_gelu_tanh(P(h), T * FF)  # the reference CPU path's GELU (tanh form)
 
-        n, dt = run_until(step, seconds)
-        per = dt / n
-        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                "ms_per_step": per * 1e3,
-                "sample": f"{n} full c3 steps on the oracle, single-threaded; GELU is the reference's tanh form"}
+        n, dt = _run_until(step, seconds)
+        return result(dt / n, 1, f"{n} c3 steps on the oracle (PE add, then LayerNorm: the reference has no "
+                                 "fused pass), one thread; GELU is the reference's tanh form")
     if name == "c4":
-        H, I = 2048, 6144
-        wq, ws = oracle.quantize_f32_to_int8((0.02 * r.standard_normal(2 * I * H, dtype=np.float32)), 2 * I, H)
-        x = r.standard_normal(H, dtype=np.float32)
-        threads = min(nproc, 16)
-
-        def step():
-            gate_up = oracle.linear_nobias_int8(x, wq, ws, 1, H, 2 * I, n_threads=threads)
-            oracle.swiglu_multiply(gate_up, 1, I)
-
-        n, dt = run_until(step, seconds)
-        per = dt / n
-        return {"value": step_bytes / 28 / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-                "ms_per_step": per * 1e3 * 28, "tokens_per_s": 1.0 / (28 * per),
-                "sample": f"{n} layer matvecs (W8A32, the reference's INT8 path) + SwiGLU on the oracle, "
-                          f"{threads} threads; one weight matrix reused, so it is LLC-warm"}
-    if name == "w8a32_decode":
-        shapes = W8A32Decode.SHAPES
-        ws = {n: (r.integers(-127, 128, o * i, dtype=np.int8), (1e-3 + 1e-4 * r.random(o)).astype(np.float32))
-              for n, (o, i) in shapes.items()}
-        xs = {n: r.standard_normal(i, dtype=np.float32) for n, (o, i) in shapes.items()}
-        threads = min(nproc, 16)
+        H, I, NL = 2048, 6144, 28
+        ws = qweights(2 * I, H, NL)
+        x = f32(H)
+        gu, o = np.empty(2 * I, np.float32), np.empty(I, np.float32)
+        it = [0]
 
         def layer():
-            for n, (o, i) in shapes.items():
-                oracle.linear_nobias_int8(xs[n], ws[n][0], ws[n][1], 1, i, o, n_threads=threads)
+            wq, sc = ws[it[0] % NL]
+            it[0] += 1
+            L.ref_linear_nobias_int8(P(gu), P(x), P(wq), P(sc), 1, H, 2 * I, nt)
+            L.ref_swiglu_multiply(P(o), P(gu), 1, I)
 
-        n, dt = run_until(layer, seconds)
-        per = dt / n
-        return {"value": step_bytes / 28 / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-                "ms_per_step": per * 1e3 * 28, "tokens_per_s": 1.0 / (28 * per),
-                "sample": f"{n} layers of the six W8A32 projections on the oracle, {threads} threads "
-                          "(one layer's weights reused, so LLC-warm)"}
-    if name == "attn_decode":
-        nq, nk, hd, seq_k = 16, 8, 128, 2048
-        q = r.standard_normal(nq * hd, dtype=np.float32)
-        k = r.standard_normal(seq_k * nk * hd, dtype=np.float32)
-        v = r.standard_normal(seq_k * nk * hd, dtype=np.float32)
-        n, dt = run_until(lambda: oracle.causal_attention(q, k, v, 1, seq_k, nq, nk, hd, hd ** -0.5,
-                                                          seq_k - 1), seconds)
-        per = dt / n
-        return {"value": step_bytes / 28 / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                "ms_per_step": per * 1e3 * 28, "tokens_per_s": 1.0 / (28 * per),
-                "sample": f"{n} single-layer decode attentions at position 2047 on the oracle, one thread "
-                          "(the reference threads over heads)"}
-    if name == "attn_prefill":
-        T, nq, nk, hd = 512, 16, 8, 128
-        q = r.standard_normal(T * nq * hd, dtype=np.float32)
-        k = r.standard_normal(T * nk * hd, dtype=np.float32)
-        v = r.standard_normal(T * nk * hd, dtype=np.float32)
-        n, dt = run_until(lambda: oracle.causal_attention(q, k, v, T, T, nq, nk, hd, hd ** -0.5, 0),
-                          seconds)
-        per = dt / n
-        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                "ms_per_step": per * 1e3, "tokens_per_s": T / per,
-                "sample": f"{n} T=512 prefill attentions on the oracle, one thread"}
+        n, dt = _run_until(layer, seconds)
+        per = dt / n * 28
+        return result(per, nt, f"{n} layer matvecs over 28 distinct [12288,2048] int8 weights (W8A32, the "
+                               f"reference's INT8 path) + SwiGLU, {nt} threads; a step is 28 layers", 1.0)
+    if name in ("c5", "c5_b32"):
+        c = DEC_1_7B
+        B, NL = (256 if name == "c5" else 32), 28
+        H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
+        ws = qweights(2 * I, H, NL)
+        x, d, y = f32(B, H), f32(B, H), np.empty((B, H), np.float32)
+        q, k = f32(B, nq * hd), f32(B, nk * hd)
+        (w, (qw, kw)) = f32(H, sc=0.1, m=1.0), qk_gains(hd)
+        cos, sin = oracle.rope_table(2048, hd, c["theta"])
+        pos = r.integers(0, 2048, B).astype(np.int32)
+        gu, o = np.empty((B, 2 * I), np.float32), np.empty((B, I), np.float32)
+        it = [0]
+
+        def layer():
+            wq, sc = ws[it[0] % NL]
+            it[0] += 1
+            L.ref_add_rms_norm(P(x), P(d), P(w), P(y), B, H, c["eps"])
+            L.ref_head_rms_norm_rope(P(q), P(k), P(qw), P(kw), P(cos), P(sin), P(pos), B, nq, nk, hd, c["eps"])
+            # the reference's INT8 path: one W8A32 matvec per stream, then swiglu_multiply
+            L.ref_linear_nobias_int8(P(gu), P(y), P(wq), P(sc), B, H, 2 * I, nt)
+            L.ref_swiglu_multiply(P(o), P(gu), B, I)
+
+        n, dt = _run_until(layer, seconds)
+        return result(dt / n, nt, f"{n} layers of the c{name[1:]} chain (B={B}) on the oracle over 28 distinct "
+                                  f"gate/up weights: norms/RoPE/SwiGLU on one thread, the INT8 W8A32 matvec "
+                                  f"(one per stream) on {nt} threads", B / 28.0)
     if name == "decode_step":
         from oracle.decoder import decode_int8_step
 
@@ -897,71 +984,83 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
         H, I, nq, nk, hd = c["hidden"], c["inter"], c["n_heads"], c["n_kv_heads"], c["head_dim"]
         pos = DecodeStep.POS
 
-        def qw(o, i):
-            return (r.integers(-127, 128, (o, i), dtype=np.int8), (1e-3 + 1e-4 * r.random(o)).astype(np.float32))
-
         def gain(n):
-            return (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+            return f32(n, sc=0.1, m=1.0)
 
-        layer = {"wq": qw(nq * hd, H), "wk": qw(nk * hd, H), "wv": qw(nk * hd, H), "wo": qw(H, nq * hd),
-                 "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": gain(hd), "k_norm": gain(hd),
-                 "input_norm": gain(H), "post_attn_norm": gain(H)}
-        w = {"layers": [layer] * 28, "norm": gain(H), "lm_head": qw(VOCAB, H)}
-        kc = r.standard_normal((28, pos + 1, nk * hd), dtype=np.float32)
-        vc = r.standard_normal((28, pos + 1, nk * hd), dtype=np.float32)
-        x = r.standard_normal(H, dtype=np.float32)
-        threads = min(nproc, 16)
-        n, dt = run_until(lambda: decode_int8_step(w, kc, vc, pos, x, nq, nk, hd, c["eps"], c["theta"],
-                                                   threads), seconds)
-        per = dt / n
-        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-                "ms_per_step": per * 1e3, "tokens_per_s": 1.0 / per,
-                "sample": f"{n} decode tokens at position {pos} on the oracle's restated decode step "
-                          f"(decoder.rs:848-965): INT8 matvecs on {threads} threads, attention on one, "
-                          "one layer's weights shared by the 28 layers (LLC-warm)"}
+        layers = []
+        for _ in range(28):
+            (wq,), (wk,), (wv,), (wo,) = (qweights(nq * hd, H), qweights(nk * hd, H), qweights(nk * hd, H),
+                                          qweights(H, nq * hd))
+            (gu,), (dn,) = qweights(2 * I, H), qweights(H, I)
+            layers.append({"wq": wq, "wk": wk, "wv": wv, "wo": wo, "gate_up": gu, "down": dn,
+                           "q_norm": gain(hd), "k_norm": gain(hd), "input_norm": gain(H),
+                           "post_attn_norm": gain(H)})
+        w = {"layers": layers, "norm": gain(H), "lm_head": qweights(VOCAB, H)[0]}
+        kc = f32(28, pos + 1, nk * hd)
+        vc = f32(28, pos + 1, nk * hd)
+        x = f32(H)
+        n, dt = _run_until(lambda: decode_int8_step(w, kc, vc, pos, x, nq, nk, hd, c["eps"], c["theta"], nt),
+                           seconds)
+        return result(dt / n, nt, f"{n} decode tokens at position {pos} on the oracle's restated decode step "
+                                  f"(decoder.rs:848-965) over 28 distinct layers of weights: INT8 matvecs on "
+                                  f"{nt} threads, attention and norms on one", 1.0)
     if name == "prefill_step":
         from oracle.decoder import prefill_int8
 
         c = DEC_0_6B
         H, I, nq, nk, hd, T = c["hidden"], c["inter"], c["n_heads"], c["n_kv_heads"], c["head_dim"], PrefillStep.T
 
-        def qw(o, i):
-            return (r.integers(-127, 128, (o, i), dtype=np.int8), (1e-3 + 1e-4 * r.random(o)).astype(np.float32))
-
         def gain(n):
-            return (1 + 0.1 * r.standard_normal(n)).astype(np.float32)
+            return f32(n, sc=0.1, m=1.0)
 
-        layer = {"wq": qw(nq * hd, H), "wk": qw(nk * hd, H), "wv": qw(nk * hd, H), "wo": qw(H, nq * hd),
-                 "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": gain(hd), "k_norm": gain(hd),
-                 "input_norm": gain(H), "post_attn_norm": gain(H)}
+        (wq,), (wk,), (wv,), (wo,) = (qweights(nq * hd, H), qweights(nk * hd, H), qweights(nk * hd, H),
+                                      qweights(H, nq * hd))
+        (gu,), (dn,) = qweights(2 * I, H), qweights(H, I)
+        layer = {"wq": wq, "wk": wk, "wv": wv, "wo": wo, "gate_up": gu, "down": dn, "q_norm": gain(hd),
+                 "k_norm": gain(hd), "input_norm": gain(H), "post_attn_norm": gain(H)}
         kc = np.zeros((1, T, nk * hd), np.float32)
         vc = np.zeros_like(kc)
-        x = r.standard_normal(T * H, dtype=np.float32)
-        threads = min(nproc, 16)
-        # whole layers of the 512-token prefill, one at a time; the step is 28 of them
-        n, dt = run_until(lambda: prefill_int8({"layers": [layer]}, kc, vc, 0, x, T, nq, nk, hd, c["eps"],
-                                               c["theta"], threads), seconds)
+        x = f32(T * H)
+        n, dt = _run_until(lambda: prefill_int8({"layers": [layer]}, kc, vc, 0, x, T, nq, nk, hd, c["eps"],
+                                                c["theta"], nt), seconds)
         per = dt / n * 28
-        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-                "ms_per_step": per * 1e3, "tokens_per_s": T / per,
-                "sample": f"{n} layers of a {T}-token prefill on the oracle's restated prefill "
-                          f"(decoder.rs:751-847; INT8 linears on {threads} threads, attention and norms on "
-                          "one), timed per layer and scaled to the 28 layers"}
+        return result(per, nt, f"{n} layers of a {T}-token prefill on the oracle's restated prefill "
+                               f"(decoder.rs:751-847; INT8 linears on {nt} threads, attention and norms on "
+                               "one), timed per layer and scaled to the 28 layers", float(T))
+    if name == "w8a32_decode":
+        shapes = W8A32Decode.SHAPES
+        ws = {nm: qweights(o, i)[0] for nm, (o, i) in shapes.items()}
+        xs = {nm: f32(i) for nm, (o, i) in shapes.items()}
+        ys = {nm: np.empty(o, np.float32) for nm, (o, i) in shapes.items()}
+
+        def layer():
+            for nm, (o, i) in shapes.items():
+                L.ref_linear_nobias_int8(P(ys[nm]), P(xs[nm]), P(ws[nm][0]), P(ws[nm][1]), 1, i, o, nt)
+
+        n, dt = _run_until(layer, seconds)
+        return result(dt / n * 28, nt, f"{n} layers of the six W8A32 projections on the oracle, {nt} threads "
+                                       "(one layer's weights reused: LLC-warm)", 1.0)
+    if name in ("attn_decode", "attn_prefill"):
+        nq, nk, hd = 16, 8, 128
+        seq_q, seq_k, off = (1, 2048, 2047) if name == "attn_decode" else (512, 512, 0)
+        q, kk, v = f32(seq_q * nq * hd), f32(seq_k * nk * hd), f32(seq_k * nk * hd)
+        o = np.empty(seq_q * nq * hd, np.float32)
+        n, dt = _run_until(lambda: L.ref_causal_attention(P(o), P(q), P(kk), P(v), seq_q, seq_k, nq, nk, hd,
+                                                          hd ** -0.5, off), seconds)
+        per = dt / n * (28 if name == "attn_decode" else 1)
+        return result(per, 1, f"{n} {name} calls on the oracle, one thread (the reference threads over heads)",
+                      1.0 if name == "attn_decode" else 512.0)
     if name == "lm_head":
         V, H = VOCAB, 1024
-        wq, ws = oracle.quantize_f32_to_int8(0.02 * r.standard_normal(V * H, dtype=np.float32), V, H)
-        x = r.standard_normal(H, dtype=np.float32)
-        threads = min(nproc, 16)
+        (wq, sc), = qweights(V, H)
+        x, lg, idx = f32(H), np.empty(V, np.float32), np.empty(1, np.int32)
 
         def step():
-            lg = oracle.linear_nobias_int8(x, wq, ws, 1, H, V, n_threads=threads)
-            oracle.argmax_rows(lg, 1, V)
+            L.ref_linear_nobias_int8(P(lg), P(x), P(wq), P(sc), 1, H, V, nt)
+            L.ref_argmax_rows(P(idx), P(lg), 1, V)
 
-        n, dt = run_until(step, seconds)
-        per = dt / n
-        return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-                "ms_per_step": per * 1e3, "tokens_per_s": 1.0 / per,
-                "sample": f"{n} INT8 lm_head matvecs + argmax on the oracle, {threads} threads"}
+        n, dt = _run_until(step, seconds)
+        return result(dt / n, nt, f"{n} INT8 lm_head matvecs + argmax on the oracle, {nt} threads", 1.0)
     raise ValueError(name)
 
 
@@ -1000,14 +1099,140 @@ def profile_kernel(torch, wl, name: str, n: int) -> int:
 
 
 # ---------------------------------------------------------------------------
+DEFAULT_CONFIGS = "c1,c1_cold,c2,c3_fused,c4,c5_b32,decode_step"
+
+
+def _round(v):
+    if isinstance(v, float):
+        return round(v, 4)
+    if isinstance(v, dict):
+        return {k: _round(x) for k, x in v.items()}
+    return v
+
+
+def measure(torch, dev, wl, K: int, W: int, use_graph: bool) -> dict:
+    """Warmup, then the step and each kernel timed (median over replays of
+    K launches), the roofline of the kernel moving the most bytes."""
+    reps = replays_for(K)
+    between = getattr(wl, "between", None)
+    for i in range(W):
+        wl.step(i)
+    torch.cuda.synchronize()
+    try:
+        step = time_stats(torch, wl.step, K, use_graph, reps, between)
+    except RuntimeError as ex:  # capture unsupported: time eagerly
+        print(f"[bench] {wl.name}: graph capture failed ({ex}); timing eagerly", file=sys.stderr)
+        use_graph = False
+        step = time_stats(torch, wl.step, K, False, reps, between)
+    ms = step["median"]
+    print(f"[bench] {wl.name}: step {ms * 1e3:.2f} us (p10 {step['p10'] * 1e3:.2f}, p90 {step['p90'] * 1e3:.2f})",
+          file=sys.stderr, flush=True)
+    per_kernel = {}
+    for kname, spec in wl.kernels.items():
+        launch, nbytes = spec[0], spec[1]
+        st = time_stats(torch, launch, K, use_graph, reps, between)
+        us = st["median"] * 1e3
+        d = {"us": us, "us_p10": st["p10"] * 1e3, "us_p90": st["p90"] * 1e3, "bytes": nbytes,
+             "GB/s": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+        if len(spec) > 2:
+            d["flops"] = spec[2]
+            d["TFLOP/s"] = spec[2] / (us * 1e-6) / 1e12
+        per_kernel[kname] = d
+        print(f"[bench] {wl.name}/{kname}: {us:.2f} us, {d['GB/s']:.0f} GB/s", file=sys.stderr, flush=True)
+    value = wl.step_bytes / (ms * 1e-3) / 1e9
+    return {"step": step, "use_graph": use_graph, "per_kernel": per_kernel, "value": value,
+            "tokens_per_s": wl.tokens_per_step / (ms * 1e-3)}
+
+
+def roofline_of(torch, dev, wl, m: dict, K: int) -> dict:
+    per_kernel = m["per_kernel"]
+    # dominant kernel = the one moving the most algorithmic bytes per step
+    dom_name = max(per_kernel, key=lambda k: per_kernel[k]["bytes"])
+    dom = per_kernel[dom_name]
+    traffic = traffic_entry = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        try:
+            data = json.loads(tfile.read_text())
+            # a derived workload (c3_fused) runs its parent's kernels at the same shapes
+            for name in [getattr(c, "name", "") for c in type(wl).__mro__]:
+                entry = data.get(name, {}).get(dom_name)
+                if entry:
+                    traffic, traffic_entry = entry["hbm_bytes_per_launch"], entry
+                    break
+        except (ValueError, OSError, KeyError, TypeError):
+            traffic = None
+    mfma_peak = getattr(wl, "mfma_peak_tflops", FP32_PEAK_TFLOPS)
+    if "flops" in dom and dom["flops"] / dom["bytes"] > mfma_peak * 1e12 / (HBM_PEAK_GBS * 1e9):
+        roofline = {"bound": "mfma", "kernel": dom_name, "achieved": round(dom["TFLOP/s"], 2),
+                    "peak": round(mfma_peak, 1), "unit": "TFLOP/s",
+                    "frac": round(dom["TFLOP/s"] / mfma_peak, 4), "traffic": traffic,
+                    "avg_us": round(dom["us"], 3), "algorithmic_flops": dom["flops"],
+                    "algorithmic_bytes": dom["bytes"],
+                    "peak_basis": getattr(wl, "mfma_peak_basis", "fp32 MFMA, 157.3 TFLOP/s dense")}
+    else:
+        roofline = {"bound": "hbm", "kernel": dom_name, "achieved": round(dom["GB/s"], 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["frac_hbm"], 4),
+                    "traffic": traffic, "avg_us": round(dom["us"], 3), "algorithmic_bytes": dom["bytes"]}
+    roofline["timing"] = "median over replays of K graph-replayed launches, HIP events on the launch stream"
+    if traffic_entry is not None:
+        roofline["traffic_source"] = (f"profiles/traffic.json: rocprofv3 FETCH_SIZE/WRITE_SIZE of "
+                                      f"{traffic_entry.get('kernel')}, scaled by a 64 MiB copy's readings")
+    if roofline["bound"] == "hbm" and m["use_graph"]:
+        # context for frac: a device copy moving the same bytes (half read, half
+        # written) over rotating buffers, timed the same way
+        n_f = max(1, dom["bytes"] // 8)
+        n_sets = sets_for(dom["bytes"])
+        src = [torch.randn(n_f, device=dev) for _ in range(n_sets)]
+        dst = [torch.empty(n_f, device=dev) for _ in range(n_sets)]
+        c = time_stats(torch, lambda i: dst[i % n_sets].copy_(src[i % n_sets]), K, True, replays_for(K))
+        c_us = c["median"] * 1e3
+        roofline["copy_same_bytes"] = {"us": round(c_us, 3), "GB/s": round(8 * n_f / (c_us * 1e-6) / 1e9, 1),
+                                       "frac": round(8 * n_f / (c_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del src, dst
+    if hasattr(wl, "gemm_ops") and "gate_up_swiglu_w8a8_gemm" in per_kernel:
+        g = per_kernel["gate_up_swiglu_w8a8_gemm"]
+        roofline["gemm_mfma_int8_TOPS"] = round(wl.gemm_ops / (g["us"] * 1e-6) / 1e12, 1)
+        roofline["gemm_mfma_frac_of_5000_TOPS"] = round(wl.gemm_ops / (g["us"] * 1e-6) / 5.0e15, 4)
+    return roofline
+
+
+def summary(wl, m: dict, cpu) -> dict:
+    st = m["step"]
+    out = {"workload": wl.description, **wl.config(),
+           "us_per_step": round(st["median"] * 1e3, 3), "us_p10": round(st["p10"] * 1e3, 3),
+           "us_p90": round(st["p90"] * 1e3, 3), "us_min": round(st["min"] * 1e3, 3), "replays": st["replays"],
+           "algorithmic_bytes_per_step": wl.step_bytes, "GB/s": round(m["value"], 1),
+           "frac_hbm": round(m["value"] / HBM_PEAK_GBS, 4), "tokens_per_s": round(m["tokens_per_s"], 1),
+           "dtype": wl.dtype,
+           "per_kernel": {k: _round(v) for k, v in m["per_kernel"].items()}}
+    if cpu is not None:
+        out["cpu_baseline"] = _round(cpu)
+    return out
+
+
+def free(torch, wl) -> None:
+    import gc
+
+    del wl
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c5", choices=sorted(WORKLOADS),
+                    help="the headline workload (value, roofline, cpu_baseline)")
+    ap.add_argument("--configs", default=DEFAULT_CONFIGS,
+                    help="comma-separated workloads also measured in this run, each reported under "
+                         "'configs' with its own CPU baseline ('none' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU sample of the headline workload")
+    ap.add_argument("--config-cpu-seconds", type=float, default=4.0, help="CPU sample of each other config")
     ap.add_argument("--eager", action="store_true", help="launch from the host instead of graph replay")
     ap.add_argument("--profile-kernel", metavar="NAME",
                     help="for counter runs under rocprofv3: launch only this kernel of the workload "
@@ -1031,124 +1256,74 @@ def main() -> int:
         return 1
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    K, W = args.steps, args.warmup
+    Workload.steps_hint = K
 
     if args.profile_kernel == "copy":
-        return profile_copy(torch, dev, args.steps)
+        return profile_copy(torch, dev, K)
     wl = WORKLOADS[args.workload](dev, torch)
     torch.cuda.synchronize()
     if args.profile_kernel:
-        return profile_kernel(torch, wl, args.profile_kernel, args.steps)
+        return profile_kernel(torch, wl, args.profile_kernel, K)
     use_graph = not args.eager
-    K, W = args.steps, args.warmup
     print(f"[bench] workload {wl.name}: {len(wl.kernels)} kernels, warmup {W}, steps {K}, "
-          f"{'graph replay' if use_graph else 'eager'}", file=sys.stderr, flush=True)
+          f"{replays_for(K)} replays, {'graph replay' if use_graph else 'eager'}", file=sys.stderr, flush=True)
 
-    # warmup (eager, then the timed region replays a graph of K steps)
-    for i in range(W):
-        wl.step(i)
-    torch.cuda.synchronize()
-
-    reps = 3
-    if use_graph:
-        try:
-            ms_step = time_replay(torch, wl.step, K, True, reps)
-        except Exception as ex:  # capture unsupported: fall back to eager timing
-            print(f"[bench] graph capture failed ({ex}); timing eagerly", file=sys.stderr)
-            use_graph = False
-    if not use_graph:
-        ms_step = time_replay(torch, wl.step, K, False, reps)
-    print(f"[bench] step {ms_step * 1e3:.2f} us", file=sys.stderr, flush=True)
-
-    per_kernel = {}
-    for kname, spec in wl.kernels.items():
-        launch, nbytes = spec[0], spec[1]
-        ms = time_replay(torch, launch, K, use_graph, reps)
-        per_kernel[kname] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / (ms * 1e-3) / 1e9,
-                             "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
-        if len(spec) > 2:
-            per_kernel[kname]["flops"] = spec[2]
-            per_kernel[kname]["TFLOP/s"] = spec[2] / (ms * 1e-3) / 1e12
-        print(f"[bench] {kname}: {ms * 1e3:.2f} us, {per_kernel[kname]['GB/s']:.0f} GB/s",
-              file=sys.stderr, flush=True)
-
-    value = wl.step_bytes / (ms_step * 1e-3) / 1e9
-    tokens_per_s = wl.tokens_per_step / (ms_step * 1e-3)
-
-    # dominant kernel = the one moving the most algorithmic bytes per step (a
-    # fixed choice per workload; by time the small c2 kernels tie within noise)
-    dom_name = max(per_kernel, key=lambda k: per_kernel[k]["bytes"])
-    dom = per_kernel[dom_name]
-    traffic = None
-    tfile = ROOT / "profiles" / "traffic.json"
-    if tfile.exists():
-        try:
-            data = json.loads(tfile.read_text())
-            # a derived workload (c3_fused) runs its parent's kernels at the same shapes
-            for name in [getattr(c, "name", "") for c in type(wl).__mro__]:
-                entry = data.get(name, {}).get(dom_name)
-                if entry:
-                    traffic = entry["hbm_bytes_per_launch"]
-                    break
-        except (ValueError, OSError, KeyError, TypeError):
-            traffic = None
-    mfma_peak = getattr(wl, "mfma_peak_tflops", FP32_PEAK_TFLOPS)
-    if "flops" in dom and dom["flops"] / dom["bytes"] > mfma_peak * 1e12 / (HBM_PEAK_GBS * 1e9):
-        # compute-bound (arithmetic intensity above the matrix-core ridge)
-        roofline = {"bound": "mfma", "kernel": dom_name, "achieved": round(dom["TFLOP/s"], 2),
-                    "peak": round(mfma_peak, 1), "unit": "TFLOP/s",
-                    "frac": round(dom["TFLOP/s"] / mfma_peak, 4), "traffic": traffic,
-                    "avg_us": round(dom["us"], 3), "algorithmic_flops": dom["flops"],
-                    "algorithmic_bytes": dom["bytes"],
-                    "peak_basis": getattr(wl, "mfma_peak_basis", "fp32 MFMA, 157.3 TFLOP/s dense")}
-    else:
-        roofline = {"bound": "hbm", "kernel": dom_name, "achieved": round(dom["GB/s"], 1),
-                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["frac_hbm"], 4),
-                    "traffic": traffic, "avg_us": round(dom["us"], 3),
-                    "algorithmic_bytes": dom["bytes"]}
-    if roofline["bound"] == "hbm" and use_graph:
-        # context for frac: a device copy moving the same bytes (half read, half
-        # written) over rotating buffers, timed the same way
-        n_f = max(1, dom["bytes"] // 8)
-        n_sets = sets_for(dom["bytes"])
-        src = [torch.randn(n_f, device=dev) for _ in range(n_sets)]
-        dst = [torch.empty(n_f, device=dev) for _ in range(n_sets)]
-        c_ms = time_replay(torch, lambda i: dst[i % n_sets].copy_(src[i % n_sets]), K, True, reps=3)
-        roofline["copy_same_bytes"] = {"us": round(c_ms * 1e3, 3),
-                                       "GB/s": round(8 * n_f / (c_ms * 1e-3) / 1e9, 1),
-                                       "frac": round(8 * n_f / (c_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        del src, dst
-    if wl.name == "c5":
-        g = per_kernel["gate_up_swiglu_w8a8_gemm"]
-        roofline["gemm_mfma_int8_TOPS"] = round(wl.gemm_ops / (g["us"] * 1e-6) / 1e12, 1)
-        roofline["gemm_mfma_frac_of_5000_TOPS"] = round(wl.gemm_ops / (g["us"] * 1e-6) / 5.0e15, 4)
-
+    m = measure(torch, dev, wl, K, W, use_graph)
+    roofline = roofline_of(torch, dev, wl, m, K)
     cpu = None
     if not args.no_cpu_baseline:
-        print(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s sample)...", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(wl.name, args.cpu_seconds, wl.step_bytes)
-
+        print(f"[bench] cpu baseline {wl.name} ({args.cpu_seconds:.0f} s sample)...", file=sys.stderr, flush=True)
+        cpu = _round(cpu_baseline(wl.name, args.cpu_seconds, wl.step_bytes))
+    head = summary(wl, m, None)
+    st = m["step"]
     out = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": round(m["value"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": W,
-        "ms_per_step": round(ms_step, 6),
+        "ms_per_step": round(st["median"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": wl.dtype,
         "data": "synthetic (seeded torch.randn inputs, random-init weights; no checkpoints)",
         "config": {"workload": wl.description, **wl.config(),
-                   "timing": "hipGraph replay of K steps, HIP events" if use_graph else "eager launches, HIP events"},
-        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "tokens_per_s": round(tokens_per_s, 1),
-        "per_kernel": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                       for k, v in per_kernel.items()},
+                   "timing": (f"median over {st['replays']} replays of a hipGraph of K steps, HIP events"
+                              if m["use_graph"] else f"median over {st['replays']} eager runs of K steps")},
+        "ms_per_step_p10": round(st["p10"], 6),
+        "ms_per_step_p90": round(st["p90"], 6),
+        "ms_per_step_min": round(st["min"], 6),
+        "pct_hbm_peak": round(100 * m["value"] / HBM_PEAK_GBS, 2),
+        "tokens_per_s": round(m["tokens_per_s"], 1),
+        "per_kernel": head["per_kernel"],
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
+    free(torch, wl)
+
+    configs = {}
+    names = [c for c in args.configs.split(",") if c and c != "none" and c != args.workload]
+    for name in names:
+        if name not in WORKLOADS:
+            print(f"bench.py: unknown config {name!r}", file=sys.stderr)
+            return 2
+        cw = WORKLOADS[name](dev, torch)
+        torch.cuda.synchronize()
+        cm = measure(torch, dev, cw, K, W, use_graph)
+        ccpu = None
+        if not args.no_cpu_baseline:
+            print(f"[bench] cpu baseline {name} ({args.config_cpu_seconds:.0f} s sample)...", file=sys.stderr,
+                  flush=True)
+            ccpu = cpu_baseline(name, args.config_cpu_seconds, cw.step_bytes)
+        configs[name] = summary(cw, cm, ccpu)
+        free(torch, cw)
+    if configs:
+        out["configs"] = configs
+    if "decode_step" in configs:
+        out["decode_tokens_per_s"] = configs["decode_step"]["tokens_per_s"]
     print(json.dumps(out), flush=True)
     return 0
 

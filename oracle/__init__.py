@@ -49,9 +49,23 @@ _SIGS = {
     "ref_gate_up_swiglu_w8a8": [_P, _P, _P, _P, _P, _P, _Z, _Z, _Z],
     "ref_argmax_rows": [_P, _P, _Z, _Z],
     "ref_causal_attention": [_P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _F, _Z],
+    "ref_decode_chain_repeat": [_Z, _Z, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                _Z, _Z, _Z, _Z, _Z, _F],
 }
 
 _LIB = None
+_LIB_KIND = "x86-64-v3"
+
+
+def _load(path: Path) -> ctypes.CDLL:
+    so = ctypes.CDLL(str(path))
+    for name, args in _SIGS.items():
+        fn = getattr(so, name)
+        fn.argtypes = args
+        fn.restype = None
+    so.ref_fast_exp.argtypes = [_F]
+    so.ref_fast_exp.restype = _F
+    return so
 
 
 def lib() -> ctypes.CDLL:
@@ -61,15 +75,24 @@ def lib() -> ctypes.CDLL:
             from . import build as _build
 
             _build.build()
-        so = ctypes.CDLL(str(SO))
-        for name, args in _SIGS.items():
-            fn = getattr(so, name)
-            fn.argtypes = args
-            fn.restype = None
-        so.ref_fast_exp.argtypes = [_F]
-        so.ref_fast_exp.restype = _F
-        _LIB = so
+        _LIB = _load(SO)
     return _LIB
+
+
+def use_native() -> str:
+    """For the timed CPU baseline only: compile the oracle with -march=native
+    on this host and route every wrapper through that copy. Returns the build
+    used ("native", or "x86-64-v3" with the reason the native build failed)."""
+    global _LIB, _LIB_KIND
+    from . import build as _build
+
+    try:
+        _LIB = _load(_build.build(native=True))
+        _LIB_KIND = "native"
+    except (RuntimeError, OSError) as ex:
+        _LIB_KIND = f"x86-64-v3 (native build failed: {ex})"
+        lib()
+    return _LIB_KIND
 
 
 def _p(a: np.ndarray | None) -> c_void_p:

@@ -671,3 +671,27 @@ ORACLE_API void ref_causal_attention(float* out, const float* q, const float* k,
     }
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* CPU-baseline driver (timing only): the batch-1 decode chain of one layer   */
+/* -- add_inplace + rms_norm (decoder.rs:908+910), the q/k head norms + RoPE   */
+/* at one position (decoder.rs:888-892), the decode loop's SwiGLU             */
+/* (decoder.rs:916-921) -- repeated `iters` times over `sets` rotating input  */
+/* sets, so a microsecond-scale chain is timed without a per-call foreign     */
+/* function overhead. Set s uses x + s*hidden, q + s*nq*hd, etc.              */
+/* ------------------------------------------------------------------------ */
+ORACLE_API void ref_decode_chain_repeat(size_t iters, size_t sets, float* x, const float* delta,
+                                        const float* w, float* out, float* q, float* k,
+                                        const float* qw, const float* kw, const float* cos_tab,
+                                        const float* sin_tab, const int32_t* positions,
+                                        float* act, const float* gate, const float* up,
+                                        size_t hidden, size_t n_heads, size_t n_kv_heads,
+                                        size_t head_dim, size_t inter, float eps) {
+  for (size_t i = 0; i < iters; ++i) {
+    const size_t s = i % sets;
+    ref_add_rms_norm(x + s * hidden, delta + s * hidden, w, out + s * hidden, 1, hidden, eps);
+    ref_head_rms_norm_rope(q + s * n_heads * head_dim, k + s * n_kv_heads * head_dim, qw, kw,
+                           cos_tab, sin_tab, positions + s, 1, n_heads, n_kv_heads, head_dim, eps);
+    ref_swiglu_split(act + s * inter, gate + s * inter, up + s * inter, inter);
+  }
+}

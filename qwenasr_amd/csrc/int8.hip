@@ -1079,8 +1079,10 @@ bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, h
 // MFMA); otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
 // 32 x 32 that fills the chip (measured at T = 512: o [1024, 2048] 20.0 ->
 // 16.7 us, down [1024, 3072] 27.4 -> 20.9 us against the LDS-staged 64 x 32).
+// Returns false when the chosen kernel cannot run the shape (K not a multiple
+// of its K step, or its LDS size refused): nothing was launched.
 template <int EPI>
-void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st) {
+bool launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st) {
   auto cols = [&](int bn) {
     unsigned c = 0;
     for (int m = 0; m < set.n; ++m) {
@@ -1092,20 +1094,11 @@ void launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
   };
   const long long rows64 = (T + 63) / 64, rows32 = (T + 31) / 32;
   unsigned c = cols(128);
-  if (c * rows64 >= 256) {
-    try_gemm<128, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
-    return;
-  }
+  if (c * rows64 >= 256) return try_gemm<128, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
   c = cols(64);
-  if (c * rows64 >= 256) {
-    try_gemm_ksplit<64, 64, 4, EPI>(set, c, x, T, K, st);
-    return;
-  }
-  if (c * rows32 >= 256) {
-    try_gemm_ksplit<64, 32, 4, EPI>(set, c, x, T, K, st);
-    return;
-  }
-  try_gemm_ksplit<32, 32, 4, EPI>(set, cols(32), x, T, K, st);
+  if (c * rows64 >= 256) return try_gemm_ksplit<64, 64, 4, EPI>(set, c, x, T, K, st);
+  if (c * rows32 >= 256) return try_gemm_ksplit<64, 32, 4, EPI>(set, c, x, T, K, st);
+  return try_gemm_ksplit<32, 32, 4, EPI>(set, cols(32), x, T, K, st);
 }
 
 }  // namespace
@@ -1169,10 +1162,9 @@ static int launch_w8a32(float* y, const float* x, const int8_t* w, const float* 
     set.b[0] = bias;
     set.N[0] = o;
     set.n = 1;
-    if (bias)
-      launch_w8a32_gemm<kGemmBias>(set, x, s, k, st);
-    else
-      launch_w8a32_gemm<kGemmRows>(set, x, s, k, st);
+    const bool ran = bias ? launch_w8a32_gemm<kGemmBias>(set, x, s, k, st)
+                          : launch_w8a32_gemm<kGemmRows>(set, x, s, k, st);
+    if (!ran) return fail(QASR_ERR_UNSUPPORTED, "linear_int8: the GEMM kernel cannot run this shape");
   } else if (vec) {
     switch (in_dim / 1024) {
       case 1: w8a32_vec_kernel<1><<<grid, 256, 0, st>>>(y, x, w, scales, bias, s, k, o); break;
@@ -1260,7 +1252,8 @@ extern "C" int qasr_gate_up_swiglu_multiply_int8_f32(float* out, const float* x,
     set.b[0] = nullptr;
     set.N[0] = (int)(2 * intermediate);
     set.n = 1;
-    launch_w8a32_gemm<kGemmSwiglu>(set, x, (int)seq_len, (int)in_dim, st);
+    if (!launch_w8a32_gemm<kGemmSwiglu>(set, x, (int)seq_len, (int)in_dim, st))
+      return fail(QASR_ERR_UNSUPPORTED, "gate_up_swiglu_multiply_int8: the GEMM kernel cannot run this shape");
   } else {
     const long long items = (long long)seq_len * (long long)intermediate;
     gate_up_swiglu_w8a32_pairs_kernel<true><<<(unsigned)((items + 3) / 4), 256, 0, st>>>(
@@ -1304,7 +1297,8 @@ extern "C" int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys
       set.N[m] = (int)out_dims[m];
     }
     set.n = (int)n_mats;
-    launch_w8a32_gemm<kGemmRows>(set, x, (int)seq_len, (int)in_dim, as_stream(stream));
+    if (!launch_w8a32_gemm<kGemmRows>(set, x, (int)seq_len, (int)in_dim, as_stream(stream)))
+      return fail(QASR_ERR_UNSUPPORTED, "linear_nobias_int8_multi: the GEMM kernel cannot run this shape");
     return launch_status("linear_nobias_int8_multi");
   }
   if (!one_launch) {

@@ -92,18 +92,32 @@ class DecoderInt8:
         self.pffn = torch.empty(T * H, **f32)
         self._pcap = T
 
-    def prepare_prefill(self, start_pos: int, T: int) -> None:
+    def _check_pos(self, pos: int | None, what: str) -> int:
+        """The reference takes the position from the cache length
+        (decoder.rs:771, 866): a position other than ``kv.len`` would leave rows
+        the cache does not count (a later growth copies ``kv.len`` rows only)."""
+        if pos is None:
+            return self.kv.len
+        if pos != self.kv.len:
+            raise ValueError(f"{what}: position {pos} != cache length {self.kv.len} "
+                             "(set kv.len for an externally filled cache)")
+        return pos
+
+    def prepare_prefill(self, start_pos: int | None, T: int) -> None:
         """Host-side growth before a prefill of T tokens at start_pos
-        (decoder.rs:770-781): cache capacity, RoPE rows, the chunk's buffers."""
+        (decoder.rs:770-781): cache capacity, RoPE rows, the chunk's buffers.
+        ``start_pos`` must equal the cache length (None: take it from there)."""
+        start_pos = self._check_pos(start_pos, "prepare_prefill")
         if start_pos + T > self.kv.max_seq:
             self.kv.grow(start_pos + T + 1024)
         self.rope.ensure(start_pos + T, self.hd, self.theta)
         self._ensure_prefill(T)
 
-    def prefill(self, embeds: torch.Tensor, T: int, start_pos: int) -> None:
+    def prefill(self, embeds: torch.Tensor, T: int, start_pos: int | None = None) -> None:
         """T tokens at positions start_pos.. (decoder.rs:751-847): writes cache rows
         start_pos..start_pos+T-1 of every layer; ``self.px[:T*H]`` receives the
         residual stream after the last layer. Call ``prepare_prefill`` first."""
+        start_pos = self._check_pos(start_pos, "prefill")
         H, I, nq, nk, hd, eps = self.H, self.I, self.nq, self.nk, self.hd, self.eps
         q_dim = nq * hd
         total = start_pos + T
@@ -129,17 +143,20 @@ class DecoderInt8:
         K.add_inplace(x, self.pffn, T * H)
         self.kv.len = total
 
-    def prepare(self, pos: int) -> None:
+    def prepare(self, pos: int | None = None) -> None:
         """Host-side growth before a decode at ``pos`` (decoder.rs:866-872):
-        cache capacity and RoPE rows. Nothing here runs in the timed step."""
+        cache capacity and RoPE rows. Nothing here runs in the timed step.
+        ``pos`` must equal the cache length (None: take it from there)."""
+        pos = self._check_pos(pos, "prepare")
         if pos >= self.kv.max_seq:
             self.kv.grow(pos + 1024)
         self.rope.ensure(pos + 1, self.hd, self.theta)
 
-    def decode(self, embed: torch.Tensor, pos: int) -> None:
+    def decode(self, embed: torch.Tensor, pos: int | None = None) -> None:
         """One token at position ``pos`` (the cache holds rows 0..pos-1):
         ``self.token`` receives the greedy next token, ``self.x_norm`` the final
         normed hidden state. Call ``prepare(pos)`` first."""
+        pos = self._check_pos(pos, "decode")
         if self.fuse_norms:
             self._decode_fused(embed, pos)
             return
@@ -192,6 +209,7 @@ class DecoderInt8:
         K.add_rms_norm(h, self.down, self.w["norm"], self.x_norm, 1, H, eps)
         K.lm_head_int8_argmax(self.token, self.logits, self.x_norm, self.lm, 1, H, self.vocab, self.lm_ws)
 
-    def finish(self, pos: int) -> None:
+    def finish(self, pos: int | None = None) -> None:
         """The cache now holds rows 0..pos (decoder.rs:926)."""
+        pos = self._check_pos(pos, "finish")
         self.kv.len = pos + 1

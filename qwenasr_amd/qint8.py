@@ -25,6 +25,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
+from . import kernels as K
 from .kernels import QuantWeight
 
 INT8, F32, BF16 = 0, 1, 2
@@ -134,6 +135,10 @@ class QuantFile:
                   ctypes.c_void_p(scales.data_ptr() if scales is not None else 0), _stream_ptr())
 
     def get_quant_weight(self, name: str, device="cuda") -> QuantWeight | None:
+        """Device copy of an INT8 entry (quantize.rs:259-273). The reference
+        returns a view for any dtype, reading an F32/BF16 entry's bytes as int8
+        with a scale pointer at offset 0; this mirror raises ``ValueError`` for
+        those entries instead of uploading bytes that are not int8 weights."""
         m = self.find(name)
         if m is None:
             return None
@@ -155,7 +160,10 @@ class QuantFile:
         return out
 
     def get_f32(self, name: str, device="cuda") -> torch.Tensor | None:
-        """F32 entries as stored; BF16 entries widened to f32 (exact)."""
+        """quantize.rs:276-306: F32 entries as stored; BF16 entries widened to
+        f32 (exact); INT8 entries dequantized, ``f32[o, k] = int8[o, k] * scale[o]``
+        (one f32 multiply per element, done by the int8 row-gather kernel over
+        every row, which is exactly that product)."""
         m = self.find(name)
         if m is None:
             return None
@@ -165,7 +173,12 @@ class QuantFile:
             return out
         if m.dtype == BF16:
             return self.get_bf16_direct(name, device).float()
-        raise ValueError(f"{name}: INT8 entries are read with get_quant_weight")
+        w = self.get_quant_weight(name, device)
+        out = torch.empty((w.out_dim, w.in_dim), dtype=torch.float32, device=device)
+        if w.out_dim and w.in_dim:
+            rows = torch.arange(w.out_dim, dtype=torch.int32, device=device)
+            K.embed_gather_i8(out, w, rows, w.out_dim, w.in_dim)
+        return out.reshape(m.shape)
 
     def fused_gate_up(self, gate_name: str, up_name: str, inter: int, hidden: int,
                       device="cuda") -> QuantWeight:

@@ -84,6 +84,66 @@ def test_decode_steps_match_the_oracle(tmp_path, dev, H, I, vocab):
             assert got == tok, (pos, got, tok)
 
 
+def test_fused_decode_at_split_positions_matches_the_oracle(tmp_path, dev):
+    """The timed decode path (fuse_norms=True: norms folded into the
+    projections, q/k norm + RoPE + cache store folded into split attention)
+    against the oracle at positions 300-302, where the keys are split over
+    workgroups: the final hidden state, the logits, the new K/V rows of every
+    layer and the token, over a cache whose rows 0..299 are the same random
+    earlier context on both sides."""
+    from qwenasr_amd.decoder import DecoderInt8
+
+    H, I, L, nq, nk, hd, vocab = 2048, 6144, 2, 16, 8, 128, 1000
+    r = np.random.default_rng([38, H])
+    w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
+    dec = DecoderInt8(_load(tmp_path, w, L, dev), H, I, L, nq, nk, hd, max_seq=512, device=dev)
+    assert dec.fuse_norms
+    kv, start = nk * hd, 300
+    kc = np.zeros((L, 512, kv), np.float32)
+    vc = np.zeros_like(kc)
+    kc[:, :start] = r.standard_normal((L, start, kv)).astype(np.float32)
+    vc[:, :start] = r.standard_normal((L, start, kv)).astype(np.float32)
+    for l in range(L):
+        dec.kv.k_layer_block(l).view(dec.kv.max_seq, kv)[:start] = torch.from_numpy(kc[l, :start]).to(dev)
+        dec.kv.v_layer_block(l).view(dec.kv.max_seq, kv)[:start] = torch.from_numpy(vc[l, :start]).to(dev)
+    dec.kv.len = start
+    for pos in (start, start + 1, start + 2):
+        x = r.standard_normal(H).astype(np.float32)
+        tok, xn, logits = decode_int8_step(w, kc, vc, pos, x, nq, nk, hd, threads=8)
+        dec.prepare()
+        dec.decode(torch.from_numpy(x).to(dev))
+        dec.finish()
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(dec.x_norm.cpu().numpy(), xn, rtol=TOL, atol=TOL, err_msg=f"pos {pos}")
+        np.testing.assert_allclose(dec.logits.cpu().numpy(), logits, rtol=TOL, atol=TOL, err_msg=f"pos {pos}")
+        for l in range(L):
+            np.testing.assert_allclose(dec.kv.k_layer(l).cpu().numpy().reshape(pos + 1, kv)[pos], kc[l, pos],
+                                       rtol=TOL, atol=TOL, err_msg=f"k row {pos} layer {l}")
+            np.testing.assert_allclose(dec.kv.v_layer(l).cpu().numpy().reshape(pos + 1, kv)[pos], vc[l, pos],
+                                       rtol=TOL, atol=TOL, err_msg=f"v row {pos} layer {l}")
+        top2 = np.sort(logits)[-2:]
+        if top2[1] - top2[0] > 2 * TOL * (1 + abs(top2[1])):
+            assert int(dec.token.cpu()[0]) == tok, pos
+
+
+def test_decoder_position_must_be_the_cache_length(tmp_path, dev):
+    """decoder.rs:771, 866 take the position from the cache length; the device
+    decoder refuses any other (a later growth would drop the rows between)."""
+    from qwenasr_amd.decoder import DecoderInt8
+
+    H, I, L, nq, nk, hd, vocab = 1024, 3072, 1, 16, 8, 128, 100
+    w = small_decoder(np.random.default_rng(39), H, I, L, nq, nk, hd, vocab)
+    dec = DecoderInt8(_load(tmp_path, w, L, dev), H, I, L, nq, nk, hd, max_seq=8, device=dev)
+    with pytest.raises(ValueError):
+        dec.prepare(3)
+    with pytest.raises(ValueError):
+        dec.prepare_prefill(2, 4)
+    with pytest.raises(ValueError):
+        dec.finish(1)
+    dec.prepare()  # position 0, from the cache length
+    assert dec.kv.len == 0
+
+
 def test_gate_up_swiglu_int8_matches_linear_plus_loop(dev):
     """The fused gate/up + SwiGLU entry against linear_nobias_int8 + the
     decode loop's SwiGLU on the oracle, one token (fused epilogue) and several
@@ -133,6 +193,7 @@ def test_fused_norm_decode_equals_unfused(tmp_path, dev):
     for pos in (0, 1, 300, 301, 302):
         x = torch.from_numpy(r.standard_normal(H).astype(np.float32)).to(dev)
         for d in decs:
+            d.kv.len = pos  # rows 2..299 stand for an earlier context
             d.prepare(pos)
             d.decode(x, pos)
             d.finish(pos)
@@ -280,6 +341,7 @@ def test_graph_replays_equal_the_eager_calls(tmp_path, dev):
         d = DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=512, device=dev, fuse_norms=fuse)
         d.kv.k.normal_(generator=gen)
         d.kv.v.normal_(generator=gen)
+        d.kv.len = pos
         d.prepare(pos)
         x = torch.randn(H, device=dev, generator=gen)
         check(d, lambda: d.decode(x, pos), ("x_norm", "logits", "token"), pos,
@@ -289,4 +351,9 @@ def test_graph_replays_equal_the_eager_calls(tmp_path, dev):
     d = DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=512, device=dev)
     d.prepare_prefill(0, T)
     e = torch.randn(T * H, device=dev, generator=gen)
-    check(d, lambda: d.prefill(e, T, 0), ("px",), slice(0, T), "prefill")
+
+    def prefill_at_0():
+        d.kv.len = 0  # every call (and replay) prefills the same chunk at position 0
+        d.prefill(e, T, 0)
+
+    check(d, prefill_at_0, ("px",), slice(0, T), "prefill")

@@ -257,6 +257,81 @@ def test_w8a32_is_exact_on_integer_inputs(golden):
     np.testing.assert_array_equal(y.astype(np.int64), golden["w8a8_dots"].astype(np.int64))
 
 
+def test_linear_int8_bias_after_row_scale():
+    # kernels/mod.rs:664-673: y = scale[o] * (W_int8 @ x)[o], then += bias[o]
+    # for every token. Checked against float64; scales far from 1 and a bias of
+    # the outputs' size make "bias before the scale", a dropped bias and a bias
+    # indexed by token instead of output row each fail.
+    r = np.random.default_rng(23)
+    T, K, O = 3, 96, 40
+    w = r.integers(-127, 128, (O, K), dtype=np.int8)
+    s = (2e-3 + 2e-2 * r.random(O)).astype(np.float32)
+    b = r.standard_normal(O).astype(np.float32)
+    x = r.standard_normal((T, K)).astype(np.float32)
+    y = oracle.linear_int8(x, w, s, b, T, K, O).reshape(T, O)
+    ref = (x.astype(np.float64) @ w.astype(np.float64).T) * s.astype(np.float64) + b.astype(np.float64)
+    assert_close(y, ref, 1e-5, 1e-6, "linear_int8")
+    wrong = ((x.astype(np.float64) @ w.astype(np.float64).T) + b) * s
+    assert np.abs(y - wrong).max() > 1e-2  # the check separates the two orders
+    # no bias: identical to linear_nobias_int8
+    np.testing.assert_array_equal(oracle.linear_int8(x, w, s, None, T, K, O),
+                                  oracle.linear_nobias_int8(x, w, s, T, K, O))
+
+
+def test_linear_int8_bias_exact_on_integer_inputs():
+    # integer x, power-of-two scales and integer biases: every step is exact in
+    # f32 (dots < 2^24), so the result is the exact integer expression
+    r = np.random.default_rng(24)
+    T, K, O = 4, 64, 24
+    w = r.integers(-127, 128, (O, K), dtype=np.int8)
+    x = r.integers(-50, 51, (T, K)).astype(np.float32)
+    s = np.array([2.0 ** -int(e) for e in r.integers(0, 4, O)], np.float32)
+    b = r.integers(-1000, 1001, O).astype(np.float32)
+    y = oracle.linear_int8(x, w, s, b, T, K, O, n_threads=3).reshape(T, O)
+    dots = x.astype(np.int64) @ w.astype(np.int64).T
+    np.testing.assert_array_equal(y.astype(np.float64), dots * s.astype(np.float64) + b)
+
+
+def _encoder_chunk_rows(mel_frames, chunk_size=100):
+    """Rows each mel chunk contributes after the conv stem (encoder.rs:252-274):
+    three 3-wide, stride-2, pad-1 convolutions over the chunk's frames."""
+    conv = lambda w: (w + 2 - 3) // 2 + 1  # noqa: E731
+    return [conv(conv(conv(min(chunk_size, mel_frames - s)))) for s in range(0, mel_frames, chunk_size)]
+
+
+@pytest.mark.parametrize("mel_frames,d", [(537, 64), (1000, 896), (100, 32), (41, 16)])
+def test_pe_add_restarts_per_chunk(mel_frames, d):
+    # encoder.rs:340-343 builds a fresh sinusoidal_pe(w3, d) for each chunk's w3
+    # rows and adds it, so the position restarts at 0 for every chunk; a full
+    # 100-frame chunk gives 13 rows and the last chunk may be shorter. The
+    # expected sum is built chunk by chunk from that rule (f32 + f32 in float64,
+    # rounded once: the f32 sum), independent of the oracle's r mod n_pos.
+    rows = _encoder_chunk_rows(mel_frames)
+    assert all(n == 13 for n in rows[:-1]) and 1 <= rows[-1] <= 13
+    T = sum(rows)
+    r = np.random.default_rng(mel_frames)
+    x = r.standard_normal((T, d)).astype(np.float32)
+    table = r.standard_normal((13, d)).astype(np.float32)  # any 13-row table
+    exp = np.empty_like(x)
+    off = 0
+    for n in rows:
+        exp[off:off + n] = (x[off:off + n].astype(np.float64) + table[:n]).astype(np.float32)
+        off += n
+    got = oracle.pe_add(x.ravel(), table.ravel(), T, d, 13).reshape(T, d)
+    np.testing.assert_array_equal(got, exp)
+    # and with the sinusoidal table itself, each row is x + PE(row within its
+    # chunk) to float64 closed-form accuracy; positions that continue across
+    # chunks (PE(13), PE(14), ...) would fail here
+    pe = oracle.sinusoidal_pe(13, d).reshape(13, d)
+    half = d // 2
+    lts = np.log(10000.0) / (half - 1)
+    inv = np.exp(-np.arange(half) * lts)
+    p = np.concatenate([np.arange(n) for n in rows]).astype(np.float64)[:, None]
+    pe64 = np.concatenate([np.sin(p * inv), np.cos(p * inv)], axis=1)
+    got = oracle.pe_add(x.ravel(), pe.ravel(), T, d, 13).reshape(T, d)
+    assert_close(got, x.astype(np.float64) + pe64, 2e-7, 1e-6, "pe_add closed form")
+
+
 def test_interleave_layout():
     r = np.random.default_rng(5)
     inter, hid = 6, 32

@@ -295,6 +295,13 @@ def test_uploads_are_bit_exact(tmp_path, dev):
             assert (w.out_dim, w.in_dim) == tuple(shape)
             assert np.array_equal(w.data.cpu().numpy(), qd)
             assert w.scales.cpu().numpy().tobytes() == sc.tobytes()
+            # get_f32 dequantizes INT8 as quantize.rs:292-303 does: int8 * row scale
+            deq = qf.get_f32(name, dev).cpu().numpy()
+            want = (qd.reshape(len(sc), -1).astype(np.float32) * sc[:, None]).reshape(shape)
+            assert deq.shape == tuple(shape) and deq.tobytes() == want.tobytes()
+        for name, shape, arr in f32 + bf16:
+            with pytest.raises(ValueError):  # not an INT8 entry
+                qf.get_quant_weight(name, dev)
         for name, shape, arr in f32:
             assert qf.get_f32(name, dev).cpu().numpy().tobytes() == arr.tobytes()
         for name, shape, arr in bf16:
