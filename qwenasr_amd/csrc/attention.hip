@@ -265,9 +265,11 @@ QASR_DEV void merge_splits(float* o, const float* ws_o, const float* ml, int nsp
 // walks whole 64-key tiles; wave w owns keys 16w .. 16w+15 of each tile, so
 // every SIMD of the CU has its own loads in flight. Each wave issues all k and
 // v loads of its 16 keys before using any (one memory round trip per tile).
-// QK: a quad of lanes owns a key (lane l covers head dims 32*(l%4) .. +31 of
-// key l/4), so each load instruction reads 16 keys x 64 contiguous bytes and
-// the quad's partial dots meet with two DPP adds. PV: lanes over head dims,
+// QK: a quad of lanes owns a key; load instruction c gives lane l the head
+// dims 16c + 4(l%4) .. +3 of key l/4, so the quad reads 64 contiguous bytes
+// of its key row (the 16 keys of an instruction touch 16 cache lines, each
+// line completed by the next instruction), and the quad's partial dots meet
+// with two DPP adds. PV: lanes over head dims,
 // probabilities broadcast with readlane. The 4 waves' (max, sum, out) merge in
 // LDS; the workgroup writes its unnormalised partial to the workspace.
 // The decode step's q/k head RMSNorm + RoPE and KV-cache store, done inside
@@ -322,9 +324,9 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
   auto load_tile = [&](int t0, float4 (&kk)[C4], float (&vv)[16][DPL]) {
     const int nkeys = min(16, k_end - t0);
     const int j = min(kq, nkeys - 1);
-    const float* kr = k + (size_t)(t0 + j) * kv_stride + (size_t)kh * HD + quarter * DQ;
+    const float* kr = k + (size_t)(t0 + j) * kv_stride + (size_t)kh * HD + 4 * quarter;
 #pragma unroll
-    for (int c = 0; c < C4; ++c) kk[c] = ld4(kr, c);
+    for (int c = 0; c < C4; ++c) kk[c] = ld4(kr, 4 * c);
     const float* vr = v + (size_t)t0 * kv_stride + (size_t)kh * HD + lane * DPL;
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
@@ -392,7 +394,7 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
     const int nkeys = min(16, k_end - t);
     if (min(kq, nkeys - 1) == nkeys - 1) {
 #pragma unroll
-      for (int c = 0; c < C4; ++c) kk[c] = *reinterpret_cast<const float4*>(&kpos[quarter * DQ + 4 * c]);
+      for (int c = 0; c < C4; ++c) kk[c] = *reinterpret_cast<const float4*>(&kpos[16 * c + 4 * quarter]);
     }
 #pragma unroll
     for (int d = 0; d < DPL; ++d) vlast[d] = vpos[lane * DPL + d];
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int c = 0; c < C4; ++c) qv[g][c] = *reinterpret_cast<const float4*>(&qs[g][quarter * DQ + 4 * c]);
+      for (int c = 0; c < C4; ++c) qv[g][c] = *reinterpret_cast<const float4*>(&qs[g][16 * c + 4 * quarter]);
     if (first) {
       float vlast[DPL];
       const bool hit = patch(t0, kk0, vlast, kpos, vpos);
@@ -461,11 +463,11 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
       t0 += 64;
     }
   } else {
-    const float* qr = q + (size_t)i * q_stride + (size_t)kh * G * HD + quarter * DQ;
+    const float* qr = q + (size_t)i * q_stride + (size_t)kh * G * HD + 4 * quarter;
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int c = 0; c < C4; ++c) qv[g][c] = ld4(qr + g * HD, c);
+      for (int c = 0; c < C4; ++c) qv[g][c] = ld4(qr + g * HD, 4 * c);
   }
   for (; t0 < k_end; t0 += 64) {
     float4 kk[C4];
