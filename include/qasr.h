@@ -465,6 +465,24 @@ int qasr_lm_head_int8_argmax_f32(int32_t* idx, float* logits, const float* x,
 /* Workspace bytes qasr_lm_head_int8_argmax_f32 can use for this vocab. */
 size_t qasr_lm_head_argmax_workspace_bytes(size_t vocab);
 
+/* qasr_lm_head_int8_argmax_f32 without a workspace and without allocating:
+ * no counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * The one-row candidates go to a 512 KiB array the library holds on each GPU
+ * it runs on until the process ends (looked up once per device on the first
+ * call there; nothing is allocated, no call here allocates). Same results as
+ * qasr_lm_head_int8_argmax_f32 with a workspace. One row needs in_dim
+ * 1024..8192 in steps of 1024 and 16-byte aligned x and w (UNSUPPORTED
+ * otherwise); vocab at most QASR_LM_HEAD_NOALLOC_MAX_VOCAB (INVALID_ARG
+ * otherwise). rows > 1 writes the logits and scans them, as the workspace
+ * form does. All calls on one GPU share the array: calls that overlap in time
+ * on one GPU (two streams or threads) race; calls ordered on one stream do
+ * not. */
+#define QASR_LM_HEAD_NOALLOC_MAX_VOCAB 262144
+int qasr_lm_head_int8_argmax_noalloc_f32(int32_t* idx, float* logits, const float* x,
+                                         const int8_t* w, const float* scales, size_t rows,
+                                         size_t in_dim, size_t vocab, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* .qint8 weight files (quantize.rs:1-34, QuantFile quantize.rs:114-300)     */
 /* ------------------------------------------------------------------------ */

@@ -15,7 +15,9 @@
 // logits are written first and scanned by one workgroup per row.
 #include "common.hpp"
 
+#include <atomic>
 #include <climits>
+#include <mutex>
 
 namespace qasr {
 namespace {
@@ -166,4 +168,82 @@ extern "C" int qasr_lm_head_int8_argmax_f32(int32_t* idx, float* logits, const f
   const int rc = qasr_linear_nobias_int8_f32(logits, x, w, scales, rows, in_dim, vocab, stream);
   if (rc != QASR_OK) return rc;
   return qasr_argmax_rows_f32(idx, logits, rows, vocab, stream);
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant: the per-workgroup candidates live in a file-scope
+// device array instead of a caller workspace, for callers that cannot
+// allocate (code under HIP graph capture, serving loops that forbid
+// hipMalloc). Each GPU the library runs on holds its own copy of the array
+// (512 KiB) until the process ends. The array's address differs per device
+// and is only known to the runtime, so it is looked up once per device
+// (hipGetSymbolAddress with that device current) and the device pointer --
+// never the host-side name of the array -- is what the kernels receive.
+// Every workgroup writes its candidate before the merge reads it, so nothing
+// needs clearing between calls. Calls on one GPU share the array: calls that
+// overlap in time on one GPU (two streams, two threads) race.
+// ---------------------------------------------------------------------------
+namespace qasr {
+namespace {
+
+// one candidate per matvec workgroup, at most one per 4 vocabulary rows
+constexpr size_t kNoAllocPairs = QASR_LM_HEAD_NOALLOC_MAX_VOCAB / 4;
+static __device__ __align__(256) float2 scratch[kNoAllocPairs];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<float2*> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch`, looked up on its first use.
+int scratch_for_current_device(float2** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return fail(QASR_ERR_HIP, "lm_head_int8_argmax_noalloc: no current device (or more than 64)");
+  float2* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !addr)
+        return fail(QASR_ERR_HIP, std::string("lm_head_int8_argmax_noalloc: hipGetSymbolAddress: ") +
+                                      hipGetErrorString(e));
+      p = static_cast<float2*>(addr);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return QASR_OK;
+}
+
+}  // namespace
+}  // namespace qasr
+
+extern "C" int qasr_lm_head_int8_argmax_noalloc_f32(int32_t* idx, float* logits, const float* x,
+                                                    const int8_t* w, const float* scales, size_t rows,
+                                                    size_t in_dim, size_t vocab, void* stream) {
+  if (rows == 0) return QASR_OK;
+  QASR_REQUIRE(idx && logits && x && w && scales, "lm_head_int8_argmax_noalloc: null pointer");
+  QASR_REQUIRE(vocab > 0, "lm_head_int8_argmax_noalloc: vocab must be positive");
+  if (rows != 1) {  // several rows: logits then a scan, no scratch used
+    const int rc = qasr_linear_nobias_int8_f32(logits, x, w, scales, rows, in_dim, vocab, stream);
+    if (rc != QASR_OK) return rc;
+    return qasr_argmax_rows_f32(idx, logits, rows, vocab, stream);
+  }
+  QASR_REQUIRE(lm_head_partials_max(vocab) <= kNoAllocPairs,
+               "lm_head_int8_argmax_noalloc: vocab above QASR_LM_HEAD_NOALLOC_MAX_VOCAB (262144)");
+  float2* part = nullptr;
+  const int rc0 = scratch_for_current_device(&part);
+  if (rc0 != QASR_OK) return rc0;
+  hipStream_t st = as_stream(stream);
+  unsigned n_part = 0;
+  if (!launch_w8a32_argmax_partials(logits, x, w, scales, in_dim, vocab, part, kNoAllocPairs, st, &n_part))
+    return fail(QASR_ERR_UNSUPPORTED,
+                "lm_head_int8_argmax_noalloc: one row needs in_dim 1024..8192 in steps of 1024 and "
+                "16-byte aligned x and w");
+  const int rc = launch_status("lm_head_int8_argmax_noalloc");
+  if (rc != QASR_OK) return rc;
+  argmax_partials_kernel<<<1, kArgmaxBlock, 0, st>>>(idx, part, (int)n_part, logits);
+  return launch_status("lm_head_int8_argmax_noalloc");
 }
