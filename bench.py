@@ -414,6 +414,91 @@ class C5Share(C5BatchedDecode):
     unit_tokens = 32
 
 
+class C5Layer(Workload):
+    """The batched decode layer's projections at B=256 with their fused
+    neighbours (decoder.rs:878-895, 908-921 per stream, W8A8): residual add +
+    input RMSNorm + int8 quantization; the q/k/v projection with the q/k head
+    norms, RoPE at each stream's position and the K/V cache rows in its
+    epilogue; residual add + post-attention RMSNorm + quantization; gate/up +
+    SwiGLU. Attention, o and down are not in this chain."""
+    name = "c5_layer"
+    B = 256
+    description = ("qwen3-asr-1.7b batched decode layer projections, B=256 streams at positions U[0,2047]: "
+                   "add+RMSNorm+int8 quant [256,2048]; W8A8 q/k/v [256,2048]x[2048,4096] with q/k head "
+                   "RMSNorm + RoPE + K/V cache store in the epilogue; add+RMSNorm+quant; W8A8 gate/up "
+                   "[256,2048]x[2048,12288] + SwiGLU; 28 distinct layers of weights rotate")
+    unit_tokens = 256
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+
+        c = DEC_1_7B
+        B, L = self.B, 28
+        H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
+        N = (nq + 2 * nk) * hd
+        self.qkv, self.gu = [], []
+        for _ in range(L):
+            for rows, dst in ((N, self.qkv), (2 * I, self.gu)):
+                w = self.randn(rows * H, 0.02)
+                q, s = K.quantize_f32_to_int8(w, rows, H)
+                del w
+                dst.append(K.pack_w8a8_tiles(K.QuantWeight(q, s, rows, H)))
+                del q
+        S = L
+        self.x = [self.randn(B * H) for _ in range(S)]
+        self.d = [self.randn(B * H) for _ in range(S)]
+        self.d2 = [self.randn(B * H) for _ in range(S)]
+        self.xq = [torch.empty(B * H, dtype=torch.int8, device=dev) for _ in range(S)]
+        self.xsc = [torch.empty(B, device=dev) for _ in range(S)]
+        self.xq2 = [torch.empty(B * H, dtype=torch.int8, device=dev) for _ in range(S)]
+        self.xsc2 = [torch.empty(B, device=dev) for _ in range(S)]
+        self.q = [torch.empty(B * nq * hd, device=dev) for _ in range(S)]
+        self.o = [torch.empty(B * I, device=dev) for _ in range(S)]
+        self.rows = 2048
+        kv = nk * hd
+        # one layer's per-stream cache blocks [B, 2048, kv] (4 GiB for K and V)
+        self.kc = torch.zeros(B * self.rows * kv, device=dev)
+        self.vc = torch.zeros(B * self.rows * kv, device=dev)
+        self.w1, self.w2 = self.randn(H, 0.1, 1.0), self.randn(H, 0.1, 1.0)
+        self.qw, self.kw = self.randn(hd, 0.1, 1.0), self.randn(hd, 0.1, 1.0)
+        self.rope = K.RopeCache(dev)
+        self.rope.ensure(self.rows, hd, c["theta"])
+        self.pos = [torch.randint(0, self.rows, (B,), generator=self.gen, device=dev, dtype=torch.int32)
+                    for _ in range(S)]
+        eps = c["eps"]
+        norm_bytes = 3 * B * H * F + H * F + B * H + B * F
+        qkv_bytes = (N * H + N * F + B * H + B * F + B * nq * hd * F + 2 * B * kv * F + 2 * hd * F
+                     + 2 * B * hd * F + B * 4)
+        gu_bytes = 2 * I * H + 2 * I * F + B * H + B * F + B * I * F
+        self.kernels = {
+            "add_rms_norm_quant": (lambda i: K.add_rms_norm_quant(
+                self.x[i % S], self.d[i % S], self.w1, None, self.xq[i % S], self.xsc[i % S], B, H, eps),
+                norm_bytes),
+            "qkv_heads_w8a8_gemm": (lambda i: K.qkv_heads_w8a8_packed(
+                self.q[i % S], self.kc, self.vc, self.rows, self.qkv[i % L], self.xq[i % S], self.xsc[i % S],
+                self.qw, self.kw, self.rope, self.pos[i % S], B, H, nq, nk, hd, eps),
+                qkv_bytes, 2 * B * N * H),
+            "add_rms_norm_quant_post": (lambda i: K.add_rms_norm_quant(
+                self.x[i % S], self.d2[i % S], self.w2, None, self.xq2[i % S], self.xsc2[i % S], B, H, eps),
+                norm_bytes),
+            "gate_up_swiglu_w8a8_gemm": (lambda i: K.gate_up_swiglu_w8a8_packed(
+                self.o[i % S], self.gu[i % L], self.xq2[i % S], self.xsc2[i % S], B, H, I),
+                gu_bytes, 2 * B * 2 * I * H),
+        }
+        self.step_bytes = sum(spec[1] for spec in self.kernels.values())
+        self.tokens_per_step = B / 28.0
+        self.dtype = "int8/int32->f32"
+        self.gemm_ops = 2 * B * 2 * I * H
+        # the int8 MFMA ceiling; both GEMMs sit below its ridge (HBM-bound)
+        self.mfma_peak_tflops = 5000.0
+        self.mfma_peak_basis = "int8 MFMA 5.0 POP/s dense"
+
+    def config(self):
+        return {"batch": self.B, "hidden": 2048, "heads": "16q/8kv x 128", "intermediate": 6144,
+                "cache_rows_per_stream": self.rows, "layers_rotated": 28}
+
+
 class W8A32Decode(Workload):
     name = "w8a32_decode"
     description = ("qwen3-asr-1.7b INT8 decode projections as the reference runs them (W8A32 "
@@ -748,7 +833,7 @@ WORKLOADS = {"c1": C1DecodeChain, "c1_cold": C1Cold, "c2": C2PrefillChain, "c3":
              "c3_fused": C3Fused,
              "enc_add_ln": EncAddLayerNorm,
              "c4": C4Int8Matvec,
-             "c5": C5BatchedDecode, "c5_b32": C5Share, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
+             "c5": C5BatchedDecode, "c5_b32": C5Share, "c5_layer": C5Layer, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
              "lm_head": LmHead, "decode_step": DecodeStep,
              "w8a32_prefill": W8A32Prefill, "prefill_step": PrefillStep}
 
@@ -977,6 +1062,41 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
         return result(dt / n, nt, f"{n} layers of the c{name[1:]} chain (B={B}) on the oracle over 28 distinct "
                                   f"gate/up weights: norms/RoPE/SwiGLU on one thread, the INT8 W8A32 matvec "
                                   f"(one per stream) on {nt} threads", B / 28.0)
+    if name == "c5_layer":
+        c = DEC_1_7B
+        B, NL = 256, 28
+        H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
+        N, kv = (nq + 2 * nk) * hd, nk * hd
+        qkv_w, gu_w = qweights(N, H, NL), qweights(2 * I, H, NL)
+        x, d, d2, y = f32(B, H), f32(B, H), f32(B, H), np.empty((B, H), np.float32)
+        w1, w2, (qw, kw) = f32(H, sc=0.1, m=1.0), f32(H, sc=0.1, m=1.0), qk_gains(hd)
+        cos, sin = oracle.rope_table(2048, hd, c["theta"])
+        pos = r.integers(0, 2048, B).astype(np.int32)
+        qkv, gu, o = np.empty((B, N), np.float32), np.empty((B, 2 * I), np.float32), np.empty((B, I), np.float32)
+        q, k = np.empty((B, nq * hd), np.float32), np.empty((B, kv), np.float32)
+        kc = np.zeros((B, 64, kv), np.float32)  # the rows written: one per stream (a 64-row block each)
+        vc = np.zeros_like(kc)
+        it = [0]
+
+        def layer():
+            (wq, sq), (wg, sg) = qkv_w[it[0] % NL], gu_w[it[0] % NL]
+            it[0] += 1
+            L.ref_add_rms_norm(P(x), P(d), P(w1), P(y), B, H, c["eps"])
+            # the reference's q/k/v calls: one W8A32 matvec per stream (decoder.rs:881-886)
+            L.ref_linear_nobias_int8(P(qkv), P(y), P(wq), P(sq), B, H, N, nt)
+            q[:] = qkv[:, :nq * hd]
+            k[:] = qkv[:, nq * hd:nq * hd + kv]
+            L.ref_head_rms_norm_rope(P(q), P(k), P(qw), P(kw), P(cos), P(sin), P(pos), B, nq, nk, hd, c["eps"])
+            kc[np.arange(B), pos % 64] = k        # the k_at / v_at row copies (decoder.rs:894-895)
+            vc[np.arange(B), pos % 64] = qkv[:, nq * hd + kv:]
+            L.ref_add_rms_norm(P(x), P(d2), P(w2), P(y), B, H, c["eps"])
+            L.ref_linear_nobias_int8(P(gu), P(y), P(wg), P(sg), B, H, 2 * I, nt)
+            L.ref_swiglu_multiply(P(o), P(gu), B, I)
+
+        n, dt = _run_until(layer, seconds)
+        return result(dt / n, nt, f"{n} layers of the c5_layer chain (B=256) on the oracle over 28 distinct "
+                                  f"q/k/v and gate/up weights: the reference's W8A32 matvec per stream on {nt} "
+                                  "threads, norms/RoPE/SwiGLU and the cache row copies on one", B / 28.0)
     if name == "decode_step":
         from oracle.decoder import decode_int8_step
 

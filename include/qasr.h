@@ -366,6 +366,45 @@ int qasr_gate_up_swiglu_w8a8_packed(float* out, const int8_t* w_packed,
                                     size_t in_dim, size_t intermediate,
                                     void* stream);
 
+/* Batched W8A8 projection on tile-packed weights (qasr_pack_w8a8_tiles):
+ *   y[m, n] = ((f32)dot[m, n] * x_scales[m]) * scales[n],
+ *   dot[m, n] = sum_k w[n, k] * xq[m, k]   (int32, exact)
+ * for m < batch streams (xq, x_scales: qasr_quantize_rows_i8 or
+ * qasr_add_rms_norm_quant_f32 of each stream's row). The reference's
+ * linear_nobias_int8 (kernels/mod.rs:650-661, one W8A32 matvec per token) with
+ * the activation quantized per row, as the batched gate/up projection does;
+ * the integer dots are exact, so y equals the oracle's bit for bit. in_dim
+ * 1024 or 2048, out_dim % 128 == 0, 16-byte aligned buffers
+ * (QASR_ERR_UNSUPPORTED otherwise). */
+int qasr_linear_w8a8_packed(float* y, const int8_t* w_packed, const float* scales,
+                            const int8_t* xq, const float* x_scales, size_t batch,
+                            size_t in_dim, size_t out_dim, void* stream);
+
+/* The q/k/v projections of `batch` decode streams, each at its own position,
+ * with the steps after them in one launch (decoder.rs:881-895 per stream):
+ * w_packed is the packed [(n_heads + 2 n_kv_heads) * head_dim, in_dim] matrix
+ * of the q rows, then the k rows, then the v rows (scales likewise). For
+ * stream m at pos = positions[m]:
+ *   q = the q rows of qasr_linear_w8a8_packed -> per-head RMSNorm (q_norm_w)
+ *       -> NeoX RoPE with table row pos, written to q_out[m, :];
+ *   k = likewise with k_norm_w, written to k_cache row pos of stream m;
+ *   v = the v rows, written to v_cache row pos of stream m.
+ * Stream m's cache block is k_cache + m * cache_rows * n_kv_heads * head_dim
+ * (the reference's KvCache layer layout, one block per stream). A position
+ * outside the RoPE table or the cache gives a NaN q row and no cache write.
+ * Bit-identical to qasr_linear_w8a8_packed followed by
+ * qasr_head_rms_norm_rope_kv_f32 with positions. head_dim 128, in_dim 1024 or
+ * 2048, 16-byte aligned buffers (QASR_ERR_UNSUPPORTED otherwise). No reference
+ * counterpart as one call (the reference decodes one stream at a time). */
+int qasr_qkv_heads_w8a8_packed(float* q_out, float* k_cache, float* v_cache, size_t cache_rows,
+                               const int8_t* w_packed, const float* scales, const int8_t* xq,
+                               const float* x_scales, const float* q_norm_w,
+                               const float* k_norm_w, const float* cos_tab,
+                               const float* sin_tab, size_t table_rows,
+                               const int32_t* positions, size_t batch, size_t in_dim,
+                               size_t n_heads, size_t n_kv_heads, size_t head_dim, float eps,
+                               void* stream);
+
 /* As qasr_gate_up_swiglu_w8a8 for batch == 1 with an fp32 input vector that
  * the kernel quantizes per-vector itself (qasr_quantize_rows_i8 arithmetic),
  * so one launch covers quantize + matvec + SwiGLU. */

@@ -48,6 +48,7 @@ _SIGS = {
     "ref_interleave_gate_up": [_P, _P, _P, _P, _P, _P, _Z, _Z],
     "ref_gate_up_swiglu_w8a8": [_P, _P, _P, _P, _P, _P, _Z, _Z, _Z],
     "ref_argmax_rows": [_P, _P, _Z, _Z],
+    "ref_linear_w8a8": [_P, _P, _P, _P, _P, _P, _Z, _Z, _Z],
     "ref_causal_attention": [_P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _F, _Z],
     "ref_decode_chain_repeat": [_Z, _Z, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                 _Z, _Z, _Z, _Z, _Z, _F],
@@ -295,6 +296,15 @@ def gate_up_swiglu_w8a8(w, scales, xq, x_scales, batch, in_dim, inter):
                                   _p(_f32(scales)), _p(np.ascontiguousarray(xq, np.int8)),
                                   _p(_f32(x_scales)), batch, in_dim, inter)
     return out, dots
+
+
+def linear_w8a8(w, scales, xq, x_scales, batch, in_dim, out_dim):
+    """Returns (y [batch*out_dim] f32, dots [batch*out_dim] int32)."""
+    y = np.empty(batch * out_dim, np.float32)
+    dots = np.empty(batch * out_dim, np.int32)
+    lib().ref_linear_w8a8(_p(y), _p(dots), _p(np.ascontiguousarray(w, np.int8)), _p(_f32(scales)),
+                          _p(np.ascontiguousarray(xq, np.int8)), _p(_f32(x_scales)), batch, in_dim, out_dim)
+    return y, dots
 
 
 def argmax_rows(x, rows, cols) -> np.ndarray:

@@ -566,6 +566,28 @@ ORACLE_API void ref_gate_up_swiglu_w8a8(float* out, int32_t* dots, const int8_t*
 }
 
 /* ------------------------------------------------------------------------ */
+/* Batched W8A8 projection (new; the reference's linear_nobias_int8,          */
+/* kernels/mod.rs:650-661, with each stream's activation row quantized per    */
+/* row by quantize_f32_to_int8, quantize.rs:633-662):                         */
+/*   dot[m,n] = sum_k w[n,k] * xq[m,k] (exact), y = ((f32)dot * xs[m]) * s[n] */
+/* -- the same dequantization as the gate/up epilogue above. dots optional.   */
+/* ------------------------------------------------------------------------ */
+ORACLE_API void ref_linear_w8a8(float* y, int32_t* dots, const int8_t* w, const float* scales,
+                                const int8_t* xq, const float* x_scales, size_t batch,
+                                size_t in_dim, size_t out_dim) {
+  for (size_t m = 0; m < batch; ++m) {
+    const int8_t* xm = xq + m * in_dim;
+    for (size_t n = 0; n < out_dim; ++n) {
+      const int8_t* wn = w + n * in_dim;
+      int64_t d = 0;
+      for (size_t k = 0; k < in_dim; ++k) d += (int64_t)wn[k] * (int64_t)xm[k];
+      if (dots) dots[m * out_dim + n] = (int32_t)d;
+      y[m * out_dim + n] = ((float)(int32_t)d * x_scales[m]) * scales[n];
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
 /* lm_head argmax, decoder.rs:941-949 (and 955-962):                         */
 /*   best = 0; best_val = logits[0];                                         */
 /*   for i in 1..n { if logits[i] > best_val { best_val = logits[i]; best = i } } */

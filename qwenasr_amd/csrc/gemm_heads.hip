@@ -1,0 +1,385 @@
+// Batched W8A8 projection on CDNA4 int8 MFMA with a per-head epilogue: the
+// q/k/v projections of B decode streams, each stream at its own position.
+//
+//   dot[m, n] = sum_k W[n, k] * Xq[m, k]                 (int32, exact)
+//   y[m, n]   = ((f32)dot[m, n] * xs[m]) * s[n]          (the W8A8 dequantization)
+//
+// W is tile-packed (qasr_pack_w8a8_tiles): [N, K] with N = (n_heads +
+// 2 n_kv_heads) * 128 rows, the q heads, then the k heads, then the v heads
+// (decoder.rs:881-886 as one matrix). A workgroup owns one 128-row head x 32
+// streams, so the epilogue sees whole heads:
+//   q heads: per-head RMSNorm (q_norm) + NeoX RoPE at the stream's position,
+//            written to q_out[m, head] (decoder.rs:888, 891);
+//   k heads: the same with k_norm, written into the stream's cache row
+//            k_cache[m][pos][kv_head] (decoder.rs:889, 892, 894);
+//   v heads: written into v_cache[m][pos][kv_head] (decoder.rs:895).
+// The norm and rotation are head_norm_rope, the device function of the
+// standalone head kernel, so the results equal the plain projection
+// (qasr_linear_w8a8_packed) followed by qasr_head_rms_norm_rope_kv_f32 bit for
+// bit. MODE 0 is that plain projection: y[m, n] in fp32.
+//
+// Structure (8 waves, 512 threads): wave w = 4*kq + rg owns rows 32*rg ..
+// 32*rg + 31 (two 16-row MFMA tiles) for both 16-stream tiles over K half kq.
+// The 32 streams' int8 rows (32 x K bytes) are staged once in LDS with the
+// 16-byte slot of row r at slot ^ (r % 16), so the b128 fragment reads of 16
+// rows at one k offset hit distinct banks; W streams from the packed tiles
+// into registers PF k-steps ahead. After the loop the two K halves of a row
+// group are added through LDS (exact int32), the dequantized tile goes to LDS
+// as [32 streams][128 dims], and groups of 16 threads -- one stream each, in
+// the lane layout head_norm_rope expects -- finish the heads.
+#include "common.hpp"
+
+#include <atomic>
+
+namespace qasr {
+namespace {
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+constexpr int kHdRows = 128;   // W rows per workgroup: one head
+constexpr int kHdTok = 32;     // streams per workgroup
+constexpr int kHdWaves = 8;
+constexpr int kHdPF = 3;       // k-steps of W in flight per wave
+constexpr int kHdTPitch = 136; // floats per stream row of the dequantized tile (pad: banks)
+constexpr int kNumXcdH = 8;
+
+struct HeadsArgs {
+  float* y;               // MODE 0: [batch, N]
+  float* q_out;           // MODE 1: [batch, n_heads * 128]
+  float* k_cache;         // MODE 1: stream m's block at k_cache + m * cache_rows * kv_dim
+  float* v_cache;
+  const int8_t* w;        // packed [N, K]
+  const float* scales;    // [N]
+  const int8_t* xq;       // [batch, K]
+  const float* xs;        // [batch]
+  const float* q_norm_w;  // [128]
+  const float* k_norm_w;
+  const float* cos_tab;   // [table_rows, 128]
+  const float* sin_tab;
+  const int32_t* positions;  // [batch]
+  long long table_rows;
+  long long cache_rows;
+  int batch;
+  int N;
+  int n_heads;
+  int n_kv_heads;
+  int n_tiles;
+  int m_tiles;
+  float eps;
+};
+
+template <int KS, int MODE>
+__global__ __launch_bounds__(64 * kHdWaves) void gemm_w8a8_heads_kernel(HeadsArgs a) {
+  constexpr int K = KS * 64;
+  constexpr int KW = KS / 2;           // k-steps per wave (one K half)
+  constexpr int SLOTS = K / 16;        // 16-byte slots per staged row
+  constexpr int XU = kHdTok * SLOTS / (64 * kHdWaves);  // staging loads per thread
+  constexpr int PF = kHdPF;
+  constexpr size_t ROW_TILE = (size_t)KS * 1024;  // bytes of one 16-row block of packed W
+  static_assert(XU * 64 * kHdWaves == kHdTok * SLOTS, "the staging covers the tile");
+  extern __shared__ __align__(16) int8_t lds[];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = wave & 3, kq = wave >> 2;
+  const int r = lane & 15, g = lane >> 4;
+
+  // XCD-aware order: block b runs on XCD b % 8; the m_tiles blocks sharing a
+  // W tile go to the same XCD back to back, so later ones hit its L2.
+  const int b = blockIdx.x;
+  int tile_n, tile_m;
+  if (a.n_tiles % kNumXcdH == 0) {
+    const int slot = b / kNumXcdH;
+    tile_m = slot % a.m_tiles;
+    tile_n = b % kNumXcdH + kNumXcdH * (slot / a.m_tiles);
+  } else {
+    tile_m = b % a.m_tiles;
+    tile_n = b / a.m_tiles;
+  }
+  const int n0 = tile_n * kHdRows, m0 = tile_m * kHdTok;
+
+  // Issue order: the stream rows, the W window, the epilogue operands.
+  v4i_t xr[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int c = threadIdx.x + 64 * kHdWaves * u;
+    const int row = c / SLOTS, slot = c % SLOTS;
+    const int src = m0 + row < a.batch ? m0 + row : a.batch - 1;  // past the batch: valid row, dropped
+    xr[u] = *reinterpret_cast<const v4i_t*>(a.xq + (size_t)src * K + 16 * slot);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int8_t* wp = a.w + ((size_t)((n0 + 32 * rg) / 16) * KS + (size_t)kq * KW) * 1024 + 16 * lane;
+  v4i_t wbuf[PF][2];
+#pragma unroll
+  for (int d = 0; d < PF; ++d)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      wbuf[d][i] = __builtin_nontemporal_load(reinterpret_cast<const v4i_t*>(wp + i * ROW_TILE + d * 1024));
+  __builtin_amdgcn_sched_barrier(0);
+  float4 sc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) sc[i] = *reinterpret_cast<const float4*>(a.scales + n0 + 32 * rg + 16 * i + 4 * g);
+  const int mt = m0 + 16 * kq + r;
+  const float xsv = a.xs[mt < a.batch ? mt : a.batch - 1];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int c = threadIdx.x + 64 * kHdWaves * u;
+    const int row = c / SLOTS, slot = c % SLOTS;
+    *reinterpret_cast<v4i_t*>(lds + row * K + 16 * (slot ^ (row & 15))) = xr[u];
+  }
+  lds_barrier();
+
+  v4i_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v4i_t{0, 0, 0, 0};
+  // B fragment of stream tile j at global k-step s: stream row 16j + r, bytes
+  // [64s + 16g, +16) = slot 4s + g
+  auto xfrag = [&](int s, int j) -> v4i_t {
+    return *reinterpret_cast<const v4i_t*>(lds + (16 * j + r) * K + 16 * ((4 * s + g) ^ r));
+  };
+  const int k0 = kq * KW;
+  v4i_t bcur[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) bcur[j] = xfrag(k0, j);
+#pragma unroll
+  for (int s0 = 0; s0 < KW; s0 += PF) {
+#pragma unroll
+    for (int d = 0; d < PF; ++d) {
+      const int s = s0 + d;
+      if (s < KW) {
+        v4i_t av[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          av[i] = wbuf[d][i];
+          if (s + PF < KW)
+            wbuf[d][i] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i_t*>(wp + i * ROW_TILE + (s + PF) * 1024));
+        }
+        // keep the prefetch and the next fragments issued here (the scheduler
+        // would sink each load next to its use)
+        __builtin_amdgcn_sched_barrier(0);
+        v4i_t bn[2];
+        if (s + 1 < KW) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) bn[j] = xfrag(k0 + s + 1, j);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bcur[j], acc[i][j], 0, 0, 0);
+        if (s + 1 < KW) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) bcur[j] = bn[j];
+        }
+      }
+    }
+  }
+
+  // The two K halves of a row group: wave kq keeps stream tile kq and adds
+  // its partner's partial sums for it (constant register indices only).
+  __syncthreads();  // X no longer read
+  v4i_t give[2], mine[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    give[i] = kq == 0 ? acc[i][1] : acc[i][0];
+    mine[i] = kq == 0 ? acc[i][0] : acc[i][1];
+  }
+  v4i_t* ex = reinterpret_cast<v4i_t*>(lds);  // [rg][receiver kq][i][lane]
+#pragma unroll
+  for (int i = 0; i < 2; ++i) ex[((rg * 2 + (1 - kq)) * 2 + i) * 64 + lane] = give[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) mine[i] += ex[((rg * 2 + kq) * 2 + i) * 64 + lane];
+  __syncthreads();  // exchange area free
+
+  // Dequantize into the [32 streams][128 dims] tile: lane holds rows
+  // 32rg + 16i + 4g + {0..3} of stream 16kq + r.
+  float* T = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float4 v;
+    v.x = ((float)mine[i][0] * xsv) * sc[i].x;
+    v.y = ((float)mine[i][1] * xsv) * sc[i].y;
+    v.z = ((float)mine[i][2] * xsv) * sc[i].z;
+    v.w = ((float)mine[i][3] * xsv) * sc[i].w;
+    *reinterpret_cast<float4*>(T + (16 * kq + r) * kHdTPitch + 32 * rg + 16 * i + 4 * g) = v;
+  }
+  lds_barrier();
+
+  // One stream per group of 16 threads: dims 4sub..4sub+3 and 64+4sub..
+  const int tok = threadIdx.x >> 4, sub = threadIdx.x & 15;
+  const int m = m0 + tok;
+  const bool live = m < a.batch;
+  float4 x1 = *reinterpret_cast<const float4*>(T + tok * kHdTPitch + 4 * sub);
+  float4 x2 = *reinterpret_cast<const float4*>(T + tok * kHdTPitch + 64 + 4 * sub);
+  if constexpr (MODE == 0) {
+    if (live) {
+      float* yr = a.y + (size_t)m * a.N + n0;
+      st4(yr, sub, x1);
+      st4(yr + 64, sub, x2);
+    }
+  } else {
+    const int h = tile_n;
+    const int kind = h < a.n_heads ? 0 : (h < a.n_heads + a.n_kv_heads ? 1 : 2);
+    const long long pos = live ? (long long)a.positions[m] : 0;
+    const bool pos_ok = pos >= 0 && pos < a.table_rows && pos < a.cache_rows;
+    const int kv_dim = a.n_kv_heads * 128;
+    if (kind < 2) {
+      const float* w = kind == 0 ? a.q_norm_w : a.k_norm_w;
+      const float4 w1 = ld4(w, sub), w2 = ld4(w + 64, sub);
+      const long long pr = pos_ok ? pos : 0;  // out-of-table rows read row 0, then become NaN
+      const float* cr = a.cos_tab + pr * 128;
+      const float* sr = a.sin_tab + pr * 128;
+      const float4 c1 = ld4(cr, sub), c2 = ld4(cr + 64, sub);
+      const float4 s1 = ld4(sr, sub), s2 = ld4(sr + 64, sub);
+      // every lane of the group joins the reduction, live or not
+      head_norm_rope<128, true, true>(x1, x2, w1, w2, c1, c2, s1, s2, pos_ok, a.eps);
+    }
+    if (live) {
+      float* dst = nullptr;
+      if (kind == 0) {
+        dst = a.q_out + (size_t)m * a.n_heads * 128 + (size_t)h * 128;
+      } else if (pos_ok) {  // a row outside the cache is not written
+        float* cache = kind == 1 ? a.k_cache : a.v_cache;
+        const int kvh = kind == 1 ? h - a.n_heads : h - a.n_heads - a.n_kv_heads;
+        dst = cache + ((size_t)m * a.cache_rows + (size_t)pos) * kv_dim + (size_t)kvh * 128;
+      }
+      if (dst) {
+        st4(dst, sub, x1);
+        st4(dst + 64, sub, x2);
+      }
+    }
+  }
+}
+
+// The staged rows (32 x K bytes) need more than the default 64 KiB of LDS at
+// K = 2048; the limit is raised once per device.
+template <auto Fn>
+bool heads_lds_ok(size_t bytes) {
+  if (bytes <= 65536) return true;
+  constexpr int kMaxDev = 64;
+  static std::atomic<signed char> state[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
+  const signed char known = state[dev].load(std::memory_order_acquire);
+  if (known != 0) return known > 0;
+  int max_lds = 0;
+  const bool ok =
+      hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+      (size_t)max_lds >= bytes &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(Fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)bytes) == hipSuccess;
+  state[dev].store(ok ? 1 : -1, std::memory_order_release);
+  return ok;
+}
+
+template <int MODE>
+int launch_heads_gemm(HeadsArgs a, size_t K, hipStream_t st, const char* what) {
+  a.n_tiles = a.N / kHdRows;
+  a.m_tiles = (a.batch + kHdTok - 1) / kHdTok;
+  const size_t grid = (size_t)a.n_tiles * (size_t)a.m_tiles;
+  QASR_REQUIRE(grid <= 0x7fffffffu, "w8a8 projection: grid too large");
+  const size_t lds = (size_t)kHdTok * K;  // >= the exchange (16 KiB) and the fp32 tile (16.5 KiB)
+  if (K == 1024) {
+    if (!heads_lds_ok<&gemm_w8a8_heads_kernel<16, MODE>>(lds))
+      return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": device LDS too small");
+    gemm_w8a8_heads_kernel<16, MODE><<<(unsigned)grid, 64 * kHdWaves, lds, st>>>(a);
+  } else {
+    if (!heads_lds_ok<&gemm_w8a8_heads_kernel<32, MODE>>(lds))
+      return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": device LDS too small");
+    gemm_w8a8_heads_kernel<32, MODE><<<(unsigned)grid, 64 * kHdWaves, lds, st>>>(a);
+  }
+  return launch_status(what);
+}
+
+int check_w8a8_common(const int8_t* w, const float* scales, const int8_t* xq, const float* xs,
+                      size_t batch, size_t in_dim, size_t out_dim, const char* what) {
+  QASR_REQUIRE(w && scales && xq && xs, std::string(what) + ": null pointer");
+  if (in_dim != 1024 && in_dim != 2048)
+    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": in_dim must be 1024 or 2048");
+  if (out_dim % kHdRows != 0)
+    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": out_dim must be a multiple of 128");
+  QASR_REQUIRE(batch <= 0x7fffffffu && out_dim <= 0x7fffffffu, std::string(what) + ": size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(batch, out_dim, &n) && mul_ok(batch, in_dim, &n) && mul_ok(out_dim, in_dim, &n),
+               std::string(what) + ": size overflows");
+  if (!aligned16(w) || !aligned16(scales) || !aligned16(xq))
+    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": w, scales and xq must be 16-byte aligned");
+  return QASR_OK;
+}
+
+}  // namespace
+}  // namespace qasr
+
+using namespace qasr;
+
+extern "C" int qasr_linear_w8a8_packed(float* y, const int8_t* w_packed, const float* scales,
+                                       const int8_t* xq, const float* x_scales, size_t batch,
+                                       size_t in_dim, size_t out_dim, void* stream) {
+  if (batch == 0 || out_dim == 0) return QASR_OK;
+  QASR_REQUIRE(y, "linear_w8a8_packed: null pointer");
+  const int rc = check_w8a8_common(w_packed, scales, xq, x_scales, batch, in_dim, out_dim, "linear_w8a8_packed");
+  if (rc != QASR_OK) return rc;
+  if (!aligned16(y) || (out_dim * 4) % 16 != 0)
+    return fail(QASR_ERR_UNSUPPORTED, "linear_w8a8_packed: y must be 16-byte aligned");
+  HeadsArgs a{};
+  a.y = y;
+  a.w = w_packed;
+  a.scales = scales;
+  a.xq = xq;
+  a.xs = x_scales;
+  a.batch = (int)batch;
+  a.N = (int)out_dim;
+  return launch_heads_gemm<0>(a, in_dim, as_stream(stream), "linear_w8a8_packed");
+}
+
+extern "C" int qasr_qkv_heads_w8a8_packed(float* q_out, float* k_cache, float* v_cache, size_t cache_rows,
+                                          const int8_t* w_packed, const float* scales, const int8_t* xq,
+                                          const float* x_scales, const float* q_norm_w,
+                                          const float* k_norm_w, const float* cos_tab,
+                                          const float* sin_tab, size_t table_rows,
+                                          const int32_t* positions, size_t batch, size_t in_dim,
+                                          size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                          float eps, void* stream) {
+  if (batch == 0) return QASR_OK;
+  QASR_REQUIRE(q_out && k_cache && v_cache && q_norm_w && k_norm_w && cos_tab && sin_tab && positions,
+               "qkv_heads_w8a8_packed: null pointer");
+  if (head_dim != 128)
+    return fail(QASR_ERR_UNSUPPORTED, "qkv_heads_w8a8_packed: head_dim must be 128");
+  QASR_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads <= 4096 && n_kv_heads <= 4096,
+               "qkv_heads_w8a8_packed: head counts must be in [1, 4096]");
+  const size_t N = (n_heads + 2 * n_kv_heads) * head_dim;
+  const int rc = check_w8a8_common(w_packed, scales, xq, x_scales, batch, in_dim, N, "qkv_heads_w8a8_packed");
+  if (rc != QASR_OK) return rc;
+  size_t n;
+  QASR_REQUIRE(cache_rows > 0 && mul_ok(batch, cache_rows, &n) && mul_ok(n, n_kv_heads * head_dim, &n),
+               "qkv_heads_w8a8_packed: cache size overflows");
+  if (!aligned16(q_out) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(q_norm_w) ||
+      !aligned16(k_norm_w) || !aligned16(cos_tab) || !aligned16(sin_tab))
+    return fail(QASR_ERR_UNSUPPORTED, "qkv_heads_w8a8_packed: buffers must be 16-byte aligned");
+  HeadsArgs a{};
+  a.q_out = q_out;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.w = w_packed;
+  a.scales = scales;
+  a.xq = xq;
+  a.xs = x_scales;
+  a.q_norm_w = q_norm_w;
+  a.k_norm_w = k_norm_w;
+  a.cos_tab = cos_tab;
+  a.sin_tab = sin_tab;
+  a.positions = positions;
+  a.table_rows = (long long)table_rows;
+  a.cache_rows = (long long)cache_rows;
+  a.batch = (int)batch;
+  a.N = (int)N;
+  a.n_heads = (int)n_heads;
+  a.n_kv_heads = (int)n_kv_heads;
+  a.eps = eps;
+  return launch_heads_gemm<1>(a, in_dim, as_stream(stream), "qkv_heads_w8a8_packed");
+}

@@ -693,6 +693,41 @@ def pack_w8a8_tiles(w: QuantWeight) -> QuantWeight:
     return QuantWeight(packed, w.scales, w.out_dim, w.in_dim)
 
 
+def linear_w8a8_packed(y, w_packed: QuantWeight, xq, x_scales, batch: int, in_dim: int, out_dim: int) -> None:
+    """Batched W8A8 projection: y[m, n] = ((f32)dot * x_scales[m]) * scales[n]."""
+    _need(y, F32, batch * out_dim, "y")
+    _need(w_packed.data, I8, out_dim * in_dim, "w.data")
+    _need(w_packed.scales, F32, out_dim, "w.scales")
+    _need(xq, I8, batch * in_dim, "xq")
+    _need(x_scales, F32, batch, "x_scales")
+    _lib.call("qasr_linear_w8a8_packed", _ptr(y), _ptr(w_packed.data), _ptr(w_packed.scales), _ptr(xq),
+              _ptr(x_scales), batch, in_dim, out_dim, _stream())
+
+
+def qkv_heads_w8a8_packed(q_out, k_cache, v_cache, cache_rows: int, w_packed: QuantWeight, xq, x_scales,
+                          q_norm_w, k_norm_w, rope: "RopeCache", positions, batch: int, in_dim: int,
+                          n_heads: int, n_kv_heads: int, head_dim: int, eps: float) -> None:
+    """q/k/v projections of ``batch`` streams + q/k head norms + RoPE at each
+    stream's position + the K/V cache rows, one launch (decoder.rs:881-895 per
+    stream). ``k_cache``/``v_cache``: [batch, cache_rows, n_kv_heads * head_dim]."""
+    n = (n_heads + 2 * n_kv_heads) * head_dim
+    kv = n_kv_heads * head_dim
+    _need(q_out, F32, batch * n_heads * head_dim, "q_out")
+    _need(k_cache, F32, batch * cache_rows * kv, "k_cache")
+    _need(v_cache, F32, batch * cache_rows * kv, "v_cache")
+    _need(w_packed.data, I8, n * in_dim, "w.data")
+    _need(w_packed.scales, F32, n, "w.scales")
+    _need(xq, I8, batch * in_dim, "xq")
+    _need(x_scales, F32, batch, "x_scales")
+    _need(q_norm_w, F32, head_dim, "q_norm_w")
+    _need(k_norm_w, F32, head_dim, "k_norm_w")
+    _need(positions, I32, batch, "positions")
+    _lib.call("qasr_qkv_heads_w8a8_packed", _ptr(q_out), _ptr(k_cache), _ptr(v_cache), cache_rows,
+              _ptr(w_packed.data), _ptr(w_packed.scales), _ptr(xq), _ptr(x_scales), _ptr(q_norm_w),
+              _ptr(k_norm_w), _ptr(rope.cos), _ptr(rope.sin), rope.cap, _ptr(positions), batch, in_dim,
+              n_heads, n_kv_heads, head_dim, eps, _stream())
+
+
 def gate_up_swiglu_w8a8_packed(out, w_packed: QuantWeight, xq, x_scales, batch: int, in_dim: int,
                                intermediate: int) -> None:
     """gate_up_swiglu_w8a8 on a pack_w8a8_tiles weight (same results)."""

@@ -1,0 +1,175 @@
+"""Batched multi-stream W8A8 projections on the GPU against the oracle.
+
+qasr_linear_w8a8_packed is the reference's linear_nobias_int8
+(kernels/mod.rs:650-661) with each stream's activation row quantized per row:
+its int32 dots are exact and its dequantization is one fixed sequence of f32
+multiplies, so the output equals oracle.linear_w8a8 bit for bit.
+
+qasr_qkv_heads_w8a8_packed is the q/k/v projections of B streams plus the
+steps after them (decoder.rs:881-895 per stream: q/k head RMSNorm, RoPE at
+the stream's own position, the K/V rows stored in the stream's cache block).
+It must equal the plain projection followed by the standalone head kernel
+bit for bit, and the oracle's composition (linear_w8a8, then
+head_rms_norm_rope looped over streams) within rel/abs 1e-5.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import assert_close
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+NQ, NK, HD = 16, 8, 128
+
+
+def _quant_rows(r, rows, cols, scale=1.0):
+    x = (scale * r.standard_normal((rows, cols))).astype(np.float32)
+    q, s = oracle.quantize_f32_to_int8(x.ravel(), rows, cols)
+    return q.reshape(rows, cols), s
+
+
+def _packed(dev, wq, ws):
+    from qwenasr_amd import kernels as K
+
+    o, i = wq.shape
+    w = K.QuantWeight(torch.from_numpy(wq.ravel().copy()).to(dev), torch.from_numpy(ws).to(dev), o, i)
+    return K.pack_w8a8_tiles(w)
+
+
+@pytest.mark.parametrize("batch,out_dim,in_dim", [(1, 128, 1024), (5, 384, 2048), (31, 256, 1024),
+                                                  (32, 2048, 2048), (33, 128, 2048), (256, 1024, 2048)])
+def test_linear_w8a8_packed_bit_exact(dev, batch, out_dim, in_dim):
+    from qwenasr_amd import kernels as K
+
+    r = np.random.default_rng([51, batch, out_dim, in_dim])
+    wq, ws = _quant_rows(r, out_dim, in_dim, 0.02)
+    xq, xs = _quant_rows(r, batch, in_dim)
+    w = _packed(dev, wq, ws)
+    y = torch.full((batch * out_dim,), float("nan"), device=dev)
+    print(f"[batched] linear_w8a8 B={batch} N={out_dim} K={in_dim}", flush=True)
+    K.linear_w8a8_packed(y, w, torch.from_numpy(xq.ravel().copy()).to(dev), torch.from_numpy(xs).to(dev),
+                         batch, in_dim, out_dim)
+    torch.cuda.synchronize()
+    ref, _ = oracle.linear_w8a8(wq, ws, xq, xs, batch, in_dim, out_dim)
+    np.testing.assert_array_equal(y.cpu().numpy(), ref)
+
+
+def _qkv_case(dev, batch, in_dim, cache_rows, seed, bad_rows=()):
+    """Inputs of one q/k/v call: packed weights, quantized rows, gains,
+    positions (with the given rows set out of range), the RoPE table."""
+    from qwenasr_amd import kernels as K
+
+    r = np.random.default_rng(seed)
+    N = (NQ + 2 * NK) * HD
+    wq, ws = _quant_rows(r, N, in_dim, 0.02)
+    xq, xs = _quant_rows(r, batch, in_dim)
+    qw = (1 + 0.1 * r.standard_normal(HD)).astype(np.float32)
+    kw = (1 + 0.1 * r.standard_normal(HD)).astype(np.float32)
+    pos = r.integers(0, cache_rows, batch).astype(np.int32)
+    for i, v in bad_rows:
+        pos[i] = v
+    rope = K.RopeCache(dev)
+    rope.ensure(cache_rows, HD, 1e6)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    return dict(wq=wq, ws=ws, xq=xq, xs=xs, qw=qw, kw=kw, pos=pos, w=_packed(dev, wq, ws), rope=rope,
+                xq_t=t(xq.ravel()), xs_t=t(xs), qw_t=t(qw), kw_t=t(kw), pos_t=t(pos))
+
+
+def _run_fused(dev, c, batch, in_dim, cache_rows, fill=7.0):
+    from qwenasr_amd import kernels as K
+
+    kv = NK * HD
+    q = torch.full((batch * NQ * HD,), float("nan"), device=dev)
+    kc = torch.full((batch * cache_rows * kv,), fill, device=dev)
+    vc = torch.full((batch * cache_rows * kv,), fill, device=dev)
+    K.qkv_heads_w8a8_packed(q, kc, vc, cache_rows, c["w"], c["xq_t"], c["xs_t"], c["qw_t"], c["kw_t"], c["rope"],
+                            c["pos_t"], batch, in_dim, NQ, NK, HD, 1e-6)
+    return q, kc, vc
+
+
+def test_qkv_heads_fused_equals_projection_then_head_kernel(dev):
+    """Ragged batch (37 streams: a partial 32-stream tile), one position
+    outside the RoPE table and one below 0: the fused launch equals
+    qasr_linear_w8a8_packed + qasr_head_rms_norm_rope_kv_f32 bit for bit --
+    q rows (NaN for the bad positions), the cache rows at each stream's
+    position, and no other cache row touched."""
+    from qwenasr_amd import kernels as K
+
+    B, Kd, rows = 37, 2048, 1024
+    c = _qkv_case(dev, B, Kd, rows, 52, bad_rows=((3, -1), (20, 5000)))
+    print("[batched] qkv heads fused", flush=True)
+    q, kc, vc = _run_fused(dev, c, B, Kd, rows)
+    # unfused: the projection, then the head kernel on its q/k/v slices
+    N, kv = (NQ + 2 * NK) * HD, NK * HD
+    y = torch.empty(B * N, device=dev)
+    K.linear_w8a8_packed(y, c["w"], c["xq_t"], c["xs_t"], B, Kd, N)
+    y = y.view(B, N)
+    q2 = y[:, :NQ * HD].contiguous().view(-1)
+    k2 = y[:, NQ * HD:(NQ + NK) * HD].contiguous().view(-1)
+    v2 = y[:, (NQ + NK) * HD:].contiguous().view(-1)
+    kc2 = torch.full((B * rows * kv,), 7.0, device=dev)
+    vc2 = torch.full((B * rows * kv,), 7.0, device=dev)
+    print("[batched] qkv heads unfused", flush=True)
+    K.head_rms_norm_rope_kv(q2, k2, v2, c["qw_t"], c["kw_t"], c["rope"], c["pos_t"], 0, B, NQ, NK, HD, 1e-6,
+                            kc2, vc2, rows)
+    torch.cuda.synchronize()
+    assert torch.equal(q.isnan(), q2.isnan())
+    assert torch.equal(torch.nan_to_num(q, 0.0), torch.nan_to_num(q2, 0.0))
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    qn = q.view(B, NQ * HD).cpu().numpy()
+    assert np.isnan(qn[3]).all() and np.isnan(qn[20]).all() and not np.isnan(np.delete(qn, [3, 20], 0)).any()
+    # exactly the valid streams' rows were written
+    written = (kc.view(B, rows, kv) != 7.0).any(dim=2).cpu().numpy()
+    want = np.zeros((B, rows), bool)
+    for b, p in enumerate(c["pos"]):
+        if 0 <= p < rows:
+            want[b, p] = True
+    np.testing.assert_array_equal(written, want)
+
+
+@pytest.mark.parametrize("in_dim", [2048, 1024])
+def test_qkv_heads_matches_oracle_at_c5_shape(dev, in_dim):
+    """256 streams at positions U[0, 2047] (the batched-decode config) against
+    the oracle: linear_w8a8, then head_rms_norm_rope with per-stream positions;
+    q rows and the K/V cache rows at each position, rel/abs 1e-5."""
+    B, rows = 256, 2048
+    c = _qkv_case(dev, B, in_dim, rows, [53, in_dim])
+    print(f"[batched] qkv heads B={B} K={in_dim}", flush=True)
+    q, kc, vc = _run_fused(dev, c, B, in_dim, rows)
+    torch.cuda.synchronize()
+    N, kv = (NQ + 2 * NK) * HD, NK * HD
+    y, _ = oracle.linear_w8a8(c["wq"], c["ws"], c["xq"], c["xs"], B, in_dim, N)
+    y = y.reshape(B, N)
+    cos, sin = oracle.rope_table(c["rope"].cap, HD, 1e6)
+    qr, kr = oracle.head_rms_norm_rope(y[:, :NQ * HD].ravel(), y[:, NQ * HD:(NQ + NK) * HD].ravel(), c["qw"],
+                                       c["kw"], cos, sin, c["pos"], B, NQ, NK, HD, 1e-6)
+    assert_close(q.cpu().numpy(), qr, 1e-5, 1e-5, "q")
+    idx = torch.from_numpy(np.arange(B) * rows + c["pos"].astype(np.int64)).to(dev)
+    k_rows = kc.view(B * rows, kv)[idx].cpu().numpy()
+    v_rows = vc.view(B * rows, kv)[idx].cpu().numpy()
+    assert_close(k_rows, kr.reshape(B, kv), 1e-5, 1e-5, "k rows")
+    np.testing.assert_array_equal(v_rows, y[:, (NQ + NK) * HD:])  # v: the dequantized rows, no rounding step
+
+
+def test_batched_projection_rejects_unsupported_shapes(dev):
+    from qwenasr_amd import _lib
+    from qwenasr_amd import kernels as K
+
+    r = np.random.default_rng(54)
+    wq, ws = _quant_rows(r, 128, 1024, 0.02)
+    w = _packed(dev, wq, ws)
+    xq = torch.zeros(1024 * 4, dtype=torch.int8, device=dev)
+    xs = torch.ones(4, device=dev)
+    y = torch.empty(4 * 128, device=dev)
+    with pytest.raises(_lib.QasrError) as e:  # in_dim 1536: no kernel (rejected before any launch)
+        w1536 = K.QuantWeight(torch.zeros(128 * 1536, dtype=torch.int8, device=dev), w.scales, 128, 1536)
+        K.linear_w8a8_packed(y, w1536, torch.zeros(1536 * 4, dtype=torch.int8, device=dev), xs, 4, 1536, 128)
+    assert e.value.code == _lib.QASR_ERR_UNSUPPORTED
+    with pytest.raises(_lib.QasrError) as e:  # out_dim not a multiple of 128
+        K.linear_w8a8_packed(y, K.QuantWeight(w.data, w.scales, 64, 1024), xq, xs, 4, 1024, 64)
+    assert e.value.code == _lib.QASR_ERR_UNSUPPORTED
+    torch.cuda.synchronize()

@@ -237,6 +237,31 @@ def test_w8a8_dots_bit_exact_and_epilogue(golden):
     assert_close(out.reshape(B, inter), golden["w8a8_y64"], 2e-6, 1e-9, "w8a8 out")
 
 
+def test_linear_w8a8_dots_exact_and_dequant():
+    # the batched W8A8 projection: int32 dots against int64 numpy, the fp32
+    # output against float64 (two f32 roundings: <= 2.4e-7 relative), and the
+    # same dequantization the gate/up epilogue applies: on the interleaved
+    # matrix its (g, u) pairs give the gate/up oracle's SwiGLU bit for bit
+    r = np.random.default_rng(41)
+    B, K, inter = 7, 192, 24
+    w = r.integers(-127, 128, (2 * inter, K), dtype=np.int8)
+    s = (1e-3 + 1e-2 * r.random(2 * inter)).astype(np.float32)
+    xq = r.integers(-127, 128, (B, K), dtype=np.int8)
+    xs = (1e-2 + r.random(B)).astype(np.float32)
+    y, dots = oracle.linear_w8a8(w, s, xq, xs, B, K, 2 * inter)
+    exact = xq.astype(np.int64) @ w.astype(np.int64).T
+    np.testing.assert_array_equal(dots.reshape(B, -1), exact)
+    ref = exact * xs.astype(np.float64)[:, None] * s.astype(np.float64)[None, :]
+    assert_close(y.reshape(B, -1), ref, 2.4e-7, 0, "w8a8 dequant")
+    gu = y.reshape(B, inter, 2).astype(np.float32)
+    g, u = gu[..., 0], gu[..., 1]
+    out, _ = oracle.gate_up_swiglu_w8a8(w, s, xq, xs, B, K, inter)
+    np.testing.assert_array_equal(out, oracle.swiglu_split(g.ravel().copy(), u.ravel().copy()))
+    # the reference kernel on the integer activations with unit scales gives the dots
+    ref32 = oracle.linear_nobias_int8(xq.astype(np.float32), w, np.ones(2 * inter, np.float32), B, K, 2 * inter)
+    np.testing.assert_array_equal(ref32.astype(np.int64), dots.astype(np.int64))
+
+
 def test_w8a32_closed_form(golden):
     w, s, x = golden["w8a8_w"], golden["w8a8_s"], golden["w8a32_x"]
     y = oracle.linear_nobias_int8(x, w, s, 2, w.shape[1], w.shape[0]).reshape(2, -1)
