@@ -654,6 +654,67 @@ class DecodeStep(Workload):
                 "heads": "16q/8kv x 128", "layers": 28, "vocab": VOCAB}
 
 
+class DecodeStepBatched(Workload):
+    """B=256 decode streams, each at its own position U[0,2047] over its own
+    KV cache, one token each through all 28 layers and the lm_head."""
+    name = "decode_step_b256"
+    B = 256
+    description = ("qwen3-asr-1.7b INT8 batched decode: 256 streams, each at its own position U[0,2047] over "
+                   "its own KV cache (28 layers x 2048 rows), one token each through all 28 layers (W8A32 "
+                   "matrix-core projections, per-stream head norm+RoPE+KV store, per-stream attention, "
+                   "gate/up with the decode SwiGLU) and the lm_head [151936,2048] with each stream's argmax")
+    unit_tokens = 256
+    dtype = "int8/f32"
+    max_steps = 10  # ~15 ms per step: 10 steps per replay keep the run short
+
+    def __init__(self, dev, torch):
+        super().__init__(dev, torch)
+        from qwenasr_amd import kernels as K
+        from qwenasr_amd.decoder import DecoderInt8Batched
+
+        c = DEC_1_7B
+        H, I, nq, nk, hd, L, B = c["hidden"], c["inter"], c["n_heads"], c["n_kv_heads"], c["head_dim"], 28, self.B
+        rows = 2048
+
+        def qw(o, i):
+            q = torch.randint(-127, 128, (o * i,), generator=self.gen, device=dev, dtype=torch.int8)
+            return K.QuantWeight(q, self.randn(o, 1e-4, 1e-3).abs_(), o, i)
+
+        def gain(n):
+            return self.randn(n, 0.1, 1.0)
+
+        layers = [{"wq": qw(nq * hd, H), "wk": qw(nk * hd, H), "wv": qw(nk * hd, H), "wo": qw(H, nq * hd),
+                   "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": gain(hd), "k_norm": gain(hd),
+                   "input_norm": gain(H), "post_attn_norm": gain(H)} for _ in range(L)]
+        weights = {"layers": layers, "norm": gain(H), "lm_head": qw(VOCAB, H)}
+        self.dec = DecoderInt8Batched(weights, H, I, L, B, rows, nq, nk, hd, c["eps"], c["theta"], device=dev)
+        # each stream's earlier context: its cache rows (all 28 layers, 120 GB in all)
+        for l in range(L):
+            self.dec.k[l].normal_(generator=self.gen)
+            self.dec.v[l].normal_(generator=self.gen)
+        pos = torch.randint(0, rows, (B,), generator=self.gen, device=dev, dtype=torch.int32)
+        self.dec.positions.copy_(pos)
+        self.embeds = [self.randn(B * H) for _ in range(2)]
+        kv, q_dim = nk * hd, nq * hd
+        keys = int(pos.to(torch.int64).sum().item()) + B  # keys 0..pos of every stream
+        w_bytes = sum(w.out_dim * w.in_dim + w.out_dim * F for k, w in layers[0].items()
+                      if isinstance(w, K.QuantWeight)) + (2 * hd + 2 * H) * F  # + norm gains
+        act = F * B * (4 * H + H + (q_dim + 2 * kv) + 2 * (q_dim + 2 * kv) + q_dim + q_dim + q_dim + H
+                       + 4 * H + H + I + I + H)
+        layer_bytes = w_bytes + act + 2 * keys * kv * F + 2 * B * kv * F
+        head_bytes = VOCAB * H + VOCAB * F + 4 * B * H * F + B * H * F + 2 * B * VOCAB * F + B * 4
+        step_bytes = L * layer_bytes + head_bytes
+        self.kernels = {"decode_step": (lambda i: self.dec.decode(self.embeds[i % 2]), step_bytes)}
+        self.step_bytes = step_bytes
+        self.tokens_per_step = float(B)
+        self.mean_position = keys / B - 1
+
+    def config(self):
+        return {"batch": self.B, "positions": "U[0,2047] per stream", "mean_position": round(self.mean_position, 1),
+                "cache_rows_per_stream": 2048, "hidden": 2048, "intermediate": 6144, "heads": "16q/8kv x 128",
+                "layers": 28, "vocab": VOCAB}
+
+
 class PrefillStep(Workload):
     name = "prefill_step"
     description = ("qwen3-asr-0.6b INT8 prefill of a 512-token chunk at position 0, fully on the device "
@@ -834,7 +895,7 @@ WORKLOADS = {"c1": C1DecodeChain, "c1_cold": C1Cold, "c2": C2PrefillChain, "c3":
              "enc_add_ln": EncAddLayerNorm,
              "c4": C4Int8Matvec,
              "c5": C5BatchedDecode, "c5_b32": C5Share, "c5_layer": C5Layer, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
-             "lm_head": LmHead, "decode_step": DecodeStep,
+             "lm_head": LmHead, "decode_step": DecodeStep, "decode_step_b256": DecodeStepBatched,
              "w8a32_prefill": W8A32Prefill, "prefill_step": PrefillStep}
 
 
@@ -1097,7 +1158,7 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
         return result(dt / n, nt, f"{n} layers of the c5_layer chain (B=256) on the oracle over 28 distinct "
                                   f"q/k/v and gate/up weights: the reference's W8A32 matvec per stream on {nt} "
                                   "threads, norms/RoPE/SwiGLU and the cache row copies on one", B / 28.0)
-    if name == "decode_step":
+    if name in ("decode_step", "decode_step_b256"):
         from oracle.decoder import decode_int8_step
 
         c = DEC_1_7B
@@ -1121,6 +1182,11 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
         x = f32(H)
         n, dt = _run_until(lambda: decode_int8_step(w, kc, vc, pos, x, nq, nk, hd, c["eps"], c["theta"], nt),
                            seconds)
+        if name == "decode_step_b256":  # the reference decodes one stream at a time: 256 in turn
+            return result(dt / n * 256, nt, f"{n} decode tokens of one stream at position {pos} (the middle of "
+                                            "U[0,2047]) on the oracle's restated decode step (decoder.rs:848-965) "
+                                            "over 28 distinct layers, scaled to 256 streams decoded in turn (the "
+                                            f"reference is single-stream): INT8 matvecs on {nt} threads", 256.0)
         return result(dt / n, nt, f"{n} decode tokens at position {pos} on the oracle's restated decode step "
                                   f"(decoder.rs:848-965) over 28 distinct layers of weights: INT8 matvecs on "
                                   f"{nt} threads, attention and norms on one", 1.0)
@@ -1205,21 +1271,38 @@ def profile_copy(torch, dev, n: int) -> int:
 
 
 def profile_kernel(torch, wl, name: str, n: int) -> int:
-    if name not in wl.kernels:
-        print(f"bench.py: workload {wl.name} has no kernel {name!r} (has {sorted(wl.kernels)})",
-              file=sys.stderr)
-        return 2
-    launch, nbytes = wl.kernels[name][0], wl.kernels[name][1]
-    for i in range(n):
-        launch(i)
-    torch.cuda.synchronize()
-    print(json.dumps({"profile_kernel": name, "workload": wl.name, "launches": n,
-                      "algorithmic_bytes": nbytes}), flush=True)
+    """Launches one kernel of the workload n times (rotating buffers), or with
+    NAME "all" every kernel in turn, n times each. In "all" mode a marker
+    dispatch (argmax_rows_kernel<false> over 3 values) precedes each kernel's
+    launches and follows the last, so a per-dispatch counter trace splits into
+    the kernels' groups by position."""
+    from qwenasr_amd import kernels as K
+
+    names = list(wl.kernels) if name == "all" else [name]
+    for nm in names:
+        if nm not in wl.kernels:
+            print(f"bench.py: workload {wl.name} has no kernel {nm!r} (has {sorted(wl.kernels)})",
+                  file=sys.stderr)
+            return 2
+    idx = torch.zeros(1, dtype=torch.int32, device=wl.dev)
+    mx = torch.zeros(3, device=wl.dev)
+    for nm in names:
+        if name == "all":
+            K.argmax_rows(idx, mx, 1, 3)
+        launch, nbytes = wl.kernels[nm][0], wl.kernels[nm][1]
+        for i in range(n):
+            launch(i)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_kernel": nm, "workload": wl.name, "launches": n,
+                          "algorithmic_bytes": nbytes}), flush=True)
+    if name == "all":
+        K.argmax_rows(idx, mx, 1, 3)
+        torch.cuda.synchronize()
     return 0
 
 
 # ---------------------------------------------------------------------------
-DEFAULT_CONFIGS = "c1,c1_cold,c2,c3_fused,c4,c5_b32,decode_step"
+DEFAULT_CONFIGS = "c1,c1_cold,c2,c3_fused,c4,c5_b32,c5_layer,decode_step,decode_step_b256"
 
 
 def _round(v):
@@ -1232,7 +1315,11 @@ def _round(v):
 
 def measure(torch, dev, wl, K: int, W: int, use_graph: bool) -> dict:
     """Warmup, then the step and each kernel timed (median over replays of
-    K launches), the roofline of the kernel moving the most bytes."""
+    K launches), the roofline of the kernel moving the most bytes. A workload
+    with a max_steps (a step of many milliseconds) times min(K, max_steps)
+    steps per replay."""
+    K = min(K, getattr(wl, "max_steps", K))
+    W = min(W, getattr(wl, "max_steps", W))
     reps = replays_for(K)
     between = getattr(wl, "between", None)
     for i in range(W):
@@ -1261,7 +1348,7 @@ def measure(torch, dev, wl, K: int, W: int, use_graph: bool) -> dict:
         print(f"[bench] {wl.name}/{kname}: {us:.2f} us, {d['GB/s']:.0f} GB/s", file=sys.stderr, flush=True)
     value = wl.step_bytes / (ms * 1e-3) / 1e9
     return {"step": step, "use_graph": use_graph, "per_kernel": per_kernel, "value": value,
-            "tokens_per_s": wl.tokens_per_step / (ms * 1e-3)}
+            "tokens_per_s": wl.tokens_per_step / (ms * 1e-3), "steps": K}
 
 
 def roofline_of(torch, dev, wl, m: dict, K: int) -> dict:
@@ -1322,6 +1409,7 @@ def summary(wl, m: dict, cpu) -> dict:
     out = {"workload": wl.description, **wl.config(),
            "us_per_step": round(st["median"] * 1e3, 3), "us_p10": round(st["p10"] * 1e3, 3),
            "us_p90": round(st["p90"] * 1e3, 3), "us_min": round(st["min"] * 1e3, 3), "replays": st["replays"],
+           "steps_per_replay": m["steps"],
            "algorithmic_bytes_per_step": wl.step_bytes, "GB/s": round(m["value"], 1),
            "frac_hbm": round(m["value"] / HBM_PEAK_GBS, 4), "tokens_per_s": round(m["tokens_per_s"], 1),
            "dtype": wl.dtype,
@@ -1444,6 +1532,8 @@ def main() -> int:
         out["configs"] = configs
     if "decode_step" in configs:
         out["decode_tokens_per_s"] = configs["decode_step"]["tokens_per_s"]
+    if "decode_step_b256" in configs:
+        out["batched_decode_tokens_per_s"] = configs["decode_step_b256"]["tokens_per_s"]
     print(json.dumps(out), flush=True)
     return 0
 

@@ -257,7 +257,10 @@ int qasr_linear_nobias_int8_f32(float* y, const float* x, const int8_t* w,
  * row-interleaved fused weight [2*intermediate, in_dim] (g0, u0, g1, u1, ...,
  * with interleaved scales), then out[s, j] = g / (1 + expf(-g)) * u with
  * g = gate_up[s, 2j], u = gate_up[s, 2j + 1] -- the decode loop's libm SwiGLU,
- * not the prefill fast_exp form. The gate_up values are never written. */
+ * not the prefill fast_exp form. The gate_up values are never written. Several
+ * rows (decode streams, seq_len >= 8, in_dim % 64 == 0, 16-byte aligned x and
+ * w) run the matrix-core GEMM of qasr_linear_nobias_int8_f32 with the SwiGLU
+ * in its epilogue. */
 int qasr_gate_up_swiglu_int8_f32(float* out, const float* x, const int8_t* w_gate_up,
                                  const float* scales_gate_up, size_t seq_len, size_t in_dim,
                                  size_t intermediate, void* stream);
@@ -470,6 +473,22 @@ int qasr_decode_attention_f32(float* out, float* q, const float* k, const float*
                               size_t n_kv_heads, size_t head_dim, float eps, float scale,
                               float* k_cache, float* v_cache, size_t cache_rows, float* workspace,
                               size_t workspace_floats, void* stream);
+
+/* Decode attention of `batch` streams, each over its own cache block
+ * (decoder.rs:900-903 per stream): for stream m at pos = positions[m], out[m]
+ * = causal attention of q[m] (n_heads*head_dim, already normalised and
+ * rotated) over rows 0..pos of k_cache/v_cache + m * cache_rows *
+ * n_kv_heads * head_dim (the block qasr_head_rms_norm_rope_kv_f32 with
+ * positions writes). The keys of a stream are not split: one workgroup per
+ * (stream, kv head) walks them and normalises its output itself. A position
+ * outside the cache gives a NaN row. head_dim 128 with n_heads/n_kv_heads in
+ * {1, 2}, or 64 with {1, 2, 4}; 16-byte aligned buffers (QASR_ERR_UNSUPPORTED
+ * otherwise). No reference counterpart as one call (the reference decodes one
+ * stream at a time). */
+int qasr_batched_decode_attention_f32(float* out, const float* q, const float* k_cache,
+                                      const float* v_cache, size_t cache_rows,
+                                      const int32_t* positions, size_t batch, size_t n_heads,
+                                      size_t n_kv_heads, size_t head_dim, float scale, void* stream);
 
 /* Workspace floats qasr_causal_attention_split_f32 can use for these sizes. */
 size_t qasr_causal_attention_workspace_floats(size_t seq_q, size_t n_heads, size_t head_dim);

@@ -288,11 +288,24 @@ struct DecodePre {
   float eps;
 };
 
-template <int HD, int G, bool PRE = false>
+// Batched decode streams (BATCH): row i is stream i, its keys are rows
+// 0..positions[i] of its own cache block (k + i * cache_rows * kv_dim), the
+// key range is not split (one workgroup per stream and kv head), and the
+// workgroup writes the normalised output row itself. A position outside the
+// cache gives NaN rows.
+struct DecodeBatch {
+  const int32_t* positions;
+  long long cache_rows;
+  float* out;
+};
+
+template <int HD, int G, bool PRE = false, bool BATCH = false>
 __global__ __launch_bounds__(256) void attention_decode_split_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     int seq_q, int seq_k, int nk, float scale, int q_offset, int keys_per_split,
-    float* __restrict__ ws_o, float* __restrict__ ws_ml, DecodePre pre = DecodePre{}) {
+    float* __restrict__ ws_o, float* __restrict__ ws_ml, DecodePre pre = DecodePre{},
+    DecodeBatch batch = DecodeBatch{}) {
+  static_assert(!(PRE && BATCH), "one decode stream or a batch of them");
   constexpr int DPL = HD / 64;
   constexpr int DQ = HD / 4;   // head dims per lane of a quad
   constexpr int C4 = DQ / 4;   // float4 loads per key per lane
@@ -303,7 +316,17 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
   const int i = blockIdx.x, kh = blockIdx.y;
   const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
   float4 qv[G][C4];
-  const int k_lim = min(q_offset + i + 1, seq_k);
+  [[maybe_unused]] bool bad_pos = false;
+  int k_lim;
+  if constexpr (BATCH) {
+    const long long p = batch.positions[i];
+    bad_pos = p < 0 || p >= batch.cache_rows;
+    k_lim = bad_pos ? 0 : (int)p + 1;
+    k += (size_t)i * (size_t)batch.cache_rows * kv_stride;
+    v += (size_t)i * (size_t)batch.cache_rows * kv_stride;
+  } else {
+    k_lim = min(q_offset + i + 1, seq_k);
+  }
   const int k_begin = min(k_lim, (int)blockIdx.z * keys_per_split);
   const int k_end = min(k_lim, k_begin + keys_per_split);
   float m[G], l[G], o[G][DPL];
@@ -509,12 +532,19 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
 #pragma unroll
         for (int d = 0; d < DPL; ++d) acc[d] = __builtin_fmaf(co[w][g][lane * DPL + d], f, acc[d]);
       }
-      const size_t slot = ((size_t)i * nk * G + (size_t)kh * G + g) * nsplit + blockIdx.z;
+      if constexpr (BATCH) {  // the whole key range: normalise as the merge kernel does
+        const float inv = lsum > 0.0f ? 1.0f / lsum : 1.0f;
+        float* orow = batch.out + ((size_t)i * nk * G + (size_t)kh * G + g) * HD;
 #pragma unroll
-      for (int d = 0; d < DPL; ++d) ws_o[slot * HD + lane * DPL + d] = acc[d];
-      if (lane == 0) {
-        ws_ml[2 * slot] = mx;
-        ws_ml[2 * slot + 1] = lsum;
+        for (int d = 0; d < DPL; ++d) orow[lane * DPL + d] = bad_pos ? qnan() : acc[d] * inv;
+      } else {
+        const size_t slot = ((size_t)i * nk * G + (size_t)kh * G + g) * nsplit + blockIdx.z;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) ws_o[slot * HD + lane * DPL + d] = acc[d];
+        if (lane == 0) {
+          ws_ml[2 * slot] = mx;
+          ws_ml[2 * slot + 1] = lsum;
+        }
       }
     }
   }
@@ -970,6 +1000,40 @@ extern "C" int qasr_decode_attention_f32(float* out, float* q, const float* k, c
   if (rc != QASR_OK) return rc;
   return attention_impl(out, q, k_cache, v_cache, 1, pos + 1, n_heads, n_kv_heads, head_dim, scale, pos,
                         workspace, workspace_floats, stream);
+}
+
+extern "C" int qasr_batched_decode_attention_f32(float* out, const float* q, const float* k_cache,
+                                                 const float* v_cache, size_t cache_rows,
+                                                 const int32_t* positions, size_t batch, size_t n_heads,
+                                                 size_t n_kv_heads, size_t head_dim, float scale,
+                                                 void* stream) {
+  if (batch == 0 || n_heads == 0) return QASR_OK;
+  QASR_REQUIRE(out && q && k_cache && v_cache && positions, "batched_decode_attention: null pointer");
+  QASR_REQUIRE(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+               "batched_decode_attention: n_heads must be a multiple of n_kv_heads");
+  QASR_REQUIRE(batch <= 0x7fffffffu && n_kv_heads <= 65535 && cache_rows > 0 && cache_rows < 0x40000000u,
+               "batched_decode_attention: size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(batch, cache_rows, &n) && mul_ok(n, n_kv_heads * head_dim, &n) &&
+                   mul_ok(batch, n_heads * head_dim, &n),
+               "batched_decode_attention: size overflows");
+  const size_t G = n_heads / n_kv_heads;
+  const bool shape = (head_dim == 128 && (G == 1 || G == 2)) || (head_dim == 64 && (G == 1 || G == 2 || G == 4));
+  if (!shape || !aligned16(out) || !aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
+    return fail(QASR_ERR_UNSUPPORTED,
+                "batched_decode_attention: needs head_dim 128 with n_heads/n_kv_heads <= 2 (or 64 with <= 4) "
+                "and 16-byte aligned buffers");
+  const DecodeBatch b{positions, (long long)cache_rows, out};
+  const dim3 grid((unsigned)batch, (unsigned)n_kv_heads, 1);
+  hipStream_t st = as_stream(stream);
+  const int nk = (int)n_kv_heads, kps = (int)cache_rows;
+#define QASR_BATCH(HD, GG)                                                                        \
+  if (head_dim == HD && G == GG)                                                                  \
+    attention_decode_split_kernel<HD, GG, false, true><<<grid, 256, 0, st>>>(                    \
+        q, k_cache, v_cache, 1, kps, nk, scale, 0, kps, nullptr, nullptr, DecodePre{}, b);
+  QASR_BATCH(128, 1) QASR_BATCH(128, 2) QASR_BATCH(64, 1) QASR_BATCH(64, 2) QASR_BATCH(64, 4)
+#undef QASR_BATCH
+  return launch_status("batched_decode_attention");
 }
 
 extern "C" size_t qasr_causal_attention_workspace_floats(size_t seq_q, size_t n_heads,

@@ -623,10 +623,12 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kGmBK = 64;           // K granularity of the GEMM path
-// GEMM epilogues: y = acc * scale; + bias; or the prefill SwiGLU of each
-// interleaved (gate, up) row pair, y[t, n/2] = swiglu(y[t, n], y[t, n + 1]),
-// an output row of N/2 (kernels::swiglu_multiply after the gate/up projection)
-enum GemmEpi { kGemmRows = 0, kGemmBias = 1, kGemmSwiglu = 2 };
+// GEMM epilogues: y = acc * scale; + bias; or the SwiGLU of each interleaved
+// (gate, up) row pair, y[t, n/2] = swiglu(y[t, n], y[t, n + 1]), an output row
+// of N/2 -- in the prefill form (kernels::swiglu_multiply's fast_exp blocks and
+// expf tail after the gate/up projection) or the decode loop's form
+// (g / (1 + expf(-g)) * u, decoder.rs:916-921) for batched decode streams
+enum GemmEpi { kGemmRows = 0, kGemmBias = 1, kGemmSwiglu = 2, kGemmSwigluLibm = 3 };
 // K chunks in flight per thread in the LDS-staged kernel (2 and 3 measured
 // slower: the extra registers cost more than the latency they hide)
 constexpr int kGemmPrefetch = 1;
@@ -677,8 +679,9 @@ QASR_DEV void tile_of(const TileMap& m, unsigned b, unsigned& bx, unsigned& by) 
 // of chunk c + NPF are issued right after chunk c is staged into LDS.
 // Rows n..n+3 (n a multiple of 4) of token t are the interleaved pairs of
 // outputs n/2 and n/2 + 1 of the SwiGLU row (N/2 wide).
+template <int EPI>
 QASR_DEV void swiglu_store(float* y, const float (&res)[4], int t, int n, int N) {
-  const int inter = N >> 1, j = n >> 1, fast_end = inter & ~7;
+  const int inter = N >> 1, j = n >> 1, fast_end = EPI == kGemmSwiglu ? inter & ~7 : 0;
   float* row = y + (size_t)t * inter;
   if (n + 1 < N) row[j] = swiglu_ref(res[0], res[1], j < fast_end);
   if (n + 3 < N) row[j + 1] = swiglu_ref(res[2], res[3], j + 1 < fast_end);
@@ -820,8 +823,8 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
           res[v] = acc[i][j][4 * q + v] * scales[nv];
           if constexpr (EPI == kGemmBias) res[v] += bias[nv];
         }
-        if constexpr (EPI == kGemmSwiglu) {
-          swiglu_store(y, res, t, n, N);
+        if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
+          swiglu_store<EPI>(y, res, t, n, N);
         } else if (vec_out && n + 3 < N) {
           *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
         } else {
@@ -914,8 +917,8 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
       if constexpr (EPI == kGemmBias) res[v] += bias[nv];
     }
     if (t >= T) continue;
-    if constexpr (EPI == kGemmSwiglu) {
-      swiglu_store(y, res, t, n, N);
+    if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
+      swiglu_store<EPI>(y, res, t, n, N);
     } else if (vec_out && n + 3 < N) {
       *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
     } else {
@@ -1223,6 +1226,17 @@ extern "C" int qasr_gate_up_swiglu_int8_f32(float* out, const float* x, const in
     launch_rows<kEpiSwiglu>((int)(in_dim / 1024), r, (unsigned)((rows + 4 * r - 1) / (4 * r)), st,
                             out, x, w_gate_up, scales_gate_up, nullptr, (int)in_dim, (int)rows,
                             nullptr);
+  } else if (w8a32_gemm_shape(seq_len, in_dim, w_gate_up, x)) {
+    // several decode streams: the matrix-core GEMM with the loop's SwiGLU in its epilogue
+    GemmSet set{};
+    set.y[0] = out;
+    set.w[0] = w_gate_up;
+    set.s[0] = scales_gate_up;
+    set.b[0] = nullptr;
+    set.N[0] = (int)rows;
+    set.n = 1;
+    if (!launch_w8a32_gemm<kGemmSwigluLibm>(set, x, (int)seq_len, (int)in_dim, st))
+      return fail(QASR_ERR_UNSUPPORTED, "gate_up_swiglu_int8: the GEMM kernel cannot run this shape");
   } else {
     const long long items = (long long)seq_len * (long long)intermediate;
     gate_up_swiglu_w8a32_pairs_kernel<false><<<(unsigned)((items + 3) / 4), 256, 0, st>>>(

@@ -213,3 +213,87 @@ class DecoderInt8:
         """The cache now holds rows 0..pos (decoder.rs:926)."""
         pos = self._check_pos(pos, "finish")
         self.kv.len = pos + 1
+
+
+class DecoderInt8Batched:
+    """B independent decode streams through the INT8 decoder in one pass per
+    layer: the reference's decode step (decoder.rs:848-965) for every stream,
+    each at its own position (its own cache length), batched on the device.
+
+    Each stream has its own KV cache with the reference's layout; layer l's
+    blocks of all streams are ``k[l]``/``v[l]`` = ``[batch, cache_rows, kv_dim]``
+    (stream m's block is what the reference's attention reads for it). Per
+    layer, in the reference's order, over all streams at once:
+      residual add + input RMSNorm; the q/k/v projections (one matrix-core
+      launch for the three, the reference's W8A32 arithmetic); q/k head
+      RMSNorm + RoPE at each stream's position with its K/V rows stored into
+      its cache; attention of each stream over its own rows 0..pos; o;
+      residual add + post-attention RMSNorm; gate/up with the decode loop's
+      SwiGLU in the GEMM epilogue; down.
+    Then the last residual add + final RMSNorm and the lm_head with each
+    stream's greedy argmax. ``positions`` (device int32) holds each stream's
+    position; ``finish`` advances them all by one (decoder.rs:926).
+    """
+
+    def __init__(self, weights: dict, hidden: int, intermediate: int, n_layers: int, batch: int,
+                 cache_rows: int, n_heads: int = 16, n_kv_heads: int = 8, head_dim: int = 128,
+                 eps: float = 1e-6, theta: float = 1e6, vocab: int | None = None, device="cuda"):
+        self.w = weights
+        self.H, self.I, self.L, self.B = hidden, intermediate, n_layers, batch
+        self.nq, self.nk, self.hd = n_heads, n_kv_heads, head_dim
+        self.eps, self.theta = eps, theta
+        self.lm = weights.get("lm_head") or weights["tok_embeddings"]  # tied weights: decoder.rs:951-954
+        self.vocab = vocab if vocab is not None else self.lm.out_dim
+        self.rows = cache_rows
+        kv = n_kv_heads * head_dim
+        f32 = dict(dtype=torch.float32, device=device)
+        B = batch
+        self.k = torch.zeros(n_layers, B * cache_rows * kv, **f32)
+        self.v = torch.zeros(n_layers, B * cache_rows * kv, **f32)
+        self.positions = torch.zeros(B, dtype=torch.int32, device=device)
+        self.x = torch.zeros(B * hidden, **f32)
+        self.x_norm = torch.empty(B * hidden, **f32)
+        self.q = torch.empty(B * n_heads * head_dim, **f32)
+        self.kk = torch.empty(B * kv, **f32)
+        self.vv = torch.empty(B * kv, **f32)
+        self.attn = torch.empty(B * n_heads * head_dim, **f32)
+        self.proj = torch.empty(B * hidden, **f32)
+        self.ffn = torch.empty(B * intermediate, **f32)
+        self.down = torch.empty(B * hidden, **f32)
+        self.logits = torch.empty(B * self.vocab, **f32)
+        self.tokens = torch.empty(B, dtype=torch.int32, device=device)
+        self.rope = K.RopeCache(device)
+        self.rope.ensure(cache_rows, head_dim, theta)
+        self.scale = 1.0 / math.sqrt(head_dim)
+
+    def decode(self, embeds: torch.Tensor) -> None:
+        """One token for every stream (``embeds``: [batch, hidden]) at its
+        position: ``tokens`` receives each stream's greedy next token,
+        ``x_norm`` the final normed hidden states. Positions outside the cache
+        give NaN rows and write no cache row."""
+        H, I, B, nq, nk, hd, eps = self.H, self.I, self.B, self.nq, self.nk, self.hd, self.eps
+        self.x.copy_(embeds[:B * H])
+        for l, lw in enumerate(self.w["layers"]):
+            if l == 0:
+                K.rms_norm(self.x_norm, self.x, lw["input_norm"], B, H, eps)
+            else:  # previous layer's residual add + this layer's input norm
+                K.add_rms_norm(self.x, self.down, lw["input_norm"], self.x_norm, B, H, eps)
+            K.linear_nobias_int8_multi([self.q, self.kk, self.vv], [lw["wq"], lw["wk"], lw["wv"]],
+                                       self.x_norm, B, H)
+            kb, vb = self.k[l], self.v[l]
+            K.head_rms_norm_rope_kv(self.q, self.kk, self.vv, lw["q_norm"], lw["k_norm"], self.rope,
+                                    self.positions, 0, B, nq, nk, hd, eps, kb, vb, self.rows)
+            K.batched_decode_attention(self.attn, self.q, kb, vb, self.rows, self.positions, B, nq, nk, hd,
+                                       self.scale)
+            wo = lw["wo"]
+            K.linear_nobias_int8(self.proj, self.attn, wo.data, wo.scales, B, nq * hd, H)
+            K.add_rms_norm(self.x, self.proj, lw["post_attn_norm"], self.x_norm, B, H, eps)
+            K.gate_up_swiglu_int8(self.ffn, self.x_norm, lw["gate_up"], B, H, I)
+            dn = lw["down"]
+            K.linear_nobias_int8(self.down, self.ffn, dn.data, dn.scales, B, I, H)
+        K.add_rms_norm(self.x, self.down, self.w["norm"], self.x_norm, B, H, eps)
+        K.lm_head_int8_argmax(self.tokens, self.logits, self.x_norm, self.lm, B, H, self.vocab)
+
+    def finish(self) -> None:
+        """Every stream's cache now holds one more row (decoder.rs:926)."""
+        self.positions.add_(1)

@@ -219,6 +219,21 @@ def causal_attention(out, q, k, v, seq_q: int, seq_k: int, n_heads: int, n_kv_he
               q_offset, _stream())
 
 
+def batched_decode_attention(out, q, k_cache, v_cache, cache_rows: int, positions, batch: int, n_heads: int,
+                             n_kv_heads: int, head_dim: int, scale: float) -> None:
+    """Decode attention of ``batch`` streams, each over rows 0..positions[m] of its
+    own cache block ``[batch, cache_rows, n_kv_heads * head_dim]`` (decoder.rs:900-903
+    per stream)."""
+    kv = n_kv_heads * head_dim
+    _need(out, F32, batch * n_heads * head_dim, "out")
+    _need(q, F32, batch * n_heads * head_dim, "q")
+    _need(k_cache, F32, batch * cache_rows * kv, "k_cache")
+    _need(v_cache, F32, batch * cache_rows * kv, "v_cache")
+    _need(positions, I32, batch, "positions")
+    _lib.call("qasr_batched_decode_attention_f32", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), cache_rows,
+              _ptr(positions), batch, n_heads, n_kv_heads, head_dim, scale, _stream())
+
+
 def attention_workspace(seq_q: int, n_heads: int, head_dim: int, device="cuda") -> torch.Tensor:
     """Workspace for causal_attention_split: allocate once, reuse per call on
     one stream."""

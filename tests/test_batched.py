@@ -173,3 +173,88 @@ def test_batched_projection_rejects_unsupported_shapes(dev):
         K.linear_w8a8_packed(y, K.QuantWeight(w.data, w.scales, 64, 1024), xq, xs, 4, 1024, 64)
     assert e.value.code == _lib.QASR_ERR_UNSUPPORTED
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("H,I,B", [(2048, 6144, 9), (1024, 3072, 3)])
+def test_batched_decode_step_matches_the_oracle_per_stream(tmp_path, dev, H, I, B):
+    """DecoderInt8Batched (B streams, each at its own position over its own
+    cache) against the oracle's decode step (decoder.rs:848-965) run stream
+    by stream: final hidden state, logits, the new K/V rows of every layer and
+    the token, over two consecutive steps. B = 9 takes the matrix-core paths
+    (8+ rows), B = 3 the per-row ones. Tolerance as for the single-stream
+    decode step (chained kernels, rel/abs 1e-4)."""
+    from oracle.decoder import decode_int8_step
+    from qwenasr_amd.decoder import DecoderInt8Batched
+    from tests.test_decoder_step import _load
+    from tests.test_oracle import small_decoder
+
+    L, vocab, rows, TOL = 2, 1000, 512, 1e-4
+    r = np.random.default_rng([55, H, B])
+    w = small_decoder(r, H, I, L, NQ, NK, HD, vocab)
+    dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev)
+    kv = NK * HD
+    pos = np.array([0, 300, 7, 64, 511 - 2, 1, 128, 255, 33][:B], np.int32)
+    kc = r.standard_normal((B, L, rows, kv)).astype(np.float32)  # earlier contexts, one per stream
+    vc = r.standard_normal((B, L, rows, kv)).astype(np.float32)
+    for l in range(L):
+        dec.k[l].view(B, rows, kv).copy_(torch.from_numpy(kc[:, l].copy()))
+        dec.v[l].view(B, rows, kv).copy_(torch.from_numpy(vc[:, l].copy()))
+    dec.positions.copy_(torch.from_numpy(pos))
+    for step in range(2):
+        x = r.standard_normal((B, H)).astype(np.float32)
+        print(f"[batched] decode step {step} H={H} B={B}", flush=True)
+        dec.decode(torch.from_numpy(x.ravel().copy()).to(dev))
+        torch.cuda.synchronize()
+        xn = dec.x_norm.view(B, H).cpu().numpy()
+        lg = dec.logits.view(B, vocab).cpu().numpy()
+        tok = dec.tokens.cpu().numpy()
+        for m in range(B):
+            p = int(pos[m]) + step
+            t_ref, xn_ref, lg_ref = decode_int8_step(w, kc[m], vc[m], p, x[m], NQ, NK, HD, threads=8)
+            np.testing.assert_allclose(xn[m], xn_ref, rtol=TOL, atol=TOL, err_msg=f"stream {m} step {step}")
+            np.testing.assert_allclose(lg[m], lg_ref, rtol=TOL, atol=TOL, err_msg=f"stream {m} step {step}")
+            for l in range(L):
+                kg = dec.k[l].view(B, rows, kv)[m, p].cpu().numpy()
+                vg = dec.v[l].view(B, rows, kv)[m, p].cpu().numpy()
+                np.testing.assert_allclose(kg, kc[m, l, p], rtol=TOL, atol=TOL, err_msg=f"k stream {m} layer {l}")
+                np.testing.assert_allclose(vg, vc[m, l, p], rtol=TOL, atol=TOL, err_msg=f"v stream {m} layer {l}")
+            top2 = np.sort(lg_ref)[-2:]
+            if top2[1] - top2[0] > 2 * TOL * (1 + abs(top2[1])):
+                assert int(tok[m]) == t_ref, (m, step)
+        dec.finish()
+    assert torch.equal(dec.positions.cpu(), torch.from_numpy(pos + 2))
+
+
+def test_batched_decode_attention_bad_position_and_graph_replay(dev):
+    """A stream at a position outside its cache gets a NaN row (the others
+    are unaffected), and the batched decode attention captured in a HIP graph
+    gives the eager result on every replay."""
+    from qwenasr_amd import kernels as K
+
+    B, rows, kv = 6, 300, NK * HD
+    r = np.random.default_rng(56)
+    q = torch.from_numpy(r.standard_normal(B * NQ * HD).astype(np.float32)).to(dev)
+    kc = torch.from_numpy(r.standard_normal(B * rows * kv).astype(np.float32)).to(dev)
+    vc = torch.from_numpy(r.standard_normal(B * rows * kv).astype(np.float32)).to(dev)
+    pos = torch.tensor([0, 299, 300, -1, 150, 64], dtype=torch.int32, device=dev)
+    out = torch.empty(B * NQ * HD, device=dev)
+    K.batched_decode_attention(out, q, kc, vc, rows, pos, B, NQ, NK, HD, HD ** -0.5)
+    torch.cuda.synchronize()
+    o = out.view(B, NQ * HD).cpu().numpy()
+    assert np.isnan(o[2]).all() and np.isnan(o[3]).all()
+    qn, kn, vn = q.cpu().numpy(), kc.cpu().numpy().reshape(B, rows, kv), vc.cpu().numpy().reshape(B, rows, kv)
+    for m in (0, 1, 4, 5):
+        p = int(pos[m])
+        ref = oracle.causal_attention(qn.reshape(B, -1)[m], kn[m, :p + 1].ravel(), vn[m, :p + 1].ravel(), 1, p + 1,
+                                      NQ, NK, HD, HD ** -0.5, p)
+        assert_close(o[m], ref, 1e-5, 1e-5, f"stream {m}")
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        K.batched_decode_attention(out, q, kc, vc, rows, pos, B, NQ, NK, HD, HD ** -0.5)
+    for rep in range(3):
+        out.fill_(0.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.isnan(), eager.isnan()) and torch.equal(out.nan_to_num(), eager.nan_to_num()), rep
