@@ -268,3 +268,41 @@ def test_add_layer_norm_validation():
     assert rc("qasr_add_layer_norm_f32", x, NULL, other, other, ctypes.c_void_p(0x200000), 4, 8, 1e-5,
               NULL) == _lib.QASR_ERR_INVALID_ARG
     assert "null" in last_error()
+
+
+def _kernel_names_in_library() -> set[str]:
+    """The device kernels the built library launches, as ``name<args>`` (their
+    host-side launch stubs, demangled; namespaces dropped)."""
+    nm = subprocess.run(["nm", "-C", str(_lib.LIB_PATH)], capture_output=True, text=True, check=True).stdout
+    names = set()
+    for line in nm.splitlines():
+        m = re.search(r"(?:^|::)([A-Za-z_][A-Za-z0-9_]*_kernel(?:<[^()]*>)?)\(", line.split(" ", 2)[-1])
+        if m:
+            names.add(re.sub(r"\(qasr::[A-Za-z_:]+\)", "", m.group(1)).replace(" ", ""))
+    return names
+
+
+def test_traffic_profile_names_current_kernels():
+    """bench.py's roofline.traffic comes from profiles/traffic.json (measured
+    rocprofv3 HBM bytes per launch). Every kernel that file names must still
+    exist in the built library with the same template arguments, so a renamed
+    or re-parameterised kernel cannot silently inherit a stale measurement."""
+    import json
+
+    _lib.lib()
+    have = _kernel_names_in_library()
+    assert any(n.startswith("rms_norm_vec_kernel<") for n in have), sorted(have)[:10]
+    data = json.loads((ROOT / "profiles" / "traffic.json").read_text())
+    stale = []
+    for workload, entries in data.items():
+        if not isinstance(entries, dict):
+            continue
+        for label, entry in entries.items():
+            if not isinstance(entry, dict) or "kernel" not in entry:
+                continue
+            for kname in entry["kernel"].split(" + "):
+                if "whole step" in kname:
+                    continue
+                if kname.replace(" ", "") not in have:
+                    stale.append(f"{workload}/{label}: {kname}")
+    assert not stale, f"kernels in profiles/traffic.json not in the library: {stale}"
