@@ -492,17 +492,31 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
 #pragma unroll
       for (int c = 0; c < C4; ++c) qv[g][c] = ld4(qr + g * HD, 4 * c);
   }
-  for (; t0 < k_end; t0 += 64) {
-    float4 kk[C4];
-    float vv[16][DPL];
-    load_tile(t0, kk, vv);
-    // every load issued before the first use (the scheduler would otherwise
-    // sink the v loads below the QK arithmetic: two round trips)
-    __builtin_amdgcn_sched_barrier(0);
+  // The remaining tiles, two register buffers deep: the next tile's loads are
+  // issued before the current tile is processed, so a wave keeps a tile in
+  // flight while it computes (a stream's many tiles in the batched form).
+  // Every load of a tile is issued before its first use (the scheduler would
+  // otherwise sink the v loads below the QK arithmetic: two round trips).
+  auto run_tile = [&](int t, float4 (&kk)[C4], float (&vv)[16][DPL]) {
     float vlast[DPL];
     bool hit = false;
-    if constexpr (PRE) hit = patch(t0, kk, vlast, kpos_p, vpos_p);
-    process_tile(t0, kk, vv, hit, vlast);
+    if constexpr (PRE) hit = patch(t, kk, vlast, kpos_p, vpos_p);
+    process_tile(t, kk, vv, hit, vlast);
+  };
+  if (t0 < k_end) {
+    float4 kka[C4], kkb[C4];
+    float vva[16][DPL], vvb[16][DPL];
+    load_tile(t0, kka, vva);
+    for (; t0 < k_end; t0 += 128) {
+      const bool more = t0 + 64 < k_end;  // uniform per wave
+      if (more) load_tile(t0 + 64, kkb, vvb);
+      __builtin_amdgcn_sched_barrier(0);
+      run_tile(t0, kka, vva);
+      if (!more) break;
+      if (t0 + 128 < k_end) load_tile(t0 + 128, kka, vva);
+      __builtin_amdgcn_sched_barrier(0);
+      run_tile(t0 + 64, kkb, vvb);
+    }
   }
   // merge the 4 waves
   if (lane == 0) {
