@@ -377,7 +377,7 @@ int qasr_gate_up_swiglu_w8a8_packed(float* out, const int8_t* w_packed,
  * linear_nobias_int8 (kernels/mod.rs:650-661, one W8A32 matvec per token) with
  * the activation quantized per row, as the batched gate/up projection does;
  * the integer dots are exact, so y equals the oracle's bit for bit. in_dim
- * 1024 or 2048, out_dim % 128 == 0, 16-byte aligned buffers
+ * 1024, 2048, 3072, 4096 or 6144, out_dim % 128 == 0, 16-byte aligned buffers
  * (QASR_ERR_UNSUPPORTED otherwise). */
 int qasr_linear_w8a8_packed(float* y, const int8_t* w_packed, const float* scales,
                             const int8_t* xq, const float* x_scales, size_t batch,
@@ -396,8 +396,9 @@ int qasr_linear_w8a8_packed(float* y, const int8_t* w_packed, const float* scale
  * (the reference's KvCache layer layout, one block per stream). A position
  * outside the RoPE table or the cache gives a NaN q row and no cache write.
  * Bit-identical to qasr_linear_w8a8_packed followed by
- * qasr_head_rms_norm_rope_kv_f32 with positions. head_dim 128, in_dim 1024 or
- * 2048, 16-byte aligned buffers (QASR_ERR_UNSUPPORTED otherwise). No reference
+ * qasr_head_rms_norm_rope_kv_f32 with positions. head_dim 128, in_dim as for
+ * qasr_linear_w8a8_packed, 16-byte aligned buffers (QASR_ERR_UNSUPPORTED
+ * otherwise). No reference
  * counterpart as one call (the reference decodes one stream at a time). */
 int qasr_qkv_heads_w8a8_packed(float* q_out, float* k_cache, float* v_cache, size_t cache_rows,
                                const int8_t* w_packed, const float* scales, const int8_t* xq,

@@ -37,7 +37,6 @@ namespace {
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
 constexpr int kHdRows = 128;   // W rows per workgroup: one head
-constexpr int kHdTok = 32;     // streams per workgroup
 constexpr int kHdWaves = 8;
 constexpr int kHdPF = 3;       // k-steps of W in flight per wave
 constexpr int kHdTPitch = 136; // floats per stream row of the dequantized tile (pad: banks)
@@ -68,15 +67,17 @@ struct HeadsArgs {
   float eps;
 };
 
-template <int KS, int MODE>
+template <int KS, int MODE, int TOK>  // K = 64 KS; TOK streams per workgroup (16 or 32)
 __global__ __launch_bounds__(64 * kHdWaves) void gemm_w8a8_heads_kernel(HeadsArgs a) {
   constexpr int K = KS * 64;
   constexpr int KW = KS / 2;           // k-steps per wave (one K half)
+  constexpr int MT = TOK / 16;         // 16-stream MFMA tiles
   constexpr int SLOTS = K / 16;        // 16-byte slots per staged row
-  constexpr int XU = kHdTok * SLOTS / (64 * kHdWaves);  // staging loads per thread
+  constexpr int XU = TOK * SLOTS / (64 * kHdWaves);  // staging loads per thread
   constexpr int PF = kHdPF;
   constexpr size_t ROW_TILE = (size_t)KS * 1024;  // bytes of one 16-row block of packed W
-  static_assert(XU * 64 * kHdWaves == kHdTok * SLOTS, "the staging covers the tile");
+  static_assert(KS % 2 == 0 && (MT == 1 || MT == 2), "K halves; one or two stream tiles");
+  static_assert(XU * 64 * kHdWaves == TOK * SLOTS, "the staging covers the tile");
   extern __shared__ __align__(16) int8_t lds[];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -95,7 +96,7 @@ __global__ __launch_bounds__(64 * kHdWaves) void gemm_w8a8_heads_kernel(HeadsArg
     tile_m = b % a.m_tiles;
     tile_n = b / a.m_tiles;
   }
-  const int n0 = tile_n * kHdRows, m0 = tile_m * kHdTok;
+  const int n0 = tile_n * kHdRows, m0 = tile_m * TOK;
 
   // Issue order: the stream rows, the W window, the epilogue operands.
   v4i_t xr[XU];
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(64 * kHdWaves) void gemm_w8a8_heads_kernel(HeadsArg
   float4 sc[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) sc[i] = *reinterpret_cast<const float4*>(a.scales + n0 + 32 * rg + 16 * i + 4 * g);
-  const int mt = m0 + 16 * kq + r;
+  const int mt = m0 + (MT == 2 ? 16 * kq : 0) + r;
   const float xsv = a.xs[mt < a.batch ? mt : a.batch - 1];
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -129,20 +130,20 @@ __global__ __launch_bounds__(64 * kHdWaves) void gemm_w8a8_heads_kernel(HeadsArg
   }
   lds_barrier();
 
-  v4i_t acc[2][2];
+  v4i_t acc[2][MT];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v4i_t{0, 0, 0, 0};
+    for (int j = 0; j < MT; ++j) acc[i][j] = v4i_t{0, 0, 0, 0};
   // B fragment of stream tile j at global k-step s: stream row 16j + r, bytes
   // [64s + 16g, +16) = slot 4s + g
   auto xfrag = [&](int s, int j) -> v4i_t {
     return *reinterpret_cast<const v4i_t*>(lds + (16 * j + r) * K + 16 * ((4 * s + g) ^ r));
   };
   const int k0 = kq * KW;
-  v4i_t bcur[2];
+  v4i_t bcur[MT];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) bcur[j] = xfrag(k0, j);
+  for (int j = 0; j < MT; ++j) bcur[j] = xfrag(k0, j);
 #pragma unroll
   for (int s0 = 0; s0 < KW; s0 += PF) {
 #pragma unroll
@@ -160,58 +161,77 @@ __global__ __launch_bounds__(64 * kHdWaves) void gemm_w8a8_heads_kernel(HeadsArg
         // keep the prefetch and the next fragments issued here (the scheduler
         // would sink each load next to its use)
         __builtin_amdgcn_sched_barrier(0);
-        v4i_t bn[2];
+        v4i_t bn[MT];
         if (s + 1 < KW) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) bn[j] = xfrag(k0 + s + 1, j);
+          for (int j = 0; j < MT; ++j) bn[j] = xfrag(k0 + s + 1, j);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
+          for (int j = 0; j < MT; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bcur[j], acc[i][j], 0, 0, 0);
         if (s + 1 < KW) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) bcur[j] = bn[j];
+          for (int j = 0; j < MT; ++j) bcur[j] = bn[j];
         }
       }
     }
   }
 
-  // The two K halves of a row group: wave kq keeps stream tile kq and adds
-  // its partner's partial sums for it (constant register indices only).
+  // The two K halves of a row group: with two stream tiles wave kq keeps
+  // tile kq and adds its partner's partial sums for it; with one, wave 0 of
+  // the pair adds wave 1's (constant register indices only).
   __syncthreads();  // X no longer read
-  v4i_t give[2], mine[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    give[i] = kq == 0 ? acc[i][1] : acc[i][0];
-    mine[i] = kq == 0 ? acc[i][0] : acc[i][1];
-  }
+  v4i_t mine[2];
   v4i_t* ex = reinterpret_cast<v4i_t*>(lds);  // [rg][receiver kq][i][lane]
+  if constexpr (MT == 2) {
+    v4i_t give[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) ex[((rg * 2 + (1 - kq)) * 2 + i) * 64 + lane] = give[i];
-  __syncthreads();
+    for (int i = 0; i < 2; ++i) {
+      give[i] = kq == 0 ? acc[i][1] : acc[i][0];
+      mine[i] = kq == 0 ? acc[i][0] : acc[i][MT - 1];
+    }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) mine[i] += ex[((rg * 2 + kq) * 2 + i) * 64 + lane];
+    for (int i = 0; i < 2; ++i) ex[((rg * 2 + (1 - kq)) * 2 + i) * 64 + lane] = give[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) mine[i] += ex[((rg * 2 + kq) * 2 + i) * 64 + lane];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) mine[i] = acc[i][0];
+    if (kq == 1) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) ex[(rg * 2 + i) * 64 + lane] = mine[i];
+    }
+    __syncthreads();
+    if (kq == 0) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) mine[i] += ex[(rg * 2 + i) * 64 + lane];
+    }
+  }
   __syncthreads();  // exchange area free
 
-  // Dequantize into the [32 streams][128 dims] tile: lane holds rows
-  // 32rg + 16i + 4g + {0..3} of stream 16kq + r.
+  // Dequantize into the [TOK streams][128 dims] tile: lane holds rows
+  // 32rg + 16i + 4g + {0..3} of stream tile row (MT == 2 ? 16kq : 0) + r.
   float* T = reinterpret_cast<float*>(lds);
+  if (MT == 2 || kq == 0) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    float4 v;
-    v.x = ((float)mine[i][0] * xsv) * sc[i].x;
-    v.y = ((float)mine[i][1] * xsv) * sc[i].y;
-    v.z = ((float)mine[i][2] * xsv) * sc[i].z;
-    v.w = ((float)mine[i][3] * xsv) * sc[i].w;
-    *reinterpret_cast<float4*>(T + (16 * kq + r) * kHdTPitch + 32 * rg + 16 * i + 4 * g) = v;
+    for (int i = 0; i < 2; ++i) {
+      float4 v;
+      v.x = ((float)mine[i][0] * xsv) * sc[i].x;
+      v.y = ((float)mine[i][1] * xsv) * sc[i].y;
+      v.z = ((float)mine[i][2] * xsv) * sc[i].z;
+      v.w = ((float)mine[i][3] * xsv) * sc[i].w;
+      *reinterpret_cast<float4*>(T + ((MT == 2 ? 16 * kq : 0) + r) * kHdTPitch + 32 * rg + 16 * i + 4 * g) = v;
+    }
   }
   lds_barrier();
 
   // One stream per group of 16 threads: dims 4sub..4sub+3 and 64+4sub..
   const int tok = threadIdx.x >> 4, sub = threadIdx.x & 15;
+  if (tok >= TOK) return;  // whole waves past the tile (TOK = 16): nothing left to do
   const int m = m0 + tok;
   const bool live = m < a.batch;
   float4 x1 = *reinterpret_cast<const float4*>(T + tok * kHdTPitch + 4 * sub);
@@ -277,30 +297,48 @@ bool heads_lds_ok(size_t bytes) {
   return ok;
 }
 
+template <int KS, int MODE, int TOK>
+int launch_heads_tile(const HeadsArgs& a, unsigned grid, hipStream_t st, const char* what) {
+  const size_t lds = (size_t)TOK * KS * 64 > 16384 ? (size_t)TOK * KS * 64 : 16384;  // >= exchange + fp32 tile
+  if (!heads_lds_ok<&gemm_w8a8_heads_kernel<KS, MODE, TOK>>(lds))
+    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": device LDS too small");
+  gemm_w8a8_heads_kernel<KS, MODE, TOK><<<grid, 64 * kHdWaves, lds, st>>>(a);
+  return launch_status(what);
+}
+
+// 32-stream tiles (the staged rows shared by twice the outputs) when K <= 2048
+// and they still give at least 256 workgroups; otherwise 16-stream tiles
+// (32 x K would not fit the LDS, or the grid would leave CUs idle).
+template <int KS, int MODE>
+int launch_heads_k(HeadsArgs a, hipStream_t st, const char* what) {
+  a.n_tiles = a.N / kHdRows;
+  const size_t m32 = ((size_t)a.batch + 31) / 32, m16 = ((size_t)a.batch + 15) / 16;
+  const bool tok32 = KS <= 32 && (size_t)a.n_tiles * m32 >= 256;
+  a.m_tiles = (int)(tok32 ? m32 : m16);
+  const size_t grid = (size_t)a.n_tiles * (size_t)a.m_tiles;
+  QASR_REQUIRE(grid <= 0x7fffffffu, std::string(what) + ": grid too large");
+  if constexpr (KS <= 32) {
+    if (tok32) return launch_heads_tile<KS, MODE, 32>(a, (unsigned)grid, st, what);
+  }
+  return launch_heads_tile<KS, MODE, 16>(a, (unsigned)grid, st, what);
+}
+
 template <int MODE>
 int launch_heads_gemm(HeadsArgs a, size_t K, hipStream_t st, const char* what) {
-  a.n_tiles = a.N / kHdRows;
-  a.m_tiles = (a.batch + kHdTok - 1) / kHdTok;
-  const size_t grid = (size_t)a.n_tiles * (size_t)a.m_tiles;
-  QASR_REQUIRE(grid <= 0x7fffffffu, "w8a8 projection: grid too large");
-  const size_t lds = (size_t)kHdTok * K;  // >= the exchange (16 KiB) and the fp32 tile (16.5 KiB)
-  if (K == 1024) {
-    if (!heads_lds_ok<&gemm_w8a8_heads_kernel<16, MODE>>(lds))
-      return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": device LDS too small");
-    gemm_w8a8_heads_kernel<16, MODE><<<(unsigned)grid, 64 * kHdWaves, lds, st>>>(a);
-  } else {
-    if (!heads_lds_ok<&gemm_w8a8_heads_kernel<32, MODE>>(lds))
-      return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": device LDS too small");
-    gemm_w8a8_heads_kernel<32, MODE><<<(unsigned)grid, 64 * kHdWaves, lds, st>>>(a);
+  switch (K) {
+    case 1024: return launch_heads_k<16, MODE>(a, st, what);
+    case 2048: return launch_heads_k<32, MODE>(a, st, what);
+    case 3072: return launch_heads_k<48, MODE>(a, st, what);
+    case 4096: return launch_heads_k<64, MODE>(a, st, what);
+    default: return launch_heads_k<96, MODE>(a, st, what);  // 6144
   }
-  return launch_status(what);
 }
 
 int check_w8a8_common(const int8_t* w, const float* scales, const int8_t* xq, const float* xs,
                       size_t batch, size_t in_dim, size_t out_dim, const char* what) {
   QASR_REQUIRE(w && scales && xq && xs, std::string(what) + ": null pointer");
-  if (in_dim != 1024 && in_dim != 2048)
-    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": in_dim must be 1024 or 2048");
+  if (in_dim != 1024 && in_dim != 2048 && in_dim != 3072 && in_dim != 4096 && in_dim != 6144)
+    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": in_dim must be 1024, 2048, 3072, 4096 or 6144");
   if (out_dim % kHdRows != 0)
     return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": out_dim must be a multiple of 128");
   QASR_REQUIRE(batch <= 0x7fffffffu && out_dim <= 0x7fffffffu, std::string(what) + ": size too large");
