@@ -480,16 +480,28 @@ int qasr_decode_attention_f32(float* out, float* q, const float* k, const float*
  * = causal attention of q[m] (n_heads*head_dim, already normalised and
  * rotated) over rows 0..pos of k_cache/v_cache + m * cache_rows *
  * n_kv_heads * head_dim (the block qasr_head_rms_norm_rope_kv_f32 with
- * positions writes). The keys of a stream are not split: one workgroup per
- * (stream, kv head) walks them and normalises its output itself. A position
- * outside the cache gives a NaN row. head_dim 128 with n_heads/n_kv_heads in
- * {1, 2}, or 64 with {1, 2, 4}; 16-byte aligned buffers (QASR_ERR_UNSUPPORTED
- * otherwise). No reference counterpart as one call (the reference decodes one
- * stream at a time). */
+ * positions writes). With a workspace of at least
+ * qasr_batched_decode_attention_workspace_floats() floats, each stream's keys
+ * are cut into chunks of 512 (streams at different positions then cost the
+ * GPU evenly) and the chunks' partial results are merged in a second launch;
+ * with workspace NULL one workgroup per (stream, kv head) walks all of its
+ * keys. Both give the oracle's result within 1e-5 (the order of the key sums
+ * differs). The workspace is scratch for one call at a time on a stream. A
+ * position outside the cache gives a NaN row. head_dim 128 with
+ * n_heads/n_kv_heads in {1, 2}, or 64 with {1, 2, 4}; 16-byte aligned
+ * buffers (QASR_ERR_UNSUPPORTED otherwise); a workspace that is too small is
+ * QASR_ERR_INVALID_ARG. No reference counterpart as one call (the reference
+ * decodes one stream at a time). */
 int qasr_batched_decode_attention_f32(float* out, const float* q, const float* k_cache,
                                       const float* v_cache, size_t cache_rows,
                                       const int32_t* positions, size_t batch, size_t n_heads,
-                                      size_t n_kv_heads, size_t head_dim, float scale, void* stream);
+                                      size_t n_kv_heads, size_t head_dim, float scale, float* workspace,
+                                      size_t workspace_floats, void* stream);
+
+/* Workspace floats qasr_batched_decode_attention_f32 uses for these sizes (0:
+ * the cache is one chunk, no workspace is needed). */
+size_t qasr_batched_decode_attention_workspace_floats(size_t batch, size_t n_heads, size_t head_dim,
+                                                      size_t cache_rows);
 
 /* Workspace floats qasr_causal_attention_split_f32 can use for these sizes. */
 size_t qasr_causal_attention_workspace_floats(size_t seq_q, size_t n_heads, size_t head_dim);

@@ -289,10 +289,13 @@ struct DecodePre {
 };
 
 // Batched decode streams (BATCH): row i is stream i, its keys are rows
-// 0..positions[i] of its own cache block (k + i * cache_rows * kv_dim), the
-// key range is not split (one workgroup per stream and kv head), and the
-// workgroup writes the normalised output row itself. A position outside the
-// cache gives NaN rows.
+// 0..positions[i] of its own cache block (k + i * cache_rows * kv_dim), cut
+// into chunks of keys_per_split keys (blockIdx.z = chunk; a chunk past the
+// stream's last key has no work and returns at once). A stream whose keys
+// fit one chunk gets its normalised output row written by that workgroup;
+// a longer one leaves one partial per chunk in the workspace (gridDim.z
+// slots per (stream, head)) for attention_combine_batch_kernel. A position
+// outside the cache gives NaN rows.
 struct DecodeBatch {
   const int32_t* positions;
   long long cache_rows;
@@ -313,7 +316,12 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
   __shared__ __align__(16) float co[4][G][HD];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int quarter = lane & 3, kq = lane >> 2;  // dim quarter, key within the wave's 16
-  const int i = blockIdx.x, kh = blockIdx.y;
+  // BATCH: blockIdx.x = stream * nk + kv head. Workgroup n runs on XCD n % 8,
+  // so with the head fastest one stream's heads fall on different XCDs and
+  // every XCD gets the same share of each stream's keys (stream-fastest put
+  // all of stream m on XCD m % 8: 15% slower at positions U[0,2047]).
+  const int i = BATCH ? (int)(blockIdx.x / (unsigned)nk) : (int)blockIdx.x;
+  const int kh = BATCH ? (int)(blockIdx.x % (unsigned)nk) : (int)blockIdx.y;
   const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
   float4 qv[G][C4];
   [[maybe_unused]] bool bad_pos = false;
@@ -322,6 +330,7 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
     const long long p = batch.positions[i];
     bad_pos = p < 0 || p >= batch.cache_rows;
     k_lim = bad_pos ? 0 : (int)p + 1;
+    if ((int)blockIdx.z * keys_per_split >= max(k_lim, 1)) return;  // uniform: a chunk with no keys
     k += (size_t)i * (size_t)batch.cache_rows * kv_stride;
     v += (size_t)i * (size_t)batch.cache_rows * kv_stride;
   } else {
@@ -546,7 +555,7 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
 #pragma unroll
         for (int d = 0; d < DPL; ++d) acc[d] = __builtin_fmaf(co[w][g][lane * DPL + d], f, acc[d]);
       }
-      if constexpr (BATCH) {  // the whole key range: normalise as the merge kernel does
+      if (BATCH && k_lim <= keys_per_split) {  // the whole key range: normalise as the merge kernel does
         const float inv = lsum > 0.0f ? 1.0f / lsum : 1.0f;
         float* orow = batch.out + ((size_t)i * nk * G + (size_t)kh * G + g) * HD;
 #pragma unroll
@@ -562,6 +571,27 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
       }
     }
   }
+}
+
+// Merges the chunk partials of the batched decode streams whose keys span
+// more than one chunk, one wave per (stream, q head); the rows of the other
+// streams were written by the attention kernel itself.
+template <int HD>
+__global__ __launch_bounds__(256) void attention_combine_batch_kernel(float* __restrict__ out,
+                                                                      const float* __restrict__ ws_o,
+                                                                      const float* __restrict__ ws_ml,
+                                                                      const int32_t* __restrict__ positions,
+                                                                      long long cache_rows, int heads,
+                                                                      long long rows_heads, int nchunk,
+                                                                      int keys_per_chunk) {
+  const int lane = threadIdx.x & 63;
+  const long long rh = (long long)blockIdx.x * 4 + threadIdx.x / 64;  // stream * heads + head
+  if (rh >= rows_heads) return;
+  const long long p = positions[rh / heads];
+  if (p < 0 || p >= cache_rows || p + 1 <= keys_per_chunk) return;
+  const int used = (int)((p + keys_per_chunk) / keys_per_chunk);
+  merge_splits<HD>(out + (size_t)rh * HD, ws_o + (size_t)rh * nchunk * HD, ws_ml + (size_t)rh * nchunk * 2,
+                   used, lane);
 }
 
 // Merges the partials of every (row, head), one wave each.
@@ -1016,11 +1046,28 @@ extern "C" int qasr_decode_attention_f32(float* out, float* q, const float* k, c
                         workspace, workspace_floats, stream);
 }
 
+// Keys per chunk of the batched decode attention: 512 (a 2 MB stream-head
+// walk becomes at most 4 workgroups, which evens out streams at different
+// positions), more for caches over 32768 rows so that a row has at most 64
+// chunks (one merge wave's lanes).
+static size_t batched_chunk_keys(size_t cache_rows) {
+  const size_t c = (cache_rows + kMaxSplits - 1) / kMaxSplits;
+  const size_t r = (c + 63) / 64 * 64;
+  return r > 512 ? r : 512;
+}
+
+extern "C" size_t qasr_batched_decode_attention_workspace_floats(size_t batch, size_t n_heads, size_t head_dim,
+                                                                 size_t cache_rows) {
+  if (cache_rows == 0) return 0;
+  const size_t nchunk = (cache_rows + batched_chunk_keys(cache_rows) - 1) / batched_chunk_keys(cache_rows);
+  return nchunk <= 1 ? 0 : batch * n_heads * nchunk * (head_dim + 2);
+}
+
 extern "C" int qasr_batched_decode_attention_f32(float* out, const float* q, const float* k_cache,
                                                  const float* v_cache, size_t cache_rows,
                                                  const int32_t* positions, size_t batch, size_t n_heads,
                                                  size_t n_kv_heads, size_t head_dim, float scale,
-                                                 void* stream) {
+                                                 float* workspace, size_t workspace_floats, void* stream) {
   if (batch == 0 || n_heads == 0) return QASR_OK;
   QASR_REQUIRE(out && q && k_cache && v_cache && positions, "batched_decode_attention: null pointer");
   QASR_REQUIRE(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
@@ -1037,14 +1084,31 @@ extern "C" int qasr_batched_decode_attention_f32(float* out, const float* q, con
     return fail(QASR_ERR_UNSUPPORTED,
                 "batched_decode_attention: needs head_dim 128 with n_heads/n_kv_heads <= 2 (or 64 with <= 4) "
                 "and 16-byte aligned buffers");
+  // chunked when a workspace is given, else one workgroup per (stream, kv head) over all its keys
+  const size_t need = qasr_batched_decode_attention_workspace_floats(batch, n_heads, head_dim, cache_rows);
+  QASR_REQUIRE(!workspace || workspace_floats >= need,
+               "batched_decode_attention: workspace smaller than "
+               "qasr_batched_decode_attention_workspace_floats()");
+  const bool chunked = workspace && need > 0;
+  const int kpc = chunked ? (int)batched_chunk_keys(cache_rows) : (int)cache_rows;
+  const int nchunk = (int)((cache_rows + kpc - 1) / kpc);
+  const size_t rows_heads = batch * n_heads;
+  float* ws_o = chunked ? workspace : nullptr;
+  float* ws_ml = chunked ? workspace + rows_heads * nchunk * head_dim : nullptr;
   const DecodeBatch b{positions, (long long)cache_rows, out};
-  const dim3 grid((unsigned)batch, (unsigned)n_kv_heads, 1);
+  QASR_REQUIRE(batch * n_kv_heads <= 0x7fffffffu, "batched_decode_attention: batch * n_kv_heads too large");
+  const dim3 grid((unsigned)(batch * n_kv_heads), 1, (unsigned)nchunk);
   hipStream_t st = as_stream(stream);
-  const int nk = (int)n_kv_heads, kps = (int)cache_rows;
-#define QASR_BATCH(HD, GG)                                                                        \
-  if (head_dim == HD && G == GG)                                                                  \
-    attention_decode_split_kernel<HD, GG, false, true><<<grid, 256, 0, st>>>(                    \
-        q, k_cache, v_cache, 1, kps, nk, scale, 0, kps, nullptr, nullptr, DecodePre{}, b);
+  const int nk = (int)n_kv_heads;
+#define QASR_BATCH(HD, GG)                                                                                 \
+  if (head_dim == HD && G == GG) {                                                                         \
+    attention_decode_split_kernel<HD, GG, false, true><<<grid, 256, 0, st>>>(                             \
+        q, k_cache, v_cache, 1, (int)cache_rows, nk, scale, 0, kpc, ws_o, ws_ml, DecodePre{}, b);          \
+    if (chunked)                                                                                           \
+      attention_combine_batch_kernel<HD><<<(unsigned)((rows_heads + 3) / 4), 256, 0, st>>>(               \
+          out, ws_o, ws_ml, positions, (long long)cache_rows, (int)n_heads, (long long)rows_heads, nchunk, \
+          kpc);                                                                                            \
+  }
   QASR_BATCH(128, 1) QASR_BATCH(128, 2) QASR_BATCH(64, 1) QASR_BATCH(64, 2) QASR_BATCH(64, 4)
 #undef QASR_BATCH
   return launch_status("batched_decode_attention");

@@ -219,11 +219,23 @@ def causal_attention(out, q, k, v, seq_q: int, seq_k: int, n_heads: int, n_kv_he
               q_offset, _stream())
 
 
+def batched_decode_workspace(batch: int, n_heads: int, head_dim: int, cache_rows: int,
+                             device="cuda") -> torch.Tensor | None:
+    """Workspace for batched_decode_attention's chunked form (None if the cache
+    is a single chunk): allocate once, reuse per call on one stream."""
+    n = _lib.lib().qasr_batched_decode_attention_workspace_floats(batch, n_heads, head_dim, cache_rows)
+    return torch.empty(n, dtype=F32, device=device) if n else None
+
+
 def batched_decode_attention(out, q, k_cache, v_cache, cache_rows: int, positions, batch: int, n_heads: int,
-                             n_kv_heads: int, head_dim: int, scale: float) -> None:
+                             n_kv_heads: int, head_dim: int, scale: float, workspace=None) -> None:
     """Decode attention of ``batch`` streams, each over rows 0..positions[m] of its
     own cache block ``[batch, cache_rows, n_kv_heads * head_dim]`` (decoder.rs:900-903
-    per stream)."""
+    per stream). With ``workspace`` (batched_decode_workspace) every stream's
+    keys are cut into chunks of 512 and the chunk partials merged; without it
+    one workgroup per (stream, kv head) walks all of its keys."""
+    if workspace is not None:
+        _need(workspace, F32, 1, "workspace")
     kv = n_kv_heads * head_dim
     _need(out, F32, batch * n_heads * head_dim, "out")
     _need(q, F32, batch * n_heads * head_dim, "q")
@@ -231,7 +243,8 @@ def batched_decode_attention(out, q, k_cache, v_cache, cache_rows: int, position
     _need(v_cache, F32, batch * cache_rows * kv, "v_cache")
     _need(positions, I32, batch, "positions")
     _lib.call("qasr_batched_decode_attention_f32", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), cache_rows,
-              _ptr(positions), batch, n_heads, n_kv_heads, head_dim, scale, _stream())
+              _ptr(positions), batch, n_heads, n_kv_heads, head_dim, scale, _ptr(workspace),
+              0 if workspace is None else workspace.numel(), _stream())
 
 
 def attention_workspace(seq_q: int, n_heads: int, head_dim: int, device="cuda") -> torch.Tensor:
