@@ -687,7 +687,8 @@ class DecodeStepBatched(Workload):
                    "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": gain(hd), "k_norm": gain(hd),
                    "input_norm": gain(H), "post_attn_norm": gain(H)} for _ in range(L)]
         weights = {"layers": layers, "norm": gain(H), "lm_head": qw(VOCAB, H)}
-        self.dec = DecoderInt8Batched(weights, H, I, L, B, rows, nq, nk, hd, c["eps"], c["theta"], device=dev)
+        self.dec = DecoderInt8Batched(weights, H, I, L, B, rows, nq, nk, hd, c["eps"], c["theta"], device=dev,
+                                      w8a8=getattr(self, "w8a8", False))
         # each stream's earlier context: its cache rows (all 28 layers, 120 GB in all)
         for l in range(L):
             self.dec.k[l].normal_(generator=self.gen)
@@ -713,6 +714,17 @@ class DecodeStepBatched(Workload):
         return {"batch": self.B, "positions": "U[0,2047] per stream", "mean_position": round(self.mean_position, 1),
                 "cache_rows_per_stream": 2048, "hidden": 2048, "intermediate": 6144, "heads": "16q/8kv x 128",
                 "layers": 28, "vocab": VOCAB}
+
+
+class DecodeStepBatchedW8A8(DecodeStepBatched):
+    """decode_step_b256 with the projections on int8 matrix cores (each
+    stream's activation rows quantized per row at the four projection inputs,
+    as the c5 gate/up does)."""
+    name = "decode_step_b256_w8a8"
+    description = DecodeStepBatched.description.replace("W8A32 matrix-core projections",
+                                                        "W8A8 int8-MFMA projections")
+    dtype = "int8/int32->f32"
+    w8a8 = True
 
 
 class PrefillStep(Workload):
@@ -896,6 +908,7 @@ WORKLOADS = {"c1": C1DecodeChain, "c1_cold": C1Cold, "c2": C2PrefillChain, "c3":
              "c4": C4Int8Matvec,
              "c5": C5BatchedDecode, "c5_b32": C5Share, "c5_layer": C5Layer, "w8a32_decode": W8A32Decode, "attn_decode": AttnDecode, "attn_prefill": AttnPrefill,
              "lm_head": LmHead, "decode_step": DecodeStep, "decode_step_b256": DecodeStepBatched,
+             "decode_step_b256_w8a8": DecodeStepBatchedW8A8,
              "w8a32_prefill": W8A32Prefill, "prefill_step": PrefillStep}
 
 
@@ -1158,7 +1171,7 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
         return result(dt / n, nt, f"{n} layers of the c5_layer chain (B=256) on the oracle over 28 distinct "
                                   f"q/k/v and gate/up weights: the reference's W8A32 matvec per stream on {nt} "
                                   "threads, norms/RoPE/SwiGLU and the cache row copies on one", B / 28.0)
-    if name in ("decode_step", "decode_step_b256"):
+    if name in ("decode_step", "decode_step_b256", "decode_step_b256_w8a8"):
         from oracle.decoder import decode_int8_step
 
         c = DEC_1_7B
@@ -1182,7 +1195,7 @@ def cpu_baseline(name: str, seconds: float, step_bytes: int) -> dict:
         x = f32(H)
         n, dt = _run_until(lambda: decode_int8_step(w, kc, vc, pos, x, nq, nk, hd, c["eps"], c["theta"], nt),
                            seconds)
-        if name == "decode_step_b256":  # the reference decodes one stream at a time: 256 in turn
+        if name.startswith("decode_step_b256"):  # the reference decodes one stream at a time: 256 in turn
             return result(dt / n * 256, nt, f"{n} decode tokens of one stream at position {pos} (the middle of "
                                             "U[0,2047]) on the oracle's restated decode step (decoder.rs:848-965) "
                                             "over 28 distinct layers, scaled to 256 streams decoded in turn (the "
@@ -1302,7 +1315,7 @@ def profile_kernel(torch, wl, name: str, n: int) -> int:
 
 
 # ---------------------------------------------------------------------------
-DEFAULT_CONFIGS = "c1,c1_cold,c2,c3_fused,c4,c5_b32,c5_layer,decode_step,decode_step_b256"
+DEFAULT_CONFIGS = "c1,c1_cold,c2,c3_fused,c4,c5_b32,c5_layer,decode_step,decode_step_b256,decode_step_b256_w8a8"
 
 
 def _round(v):
@@ -1523,9 +1536,14 @@ def main() -> int:
         cm = measure(torch, dev, cw, K, W, use_graph)
         ccpu = None
         if not args.no_cpu_baseline:
-            print(f"[bench] cpu baseline {name} ({args.config_cpu_seconds:.0f} s sample)...", file=sys.stderr,
-                  flush=True)
-            ccpu = cpu_baseline(name, args.config_cpu_seconds, cw.step_bytes)
+            # the W8A8 and W8A32 batched steps share one reference baseline (the reference is W8A32)
+            same = "decode_step_b256" if name == "decode_step_b256_w8a8" else None
+            if same in configs and configs[same].get("cpu_baseline"):
+                ccpu = configs[same]["cpu_baseline"]
+            else:
+                print(f"[bench] cpu baseline {name} ({args.config_cpu_seconds:.0f} s sample)...", file=sys.stderr,
+                      flush=True)
+                ccpu = cpu_baseline(name, args.config_cpu_seconds, cw.step_bytes)
         configs[name] = summary(cw, cm, ccpu)
         free(torch, cw)
     if configs:
@@ -1534,6 +1552,8 @@ def main() -> int:
         out["decode_tokens_per_s"] = configs["decode_step"]["tokens_per_s"]
     if "decode_step_b256" in configs:
         out["batched_decode_tokens_per_s"] = configs["decode_step_b256"]["tokens_per_s"]
+    if "decode_step_b256_w8a8" in configs:
+        out["batched_decode_w8a8_tokens_per_s"] = configs["decode_step_b256_w8a8"]["tokens_per_s"]
     print(json.dumps(out), flush=True)
     return 0
 

@@ -233,11 +233,22 @@ class DecoderInt8Batched:
     Then the last residual add + final RMSNorm and the lm_head with each
     stream's greedy argmax. ``positions`` (device int32) holds each stream's
     position; ``finish`` advances them all by one (decoder.rs:926).
+
+    ``w8a8=True`` runs the four projections on int8 matrix cores with each
+    stream's activation row quantized per row (quantize.rs:633-662 arithmetic),
+    the c5 way: add + RMSNorm + quantization in one launch; q/k/v with the head
+    norms, RoPE and the K/V cache rows in the GEMM epilogue; attention; the
+    attention rows quantized, o; add + RMSNorm + quantization; gate/up with
+    SwiGLU in the epilogue; the SwiGLU rows quantized, down. The int8 weights
+    are the same; the activations are rounded to int8 at those four points,
+    so the results follow the reference's within that rounding, not 1e-5. The
+    lm_head stays W8A32.
     """
 
     def __init__(self, weights: dict, hidden: int, intermediate: int, n_layers: int, batch: int,
                  cache_rows: int, n_heads: int = 16, n_kv_heads: int = 8, head_dim: int = 128,
-                 eps: float = 1e-6, theta: float = 1e6, vocab: int | None = None, device="cuda"):
+                 eps: float = 1e-6, theta: float = 1e6, vocab: int | None = None, device="cuda",
+                 w8a8: bool = False):
         self.w = weights
         self.H, self.I, self.L, self.B = hidden, intermediate, n_layers, batch
         self.nq, self.nk, self.hd = n_heads, n_kv_heads, head_dim
@@ -265,6 +276,38 @@ class DecoderInt8Batched:
         self.rope = K.RopeCache(device)
         self.rope.ensure(cache_rows, head_dim, theta)
         self.scale = 1.0 / math.sqrt(head_dim)
+        self.attn_ws = K.batched_decode_workspace(B, n_heads, head_dim, cache_rows, device)
+        self.w8a8 = w8a8
+        if w8a8:
+            i8 = dict(dtype=torch.int8, device=device)
+            self.xq, self.xs = torch.empty(B * hidden, **i8), torch.empty(B, **f32)
+            self.aq, self.as_ = torch.empty(B * n_heads * head_dim, **i8), torch.empty(B, **f32)
+            self.fq, self.fs = torch.empty(B * intermediate, **i8), torch.empty(B, **f32)
+            self.packed = []
+            for lw in weights["layers"]:  # the same int8 weights, re-laid into MFMA tiles once
+                ws = [lw["wq"], lw["wk"], lw["wv"]]
+                qkv = K.QuantWeight(torch.cat([w.data.reshape(-1) for w in ws]),
+                                    torch.cat([w.scales for w in ws]), sum(w.out_dim for w in ws), hidden)
+                self.packed.append({k: K.pack_w8a8_tiles(w) for k, w in
+                                    (("qkv", qkv), ("wo", lw["wo"]), ("gate_up", lw["gate_up"]),
+                                     ("down", lw["down"]))})
+
+    def _layer_w8a8(self, l: int, lw: dict) -> None:
+        H, I, B, nq, nk, hd, eps = self.H, self.I, self.B, self.nq, self.nk, self.hd, self.eps
+        pk = self.packed[l]
+        kb, vb = self.k[l], self.v[l]
+        K.add_rms_norm_quant(self.x, None if l == 0 else self.down, lw["input_norm"], None, self.xq, self.xs,
+                             B, H, eps)
+        K.qkv_heads_w8a8_packed(self.q, kb, vb, self.rows, pk["qkv"], self.xq, self.xs, lw["q_norm"],
+                                lw["k_norm"], self.rope, self.positions, B, H, nq, nk, hd, eps)
+        K.batched_decode_attention(self.attn, self.q, kb, vb, self.rows, self.positions, B, nq, nk, hd,
+                                   self.scale, self.attn_ws)
+        K.quantize_rows_i8(self.aq, self.as_, self.attn, B, nq * hd)
+        K.linear_w8a8_packed(self.proj, pk["wo"], self.aq, self.as_, B, nq * hd, H)
+        K.add_rms_norm_quant(self.x, self.proj, lw["post_attn_norm"], None, self.xq, self.xs, B, H, eps)
+        K.gate_up_swiglu_w8a8_packed(self.ffn, pk["gate_up"], self.xq, self.xs, B, H, I)
+        K.quantize_rows_i8(self.fq, self.fs, self.ffn, B, I)
+        K.linear_w8a8_packed(self.down, pk["down"], self.fq, self.fs, B, I, H)
 
     def decode(self, embeds: torch.Tensor) -> None:
         """One token for every stream (``embeds``: [batch, hidden]) at its
@@ -274,6 +317,9 @@ class DecoderInt8Batched:
         H, I, B, nq, nk, hd, eps = self.H, self.I, self.B, self.nq, self.nk, self.hd, self.eps
         self.x.copy_(embeds[:B * H])
         for l, lw in enumerate(self.w["layers"]):
+            if self.w8a8:
+                self._layer_w8a8(l, lw)
+                continue
             if l == 0:
                 K.rms_norm(self.x_norm, self.x, lw["input_norm"], B, H, eps)
             else:  # previous layer's residual add + this layer's input norm
@@ -284,7 +330,7 @@ class DecoderInt8Batched:
             K.head_rms_norm_rope_kv(self.q, self.kk, self.vv, lw["q_norm"], lw["k_norm"], self.rope,
                                     self.positions, 0, B, nq, nk, hd, eps, kb, vb, self.rows)
             K.batched_decode_attention(self.attn, self.q, kb, vb, self.rows, self.positions, B, nq, nk, hd,
-                                       self.scale)
+                                       self.scale, self.attn_ws)
             wo = lw["wo"]
             K.linear_nobias_int8(self.proj, self.attn, wo.data, wo.scales, B, nq * hd, H)
             K.add_rms_norm(self.x, self.proj, lw["post_attn_norm"], self.x_norm, B, H, eps)

@@ -434,8 +434,19 @@ def test_argmax_rows_semantics():
 
 
 # --- the INT8 decode step composition (decoder.rs:848-965) -------------------------
-def _f64_decode(w, kc, vc, pos, x, nq, nk, hd, eps=1e-6, theta=1e6):
-    """float64 numpy evaluation of the decode step's formulas (no oracle kernels)."""
+def _f64_quant(v):
+    """Per-vector int8 rounding in float64: absmax/127 steps, half away from zero."""
+    a = np.abs(v).max()
+    if a == 0:
+        return v * 0
+    q = np.clip(np.sign(v) * np.floor(np.abs(v) * (127.0 / a) + 0.5), -128, 127)
+    return q * (a / 127.0)
+
+
+def _f64_decode(w, kc, vc, pos, x, nq, nk, hd, eps=1e-6, theta=1e6, w8a8=False):
+    """float64 numpy evaluation of the decode step's formulas (no oracle
+    kernels); ``w8a8`` rounds the four projection inputs to int8 per vector."""
+    fq = _f64_quant if w8a8 else (lambda v: v)
     H = x.size
     half = hd // 2
     inv = theta ** (-(2.0 * np.arange(half)) / hd)
@@ -456,7 +467,7 @@ def _f64_decode(w, kc, vc, pos, x, nq, nk, hd, eps=1e-6, theta=1e6):
 
     x = x.astype(np.float64)
     for l, lw in enumerate(w["layers"]):
-        xn = rms(x, lw["input_norm"])
+        xn = fq(rms(x, lw["input_norm"]))
         q = heads(lin(xn, lw["wq"]), nq, lw["q_norm"])
         k = heads(lin(xn, lw["wk"]), nk, lw["k_norm"])
         kc[l, pos] = k.ravel()
@@ -468,11 +479,11 @@ def _f64_decode(w, kc, vc, pos, x, nq, nk, hd, eps=1e-6, theta=1e6):
             s = K[:, h // (nq // nk)] @ q[h] / np.sqrt(hd)
             p = np.exp(s - s.max())
             att[h] = (p / p.sum()) @ V[:, h // (nq // nk)]
-        x = x + lin(att.ravel(), lw["wo"])
-        xn = rms(x, lw["post_attn_norm"])
+        x = x + lin(fq(att.ravel()), lw["wo"])
+        xn = fq(rms(x, lw["post_attn_norm"]))
         gu = lin(xn, lw["gate_up"])
         g, u = gu[0::2], gu[1::2]
-        x = x + lin(g / (1 + np.exp(-g)) * u, lw["down"])
+        x = x + lin(fq(g / (1 + np.exp(-g)) * u), lw["down"])
     xn = rms(x, w["norm"])
     logits = lin(xn, w["lm_head"])
     return int(np.argmax(logits)), xn, logits
@@ -520,6 +531,35 @@ def test_decode_step_composition():
         np.testing.assert_allclose(logits, logits64, rtol=1e-4, atol=1e-5)
         np.testing.assert_allclose(kc[:, :pos + 1], kc64[:, :pos + 1], rtol=1e-4, atol=1e-5)
         np.testing.assert_allclose(vc[:, :pos + 1], vc64[:, :pos + 1], rtol=1e-4, atol=1e-5)
+        top2 = np.sort(logits64)[-2:]
+        if top2[1] - top2[0] > 1e-3:
+            assert tok == tok64
+
+
+def test_decode_w8a8_step_composition():
+    """The W8A8 decode step equals a float64 evaluation of the same formulas
+    with the four projection inputs rounded to int8 per vector, and differs
+    from the W8A32 step by several times the tolerance. Leaving out the
+    rounding at any one of the four points moves the result 6-30x the
+    tolerance away from the float64 evaluation (checked by planting it)."""
+    from oracle.decoder import decode_int8_step, decode_w8a8_step
+
+    r = np.random.default_rng(78)
+    H, I, L, nq, nk, hd, vocab = 64, 96, 2, 4, 2, 16, 50
+    w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
+    shape = (L, 8, nk * hd)
+    kc, vc, kc32, vc32 = (np.zeros(shape, np.float32) for _ in range(4))
+    kc64, vc64 = np.zeros(shape), np.zeros(shape)
+    for pos in range(3):
+        x = r.standard_normal(H).astype(np.float32)
+        tok, xn, logits = decode_w8a8_step(w, kc, vc, pos, x, nq, nk, hd)
+        _, xn32, _ = decode_int8_step(w, kc32, vc32, pos, x, nq, nk, hd)
+        tok64, xn64, logits64 = _f64_decode(w, kc64, vc64, pos, x, nq, nk, hd, w8a8=True)
+        np.testing.assert_allclose(xn, xn64, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(logits, logits64, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(kc[:, :pos + 1], kc64[:, :pos + 1], rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(vc[:, :pos + 1], vc64[:, :pos + 1], rtol=1e-4, atol=1e-5)
+        assert (np.abs(xn - xn32) / (1e-5 + 1e-4 * np.abs(xn32))).max() > 3.0
         top2 = np.sort(logits64)[-2:]
         if top2[1] - top2[0] > 1e-3:
             assert tok == tok64
