@@ -6,8 +6,9 @@
 //
 // W is tile-packed (qasr_pack_w8a8_tiles): [N, K] with N = (n_heads +
 // 2 n_kv_heads) * 128 rows, the q heads, then the k heads, then the v heads
-// (decoder.rs:881-886 as one matrix). A workgroup owns one 128-row head x 32
-// streams, so the epilogue sees whole heads:
+// (decoder.rs:881-886 as one matrix). A workgroup owns one 128-row head x TOK
+// streams (32, or 16 where 32 would leave fewer than 256 workgroups or the
+// staged rows would not fit the LDS), so the epilogue sees whole heads:
 //   q heads: per-head RMSNorm (q_norm) + NeoX RoPE at the stream's position,
 //            written to q_out[m, head] (decoder.rs:888, 891);
 //   k heads: the same with k_norm, written into the stream's cache row
@@ -19,13 +20,13 @@
 // bit. MODE 0 is that plain projection: y[m, n] in fp32.
 //
 // Structure (8 waves, 512 threads): wave w = 4*kq + rg owns rows 32*rg ..
-// 32*rg + 31 (two 16-row MFMA tiles) for both 16-stream tiles over K half kq.
-// The 32 streams' int8 rows (32 x K bytes) are staged once in LDS with the
+// 32*rg + 31 (two 16-row MFMA tiles) for the TOK/16 stream tiles over K half
+// kq. The TOK streams' int8 rows (TOK x K bytes) are staged once in LDS with the
 // 16-byte slot of row r at slot ^ (r % 16), so the b128 fragment reads of 16
 // rows at one k offset hit distinct banks; W streams from the packed tiles
 // into registers PF k-steps ahead. After the loop the two K halves of a row
 // group are added through LDS (exact int32), the dequantized tile goes to LDS
-// as [32 streams][128 dims], and groups of 16 threads -- one stream each, in
+// as [TOK streams][128 dims], and groups of 16 threads -- one stream each, in
 // the lane layout head_norm_rope expects -- finish the heads.
 #include "common.hpp"
 
