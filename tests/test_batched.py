@@ -190,12 +190,12 @@ def test_batched_decode_step_matches_the_oracle_per_stream(tmp_path, dev, H, I, 
     from tests.test_decoder_step import _load
     from tests.test_oracle import small_decoder
 
-    L, vocab, rows, TOL = 2, 1000, 1100, 1e-4
+    L, vocab, rows, TOL = 2, 1000, 2100, 1e-4
     r = np.random.default_rng([55, H, B])
     w = small_decoder(r, H, I, L, NQ, NK, HD, vocab)
     dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev)
     kv = NK * HD
-    pos = np.array([0, 700, 7, 64, 1100 - 3, 1, 511, 255, 1023][:B], np.int32)  # 1-3 key chunks
+    pos = np.array([0, 1500, 7, 64, 2100 - 3, 1, 510, 255, 1023][:B], np.int32)  # 1-5 key chunks
     kc = r.standard_normal((B, L, rows, kv)).astype(np.float32)  # earlier contexts, one per stream
     vc = r.standard_normal((B, L, rows, kv)).astype(np.float32)
     for l in range(L):
@@ -289,12 +289,12 @@ def test_batched_w8a8_decode_step_matches_the_oracle_per_stream(tmp_path, dev, m
     from tests.test_decoder_step import _load
     from tests.test_oracle import small_decoder
 
-    L, vocab, rows, TOL = 2, 1000, 1100, 1e-4
+    L, vocab, rows, TOL = 2, 1000, 2100, 1e-4
     r = np.random.default_rng([57, H, B])
     w = small_decoder(r, H, I, L, NQ, NK, HD, vocab)
     dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev, w8a8=True)
     kv = NK * HD
-    pos = np.array([0, 700, 7, 64, 1100 - 3, 1, 511, 255, 1023][:B], np.int32)  # 1-3 key chunks
+    pos = np.array([0, 1500, 7, 64, 2100 - 3, 1, 510, 255, 1023][:B], np.int32)  # 1-5 key chunks
     kc = r.standard_normal((B, L, rows, kv)).astype(np.float32)
     vc = r.standard_normal((B, L, rows, kv)).astype(np.float32)
     kc32, vc32 = kc.copy(), vc.copy()
@@ -340,9 +340,9 @@ def test_batched_w8a8_decode_step_matches_the_oracle_per_stream(tmp_path, dev, m
     assert torch.equal(dec.positions.cpu(), torch.from_numpy(pos + 2))
 
 
-@pytest.mark.parametrize("rows", [300, 1300])
+@pytest.mark.parametrize("rows", [300, 2300])
 def test_batched_decode_attention_bad_position_and_graph_replay(dev, rows):
-    """Streams at positions across 1-3 key chunks (chunks of 512; 300 rows:
+    """Streams at positions across 1-5 key chunks (chunks of 512; 300 rows:
     one chunk, no workspace needed) against the oracle, with and without the
     workspace (chunked and one-workgroup-per-stream forms); a stream at a
     position outside its cache gets a NaN row (the others are unaffected);
@@ -355,7 +355,7 @@ def test_batched_decode_attention_bad_position_and_graph_replay(dev, rows):
     q = torch.from_numpy(r.standard_normal(B * NQ * HD).astype(np.float32)).to(dev)
     kc = torch.from_numpy(r.standard_normal(B * rows * kv).astype(np.float32)).to(dev)
     vc = torch.from_numpy(r.standard_normal(B * rows * kv).astype(np.float32)).to(dev)
-    good = [0, rows - 1, rows // 2, 64] + ([511, 512, 1024] if rows > 1024 else [5, 100, 200])
+    good = [0, rows - 1, rows // 2, 64] + ([1023, 1024, 2048] if rows > 2048 else [5, 100, 200])
     pos_l = good[:2] + [rows, -1] + good[2:6]
     pos = torch.tensor(pos_l, dtype=torch.int32, device=dev)
     ws = K.batched_decode_workspace(B, NQ, HD, rows, dev)
