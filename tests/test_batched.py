@@ -43,7 +43,7 @@ def _packed(dev, wq, ws):
 @pytest.mark.parametrize("batch,out_dim,in_dim", [(1, 128, 1024), (5, 384, 2048), (31, 256, 1024),
                                                   (32, 2048, 2048), (33, 128, 2048), (256, 4096, 2048),
                                                   (256, 2048, 2048), (256, 2048, 6144), (17, 256, 3072),
-                                                  (3, 128, 4096)])
+                                                  (3, 128, 4096), (256, 1024, 4096), (37, 384, 6144)])
 def test_linear_w8a8_packed_bit_exact(dev, batch, out_dim, in_dim):
     from qwenasr_amd import kernels as K
 
