@@ -340,6 +340,51 @@ def test_batched_w8a8_decode_step_matches_the_oracle_per_stream(tmp_path, dev, m
     assert torch.equal(dec.positions.cpu(), torch.from_numpy(pos + 2))
 
 
+@pytest.mark.parametrize("w8a8", [False, True])
+def test_batched_decode_step_graph_replay_equals_eager(tmp_path, dev, w8a8):
+    """One batched decode step (both forms) captured in a HIP graph: every
+    replay gives the eager step's hidden state, logits, tokens and new K/V
+    rows bit for bit, with eager work and synchronisations between replays
+    (the step rewrites the same cache rows while positions stay put)."""
+    from qwenasr_amd.decoder import DecoderInt8Batched
+    from tests.test_decoder_step import _load
+    from tests.test_oracle import small_decoder
+
+    H, I, L, B, rows, vocab = 1024, 3072, 2, 12, 1300, 1000
+    r = np.random.default_rng([58, int(w8a8)])
+    w = small_decoder(r, H, I, L, NQ, NK, HD, vocab)
+    dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev, w8a8=w8a8)
+    for l in range(L):
+        dec.k[l].normal_()
+        dec.v[l].normal_()
+    dec.positions.copy_(torch.from_numpy(r.integers(0, rows, B).astype(np.int32)))
+    emb = torch.from_numpy(r.standard_normal(B * H).astype(np.float32)).to(dev)
+    kv = NK * HD
+    pos = dec.positions.long().cpu()
+
+    def outputs():
+        kr = [dec.k[l].view(B, rows, kv)[torch.arange(B), pos].clone() for l in range(L)]
+        vr = [dec.v[l].view(B, rows, kv)[torch.arange(B), pos].clone() for l in range(L)]
+        return [dec.x_norm.clone(), dec.logits.clone(), dec.tokens.clone()] + kr + vr
+
+    print(f"[batched] graph replay w8a8={w8a8}", flush=True)
+    dec.decode(emb)
+    torch.cuda.synchronize()
+    ref = outputs()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        dec.decode(emb)
+    for rep in range(3):
+        dec.x_norm.fill_(0.0)
+        dec.logits.fill_(0.0)
+        dec.tokens.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outputs(), ref)):
+            assert torch.equal(a, b), (rep, i)
+
+
 @pytest.mark.parametrize("rows", [300, 2300])
 def test_batched_decode_attention_bad_position_and_graph_replay(dev, rows):
     """Streams at positions across 1-5 key chunks (chunks of 512; 300 rows:
