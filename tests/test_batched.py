@@ -385,6 +385,34 @@ def test_batched_decode_step_graph_replay_equals_eager(tmp_path, dev, w8a8):
             assert torch.equal(a, b), (rep, i)
 
 
+@pytest.mark.parametrize("nq,nk,hd", [(8, 8, 128), (4, 4, 64), (8, 4, 64), (16, 4, 64)])
+def test_batched_decode_attention_other_head_shapes(dev, nq, nk, hd):
+    """The other head shapes the batched attention takes (G = 1 at head_dim
+    128; G = 1, 2, 4 at head_dim 64), chunked (1100 rows, workspace) and not,
+    against the oracle at 1e-5."""
+    from qwenasr_amd import kernels as K
+
+    B, rows, kv = 5, 1100, nk * hd
+    r = np.random.default_rng([59, nq, nk, hd])
+    q = r.standard_normal(B * nq * hd).astype(np.float32)
+    kc = r.standard_normal(B * rows * kv).astype(np.float32)
+    vc = r.standard_normal(B * rows * kv).astype(np.float32)
+    pos = np.array([0, 1099, 511, 512, 777], np.int32)
+    d = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    kn, vn = kc.reshape(B, rows, kv), vc.reshape(B, rows, kv)
+    for ws in (None, K.batched_decode_workspace(B, nq, hd, rows, dev)):
+        out = torch.empty(B * nq * hd, device=dev)
+        print(f"[batched] attention nq={nq} nk={nk} hd={hd} chunked={ws is not None}", flush=True)
+        K.batched_decode_attention(out, d(q), d(kc), d(vc), rows, d(pos), B, nq, nk, hd, hd ** -0.5, ws)
+        torch.cuda.synchronize()
+        o = out.view(B, -1).cpu().numpy()
+        for m in range(B):
+            p = int(pos[m])
+            ref = oracle.causal_attention(q.reshape(B, -1)[m], kn[m, :p + 1].ravel(), vn[m, :p + 1].ravel(), 1,
+                                          p + 1, nq, nk, hd, hd ** -0.5, p)
+            assert_close(o[m], ref, 1e-5, 1e-5, f"stream {m} at {p}, chunked {ws is not None}")
+
+
 @pytest.mark.parametrize("rows", [300, 2300])
 def test_batched_decode_attention_bad_position_and_graph_replay(dev, rows):
     """Streams at positions across 1-5 key chunks (chunks of 512; 300 rows:
