@@ -1077,9 +1077,12 @@ bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, h
   return true;
 }
 
-// Kernel and tile: the LDS-staged 128 x 64 tile where it still gives at least
-// 256 workgroups (its staged operands are shared by 4 waves: 128 B loaded per
-// MFMA); otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
+// Kernel and tile: the LDS-staged 256 x 64 tile where it still gives at least
+// 512 workgroups (a 256-stream lm_head: each workgroup's activation rows then
+// serve twice the weight rows, 634.7 -> 579.9 us at [256,2048]x[2048,151936];
+// 256 x 128 measured slower, one workgroup per CU), the 128 x 64 tile where it
+// gives at least 256 (its staged operands are shared by 4 waves: 128 B loaded
+// per MFMA); otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
 // 32 x 32 that fills the chip (measured at T = 512: o [1024, 2048] 20.0 ->
 // 16.7 us, down [1024, 3072] 27.4 -> 20.9 us against the LDS-staged 64 x 32).
 // Returns false when the chosen kernel cannot run the shape (K not a multiple
@@ -1096,7 +1099,9 @@ bool launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
     return c;
   };
   const long long rows64 = (T + 63) / 64, rows32 = (T + 31) / 32;
-  unsigned c = cols(128);
+  unsigned c = cols(256);
+  if (c * rows64 >= 512) return try_gemm<256, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
+  c = cols(128);
   if (c * rows64 >= 256) return try_gemm<128, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
   c = cols(64);
   if (c * rows64 >= 256) return try_gemm_ksplit<64, 64, 4, EPI>(set, c, x, T, K, st);

@@ -757,6 +757,32 @@ def test_linear_nobias_int8_w8a32(dev, seq, in_dim, out_dim):
     assert_close(host(y), oracle.linear_int8(x, wq, ws, b, seq, in_dim, out_dim), RTOL, ATOL, "w8a32+bias")
 
 
+def test_linear_nobias_int8_wide_tile(dev):
+    """The 256 x 64 tile of the many-token GEMM (taken when it gives 512+
+    workgroups, e.g. a 256-stream lm_head), ragged in tokens and rows: equal
+    bit for bit to the same product computed in column blocks that take the
+    128 x 64 tile (every tile adds each output's terms in the same order), and
+    within 1e-5 of the oracle on a slice of the rows."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(22)
+    seq, in_dim, out_dim = 200, 1024, 33000  # 129 x 4 workgroups of 256 x 64
+    wq, ws = make_qweight(r, out_dim, in_dim)
+    x = normal(r, seq * in_dim)
+    x_t, w_t, s_t = dev_t(x, dev), dev_t(wq, dev), dev_t(ws, dev)
+    y = torch.empty(seq * out_dim, dtype=torch.float32, device=dev)
+    K.linear_nobias_int8(y, x_t, w_t, s_t, seq, in_dim, out_dim)
+    got = host(y).reshape(seq, out_dim)
+    # blocks of >= 8192 rows: 64+ column blocks of 128 x 4 token blocks, < 512 of 256
+    for r0, r1 in ((0, 8192), (8192, 16384), (16384, 24576), (24576, out_dim)):
+        yb = torch.empty(seq * (r1 - r0), dtype=torch.float32, device=dev)
+        K.linear_nobias_int8(yb, x_t, w_t[r0 * in_dim:r1 * in_dim], s_t[r0:r1], seq, in_dim, r1 - r0)
+        np.testing.assert_array_equal(got[:, r0:r1], host(yb).reshape(seq, r1 - r0), err_msg=f"rows {r0}..{r1}")
+    n = 300
+    ref = oracle.linear_nobias_int8(x, wq.reshape(out_dim, in_dim)[out_dim - n:], ws[out_dim - n:], seq, in_dim, n)
+    assert_close(got[:, out_dim - n:].ravel(), ref, RTOL, ATOL, "w8a32 256x64 tile, last rows")
+
+
 def test_linear_int8_integer_inputs_exact(dev):
     # integer x, unit scales: the f32 accumulation is exact, so y is the int dot
     from qwenasr_amd import kernels as K
