@@ -1056,11 +1056,15 @@ static size_t batched_chunk_keys(size_t cache_rows) {
   return r > 512 ? r : 512;
 }
 
+// 0 also when the size would overflow (such a call is rejected anyway).
 extern "C" size_t qasr_batched_decode_attention_workspace_floats(size_t batch, size_t n_heads, size_t head_dim,
                                                                  size_t cache_rows) {
-  if (cache_rows == 0) return 0;
+  if (cache_rows == 0 || cache_rows >= 0x40000000u) return 0;
   const size_t nchunk = (cache_rows + batched_chunk_keys(cache_rows) - 1) / batched_chunk_keys(cache_rows);
-  return nchunk <= 1 ? 0 : batch * n_heads * nchunk * (head_dim + 2);
+  size_t n = 0;
+  if (nchunk <= 1 || !mul_ok(batch, n_heads, &n) || !mul_ok(n, nchunk, &n) || !mul_ok(n, head_dim + 2, &n))
+    return 0;
+  return n;
 }
 
 extern "C" int qasr_batched_decode_attention_f32(float* out, const float* q, const float* k_cache,

@@ -165,6 +165,16 @@ def test_attention_workspace_size_query():
     assert _lib.lib().qasr_causal_attention_workspace_floats(3, 2, 64) == 6 * 64 * 66
 
 
+def test_batched_attention_workspace_size_query():
+    # chunks of 512 keys: 2048 rows -> 4 partials of head_dim + 2 floats per (stream, q head)
+    q = _lib.lib().qasr_batched_decode_attention_workspace_floats
+    assert q(256, 16, 128, 2048) == 256 * 16 * 4 * 130
+    assert q(3, 4, 64, 513) == 3 * 4 * 2 * 66
+    assert q(256, 16, 128, 512) == 0  # one chunk: no workspace
+    assert q(256, 16, 128, 0) == 0
+    assert q(1 << 62, 16, 128, 2048) == 0  # would overflow
+
+
 def test_lm_head_workspace_size_query():
     # one (value, index) pair of 8 bytes per 4 logits at most
     assert _lib.lib().qasr_lm_head_argmax_workspace_bytes(151936) == 8 * 37984
@@ -242,6 +252,37 @@ def test_decode_attention_validation():
     assert f(out, NULL, k, v, qw, kw, cs, sn, 4096, 10, 16, 8, 128, 1e-6, 0.088, kc, vc, 2048, NULL, 0, NULL) == inv
     assert f(out, q, k, v, qw, kw, cs, sn, 4096, 10, 0, 8, 128, 1e-6, 0.088, kc, vc, 2048, NULL, 0, NULL) == \
         _lib.QASR_OK
+
+
+def test_batched_entry_points_validation():
+    """The batched decode entry points reject bad shapes, null pointers and a
+    too-small workspace before any launch."""
+    so = _lib.lib()
+    P = [ctypes.c_void_p(0x100000 * (i + 1)) for i in range(12)]
+    inv, uns = _lib.QASR_ERR_INVALID_ARG, _lib.QASR_ERR_UNSUPPORTED
+    att = so.qasr_batched_decode_attention_f32
+    out, q, kc, vc, pos, ws = P[:6]
+    # (out, q, k_cache, v_cache, cache_rows, positions, batch, n_heads, n_kv_heads, head_dim, scale, ws, n, stream)
+    assert att(out, q, kc, vc, 2048, pos, 4, 16, 5, 128, 0.088, NULL, 0, NULL) == inv  # 16 % 5 != 0
+    assert att(out, NULL, kc, vc, 2048, pos, 4, 16, 8, 128, 0.088, NULL, 0, NULL) == inv
+    assert att(out, q, kc, vc, 2048, pos, 4, 32, 8, 128, 0.088, NULL, 0, NULL) == uns  # G = 4 at head_dim 128
+    assert att(out, q, kc, vc, 2048, pos, 4, 16, 8, 96, 0.088, NULL, 0, NULL) == uns
+    need = so.qasr_batched_decode_attention_workspace_floats(4, 16, 128, 2048)
+    assert att(out, q, kc, vc, 2048, pos, 4, 16, 8, 128, 0.088, ws, need - 1, NULL) == inv
+    assert "workspace" in last_error()
+    assert att(out, q, kc, vc, 2048, pos, 0, 16, 8, 128, 0.088, NULL, 0, NULL) == _lib.QASR_OK
+    lin = so.qasr_linear_w8a8_packed
+    y, w, sc, xq, xs = P[6:11]
+    # (y, w_packed, scales, xq, x_scales, batch, in_dim, out_dim, stream)
+    assert lin(y, w, sc, xq, xs, 4, 1536, 128, NULL) == uns  # in_dim
+    assert lin(y, w, sc, xq, xs, 4, 2048, 100, NULL) == uns  # out_dim % 128
+    assert lin(y, NULL, sc, xq, xs, 4, 2048, 128, NULL) == inv
+    qkv = so.qasr_qkv_heads_w8a8_packed
+    cs, sn, qw, kw = P[8:12]
+    # (q_out, k_cache, v_cache, cache_rows, w, scales, xq, xs, q_norm_w, k_norm_w, cos, sin, table_rows,
+    #  positions, batch, in_dim, n_heads, n_kv_heads, head_dim, eps, stream)
+    assert qkv(q, kc, vc, 2048, w, sc, xq, xs, qw, kw, cs, sn, 2048, pos, 4, 2048, 16, 8, 64, 1e-6, NULL) == uns
+    assert qkv(q, kc, vc, 2048, w, sc, xq, xs, NULL, kw, cs, sn, 2048, pos, 4, 2048, 16, 8, 128, 1e-6, NULL) == inv
 
 
 def test_pe_add_layer_norm_validation():
