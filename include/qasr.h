@@ -490,13 +490,18 @@ int qasr_decode_attention_f32(float* out, float* q, const float* k, const float*
  * position outside the cache gives a NaN row. head_dim 128 with
  * n_heads/n_kv_heads in {1, 2}, or 64 with {1, 2, 4}; 16-byte aligned
  * buffers (QASR_ERR_UNSUPPORTED otherwise); a workspace that is too small is
- * QASR_ERR_INVALID_ARG. No reference counterpart as one call (the reference
- * decodes one stream at a time). */
+ * QASR_ERR_INVALID_ARG. With out_q and out_scales (both or neither; int8
+ * [batch, n_heads * head_dim], f32 [batch]) each stream's row is also
+ * quantized per row in the launch that merges the chunks, with the values
+ * and scale qasr_quantize_rows_i8 gives on out (the input of a W8A8 o
+ * projection; n_heads * head_dim * 4 <= 65536). No reference counterpart as
+ * one call (the reference decodes one stream at a time). */
 int qasr_batched_decode_attention_f32(float* out, const float* q, const float* k_cache,
                                       const float* v_cache, size_t cache_rows,
                                       const int32_t* positions, size_t batch, size_t n_heads,
                                       size_t n_kv_heads, size_t head_dim, float scale, float* workspace,
-                                      size_t workspace_floats, void* stream);
+                                      size_t workspace_floats, int8_t* out_q, float* out_scales,
+                                      void* stream);
 
 /* Workspace floats qasr_batched_decode_attention_f32 uses for these sizes (0:
  * the cache is one chunk, no workspace is needed). */

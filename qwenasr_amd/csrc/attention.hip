@@ -594,6 +594,57 @@ __global__ __launch_bounds__(256) void attention_combine_batch_kernel(float* __r
                    used, lane);
 }
 
+// The batched attention with each stream's row quantized per row (the W8A8
+// o projection's input): one workgroup per stream, one wave per q head (up to
+// 16, then looping). A wave merges its head's chunk partials as
+// attention_combine_batch_kernel does, or reads back the row the attention
+// kernel normalised itself (one chunk, or a NaN row for a position outside the
+// cache), into an LDS copy of the stream's row (and out); then the row's int8
+// values and scale follow quantize.rs:633-662 exactly as qasr_quantize_rows_i8
+// computes them (absmax where NaN never wins, scale = absmax / 127, the same
+// rounding), so q and scale equal that kernel's on out.
+template <int HD>
+__global__ __launch_bounds__(1024) void attention_combine_quant_kernel(
+    float* __restrict__ out, int8_t* __restrict__ out_q, float* __restrict__ out_scales,
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int32_t* __restrict__ positions,
+    long long cache_rows, int heads, int nchunk, int keys_per_chunk) {
+  extern __shared__ __align__(16) float q_row[];  // [heads * HD]
+  __shared__ float red[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const int m = blockIdx.x;
+  const long long p = positions[m];
+  const bool bad = p < 0 || p >= cache_rows;
+  const int used = bad ? 1 : (int)((p + keys_per_chunk) / keys_per_chunk);
+  const size_t row0 = (size_t)m * heads;
+  for (int h = wave; h < heads; h += nwaves) {
+    float* o = out + (row0 + h) * HD;
+    if (used > 1) {
+      merge_splits<HD>(q_row + h * HD, ws_o + (row0 + h) * nchunk * HD, ws_ml + (row0 + h) * nchunk * 2, used,
+                       lane);
+      constexpr int DPL = HD / 64;  // merge_splits' lane mapping: each lane copies out the values it wrote
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) o[lane * DPL + d] = q_row[h * HD + lane * DPL + d];
+    } else {
+      for (int d = lane; d < HD; d += 64) q_row[h * HD + d] = o[d];
+    }
+  }
+  __syncthreads();
+  const int n = heads * HD;
+  float mx = 0.0f;
+  for (int c = threadIdx.x; c < n; c += blockDim.x) {
+    const float a = fabsf(q_row[c]);
+    if (a > mx) mx = a;  // NaN never wins
+  }
+  mx = wave_max(mx);  // then over the nwaves waves present (the max is exact in any order)
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int w = 1; w < nwaves; ++w) mx = red[w] > mx ? red[w] : mx;
+  const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+  if (threadIdx.x == 0) out_scales[m] = mx / 127.0f;
+  for (int c = threadIdx.x; c < n; c += blockDim.x) out_q[(size_t)m * n + c] = (int8_t)quant_i8(q_row[c], inv);
+}
+
 // Merges the partials of every (row, head), one wave each.
 template <int HD>
 __global__ __launch_bounds__(256) void attention_combine_kernel(float* __restrict__ out,
@@ -1071,7 +1122,8 @@ extern "C" int qasr_batched_decode_attention_f32(float* out, const float* q, con
                                                  const float* v_cache, size_t cache_rows,
                                                  const int32_t* positions, size_t batch, size_t n_heads,
                                                  size_t n_kv_heads, size_t head_dim, float scale,
-                                                 float* workspace, size_t workspace_floats, void* stream) {
+                                                 float* workspace, size_t workspace_floats, int8_t* out_q,
+                                                 float* out_scales, void* stream) {
   if (batch == 0 || n_heads == 0) return QASR_OK;
   QASR_REQUIRE(out && q && k_cache && v_cache && positions, "batched_decode_attention: null pointer");
   QASR_REQUIRE(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
@@ -1093,6 +1145,9 @@ extern "C" int qasr_batched_decode_attention_f32(float* out, const float* q, con
   QASR_REQUIRE(!workspace || workspace_floats >= need,
                "batched_decode_attention: workspace smaller than "
                "qasr_batched_decode_attention_workspace_floats()");
+  QASR_REQUIRE(!out_q == !out_scales, "batched_decode_attention: out_q and out_scales go together");
+  QASR_REQUIRE(!out_q || n_heads * head_dim * 4 <= 65536,
+               "batched_decode_attention: a quantized row must fit 64 KiB of LDS");
   const bool chunked = workspace && need > 0;
   const int kpc = chunked ? (int)batched_chunk_keys(cache_rows) : (int)cache_rows;
   const int nchunk = (int)((cache_rows + kpc - 1) / kpc);
@@ -1104,11 +1159,16 @@ extern "C" int qasr_batched_decode_attention_f32(float* out, const float* q, con
   const dim3 grid((unsigned)(batch * n_kv_heads), 1, (unsigned)nchunk);
   hipStream_t st = as_stream(stream);
   const int nk = (int)n_kv_heads;
+  const unsigned qthreads = (unsigned)(64 * (n_heads < 16 ? n_heads : 16));
 #define QASR_BATCH(HD, GG)                                                                                 \
   if (head_dim == HD && G == GG) {                                                                         \
     attention_decode_split_kernel<HD, GG, false, true><<<grid, 256, 0, st>>>(                             \
         q, k_cache, v_cache, 1, (int)cache_rows, nk, scale, 0, kpc, ws_o, ws_ml, DecodePre{}, b);          \
-    if (chunked)                                                                                           \
+    if (out_q)                                                                                             \
+      attention_combine_quant_kernel<HD><<<(unsigned)batch, qthreads, n_heads * HD * 4, st>>>(           \
+          out, out_q, out_scales, ws_o, ws_ml, positions, (long long)cache_rows, (int)n_heads, nchunk,      \
+          kpc);                                                                                            \
+    else if (chunked)                                                                                      \
       attention_combine_batch_kernel<HD><<<(unsigned)((rows_heads + 3) / 4), 256, 0, st>>>(               \
           out, ws_o, ws_ml, positions, (long long)cache_rows, (int)n_heads, (long long)rows_heads, nchunk, \
           kpc);                                                                                            \

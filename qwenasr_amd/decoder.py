@@ -237,8 +237,8 @@ class DecoderInt8Batched:
     ``w8a8=True`` runs the four projections on int8 matrix cores with each
     stream's activation row quantized per row (quantize.rs:633-662 arithmetic),
     the c5 way: add + RMSNorm + quantization in one launch; q/k/v with the head
-    norms, RoPE and the K/V cache rows in the GEMM epilogue; attention; the
-    attention rows quantized, o; add + RMSNorm + quantization; gate/up with
+    norms, RoPE and the K/V cache rows in the GEMM epilogue; attention, its
+    rows quantized in the chunk-merge launch; o; add + RMSNorm + quantization; gate/up with
     SwiGLU in the epilogue; the SwiGLU rows quantized, down. The int8 weights
     are the same; the activations are rounded to int8 at those four points,
     so the results follow the reference's within that rounding, not 1e-5. The
@@ -301,8 +301,7 @@ class DecoderInt8Batched:
         K.qkv_heads_w8a8_packed(self.q, kb, vb, self.rows, pk["qkv"], self.xq, self.xs, lw["q_norm"],
                                 lw["k_norm"], self.rope, self.positions, B, H, nq, nk, hd, eps)
         K.batched_decode_attention(self.attn, self.q, kb, vb, self.rows, self.positions, B, nq, nk, hd,
-                                   self.scale, self.attn_ws)
-        K.quantize_rows_i8(self.aq, self.as_, self.attn, B, nq * hd)
+                                   self.scale, self.attn_ws, self.aq, self.as_)  # + the rows quantized
         K.linear_w8a8_packed(self.proj, pk["wo"], self.aq, self.as_, B, nq * hd, H)
         K.add_rms_norm_quant(self.x, self.proj, lw["post_attn_norm"], None, self.xq, self.xs, B, H, eps)
         K.gate_up_swiglu_w8a8_packed(self.ffn, pk["gate_up"], self.xq, self.xs, B, H, I)

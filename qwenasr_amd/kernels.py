@@ -228,14 +228,22 @@ def batched_decode_workspace(batch: int, n_heads: int, head_dim: int, cache_rows
 
 
 def batched_decode_attention(out, q, k_cache, v_cache, cache_rows: int, positions, batch: int, n_heads: int,
-                             n_kv_heads: int, head_dim: int, scale: float, workspace=None) -> None:
+                             n_kv_heads: int, head_dim: int, scale: float, workspace=None, out_q=None,
+                             out_scales=None) -> None:
     """Decode attention of ``batch`` streams, each over rows 0..positions[m] of its
     own cache block ``[batch, cache_rows, n_kv_heads * head_dim]`` (decoder.rs:900-903
     per stream). With ``workspace`` (batched_decode_workspace) every stream's
     keys are cut into chunks of 512 and the chunk partials merged; without it
-    one workgroup per (stream, kv head) walks all of its keys."""
+    one workgroup per (stream, kv head) walks all of its keys. ``out_q`` /
+    ``out_scales`` (int8 [batch * n_heads * head_dim], f32 [batch]) also get each
+    stream's row quantized per row, as quantize_rows_i8 would on ``out``."""
     if workspace is not None:
         _need(workspace, F32, 1, "workspace")
+    if (out_q is None) != (out_scales is None):
+        raise ValueError("out_q and out_scales go together")
+    if out_q is not None:
+        _need(out_q, I8, batch * n_heads * head_dim, "out_q")
+        _need(out_scales, F32, batch, "out_scales")
     kv = n_kv_heads * head_dim
     _need(out, F32, batch * n_heads * head_dim, "out")
     _need(q, F32, batch * n_heads * head_dim, "q")
@@ -244,7 +252,7 @@ def batched_decode_attention(out, q, k_cache, v_cache, cache_rows: int, position
     _need(positions, I32, batch, "positions")
     _lib.call("qasr_batched_decode_attention_f32", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), cache_rows,
               _ptr(positions), batch, n_heads, n_kv_heads, head_dim, scale, _ptr(workspace),
-              0 if workspace is None else workspace.numel(), _stream())
+              0 if workspace is None else workspace.numel(), _ptr(out_q), _ptr(out_scales), _stream())
 
 
 def attention_workspace(seq_q: int, n_heads: int, head_dim: int, device="cuda") -> torch.Tensor:

@@ -229,18 +229,22 @@ def test_batched_decode_step_matches_the_oracle_per_stream(tmp_path, dev, H, I, 
 
 class _RoundingRecorder:
     """Keeps a copy of every per-row int8 activation (values and scales) that
-    the device computes through K.add_rms_norm_quant / K.quantize_rows_i8."""
+    the device computes through K.add_rms_norm_quant, K.quantize_rows_i8 and
+    the quantized form of K.batched_decode_attention."""
+
+    # entry point -> positions of (q, scales, rows) among its arguments
+    WHERE = {"add_rms_norm_quant": (4, 5, 6), "quantize_rows_i8": (0, 1, 3), "batched_decode_attention": (12, 13, 6)}
 
     def __init__(self, monkeypatch, K):
         self.seen = []
-        for name in ("add_rms_norm_quant", "quantize_rows_i8"):
+        for name, (iq, isc, irows) in self.WHERE.items():
             orig = getattr(K, name)
 
-            def wrap(*a, _orig=orig, _name=name):
+            def wrap(*a, _orig=orig, _iq=iq, _isc=isc, _irows=irows):
                 _orig(*a)
-                q, s = (a[4], a[5]) if _name == "add_rms_norm_quant" else (a[0], a[1])
-                rows = a[6] if _name == "add_rms_norm_quant" else a[3]
-                self.seen.append((q.view(rows, -1).cpu().numpy().copy(), s[:rows].cpu().numpy().copy()))
+                if len(a) > _isc and a[_iq] is not None:
+                    q, sc, rows = a[_iq], a[_isc], a[_irows]
+                    self.seen.append((q.view(rows, -1).cpu().numpy().copy(), sc[:rows].cpu().numpy().copy()))
 
             monkeypatch.setattr(K, name, wrap)
 
@@ -383,6 +387,39 @@ def test_batched_decode_step_graph_replay_equals_eager(tmp_path, dev, w8a8):
         torch.cuda.synchronize()
         for i, (a, b) in enumerate(zip(outputs(), ref)):
             assert torch.equal(a, b), (rep, i)
+
+
+@pytest.mark.parametrize("nq,nk,hd,rows", [(16, 8, 128, 1300), (16, 8, 128, 400), (8, 8, 128, 1300),
+                                           (4, 4, 64, 700)])
+def test_batched_decode_attention_quantized_rows(dev, nq, nk, hd, rows):
+    """The quantized form: out as without it, and out_q / out_scales equal to
+    quantize_rows_i8 on out bit for bit -- rows merged from several chunks,
+    rows of one chunk, a NaN row for a position outside the cache, fewer than
+    16 heads (fewer waves in the merge workgroup), chunked and not."""
+    from qwenasr_amd import kernels as K
+
+    B, kv = 6, nk * hd
+    r = np.random.default_rng([60, nq, rows])
+    d = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    q = d(r.standard_normal(B * nq * hd).astype(np.float32))
+    kc = d(r.standard_normal(B * rows * kv).astype(np.float32))
+    vc = d(r.standard_normal(B * rows * kv).astype(np.float32))
+    pos = d(np.array([0, rows - 1, rows, rows // 2, 511, 512], np.int32))
+    for ws in (None, K.batched_decode_workspace(B, nq, hd, rows, dev)):
+        plain = torch.empty(B * nq * hd, device=dev)
+        K.batched_decode_attention(plain, q, kc, vc, rows, pos, B, nq, nk, hd, hd ** -0.5, ws)
+        out = torch.empty(B * nq * hd, device=dev)
+        oq = torch.full((B * nq * hd,), 99, dtype=torch.int8, device=dev)
+        osc = torch.full((B,), -1.0, device=dev)
+        print(f"[batched] attention quantized nq={nq} rows={rows} chunked={ws is not None}", flush=True)
+        K.batched_decode_attention(out, q, kc, vc, rows, pos, B, nq, nk, hd, hd ** -0.5, ws, oq, osc)
+        rq = torch.empty_like(oq)
+        rs = torch.empty_like(osc)
+        K.quantize_rows_i8(rq, rs, out, B, nq * hd)
+        torch.cuda.synchronize()
+        assert torch.equal(out.isnan(), plain.isnan()) and torch.equal(out.nan_to_num(), plain.nan_to_num())
+        assert out.view(B, -1)[2].isnan().all()
+        assert torch.equal(oq, rq) and torch.equal(osc, rs)
 
 
 @pytest.mark.parametrize("nq,nk,hd", [(8, 8, 128), (4, 4, 64), (8, 4, 64), (16, 4, 64)])
