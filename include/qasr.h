@@ -494,14 +494,27 @@ int qasr_decode_attention_f32(float* out, float* q, const float* k, const float*
  * [batch, n_heads * head_dim], f32 [batch]) each stream's row is also
  * quantized per row in the launch that merges the chunks, with the values
  * and scale qasr_quantize_rows_i8 gives on out (the input of a W8A8 o
- * projection; n_heads * head_dim * 4 <= 65536). No reference counterpart as
- * one call (the reference decodes one stream at a time). */
+ * projection; n_heads * head_dim * 4 <= 65536). With order (from
+ * qasr_batched_decode_order_i32 on the same positions) the streams are
+ * walked longest first, which evens out the tail of a batch at different
+ * positions; the results are the same. An order that is not a permutation of
+ * the batch leaves the rows of the streams it misses unwritten (never out of
+ * bounds). No reference counterpart as one call (the reference decodes one
+ * stream at a time). */
 int qasr_batched_decode_attention_f32(float* out, const float* q, const float* k_cache,
                                       const float* v_cache, size_t cache_rows,
                                       const int32_t* positions, size_t batch, size_t n_heads,
                                       size_t n_kv_heads, size_t head_dim, float scale, float* workspace,
                                       size_t workspace_floats, int8_t* out_q, float* out_scales,
-                                      void* stream);
+                                      const int32_t* order, void* stream);
+
+/* order[2r], order[2r + 1] = the stream of rank r and its position, ranking
+ * the batch's streams by their number of keys (positions[m] + 1; 0 for a
+ * position outside [0, cache_rows)), most first, ties by stream index. One
+ * launch; the same order serves every layer of a decode step (positions
+ * change only between steps). batch <= 65536. No reference counterpart. */
+int qasr_batched_decode_order_i32(int32_t* order, const int32_t* positions, size_t batch,
+                                  size_t cache_rows, void* stream);
 
 /* Workspace floats qasr_batched_decode_attention_f32 uses for these sizes (0:
  * the cache is one chunk, no workspace is needed). */

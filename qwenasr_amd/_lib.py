@@ -81,7 +81,8 @@ SIGNATURES: dict[str, list] = {
     "qasr_pack_w8a8_tiles": [P, P, Z, Z, P],
     "qasr_gate_up_swiglu_w8a8_packed": [P, P, P, P, P, Z, Z, Z, P],
     "qasr_linear_w8a8_packed": [P, P, P, P, P, Z, Z, Z, P],
-    "qasr_batched_decode_attention_f32": [P, P, P, P, Z, P, Z, Z, Z, Z, F, P, Z, P, P, P],
+    "qasr_batched_decode_attention_f32": [P, P, P, P, Z, P, Z, Z, Z, Z, F, P, Z, P, P, P, P],
+    "qasr_batched_decode_order_i32": [P, P, Z, Z, P],
     "qasr_qkv_heads_w8a8_packed": [P, P, P, Z, P, P, P, P, P, P, P, P, Z, P, Z, Z, Z, Z, Z, F, P],
     # .qint8 files: host-side handle calls (out-parameters are host pointers)
     "qasr_qint8_open": [c_char_p, P],

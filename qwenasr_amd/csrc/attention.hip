@@ -300,6 +300,7 @@ struct DecodeBatch {
   const int32_t* positions;
   long long cache_rows;
   float* out;
+  const int32_t* order;  // optional: [batch][2] (stream, position), the longest streams first
 };
 
 template <int HD, int G, bool PRE = false, bool BATCH = false>
@@ -316,18 +317,31 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
   __shared__ __align__(16) float co[4][G][HD];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int quarter = lane & 3, kq = lane >> 2;  // dim quarter, key within the wave's 16
-  // BATCH: blockIdx.x = stream * nk + kv head. Workgroup n runs on XCD n % 8,
+  // BATCH: blockIdx.x = rank * nk + kv head. Workgroup n runs on XCD n % 8,
   // so with the head fastest one stream's heads fall on different XCDs and
   // every XCD gets the same share of each stream's keys (stream-fastest put
-  // all of stream m on XCD m % 8: 15% slower at positions U[0,2047]).
-  const int i = BATCH ? (int)(blockIdx.x / (unsigned)nk) : (int)blockIdx.x;
+  // all of stream m on XCD m % 8: 15% slower at positions U[0,2047]). The
+  // rank is the stream itself, or with batch.order the stream of that rank
+  // in longest-first order (its position comes with it: one 8-byte load), so
+  // the longest walks are dispatched first and the short ones fill the tail.
+  const int rank = BATCH ? (int)(blockIdx.x / (unsigned)nk) : 0;
+  [[maybe_unused]] long long order_pos = 0;
+  int i = BATCH ? rank : (int)blockIdx.x;
+  if constexpr (BATCH) {
+    if (batch.order) {
+      const int2 e = reinterpret_cast<const int2*>(batch.order)[rank];
+      if ((unsigned)e.x >= gridDim.x / (unsigned)nk) return;  // not an order of this batch: nothing read
+      i = e.x;
+      order_pos = e.y;
+    }
+  }
   const int kh = BATCH ? (int)(blockIdx.x % (unsigned)nk) : (int)blockIdx.y;
   const size_t q_stride = (size_t)nk * G * HD, kv_stride = (size_t)nk * HD;
   float4 qv[G][C4];
   [[maybe_unused]] bool bad_pos = false;
   int k_lim;
   if constexpr (BATCH) {
-    const long long p = batch.positions[i];
+    const long long p = batch.order ? order_pos : (long long)batch.positions[i];
     bad_pos = p < 0 || p >= batch.cache_rows;
     k_lim = bad_pos ? 0 : (int)p + 1;
     if ((int)blockIdx.z * keys_per_split >= max(k_lim, 1)) return;  // uniform: a chunk with no keys
@@ -1107,6 +1121,54 @@ static size_t batched_chunk_keys(size_t cache_rows) {
   return r > 512 ? r : 512;
 }
 
+namespace qasr {
+namespace {
+// order[r] = (stream, position) of the stream of rank r when the streams are
+// sorted by their number of keys (position + 1; 0 outside the cache),
+// most first, ties by stream index: a strict total order, so the ranks are a
+// permutation. Each thread ranks one stream against all of them, 1024
+// positions at a time through LDS (batch^2 comparisons).
+__global__ __launch_bounds__(256) void batched_order_kernel(int32_t* __restrict__ order,
+                                                            const int32_t* __restrict__ positions, int batch,
+                                                            long long cache_rows) {
+  __shared__ int keys[1024];
+  auto key_of = [&](int j) {
+    const long long p = positions[j];
+    return (p < 0 || p >= cache_rows) ? 0 : (int)p + 1;
+  };
+  const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  const int ki = i < batch ? key_of(i) : 0;
+  int rank = 0;
+  for (int base = 0; base < batch; base += 1024) {
+    const int n = min(1024, batch - base);
+    __syncthreads();
+    for (int t = (int)threadIdx.x; t < n; t += 256) keys[t] = key_of(base + t);
+    __syncthreads();
+    if (i < batch)
+      for (int t = 0; t < n; ++t) {
+        const int kj = keys[t];
+        rank += (kj > ki) || (kj == ki && base + t < i);
+      }
+  }
+  if (i < batch) {
+    order[2 * rank] = i;
+    order[2 * rank + 1] = positions[i];
+  }
+}
+}  // namespace
+}  // namespace qasr
+
+extern "C" int qasr_batched_decode_order_i32(int32_t* order, const int32_t* positions, size_t batch,
+                                             size_t cache_rows, void* stream) {
+  if (batch == 0) return QASR_OK;
+  QASR_REQUIRE(order && positions, "batched_decode_order: null pointer");
+  QASR_REQUIRE(batch <= 65536 && cache_rows > 0 && cache_rows < 0x40000000u,
+               "batched_decode_order: batch must be at most 65536 and cache_rows in [1, 2^30)");
+  batched_order_kernel<<<(unsigned)((batch + 255) / 256), 256, 0, as_stream(stream)>>>(
+      order, positions, (int)batch, (long long)cache_rows);
+  return launch_status("batched_decode_order");
+}
+
 // 0 also when the size would overflow (such a call is rejected anyway).
 extern "C" size_t qasr_batched_decode_attention_workspace_floats(size_t batch, size_t n_heads, size_t head_dim,
                                                                  size_t cache_rows) {
@@ -1123,7 +1185,7 @@ extern "C" int qasr_batched_decode_attention_f32(float* out, const float* q, con
                                                  const int32_t* positions, size_t batch, size_t n_heads,
                                                  size_t n_kv_heads, size_t head_dim, float scale,
                                                  float* workspace, size_t workspace_floats, int8_t* out_q,
-                                                 float* out_scales, void* stream) {
+                                                 float* out_scales, const int32_t* order, void* stream) {
   if (batch == 0 || n_heads == 0) return QASR_OK;
   QASR_REQUIRE(out && q && k_cache && v_cache && positions, "batched_decode_attention: null pointer");
   QASR_REQUIRE(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
@@ -1154,7 +1216,7 @@ extern "C" int qasr_batched_decode_attention_f32(float* out, const float* q, con
   const size_t rows_heads = batch * n_heads;
   float* ws_o = chunked ? workspace : nullptr;
   float* ws_ml = chunked ? workspace + rows_heads * nchunk * head_dim : nullptr;
-  const DecodeBatch b{positions, (long long)cache_rows, out};
+  const DecodeBatch b{positions, (long long)cache_rows, out, order};
   QASR_REQUIRE(batch * n_kv_heads <= 0x7fffffffu, "batched_decode_attention: batch * n_kv_heads too large");
   const dim3 grid((unsigned)(batch * n_kv_heads), 1, (unsigned)nchunk);
   hipStream_t st = as_stream(stream);

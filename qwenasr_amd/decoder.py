@@ -227,7 +227,8 @@ class DecoderInt8Batched:
       residual add + input RMSNorm; the q/k/v projections (one matrix-core
       launch for the three, the reference's W8A32 arithmetic); q/k head
       RMSNorm + RoPE at each stream's position with its K/V rows stored into
-      its cache; attention of each stream over its own rows 0..pos; o;
+      its cache; attention of each stream over its own rows 0..pos (the
+      streams walked longest first, ``attn_chunked`` below); o;
       residual add + post-attention RMSNorm; gate/up with the decode loop's
       SwiGLU in the GEMM epilogue; down.
     Then the last residual add + final RMSNorm and the lm_head with each
@@ -238,17 +239,22 @@ class DecoderInt8Batched:
     stream's activation row quantized per row (quantize.rs:633-662 arithmetic),
     the c5 way: add + RMSNorm + quantization in one launch; q/k/v with the head
     norms, RoPE and the K/V cache rows in the GEMM epilogue; attention, its
-    rows quantized in the chunk-merge launch; o; add + RMSNorm + quantization; gate/up with
+    rows quantized in the launch after it (which also merges key chunks); o;
+    add + RMSNorm + quantization; gate/up with
     SwiGLU in the epilogue; the SwiGLU rows quantized, down. The int8 weights
     are the same; the activations are rounded to int8 at those four points,
     so the results follow the reference's within that rounding, not 1e-5. The
     lm_head stays W8A32.
+
+    ``attn_chunked`` (default: when batch * n_kv_heads < 1024) also cuts each
+    stream's keys into chunks for the attention, to give a small batch enough
+    workgroups; the results are the same either way within 1e-6.
     """
 
     def __init__(self, weights: dict, hidden: int, intermediate: int, n_layers: int, batch: int,
                  cache_rows: int, n_heads: int = 16, n_kv_heads: int = 8, head_dim: int = 128,
                  eps: float = 1e-6, theta: float = 1e6, vocab: int | None = None, device="cuda",
-                 w8a8: bool = False):
+                 w8a8: bool = False, attn_chunked: bool | None = None):
         self.w = weights
         self.H, self.I, self.L, self.B = hidden, intermediate, n_layers, batch
         self.nq, self.nk, self.hd = n_heads, n_kv_heads, head_dim
@@ -276,7 +282,14 @@ class DecoderInt8Batched:
         self.rope = K.RopeCache(device)
         self.rope.ensure(cache_rows, head_dim, theta)
         self.scale = 1.0 / math.sqrt(head_dim)
-        self.attn_ws = K.batched_decode_workspace(B, n_heads, head_dim, cache_rows, device)
+        # Attention walks the streams longest first (one order per step). With
+        # B * n_kv_heads >= 1024 workgroups that alone balances the GPU and
+        # each (stream, kv head) walks all its keys; below it the keys are also
+        # cut into chunks (merged in a second launch) to give the GPU work.
+        if attn_chunked is None:
+            attn_chunked = B * n_kv_heads < 1024
+        self.attn_ws = K.batched_decode_workspace(B, n_heads, head_dim, cache_rows, device) if attn_chunked else None
+        self.order = torch.empty(2 * B, dtype=torch.int32, device=device)
         self.w8a8 = w8a8
         if w8a8:
             i8 = dict(dtype=torch.int8, device=device)
@@ -301,7 +314,7 @@ class DecoderInt8Batched:
         K.qkv_heads_w8a8_packed(self.q, kb, vb, self.rows, pk["qkv"], self.xq, self.xs, lw["q_norm"],
                                 lw["k_norm"], self.rope, self.positions, B, H, nq, nk, hd, eps)
         K.batched_decode_attention(self.attn, self.q, kb, vb, self.rows, self.positions, B, nq, nk, hd,
-                                   self.scale, self.attn_ws, self.aq, self.as_)  # + the rows quantized
+                                   self.scale, self.attn_ws, self.aq, self.as_, self.order)  # + rows quantized
         K.linear_w8a8_packed(self.proj, pk["wo"], self.aq, self.as_, B, nq * hd, H)
         K.add_rms_norm_quant(self.x, self.proj, lw["post_attn_norm"], None, self.xq, self.xs, B, H, eps)
         K.gate_up_swiglu_w8a8_packed(self.ffn, pk["gate_up"], self.xq, self.xs, B, H, I)
@@ -315,6 +328,7 @@ class DecoderInt8Batched:
         give NaN rows and write no cache row."""
         H, I, B, nq, nk, hd, eps = self.H, self.I, self.B, self.nq, self.nk, self.hd, self.eps
         self.x.copy_(embeds[:B * H])
+        K.batched_decode_order(self.order, self.positions, B, self.rows)
         for l, lw in enumerate(self.w["layers"]):
             if self.w8a8:
                 self._layer_w8a8(l, lw)
@@ -329,7 +343,7 @@ class DecoderInt8Batched:
             K.head_rms_norm_rope_kv(self.q, self.kk, self.vv, lw["q_norm"], lw["k_norm"], self.rope,
                                     self.positions, 0, B, nq, nk, hd, eps, kb, vb, self.rows)
             K.batched_decode_attention(self.attn, self.q, kb, vb, self.rows, self.positions, B, nq, nk, hd,
-                                       self.scale, self.attn_ws)
+                                       self.scale, self.attn_ws, order=self.order)
             wo = lw["wo"]
             K.linear_nobias_int8(self.proj, self.attn, wo.data, wo.scales, B, nq * hd, H)
             K.add_rms_norm(self.x, self.proj, lw["post_attn_norm"], self.x_norm, B, H, eps)

@@ -227,9 +227,17 @@ def batched_decode_workspace(batch: int, n_heads: int, head_dim: int, cache_rows
     return torch.empty(n, dtype=F32, device=device) if n else None
 
 
+def batched_decode_order(order, positions, batch: int, cache_rows: int) -> None:
+    """order (int32 [2 * batch]) = (stream, position) pairs, the streams with the
+    most keys first, for batched_decode_attention's ``order``."""
+    _need(order, I32, 2 * batch, "order")
+    _need(positions, I32, batch, "positions")
+    _lib.call("qasr_batched_decode_order_i32", _ptr(order), _ptr(positions), batch, cache_rows, _stream())
+
+
 def batched_decode_attention(out, q, k_cache, v_cache, cache_rows: int, positions, batch: int, n_heads: int,
                              n_kv_heads: int, head_dim: int, scale: float, workspace=None, out_q=None,
-                             out_scales=None) -> None:
+                             out_scales=None, order=None) -> None:
     """Decode attention of ``batch`` streams, each over rows 0..positions[m] of its
     own cache block ``[batch, cache_rows, n_kv_heads * head_dim]`` (decoder.rs:900-903
     per stream). With ``workspace`` (batched_decode_workspace) every stream's
@@ -244,6 +252,8 @@ def batched_decode_attention(out, q, k_cache, v_cache, cache_rows: int, position
     if out_q is not None:
         _need(out_q, I8, batch * n_heads * head_dim, "out_q")
         _need(out_scales, F32, batch, "out_scales")
+    if order is not None:
+        _need(order, I32, 2 * batch, "order")
     kv = n_kv_heads * head_dim
     _need(out, F32, batch * n_heads * head_dim, "out")
     _need(q, F32, batch * n_heads * head_dim, "q")
@@ -252,7 +262,8 @@ def batched_decode_attention(out, q, k_cache, v_cache, cache_rows: int, position
     _need(positions, I32, batch, "positions")
     _lib.call("qasr_batched_decode_attention_f32", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), cache_rows,
               _ptr(positions), batch, n_heads, n_kv_heads, head_dim, scale, _ptr(workspace),
-              0 if workspace is None else workspace.numel(), _ptr(out_q), _ptr(out_scales), _stream())
+              0 if workspace is None else workspace.numel(), _ptr(out_q), _ptr(out_scales), _ptr(order),
+              _stream())
 
 
 def attention_workspace(seq_q: int, n_heads: int, head_dim: int, device="cuda") -> torch.Tensor:

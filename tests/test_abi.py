@@ -263,16 +263,20 @@ def test_batched_entry_points_validation():
     att = so.qasr_batched_decode_attention_f32
     out, q, kc, vc, pos, ws = P[:6]
     # (out, q, k_cache, v_cache, cache_rows, positions, batch, n_heads, n_kv_heads, head_dim, scale, ws, n,
-    #  out_q, out_scales, stream)
-    assert att(out, q, kc, vc, 2048, pos, 4, 16, 5, 128, 0.088, NULL, 0, NULL, NULL, NULL) == inv  # 16 % 5 != 0
-    assert att(out, NULL, kc, vc, 2048, pos, 4, 16, 8, 128, 0.088, NULL, 0, NULL, NULL, NULL) == inv
-    assert att(out, q, kc, vc, 2048, pos, 4, 32, 8, 128, 0.088, NULL, 0, NULL, NULL, NULL) == uns  # G = 4 at head_dim 128
-    assert att(out, q, kc, vc, 2048, pos, 4, 16, 8, 96, 0.088, NULL, 0, NULL, NULL, NULL) == uns
+    #  out_q, out_scales, order, stream)
+    assert att(out, q, kc, vc, 2048, pos, 4, 16, 5, 128, 0.088, NULL, 0, NULL, NULL, NULL, NULL) == inv  # 16 % 5 != 0
+    assert att(out, NULL, kc, vc, 2048, pos, 4, 16, 8, 128, 0.088, NULL, 0, NULL, NULL, NULL, NULL) == inv
+    assert att(out, q, kc, vc, 2048, pos, 4, 32, 8, 128, 0.088, NULL, 0, NULL, NULL, NULL, NULL) == uns  # G = 4 at head_dim 128
+    assert att(out, q, kc, vc, 2048, pos, 4, 16, 8, 96, 0.088, NULL, 0, NULL, NULL, NULL, NULL) == uns
     need = so.qasr_batched_decode_attention_workspace_floats(4, 16, 128, 2048)
-    assert att(out, q, kc, vc, 2048, pos, 4, 16, 8, 128, 0.088, ws, need - 1, NULL, NULL, NULL) == inv
+    assert att(out, q, kc, vc, 2048, pos, 4, 16, 8, 128, 0.088, ws, need - 1, NULL, NULL, NULL, NULL) == inv
     assert "workspace" in last_error()
-    assert att(out, q, kc, vc, 2048, pos, 0, 16, 8, 128, 0.088, NULL, 0, NULL, NULL, NULL) == _lib.QASR_OK
-    assert att(out, q, kc, vc, 2048, pos, 4, 16, 8, 128, 0.088, NULL, 0, P[6], NULL, NULL) == inv  # q without scales
+    assert att(out, q, kc, vc, 2048, pos, 0, 16, 8, 128, 0.088, NULL, 0, NULL, NULL, NULL, NULL) == _lib.QASR_OK
+    assert att(out, q, kc, vc, 2048, pos, 4, 16, 8, 128, 0.088, NULL, 0, P[6], NULL, NULL, NULL) == inv  # q without scales
+    order = so.qasr_batched_decode_order_i32
+    assert order(NULL, pos, 4, 2048, NULL) == inv
+    assert order(P[6], pos, 65537, 2048, NULL) == inv
+    assert order(P[6], pos, 0, 2048, NULL) == _lib.QASR_OK
     lin = so.qasr_linear_w8a8_packed
     y, w, sc, xq, xs = P[6:11]
     # (y, w_packed, scales, xq, x_scales, batch, in_dim, out_dim, stream)

@@ -177,14 +177,16 @@ def test_batched_projection_rejects_unsupported_shapes(dev):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("H,I,B", [(2048, 6144, 9), (1024, 3072, 3)])
-def test_batched_decode_step_matches_the_oracle_per_stream(tmp_path, dev, H, I, B):
+@pytest.mark.parametrize("H,I,B,chunked", [(2048, 6144, 9, None), (1024, 3072, 3, None), (1024, 3072, 9, False)])
+def test_batched_decode_step_matches_the_oracle_per_stream(tmp_path, dev, H, I, B, chunked):
     """DecoderInt8Batched (B streams, each at its own position over its own
     cache) against the oracle's decode step (decoder.rs:848-965) run stream
     by stream: final hidden state, logits, the new K/V rows of every layer and
     the token, over two consecutive steps. B = 9 takes the matrix-core paths
-    (8+ rows), B = 3 the per-row ones. Tolerance as for the single-stream
-    decode step (chained kernels, rel/abs 1e-4)."""
+    (8+ rows), B = 3 the per-row ones; the attention with its keys cut into
+    chunks (the small-batch default) and walked whole (the large-batch one),
+    both in longest-first order. Tolerance as for the single-stream decode
+    step (chained kernels, rel/abs 1e-4)."""
     from oracle.decoder import decode_int8_step
     from qwenasr_amd.decoder import DecoderInt8Batched
     from tests.test_decoder_step import _load
@@ -193,7 +195,7 @@ def test_batched_decode_step_matches_the_oracle_per_stream(tmp_path, dev, H, I, 
     L, vocab, rows, TOL = 2, 1000, 2100, 1e-4
     r = np.random.default_rng([55, H, B])
     w = small_decoder(r, H, I, L, NQ, NK, HD, vocab)
-    dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev)
+    dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev, attn_chunked=chunked)
     kv = NK * HD
     pos = np.array([0, 1500, 7, 64, 2100 - 3, 1, 510, 255, 1023][:B], np.int32)  # 1-5 key chunks
     kc = r.standard_normal((B, L, rows, kv)).astype(np.float32)  # earlier contexts, one per stream
@@ -344,8 +346,8 @@ def test_batched_w8a8_decode_step_matches_the_oracle_per_stream(tmp_path, dev, m
     assert torch.equal(dec.positions.cpu(), torch.from_numpy(pos + 2))
 
 
-@pytest.mark.parametrize("w8a8", [False, True])
-def test_batched_decode_step_graph_replay_equals_eager(tmp_path, dev, w8a8):
+@pytest.mark.parametrize("w8a8,chunked", [(False, True), (True, True), (False, False), (True, False)])
+def test_batched_decode_step_graph_replay_equals_eager(tmp_path, dev, w8a8, chunked):
     """One batched decode step (both forms) captured in a HIP graph: every
     replay gives the eager step's hidden state, logits, tokens and new K/V
     rows bit for bit, with eager work and synchronisations between replays
@@ -357,7 +359,8 @@ def test_batched_decode_step_graph_replay_equals_eager(tmp_path, dev, w8a8):
     H, I, L, B, rows, vocab = 1024, 3072, 2, 12, 1300, 1000
     r = np.random.default_rng([58, int(w8a8)])
     w = small_decoder(r, H, I, L, NQ, NK, HD, vocab)
-    dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev, w8a8=w8a8)
+    dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev, w8a8=w8a8,
+                             attn_chunked=chunked)
     for l in range(L):
         dec.k[l].normal_()
         dec.v[l].normal_()
@@ -387,6 +390,50 @@ def test_batched_decode_step_graph_replay_equals_eager(tmp_path, dev, w8a8):
         torch.cuda.synchronize()
         for i, (a, b) in enumerate(zip(outputs(), ref)):
             assert torch.equal(a, b), (rep, i)
+
+
+@pytest.mark.parametrize("B", [7, 300, 1500])
+def test_batched_decode_order_and_ordered_attention(dev, B):
+    """The longest-first order: a permutation of the streams sorted by number
+    of keys (position + 1, 0 outside the cache) descending, ties by stream,
+    against numpy; attention walked in that order equals the stream-order
+    call bit for bit (each stream's work is the same, only its workgroup
+    differs), chunked and not, with the quantized rows too."""
+    from qwenasr_amd import kernels as K
+
+    rows = 700
+    r = np.random.default_rng([61, B])
+    pos = r.integers(0, rows, B).astype(np.int32)
+    pos[: min(B, 4)] = [5, 5, rows, -3][: min(B, 4)]  # a tie and two positions outside the cache
+    keys = np.where((pos >= 0) & (pos < rows), pos + 1, 0)
+    want = sorted(range(B), key=lambda i: (-int(keys[i]), i))
+    order = torch.empty(2 * B, dtype=torch.int32, device=dev)
+    pos_t = torch.from_numpy(pos).to(dev)
+    print(f"[batched] order B={B}", flush=True)
+    K.batched_decode_order(order, pos_t, B, rows)
+    torch.cuda.synchronize()
+    o = order.view(B, 2).cpu().numpy()
+    np.testing.assert_array_equal(o[:, 0], want)
+    np.testing.assert_array_equal(o[:, 1], pos[want])
+    if B > 300:
+        return  # the ranking at a larger batch; the attention below at two sizes
+    nq, nk, hd = 16, 8, 128
+    kv = nk * hd
+    q = torch.from_numpy(r.standard_normal(B * nq * hd).astype(np.float32)).to(dev)
+    kc = torch.from_numpy(r.standard_normal(B * rows * kv).astype(np.float32)).to(dev)
+    vc = torch.from_numpy(r.standard_normal(B * rows * kv).astype(np.float32)).to(dev)
+    for ws in (None, K.batched_decode_workspace(B, nq, hd, rows, dev)):
+        outs = []
+        for od in (None, order):
+            out = torch.empty(B * nq * hd, device=dev)
+            oq = torch.empty(B * nq * hd, dtype=torch.int8, device=dev)
+            osc = torch.empty(B, device=dev)
+            K.batched_decode_attention(out, q, kc, vc, rows, pos_t, B, nq, nk, hd, hd ** -0.5, ws, oq, osc, od)
+            outs.append((out, oq, osc))
+        torch.cuda.synchronize()
+        (a, aq, asc), (b, bq, bsc) = outs
+        assert torch.equal(a.isnan(), b.isnan()) and torch.equal(a.nan_to_num(), b.nan_to_num())
+        assert torch.equal(aq, bq) and torch.equal(asc, bsc)
 
 
 @pytest.mark.parametrize("nq,nk,hd,rows", [(16, 8, 128, 1300), (16, 8, 128, 400), (8, 8, 128, 1300),
