@@ -1131,7 +1131,7 @@ namespace {
 __global__ __launch_bounds__(256) void batched_order_kernel(int32_t* __restrict__ order,
                                                             const int32_t* __restrict__ positions, int batch,
                                                             long long cache_rows) {
-  __shared__ int keys[1024];
+  __shared__ __align__(16) int keys[1024];
   auto key_of = [&](int j) {
     const long long p = positions[j];
     return (p < 0 || p >= cache_rows) ? 0 : (int)p + 1;
@@ -1144,11 +1144,20 @@ __global__ __launch_bounds__(256) void batched_order_kernel(int32_t* __restrict_
     __syncthreads();
     for (int t = (int)threadIdx.x; t < n; t += 256) keys[t] = key_of(base + t);
     __syncthreads();
-    if (i < batch)
-      for (int t = 0; t < n; ++t) {
-        const int kj = keys[t];
-        rank += (kj > ki) || (kj == ki && base + t < i);
+    if (i < batch) {
+      // four keys per LDS read (n is a multiple of 4 except in the last block)
+      const int n4 = n & ~3;
+#pragma unroll 4
+      for (int t = 0; t < n4; t += 4) {
+        const int4 kk = *reinterpret_cast<const int4*>(&keys[t]);
+        const int j = base + t;
+        rank += (kk.x > ki) || (kk.x == ki && j < i);
+        rank += (kk.y > ki) || (kk.y == ki && j + 1 < i);
+        rank += (kk.z > ki) || (kk.z == ki && j + 2 < i);
+        rank += (kk.w > ki) || (kk.w == ki && j + 3 < i);
       }
+      for (int t = n4; t < n; ++t) rank += (keys[t] > ki) || (keys[t] == ki && base + t < i);
+    }
   }
   if (i < batch) {
     order[2 * rank] = i;
