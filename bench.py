@@ -736,6 +736,7 @@ class PrefillStep(Workload):
     unit_tokens = 512
     dtype = "int8/f32"
     T = 512
+    max_steps = 20  # ~3.9 ms per step
 
     def __init__(self, dev, torch):
         super().__init__(dev, torch)
@@ -1315,7 +1316,7 @@ def profile_kernel(torch, wl, name: str, n: int) -> int:
 
 
 # ---------------------------------------------------------------------------
-DEFAULT_CONFIGS = "c1,c1_cold,c2,c3_fused,c4,c5_b32,c5_layer,decode_step,decode_step_b256,decode_step_b256_w8a8"
+DEFAULT_CONFIGS = "c1,c1_cold,c2,c3_fused,c4,c5_b32,c5_layer,decode_step,decode_step_b256,decode_step_b256_w8a8,prefill_step"
 
 
 def _round(v):
@@ -1554,6 +1555,8 @@ def main() -> int:
         out["batched_decode_tokens_per_s"] = configs["decode_step_b256"]["tokens_per_s"]
     if "decode_step_b256_w8a8" in configs:
         out["batched_decode_w8a8_tokens_per_s"] = configs["decode_step_b256_w8a8"]["tokens_per_s"]
+    if "prefill_step" in configs:
+        out["prefill_tokens_per_s"] = configs["prefill_step"]["tokens_per_s"]
     print(json.dumps(out), flush=True)
     return 0
 
