@@ -629,9 +629,11 @@ constexpr int kGmBK = 64;           // K granularity of the GEMM path
 // expf tail after the gate/up projection) or the decode loop's form
 // (g / (1 + expf(-g)) * u, decoder.rs:916-921) for batched decode streams
 enum GemmEpi { kGemmRows = 0, kGemmBias = 1, kGemmSwiglu = 2, kGemmSwigluLibm = 3 };
-// K chunks in flight per thread in the LDS-staged kernel (2 and 3 measured
-// slower: the extra registers cost more than the latency they hide)
+// K chunks in flight per thread in the single-buffered LDS-staged kernel (2
+// and 3 measured slower: 1.7B gate/up at T = 512 86.0 -> 88.2 / 97.5 us), and
+// register sets of the double-buffered one (4 sets measured the same as 2)
 constexpr int kGemmPrefetch = 1;
+constexpr int kGemmSets = 2;
 
 QASR_DEV unsigned short bf16_bits_trunc(float v) { return (unsigned short)(__float_as_uint(v) >> 16); }
 QASR_DEV float bf16_trunc(float v) { return __uint_as_float(__float_as_uint(v) & 0xffff0000u); }
@@ -736,14 +738,14 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
   const float* xsrc = x + (size_t)min(t0 + x_tok, T - 1) * K + XF * x_part;
 
   v4i wv[NPF][WB / 16];
-  float4 xv[NPF][XF / 4];
+  v4f xv[NPF][XF / 4];
 #pragma unroll
   for (int q = 0; q < NPF; ++q)
     if (q * BK < K) {
 #pragma unroll
       for (int c = 0; c < WB / 16; ++c) wv[q][c] = *reinterpret_cast<const v4i*>(wsrc + q * BK + 16 * c);
 #pragma unroll
-      for (int c = 0; c < XF / 4; ++c) xv[q][c] = ld4(xsrc + q * BK, c);
+      for (int c = 0; c < XF / 4; ++c) xv[q][c] = *reinterpret_cast<const v4f*>(xsrc + q * BK + 4 * c);
     }
   for (int kb = 0; kb < K; kb += NPF * BK) {
 #pragma unroll
@@ -751,17 +753,22 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
       const int k0 = kb + q * BK;
       if (k0 >= K) break;
 #pragma unroll
-      for (int c = 0; c < WB / 16; ++c)
+      for (int c = 0; c < WB / 16; ++c) {
+        v4i wc = wv[q][c];
+        asm volatile("" : "+v"(wc));  // keeps the conversion from being hoisted next to the load
 #pragma unroll
         for (int e = 0; e < 4; ++e) {  // int8 -> bf16 is exact (at most 8 significant bits)
-          const int v = wv[q][c][e];
+          const int v = wc[e];
           const uint2 h = make_uint2(bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff)),
                                      bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff)));
           *reinterpret_cast<uint2*>(&wl[w_row][WB * w_part + 16 * c + 4 * e]) = h;
         }
+      }
 #pragma unroll
       for (int c = 0; c < XF / 4; ++c) {  // x = hi + mid + lo exactly
-        const float ev[4] = {xv[q][c].x, xv[q][c].y, xv[q][c].z, xv[q][c].w};
+        v4f xc = xv[q][c];
+        asm volatile("" : "+v"(xc));
+        const float ev[4] = {xc.x, xc.y, xc.z, xc.w};
         float r1[4], r2[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -779,7 +786,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
         for (int c = 0; c < WB / 16; ++c)
           wv[q][c] = *reinterpret_cast<const v4i*>(wsrc + k0 + NPF * BK + 16 * c);
 #pragma unroll
-        for (int c = 0; c < XF / 4; ++c) xv[q][c] = ld4(xsrc + k0 + NPF * BK, c);
+        for (int c = 0; c < XF / 4; ++c) xv[q][c] = *reinterpret_cast<const v4f*>(xsrc + k0 + NPF * BK + 4 * c);
       }
 #pragma unroll
       for (int kk = 0; kk < BK; kk += 16) {
@@ -841,6 +848,197 @@ constexpr size_t gemm_lds_bytes() {
   return (size_t)(BN + 3 * BT) * (BK + 8) * 2;
 }
 
+// Double-buffered form of the LDS-staged kernel, same tiles, same products in
+// the same order per accumulator (so the same results bit for bit). Two LDS
+// stages: while the MFMAs of chunk c read one stage, chunk c + 1 is converted
+// (int8 -> bf16, fp32 -> three bf16 terms) and written to the other, a slice
+// of that work after each 16-wide k step, so the conversion's VALU work issues
+// while the matrix pipe is busy instead of after it. Chunk c + 2's global
+// loads are in flight meanwhile in a second register set. One barrier per
+// chunk: it both publishes the staged chunk and retires the reads of the stage
+// the next chunk overwrites.
+template <int BN, int BT, int BK, int NS, int EPI>
+__global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, TileMap map,
+                                                                   const float* __restrict__ x, int T, int K) {
+  constexpr int kGmRow = BK + 8;                   // LDS row in bf16 (16-byte pad)
+  constexpr int STAGE = (BN + 3 * BT) * kGmRow;    // bf16 per LDS stage
+  extern __shared__ __align__(16) unsigned short gm_lds[];  // 2 x ([BN][kGmRow] weights, [3][BT][kGmRow] terms)
+  unsigned bx, by;
+  tile_of(map, blockIdx.x, bx, by);
+  float* y = set.y[0];
+  const int8_t* w = set.w[0];
+  const float* scales = set.s[0];
+  const float* bias = set.b[0];
+  int N = set.N[0];
+  unsigned bx0 = 0;
+#pragma unroll
+  for (int m = 1; m < 4; ++m)
+    if (m < set.n && bx >= set.bx_begin[m]) {
+      y = set.y[m];
+      w = set.w[m];
+      scales = set.s[m];
+      bias = set.b[m];
+      N = set.N[m];
+      bx0 = set.bx_begin[m];
+    }
+  constexpr int MI = BN / 64, MJ = BT / 64;
+  static_assert(BN % 64 == 0 && BT % 64 == 0, "32 x 32 blocks per wave");
+  constexpr int TPW = 256 / BN, WB = BK / TPW;       // weight staging: threads per row, bytes each
+  constexpr int TPX = 256 / BT, XF = BK / TPX;       // activation staging: threads per token, floats each
+  constexpr int NW = WB / 16, NX = XF / 4;           // 16-byte staging items per thread
+  constexpr int KSTEPS = BK / 16;                    // MFMA k steps per chunk
+  static_assert(NW >= 1 && NX >= 1, "each thread stages whole 16-byte items");
+  static_assert(NS >= 2 && NS % 2 == 0, "an even number of register sets");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave & 1, wc = wave >> 1;
+  const int r = lane & 31, g = lane >> 5;
+  const int n0 = (int)(bx - bx0) * BN, t0 = (int)by * BT;
+  v16f acc[MI][MJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) acc[i][j] = v16f{};
+
+  // rows and tokens past the end re-read the last one (valid memory; not stored)
+  const int w_row = tid / TPW, w_part = tid % TPW;
+  const int8_t* wsrc = w + (size_t)min(n0 + w_row, N - 1) * K + WB * w_part;
+  const int x_tok = tid / TPX, x_part = tid % TPX;
+  const float* xsrc = x + (size_t)min(t0 + x_tok, T - 1) * K + XF * x_part;
+
+  auto load = [&](v4i (&wv)[NW], v4f (&xv)[NX], int k0) {
+#pragma unroll
+    for (int c = 0; c < NW; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc + k0 + 16 * c);
+#pragma unroll
+    for (int c = 0; c < NX; ++c) xv[c] = *reinterpret_cast<const v4f*>(xsrc + k0 + 4 * c);
+  };
+  // The staging items that go after k step `part` (item c of N after step c * KSTEPS / N).
+  // Each item passes through an empty asm first: the conversion cannot then be
+  // hoisted next to the item's load, which would wait for the load right there.
+  auto stage = [&](const v4i (&wv)[NW], const v4f (&xv)[NX], unsigned short* st, int part) {
+    auto wl = reinterpret_cast<unsigned short (*)[kGmRow]>(st);
+    auto xl = reinterpret_cast<unsigned short (*)[BT][kGmRow]>(st + BN * kGmRow);
+#pragma unroll
+    for (int c = 0; c < NW; ++c) {
+      if (part >= 0 && c * KSTEPS / NW != part) continue;
+      v4i wc = wv[c];
+      asm volatile("" : "+v"(wc));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {  // int8 -> bf16 is exact (at most 8 significant bits)
+        const int v = wc[e];
+        const uint2 h = make_uint2(bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff)),
+                                   bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff)));
+        *reinterpret_cast<uint2*>(&wl[w_row][WB * w_part + 16 * c + 4 * e]) = h;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < NX; ++c) {  // x = hi + mid + lo exactly
+      if (part >= 0 && c * KSTEPS / NX != part) continue;
+      v4f xc = xv[c];
+      asm volatile("" : "+v"(xc));
+      const float ev[4] = {xc.x, xc.y, xc.z, xc.w};
+      float r1[4], r2[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r1[e] = ev[e] - bf16_trunc(ev[e]);
+        r2[e] = r1[e] - bf16_trunc(r1[e]);  // at most 8 significant bits
+      }
+      const int col = XF * x_part + 4 * c;
+      *reinterpret_cast<uint2*>(&xl[0][x_tok][col]) = make_uint2(bf16_pair(ev[0], ev[1]), bf16_pair(ev[2], ev[3]));
+      *reinterpret_cast<uint2*>(&xl[1][x_tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
+      *reinterpret_cast<uint2*>(&xl[2][x_tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
+    }
+  };
+  // k step s of the chunk staged in `st`: every product term in the order of
+  // the single-buffered kernel (term, then row block, then token block).
+  auto mfma_step = [&](const unsigned short* st, int s) {
+    auto wl = reinterpret_cast<const unsigned short (*)[kGmRow]>(st);
+    auto xl = reinterpret_cast<const unsigned short (*)[BT][kGmRow]>(st + BN * kGmRow);
+    const int kk = 16 * s;
+    v8bf a[MI], b[3][MJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) a[i] = *reinterpret_cast<const v8bf*>(&wl[(BN / 2) * wr + 32 * i + r][kk + 8 * g]);
+#pragma unroll
+    for (int term = 0; term < 3; ++term)
+#pragma unroll
+      for (int j = 0; j < MJ; ++j)
+        b[term][j] = *reinterpret_cast<const v8bf*>(&xl[term][(BT / 2) * wc + 32 * j + r][kk + 8 * g]);
+#pragma unroll
+    for (int term = 0; term < 3; ++term)
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[term][j], acc[i][j], 0, 0, 0);
+  };
+  // One chunk: its MFMAs from stage `cur`, the next chunk staged into `nxt` a
+  // slice per k step (straight-line code, so the scheduler can interleave the
+  // slice's VALU work with the MFMAs).
+  auto chunk = [&](const unsigned short* cur, unsigned short* nxt, const v4i (&wv)[NW],
+                   const v4f (&xv)[NX]) {
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      mfma_step(cur, s);
+      stage(wv, xv, nxt, s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Register set u holds chunks u, u + NS, ...: chunk j is loaded as soon as
+  // chunk j - NS has been staged, so NS - 1 chunks of MFMAs hide its latency.
+  // Chunks past the end re-load the last one (valid memory) and the final
+  // chunk stages it into the idle stage: the loop stays free of branches.
+  // The caller guarantees K % (NS * BK) == 0.
+  unsigned short* st0 = gm_lds;
+  unsigned short* st1 = gm_lds + STAGE;
+  const int nch = K / BK;
+  v4i wreg[NS][NW];
+  v4f xreg[NS][NX];
+#pragma unroll
+  for (int u = 0; u < NS; ++u) load(wreg[u], xreg[u], min(u, nch - 1) * BK);
+  stage(wreg[0], xreg[0], st0, -1);
+  load(wreg[0], xreg[0], min(NS, nch - 1) * BK);
+  lds_barrier();
+  for (int c = 0; c < nch; c += NS) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {  // chunk c + u from stage u % 2 (NS is even)
+      chunk((u & 1) ? st1 : st0, (u & 1) ? st0 : st1, wreg[(u + 1) % NS], xreg[(u + 1) % NS]);
+      load(wreg[(u + 1) % NS], xreg[(u + 1) % NS], min(c + u + 1 + NS, nch - 1) * BK);
+      lds_barrier();
+    }
+  }
+
+  // lane l, register 4q + v of block (i, j) holds row n0 + (BN/2)wr + 32i + 8q + 4(l/32) + v
+  // of token t0 + (BT/2)wc + 32j + l%32
+  const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+  for (int j = 0; j < MJ; ++j) {
+    const int t = t0 + (BT / 2) * wc + 32 * j + r;
+    if (t >= T) continue;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + (BN / 2) * wr + 32 * i + 8 * q + 4 * g;
+        float res[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int nv = min(n + v, N - 1);
+          res[v] = acc[i][j][4 * q + v] * scales[nv];
+          if constexpr (EPI == kGemmBias) res[v] += bias[nv];
+        }
+        if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
+          swiglu_store<EPI>(y, res, t, n, N);
+        } else if (vec_out && n + 3 < N) {
+          *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+        }
+      }
+  }
+}
+
 // Column split of the XCD map that minimises the bytes one XCD reads
 // (cols/a weight blocks of BN x K int8 + rows/(8/a) token blocks of BT x K fp32);
 // 0 when no split divides the tile grid evenly.
@@ -879,7 +1077,7 @@ QASR_DEV unsigned bf16_pair_i8(int v, int byte) {  // bytes byte, byte + 1 of v 
 template <int MI, int MJ>
 struct KsplitRaw {
   v4i w[MI][2];          // per 32-wide chunk: 16 int8 of one weight row
-  float4 x[MJ][2][4];    // per 32-wide chunk: 16 floats of one token
+  v4f x[MJ][2][4];       // per 32-wide chunk: 16 floats of one token
 };
 
 // Lane l, register 4q + v of block (i, j) holds row n0 + 32i + 8q + 4(l/32) + v
@@ -983,10 +1181,23 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
 #pragma unroll
       for (int j = 0; j < MJ; ++j)
 #pragma unroll
-        for (int f = 0; f < 4; ++f) raw.x[j][c][f] = ld4(xp[j] + k, f);
+        for (int f = 0; f < 4; ++f) raw.x[j][c][f] = *reinterpret_cast<const v4f*>(xp[j] + k + 4 * f);
     }
   };
-  auto compute = [&](const KsplitRaw<MI, MJ>& raw) {
+  // Every loaded register passes through an empty asm first, so no part of
+  // the conversion is hoisted next to its load (which would wait for the load
+  // there instead of one step later).
+  auto compute = [&](const KsplitRaw<MI, MJ>& in) {
+    KsplitRaw<MI, MJ> raw = in;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) asm volatile("" : "+v"(raw.w[i][c]));
+#pragma unroll
+      for (int j = 0; j < MJ; ++j)
+#pragma unroll
+        for (int f = 0; f < 4; ++f) asm volatile("" : "+v"(raw.x[j][c][f]));
+    }
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -1004,7 +1215,7 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
         for (int j = 0; j < MJ; ++j)
 #pragma unroll
           for (int f = 0; f < 2; ++f) {
-            const float4 xv = raw.x[j][c][2 * h + f];
+            const v4f xv = raw.x[j][c][2 * h + f];
             const float e[4] = {xv.x, xv.y, xv.z, xv.w};
             float r1[4], r2[4];
 #pragma unroll
@@ -1032,17 +1243,25 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
       }
   };
 
-  // two register sets in turn: the loads of step s + KW are in flight while
-  // step s is converted and multiplied
+  // Wave `wave` takes steps wave, wave + KW, ... (n_mine of them). Two
+  // register sets in turn: step n + 1's loads are in flight while step n is
+  // converted and multiplied. The loads are unconditional (indices past the
+  // wave's last step re-load it), so the loop body is branch-free and the
+  // compiler's waits stay exact.
   const int steps = K / 64;
-  KsplitRaw<MI, MJ> ra, rb;
-  if (wave < steps) load(ra, wave);
-  for (int s = wave; s < steps; s += 2 * KW) {
-    if (s + KW < steps) load(rb, s + KW);
-    compute(ra);
-    if (s + KW >= steps) break;
-    if (s + 2 * KW < steps) load(ra, s + 2 * KW);
-    compute(rb);
+  const int n_mine = wave < steps ? (steps - wave + KW - 1) / KW : 0;  // wave-uniform
+  auto step_of = [&](int n) { return wave + KW * min(n, n_mine - 1); };
+  if (n_mine > 0) {
+    KsplitRaw<MI, MJ> ra, rb;
+    load(ra, step_of(0));
+    load(rb, step_of(1));
+    for (int n = 0; n + 2 <= n_mine; n += 2) {
+      compute(ra);
+      load(ra, step_of(n + 2));
+      compute(rb);
+      load(rb, step_of(n + 3));
+    }
+    if (n_mine & 1) compute(ra);
   }
   if constexpr (NT == 3) {
 #pragma unroll
@@ -1077,12 +1296,29 @@ bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, h
   return true;
 }
 
+template <int BN, int BT, int BK, int NS, int EPI>
+bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
+  constexpr size_t lds = 2 * gemm_lds_bytes<BN, BT, BK>();
+  if (K % (NS * BK) != 0) return false;
+  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_db_kernel<BN, BT, BK, NS, EPI>>(lds)) return false;
+  TileMap map;
+  map.cols = cols;
+  map.rows = (unsigned)((T + BT - 1) / BT);
+  map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
+  w8a32_gemm_bf16x3_db_kernel<BN, BT, BK, NS, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K);
+  return true;
+}
+
 // Kernel and tile: the LDS-staged 256 x 64 tile where it still gives at least
 // 512 workgroups (a 256-stream lm_head: each workgroup's activation rows then
 // serve twice the weight rows, 634.7 -> 579.9 us at [256,2048]x[2048,151936];
 // 256 x 128 measured slower, one workgroup per CU), the 128 x 64 tile where it
 // gives at least 256 (its staged operands are shared by 4 waves: 128 B loaded
-// per MFMA); otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
+// per MFMA) -- double-buffered when that is one workgroup per CU (T = 512
+// q/k/v: 25.7 -> 24.9 us at K = 1024, 40.4 -> 37.4 us at K = 2048); with more
+// workgroups the single-buffered kernel is faster (two or three share a CU and
+// overlap each other's staging and MFMAs; the double-buffered one's LDS allows
+// only one: 0.6B gate/up at T = 512 33.5 against 42-45 us); otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
 // 32 x 32 that fills the chip (measured at T = 512: o [1024, 2048] 20.0 ->
 // 16.7 us, down [1024, 3072] 27.4 -> 20.9 us against the LDS-staged 64 x 32).
 // Returns false when the chosen kernel cannot run the shape (K not a multiple
@@ -1102,7 +1338,10 @@ bool launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
   unsigned c = cols(256);
   if (c * rows64 >= 512) return try_gemm<256, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
   c = cols(128);
-  if (c * rows64 >= 256) return try_gemm<128, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
+  if (c * rows64 >= 256) {
+    if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st)) return true;
+    return try_gemm<128, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
+  }
   c = cols(64);
   if (c * rows64 >= 256) return try_gemm_ksplit<64, 64, 4, EPI>(set, c, x, T, K, st);
   if (c * rows32 >= 256) return try_gemm_ksplit<64, 32, 4, EPI>(set, c, x, T, K, st);

@@ -741,7 +741,13 @@ def test_add_rms_norm_gate_up_swiglu_equals_unfused(dev, H, I, with_delta):
                                                 (9, 1088, 200),
                                                 # split-K 64x64, 64x32 tiles (32x32 above), ragged
                                                 (512, 1024, 2048), (512, 1088, 2048), (520, 1024, 2000),
-                                                (512, 2048, 1024), (500, 1024, 1000)])
+                                                (512, 2048, 1024), (500, 1024, 1000),
+                                                # split-K with 1-2 k steps (waves without a step)
+                                                (16, 64, 64), (40, 128, 100),
+                                                # 128 x 64 tiles, one workgroup per CU: the
+                                                # double-buffered kernel (ragged), and a K it
+                                                # refuses (17 chunks) that falls back
+                                                (512, 1024, 4096), (500, 2048, 4000), (512, 1088, 4096)])
 def test_linear_nobias_int8_w8a32(dev, seq, in_dim, out_dim):
     from qwenasr_amd import kernels as K
 
@@ -781,6 +787,30 @@ def test_linear_nobias_int8_wide_tile(dev):
     n = 300
     ref = oracle.linear_nobias_int8(x, wq.reshape(out_dim, in_dim)[out_dim - n:], ws[out_dim - n:], seq, in_dim, n)
     assert_close(got[:, out_dim - n:].ravel(), ref, RTOL, ATOL, "w8a32 256x64 tile, last rows")
+
+
+def test_linear_nobias_int8_double_buffered_tile(dev):
+    """The double-buffered 128 x 64 kernel (grids of at most one workgroup per
+    CU) adds each output's terms in the single-buffered kernel's order: a
+    product whose first 4096 rows are computed alone (256 workgroups, double
+    buffered) equals, bit for bit, the same rows of the 6144-row product
+    (384 workgroups, single buffered), ragged in tokens."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(23)
+    seq, in_dim, out_dim, part = 500, 1024, 6144, 4096
+    wq, ws = make_qweight(r, out_dim, in_dim)
+    x = normal(r, seq * in_dim)
+    x_t, w_t, s_t = dev_t(x, dev), dev_t(wq, dev), dev_t(ws, dev)
+    y = torch.empty(seq * out_dim, dtype=torch.float32, device=dev)
+    K.linear_nobias_int8(y, x_t, w_t, s_t, seq, in_dim, out_dim)
+    yp = torch.empty(seq * part, dtype=torch.float32, device=dev)
+    K.linear_nobias_int8(yp, x_t, w_t[:part * in_dim], s_t[:part], seq, in_dim, part)
+    got = host(y).reshape(seq, out_dim)
+    np.testing.assert_array_equal(got[:, :part], host(yp).reshape(seq, part))
+    n = 200
+    ref = oracle.linear_nobias_int8(x, wq.reshape(out_dim, in_dim)[:n], ws[:n], seq, in_dim, n)
+    assert_close(host(yp).reshape(seq, part)[:, :n].ravel(), ref, RTOL, ATOL, "w8a32 double-buffered")
 
 
 def test_linear_int8_integer_inputs_exact(dev):
