@@ -597,10 +597,12 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
     for (int jj = 0; jj < 2; ++jj) mine[i][jj] += ex[(((rg * 2 + kq) * 3 + i) * 2 + jj) * 64 + lane];
 
   // Epilogue: lane holds W rows n_wave + 16i + 4g + {0..3} (two gate/up pairs)
-  // for token m0 + 16*(2kq + jj) + r.
+  // for token m0 + 16*(2kq + jj) + r. The output tile is staged past the
+  // exchange area (no barrier needed between them) with a row pitch of 100
+  // floats: at 96 the 16 tokens of one write instruction would share a bank.
   if constexpr (VEC_OUT) {
-    __syncthreads();  // exchange area free
-    float* ot = reinterpret_cast<float*>(lds);  // [64 tokens][96 outputs]
+    constexpr int OP = 100;  // staged row pitch (floats)
+    float* ot = reinterpret_cast<float*>(lds + 65536);  // [64 tokens][OP]
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int t = 16 * (2 * kq + jj) + r;
@@ -609,7 +611,7 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
         float2 o;
         o.x = swiglu_w8a8(mine[i][jj][0], mine[i][jj][1], xsv[jj], sc[i].x, sc[i].y);
         o.y = swiglu_w8a8(mine[i][jj][2], mine[i][jj][3], xsv[jj], sc[i].z, sc[i].w);
-        *reinterpret_cast<float2*>(ot + t * 96 + rg * 24 + 8 * i + 2 * g) = o;
+        *reinterpret_cast<float2*>(ot + t * OP + rg * 24 + 8 * i + 2 * g) = o;
       }
     }
     __syncthreads();
@@ -619,7 +621,7 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
       const int row = q / 24, c4 = q - row * 24;
       const int m = m0 + row;
       if (m < batch)
-        __builtin_nontemporal_store(*reinterpret_cast<const v4f*>(ot + row * 96 + 4 * c4),
+        __builtin_nontemporal_store(*reinterpret_cast<const v4f*>(ot + row * OP + 4 * c4),
                                     reinterpret_cast<v4f*>(out + (size_t)m * inter + tile_n * 96 + 4 * c4));
     }
   } else {
