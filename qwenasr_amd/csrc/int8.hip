@@ -1077,8 +1077,11 @@ QASR_DEV unsigned bf16_pair_i8(int v, int byte) {  // bytes byte, byte + 1 of v 
 template <int MI, int MJ>
 struct KsplitRaw {
   v4i w[MI][2];          // per 32-wide chunk: 16 int8 of one weight row
-  v4f x[MJ][2][4];       // per 32-wide chunk: 16 floats of one token
+  v4f x[MJ][8];          // load q: floats 4(lane % 16).. of token 4q + lane / 16 (coalesced)
 };
+// Row pitch (floats) of a wave's staged activation block [32 tokens][64 k]:
+// the 16-byte pad spreads the fragment reads of 32 rows over the banks.
+constexpr int kKsPitch = 68;
 
 // Lane l, register 4q + v of block (i, j) holds row n0 + 32i + 8q + 4(l/32) + v
 // of token t0 + 32j + l%32; the KW waves' partial tiles are added in LDS in
@@ -1133,7 +1136,9 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
   constexpr int MI = BN / 32, MJ = BT / 32;
   constexpr int NT = MI * MJ == 1 ? 3 : 1;  // accumulators per block: one per term for a single block
   static_assert(BN % 32 == 0 && BT % 32 == 0, "32 x 32 blocks");
-  extern __shared__ __align__(16) float gk_red[];  // [KW][MI * MJ * 16][64] partial tiles
+  // [KW][MI * MJ * 16][64] partial tiles after the loop; during it each
+  // wave's staged activations, [KW][MJ][32][kKsPitch]
+  extern __shared__ __align__(16) float gk_red[];
   unsigned bx, by;
   tile_of(map, blockIdx.x, bx, by);
   float* y = set.y[0];
@@ -1158,11 +1163,15 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
   const int n0 = (int)(bx - bx0) * BN, t0 = (int)by * BT;
   // rows and tokens past the end re-read the last one (valid memory; not stored)
   const int8_t* wp[MI];
-  const float* xp[MJ];
+  const float* xp[MJ][8];
 #pragma unroll
   for (int i = 0; i < MI; ++i) wp[i] = w + (size_t)min(n0 + 32 * i + r, N - 1) * K + 16 * g;
 #pragma unroll
-  for (int j = 0; j < MJ; ++j) xp[j] = x + (size_t)min(t0 + 32 * j + r, T - 1) * K + 16 * g;
+  for (int j = 0; j < MJ; ++j)
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      xp[j][q] = x + (size_t)min(t0 + 32 * j + 4 * q + (lane >> 4), T - 1) * K + 4 * (lane & 15);
+  float* xs = gk_red + (size_t)wave * MJ * 32 * kKsPitch;  // this wave's staged activations
 
   v16f acc[NT][MI][MJ];
 #pragma unroll
@@ -1178,26 +1187,43 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
       const int k = step * 64 + 32 * c;
 #pragma unroll
       for (int i = 0; i < MI; ++i) raw.w[i][c] = *reinterpret_cast<const v4i*>(wp[i] + k);
-#pragma unroll
-      for (int j = 0; j < MJ; ++j)
-#pragma unroll
-        for (int f = 0; f < 4; ++f) raw.x[j][c][f] = *reinterpret_cast<const v4f*>(xp[j] + k + 4 * f);
     }
+    // the activations as 1 KiB contiguous pieces (four tokens' 64 k each):
+    // lanes one 128-byte line apart cost the load path 8x the line lookups
+#pragma unroll
+    for (int j = 0; j < MJ; ++j)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) raw.x[j][q] = *reinterpret_cast<const v4f*>(xp[j][q] + step * 64);
   };
   // Every loaded register passes through an empty asm first, so no part of
   // the conversion is hoisted next to its load (which would wait for the load
   // there instead of one step later).
+  // The activations go through the wave's LDS block into the MFMA layout:
+  // lane (r, g) takes floats 32c + 16g .. +15 of token r (only this wave
+  // touches the block, and its LDS accesses complete in order).
   auto compute = [&](const KsplitRaw<MI, MJ>& in) {
     KsplitRaw<MI, MJ> raw = in;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int i = 0; i < MI; ++i) asm volatile("" : "+v"(raw.w[i][c]));
 #pragma unroll
-      for (int j = 0; j < MJ; ++j)
+    for (int j = 0; j < MJ; ++j)
 #pragma unroll
-        for (int f = 0; f < 4; ++f) asm volatile("" : "+v"(raw.x[j][c][f]));
-    }
+      for (int q = 0; q < 8; ++q) {
+        asm volatile("" : "+v"(raw.x[j][q]));
+        *reinterpret_cast<v4f*>(xs + (j * 32 + 4 * q + (lane >> 4)) * kKsPitch + 4 * (lane & 15)) = raw.x[j][q];
+      }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_wave_barrier();
+    v4f xf[MJ][2][4];
+#pragma unroll
+    for (int j = 0; j < MJ; ++j)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+          xf[j][c][f] = *reinterpret_cast<const v4f*>(xs + (j * 32 + r) * kKsPitch + 32 * c + 16 * g + 4 * f);
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -1215,7 +1241,7 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
         for (int j = 0; j < MJ; ++j)
 #pragma unroll
           for (int f = 0; f < 2; ++f) {
-            const v4f xv = raw.x[j][c][2 * h + f];
+            const v4f xv = xf[j][c][2 * h + f];
             const float e[4] = {xv.x, xv.y, xv.z, xv.w};
             float r1[4], r2[4];
 #pragma unroll
@@ -1267,12 +1293,15 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[0][0][0][e] = (acc[0][0][0][e] + acc[1][0][0][e]) + acc[2][0][0][e];
   }
+  __syncthreads();  // every wave's staged activations read: the partial tiles reuse the LDS
   ksplit_reduce_store<MI, MJ, KW, EPI>(acc[0], gk_red, wave, lane, y, scales, bias, N, T, n0, t0);
 }
 
 template <int BN, int BT, int KW, int EPI>
 bool try_gemm_ksplit(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
-  constexpr size_t lds = (size_t)KW * BN * BT * sizeof(float);
+  constexpr size_t red = (size_t)KW * BN * BT * sizeof(float);                 // partial tiles
+  constexpr size_t stage = (size_t)KW * (BT / 32) * 32 * kKsPitch * sizeof(float);  // staged activations
+  constexpr size_t lds = red > stage ? red : stage;
   if (K % 64 != 0) return false;
   if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_ksplit_kernel<BN, BT, KW, EPI>>(lds)) return false;
   TileMap map;
