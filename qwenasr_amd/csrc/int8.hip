@@ -732,10 +732,19 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
     for (int j = 0; j < MJ; ++j) acc[i][j] = v16f{};
 
   // rows and tokens past the end re-read the last one (valid memory; not stored)
-  const int w_row = tid / TPW, w_part = tid % TPW;
-  const int8_t* wsrc = w + (size_t)min(n0 + w_row, N - 1) * K + WB * w_part;
-  const int x_tok = tid / TPX, x_part = tid % TPX;
-  const float* xsrc = x + (size_t)min(t0 + x_tok, T - 1) * K + XF * x_part;
+  // Staging items: weight item c is 16 bytes of row 64c + tid / 4 at byte
+  // 16 (tid % 4) of the chunk; activation item c is 4 floats of token
+  // 16c + tid / 16 at float 4 (tid % 16). A wave's load then covers 16 rows x
+  // 64 bytes or 4 tokens x 256 bytes: 16 or 8 cache lines per instruction, not
+  // one line per lane pair.
+  static_assert(BK == 64 && WB / 16 == BN / 64 && XF / 4 == BT / 16, "item counts of the staging map");
+  const int w_part = tid & 3, x_part = tid & 15;
+  const int8_t* wsrc[WB / 16];
+  const float* xsrc[XF / 4];
+#pragma unroll
+  for (int c = 0; c < WB / 16; ++c) wsrc[c] = w + (size_t)min(n0 + 64 * c + (tid >> 2), N - 1) * K + 16 * w_part;
+#pragma unroll
+  for (int c = 0; c < XF / 4; ++c) xsrc[c] = x + (size_t)min(t0 + 16 * c + (tid >> 4), T - 1) * K + 4 * x_part;
 
   v4i wv[NPF][WB / 16];
   v4f xv[NPF][XF / 4];
@@ -743,9 +752,9 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
   for (int q = 0; q < NPF; ++q)
     if (q * BK < K) {
 #pragma unroll
-      for (int c = 0; c < WB / 16; ++c) wv[q][c] = *reinterpret_cast<const v4i*>(wsrc + q * BK + 16 * c);
+      for (int c = 0; c < WB / 16; ++c) wv[q][c] = *reinterpret_cast<const v4i*>(wsrc[c] + q * BK);
 #pragma unroll
-      for (int c = 0; c < XF / 4; ++c) xv[q][c] = *reinterpret_cast<const v4f*>(xsrc + q * BK + 4 * c);
+      for (int c = 0; c < XF / 4; ++c) xv[q][c] = *reinterpret_cast<const v4f*>(xsrc[c] + q * BK);
     }
   for (int kb = 0; kb < K; kb += NPF * BK) {
 #pragma unroll
@@ -761,7 +770,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
           const int v = wc[e];
           const uint2 h = make_uint2(bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff)),
                                      bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff)));
-          *reinterpret_cast<uint2*>(&wl[w_row][WB * w_part + 16 * c + 4 * e]) = h;
+          *reinterpret_cast<uint2*>(&wl[64 * c + (tid >> 2)][16 * w_part + 4 * e]) = h;
         }
       }
 #pragma unroll
@@ -775,18 +784,18 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
           r1[e] = ev[e] - bf16_trunc(ev[e]);
           r2[e] = r1[e] - bf16_trunc(r1[e]);  // at most 8 significant bits
         }
-        const int col = XF * x_part + 4 * c;
-        *reinterpret_cast<uint2*>(&xl[0][x_tok][col]) = make_uint2(bf16_pair(ev[0], ev[1]), bf16_pair(ev[2], ev[3]));
-        *reinterpret_cast<uint2*>(&xl[1][x_tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
-        *reinterpret_cast<uint2*>(&xl[2][x_tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
+        const int tok = 16 * c + (tid >> 4), col = 4 * x_part;
+        *reinterpret_cast<uint2*>(&xl[0][tok][col]) = make_uint2(bf16_pair(ev[0], ev[1]), bf16_pair(ev[2], ev[3]));
+        *reinterpret_cast<uint2*>(&xl[1][tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
+        *reinterpret_cast<uint2*>(&xl[2][tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
       }
       lds_barrier();  // the staged chunk is visible to every wave
       if (k0 + NPF * BK < K) {
 #pragma unroll
         for (int c = 0; c < WB / 16; ++c)
-          wv[q][c] = *reinterpret_cast<const v4i*>(wsrc + k0 + NPF * BK + 16 * c);
+          wv[q][c] = *reinterpret_cast<const v4i*>(wsrc[c] + k0 + NPF * BK);
 #pragma unroll
-        for (int c = 0; c < XF / 4; ++c) xv[q][c] = *reinterpret_cast<const v4f*>(xsrc + k0 + NPF * BK + 4 * c);
+        for (int c = 0; c < XF / 4; ++c) xv[q][c] = *reinterpret_cast<const v4f*>(xsrc[c] + k0 + NPF * BK);
       }
 #pragma unroll
       for (int kk = 0; kk < BK; kk += 16) {
@@ -900,16 +909,21 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
     for (int j = 0; j < MJ; ++j) acc[i][j] = v16f{};
 
   // rows and tokens past the end re-read the last one (valid memory; not stored)
-  const int w_row = tid / TPW, w_part = tid % TPW;
-  const int8_t* wsrc = w + (size_t)min(n0 + w_row, N - 1) * K + WB * w_part;
-  const int x_tok = tid / TPX, x_part = tid % TPX;
-  const float* xsrc = x + (size_t)min(t0 + x_tok, T - 1) * K + XF * x_part;
+  // staging items as in the single-buffered kernel (16 or 8 lines per load instruction)
+  static_assert(BK == 64 && NW == BN / 64 && NX == BT / 16, "item counts of the staging map");
+  const int w_part = tid & 3, x_part = tid & 15;
+  const int8_t* wsrc[NW];
+  const float* xsrc[NX];
+#pragma unroll
+  for (int c = 0; c < NW; ++c) wsrc[c] = w + (size_t)min(n0 + 64 * c + (tid >> 2), N - 1) * K + 16 * w_part;
+#pragma unroll
+  for (int c = 0; c < NX; ++c) xsrc[c] = x + (size_t)min(t0 + 16 * c + (tid >> 4), T - 1) * K + 4 * x_part;
 
   auto load = [&](v4i (&wv)[NW], v4f (&xv)[NX], int k0) {
 #pragma unroll
-    for (int c = 0; c < NW; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc + k0 + 16 * c);
+    for (int c = 0; c < NW; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc[c] + k0);
 #pragma unroll
-    for (int c = 0; c < NX; ++c) xv[c] = *reinterpret_cast<const v4f*>(xsrc + k0 + 4 * c);
+    for (int c = 0; c < NX; ++c) xv[c] = *reinterpret_cast<const v4f*>(xsrc[c] + k0);
   };
   // The staging items that go after k step `part` (item c of N after step c * KSTEPS / N).
   // Each item passes through an empty asm first: the conversion cannot then be
@@ -927,7 +941,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
         const int v = wc[e];
         const uint2 h = make_uint2(bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff)),
                                    bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff)));
-        *reinterpret_cast<uint2*>(&wl[w_row][WB * w_part + 16 * c + 4 * e]) = h;
+        *reinterpret_cast<uint2*>(&wl[64 * c + (tid >> 2)][16 * w_part + 4 * e]) = h;
       }
     }
 #pragma unroll
@@ -942,10 +956,10 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
         r1[e] = ev[e] - bf16_trunc(ev[e]);
         r2[e] = r1[e] - bf16_trunc(r1[e]);  // at most 8 significant bits
       }
-      const int col = XF * x_part + 4 * c;
-      *reinterpret_cast<uint2*>(&xl[0][x_tok][col]) = make_uint2(bf16_pair(ev[0], ev[1]), bf16_pair(ev[2], ev[3]));
-      *reinterpret_cast<uint2*>(&xl[1][x_tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
-      *reinterpret_cast<uint2*>(&xl[2][x_tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
+      const int tok = 16 * c + (tid >> 4), col = 4 * x_part;
+      *reinterpret_cast<uint2*>(&xl[0][tok][col]) = make_uint2(bf16_pair(ev[0], ev[1]), bf16_pair(ev[2], ev[3]));
+      *reinterpret_cast<uint2*>(&xl[1][tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
+      *reinterpret_cast<uint2*>(&xl[2][tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
     }
   };
   // k step s of the chunk staged in `st`: every product term in the order of
