@@ -147,12 +147,15 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
   static_assert(!(NORM && PART), "no normalised input on the argmax path");
   const int lane = threadIdx.x & (kWave - 1);
   const int o0 = (int)(block * (256 / kWave) + threadIdx.x / kWave) * R;
-  if constexpr (!PART && !NORM) {
-    if (o0 >= out_dim) return;
-  }
+
   // the row statistics' inputs are loaded before the weights: the wait for
   // them then leaves the weight loads in flight
   float4 nx[NORM ? KCH : 1], nd[NORM ? KCH : 1], ng[NORM ? KCH : 1];
+  float4 xg[NORM ? 1 : KCH];
+  if constexpr (!NORM) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) xg[i] = ld4(x, threadIdx.x + 256 * i);
+  }
   if constexpr (NORM) {
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
@@ -207,10 +210,22 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
       for (int t = 0; t < 4; ++t) xv[c][t] = xs[(c * kWave + lane) * 4 + t];
     if (o0 >= out_dim) return;  // after the workgroup's barrier
   } else {
+    // x through LDS: loaded as consecutive 16-byte pieces per lane (a lane's
+    // own 64-byte piece, read straight from global memory, put every lane of
+    // a load instruction on a different line: 4x the line lookups of the
+    // weight loads for a quarter of the bytes), once per workgroup. The
+    // barrier waits for LDS only, so the weight loads stay in flight.
+    __shared__ float4 xs[256 * KCH];
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) xs[threadIdx.x + 256 * i] = xg[i];
+    lds_barrier();
 #pragma unroll
     for (int c = 0; c < KCH; ++c)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) xv[c][t] = ld4(x + (c * kWave + lane) * 16 + 4 * t, 0);
+      for (int t = 0; t < 4; ++t) xv[c][t] = xs[(c * kWave + lane) * 4 + t];
+    if constexpr (!PART) {
+      if (o0 >= out_dim) return;  // after the workgroup's barrier
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   float acc[R];
