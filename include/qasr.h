@@ -378,7 +378,9 @@ int qasr_gate_up_swiglu_w8a8_packed(float* out, const int8_t* w_packed,
  * the activation quantized per row, as the batched gate/up projection does;
  * the integer dots are exact, so y equals the oracle's bit for bit. in_dim
  * 1024, 2048, 3072, 4096 or 6144, out_dim % 128 == 0, 16-byte aligned buffers
- * (QASR_ERR_UNSUPPORTED otherwise). */
+ * (QASR_ERR_UNSUPPORTED otherwise). Outputs wide enough for 4+ tiles per CU
+ * (a batch's lm_head) run persistent workgroups that each walk a range of
+ * column tiles; the results are the same. */
 int qasr_linear_w8a8_packed(float* y, const int8_t* w_packed, const float* scales,
                             const int8_t* xq, const float* x_scales, size_t batch,
                             size_t in_dim, size_t out_dim, void* stream);

@@ -77,13 +77,17 @@ def decode_int8_step(w: dict, k_cache: np.ndarray, v_cache: np.ndarray, pos: int
 
 def decode_w8a8_step(w: dict, k_cache: np.ndarray, v_cache: np.ndarray, pos: int,
                      embed: np.ndarray, n_heads: int, n_kv_heads: int, head_dim: int,
-                     eps: float = 1e-6, theta: float = 1e6, threads: int = 1, quant=None):
+                     eps: float = 1e-6, theta: float = 1e6, threads: int = 1, quant=None,
+                     lm_head_w8a8: bool = False):
     """``decode_int8_step`` (same arguments and results) with W8A8 projections:
     each projection input is quantized per row and multiplied as int8 x int8
-    with int32 sums; the gate/up is the fused SwiGLU W8A8 product.
+    with int32 sums; the gate/up is the fused SwiGLU W8A8 product. With
+    ``lm_head_w8a8`` the lm_head is one too (the final normed row quantized,
+    logits = ((f32)dot * x_scale) * row_scale); otherwise it stays W8A32.
     ``quant(x, n) -> (q, scale)`` replaces the per-row quantizer at the four
     points, in order per layer: input norm, attention rows, post-attention
-    norm, SwiGLU rows (tests use it to see and steer the rounding)."""
+    norm, SwiGLU rows, then (``lm_head_w8a8``) the final norm (tests use it to
+    see and steer the rounding)."""
     if quant is None:
         quant = lambda v, n: quantize_f32_to_int8(v, 1, n)  # noqa: E731
     H = embed.size
@@ -116,7 +120,11 @@ def decode_w8a8_step(w: dict, k_cache: np.ndarray, v_cache: np.ndarray, pos: int
         add_inplace(x, linear_w8a8(*lw["down"], fq, fs, 1, inter, H)[0])
     xn = rms_norm(x, w["norm"], 1, H, eps)
     vocab = w["lm_head"][1].size
-    logits = linear_nobias_int8(xn, *w["lm_head"], 1, H, vocab, threads)
+    if lm_head_w8a8:
+        xq, xs = quant(xn, H)
+        logits = linear_w8a8(*w["lm_head"], xq, xs, 1, H, vocab)[0]
+    else:
+        logits = linear_nobias_int8(xn, *w["lm_head"], 1, H, vocab, threads)
     return int(argmax_rows(logits, 1, vocab)[0]), xn, logits
 
 

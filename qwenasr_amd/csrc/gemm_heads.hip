@@ -279,6 +279,207 @@ __global__ __launch_bounds__(64 * kHdWaves) void gemm_w8a8_heads_kernel(HeadsArg
   }
 }
 
+// Persistent form of the plain projection (MODE 0) for outputs many times
+// wider than the GPU (a batch's lm_head: [256,2048]x[2048,151936] is 9496
+// one-tile workgroups of 128 rows x 32 streams, 363 us). Each workgroup keeps
+// one stream tile's rows in LDS and walks a contiguous range of column tiles,
+// the next tile's W window loading under the current tile's last k-steps and
+// epilogue, and takes 64 streams where their rows fit the LDS (K <= 2048):
+// every W byte pulled into a CU then serves twice the outputs. Workgroup b
+// runs on XCD b % 8; the m_tiles workgroups of one range sit on one XCD, so
+// each W tile is fetched into that L2 once. The exchange area lies past the
+// staged rows, which stay put; each lane stores its four dequantized rows of
+// a stream directly. Per output the arithmetic is the one-tile kernel's, so
+// the results are the same bit for bit.
+template <int KS, int TOK>
+__global__ __launch_bounds__(64 * kHdWaves) void gemm_w8a8_rows_persistent_kernel(HeadsArgs a, int groups) {
+  constexpr int K = KS * 64;
+  constexpr int KW = KS / 2;
+  constexpr int MT = TOK / 16;        // 16-stream MFMA tiles
+  constexpr int HT = MT > 1 ? MT / 2 : 1;  // stream tiles a wave finishes
+  constexpr int SLOTS = K / 16;
+  constexpr int XU = TOK * SLOTS / (64 * kHdWaves);
+  // k-steps of W in flight per wave; a divisor of KW, so the next tile's first
+  // steps land in the register slots its loop starts from
+  constexpr int PF = 4;
+  constexpr size_t ROW_TILE = (size_t)KS * 1024;
+  constexpr int X_BYTES = TOK * K;
+  static_assert(KS % 2 == 0 && (MT == 1 || MT == 2 || MT == 4), "K halves; 1, 2 or 4 stream tiles");
+  static_assert(XU * 64 * kHdWaves == TOK * SLOTS, "the staging covers the tile");
+  static_assert(KW % PF == 0, "the W window wraps into the next tile's slots");
+  extern __shared__ __align__(16) int8_t lds[];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = wave & 3, kq = wave >> 2;
+  const int r = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x, xcd = b % kNumXcdH, j32 = b / kNumXcdH;
+  const int tile_m = j32 % a.m_tiles, group = j32 / a.m_tiles;
+  if (group >= groups) return;  // uniform, before any barrier
+  const int ranges = kNumXcdH * groups, rho = xcd + kNumXcdH * group;
+  const int nt_begin = (int)((long long)rho * a.n_tiles / ranges);
+  const int nt_end = (int)((long long)(rho + 1) * a.n_tiles / ranges);
+  if (nt_begin >= nt_end) return;
+  const int m0 = tile_m * TOK;
+
+  v4i_t xr[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int c = threadIdx.x + 64 * kHdWaves * u;
+    const int row = c / SLOTS, slot = c % SLOTS;
+    const int src = m0 + row < a.batch ? m0 + row : a.batch - 1;  // past the batch: valid row, dropped
+    xr[u] = *reinterpret_cast<const v4i_t*>(a.xq + (size_t)src * K + 16 * slot);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  auto wptr = [&](int tn) {
+    return a.w + ((size_t)((tn * kHdRows + 32 * rg) / 16) * KS + (size_t)kq * KW) * 1024 + 16 * lane;
+  };
+  const int8_t* wp = wptr(nt_begin);
+  v4i_t wbuf[PF][2];
+#pragma unroll
+  for (int d = 0; d < PF; ++d)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      wbuf[d][i] = *reinterpret_cast<const v4i_t*>(wp + i * ROW_TILE + d * 1024);
+  __builtin_amdgcn_sched_barrier(0);
+  // the stream scales of the tiles this wave finishes: stream tile
+  // (MT > 1 ? kq * HT + jj : 0), row r
+  float xsv[HT];
+  int mrow[HT];
+#pragma unroll
+  for (int jj = 0; jj < HT; ++jj) {
+    mrow[jj] = m0 + 16 * (MT > 1 ? kq * HT + jj : 0) + r;
+    xsv[jj] = a.xs[mrow[jj] < a.batch ? mrow[jj] : a.batch - 1];
+  }
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int c = threadIdx.x + 64 * kHdWaves * u;
+    const int row = c / SLOTS, slot = c % SLOTS;
+    *reinterpret_cast<v4i_t*>(lds + row * K + 16 * (slot ^ (row & 15))) = xr[u];
+  }
+  lds_barrier();
+
+  v4i_t* ex = reinterpret_cast<v4i_t*>(lds + X_BYTES);  // [rg][receiver kq][i][jj][lane]
+  auto xfrag = [&](int s, int jt) -> v4i_t {
+    return *reinterpret_cast<const v4i_t*>(lds + (16 * jt + r) * K + 16 * ((4 * s + g) ^ r));
+  };
+  const int k0 = kq * KW;
+  const bool vec = (a.N & 3) == 0;  // (y is 16-byte aligned: checked by the entry point)
+  for (int tn = nt_begin; tn < nt_end; ++tn) {
+    const int n0 = tn * kHdRows;
+    const int8_t* wn = wptr(tn + 1 < nt_end ? tn + 1 : tn);  // the next tile's window (the last re-loads itself)
+    float4 sc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) sc[i] = *reinterpret_cast<const float4*>(a.scales + n0 + 32 * rg + 16 * i + 4 * g);
+    v4i_t acc[2][MT];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int jt = 0; jt < MT; ++jt) acc[i][jt] = v4i_t{0, 0, 0, 0};
+    v4i_t bcur[MT];
+#pragma unroll
+    for (int jt = 0; jt < MT; ++jt) bcur[jt] = xfrag(k0, jt);
+#pragma unroll
+    for (int s0 = 0; s0 < KW; s0 += PF) {
+#pragma unroll
+      for (int d = 0; d < PF; ++d) {
+        const int s = s0 + d;
+        v4i_t av[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          av[i] = wbuf[d][i];
+          const int8_t* src = s + PF < KW ? wp + i * ROW_TILE + (s + PF) * 1024
+                                          : wn + i * ROW_TILE + (s + PF - KW) * 1024;
+          wbuf[d][i] = *reinterpret_cast<const v4i_t*>(src);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        v4i_t bn[MT];
+        if (s + 1 < KW) {
+#pragma unroll
+          for (int jt = 0; jt < MT; ++jt) bn[jt] = xfrag(k0 + s + 1, jt);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int jt = 0; jt < MT; ++jt)
+            acc[i][jt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bcur[jt], acc[i][jt], 0, 0, 0);
+        if (s + 1 < KW) {
+#pragma unroll
+          for (int jt = 0; jt < MT; ++jt) bcur[jt] = bn[jt];
+        }
+      }
+    }
+    wp = wn;
+
+    // K halves: wave kq keeps stream tiles kq * HT .. and adds its partner's
+    // partial sums for them (with one stream tile, wave 0 of the pair adds
+    // wave 1's); constant register indices only. The barriers wait for LDS
+    // only, so the next tile's W window stays in flight.
+    v4i_t mine[2][HT];
+    if constexpr (MT > 1) {
+      v4i_t give[2][HT];
+      if (kq == 0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int jj = 0; jj < HT; ++jj) { give[i][jj] = acc[i][HT + jj]; mine[i][jj] = acc[i][jj]; }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int jj = 0; jj < HT; ++jj) { give[i][jj] = acc[i][jj]; mine[i][jj] = acc[i][HT + jj]; }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int jj = 0; jj < HT; ++jj) ex[(((rg * 2 + (1 - kq)) * 2 + i) * HT + jj) * 64 + lane] = give[i][jj];
+      lds_barrier();
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int jj = 0; jj < HT; ++jj) mine[i][jj] += ex[(((rg * 2 + kq) * 2 + i) * HT + jj) * 64 + lane];
+      lds_barrier();  // the exchange area is free for the next tile
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) mine[i][0] = acc[i][0];
+      if (kq == 1) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) ex[(rg * 2 + i) * 64 + lane] = mine[i][0];
+      }
+      lds_barrier();
+      if (kq == 0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) mine[i][0] += ex[(rg * 2 + i) * 64 + lane];
+      }
+      lds_barrier();
+    }
+    // lane: rows n0 + 32rg + 16i + 4g + {0..3} of stream mrow[jj]
+    if (MT > 1 || kq == 0) {
+#pragma unroll
+      for (int jj = 0; jj < HT; ++jj) {
+        if (mrow[jj] >= a.batch) continue;
+        float* yr = a.y + (size_t)mrow[jj] * a.N + n0 + 32 * rg + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          float4 v;
+          v.x = ((float)mine[i][jj][0] * xsv[jj]) * sc[i].x;
+          v.y = ((float)mine[i][jj][1] * xsv[jj]) * sc[i].y;
+          v.z = ((float)mine[i][jj][2] * xsv[jj]) * sc[i].z;
+          v.w = ((float)mine[i][jj][3] * xsv[jj]) * sc[i].w;
+          if (vec) {
+            *reinterpret_cast<float4*>(yr + 16 * i) = v;
+          } else {
+            yr[16 * i] = v.x;
+            yr[16 * i + 1] = v.y;
+            yr[16 * i + 2] = v.z;
+            yr[16 * i + 3] = v.w;
+          }
+        }
+      }
+    }
+  }
+}
+
 // The staged rows (32 x K bytes) need more than the default 64 KiB of LDS at
 // K = 2048; the limit is raised once per device.
 template <auto Fn>
@@ -309,6 +510,22 @@ int launch_heads_tile(const HeadsArgs& a, unsigned grid, hipStream_t st, const c
   return launch_status(what);
 }
 
+// The persistent projection: 256 workgroups (32 per XCD), the stream tile's
+// rows plus the exchange area and the dequantized tile in LDS.
+template <int KS, int TOK>
+constexpr size_t rows_persistent_lds() {  // staged rows + exchange area
+  return (size_t)TOK * KS * 64 + (size_t)4 * 2 * 2 * (TOK >= 32 ? TOK / 32 : 1) * 64 * 16;
+}
+
+template <int KS, int TOK>
+int launch_rows_persistent(const HeadsArgs& a, int groups, hipStream_t st, const char* what) {
+  constexpr size_t lds = rows_persistent_lds<KS, TOK>();
+  if (!heads_lds_ok<&gemm_w8a8_rows_persistent_kernel<KS, TOK>>(lds))
+    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": device LDS too small");
+  gemm_w8a8_rows_persistent_kernel<KS, TOK><<<kNumXcdH * 32, 64 * kHdWaves, lds, st>>>(a, groups);
+  return launch_status(what);
+}
+
 // 32-stream tiles (the staged rows shared by twice the outputs) when K <= 2048
 // and they still give at least 256 workgroups; otherwise 16-stream tiles
 // (32 x K would not fit the LDS, or the grid would leave CUs idle).
@@ -320,6 +537,31 @@ int launch_heads_k(HeadsArgs a, hipStream_t st, const char* what) {
   a.m_tiles = (int)(tok32 ? m32 : m16);
   const size_t grid = (size_t)a.n_tiles * (size_t)a.m_tiles;
   QASR_REQUIRE(grid <= 0x7fffffffu, std::string(what) + ": grid too large");
+  if constexpr (MODE == 0) {
+    // 4+ one-tile workgroups per CU: the persistent form, with the widest
+    // stream tile whose rows fit the LDS and whose count divides an XCD's 32
+    // workgroups
+    if (grid >= 1024) {
+      const size_t m64 = ((size_t)a.batch + 63) / 64;
+      HeadsArgs p = a;
+      if constexpr (rows_persistent_lds<KS, 64>() <= 163840) {
+        if (32 % m64 == 0) {
+          p.m_tiles = (int)m64;
+          return launch_rows_persistent<KS, 64>(p, (int)(32 / m64), st, what);
+        }
+      }
+      if constexpr (rows_persistent_lds<KS, 32>() <= 163840) {
+        if (32 % m32 == 0) {
+          p.m_tiles = (int)m32;
+          return launch_rows_persistent<KS, 32>(p, (int)(32 / m32), st, what);
+        }
+      }
+      if (32 % m16 == 0) {
+        p.m_tiles = (int)m16;
+        return launch_rows_persistent<KS, 16>(p, (int)(32 / m16), st, what);
+      }
+    }
+  }
   if constexpr (KS <= 32) {
     if (tok32) return launch_heads_tile<KS, MODE, 32>(a, (unsigned)grid, st, what);
   }

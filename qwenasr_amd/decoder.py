@@ -243,8 +243,12 @@ class DecoderInt8Batched:
     add + RMSNorm + quantization; gate/up with
     SwiGLU in the epilogue; the SwiGLU rows quantized, down. The int8 weights
     are the same; the activations are rounded to int8 at those four points,
-    so the results follow the reference's within that rounding, not 1e-5. The
-    lm_head stays W8A32.
+    so the results follow the reference's within that rounding, not 1e-5.
+    ``lm_head_w8a8`` (default: with ``w8a8``, when the vocabulary is a
+    multiple of 128 and hidden one of 1024..6144 in the W8A8 projection's
+    steps) makes the lm_head one too: the final add + RMSNorm quantizes the
+    rows in the same launch, the logits are ((f32)dot * x_scale) * row_scale,
+    each stream's argmax follows; otherwise the lm_head stays W8A32.
 
     ``attn_chunked`` (default: when batch * n_kv_heads < 1024) also cuts each
     stream's keys into chunks for the attention, to give a small batch enough
@@ -254,7 +258,7 @@ class DecoderInt8Batched:
     def __init__(self, weights: dict, hidden: int, intermediate: int, n_layers: int, batch: int,
                  cache_rows: int, n_heads: int = 16, n_kv_heads: int = 8, head_dim: int = 128,
                  eps: float = 1e-6, theta: float = 1e6, vocab: int | None = None, device="cuda",
-                 w8a8: bool = False, attn_chunked: bool | None = None):
+                 w8a8: bool = False, attn_chunked: bool | None = None, lm_head_w8a8: bool | None = None):
         self.w = weights
         self.H, self.I, self.L, self.B = hidden, intermediate, n_layers, batch
         self.nq, self.nk, self.hd = n_heads, n_kv_heads, head_dim
@@ -304,6 +308,15 @@ class DecoderInt8Batched:
                 self.packed.append({k: K.pack_w8a8_tiles(w) for k, w in
                                     (("qkv", qkv), ("wo", lw["wo"]), ("gate_up", lw["gate_up"]),
                                      ("down", lw["down"]))})
+        fits = self.vocab % 128 == 0 and self.vocab == self.lm.out_dim and hidden in (1024, 2048, 3072, 4096, 6144)
+        if lm_head_w8a8 is None:
+            lm_head_w8a8 = w8a8 and fits
+        if lm_head_w8a8 and not (w8a8 and fits):
+            raise ValueError("lm_head_w8a8 needs w8a8=True, a vocabulary that is a multiple of 128 "
+                             "and hidden in 1024..6144 (steps of 1024, or 6144)")
+        self.lm_head_w8a8 = lm_head_w8a8
+        if lm_head_w8a8:
+            self.lm_packed = K.pack_w8a8_tiles(self.lm)
 
     def _layer_w8a8(self, l: int, lw: dict) -> None:
         H, I, B, nq, nk, hd, eps = self.H, self.I, self.B, self.nq, self.nk, self.hd, self.eps
@@ -350,6 +363,11 @@ class DecoderInt8Batched:
             K.gate_up_swiglu_int8(self.ffn, self.x_norm, lw["gate_up"], B, H, I)
             dn = lw["down"]
             K.linear_nobias_int8(self.down, self.ffn, dn.data, dn.scales, B, I, H)
+        if self.lm_head_w8a8:
+            K.add_rms_norm_quant(self.x, self.down, self.w["norm"], self.x_norm, self.xq, self.xs, B, H, eps)
+            K.linear_w8a8_packed(self.logits, self.lm_packed, self.xq, self.xs, B, H, self.vocab)
+            K.argmax_rows(self.tokens, self.logits, B, self.vocab)
+            return
         K.add_rms_norm(self.x, self.down, self.w["norm"], self.x_norm, B, H, eps)
         K.lm_head_int8_argmax(self.tokens, self.logits, self.x_norm, self.lm, B, H, self.vocab)
 

@@ -60,6 +60,39 @@ def test_linear_w8a8_packed_bit_exact(dev, batch, out_dim, in_dim):
     np.testing.assert_array_equal(y.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("batch,out_dim,in_dim", [(8, 131072, 1024), (40, 65536, 1024), (4, 131072, 3072),
+                                                  (256, 32768, 2048)])
+def test_linear_w8a8_packed_persistent(dev, batch, out_dim, in_dim):
+    """Outputs wide enough for 4+ tiles per CU take the persistent projection
+    (each workgroup walks a range of column tiles): equal bit for bit to the
+    same product computed in 8192-row column blocks (one-tile workgroups, each
+    tile adds the same dots in the same order), and to the oracle on the first
+    and last 256 rows; ragged batches, one-, two- and eight-tile stream
+    splits, 16- and 32-stream tiles."""
+    from qwenasr_amd import kernels as K
+
+    r = np.random.default_rng([52, batch, out_dim, in_dim])
+    wq = r.integers(-127, 128, (out_dim, in_dim), dtype=np.int8)
+    ws = (r.random(out_dim) * 0.01 + 1e-3).astype(np.float32)
+    xq, xs = _quant_rows(r, batch, in_dim)
+    w = _packed(dev, wq, ws)
+    xq_t, xs_t = torch.from_numpy(xq.ravel().copy()).to(dev), torch.from_numpy(xs).to(dev)
+    y = torch.full((batch * out_dim,), float("nan"), device=dev)
+    print(f"[batched] linear_w8a8 persistent B={batch} N={out_dim} K={in_dim}", flush=True)
+    K.linear_w8a8_packed(y, w, xq_t, xs_t, batch, in_dim, out_dim)
+    got = y.view(batch, out_dim).cpu().numpy()
+    blk = 8192
+    for r0 in range(0, out_dim, blk):
+        wb = K.QuantWeight(w.data[r0 * in_dim:(r0 + blk) * in_dim], w.scales[r0:r0 + blk], blk, in_dim)
+        yb = torch.empty(batch * blk, device=dev)
+        K.linear_w8a8_packed(yb, wb, xq_t, xs_t, batch, in_dim, blk)
+        np.testing.assert_array_equal(got[:, r0:r0 + blk], yb.view(batch, blk).cpu().numpy(),
+                                      err_msg=f"rows {r0}..{r0 + blk}")
+    for r0 in (0, out_dim - 256):
+        ref, _ = oracle.linear_w8a8(wq[r0:r0 + 256], ws[r0:r0 + 256], xq, xs, batch, in_dim, 256)
+        np.testing.assert_array_equal(got[:, r0:r0 + 256], ref.reshape(batch, 256))
+
+
 def _qkv_case(dev, batch, in_dim, cache_rows, seed, bad_rows=()):
     """Inputs of one q/k/v call: packed weights, quantized rows, gains,
     positions (with the given rows set out of range), the RoPE table."""
@@ -276,8 +309,8 @@ def _steered_quant(gpu_q, gpu_s, stream, log):
     return quant
 
 
-@pytest.mark.parametrize("H,I,B", [(2048, 6144, 9), (1024, 3072, 3)])
-def test_batched_w8a8_decode_step_matches_the_oracle_per_stream(tmp_path, dev, monkeypatch, H, I, B):
+@pytest.mark.parametrize("H,I,B,vocab", [(2048, 6144, 9, 1000), (1024, 3072, 3, 1024)])
+def test_batched_w8a8_decode_step_matches_the_oracle_per_stream(tmp_path, dev, monkeypatch, H, I, B, vocab):
     """DecoderInt8Batched(w8a8=True) against the oracle's W8A8 decode step run
     stream by stream, over two steps. The integer dots are exact, but the
     device's RMSNorm and attention rows differ from the oracle's in the last
@@ -288,14 +321,16 @@ def test_batched_w8a8_decode_step_matches_the_oracle_per_stream(tmp_path, dev, m
     elements within 1e-3 of a boundary (at most 4 per stream and step), and
     then the final hidden state, logits, new K/V rows and token must match at
     rel/abs 1e-4 as in the W8A32 step. The final hidden state must also differ
-    from the W8A32 step's (the rounding is really done at the four points)."""
+    from the W8A32 step's (the rounding is really done at the four points).
+    With a vocabulary of 1024 the lm_head is W8A8 as well (a fifth rounding
+    point, the final norm), with 1000 it stays W8A32."""
     from oracle.decoder import decode_int8_step, decode_w8a8_step
     from qwenasr_amd import kernels as K
     from qwenasr_amd.decoder import DecoderInt8Batched
     from tests.test_decoder_step import _load
     from tests.test_oracle import small_decoder
 
-    L, vocab, rows, TOL = 2, 1000, 2100, 1e-4
+    L, rows, TOL = 2, 2100, 1e-4
     r = np.random.default_rng([57, H, B])
     w = small_decoder(r, H, I, L, NQ, NK, HD, vocab)
     dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev, w8a8=True)
@@ -316,7 +351,8 @@ def test_batched_w8a8_decode_step_matches_the_oracle_per_stream(tmp_path, dev, m
         rec.seen.clear()
         dec.decode(torch.from_numpy(x.ravel().copy()).to(dev))
         torch.cuda.synchronize()
-        assert len(rec.seen) == 4 * L
+        assert dec.lm_head_w8a8 == (vocab % 128 == 0)
+        assert len(rec.seen) == 4 * L + int(dec.lm_head_w8a8)
         gq, gs = [q for q, _ in rec.seen], [s for _, s in rec.seen]
         xn = dec.x_norm.view(B, H).cpu().numpy()
         lg = dec.logits.view(B, vocab).cpu().numpy()
@@ -325,7 +361,8 @@ def test_batched_w8a8_decode_step_matches_the_oracle_per_stream(tmp_path, dev, m
             p = int(pos[m]) + step
             log = []
             t_ref, xn_ref, lg_ref = decode_w8a8_step(w, kc[m], vc[m], p, x[m], NQ, NK, HD, threads=8,
-                                                     quant=_steered_quant(gq, gs, m, log))
+                                                     quant=_steered_quant(gq, gs, m, log),
+                                                     lm_head_w8a8=dec.lm_head_w8a8)
             adopted.append(sum(log))
             assert sum(log) <= 4, (m, step, log)
             msg = f"stream {m} step {step} adopted {log}"
@@ -356,11 +393,13 @@ def test_batched_decode_step_graph_replay_equals_eager(tmp_path, dev, w8a8, chun
     from tests.test_decoder_step import _load
     from tests.test_oracle import small_decoder
 
-    H, I, L, B, rows, vocab = 1024, 3072, 2, 12, 1300, 1000
+    H, I, L, B, rows = 1024, 3072, 2, 12, 1300
+    vocab = 1024 if w8a8 else 1000  # the W8A8 form then has the W8A8 lm_head too
     r = np.random.default_rng([58, int(w8a8)])
     w = small_decoder(r, H, I, L, NQ, NK, HD, vocab)
     dec = DecoderInt8Batched(_load(tmp_path, w, L, dev), H, I, L, B, rows, device=dev, w8a8=w8a8,
                              attn_chunked=chunked)
+    assert dec.lm_head_w8a8 == w8a8
     for l in range(L):
         dec.k[l].normal_()
         dec.v[l].normal_()
