@@ -288,6 +288,30 @@ int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,
                                       const size_t* out_dims, const float* x, size_t seq_len,
                                       size_t in_dim, void* stream);
 
+/* A prefill chunk's q/k/v projections with the steps after them in one launch
+ * (decoder.rs:783-810: the three linear_nobias_int8 calls, per-head RMSNorm
+ * of q and k, NeoX RoPE, and the k_at/v_at copies into the layer's cache).
+ * Token s of x [seq_len, in_dim] is at position p = start_pos + s:
+ *   q[s, :]            = rope(rms_norm_head(x[s] . wq^T * sq, q_norm_w), p)
+ *   k_cache[p, :]      = rope(rms_norm_head(x[s] . wk^T * sk, k_norm_w), p)
+ *   v_cache[p, :]      = x[s] . wv^T * sv
+ * with wq [n_heads*head_dim, in_dim], wk/wv [n_kv_heads*head_dim, in_dim] and
+ * the caches the layer's [cache_rows][n_kv_heads*head_dim] blocks. Rows
+ * start_pos..start_pos+seq_len must lie inside the cache and the RoPE table
+ * (QASR_ERR_INVALID_ARG otherwise, as qasr_head_rms_norm_rope_kv_f32).
+ * Bit-identical to qasr_linear_nobias_int8_multi_f32 (q, k, v) followed by
+ * qasr_head_rms_norm_rope_kv_f32 (positions NULL): the raw k and v rows are
+ * never written. head_dim 128, seq_len >= 8, in_dim % 64 == 0 and 16-byte
+ * aligned buffers (QASR_ERR_UNSUPPORTED otherwise). No reference counterpart
+ * as one call. */
+int qasr_qkv_heads_int8_f32(float* q, float* k_cache, float* v_cache, size_t cache_rows,
+                            const int8_t* wq, const float* sq, const int8_t* wk, const float* sk,
+                            const int8_t* wv, const float* sv, const float* x, size_t seq_len,
+                            size_t in_dim, size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                            const float* q_norm_w, const float* k_norm_w, const float* cos_tab,
+                            const float* sin_tab, size_t table_rows, size_t start_pos, float eps,
+                            void* stream);
+
 /* One decode token's layer-input residual add + RMSNorm and the projections
  * that read it, in one launch: h = x + delta (delta may be NULL: h = x),
  * xn = rms_norm(h) * norm_w, ys[m] = linear_nobias_int8(xn, ws[m], scales[m]).

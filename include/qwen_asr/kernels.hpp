@@ -493,6 +493,35 @@ inline void gate_up_swiglu_multiply_int8(F out, CF x, DevSlice<const int8_t> w_g
                 "gate_up_swiglu_multiply_int8");
 }
 
+// Prefill q/k/v with the head norms, RoPE and K/V cache rows in one launch (decoder.rs:783-810):
+// bit-identical to linear_nobias_int8_multi (q, k, v) + head_rms_norm_rope_kv without positions.
+// k_cache/v_cache are the layer's [cache_rows][n_kv_heads*head_dim] blocks.
+inline void qkv_heads_int8(F q, F k_cache, F v_cache, size_t cache_rows, DevSlice<const int8_t> wq, CF sq,
+                           DevSlice<const int8_t> wk, CF sk, DevSlice<const int8_t> wv, CF sv, CF x,
+                           size_t seq_len, size_t in_dim, size_t n_heads, size_t n_kv_heads,
+                           size_t head_dim, CF q_norm_w, CF k_norm_w, const RopeCache& rope,
+                           size_t start_pos, float eps) {
+  const size_t qd = n_heads * head_dim, kv = n_kv_heads * head_dim;
+  detail::need(q, seq_len * qd, "q");
+  detail::need(k_cache, cache_rows * kv, "k_cache");
+  detail::need(v_cache, cache_rows * kv, "v_cache");
+  detail::need(wq, qd * in_dim, "wq");
+  detail::need(sq, qd, "sq");
+  detail::need(wk, kv * in_dim, "wk");
+  detail::need(sk, kv, "sk");
+  detail::need(wv, kv * in_dim, "wv");
+  detail::need(sv, kv, "sv");
+  detail::need(x, seq_len * in_dim, "x");
+  detail::need(q_norm_w, head_dim, "q_norm_w");
+  detail::need(k_norm_w, head_dim, "k_norm_w");
+  if (rope.head_dim() != head_dim) throw Panic("qkv_heads_int8: RopeCache head_dim mismatch");
+  detail::check(qasr_qkv_heads_int8_f32(q.ptr, k_cache.ptr, v_cache.ptr, cache_rows, wq.ptr, sq.ptr, wk.ptr,
+                                        sk.ptr, wv.ptr, sv.ptr, x.ptr, seq_len, in_dim, n_heads, n_kv_heads,
+                                        head_dim, q_norm_w.ptr, k_norm_w.ptr, rope.cos().ptr, rope.sin().ptr,
+                                        rope.cap(), start_pos, eps, detail::st()),
+                "qkv_heads_int8");
+}
+
 // Decode folds (one token): h = x + delta (delta empty: h = x), the RMSNorm of h and the
 // projections of the normalised row in one launch, equal bit for bit to add_rms_norm followed by
 // the projection; h goes to h_out (empty: not written), which must not overlap x or delta.

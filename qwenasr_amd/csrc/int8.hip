@@ -642,8 +642,9 @@ constexpr int kGmBK = 64;           // K granularity of the GEMM path
 // (gate, up) row pair, y[t, n/2] = swiglu(y[t, n], y[t, n + 1]), an output row
 // of N/2 -- in the prefill form (kernels::swiglu_multiply's fast_exp blocks and
 // expf tail after the gate/up projection) or the decode loop's form
-// (g / (1 + expf(-g)) * u, decoder.rs:916-921) for batched decode streams
-enum GemmEpi { kGemmRows = 0, kGemmBias = 1, kGemmSwiglu = 2, kGemmSwigluLibm = 3 };
+// (g / (1 + expf(-g)) * u, decoder.rs:916-921) for batched decode streams;
+// or the q/k/v heads of a prefill chunk (head norms, RoPE, KV-cache rows)
+enum GemmEpi { kGemmRows = 0, kGemmBias = 1, kGemmSwiglu = 2, kGemmSwigluLibm = 3, kGemmHeads = 4 };
 // K chunks in flight per thread in the single-buffered LDS-staged kernel (2
 // and 3 measured slower: 1.7B gate/up at T = 512 86.0 -> 88.2 / 97.5 us), and
 // register sets of the double-buffered one (4 sets measured the same as 2)
@@ -704,9 +705,103 @@ QASR_DEV void swiglu_store(float* y, const float (&res)[4], int t, int n, int N)
   if (n + 3 < N) row[j + 1] = swiglu_ref(res[2], res[3], j + 1 < fast_end);
 }
 
+// The kGemmHeads epilogue: the q/k/v projections of a prefill chunk (one
+// sequence, token t at position start_pos + t) with the steps after them,
+// decoder.rs:799-810. The launch's matrices are q, k and v (set index 0, 1,
+// 2), every tile is one 128-row head x BT tokens, and per token:
+//   q head: per-head RMSNorm (q_norm_w) + NeoX RoPE, written to y (in place
+//           of the plain projection's output);
+//   k head: the same with k_norm_w, written to k_cache row start_pos + t;
+//   v head: written to v_cache row start_pos + t.
+// A position outside the RoPE table or the cache gives a NaN q row and no
+// cache write. The dequantized products are the plain epilogue's (acc *
+// scale) and the heads go through head_norm_rope, so the results equal the
+// GEMM followed by qasr_head_rms_norm_rope_kv_f32 bit for bit.
+struct GemmHeadEpi {
+  float* k_cache;  // [cache_rows][n_kv_heads * 128]
+  float* v_cache;
+  const float* q_norm_w;
+  const float* k_norm_w;
+  const float* cos_tab;  // [table_rows][128]
+  const float* sin_tab;
+  long long start_pos;
+  long long table_rows;
+  long long cache_rows;
+  int n_kv_heads;
+  float eps;
+};
+
+constexpr int kHeadTilePitch = 136;  // floats per token row of the staged head tile (pad: banks)
+
+// acc: the 4 waves' MI x MJ blocks of 32 x 32 (lane l, register 4q + v of
+// block (i, j) = row 64 wr + 32i + 8q + 4(l/32) + v of token 32 wc + 32j +
+// l%32 of the tile). Called after the k loop's last barrier (LDS free).
+template <int BT, int MI, int MJ>
+QASR_DEV void gemm_heads_epilogue(const v16f (&acc)[MI][MJ], float* tile, int mat, float* y,
+                                  const float* __restrict__ scales, int N, int n0, int t0, int T,
+                                  const GemmHeadEpi& he) {
+  static_assert(MI == 2 && BT == 64 * MJ, "a 128-row head per tile");
+  static_assert(BT * kHeadTilePitch * 4 <= (size_t)(128 + 3 * BT) * (kGmBK + 8) * 2, "the tile fits one stage");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave & 1, wc = wave >> 1;
+  const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < MJ; ++j)
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = 64 * wr + 32 * i + 8 * q + 4 * g;
+        const float4 s = *reinterpret_cast<const float4*>(scales + n0 + nl);
+        const float4 v = make_float4(acc[i][j][4 * q] * s.x, acc[i][j][4 * q + 1] * s.y,
+                                     acc[i][j][4 * q + 2] * s.z, acc[i][j][4 * q + 3] * s.w);
+        *reinterpret_cast<float4*>(tile + ((BT / 2) * wc + 32 * j + r) * kHeadTilePitch + nl) = v;
+      }
+  lds_barrier();
+  // 16 threads per token, in head_norm_rope's lane layout: dims 4sub.. and 64 + 4sub..
+  const int sub = tid & 15;
+  float4 w1, w2;
+  if (mat < 2) {
+    const float* w = mat == 0 ? he.q_norm_w : he.k_norm_w;
+    w1 = ld4(w, sub);
+    w2 = ld4(w + 64, sub);
+  }
+  const int head = n0 / 128;
+  const size_t kv_dim = (size_t)he.n_kv_heads * 128;
+#pragma unroll
+  for (int p = 0; p < BT / 16; ++p) {
+    const int tl = 16 * p + (tid >> 4), t = t0 + tl;
+    float4 x1 = *reinterpret_cast<const float4*>(tile + tl * kHeadTilePitch + 4 * sub);
+    float4 x2 = *reinterpret_cast<const float4*>(tile + tl * kHeadTilePitch + 64 + 4 * sub);
+    const long long pos = he.start_pos + t;
+    const bool pos_ok = pos < he.table_rows && pos < he.cache_rows;
+    if (mat < 2) {
+      const long long pr = pos_ok ? pos : 0;  // out-of-table rows read row 0, then become NaN
+      const float* cr = he.cos_tab + pr * 128;
+      const float* sr = he.sin_tab + pr * 128;
+      const float4 c1 = ld4(cr, sub), c2 = ld4(cr + 64, sub);
+      const float4 s1 = ld4(sr, sub), s2 = ld4(sr + 64, sub);
+      // every lane of the group joins the reduction, past T or not
+      head_norm_rope<128, true, true>(x1, x2, w1, w2, c1, c2, s1, s2, pos_ok, he.eps);
+    }
+    if (t >= T) continue;
+    float* dst = nullptr;
+    if (mat == 0) {
+      dst = y + (size_t)t * N + n0;
+    } else if (pos_ok) {  // a row outside the cache is not written
+      dst = (mat == 1 ? he.k_cache : he.v_cache) + (size_t)pos * kv_dim + (size_t)head * 128;
+    }
+    if (dst) {
+      st4(dst, sub, x1);
+      st4(dst + 64, sub, x2);
+    }
+  }
+}
+
 template <int BN, int BT, int BK, int NPF, int EPI>
 __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, TileMap map,
-                                                                const float* __restrict__ x, int T, int K) {
+                                                                const float* __restrict__ x, int T, int K,
+                                                                GemmHeadEpi he) {
   constexpr int kGmRow = BK + 8;  // LDS row in bf16 (16-byte pad)
   extern __shared__ __align__(16) unsigned short gm_lds[];  // [BN][kGmRow] weights, [3][BT][kGmRow] terms
   unsigned bx, by;
@@ -717,6 +812,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
   const float* bias = set.b[0];
   int N = set.N[0];
   unsigned bx0 = 0;
+  int mat = 0;
 #pragma unroll
   for (int m = 1; m < 4; ++m)
     if (m < set.n && bx >= set.bx_begin[m]) {
@@ -726,6 +822,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
       bias = set.b[m];
       N = set.N[m];
       bx0 = set.bx_begin[m];
+      mat = m;
     }
   // 32x32x16 products: a wave's (BN/2) x (BT/2) tile is MI x MJ blocks of 32 x 32
   // (the 16x16x32 form needs twice the independent accumulators to keep the
@@ -835,6 +932,11 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
     }
   }
 
+  if constexpr (EPI == kGemmHeads) {
+    static_assert(BN == 128, "one head per tile");
+    gemm_heads_epilogue<BT, MI, MJ>(acc, reinterpret_cast<float*>(gm_lds), mat, y, scales, N, n0, t0, T, he);
+    return;
+  }
   // lane l, register 4q + v of block (i, j) holds row n0 + (BN/2)wr + 32i + 8q + 4(l/32) + v
   // of token t0 + (BT/2)wc + 32j + l%32
   const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
@@ -883,7 +985,8 @@ constexpr size_t gemm_lds_bytes() {
 // the next chunk overwrites.
 template <int BN, int BT, int BK, int NS, int EPI>
 __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, TileMap map,
-                                                                   const float* __restrict__ x, int T, int K) {
+                                                                   const float* __restrict__ x, int T, int K,
+                                                                   GemmHeadEpi he) {
   constexpr int kGmRow = BK + 8;                   // LDS row in bf16 (16-byte pad)
   constexpr int STAGE = (BN + 3 * BT) * kGmRow;    // bf16 per LDS stage
   extern __shared__ __align__(16) unsigned short gm_lds[];  // 2 x ([BN][kGmRow] weights, [3][BT][kGmRow] terms)
@@ -895,6 +998,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
   const float* bias = set.b[0];
   int N = set.N[0];
   unsigned bx0 = 0;
+  int mat = 0;
 #pragma unroll
   for (int m = 1; m < 4; ++m)
     if (m < set.n && bx >= set.bx_begin[m]) {
@@ -904,6 +1008,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
       bias = set.b[m];
       N = set.N[m];
       bx0 = set.bx_begin[m];
+      mat = m;
     }
   constexpr int MI = BN / 64, MJ = BT / 64;
   static_assert(BN % 64 == 0 && BT % 64 == 0, "32 x 32 blocks per wave");
@@ -1036,6 +1141,11 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
     }
   }
 
+  if constexpr (EPI == kGemmHeads) {
+    static_assert(BN == 128, "one head per tile");
+    gemm_heads_epilogue<BT, MI, MJ>(acc, reinterpret_cast<float*>(gm_lds), mat, y, scales, N, n0, t0, T, he);
+    return;
+  }
   // lane l, register 4q + v of block (i, j) holds row n0 + (BN/2)wr + 32i + 8q + 4(l/32) + v
   // of token t0 + (BT/2)wc + 32j + l%32
   const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
@@ -1176,6 +1286,7 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
   const float* bias = set.b[0];
   int N = set.N[0];
   unsigned bx0 = 0;
+  int mat = 0;
 #pragma unroll
   for (int m = 1; m < 4; ++m)
     if (m < set.n && bx >= set.bx_begin[m]) {
@@ -1185,6 +1296,7 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
       bias = set.b[m];
       N = set.N[m];
       bx0 = set.bx_begin[m];
+      mat = m;
     }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches
@@ -1342,7 +1454,8 @@ bool try_gemm_ksplit(const GemmSet& set, unsigned cols, const float* x, int T, i
 }
 
 template <int BN, int BT, int BK, int NPF, int EPI>
-bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
+bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st,
+              const GemmHeadEpi& he = GemmHeadEpi{}) {
   constexpr size_t lds = gemm_lds_bytes<BN, BT, BK>();
   if (K % BK != 0) return false;
   if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, EPI>>(lds)) return false;
@@ -1350,12 +1463,13 @@ bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, h
   map.cols = cols;
   map.rows = (unsigned)((T + BT - 1) / BT);
   map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
-  w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K);
+  w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K, he);
   return true;
 }
 
 template <int BN, int BT, int BK, int NS, int EPI>
-bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st) {
+bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st,
+                 const GemmHeadEpi& he = GemmHeadEpi{}) {
   constexpr size_t lds = 2 * gemm_lds_bytes<BN, BT, BK>();
   if (K % (NS * BK) != 0) return false;
   if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_db_kernel<BN, BT, BK, NS, EPI>>(lds)) return false;
@@ -1363,7 +1477,7 @@ bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K
   map.cols = cols;
   map.rows = (unsigned)((T + BT - 1) / BT);
   map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
-  w8a32_gemm_bf16x3_db_kernel<BN, BT, BK, NS, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K);
+  w8a32_gemm_bf16x3_db_kernel<BN, BT, BK, NS, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K, he);
   return true;
 }
 
@@ -1435,6 +1549,21 @@ extern "C" int qasr_quantize_rows_i8(int8_t* q, float* scales, const float* x, s
 // From this many tokens the linear runs as one matrix-core GEMM instead of
 // per-token matvecs.
 constexpr size_t kGemmMinTokens = 8;
+
+// The q/k/v GEMM with the heads epilogue: 128-row tiles (one head), double
+// buffered where that is one workgroup per CU, as for the plain projection.
+static bool launch_w8a32_heads(GemmSet set, const float* x, int T, int K, const GemmHeadEpi& he,
+                               hipStream_t st) {
+  unsigned c = 0;
+  for (int m = 0; m < set.n; ++m) {
+    set.bx_begin[m] = c;
+    c += (unsigned)(set.N[m] / 128);
+  }
+  for (int m = set.n; m <= 4; ++m) set.bx_begin[m] = c;
+  const long long rows64 = (T + 63) / 64;
+  if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, kGemmHeads>(set, c, x, T, K, st, he)) return true;
+  return try_gemm<128, 64, 64, kGemmPrefetch, kGemmHeads>(set, c, x, T, K, st, he);
+}
 
 static bool w8a32_gemm_shape(size_t seq_len, size_t in_dim, const void* w, const void* x) {
   return seq_len >= kGemmMinTokens && in_dim % kGmBK == 0 && aligned16(w) && aligned16(x);
@@ -1576,6 +1705,69 @@ extern "C" int qasr_gate_up_swiglu_multiply_int8_f32(float* out, const float* x,
         out, x, w_gate_up, scales_gate_up, (int)seq_len, (int)in_dim, (int)intermediate);
   }
   return launch_status("gate_up_swiglu_multiply_int8");
+}
+
+extern "C" int qasr_qkv_heads_int8_f32(float* q, float* k_cache, float* v_cache, size_t cache_rows,
+                                       const int8_t* wq, const float* sq, const int8_t* wk,
+                                       const float* sk, const int8_t* wv, const float* sv,
+                                       const float* x, size_t seq_len, size_t in_dim, size_t n_heads,
+                                       size_t n_kv_heads, size_t head_dim, const float* q_norm_w,
+                                       const float* k_norm_w, const float* cos_tab,
+                                       const float* sin_tab, size_t table_rows, size_t start_pos,
+                                       float eps, void* stream) {
+  if (seq_len == 0) return QASR_OK;
+  QASR_REQUIRE(q && k_cache && v_cache && wq && sq && wk && sk && wv && sv && x && q_norm_w && k_norm_w &&
+                   cos_tab && sin_tab,
+               "qkv_heads_int8: null pointer");
+  QASR_REQUIRE(n_heads >= 1 && n_kv_heads >= 1 && n_heads <= 65536 && n_kv_heads <= 65536,
+               "qkv_heads_int8: head counts must be in [1, 65536]");
+  QASR_REQUIRE(start_pos <= cache_rows && seq_len <= cache_rows - start_pos && start_pos <= table_rows &&
+                   seq_len <= table_rows - start_pos,
+               "qkv_heads_int8: rows start_pos..start_pos+seq_len exceed the cache or the RoPE table");
+  if (head_dim != 128) return fail(QASR_ERR_UNSUPPORTED, "qkv_heads_int8: head_dim must be 128");
+  const size_t rows = (n_heads + 2 * n_kv_heads) * 128, kv_dim = n_kv_heads * 128;
+  size_t n;
+  QASR_REQUIRE(rows <= 0x7fffffffu && in_dim <= 0x7fffffffu && seq_len <= 0x7fffffffu &&
+                   start_pos <= 0x3fffffffffffffffull && table_rows <= 0x3fffffffffffffffull &&
+                   cache_rows <= 0x3fffffffffffffffull,
+               "qkv_heads_int8: size too large");
+  QASR_REQUIRE(mul_ok(rows, in_dim, &n) && mul_ok(seq_len, in_dim, &n) && mul_ok(seq_len, rows, &n) &&
+                   mul_ok(cache_rows, kv_dim, &n) && mul_ok(rows / 128, (seq_len + 63) / 64, &n) &&
+                   n <= 0x7fffffffu,
+               "qkv_heads_int8: size overflows");
+  const bool aligned = aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(sq) &&
+                       aligned16(sk) && aligned16(sv) && aligned16(q_norm_w) && aligned16(k_norm_w) &&
+                       aligned16(cos_tab) && aligned16(sin_tab) && aligned16(wk) && aligned16(wv);
+  if (!aligned || !w8a32_gemm_shape(seq_len, in_dim, wq, x))
+    return fail(QASR_ERR_UNSUPPORTED,
+                "qkv_heads_int8: needs seq_len >= 8, in_dim % 64 == 0 and 16-byte aligned buffers");
+  GemmSet set{};
+  const int8_t* ws[3] = {wq, wk, wv};
+  const float* ss[3] = {sq, sk, sv};
+  const size_t outs[3] = {n_heads * 128, kv_dim, kv_dim};
+  for (int m = 0; m < 3; ++m) {
+    set.y[m] = m == 0 ? q : nullptr;
+    set.w[m] = ws[m];
+    set.s[m] = ss[m];
+    set.b[m] = nullptr;
+    set.N[m] = (int)outs[m];
+  }
+  set.n = 3;
+  GemmHeadEpi he{};
+  he.k_cache = k_cache;
+  he.v_cache = v_cache;
+  he.q_norm_w = q_norm_w;
+  he.k_norm_w = k_norm_w;
+  he.cos_tab = cos_tab;
+  he.sin_tab = sin_tab;
+  he.start_pos = (long long)start_pos;
+  he.table_rows = (long long)table_rows;
+  he.cache_rows = (long long)cache_rows;
+  he.n_kv_heads = (int)n_kv_heads;
+  he.eps = eps;
+  if (!launch_w8a32_heads(set, x, (int)seq_len, (int)in_dim, he, as_stream(stream)))
+    return fail(QASR_ERR_UNSUPPORTED, "qkv_heads_int8: the GEMM kernel cannot run this shape");
+  return launch_status("qkv_heads_int8");
 }
 
 extern "C" int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,

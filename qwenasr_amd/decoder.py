@@ -22,10 +22,11 @@ never leave HBM.
 ``DecoderInt8.prefill`` runs the reference's INT8 prefill
 (decoder.rs:751-847) for a chunk of tokens: per layer RMSNorm (fused with the
 previous layer's residual add), q/k/v (one matrix-core GEMM launch), q/k head
-RMSNorm + RoPE with the chunk's K/V rows written into the cache, causal
-attention over the cache (matrix cores), o, residual add + post-attention
-RMSNorm, gate/up with the prefill SwiGLU (fast_exp form) in its epilogue,
-down: 8 launches per layer, then the last residual add.
+RMSNorm + RoPE with the chunk's K/V rows written into the cache (in the q/k/v
+GEMM's epilogue where that launch fills the chip, else a launch of its own),
+causal attention over the cache (matrix cores), o, residual add +
+post-attention RMSNorm, gate/up with the prefill SwiGLU (fast_exp form) in its
+epilogue, down: 7 or 8 launches per layer, then the last residual add.
 
 Weights come from ``qint8.load_decoder_int8`` (or any dict of the same
 layout); ``DecoderInt8.decode`` runs one token and can be captured in a HIP
@@ -45,7 +46,7 @@ class DecoderInt8:
     def __init__(self, weights: dict, hidden: int, intermediate: int, n_layers: int, n_heads: int = 16,
                  n_kv_heads: int = 8, head_dim: int = 128, eps: float = 1e-6, theta: float = 1e6,
                  vocab: int | None = None, max_seq: int = 256, device="cuda",
-                 fuse_norms: bool | None = None):
+                 fuse_norms: bool | None = None, fuse_prefill_heads: bool | None = None):
         self.w = weights
         self.H, self.I, self.L = hidden, intermediate, n_layers
         self.nq, self.nk, self.hd = n_heads, n_kv_heads, head_dim
@@ -58,6 +59,11 @@ class DecoderInt8:
         # the fused launches take rows of 1024..8192 floats in steps of 1024
         ok = hidden % 1024 == 0 and 1024 <= hidden <= 8192
         self.fuse_norms = ok if fuse_norms is None else (fuse_norms and ok)
+        # prefill q/k/v with the head norms, RoPE and cache rows in the GEMM's
+        # epilogue (one workgroup per 128-row head x 64 tokens): None takes it
+        # where that launch fills the chip (>= 256 workgroups); below, the
+        # unfused split-K GEMM + head kernel is faster
+        self.fuse_prefill_heads = fuse_prefill_heads
         self.x = torch.zeros(hidden, **f32)
         self.x2 = torch.zeros(hidden, **f32)  # the residual's other buffer (fused path)
         self.x_norm = torch.empty(hidden, **f32)
@@ -113,6 +119,13 @@ class DecoderInt8:
         self.rope.ensure(start_pos + T, self.hd, self.theta)
         self._ensure_prefill(T)
 
+    def prefill_heads_fused(self, T: int) -> bool:
+        """Whether a prefill of T tokens runs q/k/v with the heads in one launch."""
+        fits = self.hd == 128 and self.H % 64 == 0 and T >= 8
+        if self.fuse_prefill_heads is None:
+            return fits and (self.nq + 2 * self.nk) * ((T + 63) // 64) >= 256
+        return self.fuse_prefill_heads and fits
+
     def prefill(self, embeds: torch.Tensor, T: int, start_pos: int | None = None) -> None:
         """T tokens at positions start_pos.. (decoder.rs:751-847): writes cache rows
         start_pos..start_pos+T-1 of every layer; ``self.px[:T*H]`` receives the
@@ -121,6 +134,7 @@ class DecoderInt8:
         H, I, nq, nk, hd, eps = self.H, self.I, self.nq, self.nk, self.hd, self.eps
         q_dim = nq * hd
         total = start_pos + T
+        fused_heads = self.prefill_heads_fused(T)
         x = self.px
         x[:T * H].copy_(embeds[:T * H])
         for l, lw in enumerate(self.w["layers"]):
@@ -128,11 +142,15 @@ class DecoderInt8:
                 K.rms_norm(self.pxn, x, lw["input_norm"], T, H, eps)
             else:  # previous layer's residual add (decoder.rs:843) + this layer's input norm
                 K.add_rms_norm(x, self.pffn, lw["input_norm"], self.pxn, T, H, eps)
-            K.linear_nobias_int8_multi([self.pq, self.pk, self.pv], [lw["wq"], lw["wk"], lw["wv"]],
-                                       self.pxn, T, H)
             kb, vb = self.kv.k_layer_block(l), self.kv.v_layer_block(l)
-            K.head_rms_norm_rope_kv(self.pq, self.pk, self.pv, lw["q_norm"], lw["k_norm"], self.rope, None,
-                                    start_pos, T, nq, nk, hd, eps, kb, vb, self.kv.max_seq)
+            if fused_heads:
+                K.qkv_heads_int8(self.pq, kb, vb, self.kv.max_seq, lw["wq"], lw["wk"], lw["wv"], self.pxn, T, H,
+                                 nq, nk, hd, lw["q_norm"], lw["k_norm"], self.rope, start_pos, eps)
+            else:
+                K.linear_nobias_int8_multi([self.pq, self.pk, self.pv], [lw["wq"], lw["wk"], lw["wv"]],
+                                           self.pxn, T, H)
+                K.head_rms_norm_rope_kv(self.pq, self.pk, self.pv, lw["q_norm"], lw["k_norm"], self.rope, None,
+                                        start_pos, T, nq, nk, hd, eps, kb, vb, self.kv.max_seq)
             K.causal_attention(self.pattn, self.pq, kb, vb, T, total, nq, nk, hd, self.scale, start_pos)
             wo = lw["wo"]
             K.linear_nobias_int8(self.pproj, self.pattn, wo.data, wo.scales, T, q_dim, H)

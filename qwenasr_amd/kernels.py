@@ -615,6 +615,32 @@ def linear_nobias_int8_multi(ys, ws: list, x, seq_len: int, in_dim: int) -> None
               _stream())
 
 
+def qkv_heads_int8(q, k_cache, v_cache, cache_rows: int, wq: QuantWeight, wk: QuantWeight, wv: QuantWeight,
+                   x, seq_len: int, in_dim: int, n_heads: int, n_kv_heads: int, head_dim: int, q_norm_w,
+                   k_norm_w, rope: "RopeCache", start_pos: int, eps: float) -> None:
+    """A prefill chunk's q/k/v projections + q/k head norms + RoPE + the K/V
+    cache rows in one launch (decoder.rs:783-810). Same results, bit for bit, as
+    ``linear_nobias_int8_multi`` followed by ``head_rms_norm_rope_kv`` (positions
+    None); ``k_cache``/``v_cache`` are the layer's ``[cache_rows, kv_dim]`` blocks.
+    head_dim 128, seq_len >= 8 and in_dim % 64 == 0 (else the library raises)."""
+    kv = n_kv_heads * head_dim
+    _need(q, F32, seq_len * n_heads * head_dim, "q")
+    _need(k_cache, F32, cache_rows * kv, "k_cache")
+    _need(v_cache, F32, cache_rows * kv, "v_cache")
+    for w, rows, name in ((wq, n_heads * head_dim, "wq"), (wk, kv, "wk"), (wv, kv, "wv")):
+        _need(w.data, I8, rows * in_dim, name)
+        _need(w.scales, F32, rows, name + ".scales")
+    _need(x, F32, seq_len * in_dim, "x")
+    _need(q_norm_w, F32, head_dim, "q_norm_w")
+    _need(k_norm_w, F32, head_dim, "k_norm_w")
+    if rope.head_dim != head_dim:
+        raise ValueError("RopeCache head_dim does not match")
+    _lib.call("qasr_qkv_heads_int8_f32", _ptr(q), _ptr(k_cache), _ptr(v_cache), cache_rows, _ptr(wq.data),
+              _ptr(wq.scales), _ptr(wk.data), _ptr(wk.scales), _ptr(wv.data), _ptr(wv.scales), _ptr(x), seq_len,
+              in_dim, n_heads, n_kv_heads, head_dim, _ptr(q_norm_w), _ptr(k_norm_w), _ptr(rope.cos),
+              _ptr(rope.sin), rope.cap, start_pos, eps, _stream())
+
+
 def gate_up_swiglu_int8(out, x, w: QuantWeight, seq_len: int, in_dim: int, intermediate: int) -> None:
     """W8A32 gate/up projection on the interleaved weight + the decode loop's
     SwiGLU (decoder.rs:912-921), one launch; gate/up values are not stored."""

@@ -246,19 +246,23 @@ def _load(tmp_path, w, L, dev):
         return qint8.load_decoder_int8(qf, dims, dev)
 
 
+@pytest.mark.parametrize("fuse_heads", [True, False])
 @pytest.mark.parametrize("H,I", [(1024, 3072), (2048, 6144)])
-def test_prefill_then_decode_matches_the_oracle(tmp_path, dev, H, I):
+def test_prefill_then_decode_matches_the_oracle(tmp_path, dev, H, I, fuse_heads):
     """The device prefill (decoder.rs:751-847) of two chunks -- 37 rows at
     position 0 (ragged matrix-core GEMM tiles), then 20 rows at 37 -- against
     the oracle's restatement: the residual stream after the last layer and
     every cache row, then a decode step over the prefilled cache (token,
-    logits). Tolerance as for the decode step (chained kernels, 1e-4)."""
+    logits), with q/k/v and the heads in one launch or two. Tolerance as for
+    the decode step (chained kernels, 1e-4)."""
     from qwenasr_amd.decoder import DecoderInt8
 
     L, nq, nk, hd, vocab = 2, 16, 8, 128, 1000
     r = np.random.default_rng([35, H])
     w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
-    dec = DecoderInt8(_load(tmp_path, w, L, dev), H, I, L, nq, nk, hd, max_seq=64, device=dev)
+    dec = DecoderInt8(_load(tmp_path, w, L, dev), H, I, L, nq, nk, hd, max_seq=64, device=dev,
+                      fuse_prefill_heads=fuse_heads)
+    assert dec.prefill_heads_fused(37) == fuse_heads
     kv = nk * hd
     kc = np.zeros((L, 128, kv), np.float32)
     vc = np.zeros_like(kc)
@@ -348,12 +352,13 @@ def test_graph_replays_equal_the_eager_calls(tmp_path, dev):
               f"decode fuse_norms={fuse}")
 
     T = 64
-    d = DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=512, device=dev)
-    d.prepare_prefill(0, T)
     e = torch.randn(T * H, device=dev, generator=gen)
+    for fuse_heads in (False, True):
+        d = DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=512, device=dev, fuse_prefill_heads=fuse_heads)
+        d.prepare_prefill(0, T)
 
-    def prefill_at_0():
-        d.kv.len = 0  # every call (and replay) prefills the same chunk at position 0
-        d.prefill(e, T, 0)
+        def prefill_at_0():
+            d.kv.len = 0  # every call (and replay) prefills the same chunk at position 0
+            d.prefill(e, T, 0)
 
-    check(d, prefill_at_0, ("px",), slice(0, T), "prefill")
+        check(d, prefill_at_0, ("px",), slice(0, T), f"prefill fuse_prefill_heads={fuse_heads}")

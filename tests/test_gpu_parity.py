@@ -284,6 +284,72 @@ def test_head_rms_norm_rope_kv_single_sequence(dev, seq, start, nq, nk, hd, cach
     np.testing.assert_array_equal(kh[start:start + seq], host(k2).reshape(seq, kv_dim))
 
 
+@pytest.mark.parametrize("seq,H,start,cache_rows,exact", [
+    (512, 1024, 0, 1024, True),    # 0.6B prefill chunk: the double-buffered tile, 256 workgroups
+    (1000, 1024, 24, 1536, True),  # 512 workgroups: the single-buffered tile
+    (100, 2048, 37, 512, False),   # ragged token tile (the plain launch takes the split-K tile)
+    (64, 1088, 5, 128, False),     # in_dim % 128 = 64: single-buffered
+    (40, 1024, 88, 128, False),    # the chunk ends at the last cache row
+])
+def test_qkv_heads_int8_equals_unfused(dev, seq, H, start, cache_rows, exact):
+    """The prefill q/k/v GEMM with the heads in its epilogue equals
+    linear_nobias_int8_multi + head_rms_norm_rope_kv (decoder.rs:783-810):
+    bit for bit where the plain launch uses the same LDS-staged 128-row tile
+    (the dequantized products and head_norm_rope are shared), else within the
+    fp32 tolerance (another k order in the plain GEMM); the oracle composition
+    checks the small cases. Cache rows outside the chunk keep their contents;
+    a chunk past the cache or the RoPE table is rejected before any launch."""
+    from qwenasr_amd import kernels as K
+
+    nq, nk, hd, eps = 16, 8, 128, 1e-6
+    kv = nk * hd
+    r = rng(41, seq, H, start)
+    x = normal(r, seq * H)
+    mats = [make_qweight(r, n, H) for n in (nq * hd, kv, kv)]
+    ws = [K.QuantWeight(dev_t(wq, dev), dev_t(sc, dev), n, H) for (wq, sc), n in zip(mats, (nq * hd, kv, kv))]
+    qw, kw = normal(r, hd, 0.1, 1.0), normal(r, hd, 0.1, 1.0)
+    rope = K.RopeCache(dev)
+    rope.ensure(start + seq, hd, 1e6)
+    xt, qwt, kwt = dev_t(x, dev), dev_t(qw, dev), dev_t(kw, dev)
+
+    q1 = torch.full((seq * nq * hd,), 7.0, device=dev)
+    kc1 = torch.full((cache_rows * kv,), 7.0, device=dev)
+    vc1 = torch.full((cache_rows * kv,), 7.0, device=dev)
+    K.qkv_heads_int8(q1, kc1, vc1, cache_rows, *ws, xt, seq, H, nq, nk, hd, qwt, kwt, rope, start, eps)
+
+    q2 = torch.empty(seq * nq * hd, device=dev)
+    k2, v2 = torch.empty(seq * kv, device=dev), torch.empty(seq * kv, device=dev)
+    kc2 = torch.full((cache_rows * kv,), 7.0, device=dev)
+    vc2 = torch.full((cache_rows * kv,), 7.0, device=dev)
+    K.linear_nobias_int8_multi([q2, k2, v2], ws, xt, seq, H)
+    K.head_rms_norm_rope_kv(q2, k2, v2, qwt, kwt, rope, None, start, seq, nq, nk, hd, eps, kc2, vc2, cache_rows)
+    got = [host(t) for t in (q1, kc1, vc1)]
+    ref = [host(t) for t in (q2, kc2, vc2)]
+    for g, f, what in zip(got, ref, ("q", "k cache", "v cache")):
+        if exact:
+            np.testing.assert_array_equal(g, f, err_msg=what)
+        else:
+            assert_close(g, f, RTOL, ATOL, what)
+    live = seq
+    kh = got[1].reshape(cache_rows, kv)
+    others = np.r_[0:start, start + live:cache_rows]
+    assert (kh[others] == 7.0).all() and (got[2].reshape(cache_rows, kv)[others] == 7.0).all()
+    assert not np.isnan(got[0]).any()
+    with pytest.raises(K.QasrError, match="exceed the cache"):
+        K.qkv_heads_int8(q1, kc1, vc1, cache_rows, *ws, xt, seq, H, nq, nk, hd, qwt, kwt, rope,
+                         cache_rows - seq + 1, eps)
+    if seq <= 128:
+        pq, pk, pv = (oracle.linear_nobias_int8(x, wq, sc, seq, H, n)
+                      for (wq, sc), n in zip(mats, (nq * hd, kv, kv)))
+        cos, sin = oracle.rope_table(rope.cap, hd, 1e6)
+        pos = np.minimum(np.arange(start, start + seq), rope.cap - 1)
+        q_ref, k_rows, v_rows = kv_reference(pq, pk, pv, qw, kw, cos, sin, pos, seq, nq, nk, hd, eps)
+        assert_close(got[0].reshape(seq, -1)[:live], q_ref.reshape(seq, -1)[:live], RTOL, ATOL, "q vs oracle")
+        assert_close(kh[start:start + live], k_rows[:live], RTOL, ATOL, "k rows vs oracle")
+        assert_close(got[2].reshape(cache_rows, kv)[start:start + live], v_rows[:live], RTOL, ATOL,
+                     "v rows vs oracle")
+
+
 def test_head_rms_norm_rope_kv_per_stream(dev):
     """Batched decode: row s is stream s at its own position, each stream with
     its own [cache_rows, kv_dim] block; a position past the cache leaves that
