@@ -1265,6 +1265,14 @@ def test_causal_attention_reads_a_cache_block(dev):
     ("decode_hd64_g4", 1, 1500, 8, 2, 64, 1499),
     ("short_no_split", 1, 200, 16, 8, 128, 199),
     ("rows_end_early", 2, 3000, 16, 8, 128, 700),   # causal limit far below seq_k: empty splits
+    # prefill shapes with a workspace: many rows (the matrix-core kernel) and
+    # few rows over long key ranges (the split)
+    ("prefill_0.6b_t512", 512, 512, 16, 8, 128, 0),
+    ("prefill_chunk_at_200", 100, 300, 16, 8, 128, 200),
+    ("prefill_g1", 130, 900, 8, 8, 128, 770),
+    ("prefill_g4_long", 40, 4000, 16, 4, 128, 3960),
+    ("prefill_g8", 24, 100, 16, 2, 128, 76),
+    ("prefill_seq_k_short", 64, 200, 16, 8, 128, 300),  # every row limited by seq_k
 ])
 def test_causal_attention_split(dev, name, seq_q, seq_k, nq, nk, hd, q_offset):
     from qwenasr_amd import kernels as K
