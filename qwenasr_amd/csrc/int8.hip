@@ -1012,9 +1012,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
     }
   constexpr int MI = BN / 64, MJ = BT / 64;
   static_assert(BN % 64 == 0 && BT % 64 == 0, "32 x 32 blocks per wave");
-  constexpr int TPW = 256 / BN, WB = BK / TPW;       // weight staging: threads per row, bytes each
-  constexpr int TPX = 256 / BT, XF = BK / TPX;       // activation staging: threads per token, floats each
-  constexpr int NW = WB / 16, NX = XF / 4;           // 16-byte staging items per thread
+  constexpr int NW = BN / 64, NX = BT / 16;         // 16-byte staging items per thread
   constexpr int KSTEPS = BK / 16;                    // MFMA k steps per chunk
   static_assert(NW >= 1 && NX >= 1, "each thread stages whole 16-byte items");
   static_assert(NS >= 2 && NS % 2 == 0, "an even number of register sets");
@@ -1490,7 +1488,11 @@ bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K
 // q/k/v: 25.7 -> 24.9 us at K = 1024, 40.4 -> 37.4 us at K = 2048); with more
 // workgroups the single-buffered kernel is faster (two or three share a CU and
 // overlap each other's staging and MFMAs; the double-buffered one's LDS allows
-// only one: 0.6B gate/up at T = 512 33.5 against 42-45 us); otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
+// only one: 0.6B gate/up at T = 512 33.5 against 42-45 us), except where the
+// 128-row tiles would give some CUs two workgroups and others one while
+// 192-row tiles give at most one per CU: those run double-buffered (0.6B
+// gate/up at T = 512: 384 tiles of 128 rows 29.3 us, 256 of 192 27.3 us);
+// otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
 // 32 x 32 that fills the chip (measured at T = 512: o [1024, 2048] 20.0 ->
 // 16.7 us, down [1024, 3072] 27.4 -> 20.9 us against the LDS-staged 64 x 32).
 // Returns false when the chosen kernel cannot run the shape (K not a multiple
@@ -1509,6 +1511,11 @@ bool launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
   const long long rows64 = (T + 63) / 64, rows32 = (T + 31) / 32;
   unsigned c = cols(256);
   if (c * rows64 >= 512) return try_gemm<256, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
+  const unsigned c128 = cols(128);
+  c = cols(192);
+  if (c128 * rows64 > 256 && c * rows64 <= 256 &&
+      try_gemm_db<192, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st))
+    return true;
   c = cols(128);
   if (c * rows64 >= 256) {
     if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st)) return true;

@@ -805,6 +805,8 @@ def test_add_rms_norm_gate_up_swiglu_equals_unfused(dev, H, I, with_delta):
                                                 (8, 1024, 33), (64, 2048, 2048), (512, 1024, 6144),
                                                 (100, 3072, 1000), (17, 1024, 130), (70, 6144, 257),
                                                 (9, 1088, 200),
+                                                # 192-row double-buffered tiles, ragged rows and tokens
+                                                (500, 1024, 5000),
                                                 # split-K 64x64, 64x32 tiles (32x32 above), ragged
                                                 (512, 1024, 2048), (512, 1088, 2048), (520, 1024, 2000),
                                                 (512, 2048, 1024), (500, 1024, 1000),
