@@ -289,7 +289,7 @@ int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,
                                       size_t in_dim, void* stream);
 
 /* A prefill chunk's q/k/v projections with the steps after them in one launch
- * (decoder.rs:783-810: the three linear_nobias_int8 calls, per-head RMSNorm
+ * (decoder.rs:795-810: the three linear_nobias_int8 calls, per-head RMSNorm
  * of q and k, NeoX RoPE, and the k_at/v_at copies into the layer's cache).
  * Token s of x [seq_len, in_dim] is at position p = start_pos + s:
  *   q[s, :]            = rope(rms_norm_head(x[s] . wq^T * sq, q_norm_w), p)

@@ -493,7 +493,7 @@ inline void gate_up_swiglu_multiply_int8(F out, CF x, DevSlice<const int8_t> w_g
                 "gate_up_swiglu_multiply_int8");
 }
 
-// Prefill q/k/v with the head norms, RoPE and K/V cache rows in one launch (decoder.rs:783-810):
+// Prefill q/k/v with the head norms, RoPE and K/V cache rows in one launch (decoder.rs:795-810):
 // bit-identical to linear_nobias_int8_multi (q, k, v) + head_rms_norm_rope_kv without positions.
 // k_cache/v_cache are the layer's [cache_rows][n_kv_heads*head_dim] blocks.
 inline void qkv_heads_int8(F q, F k_cache, F v_cache, size_t cache_rows, DevSlice<const int8_t> wq, CF sq,

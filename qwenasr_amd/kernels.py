@@ -619,7 +619,7 @@ def qkv_heads_int8(q, k_cache, v_cache, cache_rows: int, wq: QuantWeight, wk: Qu
                    x, seq_len: int, in_dim: int, n_heads: int, n_kv_heads: int, head_dim: int, q_norm_w,
                    k_norm_w, rope: "RopeCache", start_pos: int, eps: float) -> None:
     """A prefill chunk's q/k/v projections + q/k head norms + RoPE + the K/V
-    cache rows in one launch (decoder.rs:783-810). Same results, bit for bit, as
+    cache rows in one launch (decoder.rs:795-810). Same results, bit for bit, as
     ``linear_nobias_int8_multi`` followed by ``head_rms_norm_rope_kv`` (positions
     None); ``k_cache``/``v_cache`` are the layer's ``[cache_rows, kv_dim]`` blocks.
     head_dim 128, seq_len >= 8 and in_dim % 64 == 0 (else the library raises)."""

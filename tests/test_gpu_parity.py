@@ -293,7 +293,7 @@ def test_head_rms_norm_rope_kv_single_sequence(dev, seq, start, nq, nk, hd, cach
 ])
 def test_qkv_heads_int8_equals_unfused(dev, seq, H, start, cache_rows, exact):
     """The prefill q/k/v GEMM with the heads in its epilogue equals
-    linear_nobias_int8_multi + head_rms_norm_rope_kv (decoder.rs:783-810):
+    linear_nobias_int8_multi + head_rms_norm_rope_kv (decoder.rs:795-810):
     bit for bit where the plain launch uses the same LDS-staged 128-row tile
     (the dequantized products and head_norm_rope are shared), else within the
     fp32 tolerance (another k order in the plain GEMM); the oracle composition
