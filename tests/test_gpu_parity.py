@@ -284,14 +284,16 @@ def test_head_rms_norm_rope_kv_single_sequence(dev, seq, start, nq, nk, hd, cach
     np.testing.assert_array_equal(kh[start:start + seq], host(k2).reshape(seq, kv_dim))
 
 
-@pytest.mark.parametrize("seq,H,start,cache_rows,exact", [
-    (512, 1024, 0, 1024, True),    # 0.6B prefill chunk: the double-buffered tile, 256 workgroups
-    (1000, 1024, 24, 1536, True),  # 512 workgroups: the single-buffered tile
-    (100, 2048, 37, 512, False),   # ragged token tile (the plain launch takes the split-K tile)
-    (64, 1088, 5, 128, False),     # in_dim % 128 = 64: single-buffered
-    (40, 1024, 88, 128, False),    # the chunk ends at the last cache row
+@pytest.mark.parametrize("seq,H,start,cache_rows,exact,nq,nk", [
+    (512, 1024, 0, 1024, True, 16, 8),    # 0.6B prefill chunk: the double-buffered tile, 256 workgroups
+    (1000, 1024, 24, 1536, True, 16, 8),  # 512 workgroups: the single-buffered tile
+    (100, 2048, 37, 512, False, 16, 8),   # ragged token tile (the plain launch takes the split-K tile)
+    (64, 1088, 5, 128, False, 16, 8),     # in_dim % 128 = 64: single-buffered
+    (40, 1024, 88, 128, False, 16, 8),    # the chunk ends at the last cache row
+    (200, 2048, 11, 256, False, 32, 4),   # 8 q heads per kv head
+    (72, 1024, 0, 96, False, 8, 8),       # one q head per kv head
 ])
-def test_qkv_heads_int8_equals_unfused(dev, seq, H, start, cache_rows, exact):
+def test_qkv_heads_int8_equals_unfused(dev, seq, H, start, cache_rows, exact, nq, nk):
     """The prefill q/k/v GEMM with the heads in its epilogue equals
     linear_nobias_int8_multi + head_rms_norm_rope_kv (decoder.rs:795-810):
     bit for bit where the plain launch uses the same LDS-staged 128-row tile
@@ -301,9 +303,9 @@ def test_qkv_heads_int8_equals_unfused(dev, seq, H, start, cache_rows, exact):
     a chunk past the cache or the RoPE table is rejected before any launch."""
     from qwenasr_amd import kernels as K
 
-    nq, nk, hd, eps = 16, 8, 128, 1e-6
+    hd, eps = 128, 1e-6
     kv = nk * hd
-    r = rng(41, seq, H, start)
+    r = rng(41, seq, H, start, nq)
     x = normal(r, seq * H)
     mats = [make_qweight(r, n, H) for n in (nq * hd, kv, kv)]
     ws = [K.QuantWeight(dev_t(wq, dev), dev_t(sc, dev), n, H) for (wq, sc), n in zip(mats, (nq * hd, kv, kv))]
