@@ -197,6 +197,28 @@ def test_linear_multi_validation():
     assert so.qasr_linear_nobias_int8_multi_f32(0, None, None, None, None, None, 1, 1024, NULL) == 0
 
 
+def test_qkv_heads_int8_validation():
+    """The prefill q/k/v + heads entry point rejects bad calls before any launch:
+    null pointers and rows past the cache or the RoPE table (INVALID_ARG, as the
+    unfused head kernel), head_dim other than 128, fewer than 8 tokens and
+    in_dim % 64 != 0 (UNSUPPORTED); zero tokens is a no-op."""
+    inv, uns = _lib.QASR_ERR_INVALID_ARG, _lib.QASR_ERR_UNSUPPORTED
+    F = FAKE
+    # (q, k_cache, v_cache, cache_rows, wq, sq, wk, sk, wv, sv, x, seq_len, in_dim, n_heads, n_kv_heads,
+    #  head_dim, q_norm_w, k_norm_w, cos, sin, table_rows, start_pos, eps, stream)
+    def call(*, q=F, cache_rows=1024, seq=64, in_dim=1024, hd=128, table=1024, start=0, qw=F):
+        return rc("qasr_qkv_heads_int8_f32", q, F, F, cache_rows, F, F, F, F, F, F, F, seq, in_dim, 16, 8, hd,
+                  qw, F, F, F, table, start, 1e-6, NULL)
+    assert call(q=NULL) == inv
+    assert call(qw=NULL) == inv
+    assert call(start=1000) == inv and "exceed the cache" in last_error()
+    assert call(table=1000, start=960) == inv
+    assert call(hd=64) == uns
+    assert call(seq=7) == uns
+    assert call(in_dim=1000) == uns
+    assert call(seq=0, q=NULL) == _lib.QASR_OK
+
+
 def test_fused_norm_projection_validation():
     """The fused add + RMSNorm + projection entry points reject, before any
     launch: an h_out that overlaps x or delta (other workgroups still read the
