@@ -55,6 +55,7 @@ FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 LLC_BYTES = 256 << 20
 ROTATE_BYTES = 2 * LLC_BYTES  # each kernel's rotating footprint must exceed 2x the LLC
+FLUSH_BYTES = 4 * LLC_BYTES   # written before every timed replay of a cold workload
 
 DEC_0_6B = dict(hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, inter=3072, eps=1e-6, theta=1e6)
 DEC_1_7B = dict(hidden=2048, n_heads=16, n_kv_heads=8, head_dim=128, inter=6144, eps=1e-6, theta=1e6)
@@ -78,6 +79,9 @@ class Workload:
     step_bytes = 0   # algorithmic bytes per step
     dtype = "f32"    # arithmetic type of the path
     steps_hint = 200  # K of the timed region (a cold workload rotates at least K buffer sets)
+    hot = False       # True: the workload is meant to run from the caches (no flush before replays)
+    min_steps = 1     # the timed region holds at least this many steps
+    rotation = None   # distinct buffer sets a kernel's launches rotate over (None: at least K)
 
     def __init__(self, dev, torch):
         self.dev = dev
@@ -106,6 +110,8 @@ class C1DecodeChain(Workload):
     description = ("qwen3-asr-0.6b decode-token chain B=1: add+RMSNorm[1,1024] + q/k head-RMSNorm"
                    "+RoPE(theta 1e6, pos~U[0,511]) + SwiGLU[3072]")
     unit_tokens = 1
+    hot = True
+    min_steps = 1000  # the configuration's 1000 repetitions per timed region
 
     def __init__(self, dev, torch):
         super().__init__(dev, torch)
@@ -114,6 +120,7 @@ class C1DecodeChain(Workload):
         c = DEC_0_6B
         H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
         self.S = self.n_sets()
+        self.rotation = self.S
         self.x = [self.randn(H) for _ in range(self.S)]
         self.d = [self.randn(H) for _ in range(self.S)]
         self.y = [torch.empty(H, device=dev) for _ in range(self.S)]
@@ -157,13 +164,14 @@ class C1Cold(C1DecodeChain):
     steps (as one layer's are across decode tokens)."""
     name = "c1_cold"
     description = C1DecodeChain.description + " -- cold: inputs read from HBM"
+    hot = False
 
     def __init__(self, dev, torch):
         super().__init__(dev, torch)
         self.flush_buf = torch.empty(1 << 28, device=dev)  # 1 GiB
 
     def n_sets(self) -> int:
-        return max(64, self.steps_hint)
+        return max(64, self.steps_hint, self.min_steps)
 
     def between(self) -> None:
         self.flush_buf.fill_(1.0)
@@ -187,6 +195,7 @@ class C2PrefillChain(Workload):
         H, nq, nk, hd, I = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["inter"]
         smallest = 5 * T * H * F  # add+RMSNorm bytes: the smallest kernel footprint
         self.S = sets_for(smallest)
+        self.rotation = self.S
         self.table = self.randn(VOCAB * H, 0.02)
         S = self.S
         self.ids = [torch.randint(0, VOCAB, (T,), generator=self.gen, device=dev, dtype=torch.int32)
@@ -236,6 +245,7 @@ class C3EncoderOps(Workload):
         c = ENC_0_6B
         T, D, FF, P = 3000, c["d_model"], c["ffn"], c["pe_rows"]
         self.S = sets_for(2 * T * D * F)
+        self.rotation = self.S
         S = self.S
         self.x = [self.randn(T * D) for _ in range(S)]
         self.y = [torch.empty(T * D, device=dev) for _ in range(S)]
@@ -323,6 +333,7 @@ class C4Int8Matvec(Workload):
         self.xs = [self.randn(H) for _ in range(L)]
         self.outs = [torch.empty(I, device=dev) for _ in range(L)]
         self.L = L
+        self.rotation = L
         self.H, self.I = H, I
         layer_bytes = 2 * I * H + 2 * I * F + H * F + I * F
 
@@ -369,6 +380,7 @@ class C5BatchedDecode(Workload):
             self.layers.append(K.pack_w8a8_tiles(K.QuantWeight(q, s, 2 * I, H)))
             del q
         S = L
+        self.rotation = S
         self.x = [self.randn(B * H) for _ in range(S)]
         self.d = [self.randn(B * H) for _ in range(S)]
         self.q = [self.randn(B * nq * hd) for _ in range(S)]
@@ -446,6 +458,7 @@ class C5Layer(Workload):
                 dst.append(K.pack_w8a8_tiles(K.QuantWeight(q, s, rows, H)))
                 del q
         S = L
+        self.rotation = S
         self.x = [self.randn(B * H) for _ in range(S)]
         self.d = [self.randn(B * H) for _ in range(S)]
         self.d2 = [self.randn(B * H) for _ in range(S)]
@@ -516,6 +529,7 @@ class W8A32Decode(Workload):
 
         L = 28
         self.L = L
+        self.rotation = L
         self.w = {n: [] for n in self.SHAPES}
         for n, (o, i) in self.SHAPES.items():
             for _ in range(L):
@@ -575,6 +589,7 @@ class W8A32Prefill(Workload):
 
         L, T = 28, self.T
         self.L = L
+        self.rotation = L
         self.w = {n: [K.QuantWeight(torch.randint(-127, 128, (o * i,), generator=self.gen, device=dev,
                                                   dtype=torch.int8), self.randn(o, 1e-4, 1e-3).abs_(), o, i)
                       for _ in range(L)] for n, (o, i) in self.SHAPES.items()}
@@ -853,6 +868,7 @@ class AttnPrefill(Workload):
         T, nq, nk, hd = 512, 16, 8, 128
         per_set = (2 * T * nq * hd + 2 * T * nk * hd) * F
         self.S = sets_for(per_set)
+        self.rotation = self.S
         S = self.S
         self.q = [self.randn(T * nq * hd) for _ in range(S)]
         self.k = [self.randn(T * nk * hd) for _ in range(S)]
@@ -1328,15 +1344,51 @@ def _round(v):
     return v
 
 
+_FLUSH = {}
+
+
+def cache_flush(torch, dev):
+    """Writes 1 GiB (4x the 256 MB last-level cache) so that nothing a timed
+    replay reads afterwards is still cached."""
+    if "buf" not in _FLUSH:
+        _FLUSH["buf"] = torch.empty(FLUSH_BYTES // 4, device=dev)
+    _FLUSH["buf"].fill_(1.0)
+
+
 def measure(torch, dev, wl, K: int, W: int, use_graph: bool) -> dict:
     """Warmup, then the step and each kernel timed (median over replays of
     K launches), the roofline of the kernel moving the most bytes. A workload
     with a max_steps (a step of many milliseconds) times min(K, max_steps)
-    steps per replay."""
+    steps per replay; one with a min_steps at least that many.
+
+    Unless the workload is hot by design, a replay that touches less than
+    2x the last-level cache (its launches x their algorithmic bytes) is
+    preceded by writing 1 GiB, and a kernel's own graph holds at most as many
+    launches as it has distinct buffer sets (its rotation): every launch in a
+    replay then reads inputs that no cache holds."""
+    K = max(K, getattr(wl, "min_steps", 1))
     K = min(K, getattr(wl, "max_steps", K))
     W = min(W, getattr(wl, "max_steps", W))
     reps = replays_for(K)
-    between = getattr(wl, "between", None)
+    n_kernel = min(K, wl.rotation or K)
+
+    def flush_for(footprint):
+        if getattr(wl, "between", None) is not None:
+            return wl.between
+        if wl.hot or footprint >= ROTATE_BYTES:
+            return None
+        return lambda: cache_flush(torch, dev)
+
+    def cache_note(footprint):
+        if wl.hot:
+            return "hot by design (no flush)"
+        if getattr(wl, "between", None) is not None:
+            return "cold: the workload's own flush before each replay"
+        if footprint >= ROTATE_BYTES:
+            return f"replay streams {footprint / 1e6:.0f} MB (>= 2x the last-level cache)"
+        return f"replay touches {footprint / 1e6:.0f} MB; 1 GiB written before each replay"
+
+    between = flush_for(K * wl.step_bytes)
     for i in range(W):
         wl.step(i)
     torch.cuda.synchronize()
@@ -1352,10 +1404,13 @@ def measure(torch, dev, wl, K: int, W: int, use_graph: bool) -> dict:
     per_kernel = {}
     for kname, spec in wl.kernels.items():
         launch, nbytes = spec[0], spec[1]
-        st = time_stats(torch, launch, K, use_graph, reps, between)
+        st = time_stats(torch, launch, n_kernel, use_graph, replays_for(n_kernel), flush_for(n_kernel * nbytes))
         us = st["median"] * 1e3
         d = {"us": us, "us_p10": st["p10"] * 1e3, "us_p90": st["p90"] * 1e3, "bytes": nbytes,
-             "GB/s": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+             "GB/s": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+             "launches_per_replay": n_kernel, "replays": st["replays"],
+             "footprint_per_replay_MB": round(n_kernel * nbytes / 1e6, 1),
+             "cache": cache_note(n_kernel * nbytes)}
         if len(spec) > 2:
             d["flops"] = spec[2]
             d["TFLOP/s"] = spec[2] / (us * 1e-6) / 1e12
@@ -1363,7 +1418,8 @@ def measure(torch, dev, wl, K: int, W: int, use_graph: bool) -> dict:
         print(f"[bench] {wl.name}/{kname}: {us:.2f} us, {d['GB/s']:.0f} GB/s", file=sys.stderr, flush=True)
     value = wl.step_bytes / (ms * 1e-3) / 1e9
     return {"step": step, "use_graph": use_graph, "per_kernel": per_kernel, "value": value,
-            "tokens_per_s": wl.tokens_per_step / (ms * 1e-3), "steps": K}
+            "tokens_per_s": wl.tokens_per_step / (ms * 1e-3), "steps": K,
+            "cache": cache_note(K * wl.step_bytes)}
 
 
 def roofline_of(torch, dev, wl, m: dict, K: int) -> dict:
@@ -1424,7 +1480,7 @@ def summary(wl, m: dict, cpu) -> dict:
     out = {"workload": wl.description, **wl.config(),
            "us_per_step": round(st["median"] * 1e3, 3), "us_p10": round(st["p10"] * 1e3, 3),
            "us_p90": round(st["p90"] * 1e3, 3), "us_min": round(st["min"] * 1e3, 3), "replays": st["replays"],
-           "steps_per_replay": m["steps"],
+           "steps_per_replay": m["steps"], "cache": m["cache"],
            "algorithmic_bytes_per_step": wl.step_bytes, "GB/s": round(m["value"], 1),
            "frac_hbm": round(m["value"] / HBM_PEAK_GBS, 4), "tokens_per_s": round(m["tokens_per_s"], 1),
            "dtype": wl.dtype,
@@ -1515,7 +1571,8 @@ def main() -> int:
         "data": "synthetic (seeded torch.randn inputs, random-init weights; no checkpoints)",
         "config": {"workload": wl.description, **wl.config(),
                    "timing": (f"median over {st['replays']} replays of a hipGraph of K steps, HIP events"
-                              if m["use_graph"] else f"median over {st['replays']} eager runs of K steps")},
+                              if m["use_graph"] else f"median over {st['replays']} eager runs of K steps"),
+                   "cache": m["cache"]},
         "ms_per_step_p10": round(st["p10"], 6),
         "ms_per_step_p90": round(st["p90"], 6),
         "ms_per_step_min": round(st["min"], 6),

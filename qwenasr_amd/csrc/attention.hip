@@ -324,8 +324,13 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
   // rank is the stream itself, or with batch.order the stream of that rank
   // in longest-first order (its position comes with it: one 8-byte load), so
   // the longest walks are dispatched first and the short ones fill the tail.
+  // The stream's entry in `positions` is loaded beside it (off the critical
+  // path): an order computed for other positions (stale) makes this stream's
+  // rows and chunk partials NaN, since the merge counts chunks from
+  // `positions`.
   const int rank = BATCH ? (int)(blockIdx.x / (unsigned)nk) : 0;
   [[maybe_unused]] long long order_pos = 0;
+  [[maybe_unused]] bool stale = false;
   int i = BATCH ? rank : (int)blockIdx.x;
   if constexpr (BATCH) {
     if (batch.order) {
@@ -333,6 +338,7 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
       if ((unsigned)e.x >= gridDim.x / (unsigned)nk) return;  // not an order of this batch: nothing read
       i = e.x;
       order_pos = e.y;
+      stale = (long long)batch.positions[i] != order_pos;  // waited for where it is used
     }
   }
   const int kh = BATCH ? (int)(blockIdx.x % (unsigned)nk) : (int)blockIdx.y;
@@ -344,7 +350,18 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
     const long long p = batch.order ? order_pos : (long long)batch.positions[i];
     bad_pos = p < 0 || p >= batch.cache_rows;
     k_lim = bad_pos ? 0 : (int)p + 1;
-    if ((int)blockIdx.z * keys_per_split >= max(k_lim, 1)) return;  // uniform: a chunk with no keys
+    if ((int)blockIdx.z * keys_per_split >= max(k_lim, 1)) {  // uniform: a chunk with no keys
+      if (stale && gridDim.z > 1 && wave == 0) {  // the merge may read this chunk: make it NaN
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const size_t slot = ((size_t)i * nk * G + (size_t)kh * G + g) * gridDim.z + blockIdx.z;
+#pragma unroll
+          for (int d = 0; d < DPL; ++d) ws_o[slot * HD + lane * DPL + d] = qnan();
+          if (lane == 0) ws_ml[2 * slot] = ws_ml[2 * slot + 1] = qnan();
+        }
+      }
+      return;
+    }
     k += (size_t)i * (size_t)batch.cache_rows * kv_stride;
     v += (size_t)i * (size_t)batch.cache_rows * kv_stride;
   } else {
@@ -569,7 +586,17 @@ __global__ __launch_bounds__(256) void attention_decode_split_kernel(
 #pragma unroll
         for (int d = 0; d < DPL; ++d) acc[d] = __builtin_fmaf(co[w][g][lane * DPL + d], f, acc[d]);
       }
-      if (BATCH && k_lim <= keys_per_split) {  // the whole key range: normalise as the merge kernel does
+      if (BATCH && stale) {  // the row and (if there are chunks) this chunk's partial are NaN
+        float* orow = batch.out + ((size_t)i * nk * G + (size_t)kh * G + g) * HD;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) orow[lane * DPL + d] = qnan();
+        if (nsplit > 1) {
+          const size_t slot = ((size_t)i * nk * G + (size_t)kh * G + g) * nsplit + blockIdx.z;
+#pragma unroll
+          for (int d = 0; d < DPL; ++d) ws_o[slot * HD + lane * DPL + d] = qnan();
+          if (lane == 0) ws_ml[2 * slot] = ws_ml[2 * slot + 1] = qnan();
+        }
+      } else if (BATCH && k_lim <= keys_per_split) {  // the whole key range: normalise as the merge kernel does
         const float inv = lsum > 0.0f ? 1.0f / lsum : 1.0f;
         float* orow = batch.out + ((size_t)i * nk * G + (size_t)kh * G + g) * HD;
 #pragma unroll

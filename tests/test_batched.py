@@ -475,6 +475,47 @@ def test_batched_decode_order_and_ordered_attention(dev, B):
         assert torch.equal(aq, bq) and torch.equal(asc, bsc)
 
 
+def test_stale_order_gives_nan_rows(dev):
+    """An order computed for other positions than the call's (the positions
+    advanced after it was made): the streams whose position changed get NaN
+    rows, whether their chunk count grew, shrank or stayed; the other streams
+    equal the stream-order call bit for bit. Chunked and not, with the
+    quantized rows too."""
+    from qwenasr_amd import kernels as K
+
+    B, rows, nq, nk, hd = 7, 700, 16, 8, 128
+    kv = nk * hd
+    r = np.random.default_rng(62)
+    old = np.array([5, 100, 650, 300, 20, 511, 512], np.int32)
+    new = old.copy()
+    new[1], new[2], new[4] = 650, 50, 21  # 1 -> 2 chunks, 2 -> 1 chunk, same chunk but one more key
+    changed = new != old
+    d = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    q = d(r.standard_normal(B * nq * hd).astype(np.float32))
+    kc = d(r.standard_normal(B * rows * kv).astype(np.float32))
+    vc = d(r.standard_normal(B * rows * kv).astype(np.float32))
+    order = torch.empty(2 * B, dtype=torch.int32, device=dev)
+    K.batched_decode_order(order, d(old), B, rows)
+    pos_new = d(new)
+    for ws in (None, K.batched_decode_workspace(B, nq, hd, rows, dev)):
+        print(f"[batched] stale order, chunked={ws is not None}", flush=True)
+        ref = torch.empty(B * nq * hd, device=dev)
+        K.batched_decode_attention(ref, q, kc, vc, rows, pos_new, B, nq, nk, hd, hd ** -0.5, ws)
+        for quant in (False, True):
+            out = torch.zeros(B * nq * hd, device=dev)
+            oq = torch.empty(B * nq * hd, dtype=torch.int8, device=dev) if quant else None
+            osc = torch.empty(B, device=dev) if quant else None
+            K.batched_decode_attention(out, q, kc, vc, rows, pos_new, B, nq, nk, hd, hd ** -0.5, ws, oq, osc,
+                                       order)
+            torch.cuda.synchronize()
+            got, want = out.view(B, -1).cpu().numpy(), ref.view(B, -1).cpu().numpy()
+            for m in range(B):
+                if changed[m]:
+                    assert np.isnan(got[m]).all(), (m, ws is not None, quant)
+                else:
+                    np.testing.assert_array_equal(got[m], want[m])
+
+
 @pytest.mark.parametrize("nq,nk,hd,rows", [(16, 8, 128, 1300), (16, 8, 128, 400), (8, 8, 128, 1300),
                                            (4, 4, 64, 700)])
 def test_batched_decode_attention_quantized_rows(dev, nq, nk, hd, rows):
