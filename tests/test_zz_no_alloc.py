@@ -72,3 +72,73 @@ def test_noalloc_lm_head_rejects_what_it_cannot_hold(dev):
     rc = so.qasr_lm_head_int8_argmax_noalloc_f32(_ptr(idx), _ptr(x), _ptr(x), _ptr(w), _ptr(x), 1, 1000, 16, st)
     assert rc == _lib.QASR_ERR_UNSUPPORTED, rc
     torch.cuda.synchronize()
+
+
+_CAPTURE_SCRIPT = r'''
+import ctypes, sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+from qwenasr_amd import _lib
+
+P = lambda t: ctypes.c_void_p(t.data_ptr())
+dev = torch.device("cuda:0")
+so = _lib.lib()
+vocab, hidden = 65536, 1024
+r = np.random.default_rng(5)
+w = torch.from_numpy(r.integers(-127, 128, (vocab, hidden), dtype=np.int8)).to(dev)
+s = torch.from_numpy((1e-3 + 1e-3 * r.random(vocab)).astype(np.float32)).to(dev)
+x = torch.from_numpy(r.standard_normal(hidden).astype(np.float32)).to(dev)
+ws = torch.empty(so.qasr_lm_head_argmax_workspace_bytes(vocab) // 8 + 1, dtype=torch.float64, device=dev)
+idx_g = torch.full((1,), -7, dtype=torch.int32, device=dev)
+lg_g = torch.full((vocab,), float("nan"), device=dev)
+idx_e = torch.full((1,), -7, dtype=torch.int32, device=dev)
+lg_e = torch.full((vocab,), float("nan"), device=dev)
+torch.cuda.synchronize()
+
+def workspace_form():
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.call("qasr_lm_head_int8_argmax_f32", P(idx_e), P(lg_e), P(x), P(w), P(s), 1, hidden, vocab,
+              P(ws), ws.numel() * 8, st)
+
+print("[no_alloc capture] first no-alloc call of the process, inside graph capture", flush=True)
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.call("qasr_lm_head_int8_argmax_noalloc_f32", P(idx_g), P(lg_g), P(x), P(w), P(s), 1, hidden,
+              vocab, st)
+torch.cuda.synchronize()
+for replay in range(3):
+    if replay:
+        x.copy_(torch.from_numpy(r.standard_normal(hidden).astype(np.float32)).to(dev))  # eager work
+        idx_g.fill_(-7)
+        lg_g.fill_(float("nan"))
+    torch.cuda.synchronize()
+    print(f"[no_alloc capture] replay {replay}", flush=True)
+    g.replay()
+    torch.cuda.synchronize()
+    workspace_form()
+    torch.cuda.synchronize()
+    assert torch.equal(lg_g, lg_e), f"replay {replay}: logits differ"
+    assert int(idx_g.item()) == int(idx_e.item()), f"replay {replay}: {idx_g.item()} != {idx_e.item()}"
+    assert 0 <= int(idx_g.item()) < vocab
+print("[no_alloc capture] ok", flush=True)
+'''
+
+
+def test_noalloc_first_call_under_graph_capture_in_a_fresh_process(dev):
+    """The scratch address lookup happens on a device's first call. Made for the
+    first time inside a graph capture, in a process that has not called the
+    entry point before, the captured kernels must still equal the workspace
+    form on every replay (three replays, new inputs written eagerly between
+    them)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, str(root)], capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "[no_alloc capture] ok" in r.stdout
