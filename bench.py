@@ -1332,6 +1332,78 @@ def profile_kernel(torch, wl, name: str, n: int) -> int:
     return 0
 
 
+PROBE_MODES = {0: "one region per XCD, all its workgroups in the same order",
+               1: "one region per XCD, each workgroup from its own rotation",
+               2: "private 64 KiB per workgroup, L2-resident",
+               3: "private region per workgroup read once (HBM stream)",
+               4: "as 2, wave pairs w, w+4 on the same addresses",
+               5: "as 3, wave pairs w, w+4 on the same addresses"}
+PROBE_BUF = 1 << 30
+PROBE_PRIV = 64 << 10
+
+
+def _probe_launch(torch, buf, out, mode, depth, grid, per_wg, i):
+    from qwenasr_amd import _lib
+
+    shift = i % 4 if mode in (3, 5) else 0
+    _lib.call("qasr_probe_read", mode, depth, grid, buf.data_ptr(), buf.numel(), out.data_ptr(), out.numel(),
+              per_wg, PROBE_PRIV, shift, torch.cuda.current_stream().cuda_stream)
+
+
+def probe_fill(torch, dev, one=None) -> int:
+    """The read-rate probe (qasr_probe_read): per mode, workgroups of 512
+    threads read 256 KiB, 512 KiB and 1 MiB per CU (256 or 512 workgroups);
+    the marginal per-CU rate between 512 KiB and 1 MiB removes the launch and
+    ramp. With ``one`` = (mode, depth, grid, KiB per workgroup): 20 eager
+    launches of that case alone, for counter passes."""
+    import numpy as np
+
+    buf = torch.randint(-128, 127, (PROBE_BUF,), dtype=torch.int8, device=dev)
+    out = torch.empty(4096 * 512, dtype=torch.int32, device=dev)
+    if one is not None:
+        mode, depth, grid, kib = one
+        for i in range(20):
+            _probe_launch(torch, buf, out, mode, depth, grid, kib << 10, i)
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": one, "launches": 20}), flush=True)
+        return 0
+    rows = []
+    for grid in (256, 512):
+        for mode in PROBE_MODES:
+            for depth in (4, 16):
+                us = []
+                per_cu = (256 << 10, 512 << 10, 1 << 20)
+                for pc in per_cu:
+                    per_wg = pc * 256 // grid
+                    g = torch.cuda.CUDAGraph()
+                    _probe_launch(torch, buf, out, mode, depth, grid, per_wg, 0)
+                    with torch.cuda.graph(g):
+                        for i in range(20):
+                            _probe_launch(torch, buf, out, mode, depth, grid, per_wg, i)
+                    g.replay()
+                    torch.cuda.synchronize()
+                    t = []
+                    for _ in range(7):
+                        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        s0.record()
+                        g.replay()
+                        e0.record()
+                        torch.cuda.synchronize()
+                        t.append(s0.elapsed_time(e0) * 1e3 / 20)
+                    us.append(float(np.median(t)))
+                    del g
+                marginal = (per_cu[2] - per_cu[1]) / ((us[2] - us[1]) * 1e-6) / 1e9
+                row = {"grid": grid, "mode": mode, "what": PROBE_MODES[mode], "depth": depth,
+                       "per_cu_KiB": [x >> 10 for x in per_cu], "us": [round(x, 2) for x in us],
+                       "TB/s": [round(256 * pc / (u * 1e-6) / 1e12, 2) for pc, u in zip(per_cu, us)],
+                       "marginal_per_cu_GB/s": round(marginal, 1)}
+                rows.append(row)
+                print(f"[probe] grid {grid} mode {mode} depth {depth}: us {row['us']} marginal per CU "
+                      f"{row['marginal_per_cu_GB/s']} GB/s", file=sys.stderr, flush=True)
+    print(json.dumps({"probe": "qasr_probe_read", "rows": rows}), flush=True)
+    return 0
+
+
 # ---------------------------------------------------------------------------
 DEFAULT_CONFIGS = "c1,c1_cold,c2,c3_fused,c4,c5_b32,c5_layer,decode_step,decode_step_b256,decode_step_b256_w8a8,prefill_step"
 
@@ -1517,6 +1589,10 @@ def main() -> int:
                     help="for counter runs under rocprofv3: launch only this kernel of the workload "
                          "--steps times (rotating buffers), eagerly, and print what ran; NAME 'copy' "
                          "launches a plain 64 MiB device-to-device copy instead (the counter calibration)")
+    ap.add_argument("--probe", action="store_true",
+                    help="run the per-CU read-rate probe (qasr_probe_read) and print its table")
+    ap.add_argument("--probe-one", metavar="MODE,DEPTH,GRID,KIB",
+                    help="for counter runs: 20 launches of one probe case (KiB read per workgroup)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -1540,6 +1616,9 @@ def main() -> int:
 
     if args.profile_kernel == "copy":
         return profile_copy(torch, dev, K)
+    if args.probe or args.probe_one:
+        one = tuple(int(v) for v in args.probe_one.split(",")) if args.probe_one else None
+        return probe_fill(torch, dev, one)
     wl = WORKLOADS[args.workload](dev, torch)
     torch.cuda.synchronize()
     if args.profile_kernel:

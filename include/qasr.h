@@ -647,6 +647,23 @@ int qasr_qint8_upload_gate_up(const qasr_qint8_file* f, const char* gate_name,
                               const char* up_name, size_t inter, size_t hidden,
                               int8_t* dev_w, float* dev_scales, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Measurement aid                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* No counterpart in the reference: a read-only probe of how fast one CU pulls
+ * bytes in (bench.py --probe). `grid` workgroups of 512 threads each read
+ * bytes_per_wg bytes of buf with 16-byte loads, `depth` (4, 8 or 16) in flight
+ * per thread, and write one int per thread to out (grid * 512 ints). mode 0:
+ * one region per XCD read by all its workgroups in the same order; 1: as 0 from
+ * a per-workgroup rotation; 2: a private priv_bytes region per workgroup read
+ * repeatedly (L2-resident); 3: a private region read once at offset
+ * shift * grid * bytes_per_wg (HBM stream); 4 / 5: as 2 / 3 with waves w and
+ * w + 4 reading the same addresses. bytes_per_wg must be a multiple of
+ * 8192 * depth; every region is checked against buf_bytes on the host. */
+int qasr_probe_read(int mode, int depth, unsigned grid, const void* buf, size_t buf_bytes, int* out,
+                    size_t out_ints, size_t bytes_per_wg, size_t priv_bytes, size_t shift, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

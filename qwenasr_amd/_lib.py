@@ -54,6 +54,7 @@ SIGNATURES: dict[str, list] = {
     "qasr_decode_attention_f32": [P, P, P, P, P, P, P, P, Z, Z, Z, Z, Z, F, F, P, P, Z, P, Z, P],
     "qasr_lm_head_int8_argmax_f32": [P, P, P, P, P, Z, Z, Z, P, Z, P],
     "qasr_lm_head_int8_argmax_noalloc_f32": [P, P, P, P, P, Z, Z, Z, P],
+    "qasr_probe_read": [c_int, c_int, ctypes.c_uint, P, Z, P, Z, Z, Z, Z, P],
     "qasr_head_rms_norm_rope_kv_f32": [P, P, P, P, P, P, P, P, Z, Z, Z, Z, Z, Z, F, P, P, Z, P],
     "qasr_rope_table_fill_f32": [P, P, Z, Z, Z, F, P],
     "qasr_swiglu_multiply_f32": [P, P, Z, Z, P],

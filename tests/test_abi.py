@@ -375,3 +375,30 @@ def test_traffic_profile_names_current_kernels():
                 if kname.replace(" ", "") not in have:
                     stale.append(f"{workload}/{label}: {kname}")
     assert not stale, f"kernels in profiles/traffic.json not in the library: {stale}"
+
+
+def test_probe_read_validation():
+    """The read-rate probe checks every region it would read against buf_bytes
+    (and its other arguments) on the host, before any launch."""
+    so = _lib.lib()
+    inv = _lib.QASR_ERR_INVALID_ARG
+    kb = 1024
+    args = dict(mode=2, depth=16, grid=256, buf=FAKE, buf_bytes=256 * 64 * kb, out=FAKE, out_ints=256 * 512,
+                per_wg=512 * kb, priv=64 * kb, shift=0)
+
+    def call(**over):
+        a = {**args, **over}
+        return so.qasr_probe_read(a["mode"], a["depth"], a["grid"], a["buf"], a["buf_bytes"], a["out"],
+                                  a["out_ints"], a["per_wg"], a["priv"], a["shift"], NULL)
+
+    assert call(buf=NULL) == inv
+    assert call(mode=6) == inv
+    assert call(depth=3) == inv
+    assert call(grid=0) == inv and call(grid=5000) == inv
+    assert call(per_wg=512 * kb + 8192) == inv          # not a multiple of 8192 * depth
+    assert call(out_ints=256 * 512 - 1) == inv
+    assert call(buf_bytes=256 * 64 * kb - 16) == inv    # the private regions do not fit
+    assert call(mode=3, buf_bytes=256 * 512 * kb * 2, shift=2) == inv  # (shift + 1) * grid * per_wg
+    assert call(mode=0, buf_bytes=8 * 512 * kb - 1) == inv
+    assert call(priv=4096) == inv
+    assert b"probe_read" in so.qasr_last_error()
