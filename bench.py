@@ -734,10 +734,14 @@ class DecodeStepBatched(Workload):
 class DecodeStepBatchedW8A8(DecodeStepBatched):
     """decode_step_b256 with the projections on int8 matrix cores (each
     stream's activation rows quantized per row at the four projection inputs,
-    as the c5 gate/up does)."""
+    as the c5 gate/up does) and the lm_head W8A8 as well: a fifth rounding
+    point before the greedy argmax, which the reference (W8A32 lm_head,
+    decoder.rs:929-963) does not have."""
     name = "decode_step_b256_w8a8"
-    description = DecodeStepBatched.description.replace("W8A32 matrix-core projections",
-                                                        "W8A8 int8-MFMA projections")
+    description = (DecodeStepBatched.description.replace("W8A32 matrix-core projections",
+                                                         "W8A8 int8-MFMA projections")
+                   + "; the lm_head is W8A8 too (final norm rows quantized per row), so its greedy "
+                     "tokens are not the reference's W8A32 ones")
     dtype = "int8/int32->f32"
     w8a8 = True
 
