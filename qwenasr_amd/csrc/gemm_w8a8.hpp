@@ -380,13 +380,15 @@ __global__ __launch_bounds__(256) void pack_w8a8_tiles_kernel(int8_t* __restrict
 // issue v_mfma_i32_16x16x64_i8 back to back at full rate, two interleaved
 // waves can.
 //
-// Xq is staged in LDS in 32 KiB chunks of [64 rows][512 bytes]; the 16-byte
-// slot p of a row holds the row's logical slot p ^ (row & 15), so the b128
-// fragment reads of 16 rows at one k offset hit 16 distinct bank groups. Each
-// wave loads its share of the first chunk of both K halves into registers and
-// writes it to LDS before the loop; the second chunks (K = 2048) arrive in
-// registers during the first k-steps and are written at step 3, read from
-// step 8. Plain loads are used rather than the direct global->LDS form: the
+// Xq is staged in LDS in 16 KiB chunks of [64 rows][256 bytes] (4 k-steps);
+// the 16-byte slot p of a row holds the row's logical slot p ^ (row & 15), so
+// the b128 fragment reads of 16 rows at one k offset hit 16 distinct bank
+// groups. Every chunk is loaded into registers in the prologue, the first
+// chunk of each K half first; those two are written to LDS before the loop,
+// so the first MFMA waits for 32 KiB of Xq instead of all of it, and chunk
+// c + 1 of each half is written at step 4c + 1 and first read at step 4c + 4
+// (a barrier at step 4c + 3). 256-byte chunks measured 0.2-0.4 us faster than
+// 512-byte ones (bit-identical: int32 sums are exact in any order). Plain loads are used rather than the direct global->LDS form: the
 // compiler cannot tell which LDS bytes a pending direct load writes, so it
 // drains every outstanding load (the whole W window) at the first LDS read;
 // with register staging its per-load waits stay exact. The workgroup barriers
@@ -405,25 +407,25 @@ __global__ __launch_bounds__(256) void pack_w8a8_tiles_kernel(int8_t* __restrict
 constexpr int kPkBN = 192;       // W rows per workgroup
 constexpr int kPkBM = 64;        // tokens per workgroup
 constexpr int kPkWaves = 8;      // 4 row groups x 2 K halves
-constexpr int kPkChunk = 512;    // bytes of K per staged X chunk
+constexpr int kPkChunk = 256;    // bytes of K per staged X chunk
 constexpr int kPkPrefetch = 3;   // k-steps of W in flight per wave
 constexpr size_t kPkLds = 131072;
 
 
-// Wave `wave`'s share of X chunk c: 4 rows-pairs t, each lane one 16-byte slot.
+// Wave `wave`'s share of X chunk c: 2 four-row groups t, each lane one 16-byte slot.
 // Rows past the batch re-read row batch - 1 (valid memory); their results are
 // never stored.
 template <int K>
 QASR_DEV const v4i* x_chunk_src(const int8_t* __restrict__ xq, int c, int t, int wave, int lane,
                                 int m0, int batch) {
-  const int d = wave * 4 + t;
-  const int row = 2 * d + (lane >> 5);
-  const int slot = (lane & 31) ^ (row & 15);
+  const int d = wave * 2 + t;          // 4-row group: rows 4d .. 4d+3, 16 slots each
+  const int row = 4 * d + (lane >> 4);
+  const int slot = (lane & 15) ^ (row & 15);
   const int src_row = m0 + row < batch ? m0 + row : batch - 1;
   return reinterpret_cast<const v4i*>(xq + (size_t)src_row * K + kPkChunk * c + 16 * slot);
 }
 QASR_DEV v4i* x_chunk_dst(int8_t* lds, int c, int t, int wave, int lane) {
-  return reinterpret_cast<v4i*>(lds + c * 32768 + (wave * 4 + t) * 1024 + 16 * lane);
+  return reinterpret_cast<v4i*>(lds + c * 16384 + (wave * 2 + t) * 1024 + 16 * lane);
 }
 
 template <int KS, bool VEC_OUT>  // KS = K / 64 (16 or 32)
@@ -433,10 +435,10 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
     int n_tiles, int m_tiles) {
   constexpr int K = KS * kPackK;
   constexpr int KW = KS / 2;                // k-steps per wave
-  constexpr int NCH = K / kPkChunk;         // X chunks (2 or 4)
+  constexpr int NCH = K / kPkChunk;         // X chunks (4 or 8)
   constexpr int CH_HALF = NCH / 2;          // chunks per K half
   constexpr int PF = kPkPrefetch;
-  static_assert(kPkWaves * 4 * 2 == 64, "a chunk is 64 rows: 8 waves x 4 row pairs");
+  static_assert(kPkWaves * 2 * 4 == 64, "a chunk is 64 rows: 8 waves x 2 four-row groups");
   extern __shared__ __align__(16) int8_t lds[];
 
   const int lane = threadIdx.x & 63;
@@ -462,11 +464,11 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
 
   // Issue order: first X chunks, W window, epilogue operands, second X
   // chunks; sched_barriers keep it (loads complete in issue order).
-  v4i xa[8], xb[8];
+  v4i xa[4], xr[CH_HALF > 1 ? (CH_HALF - 1) * 4 : 1];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < 2; ++t) {
     xa[t] = *x_chunk_src<K>(xq, 0, t, wave, lane, m0, batch);
-    xa[4 + t] = *x_chunk_src<K>(xq, CH_HALF, t, wave, lane, m0, batch);
+    xa[2 + t] = *x_chunk_src<K>(xq, CH_HALF, t, wave, lane, m0, batch);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -491,16 +493,18 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (CH_HALF > 1) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      xb[t] = *x_chunk_src<K>(xq, 1, t, wave, lane, m0, batch);
-      xb[4 + t] = *x_chunk_src<K>(xq, CH_HALF + 1, t, wave, lane, m0, batch);
-    }
+    for (int c = 1; c < CH_HALF; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        xr[(c - 1) * 4 + t] = *x_chunk_src<K>(xq, c, t, wave, lane, m0, batch);
+        xr[(c - 1) * 4 + 2 + t] = *x_chunk_src<K>(xq, CH_HALF + c, t, wave, lane, m0, batch);
+      }
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < 2; ++t) {
     *x_chunk_dst(lds, 0, t, wave, lane) = xa[t];
-    *x_chunk_dst(lds, CH_HALF, t, wave, lane) = xa[4 + t];
+    *x_chunk_dst(lds, CH_HALF, t, wave, lane) = xa[2 + t];
   }
   lds_barrier();
 
@@ -512,9 +516,9 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
 
   // B fragment of token tile j at global k-step s
   auto xfrag = [&](int s, int j) -> v4i {
-    const int c = s >> 3;
-    const int slot = 4 * (s & 7) + g;
-    return *reinterpret_cast<const v4i*>(lds + c * 32768 + (16 * j + r) * kPkChunk + 16 * (slot ^ r));
+    const int c = s >> 2;
+    const int slot = 4 * (s & 3) + g;
+    return *reinterpret_cast<const v4i*>(lds + c * 16384 + (16 * j + r) * kPkChunk + 16 * (slot ^ r));
   };
   v4i bcur[4];
 #pragma unroll
@@ -526,16 +530,21 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
     for (int d = 0; d < PF; ++d) {
       const int s = s0 + d;
       if (s < KW) {
-        if (CH_HALF > 1 && s == 3) {  // second chunks into LDS
+        if (CH_HALF > 1 && (s & 3) == 1 && (s >> 2) + 1 < CH_HALF) {  // the next chunk of each half into LDS
+          const int c = (s >> 2) + 1;
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            *x_chunk_dst(lds, 1, t, wave, lane) = xb[t];
-            *x_chunk_dst(lds, CH_HALF + 1, t, wave, lane) = xb[4 + t];
-          }
+          for (int cc = 1; cc < CH_HALF; ++cc)
+            if (cc == c) {
+#pragma unroll
+              for (int t = 0; t < 2; ++t) {
+                *x_chunk_dst(lds, cc, t, wave, lane) = xr[(cc - 1) * 4 + t];
+                *x_chunk_dst(lds, CH_HALF + cc, t, wave, lane) = xr[(cc - 1) * 4 + 2 + t];
+              }
+            }
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (CH_HALF > 1 && s == 7) {  // step 8 reads them (B fragments are loaded one step ahead)
+        if (CH_HALF > 1 && (s & 3) == 3 && (s >> 2) + 1 < CH_HALF) {  // step s+1 reads the next chunk
           __builtin_amdgcn_sched_barrier(0);
           lds_barrier();
           __builtin_amdgcn_sched_barrier(0);
