@@ -661,7 +661,9 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
 // are int32 partial sums over its K slice, and the 8 partials of each
 // accumulator tile are added in LDS (exact) by the wave that runs that tile's
 // SwiGLU epilogue -- the same epilogue, so the outputs equal the 192-row
-// kernel's bit for bit.
+// kernel's bit for bit. The epilogue's token and row scales are loaded with
+// the operands, not after the partial-sum barrier (a dependent memory round
+// trip on the tail: B=32 9.27 -> 8.87 us).
 // ---------------------------------------------------------------------------
 constexpr int kSbRows = 48;
 constexpr int kSbWaves = 8;
@@ -698,6 +700,17 @@ __global__ __launch_bounds__(64 * kSbWaves) void gemm_w8a8_swiglu_small_kernel(
       if (16 * j < batch)
         xv[s][j] = *reinterpret_cast<const v4i*>(xq + (size_t)row * K + kPackK * (s0 + s) + 16 * g);
     }
+  // the epilogue's scales for this wave's tiles (wave and wave + 8), loaded with the operands
+  float ep_xs[2];
+  float4 ep_sc[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int t = wave + kSbWaves * e;
+    const int i = (t < 12 ? t : 0) >> 2, j = (t < 12 ? t : 0) & 3;
+    const int m = 16 * j + r;
+    ep_xs[e] = xs[m < batch ? m : batch - 1];
+    ep_sc[e] = *reinterpret_cast<const float4*>(scales + n0 + 16 * i + 4 * g);
+  }
   __builtin_amdgcn_sched_barrier(0);
   v4i acc[3][4];
 #pragma unroll
@@ -722,7 +735,10 @@ __global__ __launch_bounds__(64 * kSbWaves) void gemm_w8a8_swiglu_small_kernel(
   __syncthreads();
   // wave w finishes accumulator tiles w and w + 8: lane holds W rows
   // n0 + 16i + 4g + {0..3} (two gate/up pairs) for token 16j + r
-  for (int t = wave; t < 12; t += kSbWaves) {
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int t = wave + kSbWaves * e;
+    if (t >= 12) break;
     const int i = t >> 2, j = t & 3;
     if (16 * j >= batch) continue;
     v4i sum = part[t * 64 + lane];
@@ -730,9 +746,9 @@ __global__ __launch_bounds__(64 * kSbWaves) void gemm_w8a8_swiglu_small_kernel(
     for (int u = 1; u < kSbWaves; ++u) sum += part[(u * 12 + t) * 64 + lane];
     const int m = 16 * j + r;
     if (m < batch) {
-      const float xsv = xs[m];
+      const float xsv = ep_xs[e];
       const int n = n0 + 16 * i + 4 * g;
-      const float4 sc = *reinterpret_cast<const float4*>(scales + n);
+      const float4 sc = ep_sc[e];
       float2 o;
       o.x = swiglu_w8a8(sum[0], sum[1], xsv, sc.x, sc.y);
       o.y = swiglu_w8a8(sum[2], sum[3], xsv, sc.z, sc.w);
