@@ -165,6 +165,11 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
       if (rn.delta) nd[i] = ld4(rn.delta, c);
     }
   }
+  // the epilogue's row scale (and bias) of lane r < R, loaded with the
+  // inputs: after the dot products it would be one more memory round trip
+  const int o_ep = min(o0 + (lane < R ? lane : 0), out_dim - 1);
+  const float sc_ep = scales[o_ep];
+  const float bias_ep = bias ? bias[o_ep] : 0.0f;
   v4i wv[R][KCH];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -253,8 +258,8 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
     for (int r = 1; r < R; ++r)
       if (lane == r) a = acc[r];
     const int o = o0 + lane;
-    res = a * scales[o];
-    if (bias) res += bias[o];
+    res = a * sc_ep;
+    if (bias) res += bias_ep;
     if constexpr (EPI != kEpiSwiglu) y[o] = res;
   }
   if constexpr (EPI == kEpiSwiglu) {
@@ -533,6 +538,10 @@ __global__ __launch_bounds__(256) void gateup_matvec_kernel(float* out, const in
     for (int c = 0; c < KCH; ++c) xq[c] = reinterpret_cast<const v4i*>(xq8)[c * kWave + lane];
     xs = xsc[0];
   }
+  // the epilogue's gate/up scales of lane p < NP, loaded with the activations
+  // (after the dot products they would be one more memory round trip)
+  const int j_ep = min(pair0 + (lane < NP ? lane : 0), inter - 1);
+  const float2 sc_ep = make_float2(scales[2 * j_ep], scales[2 * j_ep + 1]);
 
   // Then the weight stream: NP pairs x 2 rows x KCH slices, all in flight.
   v4i wv[NP][2][KCH];
@@ -569,7 +578,7 @@ __global__ __launch_bounds__(256) void gateup_matvec_kernel(float* out, const in
     for (int p = 1; p < NP; ++p)
       if (lane == p) { dg = acc[p][0]; du = acc[p][1]; }
     const int j = pair0 + lane;
-    out[j] = swiglu_w8a8(dg, du, xs, scales[2 * j], scales[2 * j + 1]);
+    out[j] = swiglu_w8a8(dg, du, xs, sc_ep.x, sc_ep.y);
   }
 }
 
