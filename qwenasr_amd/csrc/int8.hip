@@ -807,6 +807,28 @@ QASR_DEV void gemm_heads_epilogue(const v16f (&acc)[MI][MJ], float* tile, int ma
   }
 }
 
+// Row scales (and biases) of a wave's 32 MI rows r0 .. r0 + 32 MI - 1, loaded
+// before the k loop so that the epilogue does not wait on memory after it.
+// Lane l, register k holds row r0 + 64k + l (clamped to the last row past the
+// end); the accumulator element for row offset 32i + 8q + 4g + v is read from
+// lane (32i + 8q + 4g + v) % 64, register i / 2, with a cross-lane permute.
+template <int MI, bool BIAS>
+struct GemmEpiRows {
+  static constexpr int R = (32 * MI + 63) / 64;
+  float s[R];
+  float b[R];
+  QASR_DEV void load(const float* scales, const float* bias, int N, int r0, int lane) {
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int nv = min(r0 + 64 * k + lane, N - 1);
+      s[k] = scales[nv];
+      if constexpr (BIAS) b[k] = bias[nv];
+    }
+  }
+  QASR_DEV float scale(int i, int off) const { return __shfl(s[i >> 1], 32 * (i & 1) + off, kWave); }
+  QASR_DEV float shift(int i, int off) const { return __shfl(b[i >> 1], 32 * (i & 1) + off, kWave); }
+};
+
 template <int BN, int BT, int BK, int NPF, int EPI>
 __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, TileMap map,
                                                                 const float* __restrict__ x, int T, int K,
@@ -851,6 +873,8 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < MJ; ++j) acc[i][j] = v16f{};
+  [[maybe_unused]] GemmEpiRows<MI, EPI == kGemmBias> ep;
+  if constexpr (EPI != kGemmHeads) ep.load(scales, bias, N, n0 + (BN / 2) * wr, lane);
 
   // rows and tokens past the end re-read the last one (valid memory; not stored)
   // Staging items: weight item c is 16 bytes of row 64c + tid / 4 at byte
@@ -952,27 +976,29 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
 #pragma unroll
   for (int j = 0; j < MJ; ++j) {
     const int t = t0 + (BT / 2) * wc + 32 * j + r;
-    if (t >= T) continue;
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + (BN / 2) * wr + 32 * i + 8 * q + 4 * g;
         float res[4];
+        // the cross-lane reads run with every lane active (an inactive source
+        // lane reads as 0); lanes past the last token only skip the stores
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int nv = min(n + v, N - 1);
-          res[v] = acc[i][j][4 * q + v] * scales[nv];
-          if constexpr (EPI == kGemmBias) res[v] += bias[nv];
+          res[v] = acc[i][j][4 * q + v] * ep.scale(i, 8 * q + 4 * g + v);
+          if constexpr (EPI == kGemmBias) res[v] += ep.shift(i, 8 * q + 4 * g + v);
         }
-        if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
-          swiglu_store<EPI>(y, res, t, n, N);
-        } else if (vec_out && n + 3 < N) {
-          *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
-        } else {
+        if (t < T) {
+          if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
+            swiglu_store<EPI>(y, res, t, n, N);
+          } else if (vec_out && n + 3 < N) {
+            *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
+          } else {
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+            for (int v = 0; v < 4; ++v)
+              if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+          }
         }
       }
   }
@@ -1034,6 +1060,8 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < MJ; ++j) acc[i][j] = v16f{};
+  [[maybe_unused]] GemmEpiRows<MI, EPI == kGemmBias> ep;
+  if constexpr (EPI != kGemmHeads) ep.load(scales, bias, N, n0 + (BN / 2) * wr, lane);
 
   // rows and tokens past the end re-read the last one (valid memory; not stored)
   // staging items as in the single-buffered kernel (16 or 8 lines per load instruction)
@@ -1159,27 +1187,29 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
 #pragma unroll
   for (int j = 0; j < MJ; ++j) {
     const int t = t0 + (BT / 2) * wc + 32 * j + r;
-    if (t >= T) continue;
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + (BN / 2) * wr + 32 * i + 8 * q + 4 * g;
         float res[4];
+        // the cross-lane reads run with every lane active (an inactive source
+        // lane reads as 0); lanes past the last token only skip the stores
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int nv = min(n + v, N - 1);
-          res[v] = acc[i][j][4 * q + v] * scales[nv];
-          if constexpr (EPI == kGemmBias) res[v] += bias[nv];
+          res[v] = acc[i][j][4 * q + v] * ep.scale(i, 8 * q + 4 * g + v);
+          if constexpr (EPI == kGemmBias) res[v] += ep.shift(i, 8 * q + 4 * g + v);
         }
-        if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
-          swiglu_store<EPI>(y, res, t, n, N);
-        } else if (vec_out && n + 3 < N) {
-          *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
-        } else {
+        if (t < T) {
+          if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
+            swiglu_store<EPI>(y, res, t, n, N);
+          } else if (vec_out && n + 3 < N) {
+            *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
+          } else {
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+            for (int v = 0; v < 4; ++v)
+              if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+          }
         }
       }
   }
@@ -1238,6 +1268,22 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
                                   const float* scales, const float* bias, int N, int T, int n0, int t0) {
   const int r = lane & 31, g = lane >> 5;
   constexpr int PER_WAVE = MI * MJ * 16 * 64;  // floats
+  // Wave w reduces and stores the (block, register quad) items w, w + KW, ...
+  // Their row scales (and biases) are loaded before the partial tiles go
+  // through LDS, so that exchange hides their latency.
+  constexpr int ITEMS = (MI * MJ * 4 + KW - 1) / KW;
+  float es[ITEMS][4], eb[ITEMS][4];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int p = min(wave + KW * it, MI * MJ * 4 - 1);
+    const int n = n0 + 32 * ((p >> 2) / MJ) + 8 * (p & 3) + 4 * g;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int nv = min(n + v, N - 1);
+      es[it][v] = scales[nv];
+      eb[it][v] = EPI == kGemmBias ? bias[nv] : 0.0f;
+    }
+  }
   float* mine = red + (size_t)wave * PER_WAVE;
 #pragma unroll
   for (int i = 0; i < MI; ++i)
@@ -1247,31 +1293,35 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
       for (int e = 0; e < 16; ++e) mine[((i * MJ + j) * 16 + e) * 64 + lane] = acc[i][j][e];
   __syncthreads();
   const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
-  for (int p = wave; p < MI * MJ * 4; p += KW) {  // (block, register quad) items
-    const int blk = p >> 2, q = p & 3;
-    const int i = blk / MJ, j = blk % MJ;
-    const int t = t0 + 32 * j + r;
-    const int n = n0 + 32 * i + 8 * q + 4 * g;
-    float res[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int e = (blk * 16 + 4 * q + v) * 64 + lane;
-      float sum = red[e];
+  for (int it = 0; it < ITEMS; ++it) {
+    const int p = wave + KW * it;
+    if (p < MI * MJ * 4) {
+      const int blk = p >> 2, q = p & 3;
+      const int i = blk / MJ, j = blk % MJ;
+      const int t = t0 + 32 * j + r;
+      const int n = n0 + 32 * i + 8 * q + 4 * g;
+      float res[4];
 #pragma unroll
-      for (int ww = 1; ww < KW; ++ww) sum += red[(size_t)ww * PER_WAVE + e];
-      const int nv = min(n + v, N - 1);
-      res[v] = sum * scales[nv];
-      if constexpr (EPI == kGemmBias) res[v] += bias[nv];
-    }
-    if (t >= T) continue;
-    if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
-      swiglu_store<EPI>(y, res, t, n, N);
-    } else if (vec_out && n + 3 < N) {
-      *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
-    } else {
+      for (int v = 0; v < 4; ++v) {
+        const int e = (blk * 16 + 4 * q + v) * 64 + lane;
+        float sum = red[e];
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+        for (int ww = 1; ww < KW; ++ww) sum += red[(size_t)ww * PER_WAVE + e];
+        res[v] = sum * es[it][v];
+        if constexpr (EPI == kGemmBias) res[v] += eb[it][v];
+      }
+      if (t < T) {
+        if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
+          swiglu_store<EPI>(y, res, t, n, N);
+        } else if (vec_out && n + 3 < N) {
+          *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+        }
+      }
     }
   }
 }
