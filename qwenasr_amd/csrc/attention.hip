@@ -885,33 +885,44 @@ __global__ __launch_bounds__(64 * NW) void attention_prefill_mfma_kernel(
       sum += __shfl_xor(sum, 32, 64);
       l_run = __builtin_fmaf(l_run, corr, sum);
       m_run = m_new;
-      // the O rows of this lane are columns 4hi + r: their corrections
+      // The tile's P V goes into a zeroed accumulator and is added to the
+      // corrected running O after the tile (O = O corr + P V per column; O =
+      // P V on the wave's first tile), so the matrix-core chain never waits
+      // on the VALU correction of registers it is accumulating into.
+      v4f ot[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float c = __shfl(corr, 4 * hi + r, 64);
-#pragma unroll
-        for (int jt = 0; jt < 8; ++jt) o[jt][r] *= c;
-      }
+      for (int jt = 0; jt < 8; ++jt) ot[jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
       // next tile's first two key blocks while PV runs
       const int tn = t + NW < ntiles ? t + NW : t;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int jt = 0; jt < 8; ++jt) o[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[0][r], va[8 * r + jt], o[jt], 0, 0, 0);
+        for (int jt = 0; jt < 8; ++jt) ot[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[0][r], va[8 * r + jt], ot[jt], 0, 0, 0);
       ld_row32(ka, kbase + (size_t)min(tn * 64 + lo, last_key) * kv_stride);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int jt = 0; jt < 8; ++jt) o[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[1][r], vb[8 * r + jt], o[jt], 0, 0, 0);
+        for (int jt = 0; jt < 8; ++jt) ot[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[1][r], vb[8 * r + jt], ot[jt], 0, 0, 0);
       ld_row32(kb1, kbase + (size_t)min(tn * 64 + 16 + lo, last_key) * kv_stride);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int jt = 0; jt < 8; ++jt) o[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[2][r], vc[8 * r + jt], o[jt], 0, 0, 0);
+        for (int jt = 0; jt < 8; ++jt) ot[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[2][r], vc[8 * r + jt], ot[jt], 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int jt = 0; jt < 8; ++jt) o[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[3][r], vd[8 * r + jt], o[jt], 0, 0, 0);
+        for (int jt = 0; jt < 8; ++jt) ot[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[3][r], vd[8 * r + jt], ot[jt], 0, 0, 0);
+      if (t == w) {
+#pragma unroll
+        for (int jt = 0; jt < 8; ++jt) o[jt] = ot[jt];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float c = __shfl(corr, 4 * hi + r, 64);
+#pragma unroll
+          for (int jt = 0; jt < 8; ++jt) o[jt][r] = __builtin_fmaf(o[jt][r], c, ot[jt][r]);
+        }
+      }
     }
   }
 
