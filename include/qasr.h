@@ -312,6 +312,57 @@ int qasr_qkv_heads_int8_f32(float* q, float* k_cache, float* v_cache, size_t cac
                             const float* sin_tab, size_t table_rows, size_t start_pos, float eps,
                             void* stream);
 
+/* The prefill residual add folded into the o / down projection:
+ * h[t, :] += linear_nobias_int8(x[t, :], w, scales) for t < seq_len, and
+ * ss[t * ceil(out_dim / 64) + s] = the sum of squares of h[t, 64s .. 64s+63]
+ * after the add; with hg (and gain, [out_dim]), also hg[t, n] = h[t, n] *
+ * gain[n] -- the statistics and the gain-scaled rows the next RMSNorm needs
+ * (the two qasr_rms_norm_* entry points below). Replaces linear_nobias_int8 +
+ * add_inplace (decoder.rs:821-822, 837-838; kernels/mod.rs:486-488): h equals
+ * them bit for bit. ss holds seq_len * ceil(out_dim / 64) floats; x must not
+ * overlap h or hg; hg and gain are both NULL or both given. seq_len >= 8,
+ * in_dim % 64 == 0 and 16-byte aligned h, hg, x, w (QASR_ERR_UNSUPPORTED
+ * otherwise). No reference counterpart as one call. */
+int qasr_linear_int8_residual_f32(float* h, float* ss, float* hg, const float* gain, const float* x,
+                                  const int8_t* w, const float* scales, size_t seq_len, size_t in_dim,
+                                  size_t out_dim, void* stream);
+
+/* The prefill post-attention RMSNorm folded into the gate/up projection +
+ * SwiGLU (decoder.rs:826-833): out = swiglu_multiply(gate/up(x_norm)) as
+ * qasr_gate_up_swiglu_multiply_int8_f32, with x_norm[t] = rms_norm(h[t]) *
+ * norm_w taken as hg[t] * rinv[t]: hg = h * norm_w and the ss_slices =
+ * ceil(in_dim / 64) partial sums of squares from
+ * qasr_linear_int8_residual_f32, added in slice order into rinv =
+ * 1 / sqrt(sum / in_dim + norm_eps). The GEMM stages hg and multiplies each
+ * token's outputs by rinv; shapes it does not take (few tokens, in_dim > 2048
+ * or not a multiple of 256) write hg * rinv into x_norm ([seq_len, in_dim];
+ * x_norm == hg is allowed) and run the plain launch. Results equal the
+ * reference's rms_norm + gate/up + swiglu_multiply within fp32 rounding (rinv
+ * is factored out of the dot products; the sum of squares is added in
+ * another order). No reference counterpart as one call. */
+int qasr_rms_norm_gate_up_swiglu_multiply_int8_f32(float* out, const float* hg, const float* ss,
+                                                   size_t ss_slices, float norm_eps, float* x_norm,
+                                                   const int8_t* w_gate_up,
+                                                   const float* scales_gate_up, size_t seq_len,
+                                                   size_t in_dim, size_t intermediate,
+                                                   void* stream);
+
+/* The prefill layer-input RMSNorm folded into qasr_qkv_heads_int8_f32
+ * (decoder.rs:789-810): the activations are hg = h * input_norm, each token's
+ * outputs multiplied by its rinv from ss, as in
+ * qasr_rms_norm_gate_up_swiglu_multiply_int8_f32 (including the x_norm
+ * fallback); the rest of the contract is qasr_qkv_heads_int8_f32's (eps is the
+ * head norms'). No reference counterpart as one call. */
+int qasr_rms_norm_qkv_heads_int8_f32(float* q, float* k_cache, float* v_cache, size_t cache_rows,
+                                     const int8_t* wq, const float* sq, const int8_t* wk,
+                                     const float* sk, const int8_t* wv, const float* sv,
+                                     const float* hg, const float* ss, size_t ss_slices,
+                                     float norm_eps, float* x_norm, size_t seq_len, size_t in_dim,
+                                     size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                     const float* q_norm_w, const float* k_norm_w,
+                                     const float* cos_tab, const float* sin_tab, size_t table_rows,
+                                     size_t start_pos, float eps, void* stream);
+
 /* One decode token's layer-input residual add + RMSNorm and the projections
  * that read it, in one launch: h = x + delta (delta may be NULL: h = x),
  * xn = rms_norm(h) * norm_w, ys[m] = linear_nobias_int8(xn, ws[m], scales[m]).

@@ -522,6 +522,72 @@ inline void qkv_heads_int8(F q, F k_cache, F v_cache, size_t cache_rows, DevSlic
                 "qkv_heads_int8");
 }
 
+// Prefill folds: the residual add in the o / down GEMM (h += x W^T, plus each token's sums of
+// squares over 64-column slices of the updated h in ss and, with hg/gain, hg = h * gain), and the
+// next RMSNorm in the q/k/v or gate/up GEMM, which reads hg and multiplies each token's outputs by
+// its 1 / rms from ss (x_norm receives hg * rinv only on shapes the folded kernels do not take).
+inline size_t norm_slices(size_t hidden) { return (hidden + 63) / 64; }
+
+inline void linear_int8_residual(F h, F ss, F hg, CF gain, CF x, DevSlice<const int8_t> w, CF scales,
+                                 size_t seq_len, size_t in_dim, size_t out_dim) {
+  detail::need(h, seq_len * out_dim, "h");
+  detail::need(ss, seq_len * norm_slices(out_dim), "ss");
+  if (hg.ptr || gain.ptr) {
+    detail::need(hg, seq_len * out_dim, "hg");
+    detail::need(gain, out_dim, "gain");
+  }
+  detail::need(x, seq_len * in_dim, "x");
+  detail::need(w, out_dim * in_dim, "w");
+  detail::need(scales, out_dim, "scales");
+  detail::check(qasr_linear_int8_residual_f32(h.ptr, ss.ptr, hg.ptr, gain.ptr, x.ptr, w.ptr, scales.ptr, seq_len,
+                                              in_dim, out_dim, detail::st()),
+                "linear_int8_residual");
+}
+
+inline void rms_norm_gate_up_swiglu_multiply_int8(F out, CF hg, CF ss, float eps, F x_norm,
+                                                  DevSlice<const int8_t> w_gate_up, CF scales_gate_up,
+                                                  size_t seq_len, size_t in_dim, size_t intermediate) {
+  detail::need(out, seq_len * intermediate, "out");
+  detail::need(hg, seq_len * in_dim, "hg");
+  detail::need(ss, seq_len * norm_slices(in_dim), "ss");
+  detail::need(x_norm, seq_len * in_dim, "x_norm");
+  detail::need(w_gate_up, 2 * intermediate * in_dim, "w_gate_up");
+  detail::need(scales_gate_up, 2 * intermediate, "scales_gate_up");
+  detail::check(qasr_rms_norm_gate_up_swiglu_multiply_int8_f32(out.ptr, hg.ptr, ss.ptr, norm_slices(in_dim), eps,
+                                                               x_norm.ptr, w_gate_up.ptr, scales_gate_up.ptr,
+                                                               seq_len, in_dim, intermediate, detail::st()),
+                "rms_norm_gate_up_swiglu_multiply_int8");
+}
+
+inline void rms_norm_qkv_heads_int8(F q, F k_cache, F v_cache, size_t cache_rows, DevSlice<const int8_t> wq,
+                                    CF sq, DevSlice<const int8_t> wk, CF sk, DevSlice<const int8_t> wv, CF sv,
+                                    CF hg, CF ss, float norm_eps, F x_norm, size_t seq_len, size_t in_dim,
+                                    size_t n_heads, size_t n_kv_heads, size_t head_dim, CF q_norm_w,
+                                    CF k_norm_w, const RopeCache& rope, size_t start_pos, float eps) {
+  const size_t qd = n_heads * head_dim, kv = n_kv_heads * head_dim;
+  detail::need(q, seq_len * qd, "q");
+  detail::need(k_cache, cache_rows * kv, "k_cache");
+  detail::need(v_cache, cache_rows * kv, "v_cache");
+  detail::need(wq, qd * in_dim, "wq");
+  detail::need(sq, qd, "sq");
+  detail::need(wk, kv * in_dim, "wk");
+  detail::need(sk, kv, "sk");
+  detail::need(wv, kv * in_dim, "wv");
+  detail::need(sv, kv, "sv");
+  detail::need(hg, seq_len * in_dim, "hg");
+  detail::need(ss, seq_len * norm_slices(in_dim), "ss");
+  detail::need(x_norm, seq_len * in_dim, "x_norm");
+  detail::need(q_norm_w, head_dim, "q_norm_w");
+  detail::need(k_norm_w, head_dim, "k_norm_w");
+  if (rope.head_dim() != head_dim) throw Panic("rms_norm_qkv_heads_int8: RopeCache head_dim mismatch");
+  detail::check(qasr_rms_norm_qkv_heads_int8_f32(
+                    q.ptr, k_cache.ptr, v_cache.ptr, cache_rows, wq.ptr, sq.ptr, wk.ptr, sk.ptr, wv.ptr, sv.ptr,
+                    hg.ptr, ss.ptr, norm_slices(in_dim), norm_eps, x_norm.ptr, seq_len, in_dim, n_heads,
+                    n_kv_heads, head_dim, q_norm_w.ptr, k_norm_w.ptr, rope.cos().ptr, rope.sin().ptr, rope.cap(),
+                    start_pos, eps, detail::st()),
+                "rms_norm_qkv_heads_int8");
+}
+
 // Decode folds (one token): h = x + delta (delta empty: h = x), the RMSNorm of h and the
 // projections of the normalised row in one launch, equal bit for bit to add_rms_norm followed by
 // the projection; h goes to h_out (empty: not written), which must not overlap x or delta.

@@ -73,6 +73,10 @@ SIGNATURES: dict[str, list] = {
     "qasr_linear_int8_f32": [P, P, P, P, P, Z, Z, Z, P],
     "qasr_linear_nobias_int8_multi_f32": [Z, P, P, P, P, P, Z, Z, P],
     "qasr_qkv_heads_int8_f32": [P, P, P, Z, P, P, P, P, P, P, P, Z, Z, Z, Z, Z, P, P, P, P, Z, Z, F, P],
+    "qasr_rms_norm_qkv_heads_int8_f32": [P, P, P, Z, P, P, P, P, P, P, P, P, Z, F, P, Z, Z, Z, Z, Z, P, P, P, P,
+                                         Z, Z, F, P],
+    "qasr_linear_int8_residual_f32": [P, P, P, P, P, P, P, Z, Z, Z, P],
+    "qasr_rms_norm_gate_up_swiglu_multiply_int8_f32": [P, P, P, Z, F, P, P, P, Z, Z, Z, P],
     "qasr_gate_up_swiglu_int8_f32": [P, P, P, P, Z, Z, Z, P],
     "qasr_gate_up_swiglu_multiply_int8_f32": [P, P, P, P, Z, Z, Z, P],
     "qasr_add_rms_norm_linear_nobias_int8_multi_f32": [Z, P, P, P, P, P, P, P, P, Z, F, P],

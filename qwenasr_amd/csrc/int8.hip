@@ -653,7 +653,13 @@ constexpr int kGmBK = 64;           // K granularity of the GEMM path
 // expf tail after the gate/up projection) or the decode loop's form
 // (g / (1 + expf(-g)) * u, decoder.rs:916-921) for batched decode streams;
 // or the q/k/v heads of a prefill chunk (head norms, RoPE, KV-cache rows)
-enum GemmEpi { kGemmRows = 0, kGemmBias = 1, kGemmSwiglu = 2, kGemmSwigluLibm = 3, kGemmHeads = 4 };
+// or, in the split-K kernel only, the prefill residual add: h[t, n] += y and
+// each token's sum of squares of its updated 64-row slice (kGemmResidual).
+// kGemmXNorm added to an epilogue of the LDS-staged kernels folds the prefill
+// RMSNorm into their activation staging (see GemmXNorm).
+enum GemmEpi { kGemmRows = 0, kGemmBias = 1, kGemmSwiglu = 2, kGemmSwigluLibm = 3, kGemmHeads = 4,
+               kGemmResidual = 5 };
+constexpr int kGemmXNorm = 8;
 // K chunks in flight per thread in the single-buffered LDS-staged kernel (2
 // and 3 measured slower: 1.7B gate/up at T = 512 86.0 -> 88.2 / 97.5 us), and
 // register sets of the double-buffered one (4 sets measured the same as 2)
@@ -679,6 +685,9 @@ struct GemmSet {
   int N[4];
   unsigned bx_begin[5];
   int n;
+  float* ss;          // kGemmResidual: [T][ceil(N / 64)] sums of squares of the updated rows
+  float* hg;          // kGemmResidual (optional): the updated rows times gain[n], the next norm's input
+  const float* gain;
 };
 
 // Workgroup -> tile map. The grid is one-dimensional over cols x rows tiles
@@ -740,15 +749,50 @@ struct GemmHeadEpi {
   float eps;
 };
 
+// The prefill RMSNorm folded into the LDS-staged GEMMs (kGemmXNorm). The
+// activations are hg = h * gain, the residual stream times the norm's gain
+// (written by the kGemmResidual epilogue that produced h), staged like any
+// activations; token t's 1 / rms = 1 / sqrt(sum / K + eps), with sum the
+// `slices` partial sums of squares ss[t][0..slices-1] of h added in slice
+// order, multiplies the token's outputs in the epilogue: y = (acc * scale) *
+// rinv, the reference's rms_norm (kernels/mod.rs:897-918) + projection with
+// the scalar factored out of the dot product. Each lane loads its epilogue
+// tokens' partials when the kernel starts and adds them after the k loop.
+struct GemmXNorm {
+  const float* ss;
+  int slices;  // a multiple of 4, at most kXnMaxSlices
+  float eps;
+};
+constexpr int kXnMaxSlices = 32;  // in_dim <= 2048
+
+QASR_DEV void xnorm_load(float (&p)[kXnMaxSlices], const GemmXNorm& xn, int t) {
+  const float* row = xn.ss + (size_t)t * (size_t)xn.slices;
+#pragma unroll
+  for (int u = 0; u < kXnMaxSlices; u += 4) {
+    const float4 v = u < xn.slices ? *reinterpret_cast<const float4*>(row + u) : make_float4(0.f, 0.f, 0.f, 0.f);
+    p[u] = v.x;
+    p[u + 1] = v.y;
+    p[u + 2] = v.z;
+    p[u + 3] = v.w;
+  }
+}
+QASR_DEV float xnorm_rinv(const float (&p)[kXnMaxSlices], int K, float eps) {
+  float sum = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kXnMaxSlices; ++u) sum += p[u];  // the zero slots past `slices` add nothing
+  return 1.0f / sqrtf(sum / (float)K + eps);
+}
+
 constexpr int kHeadTilePitch = 136;  // floats per token row of the staged head tile (pad: banks)
 
 // acc: the 4 waves' MI x MJ blocks of 32 x 32 (lane l, register 4q + v of
 // block (i, j) = row 64 wr + 32i + 8q + 4(l/32) + v of token 32 wc + 32j +
-// l%32 of the tile). Called after the k loop's last barrier (LDS free).
-template <int BT, int MI, int MJ>
+// l%32 of the tile). Called after the k loop's last barrier (LDS free). RT:
+// the outputs of token column j are also multiplied by rt[j].
+template <int BT, int MI, int MJ, bool RT>
 QASR_DEV void gemm_heads_epilogue(const v16f (&acc)[MI][MJ], float* tile, int mat, float* y,
                                   const float* __restrict__ scales, int N, int n0, int t0, int T,
-                                  const GemmHeadEpi& he) {
+                                  const GemmHeadEpi& he, const float (&rt)[MJ]) {
   static_assert(MI == 2 && BT == 64 * MJ, "a 128-row head per tile");
   static_assert(BT * kHeadTilePitch * 4 <= (size_t)(128 + 3 * BT) * (kGmBK + 8) * 2, "the tile fits one stage");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -762,8 +806,14 @@ QASR_DEV void gemm_heads_epilogue(const v16f (&acc)[MI][MJ], float* tile, int ma
       for (int q = 0; q < 4; ++q) {
         const int nl = 64 * wr + 32 * i + 8 * q + 4 * g;
         const float4 s = *reinterpret_cast<const float4*>(scales + n0 + nl);
-        const float4 v = make_float4(acc[i][j][4 * q] * s.x, acc[i][j][4 * q + 1] * s.y,
-                                     acc[i][j][4 * q + 2] * s.z, acc[i][j][4 * q + 3] * s.w);
+        float4 v = make_float4(acc[i][j][4 * q] * s.x, acc[i][j][4 * q + 1] * s.y,
+                               acc[i][j][4 * q + 2] * s.z, acc[i][j][4 * q + 3] * s.w);
+        if constexpr (RT) {  // the folded RMSNorm's 1 / rms of the lane's token
+          v.x *= rt[j];
+          v.y *= rt[j];
+          v.z *= rt[j];
+          v.w *= rt[j];
+        }
         *reinterpret_cast<float4*>(tile + ((BT / 2) * wc + 32 * j + r) * kHeadTilePitch + nl) = v;
       }
   lds_barrier();
@@ -832,8 +882,10 @@ struct GemmEpiRows {
 template <int BN, int BT, int BK, int NPF, int EPI>
 __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, TileMap map,
                                                                 const float* __restrict__ x, int T, int K,
-                                                                GemmHeadEpi he) {
+                                                                GemmHeadEpi he, GemmXNorm xn) {
   constexpr int kGmRow = BK + 8;  // LDS row in bf16 (16-byte pad)
+  constexpr int EP = EPI & 7;                       // the epilogue
+  constexpr bool XN = (EPI & kGemmXNorm) != 0;      // RMSNorm folded in (1 / rms in the epilogue)
   extern __shared__ __align__(16) unsigned short gm_lds[];  // [BN][kGmRow] weights, [3][BT][kGmRow] terms
   unsigned bx, by;
   tile_of(map, blockIdx.x, bx, by);
@@ -873,8 +925,8 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < MJ; ++j) acc[i][j] = v16f{};
-  [[maybe_unused]] GemmEpiRows<MI, EPI == kGemmBias> ep;
-  if constexpr (EPI != kGemmHeads) ep.load(scales, bias, N, n0 + (BN / 2) * wr, lane);
+  [[maybe_unused]] GemmEpiRows<MI, EP == kGemmBias> ep;
+  if constexpr (EP != kGemmHeads) ep.load(scales, bias, N, n0 + (BN / 2) * wr, lane);
 
   // rows and tokens past the end re-read the last one (valid memory; not stored)
   // Staging items: weight item c is 16 bytes of row 64c + tid / 4 at byte
@@ -890,6 +942,11 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
   for (int c = 0; c < WB / 16; ++c) wsrc[c] = w + (size_t)min(n0 + 64 * c + (tid >> 2), N - 1) * K + 16 * w_part;
 #pragma unroll
   for (int c = 0; c < XF / 4; ++c) xsrc[c] = x + (size_t)min(t0 + 16 * c + (tid >> 4), T - 1) * K + 4 * x_part;
+  [[maybe_unused]] float xp[MJ][kXnMaxSlices];  // XN: the partial sums of squares of the lane's epilogue tokens
+  if constexpr (XN) {
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) xnorm_load(xp[j], xn, min(t0 + (BT / 2) * wc + 32 * j + r, T - 1));
+  }
 
   v4i wv[NPF][WB / 16];
   v4f xv[NPF][XF / 4];
@@ -965,9 +1022,15 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
     }
   }
 
-  if constexpr (EPI == kGemmHeads) {
+  [[maybe_unused]] float rt[MJ];  // XN: 1 / rms of the lane's tokens
+  if constexpr (XN) {
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) rt[j] = xnorm_rinv(xp[j], K, xn.eps);
+  }
+  if constexpr (EP == kGemmHeads) {
     static_assert(BN == 128, "one head per tile");
-    gemm_heads_epilogue<BT, MI, MJ>(acc, reinterpret_cast<float*>(gm_lds), mat, y, scales, N, n0, t0, T, he);
+    gemm_heads_epilogue<BT, MI, MJ, XN>(acc, reinterpret_cast<float*>(gm_lds), mat, y, scales, N, n0, t0, T, he,
+                                        rt);
     return;
   }
   // lane l, register 4q + v of block (i, j) holds row n0 + (BN/2)wr + 32i + 8q + 4(l/32) + v
@@ -987,11 +1050,12 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           res[v] = acc[i][j][4 * q + v] * ep.scale(i, 8 * q + 4 * g + v);
-          if constexpr (EPI == kGemmBias) res[v] += ep.shift(i, 8 * q + 4 * g + v);
+          if constexpr (XN) res[v] *= rt[j];
+          if constexpr (EP == kGemmBias) res[v] += ep.shift(i, 8 * q + 4 * g + v);
         }
         if (t < T) {
-          if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
-            swiglu_store<EPI>(y, res, t, n, N);
+          if constexpr (EP == kGemmSwiglu || EP == kGemmSwigluLibm) {
+            swiglu_store<EP>(y, res, t, n, N);
           } else if (vec_out && n + 3 < N) {
             *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
           } else {
@@ -1021,7 +1085,7 @@ constexpr size_t gemm_lds_bytes() {
 template <int BN, int BT, int BK, int NS, int EPI>
 __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, TileMap map,
                                                                    const float* __restrict__ x, int T, int K,
-                                                                   GemmHeadEpi he) {
+                                                                   GemmHeadEpi he, GemmXNorm xn) {
   constexpr int kGmRow = BK + 8;                   // LDS row in bf16 (16-byte pad)
   constexpr int STAGE = (BN + 3 * BT) * kGmRow;    // bf16 per LDS stage
   extern __shared__ __align__(16) unsigned short gm_lds[];  // 2 x ([BN][kGmRow] weights, [3][BT][kGmRow] terms)
@@ -1047,6 +1111,8 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
     }
   constexpr int MI = BN / 64, MJ = BT / 64;
   static_assert(BN % 64 == 0 && BT % 64 == 0, "32 x 32 blocks per wave");
+  constexpr int EP = EPI & 7;                       // the epilogue
+  constexpr bool XN = (EPI & kGemmXNorm) != 0;      // RMSNorm folded in (1 / rms in the epilogue)
   constexpr int NW = BN / 64, NX = BT / 16;         // 16-byte staging items per thread
   constexpr int KSTEPS = BK / 16;                    // MFMA k steps per chunk
   static_assert(NW >= 1 && NX >= 1, "each thread stages whole 16-byte items");
@@ -1060,8 +1126,8 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < MJ; ++j) acc[i][j] = v16f{};
-  [[maybe_unused]] GemmEpiRows<MI, EPI == kGemmBias> ep;
-  if constexpr (EPI != kGemmHeads) ep.load(scales, bias, N, n0 + (BN / 2) * wr, lane);
+  [[maybe_unused]] GemmEpiRows<MI, EP == kGemmBias> ep;
+  if constexpr (EP != kGemmHeads) ep.load(scales, bias, N, n0 + (BN / 2) * wr, lane);
 
   // rows and tokens past the end re-read the last one (valid memory; not stored)
   // staging items as in the single-buffered kernel (16 or 8 lines per load instruction)
@@ -1073,6 +1139,11 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
   for (int c = 0; c < NW; ++c) wsrc[c] = w + (size_t)min(n0 + 64 * c + (tid >> 2), N - 1) * K + 16 * w_part;
 #pragma unroll
   for (int c = 0; c < NX; ++c) xsrc[c] = x + (size_t)min(t0 + 16 * c + (tid >> 4), T - 1) * K + 4 * x_part;
+  [[maybe_unused]] float xp[MJ][kXnMaxSlices];  // XN: the partial sums of squares of the lane's epilogue tokens
+  if constexpr (XN) {
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) xnorm_load(xp[j], xn, min(t0 + (BT / 2) * wc + 32 * j + r, T - 1));
+  }
 
   auto load = [&](v4i (&wv)[NW], v4f (&xv)[NX], int k0) {
 #pragma unroll
@@ -1176,9 +1247,15 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
     }
   }
 
-  if constexpr (EPI == kGemmHeads) {
+  [[maybe_unused]] float rt[MJ];  // XN: 1 / rms of the lane's tokens
+  if constexpr (XN) {
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) rt[j] = xnorm_rinv(xp[j], K, xn.eps);
+  }
+  if constexpr (EP == kGemmHeads) {
     static_assert(BN == 128, "one head per tile");
-    gemm_heads_epilogue<BT, MI, MJ>(acc, reinterpret_cast<float*>(gm_lds), mat, y, scales, N, n0, t0, T, he);
+    gemm_heads_epilogue<BT, MI, MJ, XN>(acc, reinterpret_cast<float*>(gm_lds), mat, y, scales, N, n0, t0, T, he,
+                                        rt);
     return;
   }
   // lane l, register 4q + v of block (i, j) holds row n0 + (BN/2)wr + 32i + 8q + 4(l/32) + v
@@ -1198,11 +1275,12 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           res[v] = acc[i][j][4 * q + v] * ep.scale(i, 8 * q + 4 * g + v);
-          if constexpr (EPI == kGemmBias) res[v] += ep.shift(i, 8 * q + 4 * g + v);
+          if constexpr (XN) res[v] *= rt[j];
+          if constexpr (EP == kGemmBias) res[v] += ep.shift(i, 8 * q + 4 * g + v);
         }
         if (t < T) {
-          if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
-            swiglu_store<EPI>(y, res, t, n, N);
+          if constexpr (EP == kGemmSwiglu || EP == kGemmSwigluLibm) {
+            swiglu_store<EP>(y, res, t, n, N);
           } else if (vec_out && n + 3 < N) {
             *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
           } else {
@@ -1262,10 +1340,14 @@ constexpr int kKsPitch = 68;
 // Lane l, register 4q + v of block (i, j) holds row n0 + 32i + 8q + 4(l/32) + v
 // of token t0 + 32j + l%32; the KW waves' partial tiles are added in LDS in
 // wave order (deterministic), the blocks split over the waves; epilogue
-// y = sum * scale (+ bias).
+// y = sum * scale (+ bias), or (kGemmResidual) y += sum * scale with each
+// token's sum of squares of its updated 64 rows written to ss[t][n0 / 64]
+// (per lane in item order, then the two lanes of a token, then the waves in
+// order through LDS) and, with hg, hg = the updated y * gain[n].
 template <int MI, int MJ, int KW, int EPI>
 QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wave, int lane, float* y,
-                                  const float* scales, const float* bias, int N, int T, int n0, int t0) {
+                                  const float* scales, const float* bias, int N, int T, int n0, int t0,
+                                  float* ss, float* hg, const float* gain) {
   const int r = lane & 31, g = lane >> 5;
   constexpr int PER_WAVE = MI * MJ * 16 * 64;  // floats
   // Wave w reduces and stores the (block, register quad) items w, w + KW, ...
@@ -1273,6 +1355,7 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
   // through LDS, so that exchange hides their latency.
   constexpr int ITEMS = (MI * MJ * 4 + KW - 1) / KW;
   float es[ITEMS][4], eb[ITEMS][4];
+  [[maybe_unused]] float hv[ITEMS][4], gv[ITEMS][4];  // kGemmResidual: the rows to add to, the gains
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
     const int p = min(wave + KW * it, MI * MJ * 4 - 1);
@@ -1282,6 +1365,14 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
       const int nv = min(n + v, N - 1);
       es[it][v] = scales[nv];
       eb[it][v] = EPI == kGemmBias ? bias[nv] : 0.0f;
+    }
+    if constexpr (EPI == kGemmResidual) {
+      const int t = min(t0 + 32 * ((p >> 2) % MJ) + r, T - 1);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        hv[it][v] = y[(size_t)t * N + min(n + v, N - 1)];
+        gv[it][v] = hg ? gain[min(n + v, N - 1)] : 0.0f;
+      }
     }
   }
   float* mine = red + (size_t)wave * PER_WAVE;
@@ -1293,6 +1384,10 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
       for (int e = 0; e < 16; ++e) mine[((i * MJ + j) * 16 + e) * 64 + lane] = acc[i][j][e];
   __syncthreads();
   const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  static_assert(EPI != kGemmResidual || (KW == 4 && MI == 2), "residual slices: 64 rows, item it = block it");
+  [[maybe_unused]] float sq[MJ];
+#pragma unroll
+  for (int j = 0; j < MJ; ++j) sq[j] = 0.0f;
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
     const int p = wave + KW * it;
@@ -1311,7 +1406,31 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
         res[v] = sum * es[it][v];
         if constexpr (EPI == kGemmBias) res[v] += eb[it][v];
       }
-      if (t < T) {
+      if constexpr (EPI == kGemmResidual) {
+        // h + y in the residual add's order (decoder.rs:829, 843)
+        float hn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (t < T) {
+          float* hp = &y[(size_t)t * N + n];
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (n + v < N) hn[v] = hv[it][v] + res[v];
+          if (vec_out && n + 3 < N) {
+            *reinterpret_cast<float4*>(hp) = make_float4(hn[0], hn[1], hn[2], hn[3]);
+            if (hg)
+              *reinterpret_cast<float4*>(&hg[(size_t)t * N + n]) =
+                  make_float4(hn[0] * gv[it][0], hn[1] * gv[it][1], hn[2] * gv[it][2], hn[3] * gv[it][3]);
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (n + v < N) {
+                hp[v] = hn[v];
+                if (hg) hg[(size_t)t * N + n + v] = hn[v] * gv[it][v];
+              }
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sq[it % MJ] += hn[v] * hn[v];
+      } else if (t < T) {
         if constexpr (EPI == kGemmSwiglu || EPI == kGemmSwigluLibm) {
           swiglu_store<EPI>(y, res, t, n, N);
         } else if (vec_out && n + 3 < N) {
@@ -1321,6 +1440,26 @@ QASR_DEV void ksplit_reduce_store(const v16f (&acc)[MI][MJ], float* red, int wav
           for (int v = 0; v < 4; ++v)
             if (n + v < N) y[(size_t)t * N + n + v] = res[v];
         }
+      }
+    }
+  }
+  if constexpr (EPI == kGemmResidual) {
+    __shared__ float ssl[KW][MJ][32];
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+      const float both = sq[j] + __shfl_xor(sq[j], 32, kWave);  // rows 4g..4g+3 of each quad: g = 0, 1
+      if (g == 0) ssl[wave][j][r] = both;
+    }
+    __syncthreads();
+    if (wave == 0 && g == 0) {
+      const int slices = (N + 63) / 64;
+#pragma unroll
+      for (int j = 0; j < MJ; ++j) {
+        float sum = ssl[0][j][r];
+#pragma unroll
+        for (int ww = 1; ww < KW; ++ww) sum += ssl[ww][j][r];
+        const int t = t0 + 32 * j + r;
+        if (t < T) ss[(size_t)t * slices + n0 / 64] = sum;
       }
     }
   }
@@ -1492,7 +1631,8 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
     for (int e = 0; e < 16; ++e) acc[0][0][0][e] = (acc[0][0][0][e] + acc[1][0][0][e]) + acc[2][0][0][e];
   }
   __syncthreads();  // every wave's staged activations read: the partial tiles reuse the LDS
-  ksplit_reduce_store<MI, MJ, KW, EPI>(acc[0], gk_red, wave, lane, y, scales, bias, N, T, n0, t0);
+  ksplit_reduce_store<MI, MJ, KW, EPI>(acc[0], gk_red, wave, lane, y, scales, bias, N, T, n0, t0, set.ss, set.hg,
+                                       set.gain);
 }
 
 template <int BN, int BT, int KW, int EPI>
@@ -1512,7 +1652,7 @@ bool try_gemm_ksplit(const GemmSet& set, unsigned cols, const float* x, int T, i
 
 template <int BN, int BT, int BK, int NPF, int EPI>
 bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st,
-              const GemmHeadEpi& he = GemmHeadEpi{}) {
+              const GemmHeadEpi& he = GemmHeadEpi{}, const GemmXNorm& xn = GemmXNorm{}) {
   constexpr size_t lds = gemm_lds_bytes<BN, BT, BK>();
   if (K % BK != 0) return false;
   if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, EPI>>(lds)) return false;
@@ -1520,13 +1660,13 @@ bool try_gemm(const GemmSet& set, unsigned cols, const float* x, int T, int K, h
   map.cols = cols;
   map.rows = (unsigned)((T + BT - 1) / BT);
   map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
-  w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K, he);
+  w8a32_gemm_bf16x3_kernel<BN, BT, BK, NPF, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K, he, xn);
   return true;
 }
 
 template <int BN, int BT, int BK, int NS, int EPI>
 bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st,
-                 const GemmHeadEpi& he = GemmHeadEpi{}) {
+                 const GemmHeadEpi& he = GemmHeadEpi{}, const GemmXNorm& xn = GemmXNorm{}) {
   constexpr size_t lds = 2 * gemm_lds_bytes<BN, BT, BK>();
   if (K % (NS * BK) != 0) return false;
   if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_db_kernel<BN, BT, BK, NS, EPI>>(lds)) return false;
@@ -1534,7 +1674,8 @@ bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K
   map.cols = cols;
   map.rows = (unsigned)((T + BT - 1) / BT);
   map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
-  w8a32_gemm_bf16x3_db_kernel<BN, BT, BK, NS, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K, he);
+  w8a32_gemm_bf16x3_db_kernel<BN, BT, BK, NS, EPI><<<map.cols * map.rows, 256, lds, st>>>(set, map, x, T, K, he,
+                                                                                         xn);
   return true;
 }
 
@@ -1555,9 +1696,12 @@ bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K
 // 32 x 32 that fills the chip (measured at T = 512: o [1024, 2048] 20.0 ->
 // 16.7 us, down [1024, 3072] 27.4 -> 20.9 us against the LDS-staged 64 x 32).
 // Returns false when the chosen kernel cannot run the shape (K not a multiple
-// of its K step, or its LDS size refused): nothing was launched.
+// of its K step, or its LDS size refused), or when it is the split-K kernel
+// and the epilogue asks for the folded RMSNorm (kGemmXNorm, which only the
+// LDS-staged kernels stage): nothing was launched.
 template <int EPI>
-bool launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st) {
+bool launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st,
+                       const GemmXNorm& xn = GemmXNorm{}) {
   auto cols = [&](int bn) {
     unsigned c = 0;
     for (int m = 0; m < set.n; ++m) {
@@ -1568,22 +1712,27 @@ bool launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
     return c;
   };
   const long long rows64 = (T + 63) / 64, rows32 = (T + 31) / 32;
+  const GemmHeadEpi he{};
   unsigned c = cols(256);
-  if (c * rows64 >= 512) return try_gemm<256, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
+  if (c * rows64 >= 512) return try_gemm<256, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st, he, xn);
   const unsigned c128 = cols(128);
   c = cols(192);
   if (c128 * rows64 > 256 && c * rows64 <= 256 &&
-      try_gemm_db<192, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st))
+      try_gemm_db<192, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st, he, xn))
     return true;
   c = cols(128);
   if (c * rows64 >= 256) {
-    if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st)) return true;
-    return try_gemm<128, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st);
+    if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st, he, xn)) return true;
+    return try_gemm<128, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st, he, xn);
   }
-  c = cols(64);
-  if (c * rows64 >= 256) return try_gemm_ksplit<64, 64, 4, EPI>(set, c, x, T, K, st);
-  if (c * rows32 >= 256) return try_gemm_ksplit<64, 32, 4, EPI>(set, c, x, T, K, st);
-  return try_gemm_ksplit<32, 32, 4, EPI>(set, cols(32), x, T, K, st);
+  if constexpr ((EPI & kGemmXNorm) != 0) {
+    return false;
+  } else {
+    c = cols(64);
+    if (c * rows64 >= 256) return try_gemm_ksplit<64, 64, 4, EPI>(set, c, x, T, K, st);
+    if (c * rows32 >= 256) return try_gemm_ksplit<64, 32, 4, EPI>(set, c, x, T, K, st);
+    return try_gemm_ksplit<32, 32, 4, EPI>(set, cols(32), x, T, K, st);
+  }
 }
 
 }  // namespace
@@ -1619,7 +1768,7 @@ constexpr size_t kGemmMinTokens = 8;
 // The q/k/v GEMM with the heads epilogue: 128-row tiles (one head), double
 // buffered where that is one workgroup per CU, as for the plain projection.
 static bool launch_w8a32_heads(GemmSet set, const float* x, int T, int K, const GemmHeadEpi& he,
-                               hipStream_t st) {
+                               hipStream_t st, const GemmXNorm& xn = GemmXNorm{}) {
   unsigned c = 0;
   for (int m = 0; m < set.n; ++m) {
     set.bx_begin[m] = c;
@@ -1627,6 +1776,11 @@ static bool launch_w8a32_heads(GemmSet set, const float* x, int T, int K, const 
   }
   for (int m = set.n; m <= 4; ++m) set.bx_begin[m] = c;
   const long long rows64 = (T + 63) / 64;
+  constexpr int kFold = kGemmHeads | kGemmXNorm;
+  if (xn.ss) {
+    if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, kFold>(set, c, x, T, K, st, he, xn)) return true;
+    return try_gemm<128, 64, 64, kGemmPrefetch, kFold>(set, c, x, T, K, st, he, xn);
+  }
   if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, kGemmHeads>(set, c, x, T, K, st, he)) return true;
   return try_gemm<128, 64, 64, kGemmPrefetch, kGemmHeads>(set, c, x, T, K, st, he);
 }
@@ -1773,14 +1927,14 @@ extern "C" int qasr_gate_up_swiglu_multiply_int8_f32(float* out, const float* x,
   return launch_status("gate_up_swiglu_multiply_int8");
 }
 
-extern "C" int qasr_qkv_heads_int8_f32(float* q, float* k_cache, float* v_cache, size_t cache_rows,
-                                       const int8_t* wq, const float* sq, const int8_t* wk,
-                                       const float* sk, const int8_t* wv, const float* sv,
-                                       const float* x, size_t seq_len, size_t in_dim, size_t n_heads,
-                                       size_t n_kv_heads, size_t head_dim, const float* q_norm_w,
-                                       const float* k_norm_w, const float* cos_tab,
-                                       const float* sin_tab, size_t table_rows, size_t start_pos,
-                                       float eps, void* stream) {
+// The q/k/v + heads launch; with xn the activations are the residual stream
+// and the input RMSNorm is folded into the staging.
+static int qkv_heads_impl(float* q, float* k_cache, float* v_cache, size_t cache_rows, const int8_t* wq,
+                          const float* sq, const int8_t* wk, const float* sk, const int8_t* wv,
+                          const float* sv, const float* x, size_t seq_len, size_t in_dim, size_t n_heads,
+                          size_t n_kv_heads, size_t head_dim, const float* q_norm_w, const float* k_norm_w,
+                          const float* cos_tab, const float* sin_tab, size_t table_rows, size_t start_pos,
+                          float eps, void* stream, const GemmXNorm* xn) {
   if (seq_len == 0) return QASR_OK;
   QASR_REQUIRE(q && k_cache && v_cache && wq && sq && wk && sk && wv && sv && x && q_norm_w && k_norm_w &&
                    cos_tab && sin_tab,
@@ -1831,9 +1985,148 @@ extern "C" int qasr_qkv_heads_int8_f32(float* q, float* k_cache, float* v_cache,
   he.cache_rows = (long long)cache_rows;
   he.n_kv_heads = (int)n_kv_heads;
   he.eps = eps;
-  if (!launch_w8a32_heads(set, x, (int)seq_len, (int)in_dim, he, as_stream(stream)))
+  if (!launch_w8a32_heads(set, x, (int)seq_len, (int)in_dim, he, as_stream(stream), xn ? *xn : GemmXNorm{}))
     return fail(QASR_ERR_UNSUPPORTED, "qkv_heads_int8: the GEMM kernel cannot run this shape");
   return launch_status("qkv_heads_int8");
+}
+
+extern "C" int qasr_qkv_heads_int8_f32(float* q, float* k_cache, float* v_cache, size_t cache_rows,
+                                       const int8_t* wq, const float* sq, const int8_t* wk,
+                                       const float* sk, const int8_t* wv, const float* sv,
+                                       const float* x, size_t seq_len, size_t in_dim, size_t n_heads,
+                                       size_t n_kv_heads, size_t head_dim, const float* q_norm_w,
+                                       const float* k_norm_w, const float* cos_tab,
+                                       const float* sin_tab, size_t table_rows, size_t start_pos,
+                                       float eps, void* stream) {
+  return qkv_heads_impl(q, k_cache, v_cache, cache_rows, wq, sq, wk, sk, wv, sv, x, seq_len, in_dim, n_heads,
+                        n_kv_heads, head_dim, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, start_pos, eps,
+                        stream, nullptr);
+}
+
+namespace qasr {
+namespace {
+// x_norm = hg * rinv per row, rinv from the row's `slices` partial sums of
+// squares added in slice order (as the folded GEMMs do): the normalised rows
+// for the shapes the folded GEMMs do not take. In place (x_norm == hg) is fine.
+__global__ __launch_bounds__(256) void xnorm_rows_kernel(float* x_norm, const float* hg, const float* __restrict__ ss,
+                                                         int slices, int K, float eps) {
+  const size_t row = blockIdx.x;
+  const float* p = ss + row * (size_t)slices;
+  float sum = 0.0f;
+  for (int u = 0; u < slices; ++u) sum += p[u];
+  const float rinv = 1.0f / sqrtf(sum / (float)K + eps);
+  for (int k = threadIdx.x; k < K; k += 256) x_norm[row * K + k] = hg[row * K + k] * rinv;
+}
+}  // namespace
+}  // namespace qasr
+
+// Whether the folded GEMMs take these partial sums (their per-lane registers
+// hold at most kXnMaxSlices, loaded 4 at a time).
+static bool xnorm_fold_ok(const float* ss, size_t ss_slices) {
+  return ss_slices % 4 == 0 && ss_slices <= (size_t)kXnMaxSlices && aligned16(ss);
+}
+
+static int xnorm_rows(float* x_norm, const float* hg, const float* ss, size_t slices, size_t rows, size_t K,
+                      float eps, hipStream_t st) {
+  xnorm_rows_kernel<<<(unsigned)rows, 256, 0, st>>>(x_norm, hg, ss, (int)slices, (int)K, eps);
+  return launch_status("rms_norm fold: normalised rows");
+}
+
+extern "C" int qasr_rms_norm_qkv_heads_int8_f32(float* q, float* k_cache, float* v_cache, size_t cache_rows,
+                                                const int8_t* wq, const float* sq, const int8_t* wk,
+                                                const float* sk, const int8_t* wv, const float* sv,
+                                                const float* hg, const float* ss, size_t ss_slices,
+                                                float norm_eps, float* x_norm, size_t seq_len, size_t in_dim,
+                                                size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                                const float* q_norm_w, const float* k_norm_w,
+                                                const float* cos_tab, const float* sin_tab, size_t table_rows,
+                                                size_t start_pos, float eps, void* stream) {
+  if (seq_len == 0) return QASR_OK;
+  QASR_REQUIRE(hg && ss && x_norm, "rms_norm_qkv_heads_int8: null pointer");
+  QASR_REQUIRE(ss_slices == (in_dim + 63) / 64 && in_dim <= 0x7fffffffu && seq_len <= 0x7fffffffu,
+               "rms_norm_qkv_heads_int8: ss_slices must be ceil(in_dim / 64)");
+  if (xnorm_fold_ok(ss, ss_slices)) {
+    const GemmXNorm xn{ss, (int)ss_slices, norm_eps};
+    return qkv_heads_impl(q, k_cache, v_cache, cache_rows, wq, sq, wk, sk, wv, sv, hg, seq_len, in_dim, n_heads,
+                          n_kv_heads, head_dim, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, start_pos, eps,
+                          stream, &xn);
+  }
+  const int rc = xnorm_rows(x_norm, hg, ss, ss_slices, seq_len, in_dim, norm_eps, as_stream(stream));
+  if (rc != QASR_OK) return rc;
+  return qkv_heads_impl(q, k_cache, v_cache, cache_rows, wq, sq, wk, sk, wv, sv, x_norm, seq_len, in_dim, n_heads,
+                        n_kv_heads, head_dim, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, start_pos, eps,
+                        stream, nullptr);
+}
+
+extern "C" int qasr_linear_int8_residual_f32(float* h, float* ss, float* hg, const float* gain, const float* x,
+                                             const int8_t* w, const float* scales, size_t seq_len, size_t in_dim,
+                                             size_t out_dim, void* stream) {
+  if (seq_len == 0 || out_dim == 0) return QASR_OK;
+  QASR_REQUIRE(h && ss && x && w && scales, "linear_int8_residual: null pointer");
+  QASR_REQUIRE((hg == nullptr) == (gain == nullptr), "linear_int8_residual: hg and gain go together");
+  QASR_REQUIRE(seq_len <= 0x7fffffffu && in_dim <= 0x7fffffffu && out_dim <= 0x7fffffffu,
+               "linear_int8_residual: size too large");
+  size_t n;
+  QASR_REQUIRE(mul_ok(in_dim, out_dim, &n) && mul_ok(seq_len, in_dim, &n) && mul_ok(seq_len, out_dim, &n),
+               "linear_int8_residual: size overflows");
+  if (!w8a32_gemm_shape(seq_len, in_dim, w, x) || !aligned16(h) || (hg && !aligned16(hg)))
+    return fail(QASR_ERR_UNSUPPORTED,
+                "linear_int8_residual: needs seq_len >= 8, in_dim % 64 == 0 and 16-byte aligned h, hg, x, w");
+  GemmSet set{};
+  set.y[0] = h;
+  set.w[0] = w;
+  set.s[0] = scales;
+  set.b[0] = nullptr;
+  set.N[0] = (int)out_dim;
+  set.n = 1;
+  set.ss = ss;
+  set.hg = hg;
+  set.gain = gain;
+  const unsigned c = (unsigned)((out_dim + 63) / 64);
+  set.bx_begin[0] = 0;
+  for (int m = 1; m <= 4; ++m) set.bx_begin[m] = c;
+  const long long rows64 = (long long)((seq_len + 63) / 64);
+  hipStream_t st = as_stream(stream);
+  const bool ran = c * rows64 >= 256
+                       ? try_gemm_ksplit<64, 64, 4, kGemmResidual>(set, c, x, (int)seq_len, (int)in_dim, st)
+                       : try_gemm_ksplit<64, 32, 4, kGemmResidual>(set, c, x, (int)seq_len, (int)in_dim, st);
+  if (!ran) return fail(QASR_ERR_UNSUPPORTED, "linear_int8_residual: the GEMM kernel cannot run this shape");
+  return launch_status("linear_int8_residual");
+}
+
+extern "C" int qasr_rms_norm_gate_up_swiglu_multiply_int8_f32(float* out, const float* hg, const float* ss,
+                                                             size_t ss_slices, float norm_eps, float* x_norm,
+                                                             const int8_t* w_gate_up, const float* scales_gate_up,
+                                                             size_t seq_len, size_t in_dim, size_t intermediate,
+                                                             void* stream) {
+  if (seq_len == 0 || intermediate == 0) return QASR_OK;
+  QASR_REQUIRE(out && hg && ss && x_norm && w_gate_up && scales_gate_up,
+               "rms_norm_gate_up_swiglu_multiply_int8: null pointer");
+  QASR_REQUIRE(in_dim > 0 && in_dim <= 0x7fffffffu && seq_len <= 0x7fffffffu && intermediate <= 0x3fffffffu - 64,
+               "rms_norm_gate_up_swiglu_multiply_int8: size too large");
+  QASR_REQUIRE(ss_slices == (in_dim + 63) / 64,
+               "rms_norm_gate_up_swiglu_multiply_int8: ss_slices must be ceil(in_dim / 64)");
+  size_t n;
+  QASR_REQUIRE(mul_ok(2 * intermediate, in_dim, &n) && mul_ok(seq_len, in_dim, &n) &&
+                   mul_ok(seq_len, 2 * intermediate, &n) && n < ((size_t)1 << 33),
+               "rms_norm_gate_up_swiglu_multiply_int8: size overflows");
+  if (w8a32_gemm_shape(seq_len, in_dim, w_gate_up, hg) && xnorm_fold_ok(ss, ss_slices)) {
+    GemmSet set{};
+    set.y[0] = out;
+    set.w[0] = w_gate_up;
+    set.s[0] = scales_gate_up;
+    set.b[0] = nullptr;
+    set.N[0] = (int)(2 * intermediate);
+    set.n = 1;
+    const GemmXNorm xn{ss, (int)ss_slices, norm_eps};
+    if (launch_w8a32_gemm<kGemmSwiglu | kGemmXNorm>(set, hg, (int)seq_len, (int)in_dim, as_stream(stream), xn))
+      return launch_status("rms_norm_gate_up_swiglu_multiply_int8");
+  }
+  // a shape the folded kernels do not take: the normalised rows into x_norm, then the plain launch
+  const int rc = xnorm_rows(x_norm, hg, ss, ss_slices, seq_len, in_dim, norm_eps, as_stream(stream));
+  if (rc != QASR_OK) return rc;
+  return qasr_gate_up_swiglu_multiply_int8_f32(out, x_norm, w_gate_up, scales_gate_up, seq_len, in_dim,
+                                               intermediate, stream);
 }
 
 extern "C" int qasr_linear_nobias_int8_multi_f32(size_t n_mats, float* const* ys,

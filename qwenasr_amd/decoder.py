@@ -46,7 +46,8 @@ class DecoderInt8:
     def __init__(self, weights: dict, hidden: int, intermediate: int, n_layers: int, n_heads: int = 16,
                  n_kv_heads: int = 8, head_dim: int = 128, eps: float = 1e-6, theta: float = 1e6,
                  vocab: int | None = None, max_seq: int = 256, device="cuda",
-                 fuse_norms: bool | None = None, fuse_prefill_heads: bool | None = None):
+                 fuse_norms: bool | None = None, fuse_prefill_heads: bool | None = None,
+                 fuse_prefill_norms: bool | None = None):
         self.w = weights
         self.H, self.I, self.L = hidden, intermediate, n_layers
         self.nq, self.nk, self.hd = n_heads, n_kv_heads, head_dim
@@ -64,6 +65,9 @@ class DecoderInt8:
         # where that launch fills the chip (>= 256 workgroups); below, the
         # unfused split-K GEMM + head kernel is faster
         self.fuse_prefill_heads = fuse_prefill_heads
+        # prefill residual adds folded into the o / down GEMMs and the RMSNorms
+        # into the q/k/v and gate/up GEMMs' staging (None: wherever the GEMMs run)
+        self.fuse_prefill_norms = fuse_prefill_norms
         self.x = torch.zeros(hidden, **f32)
         self.x2 = torch.zeros(hidden, **f32)  # the residual's other buffer (fused path)
         self.x_norm = torch.empty(hidden, **f32)
@@ -96,6 +100,7 @@ class DecoderInt8:
         self.pproj = torch.empty(T * H, **f32)
         self.pgate = torch.empty(T * I, **f32)
         self.pffn = torch.empty(T * H, **f32)
+        self.pss = torch.empty(T * K.norm_slices(H), **f32)  # per-token partial sums of squares
         self._pcap = T
 
     def _check_pos(self, pos: int | None, what: str) -> int:
@@ -126,6 +131,13 @@ class DecoderInt8:
             return fits and (self.nq + 2 * self.nk) * ((T + 63) // 64) >= 256
         return self.fuse_prefill_heads and fits
 
+    def prefill_norms_folded(self, T: int) -> bool:
+        """Whether a prefill of T tokens folds the residual adds into the o / down
+        GEMMs and the RMSNorms into the following GEMMs (the GEMM path: T >= 8,
+        every in_dim a multiple of 64)."""
+        fits = T >= 8 and self.H % 64 == 0 and (self.nq * self.hd) % 64 == 0 and self.I % 64 == 0
+        return fits and self.fuse_prefill_norms is not False
+
     def prefill(self, embeds: torch.Tensor, T: int, start_pos: int | None = None) -> None:
         """T tokens at positions start_pos.. (decoder.rs:751-847): writes cache rows
         start_pos..start_pos+T-1 of every layer; ``self.px[:T*H]`` receives the
@@ -135,31 +147,53 @@ class DecoderInt8:
         q_dim = nq * hd
         total = start_pos + T
         fused_heads = self.prefill_heads_fused(T)
+        fold = self.prefill_norms_folded(T)
         x = self.px
         x[:T * H].copy_(embeds[:T * H])
-        for l, lw in enumerate(self.w["layers"]):
-            if l == 0:
-                K.rms_norm(self.pxn, x, lw["input_norm"], T, H, eps)
-            else:  # previous layer's residual add (decoder.rs:843) + this layer's input norm
-                K.add_rms_norm(x, self.pffn, lw["input_norm"], self.pxn, T, H, eps)
+        layers = self.w["layers"]
+        for l, lw in enumerate(layers):
             kb, vb = self.kv.k_layer_block(l), self.kv.v_layer_block(l)
-            if fused_heads:
-                K.qkv_heads_int8(self.pq, kb, vb, self.kv.max_seq, lw["wq"], lw["wk"], lw["wv"], self.pxn, T, H,
-                                 nq, nk, hd, lw["q_norm"], lw["k_norm"], self.rope, start_pos, eps)
+            if fold and l > 0 and fused_heads:  # input norm: h * gain and the sums of squares from down
+                K.rms_norm_qkv_heads_int8(self.pq, kb, vb, self.kv.max_seq, lw["wq"], lw["wk"], lw["wv"], self.pxn,
+                                          self.pss, eps, self.pxn, T, H, nq, nk, hd, lw["q_norm"], lw["k_norm"],
+                                          self.rope, start_pos, eps)
             else:
-                K.linear_nobias_int8_multi([self.pq, self.pk, self.pv], [lw["wq"], lw["wk"], lw["wv"]],
-                                           self.pxn, T, H)
-                K.head_rms_norm_rope_kv(self.pq, self.pk, self.pv, lw["q_norm"], lw["k_norm"], self.rope, None,
-                                        start_pos, T, nq, nk, hd, eps, kb, vb, self.kv.max_seq)
+                if l == 0 or fold:  # fold: the residual add happened in the down GEMM
+                    K.rms_norm(self.pxn, x, lw["input_norm"], T, H, eps)
+                else:  # previous layer's residual add (decoder.rs:837-838) + this layer's input norm
+                    K.add_rms_norm(x, self.pffn, lw["input_norm"], self.pxn, T, H, eps)
+                self._prefill_qkv(l, lw, T, start_pos, fused_heads)
             K.causal_attention(self.pattn, self.pq, kb, vb, T, total, nq, nk, hd, self.scale, start_pos)
-            wo = lw["wo"]
-            K.linear_nobias_int8(self.pproj, self.pattn, wo.data, wo.scales, T, q_dim, H)
-            K.add_rms_norm(x, self.pproj, lw["post_attn_norm"], self.pxn, T, H, eps)
-            K.gate_up_swiglu_multiply_int8(self.pgate, self.pxn, lw["gate_up"], T, H, I)
-            dn = lw["down"]
-            K.linear_nobias_int8(self.pffn, self.pgate, dn.data, dn.scales, T, I, H)
-        K.add_inplace(x, self.pffn, T * H)
+            wo, dn = lw["wo"], lw["down"]
+            if fold:
+                K.linear_int8_residual(x, self.pss, self.pattn, wo, T, q_dim, H, self.pxn, lw["post_attn_norm"])
+                K.rms_norm_gate_up_swiglu_multiply_int8(self.pgate, self.pxn, self.pss, eps, self.pxn,
+                                                        lw["gate_up"], T, H, I)
+                nxt = layers[l + 1]["input_norm"] if l + 1 < len(layers) and fused_heads else None
+                K.linear_int8_residual(x, self.pss, self.pgate, dn, T, I, H, self.pxn if nxt is not None else None,
+                                       nxt)
+            else:
+                K.linear_nobias_int8(self.pproj, self.pattn, wo.data, wo.scales, T, q_dim, H)
+                K.add_rms_norm(x, self.pproj, lw["post_attn_norm"], self.pxn, T, H, eps)
+                K.gate_up_swiglu_multiply_int8(self.pgate, self.pxn, lw["gate_up"], T, H, I)
+                K.linear_nobias_int8(self.pffn, self.pgate, dn.data, dn.scales, T, I, H)
+        if not fold:
+            K.add_inplace(x, self.pffn, T * H)
         self.kv.len = total
+
+    def _prefill_qkv(self, l: int, lw: dict, T: int, start_pos: int, fused_heads: bool) -> None:
+        """q/k/v of the normalised rows in ``self.pxn`` with the head norms, RoPE
+        and the layer's cache rows (decoder.rs:795-810)."""
+        nq, nk, hd, eps, H = self.nq, self.nk, self.hd, self.eps, self.H
+        kb, vb = self.kv.k_layer_block(l), self.kv.v_layer_block(l)
+        if fused_heads:
+            K.qkv_heads_int8(self.pq, kb, vb, self.kv.max_seq, lw["wq"], lw["wk"], lw["wv"], self.pxn, T, H,
+                             nq, nk, hd, lw["q_norm"], lw["k_norm"], self.rope, start_pos, eps)
+        else:
+            K.linear_nobias_int8_multi([self.pq, self.pk, self.pv], [lw["wq"], lw["wk"], lw["wv"]],
+                                       self.pxn, T, H)
+            K.head_rms_norm_rope_kv(self.pq, self.pk, self.pv, lw["q_norm"], lw["k_norm"], self.rope, None,
+                                    start_pos, T, nq, nk, hd, eps, kb, vb, self.kv.max_seq)
 
     def prepare(self, pos: int | None = None) -> None:
         """Host-side growth before a decode at ``pos`` (decoder.rs:866-872):

@@ -641,6 +641,80 @@ def qkv_heads_int8(q, k_cache, v_cache, cache_rows: int, wq: QuantWeight, wk: Qu
               _ptr(rope.sin), rope.cap, start_pos, eps, _stream())
 
 
+def norm_slices(hidden: int) -> int:
+    """Partial sums of squares per token that ``linear_int8_residual`` writes
+    (one per 64 columns of the residual stream)."""
+    return (hidden + 63) // 64
+
+
+def linear_int8_residual(h, ss, x, w: QuantWeight, seq_len: int, in_dim: int, out_dim: int, hg=None,
+                         gain=None) -> None:
+    """The prefill residual add folded into the o / down projection
+    (decoder.rs:821-822, 837-838): ``h += linear_nobias_int8(x, w)`` bit for bit;
+    ``ss[t, s]`` = the sum of squares of the updated ``h[t, 64s:64s+64]``, and
+    with ``hg``/``gain`` also ``hg = h * gain`` -- what the next folded RMSNorm
+    reads. seq_len >= 8 and in_dim % 64 == 0 (else the library raises)."""
+    _need(h, F32, seq_len * out_dim, "h")
+    _need(ss, F32, seq_len * norm_slices(out_dim), "ss")
+    _need(x, F32, seq_len * in_dim, "x")
+    _need(w.data, I8, out_dim * in_dim, "w")
+    _need(w.scales, F32, out_dim, "scales")
+    if (hg is None) != (gain is None):
+        raise ValueError("linear_int8_residual: hg and gain go together")
+    if hg is not None:
+        _need(hg, F32, seq_len * out_dim, "hg")
+        _need(gain, F32, out_dim, "gain")
+    _lib.call("qasr_linear_int8_residual_f32", _ptr(h), _ptr(ss), _ptr(hg) if hg is not None else None,
+              _ptr(gain) if gain is not None else None, _ptr(x), _ptr(w.data), _ptr(w.scales), seq_len, in_dim,
+              out_dim, _stream())
+
+
+def rms_norm_gate_up_swiglu_multiply_int8(out, hg, ss, eps: float, x_norm, w: QuantWeight, seq_len: int,
+                                          in_dim: int, intermediate: int) -> None:
+    """The prefill post-attention RMSNorm folded into the gate/up GEMM + SwiGLU
+    (decoder.rs:826-833): ``hg`` = h * norm gain and ``ss`` from
+    ``linear_int8_residual``; each token's outputs are multiplied by its 1 / rms.
+    ``x_norm`` ([seq_len, in_dim], may be ``hg``) receives the normalised rows
+    only on shapes the folded kernel does not take."""
+    _need(out, F32, seq_len * intermediate, "out")
+    _need(hg, F32, seq_len * in_dim, "hg")
+    _need(ss, F32, seq_len * norm_slices(in_dim), "ss")
+    _need(x_norm, F32, seq_len * in_dim, "x_norm")
+    _need(w.data, I8, 2 * intermediate * in_dim, "w")
+    _need(w.scales, F32, 2 * intermediate, "scales")
+    _lib.call("qasr_rms_norm_gate_up_swiglu_multiply_int8_f32", _ptr(out), _ptr(hg), _ptr(ss),
+              norm_slices(in_dim), eps, _ptr(x_norm), _ptr(w.data), _ptr(w.scales), seq_len, in_dim,
+              intermediate, _stream())
+
+
+def rms_norm_qkv_heads_int8(q, k_cache, v_cache, cache_rows: int, wq: QuantWeight, wk: QuantWeight,
+                            wv: QuantWeight, hg, ss, norm_eps: float, x_norm, seq_len: int, in_dim: int,
+                            n_heads: int, n_kv_heads: int, head_dim: int, q_norm_w, k_norm_w, rope: "RopeCache",
+                            start_pos: int, eps: float) -> None:
+    """``qkv_heads_int8`` on the layer-input RMSNorm folded in: ``hg`` = h *
+    input_norm and ``ss`` from ``linear_int8_residual`` (decoder.rs:789-810);
+    ``x_norm`` as in ``rms_norm_gate_up_swiglu_multiply_int8``."""
+    kv = n_kv_heads * head_dim
+    _need(q, F32, seq_len * n_heads * head_dim, "q")
+    _need(k_cache, F32, cache_rows * kv, "k_cache")
+    _need(v_cache, F32, cache_rows * kv, "v_cache")
+    for w, rows, name in ((wq, n_heads * head_dim, "wq"), (wk, kv, "wk"), (wv, kv, "wv")):
+        _need(w.data, I8, rows * in_dim, name)
+        _need(w.scales, F32, rows, name + ".scales")
+    _need(hg, F32, seq_len * in_dim, "hg")
+    _need(ss, F32, seq_len * norm_slices(in_dim), "ss")
+    _need(x_norm, F32, seq_len * in_dim, "x_norm")
+    _need(q_norm_w, F32, head_dim, "q_norm_w")
+    _need(k_norm_w, F32, head_dim, "k_norm_w")
+    if rope.head_dim != head_dim:
+        raise ValueError("RopeCache head_dim does not match")
+    _lib.call("qasr_rms_norm_qkv_heads_int8_f32", _ptr(q), _ptr(k_cache), _ptr(v_cache), cache_rows,
+              _ptr(wq.data), _ptr(wq.scales), _ptr(wk.data), _ptr(wk.scales), _ptr(wv.data), _ptr(wv.scales),
+              _ptr(hg), _ptr(ss), norm_slices(in_dim), norm_eps, _ptr(x_norm), seq_len, in_dim, n_heads,
+              n_kv_heads, head_dim, _ptr(q_norm_w), _ptr(k_norm_w), _ptr(rope.cos), _ptr(rope.sin), rope.cap,
+              start_pos, eps, _stream())
+
+
 def gate_up_swiglu_int8(out, x, w: QuantWeight, seq_len: int, in_dim: int, intermediate: int) -> None:
     """W8A32 gate/up projection on the interleaved weight + the decode loop's
     SwiGLU (decoder.rs:912-921), one launch; gate/up values are not stored."""

@@ -219,6 +219,47 @@ def test_qkv_heads_int8_validation():
     assert call(seq=0, q=NULL) == _lib.QASR_OK
 
 
+def test_prefill_norm_fold_validation():
+    """The prefill folds reject bad calls before any launch: null pointers, hg
+    without gain, and an ss slice count other than ceil(in_dim / 64)
+    (INVALID_ARG); the residual GEMM's shape limits (fewer than 8 tokens,
+    in_dim % 64 != 0: UNSUPPORTED); zero tokens is a no-op."""
+    inv, uns = _lib.QASR_ERR_INVALID_ARG, _lib.QASR_ERR_UNSUPPORTED
+    F = FAKE
+
+    def residual(*, h=F, ss=F, hg=NULL, gain=NULL, seq=64, in_dim=2048, out_dim=1024):
+        return rc("qasr_linear_int8_residual_f32", h, ss, hg, gain, F, F, F, seq, in_dim, out_dim, NULL)
+    assert residual(h=NULL) == inv
+    assert residual(ss=NULL) == inv
+    assert residual(hg=F) == inv and "go together" in last_error()
+    assert residual(gain=F) == inv
+    assert residual(seq=7) == uns and "seq_len >= 8" in last_error()
+    assert residual(in_dim=1000) == uns
+    assert residual(seq=0, h=NULL) == _lib.QASR_OK
+
+    def gate_up(*, hg=F, ss=F, slices=16, xn=F, seq=64, in_dim=1024):
+        return rc("qasr_rms_norm_gate_up_swiglu_multiply_int8_f32", F, hg, ss, slices, 1e-6, xn, F, F, seq,
+                  in_dim, 3072, NULL)
+    assert gate_up(hg=NULL) == inv
+    assert gate_up(ss=NULL) == inv
+    assert gate_up(xn=NULL) == inv
+    assert gate_up(slices=17) == inv and "ceil(in_dim / 64)" in last_error()
+    assert gate_up(seq=0, ss=NULL) == _lib.QASR_OK
+
+    # (q, k_cache, v_cache, cache_rows, wq, sq, wk, sk, wv, sv, hg, ss, ss_slices, norm_eps, x_norm, seq_len,
+    #  in_dim, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, cos, sin, table_rows, start_pos, eps, stream)
+    def qkv(*, ss=F, slices=16, xn=F, seq=64, hd=128, start=0):
+        return rc("qasr_rms_norm_qkv_heads_int8_f32", F, F, F, 1024, F, F, F, F, F, F, F, ss, slices, 1e-6, xn,
+                  seq, 1024, 16, 8, hd, F, F, F, F, 1024, start, 1e-6, NULL)
+    assert qkv(ss=NULL) == inv
+    assert qkv(xn=NULL) == inv
+    assert qkv(slices=8) == inv
+    assert qkv(start=1000) == inv and "exceed the cache" in last_error()
+    assert qkv(hd=64) == uns
+    assert qkv(seq=7) == uns
+    assert qkv(seq=0, ss=NULL) == _lib.QASR_OK
+
+
 def test_fused_norm_projection_validation():
     """The fused add + RMSNorm + projection entry points reject, before any
     launch: an h_out that overlaps x or delta (other workgroups still read the

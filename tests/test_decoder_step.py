@@ -246,23 +246,25 @@ def _load(tmp_path, w, L, dev):
         return qint8.load_decoder_int8(qf, dims, dev)
 
 
-@pytest.mark.parametrize("fuse_heads", [True, False])
+@pytest.mark.parametrize("fuse_heads,fuse_norms", [(True, True), (False, True), (True, False), (False, False)])
 @pytest.mark.parametrize("H,I", [(1024, 3072), (2048, 6144)])
-def test_prefill_then_decode_matches_the_oracle(tmp_path, dev, H, I, fuse_heads):
+def test_prefill_then_decode_matches_the_oracle(tmp_path, dev, H, I, fuse_heads, fuse_norms):
     """The device prefill (decoder.rs:751-847) of two chunks -- 37 rows at
     position 0 (ragged matrix-core GEMM tiles), then 20 rows at 37 -- against
     the oracle's restatement: the residual stream after the last layer and
     every cache row, then a decode step over the prefilled cache (token,
-    logits), with q/k/v and the heads in one launch or two. Tolerance as for
-    the decode step (chained kernels, 1e-4)."""
+    logits), with q/k/v and the heads in one launch or two, and the residual
+    adds and RMSNorms folded into the GEMMs or run as the reference's separate
+    ops. Tolerance as for the decode step (chained kernels, 1e-4)."""
     from qwenasr_amd.decoder import DecoderInt8
 
     L, nq, nk, hd, vocab = 2, 16, 8, 128, 1000
     r = np.random.default_rng([35, H])
     w = small_decoder(r, H, I, L, nq, nk, hd, vocab)
     dec = DecoderInt8(_load(tmp_path, w, L, dev), H, I, L, nq, nk, hd, max_seq=64, device=dev,
-                      fuse_prefill_heads=fuse_heads)
+                      fuse_prefill_heads=fuse_heads, fuse_prefill_norms=fuse_norms)
     assert dec.prefill_heads_fused(37) == fuse_heads
+    assert dec.prefill_norms_folded(37) == fuse_norms
     kv = nk * hd
     kc = np.zeros((L, 128, kv), np.float32)
     vc = np.zeros_like(kc)
@@ -300,7 +302,8 @@ def test_graph_replays_equal_the_eager_calls(tmp_path, dev):
     Each of three replays, with the outputs overwritten by eager fills and the
     device synchronised in between, must give the eager call's results bit for
     bit: decode (fused and unfused, key splits at position 300) and a 64-token
-    prefill (matrix-core GEMMs, cache rows of every layer)."""
+    prefill (matrix-core GEMMs, cache rows of every layer; the residual adds
+    and RMSNorms folded into the GEMMs or not)."""
     from qwenasr_amd.decoder import DecoderInt8
 
     H, I, L, nq, nk, hd, vocab = 2048, 6144, 2, 16, 8, 128, 1000
@@ -353,12 +356,14 @@ def test_graph_replays_equal_the_eager_calls(tmp_path, dev):
 
     T = 64
     e = torch.randn(T * H, device=dev, generator=gen)
-    for fuse_heads in (False, True):
-        d = DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=512, device=dev, fuse_prefill_heads=fuse_heads)
+    for fuse_heads, fuse_norms in ((False, False), (True, False), (True, True)):
+        d = DecoderInt8(weights, H, I, L, nq, nk, hd, max_seq=512, device=dev, fuse_prefill_heads=fuse_heads,
+                        fuse_prefill_norms=fuse_norms)
         d.prepare_prefill(0, T)
 
         def prefill_at_0():
             d.kv.len = 0  # every call (and replay) prefills the same chunk at position 0
             d.prefill(e, T, 0)
 
-        check(d, prefill_at_0, ("px",), slice(0, T), f"prefill fuse_prefill_heads={fuse_heads}")
+        check(d, prefill_at_0, ("px",), slice(0, T),
+              f"prefill fuse_prefill_heads={fuse_heads} fuse_prefill_norms={fuse_norms}")

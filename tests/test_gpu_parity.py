@@ -352,6 +352,143 @@ def test_qkv_heads_int8_equals_unfused(dev, seq, H, start, cache_rows, exact, nq
                      "v rows vs oracle")
 
 
+def slice_sums_of_squares(h, seq, hidden):
+    """Per token, the float64 sum of squares of each 64-column slice of h."""
+    a = h.reshape(seq, hidden).astype(np.float64) ** 2
+    n = (hidden + 63) // 64
+    return np.stack([a[:, 64 * s:64 * s + 64].sum(axis=1) for s in range(n)], axis=1)
+
+
+@pytest.mark.parametrize("seq,in_dim,out_dim,exact", [
+    (512, 2048, 1024, True),   # 0.6B o at 512 tokens: the split-K 64 x 32 tile, as the plain launch
+    (512, 3072, 1024, True),   # 0.6B down
+    (100, 2048, 2048, False),  # ragged token tile (the plain launch takes 32 x 32 tiles)
+    (37, 1088, 1000, False),   # in_dim % 128 = 64; the last 64-row slice holds 40 rows
+])
+def test_linear_int8_residual(dev, seq, in_dim, out_dim, exact):
+    """The prefill's o / down projection with its residual add folded in
+    (decoder.rs:821-822, 837-838): h equals h + linear_nobias_int8 (fp32 add,
+    the reference's add_inplace) bit for bit where the plain launch takes the
+    same split-K tile, else within the fp32 tolerance; the sums of squares of
+    the updated 64-row slices match float64 sums to 2e-5 (fp32 sums of 64
+    terms); hg is the updated h times the gain, bit for bit."""
+    from qwenasr_amd import kernels as K
+
+    r = rng(43, seq, in_dim, out_dim)
+    x = normal(r, seq * in_dim)
+    wq, sc = make_qweight(r, out_dim, in_dim)
+    h0 = normal(r, seq * out_dim)
+    w = K.QuantWeight(dev_t(wq, dev), dev_t(sc, dev), out_dim, in_dim)
+    xt, ht = dev_t(x, dev), dev_t(h0, dev)
+    ns = K.norm_slices(out_dim)
+    ss = torch.full((seq * ns,), 7.0, device=dev)
+    gain = normal(r, out_dim, 0.1, 1.0)
+    hg = torch.full((seq * out_dim,), 7.0, device=dev)
+    K.linear_int8_residual(ht, ss, xt, w, seq, in_dim, out_dim, hg, dev_t(gain, dev))
+    y = torch.empty(seq * out_dim, device=dev)
+    K.linear_nobias_int8(y, xt, w.data, w.scales, seq, in_dim, out_dim)
+    got, ref = host(ht), h0 + host(y)
+    if exact:
+        np.testing.assert_array_equal(got, ref)
+    else:
+        assert_close(got, ref, RTOL, ATOL, "h")
+    np.testing.assert_allclose(host(ss).reshape(seq, ns), slice_sums_of_squares(got, seq, out_dim), rtol=2e-5)
+    np.testing.assert_array_equal(host(hg).reshape(seq, out_dim), got.reshape(seq, out_dim) * gain)
+    h2 = dev_t(h0, dev)
+    K.linear_int8_residual(h2, ss, xt, w, seq, in_dim, out_dim)  # without hg
+    np.testing.assert_array_equal(host(h2), got)
+    if seq <= 128:
+        y_ref = oracle.linear_nobias_int8(x, wq, sc, seq, in_dim, out_dim)
+        assert_close(got, h0 + y_ref, RTOL, ATOL, "h vs oracle")
+    with pytest.raises(K.QasrError, match="seq_len >= 8"):
+        K.linear_int8_residual(ht, ss, xt, w, 7, in_dim, out_dim)
+
+
+@pytest.mark.parametrize("seq,H,I,folded", [
+    (512, 1024, 3072, True),    # 0.6B at 512 tokens: the double-buffered 192-row tile
+    (1024, 1024, 3072, True),   # the single-buffered 128-row tile
+    (1024, 2048, 6144, True),   # the 256-row tile
+    (37, 1024, 3072, False),    # too few tiles for the LDS-staged kernels: x_norm = hg * rinv + the plain launch
+])
+def test_rms_norm_gate_up_swiglu_multiply_int8(dev, seq, H, I, folded):
+    """The prefill post-attention RMSNorm folded into the gate/up GEMM + SwiGLU
+    (decoder.rs:826-833): the GEMM reads hg = h * gain and multiplies each
+    token's outputs by its 1 / rms from per-slice sums of squares; within the
+    fp32 tolerance of rms_norm + gate_up_swiglu_multiply_int8 (1 / rms is
+    factored out of the dot products and its sum added in another order), on
+    the folded kernels and on the fallback (x_norm = hg * rinv, then the plain
+    launch)."""
+    from qwenasr_amd import kernels as K
+
+    eps = 1e-6
+    r = rng(47, seq, H, I)
+    h = normal(r, seq * H)
+    g = normal(r, H, 0.1, 1.0)
+    wq, sc = make_qweight(r, 2 * I, H)
+    w = K.QuantWeight(dev_t(wq, dev), dev_t(sc, dev), 2 * I, H)
+    ss = slice_sums_of_squares(h, seq, H).astype(np.float32)
+    ht, gt = dev_t(h, dev), dev_t(g, dev)
+    hg = dev_t((h.reshape(seq, H) * g).ravel(), dev)
+    out = torch.full((seq * I,), 7.0, device=dev)
+    xn = torch.full((seq * H,), 7.0, device=dev)
+    K.rms_norm_gate_up_swiglu_multiply_int8(out, hg, dev_t(ss.ravel(), dev), eps, xn, w, seq, H, I)
+    xn2 = torch.empty(seq * H, device=dev)
+    ref = torch.empty(seq * I, device=dev)
+    K.rms_norm(xn2, ht, gt, seq, H, eps)
+    K.gate_up_swiglu_multiply_int8(ref, xn2, w, seq, H, I)
+    assert_close(host(out), host(ref), RTOL, ATOL, "gate/up + SwiGLU")
+    if folded:
+        assert (host(xn) == 7.0).all()  # not used
+    else:
+        assert_close(host(xn), host(xn2), RTOL, ATOL, "x_norm")
+
+
+@pytest.mark.parametrize("seq,H,start,cache_rows", [
+    (512, 1024, 0, 1024),    # 0.6B prefill chunk: the double-buffered tile
+    (1000, 1024, 24, 1536),  # the single-buffered tile
+    (100, 2048, 37, 512),    # ragged token tile
+])
+def test_rms_norm_qkv_heads_int8(dev, seq, H, start, cache_rows):
+    """The prefill layer-input RMSNorm folded into the q/k/v + heads GEMM
+    (decoder.rs:789-810), reading hg = h * gain with each token's 1 / rms from
+    per-slice sums of squares: within the fp32 tolerance of rms_norm followed
+    by qkv_heads_int8 (q, and the chunk's k/v cache rows); other cache rows
+    keep their contents."""
+    from qwenasr_amd import kernels as K
+
+    nq, nk, hd, eps = 16, 8, 128, 1e-6
+    kv = nk * hd
+    r = rng(53, seq, H, start)
+    h = normal(r, seq * H)
+    g = normal(r, H, 0.1, 1.0)
+    mats = [make_qweight(r, n, H) for n in (nq * hd, kv, kv)]
+    ws = [K.QuantWeight(dev_t(wq, dev), dev_t(sc, dev), n, H) for (wq, sc), n in zip(mats, (nq * hd, kv, kv))]
+    qw, kw = normal(r, hd, 0.1, 1.0), normal(r, hd, 0.1, 1.0)
+    rope = K.RopeCache(dev)
+    rope.ensure(start + seq, hd, 1e6)
+    ht, gt, qwt, kwt = dev_t(h, dev), dev_t(g, dev), dev_t(qw, dev), dev_t(kw, dev)
+    ss = dev_t(slice_sums_of_squares(h, seq, H).astype(np.float32).ravel(), dev)
+    hg = dev_t((h.reshape(seq, H) * g).ravel(), dev)
+    scratch = torch.full((seq * H,), 7.0, device=dev)
+
+    q1 = torch.full((seq * nq * hd,), 7.0, device=dev)
+    kc1 = torch.full((cache_rows * kv,), 7.0, device=dev)
+    vc1 = torch.full((cache_rows * kv,), 7.0, device=dev)
+    K.rms_norm_qkv_heads_int8(q1, kc1, vc1, cache_rows, *ws, hg, ss, eps, scratch, seq, H, nq, nk, hd, qwt, kwt,
+                              rope, start, eps)
+    xn = torch.empty(seq * H, device=dev)
+    K.rms_norm(xn, ht, gt, seq, H, eps)
+    q2 = torch.full((seq * nq * hd,), 7.0, device=dev)
+    kc2 = torch.full((cache_rows * kv,), 7.0, device=dev)
+    vc2 = torch.full((cache_rows * kv,), 7.0, device=dev)
+    K.qkv_heads_int8(q2, kc2, vc2, cache_rows, *ws, xn, seq, H, nq, nk, hd, qwt, kwt, rope, start, eps)
+    for a, b, what in ((q1, q2, "q"), (kc1, kc2, "k cache"), (vc1, vc2, "v cache")):
+        assert_close(host(a), host(b), RTOL, ATOL, what)
+    others = np.r_[0:start, start + seq:cache_rows]
+    assert (host(kc1).reshape(cache_rows, kv)[others] == 7.0).all()
+    assert (host(scratch) == 7.0).all()  # the folded kernels do not need x_norm
+
+
 def test_head_rms_norm_rope_kv_per_stream(dev):
     """Batched decode: row s is stream s at its own position, each stream with
     its own [cache_rows, kv_dim] block; a position past the cache leaves that
