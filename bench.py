@@ -749,10 +749,11 @@ class DecodeStepBatchedW8A8(DecodeStepBatched):
 class PrefillStep(Workload):
     name = "prefill_step"
     description = ("qwen3-asr-0.6b INT8 prefill of a 512-token chunk at position 0, fully on the device "
-                   "(decoder.rs:751-847): 28 layers of RMSNorm (fused with the residual add), q/k/v "
-                   "(one bf16x3 matrix-core GEMM) with q/k norm+RoPE+KV store of 512 rows in its epilogue, "
-                   "causal attention "
-                   "(fp32 matrix cores), o, add+RMSNorm, gate/up, prefill SwiGLU, down; last residual add")
+                   "(decoder.rs:751-847): 28 layers of q/k/v (one bf16x3 matrix-core GEMM with the input "
+                   "RMSNorm folded in) with q/k norm+RoPE+KV store of 512 rows in its epilogue, causal "
+                   "attention (fp32 matrix cores), o with the residual add in its epilogue, gate/up with the "
+                   "post-attention RMSNorm folded in + prefill SwiGLU, down with the residual add; layer 0's "
+                   "input RMSNorm as its own launch")
     unit_tokens = 512
     dtype = "int8/f32"
     T = 512
