@@ -753,9 +753,15 @@ void launch_attention_split(float* out, const float* q, const float* k, const fl
 //     the 8 output tiles jt (whole 128-byte lines per load instruction); the
 //     result sits at lane j+16h, register r = O[column 4h+r][that dim].
 typedef float v4f __attribute__((ext_vector_type(4)));
-// Key-tile streams per workgroup. About 200 registers per wave allow two
-// waves per SIMD, so a CU holds two 4-wave workgroups (measured at T=512,
-// 0.6B: 30.5 us; 8 waves per workgroup, one workgroup per CU: 47.7 us).
+// Key-tile streams per workgroup. Two waves per SIMD, so a CU holds two 4-wave
+// workgroups (measured at T=512, 0.6B: 30.5 us; 8 waves per workgroup, one
+// workgroup per CU: 47.7 us). The kernel asks for that occupancy explicitly:
+// the compiler then keeps the accumulators in VGPRs (222, no AGPRs) instead
+// of 190 VGPRs + 64 AGPRs with accumulator copies between the two files
+// (prefill step 3004 -> 2985 us). Loading all of a tile's V rows where the
+// source issues them (pinned with scheduling fences) takes the last registers
+// and measured slower in the step (3006 us): the compiler loads each V block
+// just before its products, which the step's L2-resident K/V rows tolerate.
 constexpr int kPrefillWaves = 4;
 
 // dims 16c + 4h .. 16c + 4h + 3 (c = 0..7) of a row, for lane group h (p points
@@ -791,7 +797,7 @@ QASR_DEV void ld_v_block(float (&dst)[32], const float* vbase, size_t kv_stride,
 }
 
 template <int G, int NW>
-__global__ __launch_bounds__(64 * NW) void attention_prefill_mfma_kernel(
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_prefill_mfma_kernel(
     float* __restrict__ out, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, int seq_q, int seq_k, int nk, float scale, int q_offset) {
   constexpr int HD = 128;
