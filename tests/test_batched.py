@@ -262,6 +262,83 @@ def test_batched_decode_step_matches_the_oracle_per_stream(tmp_path, dev, H, I, 
     assert torch.equal(dec.positions.cpu(), torch.from_numpy(pos + 2))
 
 
+def test_batched_decode_step_at_the_benchmarked_size_matches_the_oracle(dev):
+    """The 256-stream step that bench.py times (1.7B shapes: hidden 2048, 28
+    layers, vocabulary 151936; the reference's W8A32 arithmetic) against the
+    oracle's decode step (decoder.rs:848-965) for four of its streams, at
+    positions 0, 511, 512 and 639 (one key; one whole 512-key chunk; one key
+    into a second chunk; the last cache row), the other 252 streams at random
+    positions: the final hidden state at rel/abs 1e-4 as in the small-batch
+    test, the token, and all 151936 logits and the new K/V rows of all 28
+    layers at rel 1e-4 + abs 1e-4 x the RMS of their row (the logits, one
+    layer's K or V row): each is a dot product whose error is bounded by its
+    weight row's norm times the error of the normed state it reads (which 28
+    chained layers bring to ~1e-5 relative), not by its own value, which
+    cancels to near 0 for some elements. Each stream's cache holds 640 rows here (2048, as in the
+    benchmark, would take 120 GB of device memory for the same kernels and
+    launch shapes)."""
+    from oracle.decoder import decode_int8_step
+    from qwenasr_amd import kernels as K
+    from qwenasr_amd.decoder import DecoderInt8Batched
+
+    H, I, L, B, rows, vocab, TOL = 2048, 6144, 28, 256, 640, 151936, 1e-4
+    kv = NK * HD
+    gen = torch.Generator(device=dev).manual_seed(71)
+
+    def randn(n, scale=1.0, mean=0.0):
+        return torch.randn(n, generator=gen, device=dev) * scale + mean
+
+    def qw(o, i):
+        q = torch.randint(-127, 128, (o * i,), generator=gen, device=dev, dtype=torch.int8)
+        return K.QuantWeight(q, randn(o, 1e-4, 1e-3).abs_(), o, i)
+
+    print("[batched full size] weights", flush=True)
+    layers = [{"wq": qw(NQ * HD, H), "wk": qw(kv, H), "wv": qw(kv, H), "wo": qw(H, NQ * HD),
+               "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": randn(HD, 0.1, 1.0), "k_norm": randn(HD, 0.1, 1.0),
+               "input_norm": randn(H, 0.1, 1.0), "post_attn_norm": randn(H, 0.1, 1.0)} for _ in range(L)]
+    weights = {"layers": layers, "norm": randn(H, 0.1, 1.0), "lm_head": qw(vocab, H)}
+    dec = DecoderInt8Batched(weights, H, I, L, B, rows, device=dev)
+    for l in range(L):
+        dec.k[l].normal_(generator=gen)
+        dec.v[l].normal_(generator=gen)
+    pos = torch.randint(0, rows, (B,), generator=gen, dtype=torch.int32, device=dev).cpu().numpy()
+    sampled = {0: 0, 97: 511, 180: 512, 255: rows - 1}
+    for m, p in sampled.items():
+        pos[m] = p
+    dec.positions.copy_(torch.from_numpy(pos))
+    x = randn(B * H)
+    print("[batched full size] device step", flush=True)
+    dec.decode(x)
+    torch.cuda.synchronize()
+    xn = dec.x_norm.view(B, H).cpu().numpy()
+    lg = dec.logits.view(B, vocab).cpu().numpy()
+    tok = dec.tokens.cpu().numpy()
+    xh = x.view(B, H).cpu().numpy()
+
+    def host(w):
+        return (w.data.view(w.out_dim, w.in_dim).cpu().numpy(), w.scales.cpu().numpy())
+
+    w_np = {"layers": [{k: host(v) if isinstance(v, K.QuantWeight) else v.cpu().numpy() for k, v in lw.items()}
+                       for lw in layers],
+            "norm": weights["norm"].cpu().numpy(), "lm_head": host(weights["lm_head"])}
+    for m, p in sampled.items():
+        print(f"[batched full size] oracle stream {m} at position {p}", flush=True)
+        kc = np.stack([dec.k[l].view(B, rows, kv)[m].cpu().numpy() for l in range(L)])
+        vc = np.stack([dec.v[l].view(B, rows, kv)[m].cpu().numpy() for l in range(L)])
+        k_dev, v_dev = kc[:, p].copy(), vc[:, p].copy()  # the step's new rows; the oracle rewrites them
+        t_ref, xn_ref, lg_ref = decode_int8_step(w_np, kc, vc, p, xh[m], NQ, NK, HD, threads=16)
+        np.testing.assert_allclose(xn[m], xn_ref, rtol=TOL, atol=TOL, err_msg=f"stream {m}")
+        for got, ref, what in ((lg[m][None], lg_ref[None], "logits"), (k_dev, kc[:, p], "k rows"),
+                               (v_dev, vc[:, p], "v rows")):
+            rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2, axis=1, keepdims=True))
+            err = np.abs(got.astype(np.float64) - ref)
+            print(f"[batched full size] stream {m} {what}: max |diff| / row RMS {(err / rms).max():.3g}", flush=True)
+            assert (err <= TOL * np.abs(ref) + TOL * rms).all(), f"{what} stream {m}"
+        top2 = np.sort(lg_ref)[-2:]
+        if top2[1] - top2[0] > 2 * TOL * (1 + abs(top2[1])):
+            assert int(tok[m]) == t_ref, m
+
+
 class _RoundingRecorder:
     """Keeps a copy of every per-row int8 activation (values and scales) that
     the device computes through K.add_rms_norm_quant, K.quantize_rows_i8 and
