@@ -262,10 +262,14 @@ def test_batched_decode_step_matches_the_oracle_per_stream(tmp_path, dev, H, I, 
     assert torch.equal(dec.positions.cpu(), torch.from_numpy(pos + 2))
 
 
-def test_batched_decode_step_at_the_benchmarked_size_matches_the_oracle(dev):
-    """The 256-stream step that bench.py times (1.7B shapes: hidden 2048, 28
-    layers, vocabulary 151936; the reference's W8A32 arithmetic) against the
-    oracle's decode step (decoder.rs:848-965) for four of its streams, at
+@pytest.mark.parametrize("w8a8", [False, True])
+def test_batched_decode_step_at_the_benchmarked_size_matches_the_oracle(dev, monkeypatch, w8a8):
+    """The 256-stream steps that bench.py times (1.7B shapes: hidden 2048, 28
+    layers, vocabulary 151936; the reference's W8A32 arithmetic, and the W8A8
+    form with its W8A8 lm_head) against the oracle's decode step
+    (decoder.rs:848-965; W8A8: oracle.decoder.decode_w8a8_step with the
+    device's rounding adopted at near-ties as in the small-batch W8A8 test, at
+    most one element per rounding point on average) for four of its streams, at
     positions 0, 511, 512 and 639 (one key; one whole 512-key chunk; one key
     into a second chunk; the last cache row), the other 252 streams at random
     positions: the final hidden state at rel/abs 1e-4 as in the small-batch
@@ -277,7 +281,7 @@ def test_batched_decode_step_at_the_benchmarked_size_matches_the_oracle(dev):
     cancels to near 0 for some elements. Each stream's cache holds 640 rows here (2048, as in the
     benchmark, would take 120 GB of device memory for the same kernels and
     launch shapes)."""
-    from oracle.decoder import decode_int8_step
+    from oracle.decoder import decode_int8_step, decode_w8a8_step
     from qwenasr_amd import kernels as K
     from qwenasr_amd.decoder import DecoderInt8Batched
 
@@ -297,7 +301,8 @@ def test_batched_decode_step_at_the_benchmarked_size_matches_the_oracle(dev):
                "gate_up": qw(2 * I, H), "down": qw(H, I), "q_norm": randn(HD, 0.1, 1.0), "k_norm": randn(HD, 0.1, 1.0),
                "input_norm": randn(H, 0.1, 1.0), "post_attn_norm": randn(H, 0.1, 1.0)} for _ in range(L)]
     weights = {"layers": layers, "norm": randn(H, 0.1, 1.0), "lm_head": qw(vocab, H)}
-    dec = DecoderInt8Batched(weights, H, I, L, B, rows, device=dev)
+    dec = DecoderInt8Batched(weights, H, I, L, B, rows, device=dev, w8a8=w8a8)
+    assert dec.lm_head_w8a8 == w8a8
     for l in range(L):
         dec.k[l].normal_(generator=gen)
         dec.v[l].normal_(generator=gen)
@@ -307,9 +312,15 @@ def test_batched_decode_step_at_the_benchmarked_size_matches_the_oracle(dev):
         pos[m] = p
     dec.positions.copy_(torch.from_numpy(pos))
     x = randn(B * H)
-    print("[batched full size] device step", flush=True)
+    if w8a8:
+        rec = _RoundingRecorder(monkeypatch, K)
+    print(f"[batched full size] device step w8a8={w8a8}", flush=True)
     dec.decode(x)
     torch.cuda.synchronize()
+    if w8a8:
+        points = 4 * L + 1
+        assert len(rec.seen) == points
+        gq, gs = [q for q, _ in rec.seen], [sc for _, sc in rec.seen]
     xn = dec.x_norm.view(B, H).cpu().numpy()
     lg = dec.logits.view(B, vocab).cpu().numpy()
     tok = dec.tokens.cpu().numpy()
@@ -326,7 +337,17 @@ def test_batched_decode_step_at_the_benchmarked_size_matches_the_oracle(dev):
         kc = np.stack([dec.k[l].view(B, rows, kv)[m].cpu().numpy() for l in range(L)])
         vc = np.stack([dec.v[l].view(B, rows, kv)[m].cpu().numpy() for l in range(L)])
         k_dev, v_dev = kc[:, p].copy(), vc[:, p].copy()  # the step's new rows; the oracle rewrites them
-        t_ref, xn_ref, lg_ref = decode_int8_step(w_np, kc, vc, p, xh[m], NQ, NK, HD, threads=16)
+        if w8a8:
+            log = []
+            kc32, vc32 = kc.copy(), vc.copy()
+            t_ref, xn_ref, lg_ref = decode_w8a8_step(w_np, kc, vc, p, xh[m], NQ, NK, HD, threads=16,
+                                                     quant=_steered_quant(gq, gs, m, log), lm_head_w8a8=True)
+            print(f"[batched full size] stream {m}: {sum(log)} roundings adopted over {points} points", flush=True)
+            assert sum(log) <= points, log
+            _, xn32, _ = decode_int8_step(w_np, kc32, vc32, p, xh[m], NQ, NK, HD, threads=16)
+            assert np.abs(xn32 - xn[m]).max() > 10 * TOL * (1 + np.abs(xn32).max())  # really rounded
+        else:
+            t_ref, xn_ref, lg_ref = decode_int8_step(w_np, kc, vc, p, xh[m], NQ, NK, HD, threads=16)
         np.testing.assert_allclose(xn[m], xn_ref, rtol=TOL, atol=TOL, err_msg=f"stream {m}")
         for got, ref, what in ((lg[m][None], lg_ref[None], "logits"), (k_dev, kc[:, p], "k rows"),
                                (v_dev, vc[:, p], "v rows")):
