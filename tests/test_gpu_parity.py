@@ -409,6 +409,7 @@ def test_linear_int8_residual(dev, seq, in_dim, out_dim, exact):
     (1024, 1024, 3072, True),   # the single-buffered 128-row tile
     (1024, 2048, 6144, True),   # the 256-row tile
     (37, 1024, 3072, False),    # too few tiles for the LDS-staged kernels: x_norm = hg * rinv + the plain launch
+    (512, 2112, 3072, False),   # 33 slices (not a multiple of 4): the same fallback
 ])
 def test_rms_norm_gate_up_swiglu_multiply_int8(dev, seq, H, I, folded):
     """The prefill post-attention RMSNorm folded into the gate/up GEMM + SwiGLU
@@ -447,6 +448,7 @@ def test_rms_norm_gate_up_swiglu_multiply_int8(dev, seq, H, I, folded):
     (512, 1024, 0, 1024),    # 0.6B prefill chunk: the double-buffered tile
     (1000, 1024, 24, 1536),  # the single-buffered tile
     (100, 2048, 37, 512),    # ragged token tile
+    (200, 2112, 5, 256),     # 33 slices: x_norm = hg * rinv, then the plain launch
 ])
 def test_rms_norm_qkv_heads_int8(dev, seq, H, start, cache_rows):
     """The prefill layer-input RMSNorm folded into the q/k/v + heads GEMM
@@ -486,7 +488,10 @@ def test_rms_norm_qkv_heads_int8(dev, seq, H, start, cache_rows):
         assert_close(host(a), host(b), RTOL, ATOL, what)
     others = np.r_[0:start, start + seq:cache_rows]
     assert (host(kc1).reshape(cache_rows, kv)[others] == 7.0).all()
-    assert (host(scratch) == 7.0).all()  # the folded kernels do not need x_norm
+    if H // 64 <= 32 and (H // 64) % 4 == 0:
+        assert (host(scratch) == 7.0).all()  # the folded kernels do not need x_norm
+    else:
+        assert_close(host(scratch), host(xn), RTOL, ATOL, "x_norm (fallback)")
 
 
 def test_head_rms_norm_rope_kv_per_stream(dev):
