@@ -126,9 +126,10 @@ __global__ __launch_bounds__(256) void w8a32_vec_kernel(float* y, const float* x
 enum RowsEpi { kEpiRows = 0, kEpiArgmax = 1, kEpiSwiglu = 2 };
 
 // With NORM the input row is not read as given: every workgroup first forms
-// h = x (+ delta) and the RMSNorm h * rinv * gain of it in LDS, with the same
-// element assignment (thread t: float4s t, t + 256, ...) and the same block
-// reduction as rms_norm_vec_kernel<256, KCH>, so the row equals that kernel's
+// h = x (+ delta) and the RMSNorm h * rinv * gain of it in LDS, with the
+// element order of the standalone kernel for that row length
+// (rms_norm_vec_kernel<256, KCH>: thread t sums float4s t, t + 256, ...; at
+// 2048 floats rms_norm_vec_kernel<512, 1>), so the row equals that kernel's
 // output bit for bit; workgroup 0 also writes h to h_out.
 struct RowNorm {
   const float* x;
@@ -181,8 +182,8 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
   float4 xv[KCH][4];
   if constexpr (NORM) {
     __shared__ float4 xs[256 * KCH];
-    __shared__ float red[256 / kWave];
-    float ss = 0.0f;
+    __shared__ float red[2 * 256 / kWave];
+    float ss = 0.0f, ss_hi = 0.0f;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = threadIdx.x + 256 * i;
@@ -192,12 +193,30 @@ QASR_DEV void w8a32_rows_body(float* y, const float* x, const int8_t* w, const f
       }
       if (rn.h_out && blockIdx.x == 0) st4(rn.h_out, c, a);
       nx[i] = a;
-      ss += a.x * a.x;
-      ss += a.y * a.y;
-      ss += a.z * a.z;
-      ss += a.w * a.w;
+      float& s = KCH == 2 && i == 1 ? ss_hi : ss;
+      s += a.x * a.x;
+      s += a.y * a.y;
+      s += a.z * a.z;
+      s += a.w * a.w;
     }
-    ss = block_sum<256>(ss, red);
+    if constexpr (KCH == 2) {
+      // A 2048-float row: rms_norm_vec_kernel<512, 1>'s order, where float4 c
+      // is lane c % 64 of wave c / 64 and the eight wave sums are added in
+      // wave order. Here wave w's two float4 halves are that kernel's waves w
+      // and w + 4.
+      ss = wave_sum(ss);
+      ss_hi = wave_sum(ss_hi);
+      if ((threadIdx.x & (kWave - 1)) == 0) {
+        red[threadIdx.x / kWave] = ss;
+        red[256 / kWave + threadIdx.x / kWave] = ss_hi;
+      }
+      __syncthreads();
+      ss = red[0];
+#pragma unroll
+      for (int i = 1; i < 2 * 256 / kWave; ++i) ss += red[i];
+    } else {
+      ss = block_sum<256>(ss, red);
+    }
     const float rinv = 1.0f / sqrtf(ss / (float)in_dim + rn.eps);
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {

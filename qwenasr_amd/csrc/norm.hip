@@ -345,7 +345,10 @@ int launch_rms(float* x, const float* delta, const float* w, float* out, int8_t*
   } else if (rs.nv == 1) {
     rms_norm_vec_kernel<256, 1, ADD, QUANT><<<grid, 256, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   } else if (rs.nv == 2) {
-    rms_norm_vec_kernel<256, 2, ADD, QUANT><<<grid, 256, 0, st>>>(x, delta, w, out, q, qs, h, eps);
+    // Rows of 1025-2048 floats take eight waves of one float4 each: the row's
+    // loads leave from all four SIMDs at once ([256,2048] with the int8
+    // epilogue: 5.8 us with four waves of two float4, 5.5 us with eight).
+    rms_norm_vec_kernel<512, 1, ADD, QUANT><<<grid, 512, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   } else if (rs.nv == 4) {
     rms_norm_vec_kernel<256, 4, ADD, QUANT><<<grid, 256, 0, st>>>(x, delta, w, out, q, qs, h, eps);
   } else {

@@ -58,44 +58,33 @@ QASR_DEV void head_of(const HeadArgs& a, long long gh, int hd, float** base, con
 }
 
 // KV mode: head gh is a q head (in place), a k head (read k_src, write the
-// cache) or a v head (copied to the cache). Returns the kind (0 q, 1 k, 2 v).
-QASR_DEV int head_kv_of(const HeadArgs& a, long long gh, int hd, const float** src, float** dst,
-                        const float** w, long long* row, long long* pos, bool* ok) {
-  int kind;
-  long long h = 0;
+// cache) or a v head (copied to the cache). head_kv_src resolves the source,
+// gain, row and kv head h without touching memory and returns the kind (0 q,
+// 1 k, 2 v); head_kv_dst places the result once the row's position p is known.
+QASR_DEV int head_kv_src(const HeadArgs& a, long long gh, int hd, const float** src,
+                         const float** w, long long* row, long long* h) {
+  *h = 0;
   if (gh < a.q_heads) {
-    kind = 0;
     *row = gh / a.nq;
-  } else if (gh < a.kv_heads_end) {
-    kind = 1;
-    const long long g = gh - a.q_heads;
-    *row = g / a.nk;
-    h = g - *row * a.nk;
-  } else {
-    kind = 2;
-    const long long g = gh - a.kv_heads_end;
-    *row = g / a.nk;
-    h = g - *row * a.nk;
-  }
-  const long long p = a.positions ? (long long)a.positions[*row] : a.start_pos + *row;
-  *pos = p;
-  *ok = p >= 0 && p < a.table_rows && p < a.cache_rows;
-  const long long stream = a.positions ? *row : 0;
-  const long long cache_off = ((stream * a.cache_rows + (*ok ? p : 0)) * a.nk + h) * hd;
-  if (kind == 0) {
     *src = a.q + gh * hd;
-    *dst = a.q + gh * hd;
     *w = a.qw;
-  } else if (kind == 1) {
-    *src = a.k_src + (gh - a.q_heads) * hd;
-    *dst = a.k_cache + cache_off;
-    *w = a.kw;
-  } else {
-    *src = a.v + (gh - a.kv_heads_end) * hd;
-    *dst = a.v_cache + cache_off;
-    *w = nullptr;
+    return 0;
   }
-  return kind;
+  const bool k = gh < a.kv_heads_end;
+  const long long g = gh - (k ? a.q_heads : a.kv_heads_end);
+  *row = g / a.nk;
+  *h = g - *row * a.nk;
+  *src = k ? a.k_src + g * hd : a.v + g * hd;
+  *w = k ? a.kw : nullptr;
+  return k ? 1 : 2;
+}
+
+QASR_DEV float* head_kv_dst(const HeadArgs& a, int kind, long long gh, int hd, long long row,
+                            long long h, long long p, bool ok) {
+  if (kind == 0) return a.q + gh * hd;
+  const long long stream = a.positions ? row : 0;
+  const long long cache_off = ((stream * a.cache_rows + (ok ? p : 0)) * a.nk + h) * hd;
+  return (kind == 1 ? a.k_cache : a.v_cache) + cache_off;
 }
 
 template <int HD, bool NORM, bool ROPE, bool KV = false>
@@ -114,42 +103,67 @@ __global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
   long long row;
   long long pos = 0;
   bool pos_ok = true;
+  int kind = 0;
+  long long kvh = 0;
   if constexpr (KV) {
-    const int kind = head_kv_of(a, gh, HD, &src, &base, &w, &row, &pos, &pos_ok);
-    if (kind == 2) {  // v: a plain copy into the cache (decoder.rs:550, 895)
-      if (pos_ok) {
-        st4_nt(base, sub, ld4_nt(src, sub));
-        st4_nt(base + HALF, sub, ld4_nt(src + HALF, sub));
-      }
-      return;  // the head's lane group leaves together
-    }
+    kind = head_kv_src(a, gh, HD, &src, &w, &row, &kvh);
   } else {
     head_of(a, gh, HD, &base, &w, &row);
     src = base;
   }
 
-  // Every load that does not depend on the head's statistics is issued here,
-  // so the row, gains and table rows are in flight together.
+  // Two memory round trips: the head row, gains and position together, then
+  // the table rows, the only loads that depend on another. The row and gains
+  // are issued first because the wait on the position (a load under a branch
+  // on `positions`) covers everything issued before it. The fences keep the
+  // scheduler from sinking the table loads next to the rotation.
+  float4 x1 = ld4_nt(src, sub);
+  float4 x2 = ld4_nt(src + HALF, sub);
   float4 w1, w2;
   if constexpr (NORM) {
-    w1 = ld4(w, sub);
-    w2 = ld4(w + HALF, sub);
+    if (!KV || kind != 2) {
+      w1 = ld4(w, sub);
+      w2 = ld4(w + HALF, sub);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (KV) {
+    pos = a.positions ? (long long)a.positions[row] : a.start_pos + row;
+  } else if constexpr (ROPE) {
+    pos = a.positions ? (long long)a.positions[row] : row;
   }
   float4 c1, c2, s1, s2;
-  if constexpr (ROPE) {
-    if constexpr (!KV) {
-      pos = a.positions ? (long long)a.positions[row] : row;
-      pos_ok = pos >= 0 && pos < a.table_rows;
-    }
+  if constexpr (KV) {
+    pos_ok = pos >= 0 && pos < a.table_rows && pos < a.cache_rows;
+    base = head_kv_dst(a, kind, gh, HD, row, kvh, pos, pos_ok);
+  } else if constexpr (ROPE) {
+    pos_ok = pos >= 0 && pos < a.table_rows;
+  }
+  if (ROPE && (!KV || kind != 2)) {
     const long long pr = pos_ok ? pos : 0;  // out-of-table rows read row 0, then become NaN
     const float* cr = a.cos_tab + pr * HD;
     const float* sr = a.sin_tab + pr * HD;
     c1 = ld4(cr, sub); c2 = ld4(cr + HALF, sub);
     s1 = ld4(sr, sub); s2 = ld4(sr + HALF, sub);
   }
-  float4 x1 = ld4_nt(src, sub);
-  float4 x2 = ld4_nt(src + HALF, sub);
-  head_norm_rope<HD, NORM, ROPE>(x1, x2, w1, w2, c1, c2, s1, s2, pos_ok, a.eps);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (KV) {
+    if (kind == 2) {  // v: a plain copy into the cache (decoder.rs:550, 895)
+      if (pos_ok) {
+        st4_nt(base, sub, x1);
+        st4_nt(base + HALF, sub, x2);
+      }
+      return;  // the head's lane group leaves together
+    }
+  }
+  // The rotation runs on every row (an out-of-table row rotates by table row
+  // 0) and is then replaced by NaN, so the table loads are used on every path.
+  head_norm_rope<HD, NORM, ROPE>(x1, x2, w1, w2, c1, c2, s1, s2, true, a.eps);
+  if (ROPE && !pos_ok) {
+    const float n = qnan();
+    x1 = make_float4(n, n, n, n);
+    x2 = x1;
+  }
   if (KV && !pos_ok && base != src) return;  // k head outside the cache: nothing written
   st4_nt(base, sub, x1);
   st4_nt(base + HALF, sub, x2);
