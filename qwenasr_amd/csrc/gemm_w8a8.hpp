@@ -651,6 +651,220 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// 96 x 128 tile (batch > 128). A workgroup owns 96 W rows x 128 tokens, so a CU
+// reads 192 KiB of W and 256 KiB of Xq: 448 KiB against the 192 x 64 tile's
+// 384 + 128 = 512 KiB. The 2 workgroups of a W tile sit on one XCD.
+//
+// Three MFMA waves each own two 16-row blocks over all 8 token tiles and the
+// whole K: every W byte is loaded by one wave, each B fragment read from LDS
+// feeds two MFMAs, and no partial sums change hands. The Xq tile (256 KiB) does
+// not fit in LDS: two loader waves stream it in 32 KiB chunks (4 k-steps x 128
+// tokens) through a ring of 3, with direct global->LDS loads. Each chunk is one
+// barrier: barrier c means chunk c has landed and every MFMA wave is done with
+// chunk c - 1, whose slot then takes chunk c + 2. A loader waits on its own
+// loads (vmcnt) before each barrier. The MFMA waves issue no direct LDS load,
+// so the compiler puts no drain of their W prefetch in front of their LDS
+// reads, and their barrier waits on LDS only.
+//
+// Chunk layout: token row t of a chunk is 256 bytes (16 slots of 16 bytes), and
+// LDS slot l of row t holds the row's data slot l ^ (t & 15), so the 16 tokens
+// of one B-fragment read hit 16 different bank groups. The SwiGLU epilogue is
+// the 192-row kernel's; results equal it bit for bit (int32 sums are exact).
+//
+// Measured at [256,2048] x [2048,12288]: 11.45 us against 12.1 us for the
+// 192 x 64 tile. Timing-only copies put 1.25 us on the W loads and 1.7 us on
+// the Xq loads; the rest is the launch, the MFMAs of the busiest SIMD (a third
+// of the tile: 6 row blocks do not split over 4 SIMDs without loading W twice)
+// and the SwiGLU epilogue (~1 us of transcendentals on 3 SIMDs).
+// ---------------------------------------------------------------------------
+constexpr int kT9BN = 96;                                // W rows per workgroup
+constexpr int kT9BM = 128;                               // tokens per workgroup
+constexpr int kT9BlocksPerWave = 2;                      // 16-row blocks per MFMA wave
+constexpr int kT9MfmaWaves = kT9BN / kPackRows / kT9BlocksPerWave;
+constexpr int kT9Loaders = 2;                            // loader waves
+constexpr int kT9Waves = kT9MfmaWaves + kT9Loaders;
+constexpr int kT9Ring = 3;                               // chunk slots
+constexpr int kT9ChunkBytes = kT9BM * kPkChunk;          // 32 KiB
+constexpr int kT9PiecesPerLoader = kT9ChunkBytes / 1024 / kT9Loaders;  // 1 KiB direct loads per chunk
+constexpr size_t kT9Lds = (size_t)kT9Ring * kT9ChunkBytes;
+constexpr int kT9Prefetch = 3;                           // k-steps of W in flight per MFMA wave
+constexpr int kT9OutPitch = 52;                          // staged output row pitch (floats)
+
+// s_waitcnt immediate that waits until at most n vector memory operations of
+// this wave are outstanding (LDS and export counters left free).
+constexpr int vmcnt_at_most(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+template <int KS>  // KS = K / 64 (16 or 32)
+__global__ __launch_bounds__(64 * kT9Waves) void gemm_w8a8_swiglu_t96_kernel(
+    float* __restrict__ out, const int8_t* __restrict__ wpk, const float* __restrict__ scales,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, int batch, int inter,
+    int n_tiles, int m_tiles) {
+  constexpr int K = KS * kPackK;
+  constexpr int NCH = K / kPkChunk;          // chunks (8 or 4)
+  constexpr int SPC = kPkChunk / kPackK;     // k-steps per chunk (4)
+  constexpr int PF = kT9Prefetch;
+  constexpr int RB = kT9BlocksPerWave;
+  static_assert(NCH >= kT9Ring - 1 && kT9Ring >= 2 && kT9Ring <= 4 &&
+                    kT9PiecesPerLoader * 1024 * kT9Loaders == kT9ChunkBytes &&
+                    (kT9Ring - 2) * kT9PiecesPerLoader <= 63,
+                "ring schedule: the chunks outstanding behind the one waited for fit vmcnt");
+  static_assert(kT9BM * kT9OutPitch * 4 <= (int)kT9Lds, "output staging fits the ring");
+  extern __shared__ __align__(16) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+
+  // Block b runs on XCD b % 8; the m_tiles blocks of one W tile share an XCD.
+  const int b = blockIdx.x;
+  int tile_n, tile_m;
+  if (n_tiles % kNumXcd == 0) {
+    const int slot = b / kNumXcd;
+    tile_m = slot % m_tiles;
+    tile_n = b % kNumXcd + kNumXcd * (slot / m_tiles);
+  } else {
+    tile_m = b % m_tiles;
+    tile_n = b / m_tiles;
+  }
+  const int m0 = tile_m * kT9BM;
+
+  v4i acc[RB][8];
+  float4 sc[RB];
+  float xsv[8];
+  if (wave >= kT9MfmaWaves) {
+    // Loader: 1 KiB piece p of a chunk is token rows 4p .. 4p + 3; lane l fills
+    // LDS slot l & 15 of row 4p + l / 16. Rows past the batch re-read row
+    // batch - 1 (valid memory); their results are never stored.
+    const int pw = wave - kT9MfmaWaves;
+    auto issue = [&](int c) {
+      int8_t* slot_base = lds + (c % kT9Ring) * kT9ChunkBytes;
+#pragma unroll
+      for (int i = 0; i < kT9PiecesPerLoader; ++i) {
+        const int piece = kT9PiecesPerLoader * pw + i;
+        const int row = 4 * piece + (lane >> 4);
+        const int data_slot = (lane & 15) ^ (row & 15);
+        const int src_row = m0 + row < batch ? m0 + row : batch - 1;
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(xq + (size_t)src_row * K + kPkChunk * c + 16 * data_slot),
+            (__attribute__((address_space(3))) void*)(slot_base + piece * 1024), 16, 0, 0);
+      }
+    };
+    constexpr int AHEAD = kT9Ring - 1;  // chunks issued beyond the one being read
+#pragma unroll
+    for (int c = 0; c < AHEAD; ++c) issue(c);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      // chunk c has landed once at most the chunks issued after it are outstanding
+      const int after = (c + AHEAD - 1 < NCH - 1 ? c + AHEAD - 1 : NCH - 1) - c;
+      if (after >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_at_most(2 * kT9PiecesPerLoader));
+      else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_at_most(kT9PiecesPerLoader));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_at_most(0));
+      asm volatile("s_barrier" ::: "memory");
+      // into the slot of chunk c - 1, which every MFMA wave has left
+      if (c + AHEAD < NCH) issue(c + AHEAD);
+    }
+  } else {
+    const int rb0 = tile_n * (kT9BN / kPackRows) + RB * wave;  // this wave's first 16-row block
+    const int8_t* wp = wpk + packed_tile_offset(rb0, 0, KS) + 16 * lane;
+    constexpr size_t ROW_TILE = (size_t)KS * 1024;
+    v4i wbuf[PF][RB];
+#pragma unroll
+    for (int d = 0; d < PF; ++d)
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+        wbuf[d][i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + i * ROW_TILE + d * 1024));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < RB; ++i) sc[i] = *reinterpret_cast<const float4*>(scales + 16 * (rb0 + i) + 4 * g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int m = m0 + 16 * j + r;
+      xsv[j] = xs[m < batch ? m : batch - 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    // B fragment of token tile j at k-step s
+    auto bfrag = [&](int s, int j) -> v4i {
+      const int slot = SPC * (s % SPC) + g;
+      return *reinterpret_cast<const v4i*>(lds + ((s / SPC) % kT9Ring) * kT9ChunkBytes +
+                                           (16 * j + r) * kPkChunk + 16 * (slot ^ r));
+    };
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      lds_barrier();  // chunk c is in LDS; chunk c - 1's slot is released
+      v4i bcur[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bcur[j] = bfrag(SPC * c, j);
+#pragma unroll
+      for (int q = 0; q < SPC; ++q) {
+        const int s = SPC * c + q;
+        v4i a[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          a[i] = wbuf[s % PF][i];
+          if (s + PF < KS)
+            wbuf[s % PF][i] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i*>(wp + i * ROW_TILE + (s + PF) * 1024));
+        }
+        // keep the prefetch and the next B fragments issued here (the
+        // scheduler would otherwise sink each load next to its use)
+        __builtin_amdgcn_sched_barrier(0);
+        v4i bn[8];
+        if (q + 1 < SPC) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) bn[j] = bfrag(s + 1, j);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int i = 0; i < RB; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], bcur[j], acc[i][j], 0, 0, 0);
+        if (q + 1 < SPC) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) bcur[j] = bn[j];
+        }
+      }
+    }
+  }
+
+  // Epilogue: MFMA wave w, lane (r, g), block i holds W rows 16 rb + 4g + {0..3}
+  // (rb = 6 tile_n + RB w + i: two gate/up pairs, outputs 48 tile_n + 8 (RB w + i)
+  // + 2g + {0, 1}) for tokens m0 + 16j + r. Staged as a [128][52] fp32 tile over
+  // the ring, then written with 16-byte stores, each token's 48 outputs (192
+  // bytes) contiguous.
+  lds_barrier();  // every X read is done (MFMA waves) and every load has landed (loaders)
+  float* ot = reinterpret_cast<float*>(lds);
+  if (wave < kT9MfmaWaves) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float2 o;
+        o.x = swiglu_w8a8(acc[i][j][0], acc[i][j][1], xsv[j], sc[i].x, sc[i].y);
+        o.y = swiglu_w8a8(acc[i][j][2], acc[i][j][3], xsv[j], sc[i].z, sc[i].w);
+        *reinterpret_cast<float2*>(ot + (16 * j + r) * kT9OutPitch + 8 * (RB * wave + i) + 2 * g) = o;
+      }
+  }
+  lds_barrier();
+  constexpr int V4_PER_ROW = kT9BN / 2 / 4;  // 12
+  constexpr int NV4 = kT9BM * V4_PER_ROW;
+#pragma unroll
+  for (int t = 0; t < (NV4 + 64 * kT9Waves - 1) / (64 * kT9Waves); ++t) {
+    const int q = t * 64 * kT9Waves + threadIdx.x;
+    const int row = q / V4_PER_ROW, c4 = q - row * V4_PER_ROW;
+    const int m = m0 + row;
+    if (q < NV4 && m < batch)
+      __builtin_nontemporal_store(*reinterpret_cast<const v4f*>(ot + row * kT9OutPitch + 4 * c4),
+                                  reinterpret_cast<v4f*>(out + (size_t)m * inter + tile_n * (kT9BN / 2) + 4 * c4));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Small-batch packed kernel (batch <= 64): one 8-wave workgroup per 48 W rows.
 //
 // With a single 64-token tile the 192-row kernel launches only 2*inter/192
@@ -766,6 +980,11 @@ inline bool packed_gemm_shape(size_t K, size_t inter) {
   return (K == 1024 || K == 2048) && (2 * inter) % kPkBN == 0;
 }
 
+template <int KS>
+bool t96_kernel_ready() {
+  return raise_lds_limit<&gemm_w8a8_swiglu_t96_kernel<KS>>(kT9Lds);
+}
+
 template <int KS, bool VEC_OUT>
 bool packed_kernel_ready() {
   return raise_lds_limit<&gemm_w8a8_swiglu_packed_kernel<KS, VEC_OUT>>(kPkLds);
@@ -799,6 +1018,21 @@ inline bool try_packed_gemm(float* out, const int8_t* wpk, const float* scales, 
     if (K == 2048 && small_kernel_ready<32>()) {
       gemm_w8a8_swiglu_small_kernel<32><<<grid, 64 * kSbWaves, kSbLds, st>>>(out, wpk, scales, xq, xs, B, I);
       return true;
+    }
+  }
+  if (vec && batch > (size_t)kT9BM && (2 * inter) % kT9BN == 0) {  // two or more 128-token tiles
+    const size_t nt = 2 * inter / kT9BN, mt = (batch + kT9BM - 1) / kT9BM;
+    if (nt * mt <= 0x7fffffffu) {
+      if (K == 1024 && t96_kernel_ready<16>()) {
+        gemm_w8a8_swiglu_t96_kernel<16><<<(unsigned)(nt * mt), 64 * kT9Waves, kT9Lds, st>>>(
+            out, wpk, scales, xq, xs, B, I, (int)nt, (int)mt);
+        return true;
+      }
+      if (K == 2048 && t96_kernel_ready<32>()) {
+        gemm_w8a8_swiglu_t96_kernel<32><<<(unsigned)(nt * mt), 64 * kT9Waves, kT9Lds, st>>>(
+            out, wpk, scales, xq, xs, B, I, (int)nt, (int)mt);
+        return true;
+      }
     }
   }
   if (K == 1024)

@@ -1181,8 +1181,11 @@ def test_pack_w8a8_tiles_layout(dev, rows, cols):
     np.testing.assert_array_equal(host(p.data), pack_tiles_reference(w))
 
 
+# batch > 128 takes the 96-row x 128-token tile (c5, t96_*), 64 < batch <= 128
+# the 192-row x 64-token tile, batch <= 64 the 48-row small kernel.
 PACKED_CASES = [("c5", 256, 2048, 6144), ("ragged", 37, 2048, 96), ("k1024", 100, 1024, 3072),
-                ("b1", 1, 2048, 96)]
+                ("b1", 1, 2048, 96), ("t96_ragged", 200, 2048, 6144), ("t96_k1024", 300, 1024, 3072),
+                ("t96_10tiles", 129, 2048, 480), ("b128", 128, 2048, 6144)]
 
 
 @pytest.mark.parametrize("name,batch,in_dim,inter", PACKED_CASES)
