@@ -500,35 +500,6 @@ QASR_DEV int dot16(v4i a, v4i b, int acc) {
   return acc;
 }
 
-// Quantizes this lane's 16*KCH activations (positions 1024*c + 16*lane + t)
-// with the per-vector absmax of the whole input (wave-wide max), packing them
-// into int8x16 registers; returns the vector's scale.
-template <int KCH>
-QASR_DEV float quantize_lane_values(const float (&v)[KCH][16], v4i* xq) {
-  float m = 0.0f;
-#pragma unroll
-  for (int c = 0; c < KCH; ++c)
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const float a = fabsf(v[c][t]);
-      if (a > m) m = a;
-    }
-  m = wave_max(m);
-  const float inv = m > 0.0f ? 127.0f / m : 0.0f;
-#pragma unroll
-  for (int c = 0; c < KCH; ++c) {
-    int p[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      p[t] = (quant_i8(v[c][4 * t], inv) & 0xff) | ((quant_i8(v[c][4 * t + 1], inv) & 0xff) << 8) |
-             ((quant_i8(v[c][4 * t + 2], inv) & 0xff) << 16) |
-             ((quant_i8(v[c][4 * t + 3], inv) & 0xff) << 24);
-    }
-    xq[c] = v4i{p[0], p[1], p[2], p[3]};
-  }
-  return m / 127.0f;
-}
-
 template <int KCH, int NP, bool F32IN>
 __global__ __launch_bounds__(256) void gateup_matvec_kernel(float* out, const int8_t* w,
                                                             const float* scales, const int8_t* xq8,
@@ -537,21 +508,21 @@ __global__ __launch_bounds__(256) void gateup_matvec_kernel(float* out, const in
   constexpr int K = KCH * 1024;
   const int lane = threadIdx.x & (kWave - 1);
   const int pair0 = (blockIdx.x * (256 / kWave) + threadIdx.x / kWave) * NP;
-  if (pair0 >= inter) return;
+  // With F32IN the workgroup quantizes x together (two barriers), so no wave
+  // leaves early: waves past the last pair clamp their loads and store nothing.
+  if (!F32IN && pair0 >= inter) return;
 
   // Activations first: their loads (L2-resident) retire before the weight
-  // stream's, since a wave's vector loads complete in issue order.
+  // stream's, since a wave's vector loads complete in issue order. fp32 input
+  // is read once per workgroup with consecutive 16-byte pieces per lane
+  // (thread t: float4 t + 256c); a lane's own 64-byte run of x would put the
+  // 64 lanes of one load on 32 different lines.
   v4i xq[KCH];
   float xs = 0.0f;
-  float xv[F32IN ? KCH : 1][16];
+  float4 xf4[F32IN ? KCH : 1];
   if constexpr (F32IN) {
 #pragma unroll
-    for (int c = 0; c < KCH; ++c)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float4 f = ld4(xf + c * 1024 + lane * 16 + 4 * t, 0);
-        xv[c][4 * t] = f.x; xv[c][4 * t + 1] = f.y; xv[c][4 * t + 2] = f.z; xv[c][4 * t + 3] = f.w;
-      }
+    for (int c = 0; c < KCH; ++c) xf4[c] = ld4(xf, threadIdx.x + 256 * c);
   } else {
 #pragma unroll
     for (int c = 0; c < KCH; ++c) xq[c] = reinterpret_cast<const v4i*>(xq8)[c * kWave + lane];
@@ -578,8 +549,38 @@ __global__ __launch_bounds__(256) void gateup_matvec_kernel(float* out, const in
   // sink them next to their dot products and serialise their latency).
   __builtin_amdgcn_sched_barrier(0);
 
-  // Per-vector quantization of x overlaps the weight stream.
-  if constexpr (F32IN) xs = quantize_lane_values<KCH>(xv, xq);
+  // Per-vector quantization of x (quantize.rs:633-662) overlaps the weight
+  // stream: the workgroup's absmax (NaN never wins, as `if abs > absmax`),
+  // the int8 vector into LDS, then each lane's 16*KCH bytes back out. The
+  // barriers wait on LDS only, so the weight loads stay in flight.
+  if constexpr (F32IN) {
+    __shared__ float red[256 / kWave];
+    __shared__ int xq_lds[KCH * 256];
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const float a[4] = {fabsf(xf4[c].x), fabsf(xf4[c].y), fabsf(xf4[c].z), fabsf(xf4[c].w)};
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (a[t] > m) m = a[t];
+    }
+    m = wave_max(m);
+    if (lane == 0) red[threadIdx.x / kWave] = m;
+    lds_barrier();
+    m = red[0];
+#pragma unroll
+    for (int i = 1; i < 256 / kWave; ++i) m = red[i] > m ? red[i] : m;
+    const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c)
+      xq_lds[threadIdx.x + 256 * c] = (quant_i8(xf4[c].x, inv) & 0xff) | ((quant_i8(xf4[c].y, inv) & 0xff) << 8) |
+                                      ((quant_i8(xf4[c].z, inv) & 0xff) << 16) |
+                                      ((quant_i8(xf4[c].w, inv) & 0xff) << 24);
+    lds_barrier();
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) xq[c] = reinterpret_cast<const v4i*>(xq_lds)[c * kWave + lane];
+    xs = m / 127.0f;
+  }
 
   int acc[NP][2];
 #pragma unroll
@@ -1501,7 +1502,6 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
   const float* bias = set.b[0];
   int N = set.N[0];
   unsigned bx0 = 0;
-  int mat = 0;
 #pragma unroll
   for (int m = 1; m < 4; ++m)
     if (m < set.n && bx >= set.bx_begin[m]) {
@@ -1511,7 +1511,6 @@ __global__ __launch_bounds__(64 * KW) void w8a32_gemm_ksplit_kernel(GemmSet set,
       bias = set.b[m];
       N = set.N[m];
       bx0 = set.bx_begin[m];
-      mat = m;
     }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches

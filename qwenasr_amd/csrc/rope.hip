@@ -87,15 +87,17 @@ QASR_DEV float* head_kv_dst(const HeadArgs& a, int kind, long long gh, int hd, l
   return (kind == 1 ? a.k_cache : a.v_cache) + cache_off;
 }
 
+constexpr int kHeadBlock = 128;  // threads per workgroup of the vector head kernel
+
 template <int HD, bool NORM, bool ROPE, bool KV = false>
-__global__ __launch_bounds__(256) void head_vec_kernel(HeadArgs a) {
+__global__ __launch_bounds__(kHeadBlock) void head_vec_kernel(HeadArgs a) {
   constexpr int L = HD / 8;
   constexpr int HPW = kWave / L;
   constexpr int HALF = HD / 2;
   const int lane = threadIdx.x & (kWave - 1);
   const int sub = lane & (L - 1);
   const long long gh =
-      ((long long)blockIdx.x * (256 / kWave) + threadIdx.x / kWave) * HPW + lane / L;
+      ((long long)blockIdx.x * (kHeadBlock / kWave) + threadIdx.x / kWave) * HPW + lane / L;
   if (gh >= a.total_heads) return;  // whole lane groups leave together
   float* base;        // where the result goes
   const float* src;   // where the head is read
@@ -219,13 +221,13 @@ int launch_heads(const HeadArgs& a, int hd, hipStream_t st) {
                    (!ROPE || (aligned16(a.cos_tab) && aligned16(a.sin_tab)));
   if (vec) {
     const long long hpw = kWave / (hd / 8);
-    const long long heads_per_block = hpw * (256 / kWave);
+    const long long heads_per_block = hpw * (kHeadBlock / kWave);
     const unsigned grid = (unsigned)((a.total_heads + heads_per_block - 1) / heads_per_block);
     switch (hd) {
-      case 64: head_vec_kernel<64, NORM, ROPE><<<grid, 256, 0, st>>>(a); break;
-      case 128: head_vec_kernel<128, NORM, ROPE><<<grid, 256, 0, st>>>(a); break;
-      case 256: head_vec_kernel<256, NORM, ROPE><<<grid, 256, 0, st>>>(a); break;
-      default: head_vec_kernel<512, NORM, ROPE><<<grid, 256, 0, st>>>(a); break;
+      case 64: head_vec_kernel<64, NORM, ROPE><<<grid, kHeadBlock, 0, st>>>(a); break;
+      case 128: head_vec_kernel<128, NORM, ROPE><<<grid, kHeadBlock, 0, st>>>(a); break;
+      case 256: head_vec_kernel<256, NORM, ROPE><<<grid, kHeadBlock, 0, st>>>(a); break;
+      default: head_vec_kernel<512, NORM, ROPE><<<grid, kHeadBlock, 0, st>>>(a); break;
     }
   } else {
     const unsigned grid = (unsigned)((a.total_heads + 3) / 4);
@@ -396,14 +398,14 @@ extern "C" int qasr_head_rms_norm_rope_kv_f32(float* q, const float* k, const fl
   a.start_pos = (long long)start_pos;
   a.cache_rows = (long long)cache_rows;
   const int hd = (int)head_dim;
-  const long long heads_per_block = (kWave / (hd / 8)) * (256 / kWave);
+  const long long heads_per_block = (kWave / (hd / 8)) * (kHeadBlock / kWave);
   const unsigned grid = (unsigned)((a.total_heads + heads_per_block - 1) / heads_per_block);
   hipStream_t st = as_stream(stream);
   switch (hd) {
-    case 64: head_vec_kernel<64, true, true, true><<<grid, 256, 0, st>>>(a); break;
-    case 128: head_vec_kernel<128, true, true, true><<<grid, 256, 0, st>>>(a); break;
-    case 256: head_vec_kernel<256, true, true, true><<<grid, 256, 0, st>>>(a); break;
-    default: head_vec_kernel<512, true, true, true><<<grid, 256, 0, st>>>(a); break;
+    case 64: head_vec_kernel<64, true, true, true><<<grid, kHeadBlock, 0, st>>>(a); break;
+    case 128: head_vec_kernel<128, true, true, true><<<grid, kHeadBlock, 0, st>>>(a); break;
+    case 256: head_vec_kernel<256, true, true, true><<<grid, kHeadBlock, 0, st>>>(a); break;
+    default: head_vec_kernel<512, true, true, true><<<grid, kHeadBlock, 0, st>>>(a); break;
   }
   return launch_status("head_rms_norm_rope_kv");
 }
