@@ -152,6 +152,9 @@ QASR_DEV float qnan() { return __int_as_float(0x7fc00000); }
 // s_waitcnt lgkmcnt(0) with vmcnt and expcnt left at their maxima (gfx9
 // encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
 constexpr int kWaitLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
+// s_waitcnt immediate that waits until at most n vector memory operations of
+// this wave are outstanding (LDS and export counters left free).
+constexpr int vmcnt_at_most(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
 
 // Workgroup barrier without a global-memory fence: the workgroup's LDS writes
 // are complete (lgkmcnt(0)) and visible after it; outstanding global loads and

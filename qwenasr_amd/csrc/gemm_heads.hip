@@ -279,6 +279,216 @@ __global__ __launch_bounds__(64 * kHdWaves) void gemm_w8a8_heads_kernel(HeadsArg
   }
 }
 
+// Streamed form of the q/k/v + heads kernel for 32-stream tiles (K = 1024 or
+// 2048). Eight MFMA waves each own one 16-row block of the head over the whole
+// K (no K halves to add up), and two loader waves bring the 32 stream rows in
+// with direct global->LDS loads, in chunks of 4 k-steps (32 rows x 256 bytes,
+// token row t's LDS slot l holding its data slot l ^ (t & 15)). All chunks are
+// issued at once and the whole tile stays in LDS; barrier c means chunk c has
+// landed, so the MFMAs start on the first 8 KiB instead of the whole tile. The
+// epilogue's position is loaded at entry and its gains and table rows under
+// the first chunk. Same dots, dequantization and head_norm_rope as
+// gemm_w8a8_heads_kernel<KS, 1, 32>: the results equal it bit for bit.
+constexpr int kHsMfma = kHdRows / 16;                     // 8: one 16-row block each
+constexpr int kHsLoaders = 2;
+constexpr int kHsWaves = kHsMfma + kHsLoaders;
+constexpr int kHsTok = 32;
+constexpr int kHsChunk = 256;                             // bytes of K per chunk
+constexpr int kHsChunkBytes = kHsTok * kHsChunk;          // 8 KiB
+constexpr int kHsPieces = kHsChunkBytes / 1024 / kHsLoaders;  // 1 KiB direct loads per chunk per loader
+constexpr int kHsPF = 8;                                  // k-steps of W in flight per MFMA wave
+
+template <int KS>
+constexpr size_t heads_stream_lds() {
+  return (size_t)kHsTok * KS * 64 + (size_t)kHsTok * kHdTPitch * sizeof(float);
+}
+
+// Waits until at most 4n of this wave's vector memory operations are
+// outstanding (n < 16; the immediate must be a constant).
+QASR_DEV void wait_vm_pieces(int n) {
+  static_assert(kHsPieces == 4, "the cases below count 4 loads per chunk");
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(0)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(4)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(8)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(12)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(16)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(20)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(24)); break;
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(28)); break;
+  }
+}
+
+template <int KS>  // K = 64 KS (16 or 32)
+__global__ __launch_bounds__(64 * kHsWaves) void gemm_w8a8_heads_stream_kernel(HeadsArgs a) {
+  constexpr int K = KS * 64;
+  constexpr int NCH = K / kHsChunk;       // chunks (4 or 8)
+  constexpr int SPC = kHsChunk / 64;      // k-steps per chunk
+  constexpr int PF = kHsPF;
+  static_assert(NCH * kHsPieces <= 63 && NCH <= 8, "every chunk in flight at once");
+  static_assert(kHsTok * 16 == 64 * kHsMfma, "one 16-thread group per stream in the MFMA waves");
+  extern __shared__ __align__(16) int8_t lds[];
+  float* T = reinterpret_cast<float*>(lds + (size_t)NCH * kHsChunkBytes);  // [32 streams][kHdTPitch]
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x;
+  int tile_n, tile_m;
+  if (a.n_tiles % kNumXcdH == 0) {
+    const int slot = b / kNumXcdH;
+    tile_m = slot % a.m_tiles;
+    tile_n = b % kNumXcdH + kNumXcdH * (slot / a.m_tiles);
+  } else {
+    tile_m = b % a.m_tiles;
+    tile_n = b / a.m_tiles;
+  }
+  const int n0 = tile_n * kHdRows, m0 = tile_m * kHsTok;
+  const int h = tile_n;
+  const int kind = h < a.n_heads ? 0 : (h < a.n_heads + a.n_kv_heads ? 1 : 2);
+
+  // epilogue: one stream per group of 16 threads of the MFMA waves
+  const int tok = threadIdx.x >> 4, sub = threadIdx.x & 15;
+  const int m = m0 + tok;
+  const bool live = wave < kHsMfma && m < a.batch;
+  float4 w1, w2, c1, c2, s1, s2;
+  int pos32 = 0;  // widened where it is used, after the first barrier
+  bool pos_ok = false;
+
+  v4i_t acc[2];
+  float4 sc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float xsv[2];
+  if (wave >= kHsMfma) {
+    // Loader: 1 KiB piece p of a chunk is stream rows 4p .. 4p + 3; lane l
+    // fills LDS slot l & 15 of row 4p + l / 16. Rows past the batch re-read
+    // row batch - 1 (valid memory); their results are never stored.
+    const int pw = wave - kHsMfma;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int i = 0; i < kHsPieces; ++i) {
+        const int piece = kHsPieces * pw + i;
+        const int row = 4 * piece + (lane >> 4);
+        const int data_slot = (lane & 15) ^ (row & 15);
+        const int src = m0 + row < a.batch ? m0 + row : a.batch - 1;
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(a.xq + (size_t)src * K + kHsChunk * c + 16 * data_slot),
+            (__attribute__((address_space(3))) void*)(lds + c * kHsChunkBytes + piece * 1024), 16, 0, 0);
+      }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      wait_vm_pieces(NCH - 1 - c);  // chunk c has landed
+      asm volatile("s_barrier" ::: "memory");
+    }
+  } else {
+    // the position first: waiting for it then leaves every later load in flight.
+    // Unconditional (a clamped, valid index): a load under a branch is waited
+    // for, with everything issued before it, where the branch ends.
+    pos32 = a.positions[m < a.batch ? m : a.batch - 1];
+    const int8_t* wp = a.w + ((size_t)(n0 / 16 + wave) * KS) * 1024 + 16 * lane;
+    v4i_t wbuf[PF];
+#pragma unroll
+    for (int d = 0; d < PF; ++d) wbuf[d] = *reinterpret_cast<const v4i_t*>(wp + d * 1024);
+    __builtin_amdgcn_sched_barrier(0);
+    sc = *reinterpret_cast<const float4*>(a.scales + n0 + 16 * wave + 4 * g);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int mt = m0 + 16 * j + r;
+      xsv[j] = a.xs[mt < a.batch ? mt : a.batch - 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[j] = v4i_t{0, 0, 0, 0};
+
+    // B fragment of stream tile j at k-step s
+    auto xfrag = [&](int s, int j) -> v4i_t {
+      const int slot = SPC * (s % SPC) + g;
+      return *reinterpret_cast<const v4i_t*>(lds + (s / SPC) * kHsChunkBytes + (16 * j + r) * kHsChunk +
+                                             16 * (slot ^ r));
+    };
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      lds_barrier();  // chunk c is in LDS
+      if (c == 0 && kind < 2) {
+        // the epilogue's gains and table rows, under the stream rows' loads
+        asm volatile("" : "+v"(pos32));  // first use here: the compiler would hoist the widening above the barrier
+        const long long pos = pos32;
+        pos_ok = m < a.batch && pos >= 0 && pos < a.table_rows && pos < a.cache_rows;
+        const long long pr = pos_ok ? pos : 0;  // out-of-table rows read row 0, then become NaN
+        const float* w = kind == 0 ? a.q_norm_w : a.k_norm_w;
+        w1 = ld4(w, sub);
+        w2 = ld4(w + 64, sub);
+        c1 = ld4(a.cos_tab + pr * 128, sub);
+        c2 = ld4(a.cos_tab + pr * 128 + 64, sub);
+        s1 = ld4(a.sin_tab + pr * 128, sub);
+        s2 = ld4(a.sin_tab + pr * 128 + 64, sub);
+      }
+      v4i_t bcur[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bcur[j] = xfrag(SPC * c, j);
+#pragma unroll
+      for (int q = 0; q < SPC; ++q) {
+        const int s = SPC * c + q;
+        const v4i_t av = wbuf[s % PF];
+        if (s + PF < KS) wbuf[s % PF] = *reinterpret_cast<const v4i_t*>(wp + (s + PF) * 1024);
+        // keep the prefetch and the next fragments issued here (the scheduler
+        // would sink each load next to its use)
+        __builtin_amdgcn_sched_barrier(0);
+        v4i_t bn[2];
+        if (q + 1 < SPC) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) bn[j] = xfrag(s + 1, j);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bcur[j], acc[j], 0, 0, 0);
+        if (q + 1 < SPC) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) bcur[j] = bn[j];
+        }
+      }
+    }
+    // Dequantize into the [32 streams][128 dims] tile (past the staged rows:
+    // no barrier needed before it): lane holds rows 16 wave + 4g + {0..3} of
+    // stream 16j + r.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float4 v;
+      v.x = ((float)acc[j][0] * xsv[j]) * sc.x;
+      v.y = ((float)acc[j][1] * xsv[j]) * sc.y;
+      v.z = ((float)acc[j][2] * xsv[j]) * sc.z;
+      v.w = ((float)acc[j][3] * xsv[j]) * sc.w;
+      *reinterpret_cast<float4*>(T + (16 * j + r) * kHdTPitch + 16 * wave + 4 * g) = v;
+    }
+  }
+  lds_barrier();
+  if (wave >= kHsMfma) return;  // loaders: done (no barrier follows)
+
+  float4 x1 = *reinterpret_cast<const float4*>(T + tok * kHdTPitch + 4 * sub);
+  float4 x2 = *reinterpret_cast<const float4*>(T + tok * kHdTPitch + 64 + 4 * sub);
+  const long long pos = pos32;
+  if (kind < 2) {
+    // every lane of the group joins the reduction, live or not
+    head_norm_rope<128, true, true>(x1, x2, w1, w2, c1, c2, s1, s2, pos_ok, a.eps);
+  } else {
+    pos_ok = m < a.batch && pos >= 0 && pos < a.table_rows && pos < a.cache_rows;
+  }
+  if (live) {
+    const int kv_dim = a.n_kv_heads * 128;
+    float* dst = nullptr;
+    if (kind == 0) {
+      dst = a.q_out + (size_t)m * a.n_heads * 128 + (size_t)h * 128;
+    } else if (pos_ok) {  // a row outside the cache is not written
+      float* cache = kind == 1 ? a.k_cache : a.v_cache;
+      const int kvh = kind == 1 ? h - a.n_heads : h - a.n_heads - a.n_kv_heads;
+      dst = cache + ((size_t)m * a.cache_rows + (size_t)pos) * kv_dim + (size_t)kvh * 128;
+    }
+    if (dst) {
+      st4(dst, sub, x1);
+      st4(dst + 64, sub, x2);
+    }
+  }
+}
+
 // Persistent form of the plain projection (MODE 0) for outputs many times
 // wider than the GPU (a batch's lm_head: [256,2048]x[2048,151936] is 9496
 // one-tile workgroups of 128 rows x 32 streams, 363 us). Each workgroup keeps
@@ -510,6 +720,15 @@ int launch_heads_tile(const HeadsArgs& a, unsigned grid, hipStream_t st, const c
   return launch_status(what);
 }
 
+template <int KS>
+int launch_heads_stream(const HeadsArgs& a, unsigned grid, hipStream_t st, const char* what) {
+  constexpr size_t lds = heads_stream_lds<KS>();
+  if (!heads_lds_ok<&gemm_w8a8_heads_stream_kernel<KS>>(lds))
+    return fail(QASR_ERR_UNSUPPORTED, std::string(what) + ": device LDS too small");
+  gemm_w8a8_heads_stream_kernel<KS><<<grid, 64 * kHsWaves, lds, st>>>(a);
+  return launch_status(what);
+}
+
 // The persistent projection: 256 workgroups (32 per XCD), the stream tile's
 // rows plus the exchange area and the dequantized tile in LDS.
 template <int KS, int TOK>
@@ -563,6 +782,9 @@ int launch_heads_k(HeadsArgs a, hipStream_t st, const char* what) {
     }
   }
   if constexpr (KS <= 32) {
+    if constexpr (MODE == 1) {
+      if (tok32) return launch_heads_stream<KS>(a, (unsigned)grid, st, what);
+    }
     if (tok32) return launch_heads_tile<KS, MODE, 32>(a, (unsigned)grid, st, what);
   }
   return launch_heads_tile<KS, MODE, 16>(a, (unsigned)grid, st, what);

@@ -690,10 +690,6 @@ constexpr size_t kT9Lds = (size_t)kT9Ring * kT9ChunkBytes;
 constexpr int kT9Prefetch = 3;                           // k-steps of W in flight per MFMA wave
 constexpr int kT9OutPitch = 52;                          // staged output row pitch (floats)
 
-// s_waitcnt immediate that waits until at most n vector memory operations of
-// this wave are outstanding (LDS and export counters left free).
-constexpr int vmcnt_at_most(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
-
 template <int KS>  // KS = K / 64 (16 or 32)
 __global__ __launch_bounds__(64 * kT9Waves) void gemm_w8a8_swiglu_t96_kernel(
     float* __restrict__ out, const int8_t* __restrict__ wpk, const float* __restrict__ scales,

@@ -126,17 +126,19 @@ def _run_fused(dev, c, batch, in_dim, cache_rows, fill=7.0):
     return q, kc, vc
 
 
-def test_qkv_heads_fused_equals_projection_then_head_kernel(dev):
-    """Ragged batch (37 streams: a partial 32-stream tile), one position
-    outside the RoPE table and one below 0: the fused launch equals
+@pytest.mark.parametrize("B,Kd", [(37, 2048), (250, 2048), (250, 1024)])
+def test_qkv_heads_fused_equals_projection_then_head_kernel(dev, B, Kd):
+    """Ragged batches (37 streams in 16-stream tiles; 250 in 32-stream tiles,
+    the streamed kernel, the last tile partial), one position outside the
+    RoPE table and one below 0: the fused launch equals
     qasr_linear_w8a8_packed + qasr_head_rms_norm_rope_kv_f32 bit for bit --
     q rows (NaN for the bad positions), the cache rows at each stream's
     position, and no other cache row touched."""
     from qwenasr_amd import kernels as K
 
-    B, Kd, rows = 37, 2048, 1024
-    c = _qkv_case(dev, B, Kd, rows, 52, bad_rows=((3, -1), (20, 5000)))
-    print("[batched] qkv heads fused", flush=True)
+    rows = 1024 if B < 64 else 256
+    c = _qkv_case(dev, B, Kd, rows, [52, B, Kd], bad_rows=((3, -1), (20, 5000)))
+    print(f"[batched] qkv heads fused B={B} K={Kd}", flush=True)
     q, kc, vc = _run_fused(dev, c, B, Kd, rows)
     # unfused: the projection, then the head kernel on its q/k/v slices
     N, kv = (NQ + 2 * NK) * HD, NK * HD
