@@ -672,10 +672,11 @@ __global__ __launch_bounds__(64 * kPkWaves) void gemm_w8a8_swiglu_packed_kernel(
 // the 192-row kernel's; results equal it bit for bit (int32 sums are exact).
 //
 // Measured at [256,2048] x [2048,12288]: 11.45 us against 12.1 us for the
-// 192 x 64 tile. Timing-only copies put 1.25 us on the W loads and 1.7 us on
-// the Xq loads; the rest is the launch, the MFMAs of the busiest SIMD (a third
-// of the tile: 6 row blocks do not split over 4 SIMDs without loading W twice)
-// and the SwiGLU epilogue (~1 us of transcendentals on 3 SIMDs).
+// 192 x 64 tile. Timing-only copies put 1.25 us on the W loads, 1.7 us on the
+// Xq loads, ~1 us on the MFMAs (the busiest SIMD issues a third of them: 6
+// row blocks do not split over 4 SIMDs without loading W twice; most of their
+// 3.4 us hides under the loads) and 0.65 us on the SwiGLU arithmetic; the rest
+// is the launch, the wait for the first chunk and the stores.
 // ---------------------------------------------------------------------------
 constexpr int kT9BN = 96;                                // W rows per workgroup
 constexpr int kT9BM = 128;                               // tokens per workgroup
