@@ -685,6 +685,7 @@ constexpr int kGemmXNorm = 8;
 // register sets of the double-buffered one (4 sets measured the same as 2)
 constexpr int kGemmPrefetch = 1;
 constexpr int kGemmSets = 2;
+constexpr int kGemmPcSets = 4;  // the producer/consumer kernel's register sets (chunks in flight)
 
 QASR_DEV unsigned short bf16_bits_trunc(float v) { return (unsigned short)(__float_as_uint(v) >> 16); }
 QASR_DEV float bf16_trunc(float v) { return __uint_as_float(__float_as_uint(v) & 0xffff0000u); }
@@ -899,6 +900,66 @@ struct GemmEpiRows {
   QASR_DEV float shift(int i, int off) const { return __shfl(b[i >> 1], 32 * (i & 1) + off, kWave); }
 };
 
+// The epilogue of the LDS-staged kernels, run by the 4 waves that hold the
+// accumulators (threads 0..255) after the k loop's last barrier: 1 / rms of
+// the folded RMSNorm, then the heads epilogue or the row scales (and biases)
+// with a plain, SwiGLU or bias store.
+template <int BN, int BT, int EPI, int MI, int MJ>
+QASR_DEV void gemm_tile_epilogue(const v16f (&acc)[MI][MJ], const GemmEpiRows<MI, (EPI & 7) == kGemmBias>& ep,
+                                 const float (&xp)[MJ][kXnMaxSlices], const GemmXNorm& xn, int K,
+                                 unsigned short* lds, int mat, float* y, const float* __restrict__ scales, int N,
+                                 int n0, int t0, int T, const GemmHeadEpi& he) {
+  constexpr int EP = EPI & 7;
+  constexpr bool XN = (EPI & kGemmXNorm) != 0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wr = wave & 1, wc = wave >> 1;
+  const int r = lane & 31, g = lane >> 5;
+  [[maybe_unused]] float rt[MJ];  // XN: 1 / rms of the lane's tokens
+  if constexpr (XN) {
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) rt[j] = xnorm_rinv(xp[j], K, xn.eps);
+  }
+  if constexpr (EP == kGemmHeads) {
+    static_assert(BN == 128, "one head per tile");
+    gemm_heads_epilogue<BT, MI, MJ, XN>(acc, reinterpret_cast<float*>(lds), mat, y, scales, N, n0, t0, T, he,
+                                        rt);
+    return;
+  }
+  // lane l, register 4q + v of block (i, j) holds row n0 + (BN/2)wr + 32i + 8q + 4(l/32) + v
+  // of token t0 + (BT/2)wc + 32j + l%32
+  const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+  for (int j = 0; j < MJ; ++j) {
+    const int t = t0 + (BT / 2) * wc + 32 * j + r;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + (BN / 2) * wr + 32 * i + 8 * q + 4 * g;
+        float res[4];
+        // the cross-lane reads run with every lane active (an inactive source
+        // lane reads as 0); lanes past the last token only skip the stores
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          res[v] = acc[i][j][4 * q + v] * ep.scale(i, 8 * q + 4 * g + v);
+          if constexpr (XN) res[v] *= rt[j];
+          if constexpr (EP == kGemmBias) res[v] += ep.shift(i, 8 * q + 4 * g + v);
+        }
+        if (t < T) {
+          if constexpr (EP == kGemmSwiglu || EP == kGemmSwigluLibm) {
+            swiglu_store<EP>(y, res, t, n, N);
+          } else if (vec_out && n + 3 < N) {
+            *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (n + v < N) y[(size_t)t * N + n + v] = res[v];
+          }
+        }
+      }
+  }
+}
+
 template <int BN, int BT, int BK, int NPF, int EPI>
 __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, TileMap map,
                                                                 const float* __restrict__ x, int T, int K,
@@ -1042,50 +1103,7 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_kernel(GemmSet set, Til
     }
   }
 
-  [[maybe_unused]] float rt[MJ];  // XN: 1 / rms of the lane's tokens
-  if constexpr (XN) {
-#pragma unroll
-    for (int j = 0; j < MJ; ++j) rt[j] = xnorm_rinv(xp[j], K, xn.eps);
-  }
-  if constexpr (EP == kGemmHeads) {
-    static_assert(BN == 128, "one head per tile");
-    gemm_heads_epilogue<BT, MI, MJ, XN>(acc, reinterpret_cast<float*>(gm_lds), mat, y, scales, N, n0, t0, T, he,
-                                        rt);
-    return;
-  }
-  // lane l, register 4q + v of block (i, j) holds row n0 + (BN/2)wr + 32i + 8q + 4(l/32) + v
-  // of token t0 + (BT/2)wc + 32j + l%32
-  const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
-#pragma unroll
-  for (int j = 0; j < MJ; ++j) {
-    const int t = t0 + (BT / 2) * wc + 32 * j + r;
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + (BN / 2) * wr + 32 * i + 8 * q + 4 * g;
-        float res[4];
-        // the cross-lane reads run with every lane active (an inactive source
-        // lane reads as 0); lanes past the last token only skip the stores
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          res[v] = acc[i][j][4 * q + v] * ep.scale(i, 8 * q + 4 * g + v);
-          if constexpr (XN) res[v] *= rt[j];
-          if constexpr (EP == kGemmBias) res[v] += ep.shift(i, 8 * q + 4 * g + v);
-        }
-        if (t < T) {
-          if constexpr (EP == kGemmSwiglu || EP == kGemmSwigluLibm) {
-            swiglu_store<EP>(y, res, t, n, N);
-          } else if (vec_out && n + 3 < N) {
-            *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
-          } else {
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-              if (n + v < N) y[(size_t)t * N + n + v] = res[v];
-          }
-        }
-      }
-  }
+  gemm_tile_epilogue<BN, BT, EPI>(acc, ep, xp, xn, K, gm_lds, mat, y, scales, N, n0, t0, T, he);
 }
 
 template <int BN, int BT, int BK>
@@ -1267,50 +1285,193 @@ __global__ __launch_bounds__(256) void w8a32_gemm_bf16x3_db_kernel(GemmSet set, 
     }
   }
 
-  [[maybe_unused]] float rt[MJ];  // XN: 1 / rms of the lane's tokens
-  if constexpr (XN) {
+  gemm_tile_epilogue<BN, BT, EPI>(acc, ep, xp, xn, K, gm_lds, mat, y, scales, N, n0, t0, T, he);
+}
+
+// Producer/consumer form of the double-buffered kernel: 8 waves, the same
+// tiles, stages and products in the same order per accumulator (so the same
+// results bit for bit). Waves 0-3 hold the accumulators: each chunk they only
+// read the staged operands and issue the MFMAs. Waves 4-7, the converters (one
+// per SIMD beside an MFMA wave), load the chunks NS ahead into registers,
+// convert them (int8 -> bf16, fp32 -> three bf16 terms) and write them to the
+// stage the MFMA waves read next. The conversion's VALU work and the waits for
+// the loads then sit on other waves than the products: the SIMD issues a
+// converter's VALU instructions while its MFMA wave's products run, and an
+// MFMA wave never waits on global memory. One barrier per chunk publishes the
+// next stage and retires the reads of the stage the converters overwrite
+// after it. The converters return after the loop's last barrier; the
+// epilogue's barriers then count the 4 MFMA waves only.
+template <int BN, int BT, int BK, int NS, int EPI>
+__global__ __launch_bounds__(512) void w8a32_gemm_bf16x3_pc_kernel(GemmSet set, TileMap map,
+                                                                   const float* __restrict__ x, int T, int K,
+                                                                   GemmHeadEpi he, GemmXNorm xn) {
+  constexpr int kGmRow = BK + 8;                   // LDS row in bf16 (16-byte pad)
+  constexpr int STAGE = (BN + 3 * BT) * kGmRow;    // bf16 per LDS stage
+  extern __shared__ __align__(16) unsigned short gm_lds[];  // 2 x ([BN][kGmRow] weights, [3][BT][kGmRow] terms)
+  unsigned bx, by;
+  tile_of(map, blockIdx.x, bx, by);
+  float* y = set.y[0];
+  const int8_t* w = set.w[0];
+  const float* scales = set.s[0];
+  const float* bias = set.b[0];
+  int N = set.N[0];
+  unsigned bx0 = 0;
+  int mat = 0;
 #pragma unroll
-    for (int j = 0; j < MJ; ++j) rt[j] = xnorm_rinv(xp[j], K, xn.eps);
-  }
-  if constexpr (EP == kGemmHeads) {
-    static_assert(BN == 128, "one head per tile");
-    gemm_heads_epilogue<BT, MI, MJ, XN>(acc, reinterpret_cast<float*>(gm_lds), mat, y, scales, N, n0, t0, T, he,
-                                        rt);
-    return;
-  }
-  // lane l, register 4q + v of block (i, j) holds row n0 + (BN/2)wr + 32i + 8q + 4(l/32) + v
-  // of token t0 + (BT/2)wc + 32j + l%32
-  const bool vec_out = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  for (int m = 1; m < 4; ++m)
+    if (m < set.n && bx >= set.bx_begin[m]) {
+      y = set.y[m];
+      w = set.w[m];
+      scales = set.s[m];
+      bias = set.b[m];
+      N = set.N[m];
+      bx0 = set.bx_begin[m];
+      mat = m;
+    }
+  constexpr int MI = BN / 64, MJ = BT / 64;
+  static_assert(BN % 64 == 0 && BT % 64 == 0, "32 x 32 blocks per wave");
+  constexpr int EP = EPI & 7;
+  constexpr bool XN = (EPI & kGemmXNorm) != 0;
+  constexpr int NW = BN / 64, NX = BT / 16;         // 16-byte staging items per converter thread
+  constexpr int KSTEPS = BK / 16;                    // MFMA k steps per chunk
+  static_assert(BK == 64 && NW >= 1 && NX >= 1, "the staging map of the double-buffered kernel");
+  static_assert(NS >= 2 && NS % 2 == 0, "an even number of register sets");
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // uniform: scalar branches
+  const int n0 = (int)(bx - bx0) * BN, t0 = (int)by * BT;
+  const int nch = K / BK;
+  unsigned short* st0 = gm_lds;
+  unsigned short* st1 = gm_lds + STAGE;
+
+  if (wave >= 4) {
+    // Converter thread ct stages the items of thread ct of the 256-thread kernel.
+    const int ct = (int)threadIdx.x - 256;
+    const int w_part = ct & 3, x_part = ct & 15;
+    const int8_t* wsrc[NW];
+    const float* xsrc[NX];
+    // rows and tokens past the end re-read the last one (valid memory; not stored)
 #pragma unroll
-  for (int j = 0; j < MJ; ++j) {
-    const int t = t0 + (BT / 2) * wc + 32 * j + r;
+    for (int c = 0; c < NW; ++c) wsrc[c] = w + (size_t)min(n0 + 64 * c + (ct >> 2), N - 1) * K + 16 * w_part;
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int c = 0; c < NX; ++c) xsrc[c] = x + (size_t)min(t0 + 16 * c + (ct >> 4), T - 1) * K + 4 * x_part;
+    auto load = [&](v4i (&wv)[NW], v4f (&xv)[NX], int k0) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + (BN / 2) * wr + 32 * i + 8 * q + 4 * g;
-        float res[4];
-        // the cross-lane reads run with every lane active (an inactive source
-        // lane reads as 0); lanes past the last token only skip the stores
+      for (int c = 0; c < NW; ++c) wv[c] = *reinterpret_cast<const v4i*>(wsrc[c] + k0);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          res[v] = acc[i][j][4 * q + v] * ep.scale(i, 8 * q + 4 * g + v);
-          if constexpr (XN) res[v] *= rt[j];
-          if constexpr (EP == kGemmBias) res[v] += ep.shift(i, 8 * q + 4 * g + v);
-        }
-        if (t < T) {
-          if constexpr (EP == kGemmSwiglu || EP == kGemmSwigluLibm) {
-            swiglu_store<EP>(y, res, t, n, N);
-          } else if (vec_out && n + 3 < N) {
-            *reinterpret_cast<float4*>(&y[(size_t)t * N + n]) = make_float4(res[0], res[1], res[2], res[3]);
-          } else {
+      for (int c = 0; c < NX; ++c) xv[c] = *reinterpret_cast<const v4f*>(xsrc[c] + k0);
+    };
+    auto stage = [&](const v4i (&wv)[NW], const v4f (&xv)[NX], unsigned short* st) {
+      auto wl = reinterpret_cast<unsigned short (*)[kGmRow]>(st);
+      auto xl = reinterpret_cast<unsigned short (*)[BT][kGmRow]>(st + BN * kGmRow);
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-              if (n + v < N) y[(size_t)t * N + n + v] = res[v];
-          }
+      for (int c = 0; c < NW; ++c) {
+        const v4i wc = wv[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {  // int8 -> bf16 is exact (at most 8 significant bits)
+          const int v = wc[e];
+          const uint2 h = make_uint2(bf16_pair((float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff)),
+                                     bf16_pair((float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)((v >> 24) & 0xff)));
+          *reinterpret_cast<uint2*>(&wl[64 * c + (ct >> 2)][16 * w_part + 4 * e]) = h;
         }
       }
+#pragma unroll
+      for (int c = 0; c < NX; ++c) {  // x = hi + mid + lo exactly
+        const v4f xc = xv[c];
+        const float ev[4] = {xc.x, xc.y, xc.z, xc.w};
+        float r1[4], r2[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          r1[e] = ev[e] - bf16_trunc(ev[e]);
+          r2[e] = r1[e] - bf16_trunc(r1[e]);  // at most 8 significant bits
+        }
+        const int tok = 16 * c + (ct >> 4), col = 4 * x_part;
+        *reinterpret_cast<uint2*>(&xl[0][tok][col]) = make_uint2(bf16_pair(ev[0], ev[1]), bf16_pair(ev[2], ev[3]));
+        *reinterpret_cast<uint2*>(&xl[1][tok][col]) = make_uint2(bf16_pair(r1[0], r1[1]), bf16_pair(r1[2], r1[3]));
+        *reinterpret_cast<uint2*>(&xl[2][tok][col]) = make_uint2(bf16_pair(r2[0], r2[1]), bf16_pair(r2[2], r2[3]));
+      }
+    };
+    // Register set u holds chunks u, u + NS, ...: chunk j is loaded as soon as
+    // chunk j - NS has been staged, NS - 1 chunks of products ahead of its use.
+    // Chunks past the end re-load the last one (valid memory) and the final
+    // pass stages it into the idle stage: the loop stays free of branches.
+    // The caller guarantees K % (NS * BK) == 0.
+    v4i wreg[NS][NW];
+    v4f xreg[NS][NX];
+#pragma unroll
+    for (int u = 0; u < NS; ++u) load(wreg[u], xreg[u], min(u, nch - 1) * BK);
+    stage(wreg[0], xreg[0], st0);
+    load(wreg[0], xreg[0], min(NS, nch - 1) * BK);
+    lds_barrier();
+    for (int c = 0; c < nch; c += NS) {
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {  // while chunk c + u is multiplied from stage u % 2, stage chunk c + u + 1
+        stage(wreg[(u + 1) % NS], xreg[(u + 1) % NS], (u & 1) ? st0 : st1);
+        load(wreg[(u + 1) % NS], xreg[(u + 1) % NS], min(c + u + 1 + NS, nch - 1) * BK);
+        lds_barrier();
+      }
+    }
+    return;
   }
+
+  const int lane = threadIdx.x & 63;
+  const int wr = wave & 1, wc = wave >> 1;
+  const int r = lane & 31, g = lane >> 5;
+  v16f acc[MI][MJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) acc[i][j] = v16f{};
+  [[maybe_unused]] GemmEpiRows<MI, EP == kGemmBias> ep;
+  if constexpr (EP != kGemmHeads) ep.load(scales, bias, N, n0 + (BN / 2) * wr, lane);
+  [[maybe_unused]] float xp[MJ][kXnMaxSlices];  // XN: the partial sums of squares of the lane's epilogue tokens
+  if constexpr (XN) {
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) xnorm_load(xp[j], xn, min(t0 + (BT / 2) * wc + 32 * j + r, T - 1));
+  }
+  // The operand fragments of k step s of the chunk staged in `st`, and the
+  // step's products in the order of the single-buffered kernel (term, then
+  // row block, then token block). The fragments of step s + 1 are read before
+  // the products of step s issue (two register sets), so the LDS latency hides
+  // under six MFMAs instead of stalling each term's products.
+  auto read_step = [&](const unsigned short* st, int s, v8bf (&a)[MI], v8bf (&b)[3][MJ]) {
+    auto wl = reinterpret_cast<const unsigned short (*)[kGmRow]>(st);
+    auto xl = reinterpret_cast<const unsigned short (*)[BT][kGmRow]>(st + BN * kGmRow);
+    const int kk = 16 * s;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) a[i] = *reinterpret_cast<const v8bf*>(&wl[(BN / 2) * wr + 32 * i + r][kk + 8 * g]);
+#pragma unroll
+    for (int term = 0; term < 3; ++term)
+#pragma unroll
+      for (int j = 0; j < MJ; ++j)
+        b[term][j] = *reinterpret_cast<const v8bf*>(&xl[term][(BT / 2) * wc + 32 * j + r][kk + 8 * g]);
+  };
+  auto mfma_step = [&](const v8bf (&a)[MI], const v8bf (&b)[3][MJ]) {
+#pragma unroll
+    for (int term = 0; term < 3; ++term)
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[term][j], acc[i][j], 0, 0, 0);
+  };
+  auto chunk = [&](const unsigned short* st) {
+    v8bf a[2][MI], b[2][3][MJ];
+    read_step(st, 0, a[0], b[0]);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      if (s + 1 < KSTEPS) read_step(st, s + 1, a[(s + 1) & 1], b[(s + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_step(a[s & 1], b[s & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  lds_barrier();  // chunk 0 staged
+  for (int c = 0; c < nch; c += 2) {  // nch is even (a multiple of NS)
+    chunk(st0);
+    lds_barrier();
+    chunk(st1);
+    lds_barrier();
+  }
+  gemm_tile_epilogue<BN, BT, EPI>(acc, ep, xp, xn, K, gm_lds, mat, y, scales, N, n0, t0, T, he);
 }
 
 // Column split of the XCD map that minimises the bytes one XCD reads
@@ -1697,6 +1858,21 @@ bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K
   return true;
 }
 
+template <int BN, int BT, int BK, int NS, int EPI>
+bool try_gemm_pc(const GemmSet& set, unsigned cols, const float* x, int T, int K, hipStream_t st,
+                 const GemmHeadEpi& he = GemmHeadEpi{}, const GemmXNorm& xn = GemmXNorm{}) {
+  constexpr size_t lds = 2 * gemm_lds_bytes<BN, BT, BK>();
+  if (K % (NS * BK) != 0) return false;
+  if (lds > 65536 && !raise_lds_limit<&w8a32_gemm_bf16x3_pc_kernel<BN, BT, BK, NS, EPI>>(lds)) return false;
+  TileMap map;
+  map.cols = cols;
+  map.rows = (unsigned)((T + BT - 1) / BT);
+  map.split_cols = xcd_split_cols(map.cols, map.rows, BN, BT);
+  w8a32_gemm_bf16x3_pc_kernel<BN, BT, BK, NS, EPI><<<map.cols * map.rows, 512, lds, st>>>(set, map, x, T, K, he,
+                                                                                         xn);
+  return true;
+}
+
 // Kernel and tile: the LDS-staged 256 x 64 tile where it still gives at least
 // 512 workgroups (a 256-stream lm_head: each workgroup's activation rows then
 // serve twice the weight rows, 634.7 -> 579.9 us at [256,2048]x[2048,151936];
@@ -1709,8 +1885,11 @@ bool try_gemm_db(const GemmSet& set, unsigned cols, const float* x, int T, int K
 // only one: 0.6B gate/up at T = 512 33.5 against 42-45 us), except where the
 // 128-row tiles would give some CUs two workgroups and others one while
 // 192-row tiles give at most one per CU: those run double-buffered (0.6B
-// gate/up at T = 512: 384 tiles of 128 rows 29.3 us, 256 of 192 27.3 us);
-// otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
+// gate/up at T = 512: 384 tiles of 128 rows 29.3 us, 256 of 192 27.3 us).
+// Where the double-buffered kernel would run, its producer/consumer form runs
+// instead when K is a multiple of 4 chunks (0.6B at T = 512, one box, cold
+// inputs: q/k/v 24.7 -> 21.8 us, gate/up 29.6 -> 26.8 us; the prefill step
+// 3004 -> 2861 us); otherwise the split-K kernel with the largest of 64 x 64, 64 x 32 and
 // 32 x 32 that fills the chip (measured at T = 512: o [1024, 2048] 20.0 ->
 // 16.7 us, down [1024, 3072] 27.4 -> 20.9 us against the LDS-staged 64 x 32).
 // Returns false when the chosen kernel cannot run the shape (K not a multiple
@@ -1736,11 +1915,14 @@ bool launch_w8a32_gemm(GemmSet set, const float* x, int T, int K, hipStream_t st
   const unsigned c128 = cols(128);
   c = cols(192);
   if (c128 * rows64 > 256 && c * rows64 <= 256 &&
-      try_gemm_db<192, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st, he, xn))
+      (try_gemm_pc<192, 64, 64, kGemmPcSets, EPI>(set, c, x, T, K, st, he, xn) ||
+       try_gemm_db<192, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st, he, xn)))
     return true;
   c = cols(128);
   if (c * rows64 >= 256) {
-    if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st, he, xn)) return true;
+    if (c * rows64 <= 256 && (try_gemm_pc<128, 64, 64, kGemmPcSets, EPI>(set, c, x, T, K, st, he, xn) ||
+                              try_gemm_db<128, 64, 64, kGemmSets, EPI>(set, c, x, T, K, st, he, xn)))
+      return true;
     return try_gemm<128, 64, 64, kGemmPrefetch, EPI>(set, c, x, T, K, st, he, xn);
   }
   if constexpr ((EPI & kGemmXNorm) != 0) {
@@ -1783,8 +1965,9 @@ extern "C" int qasr_quantize_rows_i8(int8_t* q, float* scales, const float* x, s
 // per-token matvecs.
 constexpr size_t kGemmMinTokens = 8;
 
-// The q/k/v GEMM with the heads epilogue: 128-row tiles (one head), double
-// buffered where that is one workgroup per CU, as for the plain projection.
+// The q/k/v GEMM with the heads epilogue: 128-row tiles (one head), the
+// producer/consumer (else double-buffered) kernel where that is one workgroup
+// per CU, as for the plain projection.
 static bool launch_w8a32_heads(GemmSet set, const float* x, int T, int K, const GemmHeadEpi& he,
                                hipStream_t st, const GemmXNorm& xn = GemmXNorm{}) {
   unsigned c = 0;
@@ -1796,10 +1979,14 @@ static bool launch_w8a32_heads(GemmSet set, const float* x, int T, int K, const 
   const long long rows64 = (T + 63) / 64;
   constexpr int kFold = kGemmHeads | kGemmXNorm;
   if (xn.ss) {
-    if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, kFold>(set, c, x, T, K, st, he, xn)) return true;
+    if (c * rows64 <= 256 && (try_gemm_pc<128, 64, 64, kGemmPcSets, kFold>(set, c, x, T, K, st, he, xn) ||
+                              try_gemm_db<128, 64, 64, kGemmSets, kFold>(set, c, x, T, K, st, he, xn)))
+      return true;
     return try_gemm<128, 64, 64, kGemmPrefetch, kFold>(set, c, x, T, K, st, he, xn);
   }
-  if (c * rows64 <= 256 && try_gemm_db<128, 64, 64, kGemmSets, kGemmHeads>(set, c, x, T, K, st, he)) return true;
+  if (c * rows64 <= 256 && (try_gemm_pc<128, 64, 64, kGemmPcSets, kGemmHeads>(set, c, x, T, K, st, he) ||
+                            try_gemm_db<128, 64, 64, kGemmSets, kGemmHeads>(set, c, x, T, K, st, he)))
+    return true;
   return try_gemm<128, 64, 64, kGemmPrefetch, kGemmHeads>(set, c, x, T, K, st, he);
 }
 
