@@ -1430,8 +1430,8 @@ __global__ __launch_bounds__(512) void w8a32_gemm_bf16x3_pc_kernel(GemmSet set, 
   // The operand fragments of k step s of the chunk staged in `st`, and the
   // step's products in the order of the single-buffered kernel (term, then
   // row block, then token block). The fragments of step s + 1 are read before
-  // the products of step s issue (two register sets), so the LDS latency hides
-  // under six MFMAs instead of stalling each term's products.
+  // the products of step s issue (two register sets), so each step's products
+  // wait only for their own fragments.
   auto read_step = [&](const unsigned short* st, int s, v8bf (&a)[MI], v8bf (&b)[3][MJ]) {
     auto wl = reinterpret_cast<const unsigned short (*)[kGmRow]>(st);
     auto xl = reinterpret_cast<const unsigned short (*)[BT][kGmRow]>(st + BN * kGmRow);
