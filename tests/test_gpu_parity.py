@@ -285,7 +285,9 @@ def test_head_rms_norm_rope_kv_single_sequence(dev, seq, start, nq, nk, hd, cach
 
 
 @pytest.mark.parametrize("seq,H,start,cache_rows,exact,nq,nk", [
-    (512, 1024, 0, 1024, True, 16, 8),    # 0.6B prefill chunk: the double-buffered tile, 256 workgroups
+    (512, 1024, 0, 1024, True, 16, 8),    # 0.6B prefill chunk: the producer/consumer tile, 256 workgroups
+    (500, 1024, 3, 1024, True, 16, 8),    # ragged last token tile, the same kernel
+    (512, 1152, 0, 1024, True, 16, 8),    # K not a multiple of 4 chunks: the double-buffered kernel
     (1000, 1024, 24, 1536, True, 16, 8),  # 512 workgroups: the single-buffered tile
     (100, 2048, 37, 512, False, 16, 8),   # ragged token tile (the plain launch takes the split-K tile)
     (64, 1088, 5, 128, False, 16, 8),     # in_dim % 128 = 64: single-buffered
@@ -405,7 +407,8 @@ def test_linear_int8_residual(dev, seq, in_dim, out_dim, exact):
 
 
 @pytest.mark.parametrize("seq,H,I,folded", [
-    (512, 1024, 3072, True),    # 0.6B at 512 tokens: the double-buffered 192-row tile
+    (512, 1024, 3072, True),    # 0.6B at 512 tokens: the producer/consumer 192-row tile
+    (500, 1024, 3072, True),    # ragged last token tile, the same kernel
     (1024, 1024, 3072, True),   # the single-buffered 128-row tile
     (1024, 2048, 6144, True),   # the 256-row tile
     (37, 1024, 3072, False),    # too few tiles for the LDS-staged kernels: x_norm = hg * rinv + the plain launch
@@ -445,7 +448,8 @@ def test_rms_norm_gate_up_swiglu_multiply_int8(dev, seq, H, I, folded):
 
 
 @pytest.mark.parametrize("seq,H,start,cache_rows", [
-    (512, 1024, 0, 1024),    # 0.6B prefill chunk: the double-buffered tile
+    (512, 1024, 0, 1024),    # 0.6B prefill chunk: the producer/consumer tile
+    (500, 1024, 7, 1024),    # ragged last token tile, the same kernel
     (1000, 1024, 24, 1536),  # the single-buffered tile
     (100, 2048, 37, 512),    # ragged token tile
     (200, 2112, 5, 256),     # 33 slices: x_norm = hg * rinv, then the plain launch
@@ -1040,18 +1044,27 @@ def test_linear_int8_integer_inputs_exact(dev):
     np.testing.assert_array_equal(host(y).astype(np.int64), exact)
 
 
-@pytest.mark.parametrize("seq", [1, 64])
-def test_linear_int8_integer_inputs_exact_many_tokens(dev, seq):
+@pytest.mark.parametrize("seq,in_dim,out_dim", [
+    (1, 2048, 300),      # the one-token rows kernel
+    (64, 2048, 300),     # the split-K GEMM
+    (500, 1024, 4096),   # the producer/consumer 128-row tile, ragged last token tile
+    (512, 1024, 6144),   # its 192-row tile
+])
+def test_linear_int8_integer_inputs_exact_many_tokens(dev, seq, in_dim, out_dim):
     """Integer activations with unit scales: every path (one-token rows kernel,
-    matrix-core GEMM) returns the exact integer dots -- the three-term bf16
+    matrix-core GEMMs) returns the exact integer dots -- the three-term bf16
     split of an integer is exact and the fp32 sums stay below 2^24."""
     from qwenasr_amd import kernels as K
 
-    r = rng(21, seq)
-    in_dim, out_dim = 2048, 300
+    r = rng(21, seq, in_dim, out_dim)
     wq = r.integers(-128, 128, (out_dim, in_dim), dtype=np.int8)
     x = r.integers(-20, 21, (seq, in_dim)).astype(np.float32)
-    x[0, :5] = [1e-3, -2.5e-2, 3.75, 1 / 3, 65.0]  # non-integers: compared to float64 below
+    # row 0 non-integer throughout (compared to float64 below); small entries
+    # beside the five specials keep its partial sums near its result, so fp32
+    # accumulation stays inside the tolerance (integers up to 20 in the row
+    # would cancel down to outputs far below the partial sums)
+    x[0] = normal(r, in_dim, 1e-3)
+    x[0, :5] = [1e-3, -2.5e-2, 3.75, 1 / 3, 65.0]
     y = torch.empty(seq * out_dim, dtype=torch.float32, device=dev)
     K.linear_nobias_int8(y, dev_t(x.ravel(), dev), dev_t(wq, dev), torch.ones(out_dim, device=dev), seq,
                          in_dim, out_dim)
