@@ -953,7 +953,7 @@ def test_add_rms_norm_gate_up_swiglu_equals_unfused(dev, H, I, with_delta):
                                                 (8, 1024, 33), (64, 2048, 2048), (512, 1024, 6144),
                                                 (100, 3072, 1000), (17, 1024, 130), (70, 6144, 257),
                                                 (9, 1088, 200),
-                                                # 192-row double-buffered tiles, ragged rows and tokens
+                                                # 192-row producer/consumer tiles, ragged rows and tokens
                                                 (500, 1024, 5000),
                                                 # split-K 64x64, 64x32 tiles (32x32 above), ragged
                                                 (512, 1024, 2048), (512, 1088, 2048), (520, 1024, 2000),
@@ -961,8 +961,9 @@ def test_add_rms_norm_gate_up_swiglu_equals_unfused(dev, H, I, with_delta):
                                                 # split-K with 1-2 k steps (waves without a step)
                                                 (16, 64, 64), (40, 128, 100),
                                                 # 128 x 64 tiles, one workgroup per CU: the
-                                                # double-buffered kernel (ragged), and a K it
-                                                # refuses (17 chunks) that falls back
+                                                # producer/consumer kernel (ragged), and a K
+                                                # (17 chunks) that it and the double-buffered
+                                                # kernel refuse: the single-buffered one
                                                 (512, 1024, 4096), (500, 2048, 4000), (512, 1088, 4096)])
 def test_linear_nobias_int8_w8a32(dev, seq, in_dim, out_dim):
     from qwenasr_amd import kernels as K
